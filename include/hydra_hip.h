@@ -1,0 +1,193 @@
+/*
+ * hydra_hip.h — C ABI of HydraHIP, the MI355X (gfx950) mixture-of-experts layer.
+ *
+ * This header is the drop-in boundary that replaces the Metal MoE passes of Hydra's
+ * HydraMetal module behind the HydraCore layer interface. Plain C: no C++ types, no torch
+ * types, caller-owned device pointers, int status codes.
+ *
+ * Conventions
+ *   - Every function returns HH_OK (0) or a negative HH_E* code, and never aborts.
+ *     hh_last_error() returns a human-readable message for the calling thread.
+ *   - Tensors are device pointers from hipMalloc (or any allocation the HIP device can read).
+ *     Weight blobs follow the reference's expert blob layout byte for byte
+ *     (Sources/HydraCore/ExpertBlobLayout.swift:78-103 MXFP4, :127-143 BF16, :193-223 MLX);
+ *     hh_expert_blob_layout() returns the sub-tensor offsets.
+ *   - One hh_ctx owns one HIP stream (the "serial encoder" of the reference,
+ *     Sources/HydraMetal/MetalContext.swift:139-178). Work is enqueued in call order and no
+ *     entry point synchronises the host except hh_ctx_synchronize().
+ *   - bf16 values are passed as uint16_t bit patterns (little endian), fp32 as float.
+ *
+ * Enumerations keep the same numeric values in the fp64 oracle under oracle/.
+ */
+#ifndef HYDRA_HIP_H
+#define HYDRA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------------------------- */
+#define HH_OK        0
+#define HH_EINVAL   -1  /* a dimension or enum is out of range, or a required pointer is NULL */
+#define HH_EALIGN   -2  /* a pointer or dimension breaks an alignment the kernels rely on */
+#define HH_ETOPK    -3  /* top_k outside 1..8 or above the expert count */
+#define HH_EHIP     -4  /* a HIP runtime call failed; hh_last_error() has the HIP message */
+#define HH_ENOMEM   -5  /* the context could not allocate its scratch arena */
+#define HH_ESHAPE   -6  /* a dimension is not a multiple the format requires */
+
+/* ---- enumerations ---------------------------------------------------------------------- */
+/* Expert weight format. Also fixes how gate and up are stored:
+ *   MXFP4: one fused gate_up matrix [2I][H], rows interleaved gate0, up0, gate1, ...
+ *          (Sources/HydraReference/ReferenceLayer.swift:11; ReferenceOps.swift:81-82)
+ *   BF16 : one fused gate_up matrix [2I][H], gate = rows 0..I-1, up = rows I..2I-1
+ *          (Sources/HydraMetal/Gemma4Weights.swift:107-112)
+ *   MLX4/MLX8: separate gate [I][H], up [I][H] and down [H][I] affine matrices
+ *          (Sources/HydraCore/ExpertBlobLayout.swift:163-224)                                   */
+typedef enum { HH_QUANT_MXFP4 = 0, HH_QUANT_MLX4 = 1, HH_QUANT_MLX8 = 2, HH_QUANT_BF16 = 3 } hh_quant;
+
+/* Gated activation applied to (gate, up):
+ *   SWIGLU_OAI: g=min(g,limit), u=clamp(u,±limit), g·σ(alpha·g)·(u+1)  (ReferenceOps.swift:87-99)
+ *   SILU      : g·σ(g)·u                                              (QwenReferenceOps.swift:149-151)
+ *   GELU_TANH : 0.5·g·(1+tanh(√(2/π)(g+0.044715g³)))·u               (Gemma4ReferenceOps.swift:37-45) */
+typedef enum { HH_ACT_SWIGLU_OAI = 0, HH_ACT_SILU = 1, HH_ACT_GELU_TANH = 2 } hh_act;
+
+/* Router convention:
+ *   TOPK_SOFTMAX        : top-k of the logits, softmax over the k      (ReferenceOps.swift:173-183)
+ *   SOFTMAX_TOPK_RENORM : softmax over all, top-k, renormalise        (QwenReferenceOps.swift:159-179)
+ *   GEMMA               : unscaled RMSNorm·scale·H^-½ → logits → softmax → top-k → renormalise
+ *                         → × per-expert scale                          (Gemma4ReferenceOps.swift:131-156)
+ * Ties select the smaller expert index in every convention.                                 */
+typedef enum { HH_ROUTER_TOPK_SOFTMAX = 0, HH_ROUTER_SOFTMAX_TOPK_RENORM = 1, HH_ROUTER_GEMMA = 2 } hh_router;
+
+/* ---- layer description ----------------------------------------------------------------- */
+/* Mirrors the hot-path fields of HydraCore's GptOssConfig (GptOssConfig.swift:60-86),
+ * Qwen35MoeConfig (Qwen35MoeConfig.swift:73-128) and Gemma4Config (Gemma4Config.swift:73-77). */
+typedef struct hh_moe_desc {
+    int32_t hidden;              /* H: multiple of 64                                          */
+    int32_t intermediate;        /* I: expert intermediate, multiple of 64                      */
+    int32_t experts;             /* E: 1..512                                                   */
+    int32_t top_k;               /* K: 1..8 (the reference's maxRouterTopK, ForwardEncoder.swift:133) */
+    int32_t shared_intermediate; /* 0 = no shared expert; else the shared expert's I            */
+    int32_t quant;               /* hh_quant                                                    */
+    int32_t group_size;          /* MLX affine group (64); ignored otherwise                   */
+    int32_t activation;          /* hh_act                                                      */
+    int32_t router;              /* hh_router                                                   */
+    int32_t expert_bias;         /* 1: MXFP4 blobs carry bf16 gate_up and down biases (GPT-OSS) */
+    float   swiglu_alpha;        /* 1.702 for GPT-OSS                                           */
+    float   swiglu_limit;        /* 7.0 for GPT-OSS                                             */
+    float   router_eps;          /* RMSNorm epsilon of the GEMMA router (1e-6)                  */
+} hh_moe_desc;
+
+/* Device pointers to the layer's weights. */
+typedef struct hh_moe_weights {
+    const void *experts;             /* E expert blobs, reference blob layout for desc->quant  */
+    size_t      expert_stride;       /* bytes between blobs; 0 = the reference stride (16 KiB aligned) */
+    const void *shared_expert;       /* one blob of shared_intermediate, same format, or NULL   */
+    const uint16_t *router_weight;   /* bf16 [E][H]                                             */
+    const uint16_t *router_bias;     /* bf16 [E] or NULL (GPT-OSS router bias)                  */
+    const uint16_t *router_scale;    /* bf16 [H], GEMMA router only                             */
+    const uint16_t *router_expert_scale; /* bf16 [E], GEMMA router only                         */
+    const uint16_t *shared_gate;     /* bf16 [H]: the shared expert's sigmoid gate row          */
+} hh_moe_weights;
+
+/* Byte layout of one expert blob (offsets from the blob start). Slots in consumption order:
+ *   MXFP4: gate_up blocks, gate_up scales, gate_up bias, down blocks, down scales, down bias
+ *   BF16 : gate_up, down
+ *   MLX  : gate words, gate scales, gate biases, up words/scales/biases, down words/scales/biases */
+typedef struct hh_blob_layout {
+    int32_t slot_count;
+    size_t  offset[9];
+    size_t  bytes[9];
+    size_t  payload_bytes;   /* end of the last slot                                            */
+    size_t  stride_bytes;    /* payload rounded up to 16 KiB                                     */
+} hh_blob_layout;
+
+typedef struct hh_ctx hh_ctx;
+
+/* ---- context ----------------------------------------------------------------------------- */
+/* Replaces MetalContext (Sources/HydraMetal/MetalContext.swift:44-70): binds device `device`
+ * and creates one default-priority stream owned by the context.                              */
+int hh_ctx_create(hh_ctx **out, int32_t device);
+int hh_ctx_destroy(hh_ctx *ctx);
+/* The context's stream as a hipStream_t (opaque here). */
+void *hh_ctx_stream(hh_ctx *ctx);
+/* Waits for every enqueued call; the analogue of MetalContext.wait (MetalContext.swift:191-202),
+ * which reports a failed command buffer instead of returning silent zeros.                   */
+int hh_ctx_synchronize(hh_ctx *ctx);
+/* Pre-sizes the scratch arena for up to max_tokens tokens of layers shaped like `desc`, so
+ * that later hh_moe_forward calls within that bound allocate nothing (the reference's
+ * preallocated scratch, LayerRunner.swift:6-10).                                             */
+int hh_ctx_reserve(hh_ctx *ctx, const hh_moe_desc *desc, int32_t max_tokens);
+/* Kernel launches issued through this context since creation (the DispatchCounter analogue,
+ * ForwardEncoder.swift:34-68).                                                               */
+int64_t hh_dispatch_count(const hh_ctx *ctx);
+const char *hh_last_error(void);
+
+/* ---- description helpers ------------------------------------------------------------------ */
+/* Validates a description; HH_OK or the code hh_moe_forward would return for it.             */
+int hh_desc_check(const hh_moe_desc *desc);
+/* Blob layout for an expert of `intermediate` rows under desc's format (pass desc->intermediate
+ * for routed experts, desc->shared_intermediate for the shared one).                          */
+int hh_expert_blob_layout(const hh_moe_desc *desc, int32_t intermediate, hh_blob_layout *out);
+
+/* ---- the layer ----------------------------------------------------------------------------- */
+/* One MoE layer over T tokens, entirely on device with no host synchronisation:
+ * router logits → top-k weights → dispatch/permutation → gate-up product + activation →
+ * down product → rank-ordered weighted combine (+ sigmoid-gated shared expert).
+ *
+ * Replaces, as one call, LayerRunner.encodeAttentionAndRouter's router half, selectedExperts,
+ * encodeSingleExpert ×K and encodeCombineSlices (LayerRunner.swift:130-301) for decode, and
+ * PrefillRunner.encodeExpert (PrefillRunner.swift:252-302), QwenMixtureBlock
+ * .encodeRouterAndShared/encodeExperts/encodeCombine (QwenMixtureBlock.swift:122-263) and
+ * Gemma4LayerRunner.encodeSingleExpert/encodeExpertGroup (Gemma4LayerRunner.swift:579-677)
+ * for the other families. Semantics follow ReferenceLayer.swift:189-204,
+ * QwenReferenceLayer.swift:387-405 and Gemma4ReferenceLayer.swift:188-204.
+ *
+ *   x        bf16 [T][H]   the expert (and, unless x_router is given, router) input
+ *   x_router bf16 [T][H]   router input, or NULL for x (Gemma routes on the residual)
+ *   y        fp32 [T][H]   the mixture's contribution; the caller adds the residual
+ *   topk_idx int32 [T][K]  selected experts in rank order, or NULL
+ *   topk_w   fp32 [T][K]   their weights, or NULL
+ *
+ * A token's result does not depend on T or on the other tokens in the call: a T-token call
+ * equals T one-token calls bit for bit.                                                      */
+int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *desc, const hh_moe_weights *w,
+                   const uint16_t *x, const uint16_t *x_router, int32_t tokens,
+                   float *y, int32_t *topk_idx, float *topk_w);
+
+/* ---- operator-level entry points (parity tests mirror the encoder passes) ----------------- */
+/* MXFP4 → fp32 (MXFP4.swift:67-99; GPU mxfp4_dequantize, mxfp4.metal:25). `blocks` is
+ * nblocks×16 bytes, `scales` nblocks bytes, `out` nblocks×32 floats. Uses the same decode
+ * the expert products use.                                                                    */
+int hh_mxfp4_dequant(hh_ctx *ctx, const uint8_t *blocks, const uint8_t *scales,
+                     int64_t nblocks, float *out);
+/* MLX affine → fp32, value = fma(q, scale, bias) (Gemma4ReferenceOps.swift:196-221).
+ * words uint32 [rows][cols/(32/bits)], scales/biases bf16 [rows][cols/group].               */
+int hh_mlx_dequant(hh_ctx *ctx, const uint32_t *words, const uint16_t *scales,
+                   const uint16_t *biases, int32_t rows, int32_t cols, int32_t bits,
+                   int32_t group_size, float *out);
+/* Router only: logits (fp64 accumulation) → top-k → weights, per desc->router.
+ * Replaces routerTopK / routerTopKBatched / gemmaRouterTopK(Batched)
+ * (ForwardEncoder.swift:1183-1200, 1283-1323). logits may be NULL; shared_w (fp32 [T], the
+ * shared expert's sigmoid gate) may be NULL.                                                   */
+int hh_router_topk(hh_ctx *ctx, const hh_moe_desc *desc, const hh_moe_weights *w,
+                   const uint16_t *x_router, int32_t tokens, double *logits,
+                   int32_t *topk_idx, float *topk_w, float *shared_w);
+/* Gated activation on fp32 pairs (swiglu/qwen_silu_multiply/gelu_mul, attention.metal:81,
+ * qwen.metal:279, gemma.metal:77): out[i] = act(gate[i], up[i]) with the same device
+ * function the fused gate-up epilogue uses.                                                   */
+int hh_activation(hh_ctx *ctx, const hh_moe_desc *desc, const float *gate, const float *up,
+                  int64_t n, float *out);
+/* Token→expert permutation (PrefillRunner.assignments, PrefillRunner.swift:224-246, done on
+ * device): for topk_idx [T][K], writes seg_offsets int32 [E+1] and order int32 [T·K], the
+ * assignment ids t·K+r grouped by expert in ascending expert order, stable in (t, r).       */
+int hh_permute(hh_ctx *ctx, const int32_t *topk_idx, int32_t tokens, int32_t top_k,
+               int32_t experts, int32_t *seg_offsets, int32_t *order);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HYDRA_HIP_H */
