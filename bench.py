@@ -1,0 +1,272 @@
+"""Benchmark of the HydraHIP MoE layer on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Headline (`value`): GPT-OSS-20B-shaped MXFP4 MoE layer in decode at T=1 (BASELINE.json
+configs[1]), whole-layer tokens/s (router + top-k + dispatch + gate-up + SwiGLU + down +
+combine) with inputs already in HBM. A step is one layer over one token batch; steps cycle over
+several resident copies of the layer (> 256 MB Infinity Cache) and over a bank of inputs, so
+every step streams its experts from HBM as consecutive layers of a model would.
+
+Also reported: decode at T=2, 4, 8; the GPT-OSS-120B-shaped Zipf-skewed chunked prefill at
+T=512 and T=2048; the roofline of the dominant kernel (the gate-up expert
+product) from HIP events on the library's stream; and the fp64 CPU restatement of the
+reference path timed on this host.
+
+Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from hydra_amd import formats as F  # noqa: E402
+from hydra_amd import synth  # noqa: E402
+
+METRIC = "MoE-layer tokens/s at T=1 and T=512; % HBM GB/s (decode), % MFMA peak (prefill)"
+HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+MXFP4_MFMA_PEAK_TFLOPS = 10100.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def up_bytes(desc: F.MoEDesc) -> int:
+    """Algorithmic bytes of one expert's gate-up product: the gate_up tensors (blocks, scales
+    and, when used, bias)."""
+    lay = F.blob_layout(desc)
+    if desc.quant == F.QUANT_MXFP4:
+        return lay.sizes[0] + lay.sizes[1] + (lay.sizes[2] if desc.expert_bias else 0)
+    if desc.quant == F.QUANT_BF16:
+        return lay.sizes[0]
+    return sum(lay.sizes[:6])
+
+
+def flops_per_token(desc: F.MoEDesc) -> float:
+    H, I, K = desc.hidden, desc.intermediate, desc.top_k
+    f = 2.0 * K * (2 * I * H + H * I)
+    if desc.shared_intermediate:
+        f += 2.0 * 3 * desc.shared_intermediate * H
+    return f
+
+
+class Workload:
+    """`copies` resident copies of one synthetic layer and, per token count, a bank of token
+    batches already in HBM."""
+
+    def __init__(self, torch, desc, copies, zipf=None, seed=0):
+        from hydra_amd.layer import Context, MoELayer
+        self.torch, self.desc = torch, desc
+        t0 = time.time()
+        host = synth.make_layer(desc, seed=seed, zipf=zipf)
+        log(f"{desc.experts}x{desc.hidden} layer generated in {time.time() - t0:.1f}s")
+        self.ctx = Context(0)
+        self.layer = MoELayer(host, self.ctx)
+        del host
+        self.copies = [self.layer.experts] + [self.layer.experts.clone() for _ in range(copies - 1)]
+        self.wc = [self.layer.weights_c(e) for e in self.copies]
+        torch.cuda.synchronize()
+
+    def prepare(self, T, bank):
+        from hydra_amd.layer import to_device
+        torch, dev = self.torch, "cuda:0"
+        self.T = T
+        self.bank = [to_device(synth.make_tokens(self.desc.hidden, T, seed=1000 + i), dev)
+                     for i in range(bank)]
+        self.y = torch.empty((T, self.desc.hidden), dtype=torch.float32, device=dev)
+        self.idx = torch.empty((bank, T, self.desc.top_k), dtype=torch.int32, device=dev)
+        self.w = torch.empty((T, self.desc.top_k), dtype=torch.float32, device=dev)
+        self.ctx.reserve(self.desc, T)
+        torch.cuda.synchronize()
+
+    def step(self, i):
+        b = i % len(self.bank)
+        self.layer.forward_into(self.bank[b], self.y, self.idx[b], self.w,
+                                weights_c=self.wc[i % len(self.wc)])
+
+    def run(self, steps, warmup):
+        torch = self.torch
+        for i in range(warmup):
+            self.step(i)
+        self.ctx.synchronize()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            self.step(i)
+        self.ctx.synchronize()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps
+
+    def profiled(self, steps):
+        """Per-phase mean ms from HIP events on the library stream, over `steps` steps."""
+        self.ctx.profile(True)
+        for i in range(steps):
+            self.step(i)
+        ms, calls = self.ctx.profile_read()
+        self.ctx.profile(False)
+        return [m / max(calls, 1) for m in ms]
+
+    def unique_experts(self):
+        """Mean distinct experts per step over the bank's routing."""
+        idx = self.idx.cpu().numpy()
+        return float(np.mean([np.unique(idx[i]).size for i in range(idx.shape[0])]))
+
+    def close(self):
+        self.copies = self.wc = self.bank = None
+        self.layer = None
+        self.ctx.close()
+        self.torch.cuda.empty_cache()
+
+
+def measure_decode(wl, T, steps, warmup):
+    desc = wl.desc
+    wl.prepare(T, bank=64)
+    sec = wl.run(steps, warmup)
+    phases = wl.profiled(min(steps, 200))
+    U = wl.unique_experts()
+    up_b = U * up_bytes(desc) + T * desc.hidden * 2
+    layer_b = U * F.streamed_expert_bytes(desc) + desc.experts * desc.hidden * 2
+    return {
+        "T": T, "tokens_per_s": T / sec, "ms_per_step": sec * 1e3,
+        "unique_experts": U, "phase_ms": dict(zip(["route", "gate_up", "down", "combine"], phases)),
+        "gate_up_GBps": up_b / (phases[1] * 1e-3) / 1e9,
+        "down_GBps": U * (F.streamed_expert_bytes(desc) - up_bytes(desc)) / (phases[2] * 1e-3) / 1e9,
+        "layer_GBps": layer_b / sec / 1e9,
+        "layer_hbm_frac": layer_b / sec / 1e9 / HBM_PEAK_GBS,
+        "up_bytes_per_launch": up_b,
+    }
+
+
+def measure_prefill(wl, T, steps, warmup):
+    desc = wl.desc
+    wl.prepare(T, bank=4)
+    sec = wl.run(steps, warmup)
+    phases = wl.profiled(min(steps, 20))
+    U = wl.unique_experts()
+    fl = flops_per_token(desc) * T
+    by = U * F.streamed_expert_bytes(desc)
+    t_exp = (phases[1] + phases[2]) * 1e-3
+    return {
+        "T": T, "tokens_per_s": T / sec, "ms_per_step": sec * 1e3, "unique_experts": U,
+        "phase_ms": dict(zip(["route", "gate_up", "down", "combine"], phases)),
+        "expert_TFLOPs": fl / t_exp / 1e12,
+        "mfma_frac_bf16": fl / t_exp / 1e12 / BF16_MFMA_PEAK_TFLOPS,
+        "mfma_frac_mxfp4": fl / t_exp / 1e12 / MXFP4_MFMA_PEAK_TFLOPS,
+        "expert_GBps": by / t_exp / 1e9,
+        "hbm_frac": by / t_exp / 1e9 / HBM_PEAK_GBS,
+    }
+
+
+def cpu_baseline(seconds=10.0):
+    """The fp64 restatement of the reference's CPU path (oracle/), GPT-OSS-20B shape
+    (configs[0]), timed on this host: T=16 tokens per call, OpenMP over rows."""
+    from oracle import oracle as O
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    layer = synth.make_layer(F.GPT_OSS_20B, seed=0)
+    x = synth.make_tokens(F.GPT_OSS_20B.hidden, 16, seed=0)
+    O.moe_forward(layer, x[:1], nthreads=threads)           # warm
+    done, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        O.moe_forward(layer, x, nthreads=threads)
+        done += 16
+    rate = done / (time.perf_counter() - t0)
+    t1 = time.perf_counter()
+    O.moe_forward(layer, x[:1], nthreads=1)
+    single = 1.0 / (time.perf_counter() - t1)
+    return {"value": rate, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"gpt-oss-20b MXFP4 MoE layer (BASELINE configs[0]), T=16 per call, "
+                      f"fp64 oracle with OpenMP over rows, {done} tokens in ~{seconds:.0f}s; "
+                      f"single-thread T=1: {single:.2f} tokens/s"}
+
+
+def load_traffic():
+    p = os.path.join(ROOT, "profiles", "traffic_gate_up_gptoss20b_T1.json")
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f)
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--copies", type=int, default=8, help="resident layer copies (decode)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--only-t1", action="store_true", help="decode T=1 only (for profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X only: this build has no multi-GPU path "
+              "(expert/tensor parallel sharding is design-only). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    from hydra_amd._lib import lib
+    lib()  # fail loudly if the HIP library is missing
+
+    decode = {}
+    wl = Workload(torch, F.GPT_OSS_20B, copies=args.copies)
+    for T in ([1] if args.only_t1 else [1, 2, 4, 8]):
+        log(f"decode T={T}")
+        steps = args.steps if T == 1 else max(100, args.steps // 4)
+        decode[T] = measure_decode(wl, T, steps, args.warmup if T == 1 else 10)
+    wl.close()
+    prefill = {}
+    if not args.no_prefill and not args.only_t1:
+        wl = Workload(torch, F.GPT_OSS_120B, copies=2, zipf=1.1)
+        for T in [512, 2048]:
+            log(f"prefill T={T}")
+            prefill[T] = measure_prefill(wl, T, 20 if T == 512 else 10, 3)
+        wl.close()
+    cpu = None if args.no_cpu else cpu_baseline()
+
+    d1 = decode[1]
+    achieved = d1["gate_up_GBps"]
+    out = {
+        "metric": METRIC,
+        "value": d1["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": d1["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "gpt-oss-20b-shaped MXFP4 MoE layer, decode T=1 (BASELINE configs[1])",
+                   "hidden": 2880, "intermediate": 2880, "experts": 32, "top_k": 4,
+                   "weights": "mxfp4 e2m1 + e8m0/32", "layer_copies": args.copies},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "expert_gemm gate-up (MXFP4, 16-token tile)",
+                     "bytes_per_launch": d1["up_bytes_per_launch"],
+                     "avg_launch_ms": d1["phase_ms"]["gate_up"]},
+        "cpu_baseline": cpu,
+        "decode": {str(T): v for T, v in decode.items()},
+        "prefill_gpt_oss_120b_zipf": {str(T): v for T, v in prefill.items()},
+    }
+    tr = load_traffic()
+    if tr is not None:
+        out["roofline"]["traffic"] = tr.get("bytes_per_launch")
+        out["roofline"]["traffic_source"] = "profiles/traffic_gate_up_gptoss20b_T1.json"
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

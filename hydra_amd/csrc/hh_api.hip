@@ -1,0 +1,493 @@
+// hh_api.hip — the C ABI of include/hydra_hip.h: context, validation, scratch arena and the
+// per-layer launch sequence (route → gate-up → down → combine), all on the context's stream.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "hh_common.hpp"
+#include "hydra_hip.h"
+
+namespace hh {
+hipError_t launch_route(const RouteArgs &a, hipStream_t s);
+hipError_t launch_permute(const RouteArgs &a, hipStream_t s);
+hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStream_t s);
+int gemm_rows_per_block(int nt);
+hipError_t launch_combine(const float *slot_out, int slots, int H, int T, float *y, hipStream_t s);
+hipError_t launch_mxfp4_dequant(const uint8_t *blocks, const uint8_t *scales, int64_t n,
+                                float *out, hipStream_t s);
+hipError_t launch_mlx_dequant(const uint32_t *words, const uint16_t *scales,
+                              const uint16_t *biases, int rows, int cols, int bits, int group,
+                              float *out, hipStream_t s);
+hipError_t launch_activation(int act, float alpha, float limit, const float *gate,
+                             const float *up, int64_t n, float *out, hipStream_t s);
+}  // namespace hh
+
+struct hh_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  uint8_t *arena = nullptr;
+  size_t arena_bytes = 0;
+  int64_t dispatches = 0;
+  // Profiling: a pool of events, five per profiled forward call (phase boundaries).
+  bool profile = false;
+  std::vector<hipEvent_t> events;
+  size_t events_used = 0;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, const std::string &msg) {
+  g_error = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+  return fail(HH_EHIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define HH_HIP(call)                                  \
+  do {                                                \
+    hipError_t e_ = (call);                           \
+    if (e_ != hipSuccess) return hip_fail(e_, #call); \
+  } while (0)
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+constexpr int kMaxTokens = 1 << 16;  // tokens per call
+
+// Scratch carve-up for T tokens of a layer shaped like d. All offsets 256-byte aligned.
+struct Scratch {
+  size_t lg64, topk_idx, topk_w, slot_w, seg, order, work, n_work, h_hi, h_lo, slot_out, total;
+  int slots, positions, ldh, max_work, tile_tokens, nt;
+};
+
+int token_tile_nt(const hh_moe_desc &d, int T) {
+  // One 16-token tile per work item while experts see a handful of tokens (decode), four
+  // (64 tokens) once batches are large enough for experts to fill them (prefill).
+  return (T >= 64) ? 4 : 1;
+}
+
+Scratch plan(const hh_moe_desc &d, int T) {
+  Scratch s{};
+  const int E = d.experts, K = d.top_k, H = d.hidden;
+  const bool shared = d.shared_intermediate > 0;
+  s.slots = K + (shared ? 1 : 0);
+  s.positions = T * K + (shared ? T : 0);
+  s.ldh = (int)align_up((size_t)std::max(d.intermediate, d.shared_intermediate), 64);
+  s.nt = token_tile_nt(d, T);
+  s.tile_tokens = 16 * s.nt;
+  const int A = T * K;
+  s.max_work = std::min(E, A) + (A + s.tile_tokens - 1) / s.tile_tokens +
+               (shared ? (T + s.tile_tokens - 1) / s.tile_tokens : 0);
+  size_t c = 0;
+  auto take = [&](size_t bytes) {
+    size_t o = c;
+    c = align_up(c + bytes, 256);
+    return o;
+  };
+  s.lg64 = take(sizeof(double) * (size_t)std::min(T, 16) * (E + 1));
+  s.topk_idx = take(sizeof(int32_t) * (size_t)A);
+  s.topk_w = take(sizeof(float) * (size_t)A);
+  s.slot_w = take(sizeof(float) * (size_t)T * s.slots);
+  s.seg = take(sizeof(int32_t) * (size_t)(E + 2));
+  s.order = take(sizeof(int32_t) * (size_t)s.positions);
+  s.work = take(sizeof(int4) * (size_t)s.max_work);
+  s.n_work = take(sizeof(int32_t));
+  s.h_hi = take(sizeof(uint16_t) * (size_t)s.positions * s.ldh);
+  s.h_lo = take(sizeof(uint16_t) * (size_t)s.positions * s.ldh);
+  s.slot_out = take(sizeof(float) * (size_t)T * s.slots * H);
+  s.total = c;
+  return s;
+}
+
+int ensure_arena(hh_ctx *ctx, size_t bytes) {
+  if (ctx->arena_bytes >= bytes) return HH_OK;
+  HH_HIP(hipSetDevice(ctx->device));
+  if (ctx->arena) {
+    HH_HIP(hipStreamSynchronize(ctx->stream));
+    HH_HIP(hipFree(ctx->arena));
+    ctx->arena = nullptr;
+    ctx->arena_bytes = 0;
+  }
+  void *p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess) return fail(HH_ENOMEM, "scratch arena allocation failed");
+  ctx->arena = (uint8_t *)p;
+  ctx->arena_bytes = bytes;
+  return HH_OK;
+}
+
+int check_desc(const hh_moe_desc *d) {
+  if (!d) return fail(HH_EINVAL, "desc is NULL");
+  if (d->hidden <= 0 || d->intermediate <= 0 || d->experts <= 0)
+    return fail(HH_EINVAL, "hidden, intermediate and experts must be positive");
+  if (d->experts > hh::kMaxExperts) return fail(HH_EINVAL, "at most 512 experts");
+  if (d->top_k < 1 || d->top_k > hh::kMaxTopK || d->top_k > d->experts)
+    return fail(HH_ETOPK, "top_k must be in 1..8 and at most the expert count");
+  if (d->quant < HH_QUANT_MXFP4 || d->quant > HH_QUANT_BF16) return fail(HH_EINVAL, "unknown quant");
+  if (d->activation < HH_ACT_SWIGLU_OAI || d->activation > HH_ACT_GELU_TANH)
+    return fail(HH_EINVAL, "unknown activation");
+  if (d->router < HH_ROUTER_TOPK_SOFTMAX || d->router > HH_ROUTER_GEMMA)
+    return fail(HH_EINVAL, "unknown router");
+  if (d->shared_intermediate < 0) return fail(HH_EINVAL, "negative shared_intermediate");
+  if (d->hidden % 64 || d->intermediate % 64 || d->shared_intermediate % 64)
+    return fail(HH_ESHAPE, "hidden, intermediate and shared_intermediate must be multiples of 64");
+  if ((d->quant == HH_QUANT_MLX4 || d->quant == HH_QUANT_MLX8) && d->group_size != 64)
+    return fail(HH_ESHAPE, "MLX affine layers must use group_size 64");
+  return HH_OK;
+}
+
+hh::RouteArgs route_args(const hh_moe_desc &d, const hh_moe_weights *w, uint8_t *base,
+                         const Scratch &s, const uint16_t *x, const uint16_t *xr, int T) {
+  hh::RouteArgs r{};
+  r.x = x;
+  r.xr = xr ? xr : x;
+  r.router_w = w ? w->router_weight : nullptr;
+  r.router_b = w ? w->router_bias : nullptr;
+  r.router_scale = w ? w->router_scale : nullptr;
+  r.router_pes = w ? w->router_expert_scale : nullptr;
+  r.shared_gate = (w && d.shared_intermediate > 0) ? w->shared_gate : nullptr;
+  r.tokens = T;
+  r.hidden = d.hidden;
+  r.experts = d.experts;
+  r.top_k = d.top_k;
+  r.slots = s.slots;
+  r.router = d.router;
+  r.tile_tokens = s.tile_tokens;
+  r.want_dispatch = 1;
+  r.eps = d.router_eps;
+  r.logits = nullptr;
+  r.lg64 = (double *)(base + s.lg64);
+  r.topk_idx = (int32_t *)(base + s.topk_idx);
+  r.topk_w = (float *)(base + s.topk_w);
+  r.slot_w = (float *)(base + s.slot_w);
+  r.shared_w = nullptr;
+  r.seg = (int32_t *)(base + s.seg);
+  r.order = (int32_t *)(base + s.order);
+  r.work = (int4 *)(base + s.work);
+  r.n_work = (int32_t *)(base + s.n_work);
+  r.max_work = s.max_work;
+  return r;
+}
+
+void fill_group(hh::ExpertGroup &g, const hh_moe_desc &d, const void *blobs, size_t stride,
+                int inter) {
+  hh_blob_layout lay;
+  hh_expert_blob_layout(&d, inter, &lay);
+  g.blobs = (const uint8_t *)blobs;
+  g.stride = stride ? stride : lay.stride_bytes;
+  g.inter = inter;
+  for (int i = 0; i < 9; ++i) g.off[i] = i < lay.slot_count ? lay.offset[i] : 0;
+}
+
+// Records the next phase-boundary event when profiling is on.
+int mark(hh_ctx *ctx) {
+  if (!ctx->profile) return HH_OK;
+  if (ctx->events_used == ctx->events.size()) {
+    hipEvent_t ev;
+    HH_HIP(hipEventCreate(&ev));
+    ctx->events.push_back(ev);
+  }
+  HH_HIP(hipEventRecord(ctx->events[ctx->events_used++], ctx->stream));
+  return HH_OK;
+}
+
+#define HH_MARK(ctx)              \
+  do {                            \
+    int rc_ = mark(ctx);          \
+    if (rc_) return rc_;          \
+  } while (0)
+
+}  // namespace
+
+extern "C" {
+
+const char *hh_last_error(void) { return g_error.c_str(); }
+
+int hh_ctx_create(hh_ctx **out, int32_t device) {
+  if (!out) return fail(HH_EINVAL, "out is NULL");
+  *out = nullptr;
+  int n = 0;
+  HH_HIP(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n) return fail(HH_EINVAL, "no such device");
+  HH_HIP(hipSetDevice(device));
+  hh_ctx *c = new hh_ctx();
+  c->device = device;
+  // Default priority, non-blocking with respect to the legacy default stream.
+  hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete c;
+    return hip_fail(e, "hipStreamCreateWithFlags");
+  }
+  *out = c;
+  return HH_OK;
+}
+
+int hh_ctx_destroy(hh_ctx *ctx) {
+  if (!ctx) return HH_OK;
+  hipSetDevice(ctx->device);
+  if (ctx->stream) hipStreamSynchronize(ctx->stream);
+  if (ctx->arena) hipFree(ctx->arena);
+  for (hipEvent_t ev : ctx->events) hipEventDestroy(ev);
+  if (ctx->stream) hipStreamDestroy(ctx->stream);
+  delete ctx;
+  return HH_OK;
+}
+
+void *hh_ctx_stream(hh_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int hh_ctx_synchronize(hh_ctx *ctx) {
+  if (!ctx) return fail(HH_EINVAL, "ctx is NULL");
+  HH_HIP(hipSetDevice(ctx->device));
+  HH_HIP(hipStreamSynchronize(ctx->stream));
+  return HH_OK;
+}
+
+int64_t hh_dispatch_count(const hh_ctx *ctx) { return ctx ? ctx->dispatches : 0; }
+
+int hh_ctx_profile(hh_ctx *ctx, int32_t enable) {
+  if (!ctx) return fail(HH_EINVAL, "ctx is NULL");
+  ctx->profile = enable != 0;
+  return HH_OK;
+}
+
+int hh_ctx_profile_read(hh_ctx *ctx, double *phase_ms, int64_t *calls) {
+  if (!ctx || !phase_ms || !calls) return fail(HH_EINVAL, "NULL argument");
+  HH_HIP(hipSetDevice(ctx->device));
+  HH_HIP(hipStreamSynchronize(ctx->stream));
+  for (int p = 0; p < 4; ++p) phase_ms[p] = 0.0;
+  const size_t n = ctx->events_used / 5;
+  for (size_t c = 0; c < n; ++c)
+    for (int p = 0; p < 4; ++p) {
+      float ms = 0.f;
+      HH_HIP(hipEventElapsedTime(&ms, ctx->events[5 * c + p], ctx->events[5 * c + p + 1]));
+      phase_ms[p] += ms;
+    }
+  *calls = (int64_t)n;
+  ctx->events_used = 0;
+  return HH_OK;
+}
+
+int hh_desc_check(const hh_moe_desc *desc) { return check_desc(desc); }
+
+int hh_expert_blob_layout(const hh_moe_desc *d, int32_t inter, hh_blob_layout *out) {
+  if (!d || !out) return fail(HH_EINVAL, "NULL argument");
+  const size_t H = (size_t)d->hidden, I = (size_t)inter;
+  size_t sizes[9];
+  int n;
+  // ExpertBlobLayout.swift:78-103 (MXFP4), :127-143 (BF16), :193-223 (MLX), with the
+  // MLXAffineLayout byte counts (MLXAffineLayout.swift:51-54).
+  if (d->quant == HH_QUANT_MXFP4) {
+    n = 6;
+    sizes[0] = 2 * I * (H / 32) * 16; sizes[1] = 2 * I * (H / 32); sizes[2] = 2 * I * 2;
+    sizes[3] = H * (I / 32) * 16;     sizes[4] = H * (I / 32);     sizes[5] = H * 2;
+  } else if (d->quant == HH_QUANT_BF16) {
+    n = 2;
+    sizes[0] = 2 * I * H * 2; sizes[1] = H * I * 2;
+  } else if (d->quant == HH_QUANT_MLX4 || d->quant == HH_QUANT_MLX8) {
+    const size_t bits = d->quant == HH_QUANT_MLX4 ? 4 : 8, g = (size_t)d->group_size;
+    if (g == 0) return fail(HH_EINVAL, "group_size is 0");
+    n = 9;
+    const size_t gw = I * H * bits / 8, gs = I * (H / g) * 2, dw = H * I * bits / 8, ds = H * (I / g) * 2;
+    sizes[0] = gw; sizes[1] = gs; sizes[2] = gs;
+    sizes[3] = gw; sizes[4] = gs; sizes[5] = gs;
+    sizes[6] = dw; sizes[7] = ds; sizes[8] = ds;
+  } else {
+    return fail(HH_EINVAL, "unknown quant");
+  }
+  size_t cursor = 0;
+  out->slot_count = n;
+  for (int i = 0; i < 9; ++i) {
+    if (i < n) {
+      cursor = align_up(cursor, 256);
+      out->offset[i] = cursor;
+      out->bytes[i] = sizes[i];
+      cursor += sizes[i];
+    } else {
+      out->offset[i] = out->bytes[i] = 0;
+    }
+  }
+  out->payload_bytes = cursor;
+  out->stride_bytes = align_up(cursor, 16384);
+  return HH_OK;
+}
+
+int hh_ctx_reserve(hh_ctx *ctx, const hh_moe_desc *d, int32_t max_tokens) {
+  if (!ctx) return fail(HH_EINVAL, "ctx is NULL");
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (max_tokens <= 0 || max_tokens > kMaxTokens) return fail(HH_EINVAL, "max_tokens outside 1..65536");
+  // The plan for a batch that switches to 64-token tiles can be smaller than for a batch just
+  // below the switch; reserve the larger of the two.
+  size_t need = plan(*d, max_tokens).total;
+  if (max_tokens >= 64) need = std::max(need, plan(*d, 63).total);
+  return ensure_arena(ctx, need);
+}
+
+int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
+                   const uint16_t *x, const uint16_t *x_router, int32_t T, float *y,
+                   int32_t *topk_idx, float *topk_w) {
+  if (!ctx) return fail(HH_EINVAL, "ctx is NULL");
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (!w || !w->experts || !w->router_weight || !x || !y)
+    return fail(HH_EINVAL, "experts, router_weight, x and y are required");
+  if (d->router == HH_ROUTER_GEMMA && (!w->router_scale || !w->router_expert_scale))
+    return fail(HH_EINVAL, "the GEMMA router needs router_scale and router_expert_scale");
+  if (d->shared_intermediate > 0 && (!w->shared_expert || !w->shared_gate))
+    return fail(HH_EINVAL, "a shared expert needs shared_expert and shared_gate");
+  if (T < 0 || T > kMaxTokens) return fail(HH_EINVAL, "token count outside 0..65536");
+  if (T == 0) return HH_OK;
+  if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)w->experts | (uintptr_t)w->router_weight |
+       (uintptr_t)(x_router ? x_router : x)) & 15)
+    return fail(HH_EALIGN, "x, x_router, y, experts and router_weight must be 16-byte aligned");
+  if (w->expert_stride % 256) return fail(HH_EALIGN, "expert_stride must be a multiple of 256");
+  if (w->shared_expert && ((uintptr_t)w->shared_expert & 255))
+    return fail(HH_EALIGN, "shared_expert must be 256-byte aligned");
+  if ((uintptr_t)w->experts & 255) return fail(HH_EALIGN, "experts must be 256-byte aligned");
+
+  HH_HIP(hipSetDevice(ctx->device));
+  const Scratch s = plan(*d, T);
+  rc = ensure_arena(ctx, s.total);
+  if (rc) return rc;
+  uint8_t *base = ctx->arena;
+
+  hh::RouteArgs r = route_args(*d, w, base, s, x, x_router, T);
+  if (topk_idx) r.topk_idx = topk_idx;
+  if (topk_w) r.topk_w = topk_w;
+  HH_MARK(ctx);
+  HH_HIP(hh::launch_route(r, ctx->stream));
+  HH_MARK(ctx);
+
+  hh::GemmArgs g{};
+  fill_group(g.grp[0], *d, w->experts, w->expert_stride, d->intermediate);
+  if (d->shared_intermediate > 0) fill_group(g.grp[1], *d, w->shared_expert, 0, d->shared_intermediate);
+  else g.grp[1] = g.grp[0];
+  g.hidden = d->hidden;
+  g.experts = d->experts;
+  g.top_k = d->top_k;
+  g.slots = s.slots;
+  g.quant = d->quant;
+  g.act = d->activation;
+  g.expert_bias = d->expert_bias;
+  g.group = d->group_size;
+  g.alpha = d->swiglu_alpha;
+  g.limit = d->swiglu_limit;
+  g.ldh = s.ldh;
+  g.max_work = s.max_work;
+  g.x = x;
+  g.order = r.order;
+  g.work = r.work;
+  g.n_work = r.n_work;
+  g.h_hi = (uint16_t *)(base + s.h_hi);
+  g.h_lo = (uint16_t *)(base + s.h_lo);
+  g.slot_w = r.slot_w;
+  g.slot_out = (float *)(base + s.slot_out);
+
+  const int rows = hh::gemm_rows_per_block(s.nt);
+  g.row_tiles = (s.ldh + rows - 1) / rows;
+  HH_HIP(hh::launch_gemm(0, d->quant, s.nt, g, ctx->stream));
+  HH_MARK(ctx);
+  g.row_tiles = (d->hidden + rows - 1) / rows;
+  HH_HIP(hh::launch_gemm(1, d->quant, s.nt, g, ctx->stream));
+  HH_MARK(ctx);
+  HH_HIP(hh::launch_combine(g.slot_out, s.slots, d->hidden, T, y, ctx->stream));
+  HH_MARK(ctx);
+  ctx->dispatches += 4;
+  return HH_OK;
+}
+
+int hh_mxfp4_dequant(hh_ctx *ctx, const uint8_t *blocks, const uint8_t *scales, int64_t n,
+                     float *out) {
+  if (!ctx || !blocks || !scales || !out) return fail(HH_EINVAL, "NULL argument");
+  if (n < 0) return fail(HH_EINVAL, "negative block count");
+  if (((uintptr_t)blocks | (uintptr_t)out) & 15) return fail(HH_EALIGN, "blocks and out must be 16-byte aligned");
+  HH_HIP(hipSetDevice(ctx->device));
+  HH_HIP(hh::launch_mxfp4_dequant(blocks, scales, n, out, ctx->stream));
+  ctx->dispatches += 1;
+  return HH_OK;
+}
+
+int hh_mlx_dequant(hh_ctx *ctx, const uint32_t *words, const uint16_t *scales,
+                   const uint16_t *biases, int32_t rows, int32_t cols, int32_t bits,
+                   int32_t group, float *out) {
+  if (!ctx || !words || !scales || !biases || !out) return fail(HH_EINVAL, "NULL argument");
+  if (bits != 4 && bits != 8) return fail(HH_EINVAL, "bits must be 4 or 8");
+  if (rows < 0 || cols < 0 || group <= 0 || cols % group || group % (32 / bits))
+    return fail(HH_ESHAPE, "cols must divide into groups and groups into words");
+  HH_HIP(hipSetDevice(ctx->device));
+  HH_HIP(hh::launch_mlx_dequant(words, scales, biases, rows, cols, bits, group, out, ctx->stream));
+  ctx->dispatches += 1;
+  return HH_OK;
+}
+
+int hh_router_topk(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
+                   const uint16_t *x_router, int32_t T, double *logits, int32_t *topk_idx,
+                   float *topk_w, float *shared_w) {
+  if (!ctx) return fail(HH_EINVAL, "ctx is NULL");
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (!w || !w->router_weight || !x_router || !topk_idx || !topk_w)
+    return fail(HH_EINVAL, "router_weight, x_router, topk_idx and topk_w are required");
+  if (d->router == HH_ROUTER_GEMMA && (!w->router_scale || !w->router_expert_scale))
+    return fail(HH_EINVAL, "the GEMMA router needs router_scale and router_expert_scale");
+  if (((uintptr_t)x_router | (uintptr_t)w->router_weight) & 15)
+    return fail(HH_EALIGN, "x_router and router_weight must be 16-byte aligned");
+  if (T < 0 || T > kMaxTokens) return fail(HH_EINVAL, "token count outside 0..65536");
+  if (T == 0) return HH_OK;
+  HH_HIP(hipSetDevice(ctx->device));
+  const Scratch s = plan(*d, T);
+  rc = ensure_arena(ctx, s.total);
+  if (rc) return rc;
+  hh::RouteArgs r = route_args(*d, w, ctx->arena, s, x_router, x_router, T);
+  r.want_dispatch = 0;
+  r.logits = logits;
+  r.topk_idx = topk_idx;
+  r.topk_w = topk_w;
+  r.shared_w = shared_w;
+  if (d->shared_intermediate > 0 && !w->shared_gate) r.shared_gate = nullptr;
+  HH_HIP(hh::launch_route(r, ctx->stream));
+  ctx->dispatches += 1;
+  return HH_OK;
+}
+
+int hh_activation(hh_ctx *ctx, const hh_moe_desc *d, const float *gate, const float *up,
+                  int64_t n, float *out) {
+  if (!ctx || !d || !gate || !up || !out) return fail(HH_EINVAL, "NULL argument");
+  if (d->activation < HH_ACT_SWIGLU_OAI || d->activation > HH_ACT_GELU_TANH)
+    return fail(HH_EINVAL, "unknown activation");
+  HH_HIP(hipSetDevice(ctx->device));
+  HH_HIP(hh::launch_activation(d->activation, d->swiglu_alpha, d->swiglu_limit, gate, up, n,
+                               out, ctx->stream));
+  ctx->dispatches += 1;
+  return HH_OK;
+}
+
+int hh_permute(hh_ctx *ctx, const int32_t *topk_idx, int32_t T, int32_t K, int32_t E,
+               int32_t *seg_offsets, int32_t *order) {
+  if (!ctx || !topk_idx || !seg_offsets || !order) return fail(HH_EINVAL, "NULL argument");
+  if (E <= 0 || E > hh::kMaxExperts) return fail(HH_EINVAL, "experts must be in 1..512");
+  if (K < 1 || K > hh::kMaxTopK || K > E) return fail(HH_ETOPK, "top_k must be in 1..8");
+  if (T < 0 || T > kMaxTokens) return fail(HH_EINVAL, "token count outside 0..65536");
+  HH_HIP(hipSetDevice(ctx->device));
+  hh_moe_desc d{};
+  d.hidden = 64; d.intermediate = 64; d.experts = E; d.top_k = K;
+  const Scratch s = plan(d, std::max(T, 1));
+  int rc = ensure_arena(ctx, s.total);
+  if (rc) return rc;
+  hh::RouteArgs r = route_args(d, nullptr, ctx->arena, s, nullptr, nullptr, T);
+  r.topk_idx = const_cast<int32_t *>(topk_idx);
+  r.order = order;
+  HH_HIP(hh::launch_permute(r, ctx->stream));
+  ctx->dispatches += 1;
+  HH_HIP(hipMemcpyAsync(seg_offsets, r.seg, sizeof(int32_t) * (E + 1), hipMemcpyDeviceToDevice,
+                        ctx->stream));
+  return HH_OK;
+}
+
+}  // extern "C"

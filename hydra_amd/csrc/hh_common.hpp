@@ -1,0 +1,122 @@
+// hh_common.hpp — shared device helpers and kernel argument blocks of HydraHIP (gfx950).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hh {
+
+enum Quant { Q_MXFP4 = 0, Q_MLX4 = 1, Q_MLX8 = 2, Q_BF16 = 3 };
+enum Act { A_SWIGLU_OAI = 0, A_SILU = 1, A_GELU_TANH = 2 };
+enum Router { R_TOPK_SOFTMAX = 0, R_SOFTMAX_TOPK_RENORM = 1, R_GEMMA = 2 };
+
+constexpr int kMaxTopK = 8;
+constexpr int kMaxExperts = 512;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---- bf16 (the reference's BF16.toFloat / fromFloat, BF16.swift:20-33) ----------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if (f != f) return (u >> 16) | 0x40u;
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// e8m0 scale byte → fp32 factor 2^(s-127), exactly (s = 0 is the subnormal 2^-127, s = 255 is
+// +inf as in the reference's exp2, MXFP4.swift:37-42).
+__device__ __forceinline__ float e8m0_to_f32(uint32_t s) {
+  return __uint_as_float(s == 0 ? 0x00400000u : (s << 23));
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4 &v) { return __builtin_bit_cast(bf16x8, v); }
+
+// 8 MXFP4 values (one dword, low nibble first) → 8 bf16 scaled by 2^(s-127). The values are
+// e2m1·2^k, exact in bf16.
+__device__ __forceinline__ bf16x8 mxfp4_to_bf16(uint32_t w, float scale) {
+  bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0);
+  bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1);
+  bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2);
+  bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3);
+  u32x4 r = {__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
+             __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3)};
+  return as_bf16x8(r);
+}
+
+// ---- gated activations (device twins of the oracle's act_pair) ------------------------------
+__device__ __forceinline__ float activate(int act, float g, float u, float alpha, float limit) {
+  if (act == A_SWIGLU_OAI) {
+    // ReferenceOps.swiglu (ReferenceOps.swift:87-99).
+    g = fminf(g, limit);
+    u = fminf(fmaxf(u, -limit), limit);
+    return g * (1.0f / (1.0f + expf(-alpha * g))) * (u + 1.0f);
+  }
+  if (act == A_SILU) {
+    // QwenReferenceOps.siluMultiply (QwenReferenceOps.swift:149-151).
+    return g * (1.0f / (1.0f + expf(-g))) * u;
+  }
+  // Gemma4ReferenceOps.gelu (Gemma4ReferenceOps.swift:37-40); the tanh argument is clamped to
+  // ±15 where tanh is 1 to within float precision (as gemma.metal:77-88 does) so a large gate
+  // cannot produce inf/inf.
+  float inner = 0.7978845608028654f * (g + 0.044715f * g * g * g);
+  inner = fminf(fmaxf(inner, -15.0f), 15.0f);
+  return 0.5f * g * (1.0f + tanhf(inner)) * u;
+}
+
+// ---- kernel argument blocks -----------------------------------------------------------------
+// One group of experts sharing a shape: [0] the routed experts, [1] the shared expert.
+struct ExpertGroup {
+  const uint8_t *blobs;   // blob of expert 0 of the group
+  uint64_t stride;        // bytes between consecutive blobs
+  int32_t inter;          // I of the group
+  int32_t pad;
+  uint64_t off[9];        // sub-tensor offsets inside a blob (reference blob layout)
+};
+
+struct GemmArgs {
+  ExpertGroup grp[2];
+  int32_t hidden, experts, top_k, slots;   // slots = top_k + (shared ? 1 : 0)
+  int32_t quant, act, expert_bias, group;
+  float alpha, limit;
+  int32_t ldh;                  // row stride (elements) of h_hi / h_lo; multiple of 64
+  int32_t max_work;             // grid rows of work items
+  int32_t row_tiles;            // workgroup row tiles along the output dimension
+  int32_t pad2;
+  const uint16_t *x;            // bf16 [T][H]
+  const int32_t *order;         // [positions] slot id (t·slots + r) of each permuted position
+  const int4 *work;             // [max_work] {expert (E = shared), pos0, n, 0}
+  const int32_t *n_work;        // device count of valid work items
+  uint16_t *h_hi, *h_lo;        // bf16 [positions][ldh]: activation, hi + lo split
+  const float *slot_w;          // fp32 [T·slots] routing weight of each slot
+  float *slot_out;              // fp32 [T·slots][H]
+};
+
+struct RouteArgs {
+  const uint16_t *x;            // bf16 [T][H] expert input (and shared-gate input)
+  const uint16_t *xr;           // bf16 [T][H] router input
+  const uint16_t *router_w;     // bf16 [E][H]
+  const uint16_t *router_b;     // bf16 [E] or null
+  const uint16_t *router_scale; // bf16 [H] (GEMMA)
+  const uint16_t *router_pes;   // bf16 [E] (GEMMA)
+  const uint16_t *shared_gate;  // bf16 [H] or null
+  int32_t tokens, hidden, experts, top_k, slots, router, tile_tokens, want_dispatch;
+  float eps;
+  double *logits;               // fp64 [T][K] exact logits of the selected experts, or null
+  double *lg64;                 // fp64 [T][E+1] scratch for T ≤ 16 (last column: shared gate)
+  int32_t *topk_idx;            // [T][K]
+  float *topk_w;                // [T][K]
+  float *slot_w;                // [T·slots]
+  float *shared_w;              // [T] or null
+  // dispatch outputs
+  int32_t *seg;                 // [E+2] segment offsets (routed experts, then shared)
+  int32_t *order;               // [positions]
+  int4 *work;                   // [max_work]
+  int32_t *n_work;              // [1]
+  int32_t max_work;
+};
+
+}  // namespace hh

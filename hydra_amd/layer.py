@@ -1,0 +1,131 @@
+"""Host-side MoE layer over the HydraHIP C ABI.
+
+`MoELayer` plays the part of the reference's layer runners for the MoE half of a layer
+(LayerRunner.encodeMixtureOfExperts, LayerRunner.swift:304-353; PrefillRunner.encodeExpert,
+PrefillRunner.swift:252-302; QwenMixtureBlock, QwenMixtureBlock.swift:122-263;
+Gemma4LayerRunner.encodeExpertGroup, Gemma4LayerRunner.swift:579-616): it owns the layer's
+weights resident in HBM and runs router → dispatch → experts → combine on device through
+`hh_moe_forward`, with no host synchronisation inside a call.
+
+PyTorch is used only to own device memory and to wrap the context's stream.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import torch
+
+from . import formats as F
+from ._lib import MoEWeightsC, check, desc_c, lib
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+class Context:
+    """One hh_ctx: a device, its stream and the scratch arena."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        check(lib().hh_ctx_create(C.byref(h), device))
+        self.handle = h
+        self.device = device
+        self.stream = torch.cuda.ExternalStream(lib().hh_ctx_stream(h), device=f"cuda:{device}")
+
+    def synchronize(self):
+        check(lib().hh_ctx_synchronize(self.handle))
+
+    def reserve(self, desc: F.MoEDesc, max_tokens: int):
+        d = desc_c(desc)
+        check(lib().hh_ctx_reserve(self.handle, C.byref(d), max_tokens))
+
+    def profile(self, enable: bool = True):
+        check(lib().hh_ctx_profile(self.handle, 1 if enable else 0))
+
+    def profile_read(self):
+        """(per-phase summed ms [route, gate-up, down, combine], profiled calls)."""
+        ms = (C.c_double * 4)()
+        calls = C.c_int64()
+        check(lib().hh_ctx_profile_read(self.handle, ms, C.byref(calls)))
+        return list(ms), calls.value
+
+    @property
+    def dispatches(self) -> int:
+        return lib().hh_dispatch_count(self.handle)
+
+    def close(self):
+        if self.handle:
+            lib().hh_ctx_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def to_device(a: np.ndarray | None, device) -> torch.Tensor | None:
+    """Host array → device tensor of the same bytes (bf16 bit patterns travel as int16)."""
+    if a is None:
+        return None
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    elif a.dtype == np.uint32:
+        a = a.view(np.int32)
+    return torch.from_numpy(a).to(device)
+
+
+class MoELayer:
+    """One MoE layer with its weights in HBM, in the reference's expert blob layout."""
+
+    def __init__(self, layer: dict, ctx: Context | None = None, device: int = 0):
+        self.desc: F.MoEDesc = layer["desc"]
+        self.ctx = ctx or Context(device)
+        dev = torch.device(f"cuda:{self.ctx.device}")
+        torch.cuda.synchronize(dev)
+        self.experts = to_device(layer["experts"], dev)
+        self.expert_stride = int(layer["experts"].shape[1])
+        self.tensors = {k: to_device(layer.get(k), dev) for k in
+                        ["shared_expert", "router_weight", "router_bias", "router_scale",
+                         "router_expert_scale", "shared_gate"]}
+        torch.cuda.synchronize(dev)
+        self._desc_c = desc_c(self.desc)
+        self._weights_c = self.weights_c()
+
+    def weights_c(self, experts: torch.Tensor | None = None) -> MoEWeightsC:
+        t = self.tensors
+        ex = self.experts if experts is None else experts
+        return MoEWeightsC(ex.data_ptr(), self.expert_stride, _ptr(t["shared_expert"]),
+                           _ptr(t["router_weight"]), _ptr(t["router_bias"]),
+                           _ptr(t["router_scale"]), _ptr(t["router_expert_scale"]),
+                           _ptr(t["shared_gate"]))
+
+    def forward_into(self, x: torch.Tensor, y: torch.Tensor, idx: torch.Tensor | None = None,
+                     w: torch.Tensor | None = None, x_router: torch.Tensor | None = None,
+                     weights_c: MoEWeightsC | None = None) -> None:
+        """Enqueues the layer on the context's stream (no host synchronisation)."""
+        T = x.shape[0]
+        check(lib().hh_moe_forward(self.ctx.handle, C.byref(self._desc_c),
+                                   C.byref(weights_c or self._weights_c), _ptr(x),
+                                   _ptr(x_router), T, _ptr(y), _ptr(idx), _ptr(w)))
+
+    def forward(self, x, x_router=None):
+        """x: bf16 bits [T][H] (numpy uint16 or device int16). Returns (y fp32 [T][H],
+        top-k indices [T][K], top-k weights [T][K]) as device tensors, synchronised."""
+        dev = torch.device(f"cuda:{self.ctx.device}")
+        if isinstance(x, np.ndarray):
+            x = to_device(np.atleast_2d(x), dev)
+        if isinstance(x_router, np.ndarray):
+            x_router = to_device(np.atleast_2d(x_router), dev)
+        T = x.shape[0]
+        y = torch.empty((T, self.desc.hidden), dtype=torch.float32, device=dev)
+        idx = torch.empty((T, self.desc.top_k), dtype=torch.int32, device=dev)
+        w = torch.empty((T, self.desc.top_k), dtype=torch.float32, device=dev)
+        torch.cuda.synchronize(dev)
+        self.forward_into(x, y, idx, w, x_router)
+        self.ctx.synchronize()
+        return y, idx, w

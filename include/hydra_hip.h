@@ -125,6 +125,13 @@ int hh_ctx_reserve(hh_ctx *ctx, const hh_moe_desc *desc, int32_t max_tokens);
  * ForwardEncoder.swift:34-68).                                                               */
 int64_t hh_dispatch_count(const hh_ctx *ctx);
 const char *hh_last_error(void);
+/* Per-phase GPU timing with HIP events recorded on the context's stream around each kernel of
+ * hh_moe_forward (phase 0 route, 1 gate-up product, 2 down product, 3 combine): the
+ * reference's GPU start/end timing (Qwen35MoeRunner.swift:281) per pass. Off by default.
+ * hh_ctx_profile_read synchronises the stream, returns the summed milliseconds of each phase
+ * and the number of profiled forward calls, and clears the record.                           */
+int hh_ctx_profile(hh_ctx *ctx, int32_t enable);
+int hh_ctx_profile_read(hh_ctx *ctx, double *phase_ms /* [4] */, int64_t *calls);
 
 /* ---- description helpers ------------------------------------------------------------------ */
 /* Validates a description; HH_OK or the code hh_moe_forward would return for it.             */
@@ -169,10 +176,11 @@ int hh_mxfp4_dequant(hh_ctx *ctx, const uint8_t *blocks, const uint8_t *scales,
 int hh_mlx_dequant(hh_ctx *ctx, const uint32_t *words, const uint16_t *scales,
                    const uint16_t *biases, int32_t rows, int32_t cols, int32_t bits,
                    int32_t group_size, float *out);
-/* Router only: logits (fp64 accumulation) → top-k → weights, per desc->router.
- * Replaces routerTopK / routerTopKBatched / gemmaRouterTopK(Batched)
- * (ForwardEncoder.swift:1183-1200, 1283-1323). logits may be NULL; shared_w (fp32 [T], the
- * shared expert's sigmoid gate) may be NULL.                                                   */
+/* Router only: logits → top-k → weights, per desc->router, with top-k indices equal to those
+ * of fp64 logits. Replaces routerTopK / routerTopKBatched / gemmaRouterTopK(Batched)
+ * (ForwardEncoder.swift:1183-1200, 1283-1323). logits (fp64 [T][K], the selected experts'
+ * logits in rank order), and shared_w (fp32 [T], the shared expert's sigmoid gate) may be
+ * NULL.                                                                                        */
 int hh_router_topk(hh_ctx *ctx, const hh_moe_desc *desc, const hh_moe_weights *w,
                    const uint16_t *x_router, int32_t tokens, double *logits,
                    int32_t *topk_idx, float *topk_w, float *shared_w);

@@ -1,0 +1,372 @@
+"""GPU parity: the HIP path against the fp64 oracle and against itself.
+
+Bars: dequantisation and top-k indices bit-exact; layer output
+within rel-L2 1e-3 of the oracle (fp32 accumulation); a T-token call bit-identical to T
+one-token calls. Every test calls the library through its C ABI.
+"""
+import ctypes as C
+import os
+import sys
+
+import numpy as np
+import pytest
+
+from hydra_amd import formats as F
+from hydra_amd import synth
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 1e-3          # layer output tolerance (north_star)
+
+
+def say(msg):
+    print(f"[gpu] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need an MI355X"
+    return torch
+
+
+@pytest.fixture(scope="module")
+def ctx(torch_dev):
+    from hydra_amd.layer import Context
+    c = Context(0)
+    yield c
+    c.close()
+
+
+def rel_l2(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def dev(torch, a):
+    """Host array → device tensor, with torch's copy finished before the library's stream
+    (a different stream) reads it."""
+    from hydra_amd.layer import to_device
+    t = to_device(a, "cuda:0")
+    torch.cuda.synchronize()
+    return t
+
+
+def _p(t):
+    return C.c_void_p(t.data_ptr())
+
+
+# ---- dequantisation -------------------------------------------------------------------------
+
+def test_mxfp4_dequant_matches_reference_golden(torch_dev, ctx, golden_dir):
+    from hydra_amd._lib import check, lib
+    torch = torch_dev
+    say("mxfp4 dequant golden")
+    packed = np.fromfile(os.path.join(golden_dir, "mxfp4_packed.bin"), np.uint8)
+    scales = np.fromfile(os.path.join(golden_dir, "mxfp4_scales.bin"), np.uint8)
+    expected = np.fromfile(os.path.join(golden_dir, "mxfp4_expected.f32"), np.float32)
+    b, s = dev(torch, packed), dev(torch, scales)
+    out = torch.empty(expected.size, dtype=torch.float32, device="cuda:0")
+    check(lib().hh_mxfp4_dequant(ctx.handle, _p(b), _p(s), scales.size, _p(out)))
+    ctx.synchronize()
+    got = out.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), expected.view(np.uint32))
+
+
+def test_mxfp4_dequant_exhaustive_bytes_and_scales(torch_dev, ctx):
+    """Every packed byte under every e8m0 scale byte, bit for bit against the oracle."""
+    from hydra_amd._lib import check, lib
+    torch = torch_dev
+    say("mxfp4 dequant exhaustive")
+    packed = np.tile(np.arange(256, dtype=np.uint8), 256)          # 256 blocks of 16 → 16 per scale
+    scales = np.repeat(np.arange(256, dtype=np.uint8), 16)
+    exp = O.mxfp4_decode(packed, scales)
+    b, s = dev(torch, packed), dev(torch, scales)
+    out = torch.empty(exp.size, dtype=torch.float32, device="cuda:0")
+    check(lib().hh_mxfp4_dequant(ctx.handle, _p(b), _p(s), scales.size, _p(out)))
+    ctx.synchronize()
+    got = out.cpu().numpy()
+    both_nan = np.isnan(got) & np.isnan(exp)
+    same = (got.view(np.uint32) == exp.view(np.uint32)) | both_nan
+    bad = np.nonzero(~same)[0]
+    assert bad.size == 0, f"{bad.size} mismatches, first scale bytes {sorted(set(scales[bad // 32][:20].tolist()))}"
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_mlx_dequant_bit_exact(torch_dev, ctx, bits):
+    from hydra_amd._lib import check, lib
+    torch = torch_dev
+    say(f"mlx{bits} dequant")
+    rows, cols, group = 37, 512, 64
+    words = synth.u64(5, "w", rows * cols * bits // 64).view(np.uint32)
+    sc = synth.bf16_normal(5, "s", rows * cols // group, 0.01, 0.002)
+    bi = synth.f32_to_bf16(-7.5 * synth.bf16_to_f32(sc))
+    exp = np.stack([O.mlx_dequant(words.reshape(rows, -1)[r], synth.bf16_to_f32(sc.reshape(rows, -1)[r]),
+                                  synth.bf16_to_f32(bi.reshape(rows, -1)[r]), cols, bits, group)
+                    for r in range(rows)]).astype(np.float32)
+    out = torch.empty((rows, cols), dtype=torch.float32, device="cuda:0")
+    dw, ds, db = dev(torch, words), dev(torch, sc), dev(torch, bi)   # kept alive for the call
+    check(lib().hh_mlx_dequant(ctx.handle, _p(dw), _p(ds), _p(db), rows, cols, bits, group, _p(out)))
+    ctx.synchronize()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), exp.view(np.uint32))
+
+
+# ---- activation -----------------------------------------------------------------------------
+
+@pytest.mark.parametrize("act", [F.ACT_SWIGLU_OAI, F.ACT_SILU, F.ACT_GELU_TANH])
+def test_activation_matches_oracle(torch_dev, ctx, act):
+    from hydra_amd._lib import check, desc_c, lib
+    torch = torch_dev
+    say(f"activation {act}")
+    rng = np.random.default_rng(act)
+    g = np.concatenate([rng.normal(0, 3, 5000), [-20, -7.5, 0, 6.99, 7, 7.01, 30, 12, -12]]).astype(np.float32)
+    u = np.concatenate([rng.normal(0, 3, 5000), [1, -8, 2, 7.5, -7.5, 0.5, 8, 3, 3]]).astype(np.float32)
+    d = desc_c(F.GPT_OSS_20B.replace(activation=act))
+    out = torch.empty(g.size, dtype=torch.float32, device="cuda:0")
+    dg, du = dev(torch, g), dev(torch, u)   # kept alive for the call
+    check(lib().hh_activation(ctx.handle, C.byref(d), _p(dg), _p(du), g.size, _p(out)))
+    ctx.synchronize()
+    got = out.cpu().numpy().astype(np.float64)
+    if act == F.ACT_SWIGLU_OAI:
+        ref = np.array([O.swiglu([a, b])[0] for a, b in zip(g, u)])
+    elif act == F.ACT_SILU:
+        ref = np.array([O.silu(a) * b for a, b in zip(g, u)])
+    else:
+        ref = np.array([O.gelu_tanh(a) * b for a, b in zip(g, u)])
+    # fp32 bound: 2e-6 relative, plus the absolute rounding of 1 + tanh(·) (or of the sigmoid)
+    # near saturation, where the value is tiny and scales with |g|·|u|.
+    g64, u64 = g.astype(np.float64), u.astype(np.float64)
+    bound = 2e-6 * np.abs(ref) + 1e-7 * (np.abs(g64) + 1) * (np.abs(u64) + 1)
+    assert np.all(np.abs(got - ref) <= bound)
+
+
+# ---- router ---------------------------------------------------------------------------------
+
+ROUTER_CASES = {
+    "gpt-oss-20b": (F.GPT_OSS_20B, None),
+    "gpt-oss-120b-zipf": (F.GPT_OSS_120B, 1.1),
+    "qwen-q4": (F.QWEN_35B_A3B_Q4, None),
+    "gemma": (F.GEMMA_BF16, None),
+}
+
+
+@pytest.mark.parametrize("name", list(ROUTER_CASES))
+def test_router_indices_bit_exact(torch_dev, ctx, name):
+    from hydra_amd._lib import check, desc_c, lib
+    from hydra_amd.layer import MoELayer
+    torch = torch_dev
+    desc, zipf = ROUTER_CASES[name]
+    say(f"router {name}")
+    small = desc.replace(intermediate=64, shared_intermediate=64 if desc.shared_intermediate else 0)
+    layer = synth.make_layer(small, seed=21, zipf=zipf)
+    T = 96
+    x = synth.make_tokens(desc.hidden, T, seed=22)
+    L = MoELayer(layer, ctx)
+    d = desc_c(small)
+    idx = torch.empty((T, desc.top_k), dtype=torch.int32, device="cuda:0")
+    w = torch.empty((T, desc.top_k), dtype=torch.float32, device="cuda:0")
+    lg = torch.empty((T, desc.top_k), dtype=torch.float64, device="cuda:0")
+    xd = dev(torch, x)
+    torch.cuda.synchronize()
+    check(lib().hh_router_topk(ctx.handle, C.byref(d), C.byref(L._weights_c), _p(xd), T, _p(lg),
+                               _p(idx), _p(w), None))
+    ctx.synchronize()
+    ref_logits = O.router_logits(small, layer, x)
+    got_idx = idx.cpu().numpy()
+    sel = np.take_along_axis(ref_logits, got_idx.astype(np.int64), axis=1)
+    assert np.max(np.abs(lg.cpu().numpy() - sel)) < 1e-9
+    ridx = np.empty((T, desc.top_k), np.int64)
+    rw = np.empty((T, desc.top_k))
+    for t in range(T):
+        if small.router == F.ROUTER_TOPK_SOFTMAX:
+            i, ww = O.router_topk_softmax(ref_logits[t], desc.top_k)
+        else:
+            i, ww = O.router_softmax_topk_renorm(ref_logits[t], desc.top_k)
+            if small.router == F.ROUTER_GEMMA:
+                ww = ww * synth.bf16_to_f32(layer["router_expert_scale"])[i]
+        ridx[t], rw[t] = i, ww
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    assert np.max(np.abs(w.cpu().numpy() - rw)) < 1e-6
+
+
+def test_permute_is_stable_grouping(torch_dev, ctx):
+    from hydra_amd._lib import check, lib
+    torch = torch_dev
+    say("permute")
+    rng = np.random.default_rng(9)
+    for T, K, E in [(1, 4, 32), (7, 2, 5), (300, 8, 256), (2048, 4, 128), (1000, 8, 512)]:
+        topk = np.stack([rng.choice(E, K, replace=False) for _ in range(T)]).astype(np.int32)
+        seg = torch.empty(E + 1, dtype=torch.int32, device="cuda:0")
+        order = torch.empty(T * K, dtype=torch.int32, device="cuda:0")
+        ti = dev(torch, topk)
+        torch.cuda.synchronize()
+        check(lib().hh_permute(ctx.handle, _p(ti), T, K, E, _p(seg), _p(order)))
+        ctx.synchronize()
+        flat = topk.ravel()
+        exp_order = np.argsort(flat, kind="stable")
+        exp_seg = np.concatenate([[0], np.cumsum(np.bincount(flat, minlength=E))])
+        assert np.array_equal(order.cpu().numpy(), exp_order), (T, K, E)
+        assert np.array_equal(seg.cpu().numpy(), exp_seg), (T, K, E)
+
+
+# ---- the layer ------------------------------------------------------------------------------
+
+TINY = {
+    "mxfp4": F.MoEDesc(hidden=256, intermediate=128, experts=6, top_k=2, quant=F.QUANT_MXFP4,
+                       activation=F.ACT_SWIGLU_OAI, router=F.ROUTER_TOPK_SOFTMAX, expert_bias=1),
+    "mxfp4-ragged": F.MoEDesc(hidden=2880, intermediate=320, experts=5, top_k=3,
+                              quant=F.QUANT_MXFP4, activation=F.ACT_SWIGLU_OAI,
+                              router=F.ROUTER_TOPK_SOFTMAX, expert_bias=1),
+    "mlx4": F.MoEDesc(hidden=256, intermediate=128, experts=8, top_k=3, quant=F.QUANT_MLX4,
+                      activation=F.ACT_SILU, router=F.ROUTER_SOFTMAX_TOPK_RENORM,
+                      shared_intermediate=192, group_size=64),
+    "mlx8": F.MoEDesc(hidden=256, intermediate=192, experts=8, top_k=3, quant=F.QUANT_MLX8,
+                      activation=F.ACT_SILU, router=F.ROUTER_SOFTMAX_TOPK_RENORM,
+                      shared_intermediate=64, group_size=64),
+    "bf16": F.MoEDesc(hidden=320, intermediate=192, experts=5, top_k=2, quant=F.QUANT_BF16,
+                      activation=F.ACT_GELU_TANH, router=F.ROUTER_GEMMA),
+}
+
+
+@pytest.mark.parametrize("name", list(TINY))
+@pytest.mark.parametrize("T", [1, 5, 70])
+def test_layer_matches_oracle_small(torch_dev, ctx, name, T):
+    from hydra_amd.layer import MoELayer
+    desc = TINY[name]
+    say(f"layer {name} T={T}")
+    layer = synth.make_layer(desc, seed=31)
+    x = synth.make_tokens(desc.hidden, T, seed=32)
+    y, idx, w = MoELayer(layer, ctx).forward(x)
+    ry, ridx, rw, _ = O.moe_forward(layer, x)
+    assert np.array_equal(idx.cpu().numpy(), ridx)
+    assert np.max(np.abs(w.cpu().numpy() - rw)) < 1e-6
+    assert rel_l2(y.cpu().numpy(), ry) < REL_L2
+
+
+@pytest.mark.parametrize("name", list(TINY))
+def test_prefill_equals_token_by_token_bit_for_bit(torch_dev, ctx, name):
+    from hydra_amd.layer import MoELayer
+    desc = TINY[name]
+    say(f"prefill==decode {name}")
+    layer = synth.make_layer(desc, seed=41)
+    T = 80                                   # crosses the 64-token tile switch
+    x = synth.make_tokens(desc.hidden, T, seed=42)
+    L = MoELayer(layer, ctx)
+    y_all, idx_all, w_all = L.forward(x)
+    y_all = y_all.cpu().numpy()
+    for t in range(T):
+        y1, i1, w1 = L.forward(x[t:t + 1])
+        assert np.array_equal(i1.cpu().numpy()[0], idx_all.cpu().numpy()[t])
+        assert np.array_equal(y1.cpu().numpy()[0].view(np.uint32), y_all[t].view(np.uint32)), t
+    # chunked prefill: uneven chunks give the same bits too
+    parts = [L.forward(x[a:b])[0].cpu().numpy() for a, b in [(0, 3), (3, 67), (67, 80)]]
+    assert np.array_equal(np.concatenate(parts).view(np.uint32), y_all.view(np.uint32))
+
+
+def test_layer_is_deterministic_and_order_independent(torch_dev, ctx):
+    from hydra_amd.layer import MoELayer
+    desc = TINY["mxfp4"]
+    say("determinism")
+    layer = synth.make_layer(desc, seed=51)
+    x = synth.make_tokens(desc.hidden, 100, seed=52)
+    L = MoELayer(layer, ctx)
+    a = L.forward(x)[0].cpu().numpy()
+    b = L.forward(x)[0].cpu().numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    perm = np.random.default_rng(0).permutation(100)
+    c = L.forward(x[perm])[0].cpu().numpy()
+    assert np.array_equal(c.view(np.uint32), a[perm].view(np.uint32))
+
+
+# ---- real shapes ----------------------------------------------------------------------------
+
+FULL = {
+    "gpt-oss-20b": (F.GPT_OSS_20B, None, [1, 2, 4, 8]),
+    "gpt-oss-120b-zipf": (F.GPT_OSS_120B, 1.1, [512]),
+    "qwen-q4": (F.QWEN_35B_A3B_Q4, None, [1, 1024]),
+    "qwen-q8": (F.QWEN_35B_A3B_Q8, None, [1, 1024]),
+    "gemma-bf16": (F.GEMMA_BF16, None, [1, 2048]),
+}
+
+
+@pytest.mark.parametrize("name", list(FULL))
+def test_full_size_layers_against_oracle_sample(torch_dev, ctx, name):
+    """Each BASELINE configuration at its real shape: every token's top-k and a sample of
+    tokens' outputs against the oracle; the whole batch against token-by-token decode."""
+    from hydra_amd.layer import MoELayer
+    torch = torch_dev
+    desc, zipf, Ts = FULL[name]
+    say(f"full {name}: building layer")
+    layer = synth.make_layer(desc, seed=0, zipf=zipf)
+    L = MoELayer(layer, ctx)
+    for T in Ts:
+        say(f"full {name} T={T}")
+        x = synth.make_tokens(desc.hidden, T, seed=1)
+        y, idx, w = L.forward(x)
+        y = y.cpu().numpy()
+        idx = idx.cpu().numpy()
+        logits = O.router_logits(desc, layer, x)
+        for t in range(T):
+            if desc.router == F.ROUTER_TOPK_SOFTMAX:
+                ri, _ = O.router_topk_softmax(logits[t], desc.top_k)
+            else:
+                ri, _ = O.router_softmax_topk_renorm(logits[t], desc.top_k)
+            assert np.array_equal(idx[t], ri), t
+        sample = sorted(set([0, T - 1] + list(np.random.default_rng(T).choice(T, min(T, 3), replace=False))))
+        ry, _, _, _ = O.moe_forward(layer, x[sample], nthreads=min(16, os.cpu_count() or 1))
+        assert rel_l2(y[sample], ry) < REL_L2
+        # the batch equals one-token calls, bit for bit, on a sample of tokens
+        for t in sample:
+            y1 = L.forward(x[t:t + 1])[0].cpu().numpy()[0]
+            assert np.array_equal(y1.view(np.uint32), y[t].view(np.uint32)), (T, t)
+        if zipf:
+            counts = np.bincount(idx.ravel(), minlength=desc.experts)
+            assert counts.max() > 8 * max(1, np.median(counts))   # the load really is skewed
+    del L
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("router", [F.ROUTER_TOPK_SOFTMAX, F.ROUTER_SOFTMAX_TOPK_RENORM, F.ROUTER_GEMMA])
+def test_router_near_ties_resolved_exactly(torch_dev, ctx, router):
+    """Router rows that are exact duplicates (ties → smaller index) or differ by one ulp of a
+    tiny element (logits that fp32 cannot separate but fp64 can)."""
+    from hydra_amd._lib import check, desc_c, lib
+    from hydra_amd.layer import MoELayer
+    torch = torch_dev
+    say(f"router near ties {router}")
+    desc = F.MoEDesc(hidden=2880, intermediate=64, experts=32, top_k=4, quant=F.QUANT_MXFP4,
+                     activation=F.ACT_SWIGLU_OAI, router=router, expert_bias=0)
+    layer = synth.make_layer(desc, seed=61)
+    W = layer["router_weight"].copy()
+    W[:, 5] = synth.f32_to_bf16(np.float32(1e-7) * np.ones(32, np.float32))
+    for a_, b_ in [(3, 4), (10, 11), (20, 21)]:
+        W[b_] = W[a_]                         # exact duplicate
+    for a_, b_ in [(7, 8), (14, 15), (25, 26)]:
+        W[b_] = W[a_]
+        W[b_, 5] = W[a_, 5] + 1               # one ulp of a 1e-7 weight
+    # make the duplicated experts strong so they land in the top-k
+    for e in [3, 4, 7, 8, 10, 11, 14, 15, 20, 21, 25, 26]:
+        keep = W[e, 5]
+        W[e] = synth.f32_to_bf16(synth.bf16_to_f32(W[e]) * np.float32(1.5))
+        W[e, 5] = keep
+    layer["router_weight"] = W
+    T = 64
+    x = synth.make_tokens(desc.hidden, T, seed=62)
+    L = MoELayer(layer, ctx)
+    d = desc_c(desc)
+    idx = torch.empty((T, 4), dtype=torch.int32, device="cuda:0")
+    w = torch.empty((T, 4), dtype=torch.float32, device="cuda:0")
+    xd = dev(torch, x)
+    check(lib().hh_router_topk(ctx.handle, C.byref(d), C.byref(L._weights_c), _p(xd), T, None,
+                               _p(idx), _p(w), None))
+    ctx.synchronize()
+    ref_logits = O.router_logits(desc, layer, x)
+    got = idx.cpu().numpy()
+    for t in range(T):
+        if router == F.ROUTER_TOPK_SOFTMAX:
+            ri, _ = O.router_topk_softmax(ref_logits[t], 4)
+        else:
+            ri, _ = O.router_softmax_topk_renorm(ref_logits[t], 4)
+        assert np.array_equal(got[t], ri), (t, got[t], ri)
