@@ -206,6 +206,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--only-t1", action="store_true", help="decode T=1 only (for profiling)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run one 256 MiB device-to-device copy and exit (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X only: this build has no multi-GPU path "
@@ -215,6 +217,16 @@ def main():
 
     import torch
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.copy_calibration:
+        # A plain copy of known size: its FETCH_SIZE / WRITE_SIZE per dispatch should read
+        # 262144 KiB each; the ratio scales the counters of the expert kernels.
+        src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": 256 << 20}))
+        return
     from hydra_amd._lib import lib
     lib()  # fail loudly if the HIP library is missing
 

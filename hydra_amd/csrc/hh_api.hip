@@ -12,11 +12,12 @@
 #include "hydra_hip.h"
 
 namespace hh {
-hipError_t launch_route(const RouteArgs &a, hipStream_t s);
+hipError_t launch_route(const RouteArgs &a, hipStream_t s, Timing tm = {});
 hipError_t launch_permute(const RouteArgs &a, hipStream_t s);
-hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStream_t s);
-int gemm_rows_per_block(int nt);
-hipError_t launch_combine(const float *slot_out, int slots, int H, int T, float *y, hipStream_t s);
+hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStream_t s, Timing tm);
+int gemm_rows_per_block(int nt, int quant);
+hipError_t launch_combine(const float *slot_out, int slots, int H, int T, float *y, hipStream_t s,
+                          Timing tm);
 hipError_t launch_mxfp4_dequant(const uint8_t *blocks, const uint8_t *scales, int64_t n,
                                 float *out, hipStream_t s);
 hipError_t launch_mlx_dequant(const uint32_t *words, const uint16_t *scales,
@@ -32,7 +33,7 @@ struct hh_ctx {
   uint8_t *arena = nullptr;
   size_t arena_bytes = 0;
   int64_t dispatches = 0;
-  // Profiling: a pool of events, five per profiled forward call (phase boundaries).
+  // Profiling: a pool of events, a start/stop pair per phase of each profiled forward call.
   bool profile = false;
   std::vector<hipEvent_t> events;
   size_t events_used = 0;
@@ -68,9 +69,9 @@ struct Scratch {
 };
 
 int token_tile_nt(const hh_moe_desc &d, int T) {
-  // One 16-token tile per work item while experts see a handful of tokens (decode), four
-  // (64 tokens) once batches are large enough for experts to fill them (prefill).
-  return (T >= 64) ? 4 : 1;
+  // Decode kernel (16-token tiles) while experts see a handful of tokens, the prefill kernel
+  // (32-token tiles) once batches are large enough for experts to fill them.
+  return (T >= 64) ? 2 : 1;
 }
 
 Scratch plan(const hh_moe_desc &d, int T) {
@@ -185,23 +186,19 @@ void fill_group(hh::ExpertGroup &g, const hh_moe_desc &d, const void *blobs, siz
   for (int i = 0; i < 9; ++i) g.off[i] = i < lay.slot_count ? lay.offset[i] : 0;
 }
 
-// Records the next phase-boundary event when profiling is on.
-int mark(hh_ctx *ctx) {
+// The timing events of the next phase when profiling is on (none otherwise).
+int phase_timing(hh_ctx *ctx, hh::Timing *tm) {
+  *tm = hh::Timing{};
   if (!ctx->profile) return HH_OK;
-  if (ctx->events_used == ctx->events.size()) {
+  while (ctx->events_used + 2 > ctx->events.size()) {
     hipEvent_t ev;
     HH_HIP(hipEventCreate(&ev));
     ctx->events.push_back(ev);
   }
-  HH_HIP(hipEventRecord(ctx->events[ctx->events_used++], ctx->stream));
+  tm->start = ctx->events[ctx->events_used++];
+  tm->stop = ctx->events[ctx->events_used++];
   return HH_OK;
 }
-
-#define HH_MARK(ctx)              \
-  do {                            \
-    int rc_ = mark(ctx);          \
-    if (rc_) return rc_;          \
-  } while (0)
 
 }  // namespace
 
@@ -261,11 +258,11 @@ int hh_ctx_profile_read(hh_ctx *ctx, double *phase_ms, int64_t *calls) {
   HH_HIP(hipSetDevice(ctx->device));
   HH_HIP(hipStreamSynchronize(ctx->stream));
   for (int p = 0; p < 4; ++p) phase_ms[p] = 0.0;
-  const size_t n = ctx->events_used / 5;
+  const size_t n = ctx->events_used / 8;
   for (size_t c = 0; c < n; ++c)
     for (int p = 0; p < 4; ++p) {
       float ms = 0.f;
-      HH_HIP(hipEventElapsedTime(&ms, ctx->events[5 * c + p], ctx->events[5 * c + p + 1]));
+      HH_HIP(hipEventElapsedTime(&ms, ctx->events[8 * c + 2 * p], ctx->events[8 * c + 2 * p + 1]));
       phase_ms[p] += ms;
     }
   *calls = (int64_t)n;
@@ -360,9 +357,10 @@ int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
   hh::RouteArgs r = route_args(*d, w, base, s, x, x_router, T);
   if (topk_idx) r.topk_idx = topk_idx;
   if (topk_w) r.topk_w = topk_w;
-  HH_MARK(ctx);
-  HH_HIP(hh::launch_route(r, ctx->stream));
-  HH_MARK(ctx);
+  hh::Timing tm;
+  rc = phase_timing(ctx, &tm);
+  if (rc) return rc;
+  HH_HIP(hh::launch_route(r, ctx->stream, tm));
 
   hh::GemmArgs g{};
   fill_group(g.grp[0], *d, w->experts, w->expert_stride, d->intermediate);
@@ -389,15 +387,15 @@ int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
   g.slot_w = r.slot_w;
   g.slot_out = (float *)(base + s.slot_out);
 
-  const int rows = hh::gemm_rows_per_block(s.nt);
+  const int rows = hh::gemm_rows_per_block(s.nt, d->quant);
   g.row_tiles = (s.ldh + rows - 1) / rows;
-  HH_HIP(hh::launch_gemm(0, d->quant, s.nt, g, ctx->stream));
-  HH_MARK(ctx);
+  if ((rc = phase_timing(ctx, &tm))) return rc;
+  HH_HIP(hh::launch_gemm(0, d->quant, s.nt, g, ctx->stream, tm));
   g.row_tiles = (d->hidden + rows - 1) / rows;
-  HH_HIP(hh::launch_gemm(1, d->quant, s.nt, g, ctx->stream));
-  HH_MARK(ctx);
-  HH_HIP(hh::launch_combine(g.slot_out, s.slots, d->hidden, T, y, ctx->stream));
-  HH_MARK(ctx);
+  if ((rc = phase_timing(ctx, &tm))) return rc;
+  HH_HIP(hh::launch_gemm(1, d->quant, s.nt, g, ctx->stream, tm));
+  if ((rc = phase_timing(ctx, &tm))) return rc;
+  HH_HIP(hh::launch_combine(g.slot_out, s.slots, d->hidden, T, y, ctx->stream, tm));
   ctx->dispatches += 4;
   return HH_OK;
 }

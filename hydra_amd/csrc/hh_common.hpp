@@ -1,6 +1,7 @@
 // hh_common.hpp — shared device helpers and kernel argument blocks of HydraHIP (gfx950).
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 
 namespace hh {
@@ -117,6 +118,13 @@ struct RouteArgs {
   int4 *work;                   // [max_work]
   int32_t *n_work;              // [1]
   int32_t max_work;
+};
+
+// Optional profiling events of a launch sequence: `start` is attached to the first kernel's
+// dispatch packet and `stop` to the last one's (hipExtLaunchKernelGGL), so the interval covers
+// exactly the kernels' execution, as a kernel trace would. Null events launch normally.
+struct Timing {
+  hipEvent_t start = nullptr, stop = nullptr;
 };
 
 }  // namespace hh

@@ -150,6 +150,74 @@ __device__ __forceinline__ float sum8_bf16(const u32x4 &v) {
   return s;
 }
 
+// Σ of the group's 64 B values of one token column (x, or h_hi + h_lo) from the lane's 2×NH
+// vectors, in a fixed order (hi then lo per MFMA step, steps in order), then across the lane
+// groups. Shared by every kernel so the affine bias term is computed identically.
+template <int NH>
+__device__ __forceinline__ float group_sum(const u32x4 (&bv)[NH][2]) {
+  float v = 0.f;
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    v += sum8_bf16(bv[0][jj]);
+    if (NH > 1) v += sum8_bf16(bv[NH - 1][jj]);
+  }
+  return sum_lane_groups(v);
+}
+
+// The 4 K partials of an output element, summed in partial order.
+__device__ __forceinline__ f32x4 sum_partials4(const f32x4 &p0, const f32x4 &p1, const f32x4 &p2,
+                                               const f32x4 &p3) {
+  f32x4 r;
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) r[ii] = ((p0[ii] + p1[ii]) + p2[ii]) + p3[ii];
+  return r;
+}
+
+// Gate-up epilogue of 4 intermediates i0..i0+3 of position `pos`: bias, activation, bf16 hi/lo.
+template <int FMT>
+__device__ __forceinline__ void up_epilogue(const GemmArgs &a, const uint8_t *blob,
+                                            const ExpertGroup &grp, int i0, int pos,
+                                            const f32x4 &gate, const f32x4 &up) {
+  float gb[4] = {0.f, 0.f, 0.f, 0.f}, ub[4] = {0.f, 0.f, 0.f, 0.f};
+  if (FMT == Q_MXFP4 && a.expert_bias) {
+    const uint16_t *bias = (const uint16_t *)(blob + grp.off[2]);
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      gb[ii] = bf16_bits_to_f32(bias[2 * (i0 + ii)]);
+      ub[ii] = bf16_bits_to_f32(bias[2 * (i0 + ii) + 1]);
+    }
+  }
+  uint32_t hi[4], lo[4];
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) {
+    const float y = activate(a.act, gate[ii] + gb[ii], up[ii] + ub[ii], a.alpha, a.limit);
+    hi[ii] = f32_to_bf16_bits(y);
+    lo[ii] = f32_to_bf16_bits(y - bf16_bits_to_f32(hi[ii]));
+  }
+  const size_t o = (size_t)pos * a.ldh + i0;
+  *(u32x2 *)(a.h_hi + o) = u32x2{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
+  *(u32x2 *)(a.h_lo + o) = u32x2{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
+}
+
+// Down epilogue of hidden rows h0..h0+3 of position `pos`: bias, routing weight, slot store.
+template <int FMT>
+__device__ __forceinline__ void down_epilogue(const GemmArgs &a, const uint8_t *blob,
+                                              const ExpertGroup &grp, int h0, int pos,
+                                              const f32x4 &r) {
+  const int slot_id = a.order[pos];
+  const float w = a.slot_w[slot_id];
+  float db[4] = {0.f, 0.f, 0.f, 0.f};
+  if (FMT == Q_MXFP4 && a.expert_bias) {
+    const uint16_t *bias = (const uint16_t *)(blob + grp.off[5]);
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) db[ii] = bf16_bits_to_f32(bias[h0 + ii]);
+  }
+  f32x4 o;
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) o[ii] = w * (r[ii] + db[ii]);
+  *(f32x4 *)(a.slot_out + (size_t)slot_id * a.hidden + h0) = o;
+}
+
 // KS = K partials per output element: partial p accumulates chunks c ≡ p (mod KS) in increasing
 // order and the partials are summed in p order. The workgroup's 4 waves are 4/KS row groups ×
 // KS partials. Every variant used on one layer shares KS, so a token's result does not depend
@@ -352,17 +420,10 @@ __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
         float gsum[NT];
 #pragma unroll
         for (int st = 0; st < NT; ++st) {
-          float v = 0.f;
+          u32x4 gb2[NH][2];
 #pragma unroll
-          for (int jj = 0; jj < 2; ++jj) {
-            if (NH == 1) {
-              v += sum8_bf16(sbv.bv[st][0][jj]);
-            } else {
-              v += sum8_bf16(sbv.bv[st][0][jj]);
-              v += sum8_bf16(sbv.bv[st][NH - 1][jj]);
-            }
-          }
-          gsum[st] = sum_lane_groups(v);
+          for (int hh = 0; hh < NH; ++hh) { gb2[hh][0] = sbv.bv[st][hh][0]; gb2[hh][1] = sbv.bv[st][hh][1]; }
+          gsum[st] = group_sum<NH>(gb2);
         }
         // acc += s·P + b·Σ per D row (affine factorisation, gemma.metal:234-236).
 #pragma unroll
@@ -435,52 +496,260 @@ __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
         }
       }
       if (j >= ntok) continue;
-      if constexpr (PH == PH_UP) {
 #pragma unroll
-        for (int q = 0; q < RT; ++q) {
-          if (rb + 16 * q >= out_dim) continue;
-          const int i0 = rb + 16 * q + 4 * g;    // first of this lane's 4 intermediates
-          float gb[4] = {0.f, 0.f, 0.f, 0.f}, ub[4] = {0.f, 0.f, 0.f, 0.f};
-          if (FMT == Q_MXFP4 && a.expert_bias) {
-            const uint16_t *bias = (const uint16_t *)(blob + grp.off[2]);
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii) {
-              gb[ii] = bf16_bits_to_f32(bias[2 * (i0 + ii)]);
-              ub[ii] = bf16_bits_to_f32(bias[2 * (i0 + ii) + 1]);
-            }
-          }
-          uint32_t hi[4], lo[4];
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) {
-            const float y = activate(a.act, r[q][ii] + gb[ii], r[RT + q][ii] + ub[ii], a.alpha, a.limit);
-            hi[ii] = f32_to_bf16_bits(y);
-            lo[ii] = f32_to_bf16_bits(y - bf16_bits_to_f32(hi[ii]));
-          }
-          const size_t o = (size_t)bpos[st] * a.ldh + i0;
-          *(u32x2 *)(a.h_hi + o) = u32x2{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
-          *(u32x2 *)(a.h_lo + o) = u32x2{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
-        }
-      } else {
-        const int slot_id = a.order[bpos[st]];
-        const float w = a.slot_w[slot_id];
-#pragma unroll
-        for (int q = 0; q < RT; ++q) {
-          if (rb + 16 * q >= out_dim) continue;
-          const int h0 = rb + 16 * q + 4 * g;
-          float db[4] = {0.f, 0.f, 0.f, 0.f};
-          if (FMT == Q_MXFP4 && a.expert_bias) {
-            const uint16_t *bias = (const uint16_t *)(blob + grp.off[5]);
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii) db[ii] = bf16_bits_to_f32(bias[h0 + ii]);
-          }
-          f32x4 o;
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) o[ii] = w * (r[q][ii] + db[ii]);
-          *(f32x4 *)(a.slot_out + (size_t)slot_id * H + h0) = o;
-        }
+      for (int q = 0; q < RT; ++q) {
+        if (rb + 16 * q >= out_dim) continue;
+        if constexpr (PH == PH_UP) up_epilogue<FMT>(a, blob, grp, rb + 16 * q + 4 * g, bpos[st], r[q], r[RT + q]);
+        else down_epilogue<FMT>(a, blob, grp, rb + 16 * q + 4 * g, bpos[st], r[q]);
       }
     }
     if constexpr (KS > 1 || TP > 0) __syncthreads();   // s_red / s_b are reused by the next pass
+  }
+}
+
+// ---- prefill: B chunks staged once per workgroup, waves on different rows ---------------------
+// The 4 waves own 4·RT consecutive 16-row tiles and walk all of K together: the B operand of
+// each chunk (TOK = 16·NT tokens × one chunk of columns, x or h_hi + h_lo) is loaded once by the
+// whole workgroup into LDS (double-buffered, 16-byte segments XOR-swizzled by row so the MFMA
+// reads are bank-conflict free) and shared by the 4 waves. Each wave keeps the 4 K partials
+// (chunk c → partial c mod 4) in separate accumulators and sums them in partial order, which is
+// the arithmetic expert_gemm performs with its 4 waves: a token's result is the same bits
+// whichever kernel computed it.
+template <int PH, int FMT, int RT, int NT, int DA>
+__global__ __launch_bounds__(256) void prefill_gemm(GemmArgs a) {
+  using F = Fmt<FMT>;
+  constexpr bool MLX = (FMT == Q_MLX4 || FMT == Q_MLX8);
+  constexpr int NM = (PH == PH_UP) ? 2 * RT : RT;
+  constexpr int NBV = F::NB;                          // B vectors per lane per chunk
+  constexpr int NH = (PH == PH_UP) ? 1 : 2;
+  constexpr int ROWS = 4 * 16 * RT;
+  constexpr int TOK = 16 * NT;
+  constexpr int NSEG = F::CHUNK / 8;                  // 16-byte segments per B row chunk
+  constexpr int BVEC = NH * TOK * NSEG;               // 16-byte vectors per B chunk
+  constexpr int BPT = (BVEC + 255) / 256;             // per thread
+  static_assert(DA == 1 || DA == 2 || DA == 4, "DA divides the 4-chunk unroll");
+  __shared__ __align__(16) u32x4 s_bv[2][BVEC];
+
+  const int nblk = gridDim.x;
+  const int b = blockIdx.x;
+  const int xcd = b & 7, slot = b >> 3;
+  const int per = (nblk + 7) >> 3;
+  int rem = nblk & 7;
+  if (rem == 0) rem = 8;
+  const int logical = (xcd < rem ? xcd * per : rem * per + (xcd - rem) * (per - 1)) + slot;
+  const int rt = logical / a.max_work;
+  const int wi = logical - rt * a.max_work;
+  if (rt >= a.row_tiles || wi >= *a.n_work) return;
+
+  const int4 item = a.work[wi];
+  const int e = item.x, pos0 = item.y, nitem = item.z;
+  const int gsel = (e == a.experts) ? 1 : 0;
+  const ExpertGroup &grp = a.grp[gsel];
+  const uint8_t *blob = grp.blobs + (gsel ? 0 : (size_t)e * grp.stride);
+  const int I = grp.inter, H = a.hidden;
+  const int out_dim = (PH == PH_UP) ? I : H;
+  const int K = (PH == PH_UP) ? H : I;
+  if (rt * ROWS >= out_dim) return;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, l16 = lane & 15;
+  const int rb = rt * ROWS + wave * 16 * RT;
+
+  typename F::Row arow[NM];
+  const uint8_t *mscale[NM];
+  const uint8_t *mbias[NM];
+  int tile_row0[NM];
+#pragma unroll
+  for (int m = 0; m < NM; ++m) {
+    const int q = m % RT;
+    const bool is_up = (PH == PH_UP) && (m >= RT);
+    const int r0 = min(rb + 16 * q, out_dim - 16);
+    const int orow = r0 + l16;
+    tile_row0[m] = r0;
+    if constexpr (FMT == Q_MXFP4) {
+      if (PH == PH_UP) arow[m] = F::row(blob + grp.off[0], blob + grp.off[1], 2 * orow + (is_up ? 1 : 0), K);
+      else arow[m] = F::row(blob + grp.off[3], blob + grp.off[4], orow, K);
+    } else if constexpr (FMT == Q_BF16) {
+      if (PH == PH_UP) arow[m] = F::row(blob + grp.off[0], orow + (is_up ? I : 0), K);
+      else arow[m] = F::row(blob + grp.off[1], orow, K);
+    } else {
+      const int mat = (PH == PH_UP) ? (is_up ? 1 : 0) : 2;
+      arow[m] = F::row(blob + grp.off[3 * mat], orow, K);
+      mscale[m] = blob + grp.off[3 * mat + 1];
+      mbias[m] = blob + grp.off[3 * mat + 2];
+    }
+  }
+  const int nch = (K + F::CHUNK - 1) / F::CHUNK;
+
+  for (int t0 = 0; t0 < nitem; t0 += TOK) {
+    const int ntok = min(TOK, nitem - t0);
+    // Staging assignment: vector v = tid + 256·k ↦ (term hh, token row n, segment sg).
+    const uint16_t *bsrc[BPT];
+    int bcol[BPT], bdst[BPT];
+#pragma unroll
+    for (int k = 0; k < BPT; ++k) {
+      const int v = min(tid + 256 * k, BVEC - 1);
+      const int hh = v / (TOK * NSEG);
+      const int n = (v / NSEG) % TOK;
+      const int sg = v % NSEG;
+      const int p = pos0 + t0 + (n < ntok ? n : 0);
+      const uint16_t *row;
+      if (PH == PH_UP) row = a.x + (size_t)(a.order[p] / a.slots) * H;
+      else row = (hh == 0 ? a.h_hi : a.h_lo) + (size_t)p * a.ldh;
+      bsrc[k] = row;
+      bcol[k] = 8 * sg;
+      bdst[k] = (hh * TOK + n) * NSEG + (sg ^ (n & (NSEG - 1)));
+    }
+    u32x4 breg[BPT];
+    auto load_b = [&](int c) {
+      // Columns past K (a tail chunk, or K shorter than a chunk) are clamped into the row:
+      // those B values only meet zeroed weights.
+      const int cc = min(c, nch - 1);
+#pragma unroll
+      for (int k = 0; k < BPT; ++k)
+        breg[k] = *(const u32x4 *)(bsrc[k] + min(cc * F::CHUNK + bcol[k], K - 8));
+    };
+    auto store_b = [&](int buf) {
+#pragma unroll
+      for (int k = 0; k < BPT; ++k)
+        if (tid + 256 * k < BVEC) s_bv[buf][bdst[k]] = breg[k];
+    };
+    int bpos[NT];
+#pragma unroll
+    for (int st = 0; st < NT; ++st) {
+      const int j = 16 * st + l16;
+      bpos[st] = pos0 + t0 + (j < ntok ? j : 0);
+    }
+
+    f32x4 acc[4][NM][NT];
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp)
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int st = 0; st < NT; ++st) acc[pp][m][st] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    typename F::A sa[DA][NM];
+    auto load_a = [&](typename F::A (&w)[NM], int c) {
+      const int cc = min(c, nch - 1);
+#pragma unroll
+      for (int m = 0; m < NM; ++m) F::load(w[m], arow[m], cc, g, K);
+    };
+
+    // B operand of token tile st, MFMA step v, term hh from LDS buffer buf.
+    auto bvec = [&](int buf, int st, int hh, int v) -> u32x4 {
+      const int n = 16 * st + l16;
+      const int sg = MLX ? (2 * g + v) : (4 * g + v);
+      return s_bv[buf][(hh * TOK + n) * NSEG + (sg ^ (n & (NSEG - 1)))];
+    };
+
+    auto compute = [&](const typename F::A (&w)[NM], int buf, int c, f32x4 (&ac)[NM][NT]) {
+      if constexpr (!MLX) {
+        const bool ok = F::lane_valid(c, g, K);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          u32x4 bv[NT][NH];
+#pragma unroll
+          for (int st = 0; st < NT; ++st)
+#pragma unroll
+            for (int hh = 0; hh < NH; ++hh) bv[st][hh] = bvec(buf, st, hh, v);
+#pragma unroll
+          for (int m = 0; m < NM; ++m) {
+            bf16x8 av;
+            if constexpr (FMT == Q_MXFP4) av = mxfp4_to_bf16(ok ? w[m].w[v] : 0u, e8m0_to_f32(w[m].s));
+            else av = as_bf16x8(ok ? w[m].w[v] : u32x4{0u, 0u, 0u, 0u});
+#pragma unroll
+            for (int st = 0; st < NT; ++st)
+#pragma unroll
+              for (int hh = 0; hh < NH; ++hh) ac[m][st] = mfma(av, as_bf16x8(bv[st][hh]), ac[m][st]);
+          }
+        }
+      } else {
+        u32x4 bv[NT][NH][2];
+#pragma unroll
+        for (int st = 0; st < NT; ++st)
+#pragma unroll
+          for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) bv[st][hh][jj] = bvec(buf, st, hh, jj);
+        f32x4 P[NM][NT];
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+          for (int st = 0; st < NT; ++st) P[m][st] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+          for (int m = 0; m < NM; ++m) {
+            const bf16x8 av = F::decode(w[m], jj);
+#pragma unroll
+            for (int st = 0; st < NT; ++st)
+#pragma unroll
+              for (int hh = 0; hh < NH; ++hh) P[m][st] = mfma(av, as_bf16x8(bv[st][hh][jj]), P[m][st]);
+          }
+        float gsum[NT];
+#pragma unroll
+        for (int st = 0; st < NT; ++st) gsum[st] = group_sum<NH>(bv[st]);
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) {
+            const size_t ri = (size_t)(tile_row0[m] + 4 * g + ii) * (K / 64) + c;
+            const float sc = bf16_bits_to_f32(((const uint16_t *)mscale[m])[ri]);
+            const float bi = bf16_bits_to_f32(((const uint16_t *)mbias[m])[ri]);
+#pragma unroll
+            for (int st = 0; st < NT; ++st) {
+              ac[m][st][ii] = __builtin_fmaf(sc, P[m][st][ii], ac[m][st][ii]);
+              ac[m][st][ii] = __builtin_fmaf(bi, gsum[st], ac[m][st][ii]);
+            }
+          }
+      }
+    };
+
+    // Prologue: B of chunk 0 in LDS, B of chunk 1 in registers, A of chunks 0..DA-1 in flight.
+    load_b(0);
+    store_b(0);
+    load_b(1);
+#pragma unroll
+    for (int u = 0; u < DA; ++u) load_a(sa[u], u);
+    __syncthreads();
+    // Chunk c: compute from LDS buffer c % 2; then stage B of c + 1 into the other buffer and
+    // fetch B of c + 2 and A of c + DA; one barrier per chunk.
+    for (int c0 = 0; c0 < nch; c0 += 4) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int c = c0 + u;
+        if (c < nch) {
+          compute(sa[u % DA], u & 1, c, acc[u]);
+          load_a(sa[u % DA], c + DA);
+          store_b((u + 1) & 1);
+          load_b(c + 2);
+          __syncthreads();
+        }
+      }
+    }
+
+    // Epilogue: partials summed in order, 4 intermediates / hidden rows per lane.
+#pragma unroll
+    for (int st = 0; st < NT; ++st) {
+      const int j = 16 * st + l16;
+      if (j >= ntok) continue;
+#pragma unroll
+      for (int q = 0; q < RT; ++q) {
+        if (rb + 16 * q >= out_dim) continue;
+        if constexpr (PH == PH_UP) {
+          const f32x4 gate = sum_partials4(acc[0][q][st], acc[1][q][st], acc[2][q][st], acc[3][q][st]);
+          const f32x4 up = sum_partials4(acc[0][RT + q][st], acc[1][RT + q][st], acc[2][RT + q][st],
+                                         acc[3][RT + q][st]);
+          up_epilogue<FMT>(a, blob, grp, rb + 16 * q + 4 * g, bpos[st], gate, up);
+        } else {
+          const f32x4 r = sum_partials4(acc[0][q][st], acc[1][q][st], acc[2][q][st], acc[3][q][st]);
+          down_epilogue<FMT>(a, blob, grp, rb + 16 * q + 4 * g, bpos[st], r);
+        }
+      }
+    }
+    __syncthreads();   // the next pass restages s_bv
   }
 }
 
@@ -514,11 +783,16 @@ template <int PH, int FMT>
 static GemmKernel pick(int nt) {
   constexpr int DA_DECODE = (FMT == Q_BF16) ? 2 : 4;
   if (nt <= 1) return expert_gemm<PH, FMT, 1, 1, DA_DECODE, 1, LAYER_KS, DECODE_TP>;
-  if constexpr (PH == PH_UP) return expert_gemm<PH, FMT, 2, 4, 2, 2, LAYER_KS, 0>;
-  else return expert_gemm<PH, FMT, 2, 2, 2, 2, LAYER_KS, 0>;
+  // Prefill: 4 waves × RT 16-row tiles × 32 tokens (BF16 keeps one tile per wave: its
+  // weight operand is 4× wider per chunk).
+  constexpr int RT_P = (FMT == Q_BF16) ? 1 : 2;
+  return prefill_gemm<PH, FMT, RT_P, 2, 2>;
 }
 
-int gemm_rows_per_block(int nt) { return (4 / LAYER_KS) * 16 * (nt <= 1 ? 1 : 2); }
+int gemm_rows_per_block(int nt, int quant) {
+  if (nt <= 1) return (4 / LAYER_KS) * 16;
+  return 4 * 16 * (quant == Q_BF16 ? 1 : 2);
+}
 
 static GemmKernel gemm_kernel(int phase, int quant, int nt) {
   switch (quant) {
@@ -529,21 +803,24 @@ static GemmKernel gemm_kernel(int phase, int quant, int nt) {
   }
 }
 
-hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStream_t s) {
+hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStream_t s, Timing tm) {
   const unsigned blocks = (unsigned)a.row_tiles * (unsigned)a.max_work;
   if (blocks == 0) return hipSuccess;
   // Decode stages DECODE_TP B rows (x, or h_hi and h_lo) of up to K = max(H, ldh) columns.
   const size_t kmax = (size_t)std::max(a.hidden, a.ldh);
   const size_t lds = nt <= 1 ? (size_t)DECODE_TP * kmax * 2 * (phase == PH_UP ? 1 : 2) : 0;
-  hipLaunchKernelGGL(gemm_kernel(phase, quant, nt), dim3(blocks), dim3(256), lds, s, a);
+  hipExtLaunchKernelGGL(gemm_kernel(phase, quant, nt), dim3(blocks), dim3(256), lds, s, tm.start,
+                        tm.stop, 0, a);
   return hipGetLastError();
 }
 
-hipError_t launch_combine(const float *slot_out, int slots, int H, int T, float *y, hipStream_t s) {
+hipError_t launch_combine(const float *slot_out, int slots, int H, int T, float *y, hipStream_t s,
+                          Timing tm) {
   const size_t n4 = (size_t)T * H / 4;
   unsigned blocks = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
   if (blocks == 0) return hipSuccess;
-  hipLaunchKernelGGL(combine_kernel, dim3(blocks), dim3(256), 0, s, slot_out, slots, H, T, y);
+  hipExtLaunchKernelGGL(combine_kernel, dim3(blocks), dim3(256), 0, s, tm.start, tm.stop, 0,
+                        slot_out, slots, H, T, y);
   return hipGetLastError();
 }
 

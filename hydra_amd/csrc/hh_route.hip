@@ -463,20 +463,23 @@ __global__ __launch_bounds__(256) void dispatch_kernel(RouteArgs a) { dispatch_b
 namespace hh {
 // Router + top-k + dispatch: exact fp64 logits then one selecting workgroup when T ≤ 16;
 // the MFMA-screened tiles then the dispatch workgroup otherwise.
-hipError_t launch_route(const RouteArgs &a, hipStream_t s) {
+hipError_t launch_route(const RouteArgs &a, hipStream_t s, Timing tm) {
   if (a.tokens <= RT_TOK) {
     const int pairs = a.tokens * (a.experts + 1);
-    hipLaunchKernelGGL(logits64_kernel, dim3((pairs + 3) / 4), dim3(256), 0, s, a);
+    hipExtLaunchKernelGGL(logits64_kernel, dim3((pairs + 3) / 4), dim3(256), 0, s, tm.start,
+                          nullptr, 0, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(select_kernel, dim3(1), dim3(256), 0, s, a);
+    hipExtLaunchKernelGGL(select_kernel, dim3(1), dim3(256), 0, s, nullptr, tm.stop, 0, a);
     return hipGetLastError();
   }
   const int tiles = (a.tokens + RT_TOK - 1) / RT_TOK;
-  hipLaunchKernelGGL(route_kernel, dim3(tiles), dim3(256), 0, s, a);
+  const bool second = a.want_dispatch != 0;
+  hipExtLaunchKernelGGL(route_kernel, dim3(tiles), dim3(256), 0, s, tm.start,
+                        second ? nullptr : tm.stop, 0, a);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || !a.want_dispatch || tiles == 1) return e;
-  hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(256), 0, s, a);
+  if (e != hipSuccess || !second) return e;
+  hipExtLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(256), 0, s, nullptr, tm.stop, 0, a);
   return hipGetLastError();
 }
 // Stand-alone permutation of a given top-k table (hh_permute).

@@ -219,6 +219,9 @@ TINY = {
     "mxfp4-ragged": F.MoEDesc(hidden=2880, intermediate=320, experts=5, top_k=3,
                               quant=F.QUANT_MXFP4, activation=F.ACT_SWIGLU_OAI,
                               router=F.ROUTER_TOPK_SOFTMAX, expert_bias=1),
+    "mxfp4-narrow": F.MoEDesc(hidden=192, intermediate=64, experts=4, top_k=2,
+                              quant=F.QUANT_MXFP4, activation=F.ACT_SWIGLU_OAI,
+                              router=F.ROUTER_TOPK_SOFTMAX, expert_bias=1),
     "mlx4": F.MoEDesc(hidden=256, intermediate=128, experts=8, top_k=3, quant=F.QUANT_MLX4,
                       activation=F.ACT_SILU, router=F.ROUTER_SOFTMAX_TOPK_RENORM,
                       shared_intermediate=192, group_size=64),
