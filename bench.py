@@ -206,6 +206,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--only-t1", action="store_true", help="decode T=1 only (for profiling)")
+    ap.add_argument("--only-prefill", action="store_true", help="prefill only (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 256 MiB device-to-device copy and exit (HBM counter calibration)")
     args = ap.parse_args()
@@ -231,12 +232,13 @@ def main():
     lib()  # fail loudly if the HIP library is missing
 
     decode = {}
-    wl = Workload(torch, F.GPT_OSS_20B, copies=args.copies)
-    for T in ([1] if args.only_t1 else [1, 2, 4, 8]):
-        log(f"decode T={T}")
-        steps = args.steps if T == 1 else max(100, args.steps // 4)
-        decode[T] = measure_decode(wl, T, steps, args.warmup if T == 1 else 10)
-    wl.close()
+    if not args.only_prefill:
+        wl = Workload(torch, F.GPT_OSS_20B, copies=args.copies)
+        for T in ([1] if args.only_t1 else [1, 2, 4, 8]):
+            log(f"decode T={T}")
+            steps = args.steps if T == 1 else max(100, args.steps // 4)
+            decode[T] = measure_decode(wl, T, steps, args.warmup if T == 1 else 10)
+        wl.close()
     prefill = {}
     if not args.no_prefill and not args.only_t1:
         wl = Workload(torch, F.GPT_OSS_120B, copies=2, zipf=1.1)
@@ -245,6 +247,9 @@ def main():
             prefill[T] = measure_prefill(wl, T, 20 if T == 512 else 10, 3)
         wl.close()
     cpu = None if args.no_cpu else cpu_baseline()
+    if args.only_prefill:
+        print(json.dumps({"prefill_gpt_oss_120b_zipf": {str(T): v for T, v in prefill.items()}}))
+        return
 
     d1 = decode[1]
     achieved = d1["gate_up_GBps"]
