@@ -64,7 +64,7 @@ constexpr int kMaxTokens = 1 << 16;  // tokens per call
 
 // Scratch carve-up for T tokens of a layer shaped like d. All offsets 256-byte aligned.
 struct Scratch {
-  size_t lg64, topk_idx, topk_w, slot_w, seg, order, work, n_work, h_hi, h_lo, slot_out, total;
+  size_t lg64, lg32, wn, topk_idx, topk_w, slot_w, seg, order, work, n_work, h_hi, h_lo, slot_out, total;
   int slots, positions, ldh, max_work, tile_tokens, nt;
 };
 
@@ -93,6 +93,8 @@ Scratch plan(const hh_moe_desc &d, int T) {
     return o;
   };
   s.lg64 = take(sizeof(double) * (size_t)std::min(T, 16) * (E + 1));
+  s.lg32 = take(sizeof(float) * (size_t)T * E);
+  s.wn = take(sizeof(float) * (size_t)E);
   s.topk_idx = take(sizeof(int32_t) * (size_t)A);
   s.topk_w = take(sizeof(float) * (size_t)A);
   s.slot_w = take(sizeof(float) * (size_t)T * s.slots);
@@ -164,6 +166,8 @@ hh::RouteArgs route_args(const hh_moe_desc &d, const hh_moe_weights *w, uint8_t 
   r.eps = d.router_eps;
   r.logits = nullptr;
   r.lg64 = (double *)(base + s.lg64);
+  r.lg32 = (float *)(base + s.lg32);
+  r.wn = (float *)(base + s.wn);
   r.topk_idx = (int32_t *)(base + s.topk_idx);
   r.topk_w = (float *)(base + s.topk_w);
   r.slot_w = (float *)(base + s.slot_w);

@@ -107,7 +107,9 @@ struct RouteArgs {
   int32_t tokens, hidden, experts, top_k, slots, router, tile_tokens, want_dispatch;
   float eps;
   double *logits;               // fp64 [T][K] exact logits of the selected experts, or null
-  double *lg64;                 // fp64 [T][E+1] scratch for T ≤ 16 (last column: shared gate)
+  double *lg64;                 // fp64 [T][E+1] exact logits (batches of ≤ 16 tokens; column E: shared gate)
+  float *lg32;                  // fp32 [T][E] screening logits (batches above 16 tokens)
+  float *wn;                    // fp32 [E] router row norms
   int32_t *topk_idx;            // [T][K]
   float *topk_w;                // [T][K]
   float *slot_w;                // [T·slots]

@@ -1,20 +1,23 @@
 // hh_route.hip — router logits, top-k weights and token→expert dispatch.
 //
-// route_kernel: one 256-thread workgroup per 16-token tile, no cross-workgroup synchronisation.
-//   A. Router logits of the tile against every expert with v_mfma_f32_16x16x32_bf16 (exact
-//      bf16·bf16 products, fp32 accumulation), the 4 waves splitting K, plus each expert row's
-//      norm.
-//   B. Per token: every fp32 logit lies within err = 2·H·2^-23·‖x‖·‖w_e‖ of the exact one
-//      (recursive summation bound with Cauchy-Schwarz). Experts whose upper bound reaches the
-//      K-th largest lower bound are the only ones that can be in the exact top-k; their logits
-//      are recomputed in fp64 (the oracle's arithmetic) and the top-k is selected among them
-//      with ties to the smaller index. Indices therefore equal those of an fp64 router, and
-//      weights are computed from fp64 logits.
-//   C. dispatch_kernel then groups the batch's assignments by expert.
+// Selection is exact: top-k indices equal those of fp64 logits (the oracle's arithmetic).
+//   A. Screening logits with v_mfma_f32_16x16x32_bf16 (exact bf16·bf16 products, fp32
+//      accumulation) for 16-token × 16-expert tiles, plus each expert row's norm ‖w_e‖.
+//   B. Per token (one wave): every fp32 logit lies within err = 2·H·2^-23·‖u‖·‖w_e‖ (+ the
+//      rounding of the bias add and final scaling) of the exact one (recursive summation bound
+//      with Cauchy-Schwarz). Experts whose upper bound reaches the K-th largest lower bound are
+//      the only ones that can be in the exact top-k; their logits are recomputed in fp64 and
+//      the top-k is selected among them with ties to the smaller index. Weights come from the
+//      fp64 logits.
+//   C. Dispatch: the batch's (token, rank) assignments grouped by expert, stable, plus the
+//      work list of the expert products.
 //
-// Batches of at most 16 tokens skip the screening: logits64_kernel computes every logit in
-// fp64 (one wave per (token, expert)) and select_kernel selects and dispatches in one
-// workgroup.
+// Batches of at most 16 tokens skip the screening: logits64_kernel computes every logit in fp64
+// (one wave per (token, expert) pair, spread over many compute units), and select_small_kernel
+// selects and dispatches in one workgroup. Larger batches run A over a (token tile × expert
+// tile) grid (route_logits_kernel), B one wave per token (route_select_kernel) and C in one
+// workgroup (dispatch_kernel). No kernel synchronises
+// with another workgroup: the stream orders the phases.
 //
 // Reference: router_topk / router_topk_batch (attention.metal:249, batch.metal:430),
 // gemma_router_topk (gemma.metal:158), ReferenceOps.router (ReferenceOps.swift:173-183),
@@ -36,8 +39,9 @@ __device__ __forceinline__ double wave_max_f64(double v) {
   return v;
 }
 
-// Exclusive scan of data[0..n) in place (n ≤ 512), 256 threads; returns the total.
-__device__ int block_exclusive_scan(int *data, int n, int *s_wave) {
+// Exclusive scan of data[0..n) in place (n ≤ 128·NW), 64·NW threads; returns the total.
+template <int NW>
+__device__ __forceinline__ int block_exclusive_scan(int *data, int n, int *s_wave) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int a0 = (2 * tid < n) ? data[2 * tid] : 0;
   int a1 = (2 * tid + 1 < n) ? data[2 * tid + 1] : 0;
@@ -49,9 +53,12 @@ __device__ int block_exclusive_scan(int *data, int n, int *s_wave) {
   }
   if (lane == 63) s_wave[wave] = inc;
   __syncthreads();
-  int base = 0;
-  for (int w = 0; w < wave; ++w) base += s_wave[w];
-  int total = s_wave[0] + s_wave[1] + s_wave[2] + s_wave[3];
+  int base = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    base += (w < wave) ? s_wave[w] : 0;
+    total += s_wave[w];
+  }
   int ex = base + inc - v;
   __syncthreads();
   if (2 * tid < n) data[2 * tid] = ex;
@@ -60,39 +67,43 @@ __device__ int block_exclusive_scan(int *data, int n, int *s_wave) {
   return total;
 }
 
-// Stable token→expert permutation of the whole batch by one workgroup.
-__device__ void dispatch_batch(const RouteArgs &a) {
+// Stable token→expert permutation of the whole batch by one workgroup of NW waves; `idx` is
+// the top-k table [T][K] (global or LDS).
+template <int NW>
+__device__ __forceinline__ void dispatch_batch(const RouteArgs &a, const int32_t *idx) {
+  constexpr int NT = 64 * NW;
   __shared__ int s_cnt[kMaxExperts + 1];
   __shared__ int s_off[kMaxExperts + 1];
   __shared__ int s_tiles[kMaxExperts + 1];
   __shared__ int s_run[kMaxExperts];
-  __shared__ int s_wcnt[4][kMaxExperts];
-  __shared__ int s_wave[4];
+  __shared__ int s_wcnt[NW][kMaxExperts];
+  __shared__ int s_wave[NW];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int E = a.experts, K = a.top_k, T = a.tokens, A = T * K;
   const int TN = a.tile_tokens;
-  for (int e = tid; e <= E; e += 256) s_cnt[e] = 0;
-  for (int e = tid; e < E; e += 256) {
+  for (int e = tid; e <= E; e += NT) s_cnt[e] = 0;
+  for (int e = tid; e < E; e += NT) {
     s_run[e] = 0;
-    for (int w = 0; w < 4; ++w) s_wcnt[w][e] = 0;
+    for (int w = 0; w < NW; ++w) s_wcnt[w][e] = 0;
   }
   __syncthreads();
-  for (int i = tid; i < A; i += 256) atomicAdd(&s_cnt[a.topk_idx[i]], 1);
+  for (int i = tid; i < A; i += NT) atomicAdd(&s_cnt[idx[i]], 1);
   __syncthreads();
-  for (int e = tid; e < E; e += 256) {
+  for (int e = tid; e < E; e += NT) {
     s_off[e] = s_cnt[e];
     s_tiles[e] = (s_cnt[e] + TN - 1) / TN;
   }
   __syncthreads();
-  int routed_positions = block_exclusive_scan(s_off, E, s_wave);
-  int routed_tiles = block_exclusive_scan(s_tiles, E, s_wave);
-  (void)routed_positions;
-  // Stable scatter in chunks of 256 assignments, (t, r) order preserved inside each expert.
+  block_exclusive_scan<NW>(s_off, E, s_wave);
+  const int routed_tiles = block_exclusive_scan<NW>(s_tiles, E, s_wave);
+  // Stable scatter in chunks of NT assignments, (t, r) order preserved inside each expert:
+  // a lane's rank among the lanes of its wave with the same expert (matched by ballots over
+  // the expert id's bits), plus the counts of earlier waves and earlier chunks.
   const int nbits = E > 1 ? 32 - __clz(E - 1) : 1;
-  for (int base = 0; base < A; base += 256) {
+  for (int base = 0; base < A; base += NT) {
     const int i = base + tid;
     const bool valid = i < A;
-    const int e = valid ? a.topk_idx[i] : 0;
+    const int e = valid ? idx[i] : 0;
     uint64_t peers = __ballot(valid);
     for (int b = 0; b < nbits; ++b) {
       uint64_t m = __ballot(valid && ((e >> b) & 1));
@@ -108,14 +119,19 @@ __device__ void dispatch_batch(const RouteArgs &a) {
       a.order[pos] = t * a.slots + r;
     }
     __syncthreads();
-    for (int x = tid; x < E; x += 256) {
-      s_run[x] += s_wcnt[0][x] + s_wcnt[1][x] + s_wcnt[2][x] + s_wcnt[3][x];
-      s_wcnt[0][x] = s_wcnt[1][x] = s_wcnt[2][x] = s_wcnt[3][x] = 0;
+    for (int x = tid; x < E; x += NT) {
+      int add = 0;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        add += s_wcnt[w][x];
+        s_wcnt[w][x] = 0;
+      }
+      s_run[x] += add;
     }
     __syncthreads();
   }
   // Segments and work items (expert, first position, tokens), ascending expert order.
-  for (int e = tid; e < E; e += 256) {
+  for (int e = tid; e < E; e += NT) {
     a.seg[e] = s_off[e];
     const int n = s_cnt[e];
     for (int j = 0; j * TN < n; ++j)
@@ -124,9 +140,9 @@ __device__ void dispatch_batch(const RouteArgs &a) {
   int nwork = routed_tiles;
   if (a.shared_gate) {
     // The shared expert is expert id E over every token, after the routed positions.
-    for (int t = tid; t < T; t += 256) a.order[A + t] = t * a.slots + K;
+    for (int t = tid; t < T; t += NT) a.order[A + t] = t * a.slots + K;
     const int st = (T + TN - 1) / TN;
-    for (int j = tid; j < st; j += 256)
+    for (int j = tid; j < st; j += NT)
       a.work[routed_tiles + j] = make_int4(E, A + j * TN, min(TN, T - j * TN), 0);
     nwork += st;
     if (tid == 0) { a.seg[E] = A; a.seg[E + 1] = A + T; }
@@ -144,18 +160,16 @@ constexpr int RT_MAXCAND = 64;      // exact-recompute candidates handled per pa
 __device__ __forceinline__ float bf_lo(uint32_t v) { return bf16_bits_to_f32(v & 0xFFFF); }
 __device__ __forceinline__ float bf_hi(uint32_t v) { return bf16_bits_to_f32(v >> 16); }
 
-// Projection input of the router for token row `xr` at column block [h, h+8): GEMMA uses
-// u = x·scale split exactly into bf16 hi + lo (x·scale has at most 16 significant bits);
-// the other routers use x itself (lo = 0).
-__device__ __forceinline__ void router_operand(const RouteArgs &a, const uint16_t *xr, int h,
+// Projection input of the router from 8 columns of a token row (xv) and of the GEMMA scale
+// (sv): GEMMA uses u = x·scale split exactly into bf16 hi + lo (x·scale has at most 16
+// significant bits); the other routers use x itself (lo = 0).
+__device__ __forceinline__ void router_operand(bool gemma, const u32x4 &xv, const u32x4 &sv,
                                                u32x4 &hi, u32x4 &lo) {
-  const u32x4 xv = *(const u32x4 *)(xr + h);
-  if (a.router != R_GEMMA) {
+  if (!gemma) {
     hi = xv;
     lo = u32x4{0u, 0u, 0u, 0u};
     return;
   }
-  const u32x4 sv = *(const u32x4 *)(a.router_scale + h);
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const float u0 = bf_lo(xv[k]) * bf_lo(sv[k]), u1 = bf_hi(xv[k]) * bf_hi(sv[k]);
@@ -168,48 +182,165 @@ __device__ __forceinline__ void router_operand(const RouteArgs &a, const uint16_
 }
 
 // Exact (fp64) router logit of expert e for token row xr, in the oracle's arithmetic: one wave.
-// GEMMA: Σ (((x·s)·scale)·root)·w with s = (Σx²/H + eps)^-½ passed in `norm`.
-__device__ double exact_logit(const RouteArgs &a, const uint16_t *xr, const uint16_t *wrow,
-                              bool gemma, double norm, double root) {
+// A bf16·bf16 product is exact in fp32, so each term is formed in fp32 and added in fp64:
+// the same value as an fp64 fma. GEMMA: Σ (((x·s)·scale)·root)·w in fp64 with
+// s = (Σx²/H + eps)^-½ passed in `norm`. Each lane issues the loads of four 512-column steps
+// before their products and keeps one accumulator per step, so a dot costs about one memory
+// latency and a short dependency chain.
+template <bool gemma>
+__device__ __forceinline__ double exact_logit(const RouteArgs &a, const uint16_t *xr,
+                                              const uint16_t *wrow, double norm, double root) {
   const int lane = threadIdx.x & 63, H = a.hidden;
-  double acc = 0.0;
-  for (int h = lane * 8; h < H; h += 512) {
-    const u32x4 xv = *(const u32x4 *)(xr + h);
-    const u32x4 wv = *(const u32x4 *)(wrow + h);
+  double acc[4] = {0.0, 0.0, 0.0, 0.0};
+  for (int base = 0; base < H; base += 2048) {
+    u32x4 xv[4], wv[4], sv[4];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      double xd = bf16_bits_to_f32((xv[k >> 1] >> ((k & 1) * 16)) & 0xFFFF);
-      const double wd = bf16_bits_to_f32((wv[k >> 1] >> ((k & 1) * 16)) & 0xFFFF);
-      if (gemma) xd = ((xd * norm) * (double)bf16_bits_to_f32(a.router_scale[h + k])) * root;
-      acc = fma(xd, wd, acc);
+    for (int u = 0; u < 4; ++u) {
+      // Loads are unconditional (clamped into the row) and masked afterwards: a load under a
+      // lane-dependent branch would be waited for before the next one is issued.
+      const int h = base + lane * 8 + 512 * u;
+      const int hc = min(h, H - 8);
+      const bool ok = h < H;
+      xv[u] = *(const u32x4 *)(xr + hc);
+      wv[u] = *(const u32x4 *)(wrow + hc);
+      sv[u] = gemma ? *(const u32x4 *)(a.router_scale + hc) : u32x4{0u, 0u, 0u, 0u};
+      if (!ok) wv[u] = u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int sh = (k & 1) * 16;
+        const float xf = bf16_bits_to_f32((xv[u][k >> 1] >> sh) & 0xFFFF);
+        const float wf = bf16_bits_to_f32((wv[u][k >> 1] >> sh) & 0xFFFF);
+        if constexpr (gemma) {
+          const double xd = (((double)xf * norm) *
+                             (double)bf16_bits_to_f32((sv[u][k >> 1] >> sh) & 0xFFFF)) * root;
+          acc[u] = fma(xd, (double)wf, acc[u]);
+        } else {
+          acc[u] += (double)(xf * wf);
+        }
+      }
     }
   }
-  return wave_sum_f64(acc);
+  return wave_sum_f64((acc[0] + acc[1]) + (acc[2] + acc[3]));
 }
 
-// Weights of one token's selection (by lane 0): sel_v are fp64 logits in rank order.
-__device__ void finish_token(const RouteArgs &a, int t, const double *sel_v, const int *sel_i,
-                             double sg_logit) {
-  const int K = a.top_k;
-  double w[kMaxTopK];
-  double total = 0.0;
+// Screening logits of a 16-token × 16-expert tile over the 128-column chunks c ≡ kq (mod nk):
+// lane (g, l16) supplies router row et·16 + l16 (A) and token t0 + l16 (B) at columns
+// 128c + 32g + 8v. Returns the D fragment (experts 4g..4g+3 of the tile, token l16) and, in
+// wsq, Σw² of row l16 over the same columns (in the lanes of group l16 / 4; the caller sums
+// the K slices). Σw² is accumulated in fp32 like the logits: its relative error (≤ H·2^-24)
+// is far inside the factor 4 of slack the screening bound carries.
+// Chunks are loaded two at a time before either is used, so the loop costs about one memory
+// latency per two chunks.
+template <bool gemma>
+__device__ __forceinline__ f32x4 tile_logits(const RouteArgs &a, int t0, int ntok, int et, int kq, int nk,
+                             float &wsq) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, l16 = lane & 15;
+  const int E = a.experts, H = a.hidden;
+  const uint16_t *xr = a.xr + (size_t)(t0 + min(l16, ntok - 1)) * H;
+  const uint16_t *wrow = a.router_w + (size_t)min(et * 16 + l16, E - 1) * H;
+  const int nch = (H + 127) / 128;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f}, wacc = {0.f, 0.f, 0.f, 0.f};
+  for (int c0 = kq; c0 < nch; c0 += 2 * nk) {
+    u32x4 wv[2][4], xv[2][4], sv[2][4];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int c = c0 + b * nk;
+      const int col = min(128 * min(c, nch - 1) + 32 * g, H - 32);
+      const bool ok = c < nch && 128 * c + 32 * g < H;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        // Unconditional (clamped) loads, masked afterwards (see exact_logit).
+        wv[b][v] = *(const u32x4 *)(wrow + col + 8 * v);
+        xv[b][v] = *(const u32x4 *)(xr + col + 8 * v);
+        sv[b][v] = gemma ? *(const u32x4 *)(a.router_scale + col + 8 * v) : u32x4{0u, 0u, 0u, 0u};
+        if (!ok) wv[b][v] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        u32x4 xh, xl;
+        router_operand(gemma, xv[b][v], sv[b][v], xh, xl);
+        wacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[b][v]), as_bf16x8(wv[b][v]), wacc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[b][v]), as_bf16x8(xh), acc, 0, 0, 0);
+        if constexpr (gemma)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[b][v]), as_bf16x8(xl), acc, 0, 0, 0);
+      }
+    }
+  }
+  // ‖w_i‖² is the diagonal of W·Wᵀ: row i sits in lane (g = i/4, l16 = i), element i % 4;
+  // the lanes of lane group l16 / 4 return it (0 elsewhere).
+  wsq = (g == (l16 >> 2)) ? wacc[l16 & 3] : 0.f;
+  return acc;
+}
+
+// Screening result of one token: candidate count and the GEMMA normaliser of its input.
+struct TokenScreen {
+  int nc = 0;
+  double norm = 1.0;
+};
+
+// Running exact top-k, descending, ties to the smaller index. Every lane of a wave holds the
+// same copy.
+struct TopK {
+  double v[kMaxTopK];
+  int i[kMaxTopK];
+  __device__ TopK() {
+#pragma unroll
+    for (int r = 0; r < kMaxTopK; ++r) { v[r] = -INFINITY; i[r] = 0x7FFFFFFF; }
+  }
+  // One bubble pass with static indices (registers only). The carried entry (the new one,
+  // then each displaced one) goes ahead of an entry with a smaller value, or an equal value and
+  // a larger index.
+  __device__ void insert(double x, int e, int K) {
+#pragma unroll
+    for (int r = 0; r < kMaxTopK; ++r) {
+      if (r < K && (x > v[r] || (x == v[r] && e < i[r]))) {
+        const double tv = v[r];
+        const int ti = i[r];
+        v[r] = x;
+        i[r] = e;
+        x = tv;
+        e = ti;
+      }
+    }
+  }
+};
+
+// Weights of one token's selection (whole wave; lane r < K handles rank r): tk holds the fp64
+// logits in rank order.
+__device__ __forceinline__ void finish_token(const RouteArgs &a, int t, const TopK &tk, double sg_logit) {
+  const int K = a.top_k, lane = threadIdx.x & 63;
+  double v = -INFINITY;
+  int e = 0;
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r)
+    if (lane == r) { v = tk.v[r]; e = tk.i[r]; }
   // TOPK_SOFTMAX: softmax over the k selected logits (ReferenceOps.swift:178-182).
   // SOFTMAX_TOPK_RENORM and GEMMA: softmax over all experts, renormalised over the k
   // (QwenReferenceOps.swift:159-179, Gemma4ReferenceOps.swift:146-155); the full-softmax
-  // denominator cancels, leaving the same softmax of the k selected logits.
-  const double peak = sel_v[0];
-  for (int r = 0; r < K; ++r) { w[r] = exp(sel_v[r] - peak); total += w[r]; }
-  for (int r = 0; r < K; ++r) w[r] /= total;
-  if (a.router == R_GEMMA)
-    for (int r = 0; r < K; ++r) w[r] *= (double)bf16_bits_to_f32(a.router_pes[sel_i[r]]);
-  for (int r = 0; r < K; ++r) {
-    a.topk_idx[(size_t)t * K + r] = sel_i[r];
-    a.topk_w[(size_t)t * K + r] = (float)w[r];
-    a.slot_w[(size_t)t * a.slots + r] = (float)w[r];
+  // denominator cancels, leaving the same softmax of the k selected logits. The sum runs in
+  // rank order.
+  double w = lane < K ? exp(v - tk.v[0]) : 0.0;
+  double total = 0.0;
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r) {
+    const double wr = __shfl(w, r);
+    if (r < K) total += wr;
   }
-  if (a.logits)
-    for (int r = 0; r < K; ++r) a.logits[(size_t)t * K + r] = sel_v[r];
-  if (a.shared_gate) {
+  w /= total;
+  if (lane < K) {
+    if (a.router == R_GEMMA) w *= (double)bf16_bits_to_f32(a.router_pes[e]);
+    a.topk_idx[(size_t)t * K + lane] = e;
+    a.topk_w[(size_t)t * K + lane] = (float)w;
+    a.slot_w[(size_t)t * a.slots + lane] = (float)w;
+    if (a.logits) a.logits[(size_t)t * K + lane] = v;
+  }
+  if (a.shared_gate && lane == 0) {
     // σ of the shared gate row, applied to the shared expert's output
     // (QwenReferenceLayer.swift:399-404).
     const double sg = 1.0 / (1.0 + exp(-sg_logit));
@@ -218,273 +349,289 @@ __device__ void finish_token(const RouteArgs &a, int t, const double *sel_v, con
   }
 }
 
-__global__ __launch_bounds__(256) void route_kernel(RouteArgs a) {
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int g = lane >> 4, l16 = lane & 15;
-  const int E = a.experts, H = a.hidden, K = a.top_k, T = a.tokens;
-  const int t0 = blockIdx.x * RT_TOK;
-  const int ntok = min(RT_TOK, T - t0);
-  const bool gemma = (a.router == R_GEMMA);
-
-  __shared__ float s_part[4][16][16];          // [wave][expert in tile][token]
-  __shared__ float s_wpart[4][16];              // [wave][expert in tile] Σw² partials
-  __shared__ float s_logit[RT_TOK][kMaxExperts];
-  __shared__ float s_wn[kMaxExperts];           // ‖w_e‖
-  __shared__ int s_cand[4][RT_MAXCAND];
-  __shared__ double s_exact[4][RT_MAXCAND];
-
-  // ---- A: fp32 logits of the tile, K split over the 4 waves ----
-  const int tok_lane = t0 + min(l16, ntok - 1);
-  const uint16_t *xr_lane = a.xr + (size_t)tok_lane * H;
-  const int nch = H / 128 + ((H % 128) ? 1 : 0);
-  const int ntiles = (E + 15) / 16;
-  for (int et = 0; et < ntiles; ++et) {
-    const int e_lane = min(et * 16 + l16, E - 1);
-    const uint16_t *wrow = a.router_w + (size_t)e_lane * H;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    float wsq = 0.f;
-    for (int c = wave; c < nch; c += 4) {
-      const int col = min(128 * c + 32 * g, H - 32);
-      const bool ok = 128 * c + 32 * g < H;
-      u32x4 wv[4], xh[4], xl[4];
+// Screens token t (one wave): bounds every fp32 logit lgf(e) by err_e, θ = the K-th largest
+// lower bound, and writes the candidates {e : ub_e ≥ θ} to cl[] in ascending order.
+template <bool gemma, class LG, class WN>
+__device__ __forceinline__ TokenScreen screen_token(const RouteArgs &a, int t, LG lgf, WN wnf, int *cl) {
+  const int lane = threadIdx.x & 63;
+  const int E = a.experts, H = a.hidden, K = a.top_k;
+  const uint16_t *xr = a.xr + (size_t)t * H;
+  // ‖u‖ of the projection input (u = x, or x·scale for GEMMA) and Σx² for GEMMA's norm.
+  double uu = 0.0, xx = 0.0;
+  for (int base = 0; base < H; base += 2048) {
+    u32x4 xv[4], sv[4];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        wv[v] = ok ? *(const u32x4 *)(wrow + col + 8 * v) : u32x4{0u, 0u, 0u, 0u};
-        router_operand(a, xr_lane, col + 8 * v, xh[v], xl[v]);
-      }
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const float w0 = bf_lo(wv[v][k]), w1 = bf_hi(wv[v][k]);
-          wsq = __builtin_fmaf(w0, w0, wsq);
-          wsq = __builtin_fmaf(w1, w1, wsq);
-        }
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[v]), as_bf16x8(xh[v]), acc, 0, 0, 0);
-        if (gemma)
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[v]), as_bf16x8(xl[v]), acc, 0, 0, 0);
-      }
+    for (int u = 0; u < 4; ++u) {
+      const int h = base + lane * 8 + 512 * u;
+      const int hc = min(h, H - 8);
+      xv[u] = *(const u32x4 *)(xr + hc);
+      sv[u] = gemma ? *(const u32x4 *)(a.router_scale + hc) : u32x4{0u, 0u, 0u, 0u};
+      if (h >= H) xv[u] = u32x4{0u, 0u, 0u, 0u};
     }
-    // D: lane holds experts 4g..4g+3 of the tile for token l16.
+    // x² and (x·scale) are exact in fp32; partial sums per step in fp32 are not, so they
+    // are kept per element pair in fp64 (the sums only feed an error bound and GEMMA's norm).
 #pragma unroll
-    for (int ii = 0; ii < 4; ++ii) s_part[wave][4 * g + ii][l16] = acc[ii];
-    wsq += __shfl_xor(wsq, 16);
-    wsq += __shfl_xor(wsq, 32);
-    if (g == 0) s_wpart[wave][l16] = wsq;
-    __syncthreads();
-    {
-      const int el = tid >> 4, tk = tid & 15;   // 256 threads = 16 experts × 16 tokens
-      const int e = et * 16 + el;
-      if (e < E) {
-        float v = ((s_part[0][el][tk] + s_part[1][el][tk]) + s_part[2][el][tk]) + s_part[3][el][tk];
-        if (a.router_b) v += bf16_bits_to_f32(a.router_b[e]);
-        s_logit[tk][e] = v;
-        if (tk == 0)
-          s_wn[e] = sqrtf(((s_wpart[0][el] + s_wpart[1][el]) + s_wpart[2][el]) + s_wpart[3][el]);
-      }
-    }
-    __syncthreads();
-  }
-
-  // ---- B: per token, candidates → exact logits → top-k ----
-  const double root = gemma ? pow((double)H, -0.5) : 1.0;
-  for (int tl = wave; tl < ntok; tl += 4) {
-    const int t = t0 + tl;
-    const uint16_t *xr = a.xr + (size_t)t * H;
-    // ‖u‖ of the projection input (u = x, or x·scale for GEMMA) and Σx² for GEMMA's norm.
-    double uu = 0.0, xx = 0.0;
-    for (int h = lane * 8; h < H; h += 512) {
-      const u32x4 xv = *(const u32x4 *)(xr + h);
+    for (int u = 0; u < 4; ++u) {
+      double pu = 0.0, px = 0.0;
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        const double xd = bf16_bits_to_f32((xv[k >> 1] >> ((k & 1) * 16)) & 0xFFFF);
-        const double ud = gemma ? xd * (double)bf16_bits_to_f32(a.router_scale[h + k]) : xd;
-        uu = fma(ud, ud, uu);
-        xx = fma(xd, xd, xx);
-      }
-    }
-    uu = wave_sum_f64(uu);
-    xx = wave_sum_f64(xx);
-    const double norm = gemma ? pow(xx / (double)H + (double)a.eps, -0.5) : 1.0;
-    const double fscale = gemma ? norm * root : 1.0;   // logit = fscale · Σ u·w
-    // |fp32 − exact| ≤ fscale·(2·H·2^-23·‖u‖‖w‖) + 2^-22·|logit| (bias add, final scaling).
-    const float cb = (float)(fscale * 2.0 * H * 1.1920928955078125e-07 * sqrt(uu));
-    // K-th largest lower bound.
-    float lb[8], ub[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int e = lane + 64 * j;
-      if (e < E) {
-        const float l = (float)(fscale * (double)s_logit[tl][e]);
-        const float err = cb * s_wn[e] + 2.384185791015625e-07f * fabsf(l) + 1e-30f;
-        lb[j] = l - err;
-        ub[j] = l + err;
-      } else {
-        lb[j] = -INFINITY;
-        ub[j] = -INFINITY;
-      }
-    }
-    uint32_t taken = 0;
-    float theta = INFINITY;
-    for (int r = 0; r < K; ++r) {
-      float bv = -INFINITY;
-      int bi = 0x7FFFFFFF;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int e = lane + 64 * j;
-        if (e < E && !(taken & (1u << j)) && (lb[j] > bv || bi == 0x7FFFFFFF)) { bv = lb[j]; bi = e; }
-      }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(bv, o);
-        const int oi = __shfl_xor(bi, o);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-      }
-      if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-      theta = bv;
-    }
-    // Exact top-k over the candidates {e : ub_e ≥ θ}, processed in passes of ≤ 64.
-    double sel_v[kMaxTopK];
-    int sel_i[kMaxTopK];
-    for (int r = 0; r < K; ++r) { sel_v[r] = -INFINITY; sel_i[r] = 0x7FFFFFFF; }
-    int nsel = 0;
-    for (int j = 0; j < 8; ++j) {
-      const int e = lane + 64 * j;
-      const bool is_c = (e < E) && (ub[j] >= theta);
-      const uint64_t m = __ballot(is_c);
-      const int nc = __popcll(m);
-      if (is_c) s_cand[wave][__popcll(m & ((1ull << lane) - 1ull))] = e;
-      __builtin_amdgcn_wave_barrier();
-      for (int ci = 0; ci < nc; ++ci) {
-        const int ce = s_cand[wave][ci];
-        double v = exact_logit(a, xr, a.router_w + (size_t)ce * H, gemma, norm, root);
-        if (a.router_b) v += (double)bf16_bits_to_f32(a.router_b[ce]);
-        // Insert (v, ce) into the running top-k (descending, ties to the smaller index);
-        // candidates arrive in ascending index order, so a tie never displaces an earlier one.
-        if (nsel < K || v > sel_v[K - 1]) {
-          int pos = min(nsel, K - 1);
-          while (pos > 0 && v > sel_v[pos - 1]) {
-            sel_v[pos] = sel_v[pos - 1];
-            sel_i[pos] = sel_i[pos - 1];
-            --pos;
-          }
-          sel_v[pos] = v;
-          sel_i[pos] = ce;
-          nsel = min(nsel + 1, K);
+        const int sh = (k & 1) * 16;
+        const float xf = bf16_bits_to_f32((xv[u][k >> 1] >> sh) & 0xFFFF);
+        px += (double)(xf * xf);
+        if constexpr (gemma) {
+          const double ud = (double)(xf * bf16_bits_to_f32((sv[u][k >> 1] >> sh) & 0xFFFF));
+          pu = fma(ud, ud, pu);
         }
       }
-      __builtin_amdgcn_wave_barrier();
+      xx += px;
+      uu += gemma ? pu : px;
     }
-    double sg_logit = 0.0;
-    if (a.shared_gate)
-      sg_logit = exact_logit(a, a.x + (size_t)t * H, a.shared_gate, false, 1.0, 1.0);
-    if (lane == 0) finish_token(a, t, sel_v, sel_i, sg_logit);
   }
-
+  uu = wave_sum_f64(uu);
+  xx = wave_sum_f64(xx);
+  TokenScreen ts;
+  ts.norm = gemma ? pow(xx / (double)H + (double)a.eps, -0.5) : 1.0;
+  const double fscale = gemma ? ts.norm * pow((double)H, -0.5) : 1.0;   // logit = fscale·Σu·w
+  // |fp32 − exact| ≤ fscale·(2·H·2^-23·‖u‖‖w‖) + 2^-22·|logit| (bias add, final scaling).
+  const float cb = (float)(fscale * 2.0 * H * 1.1920928955078125e-07 * sqrt(uu));
+  float lb[8], ub[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int e = lane + 64 * j;
+    if (e < E) {
+      const float l = (float)(fscale * (double)lgf(e));
+      const float err = cb * wnf(e) + 2.384185791015625e-07f * fabsf(l) + 1e-30f;
+      lb[j] = l - err;
+      ub[j] = l + err;
+    } else {
+      lb[j] = -INFINITY;
+      ub[j] = -INFINITY;
+    }
+  }
+  uint32_t taken = 0;
+  float theta = INFINITY;
+  for (int r = 0; r < K; ++r) {
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E && !(taken & (1u << j)) && (lb[j] > bv || bi == 0x7FFFFFFF)) { bv = lb[j]; bi = e; }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o);
+      const int oi = __shfl_xor(bi, o);
+      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+    theta = bv;
+  }
+  int nc = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int e = lane + 64 * j;
+    const bool is_c = (e < E) && (ub[j] >= theta);
+    const uint64_t m = __ballot(is_c);
+    if (is_c) cl[nc + __popcll(m & ((1ull << lane) - 1ull))] = e;
+    nc += __popcll(m);
+  }
+  __builtin_amdgcn_wave_barrier();
+  ts.nc = nc;
+  return ts;
 }
 
-// ---- small batches (T ≤ 16): every logit exactly in fp64, one wave per (token, expert) ----
-__global__ __launch_bounds__(256) void logits64_kernel(RouteArgs a) {
+// Exact logit (bias included) of candidate e of token t (one wave).
+template <bool gemma>
+__device__ __forceinline__ double exact_candidate(const RouteArgs &a, int t, int e,
+                                                  const TokenScreen &ts) {
+  const double root = gemma ? pow((double)a.hidden, -0.5) : 1.0;
+  double v = exact_logit<gemma>(a, a.xr + (size_t)t * a.hidden, a.router_w + (size_t)e * a.hidden,
+                                ts.norm, root);
+  if (a.router_b) v += (double)bf16_bits_to_f32(a.router_b[e]);
+  return v;
+}
+
+// ---- large batches ---------------------------------------------------------------------------
+// A: one workgroup per (16-token tile, 16-expert tile), the 4 waves splitting K; writes the
+// screening logits lg32 [T][E] and, from the first token tile, ‖w_e‖.
+template <bool gemma>
+__global__ __launch_bounds__(256) void route_logits_kernel(RouteArgs a) {
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int g = lane >> 4, l16 = lane & 15;
+  const int E = a.experts, T = a.tokens;
+  const int ntiles = (E + 15) / 16;
+  const int tt = blockIdx.x / ntiles, et = blockIdx.x - tt * ntiles;
+  const int t0 = tt * RT_TOK;
+  const int ntok = min(RT_TOK, T - t0);
+  __shared__ float s_part[4][16][16];   // [wave][expert in tile][token]
+  __shared__ float s_wpart[4][16];
+  float wsq;
+  const f32x4 acc = tile_logits<gemma>(a, t0, ntok, et, wave, 4, wsq);
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) s_part[wave][4 * g + ii][l16] = acc[ii];
+  if (g == (l16 >> 2)) s_wpart[wave][l16] = wsq;
+  __syncthreads();
+  const int el = tid >> 4, tk = tid & 15;
+  const int e = et * 16 + el;
+  if (e < E && tk < ntok) {
+    float v = ((s_part[0][el][tk] + s_part[1][el][tk]) + s_part[2][el][tk]) + s_part[3][el][tk];
+    if (a.router_b) v += bf16_bits_to_f32(a.router_b[e]);
+    a.lg32[(size_t)(t0 + tk) * E + e] = v;
+    if (tt == 0 && tk == 0)
+      a.wn[e] = sqrtf(((s_wpart[0][el] + s_wpart[1][el]) + s_wpart[2][el]) + s_wpart[3][el]);
+  }
+}
+
+// B: one wave per token: screen, then the exact logits of its candidates in ascending order.
+template <bool gemma>
+__global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
   const int wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wave;
+  __shared__ int s_cl[4][kMaxExperts];
+  if (t >= a.tokens) return;
+  const float *lg = a.lg32 + (size_t)t * a.experts;
+  const float *wn = a.wn;
+  const TokenScreen ts = screen_token<gemma>(a, t, [&](int e) { return lg[e]; },
+                                      [&](int e) { return wn[e]; }, s_cl[wave]);
+  TopK tk;
+  for (int ci = 0; ci < ts.nc; ++ci) {
+    const int e = s_cl[wave][ci];
+    tk.insert(exact_candidate<gemma>(a, t, e, ts), e, a.top_k);
+  }
+  const double sg = a.shared_gate ? exact_logit<false>(a, a.x + (size_t)t * a.hidden, a.shared_gate, 1.0, 1.0) : 0.0;
+  finish_token(a, t, tk, sg);
+}
+
+// C.
+__global__ __launch_bounds__(1024) void dispatch_kernel(RouteArgs a) {
+  dispatch_batch<16>(a, a.topk_idx);
+}
+
+// ---- small batches (T ≤ 16): every logit exactly in fp64, then one selecting workgroup --------
+// The router rows are spread over many workgroups: one compute unit's load path would take
+// several microseconds to stream even a 32-expert router.
+// A: one wave per (token, expert) pair; expert id E is the shared expert's gate row.
+template <bool gemma>
+__global__ __launch_bounds__(256) void logits64_kernel(RouteArgs a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int E = a.experts, E1 = E + 1, H = a.hidden;
   const int p = blockIdx.x * 4 + wave;
   if (p >= a.tokens * E1) return;
   const int t = p / E1, e = p - t * E1;
   if (e == E && !a.shared_gate) return;
-  const bool gemma = (a.router == R_GEMMA) && e < E;
-  const uint16_t *xr = (e < E ? a.xr : a.x) + (size_t)t * H;
-  double norm = 1.0, root = 1.0;
-  if (gemma) {
-    const int lane = threadIdx.x & 63;
-    double xx = 0.0;
-    for (int h = lane * 8; h < H; h += 512) {
-      const u32x4 xv = *(const u32x4 *)(xr + h);
+  double v;
+  if (e < E) {
+    const uint16_t *xr = a.xr + (size_t)t * H;
+    double norm = 1.0, root = 1.0;
+    if constexpr (gemma) {
+      double xx = 0.0;
+      for (int base = 0; base < H; base += 2048) {
+        u32x4 xv[4];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const double xd = bf16_bits_to_f32((xv[k >> 1] >> ((k & 1) * 16)) & 0xFFFF);
-        xx = fma(xd, xd, xx);
+        for (int u = 0; u < 4; ++u) {
+          const int h = base + lane * 8 + 512 * u;
+          xv[u] = *(const u32x4 *)(xr + min(h, H - 8));
+          if (h >= H) xv[u] = u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          double px = 0.0;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const float xf = bf16_bits_to_f32((xv[u][k >> 1] >> ((k & 1) * 16)) & 0xFFFF);
+            px += (double)(xf * xf);
+          }
+          xx += px;
+        }
       }
+      xx = wave_sum_f64(xx);
+      norm = pow(xx / (double)H + (double)a.eps, -0.5);
+      root = pow((double)H, -0.5);
     }
-    xx = wave_sum_f64(xx);
-    norm = pow(xx / (double)H + (double)a.eps, -0.5);
-    root = pow((double)H, -0.5);
+    v = exact_logit<gemma>(a, xr, a.router_w + (size_t)e * H, norm, root);
+    if (a.router_b) v += (double)bf16_bits_to_f32(a.router_b[e]);
+  } else {
+    v = exact_logit<false>(a, a.x + (size_t)t * H, a.shared_gate, 1.0, 1.0);
   }
-  const uint16_t *wrow = e < E ? a.router_w + (size_t)e * H : a.shared_gate;
-  double v = exact_logit(a, xr, wrow, gemma, norm, root);
-  if (e < E && a.router_b) v += (double)bf16_bits_to_f32(a.router_b[e]);
-  if ((threadIdx.x & 63) == 0) a.lg64[(size_t)t * E1 + e] = v;
+  if (lane == 0) a.lg64[(size_t)t * E1 + e] = v;
 }
 
-// Top-k of every token from the exact logits (one wave per token), then the dispatch.
-__global__ __launch_bounds__(256) void select_kernel(RouteArgs a) {
+// B + C: wave t selects token t's top-k from its exact logits, then the workgroup dispatches.
+__global__ __launch_bounds__(1024) void select_small_kernel(RouteArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int E = a.experts, E1 = E + 1, K = a.top_k;
-  for (int t = wave; t < a.tokens; t += 4) {
-    const double *lg = a.lg64 + (size_t)t * E1;
+  const int E = a.experts, E1 = E + 1, K = a.top_k, T = a.tokens;
+  __shared__ int s_idx[RT_TOK * kMaxTopK];
+  if (wave < T) {
+    const double *lg = a.lg64 + (size_t)wave * E1;
     double v[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int e = lane + 64 * j;
       v[j] = e < E ? lg[e] : -INFINITY;
     }
+    TopK tk;
     uint32_t taken = 0;
-    double sel_v[kMaxTopK];
-    int sel_i[kMaxTopK];
-    for (int r = 0; r < K; ++r) {
-      double bv = -INFINITY;
-      int bi = 0x7FFFFFFF;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int e = lane + 64 * j;
-        if (e < E && !(taken & (1u << j)) && (v[j] > bv || bi == 0x7FFFFFFF)) { bv = v[j]; bi = e; }
-      }
-      // Larger value first, smaller index on ties (attention.metal:270, ReferenceOps.swift:174-176).
+    for (int r = 0; r < kMaxTopK; ++r) {
+      if (r < K) {
+        double bv = -INFINITY;
+        int bi = 0x7FFFFFFF;
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const double ov = __shfl_xor(bv, o);
-        const int oi = __shfl_xor(bi, o);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        for (int j = 0; j < 8; ++j) {
+          const int e = lane + 64 * j;
+          if (e < E && !(taken & (1u << j)) && (v[j] > bv || bi == 0x7FFFFFFF)) { bv = v[j]; bi = e; }
+        }
+        // Larger value first, smaller index on ties (attention.metal:270,
+        // ReferenceOps.swift:174-176).
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+          const double ov = __shfl_xor(bv, o);
+          const int oi = __shfl_xor(bi, o);
+          if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        tk.v[r] = bv;
+        tk.i[r] = bi;
+        if (lane == 0) s_idx[wave * K + r] = bi;
       }
-      if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-      sel_v[r] = bv;
-      sel_i[r] = bi;
     }
-    if (lane == 0) finish_token(a, t, sel_v, sel_i, a.shared_gate ? lg[E] : 0.0);
+    finish_token(a, wave, tk, a.shared_gate ? lg[E] : 0.0);
   }
-  if (a.want_dispatch) {
-    __syncthreads();
-    dispatch_batch(a);
-  }
+  __syncthreads();
+  if (a.want_dispatch) dispatch_batch<16>(a, s_idx);
 }
-
-__global__ __launch_bounds__(256) void dispatch_kernel(RouteArgs a) { dispatch_batch(a); }
 }  // namespace hh
 
 namespace hh {
-// Router + top-k + dispatch: exact fp64 logits then one selecting workgroup when T ≤ 16;
-// the MFMA-screened tiles then the dispatch workgroup otherwise.
 hipError_t launch_route(const RouteArgs &a, hipStream_t s, Timing tm) {
   if (a.tokens <= RT_TOK) {
     const int pairs = a.tokens * (a.experts + 1);
-    hipExtLaunchKernelGGL(logits64_kernel, dim3((pairs + 3) / 4), dim3(256), 0, s, tm.start,
-                          nullptr, 0, a);
+    hipExtLaunchKernelGGL(a.router == R_GEMMA ? logits64_kernel<true> : logits64_kernel<false>,
+                          dim3((pairs + 3) / 4), dim3(256), 0, s, tm.start, nullptr, 0, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipExtLaunchKernelGGL(select_kernel, dim3(1), dim3(256), 0, s, nullptr, tm.stop, 0, a);
+    hipExtLaunchKernelGGL(select_small_kernel, dim3(1), dim3(1024), 0, s, nullptr, tm.stop, 0, a);
     return hipGetLastError();
   }
-  const int tiles = (a.tokens + RT_TOK - 1) / RT_TOK;
-  const bool second = a.want_dispatch != 0;
-  hipExtLaunchKernelGGL(route_kernel, dim3(tiles), dim3(256), 0, s, tm.start,
-                        second ? nullptr : tm.stop, 0, a);
+  const int ttiles = (a.tokens + RT_TOK - 1) / RT_TOK;
+  const int etiles = (a.experts + 15) / 16;
+  const bool third = a.want_dispatch != 0;
+  const bool g = a.router == R_GEMMA;
+  hipExtLaunchKernelGGL(g ? route_logits_kernel<true> : route_logits_kernel<false>, dim3(ttiles * etiles), dim3(256), 0, s, tm.start,
+                        nullptr, 0, a);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || !second) return e;
-  hipExtLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(256), 0, s, nullptr, tm.stop, 0, a);
+  if (e != hipSuccess) return e;
+  hipExtLaunchKernelGGL(g ? route_select_kernel<true> : route_select_kernel<false>, dim3((a.tokens + 3) / 4), dim3(256), 0, s, nullptr,
+                        third ? nullptr : tm.stop, 0, a);
+  e = hipGetLastError();
+  if (e != hipSuccess || !third) return e;
+  hipExtLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, nullptr, tm.stop, 0, a);
   return hipGetLastError();
 }
 // Stand-alone permutation of a given top-k table (hh_permute).
 hipError_t launch_permute(const RouteArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, a);
   return hipGetLastError();
 }
 }  // namespace hh

@@ -153,15 +153,15 @@ ROUTER_CASES = {
 
 
 @pytest.mark.parametrize("name", list(ROUTER_CASES))
-def test_router_indices_bit_exact(torch_dev, ctx, name):
+@pytest.mark.parametrize("T", [5, 96])
+def test_router_indices_bit_exact(torch_dev, ctx, name, T):
     from hydra_amd._lib import check, desc_c, lib
     from hydra_amd.layer import MoELayer
     torch = torch_dev
     desc, zipf = ROUTER_CASES[name]
-    say(f"router {name}")
+    say(f"router {name} T={T}")
     small = desc.replace(intermediate=64, shared_intermediate=64 if desc.shared_intermediate else 0)
     layer = synth.make_layer(small, seed=21, zipf=zipf)
-    T = 96
     x = synth.make_tokens(desc.hidden, T, seed=22)
     L = MoELayer(layer, ctx)
     d = desc_c(small)
@@ -355,21 +355,22 @@ def test_router_near_ties_resolved_exactly(torch_dev, ctx, router):
         W[e] = synth.f32_to_bf16(synth.bf16_to_f32(W[e]) * np.float32(1.5))
         W[e, 5] = keep
     layer["router_weight"] = W
-    T = 64
-    x = synth.make_tokens(desc.hidden, T, seed=62)
+    x_all = synth.make_tokens(desc.hidden, 64, seed=62)
     L = MoELayer(layer, ctx)
     d = desc_c(desc)
-    idx = torch.empty((T, 4), dtype=torch.int32, device="cuda:0")
-    w = torch.empty((T, 4), dtype=torch.float32, device="cuda:0")
-    xd = dev(torch, x)
-    check(lib().hh_router_topk(ctx.handle, C.byref(d), C.byref(L._weights_c), _p(xd), T, None,
-                               _p(idx), _p(w), None))
-    ctx.synchronize()
-    ref_logits = O.router_logits(desc, layer, x)
-    got = idx.cpu().numpy()
-    for t in range(T):
-        if router == F.ROUTER_TOPK_SOFTMAX:
-            ri, _ = O.router_topk_softmax(ref_logits[t], 4)
-        else:
-            ri, _ = O.router_softmax_topk_renorm(ref_logits[t], 4)
-        assert np.array_equal(got[t], ri), (t, got[t], ri)
+    ref_all = O.router_logits(desc, layer, x_all)
+    for T in (64, 8):   # the screened multi-workgroup path and the one-workgroup path
+        x = x_all[:T]
+        idx = torch.empty((T, 4), dtype=torch.int32, device="cuda:0")
+        w = torch.empty((T, 4), dtype=torch.float32, device="cuda:0")
+        xd = dev(torch, x)
+        check(lib().hh_router_topk(ctx.handle, C.byref(d), C.byref(L._weights_c), _p(xd), T,
+                                   None, _p(idx), _p(w), None))
+        ctx.synchronize()
+        got = idx.cpu().numpy()
+        for t in range(T):
+            if router == F.ROUTER_TOPK_SOFTMAX:
+                ri, _ = O.router_topk_softmax(ref_all[t], 4)
+            else:
+                ri, _ = O.router_softmax_topk_renorm(ref_all[t], 4)
+            assert np.array_equal(got[t], ri), (T, t, got[t], ri)
