@@ -64,7 +64,7 @@ constexpr int kMaxTokens = 1 << 16;  // tokens per call
 
 // Scratch carve-up for T tokens of a layer shaped like d. All offsets 256-byte aligned.
 struct Scratch {
-  size_t lg64, lg32, wn, topk_idx, topk_w, slot_w, seg, order, work, n_work, h_hi, h_lo, slot_out, total;
+  size_t ticket, lg64, lg32, wn, topk_idx, topk_w, slot_w, seg, order, work, n_work, h_hi, h_lo, slot_out, total;
   int slots, positions, ldh, max_work, tile_tokens, nt;
 };
 
@@ -92,6 +92,7 @@ Scratch plan(const hh_moe_desc &d, int T) {
     c = align_up(c + bytes, 256);
     return o;
   };
+  s.ticket = take(sizeof(int32_t));   // first: its offset is the same for every T
   s.lg64 = take(sizeof(double) * (size_t)std::min(T, 16) * (E + 1));
   s.lg32 = take(sizeof(float) * (size_t)T * E);
   s.wn = take(sizeof(float) * (size_t)E);
@@ -122,6 +123,8 @@ int ensure_arena(hh_ctx *ctx, size_t bytes) {
   if (hipMalloc(&p, bytes) != hipSuccess) return fail(HH_ENOMEM, "scratch arena allocation failed");
   ctx->arena = (uint8_t *)p;
   ctx->arena_bytes = bytes;
+  // The routing ticket (offset 0) starts at zero; every call leaves it at zero.
+  HH_HIP(hipMemsetAsync(p, 0, 256, ctx->stream));
   return HH_OK;
 }
 
@@ -165,6 +168,7 @@ hh::RouteArgs route_args(const hh_moe_desc &d, const hh_moe_weights *w, uint8_t 
   r.want_dispatch = 1;
   r.eps = d.router_eps;
   r.logits = nullptr;
+  r.ticket = (int32_t *)(base + s.ticket);
   r.lg64 = (double *)(base + s.lg64);
   r.lg32 = (float *)(base + s.lg32);
   r.wn = (float *)(base + s.wn);
@@ -400,7 +404,7 @@ int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
   HH_HIP(hh::launch_gemm(1, d->quant, s.nt, g, ctx->stream, tm));
   if ((rc = phase_timing(ctx, &tm))) return rc;
   HH_HIP(hh::launch_combine(g.slot_out, s.slots, d->hidden, T, y, ctx->stream, tm));
-  ctx->dispatches += 4;
+  ctx->dispatches += (T <= 16 ? 2 : 3) + 3;   // route, gate-up, down, combine
   return HH_OK;
 }
 
@@ -454,7 +458,7 @@ int hh_router_topk(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
   r.shared_w = shared_w;
   if (d->shared_intermediate > 0 && !w->shared_gate) r.shared_gate = nullptr;
   HH_HIP(hh::launch_route(r, ctx->stream));
-  ctx->dispatches += 1;
+  ctx->dispatches += 2;
   return HH_OK;
 }
 

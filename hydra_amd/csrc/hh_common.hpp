@@ -120,6 +120,7 @@ struct RouteArgs {
   int4 *work;                   // [max_work]
   int32_t *n_work;              // [1]
   int32_t max_work;
+  int32_t *ticket;              // [1] workgroup counter of route_small_kernel, 0 between calls
 };
 
 // Optional profiling events of a launch sequence: `start` is attached to the first kernel's

@@ -12,12 +12,12 @@
 //   C. Dispatch: the batch's (token, rank) assignments grouped by expert, stable, plus the
 //      work list of the expert products.
 //
-// Batches of at most 16 tokens skip the screening: logits64_kernel computes every logit in fp64
-// (one wave per (token, expert) pair, spread over many compute units), and select_small_kernel
-// selects and dispatches in one workgroup. Larger batches run A over a (token tile × expert
-// tile) grid (route_logits_kernel), B one wave per token (route_select_kernel) and C in one
-// workgroup (dispatch_kernel). No kernel synchronises
-// with another workgroup: the stream orders the phases.
+// Batches of at most 16 tokens skip the screening: route_small_kernel computes every logit in
+// fp64 (one wave per (token, expert) pair, spread over many compute units) and the workgroup that
+// finishes last (a ticket counter, with release/acquire fences around it) selects and
+// dispatches. Larger batches run A over a (token tile × expert tile) grid (route_logits_kernel),
+// B one wave per token (route_select_kernel) and C in one workgroup (dispatch_kernel), ordered by
+// the stream.
 //
 // Reference: router_topk / router_topk_batch (attention.metal:249, batch.metal:430),
 // gemma_router_topk (gemma.metal:158), ReferenceOps.router (ReferenceOps.swift:173-183),
@@ -508,62 +508,19 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(RouteArgs a) {
   dispatch_batch<16>(a, a.topk_idx);
 }
 
-// ---- small batches (T ≤ 16): every logit exactly in fp64, then one selecting workgroup --------
-// The router rows are spread over many workgroups: one compute unit's load path would take
-// several microseconds to stream even a 32-expert router.
-// A: one wave per (token, expert) pair; expert id E is the shared expert's gate row.
-template <bool gemma>
-__global__ __launch_bounds__(256) void logits64_kernel(RouteArgs a) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int E = a.experts, E1 = E + 1, H = a.hidden;
-  const int p = blockIdx.x * 4 + wave;
-  if (p >= a.tokens * E1) return;
-  const int t = p / E1, e = p - t * E1;
-  if (e == E && !a.shared_gate) return;
-  double v;
-  if (e < E) {
-    const uint16_t *xr = a.xr + (size_t)t * H;
-    double norm = 1.0, root = 1.0;
-    if constexpr (gemma) {
-      double xx = 0.0;
-      for (int base = 0; base < H; base += 2048) {
-        u32x4 xv[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int h = base + lane * 8 + 512 * u;
-          xv[u] = *(const u32x4 *)(xr + min(h, H - 8));
-          if (h >= H) xv[u] = u32x4{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          double px = 0.0;
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            const float xf = bf16_bits_to_f32((xv[u][k >> 1] >> ((k & 1) * 16)) & 0xFFFF);
-            px += (double)(xf * xf);
-          }
-          xx += px;
-        }
-      }
-      xx = wave_sum_f64(xx);
-      norm = pow(xx / (double)H + (double)a.eps, -0.5);
-      root = pow((double)H, -0.5);
-    }
-    v = exact_logit<gemma>(a, xr, a.router_w + (size_t)e * H, norm, root);
-    if (a.router_b) v += (double)bf16_bits_to_f32(a.router_b[e]);
-  } else {
-    v = exact_logit<false>(a, a.x + (size_t)t * H, a.shared_gate, 1.0, 1.0);
-  }
-  if (lane == 0) a.lg64[(size_t)t * E1 + e] = v;
-}
+// ---- small batches (T ≤ 16): every logit exactly in fp64, one launch ---------------------------
+// The router rows are spread over many workgroups (one compute unit's load path would take several
+// microseconds to stream even a 32-expert router); the last workgroup to finish selects and
+// dispatches, so routing a decode step is one kernel launch.
 
-// B + C: wave t selects token t's top-k from its exact logits, then the workgroup dispatches.
-__global__ __launch_bounds__(1024) void select_small_kernel(RouteArgs a) {
+// Top-k of every token from its exact logits (wave w: tokens w, w + NW, ...), then the dispatch.
+template <int NW>
+__device__ __forceinline__ void select_and_dispatch(const RouteArgs &a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int E = a.experts, E1 = E + 1, K = a.top_k, T = a.tokens;
   __shared__ int s_idx[RT_TOK * kMaxTopK];
-  if (wave < T) {
-    const double *lg = a.lg64 + (size_t)wave * E1;
+  for (int t = wave; t < T; t += NW) {
+    const double *lg = a.lg64 + (size_t)t * E1;
     double v[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -593,13 +550,73 @@ __global__ __launch_bounds__(1024) void select_small_kernel(RouteArgs a) {
         if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
         tk.v[r] = bv;
         tk.i[r] = bi;
-        if (lane == 0) s_idx[wave * K + r] = bi;
+        if (lane == 0) s_idx[t * K + r] = bi;
       }
     }
-    finish_token(a, wave, tk, a.shared_gate ? lg[E] : 0.0);
+    finish_token(a, t, tk, a.shared_gate ? lg[E] : 0.0);
   }
   __syncthreads();
-  if (a.want_dispatch) dispatch_batch<16>(a, s_idx);
+  if (a.want_dispatch) dispatch_batch<NW>(a, s_idx);
+}
+
+// A: one wave per (token, expert) pair; expert id E is the shared expert's gate row. B + C: the
+// workgroup that takes the last ticket. Each workgroup releases its logits (fence) before taking
+// a ticket; the last one acquires them (fence) and re-arms the ticket for the next call, which
+// the stream orders after this one.
+template <bool gemma>
+__global__ __launch_bounds__(256) void route_small_kernel(RouteArgs a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int E = a.experts, E1 = E + 1, H = a.hidden;
+  const int p = blockIdx.x * 4 + wave;
+  const int t = p / E1, e = p - t * E1;
+  if (p < a.tokens * E1 && (e < E || a.shared_gate)) {
+    double v;
+    if (e < E) {
+      const uint16_t *xr = a.xr + (size_t)t * H;
+      double norm = 1.0, root = 1.0;
+      if constexpr (gemma) {
+        double xx = 0.0;
+        for (int base = 0; base < H; base += 2048) {
+          u32x4 xv[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int h = base + lane * 8 + 512 * u;
+            xv[u] = *(const u32x4 *)(xr + min(h, H - 8));
+            if (h >= H) xv[u] = u32x4{0u, 0u, 0u, 0u};
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            double px = 0.0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              const float xf = bf16_bits_to_f32((xv[u][k >> 1] >> ((k & 1) * 16)) & 0xFFFF);
+              px += (double)(xf * xf);
+            }
+            xx += px;
+          }
+        }
+        xx = wave_sum_f64(xx);
+        norm = pow(xx / (double)H + (double)a.eps, -0.5);
+        root = pow((double)H, -0.5);
+      }
+      v = exact_logit<gemma>(a, xr, a.router_w + (size_t)e * H, norm, root);
+      if (a.router_b) v += (double)bf16_bits_to_f32(a.router_b[e]);
+    } else {
+      v = exact_logit<false>(a, a.x + (size_t)t * H, a.shared_gate, 1.0, 1.0);
+    }
+    if (lane == 0) a.lg64[(size_t)t * E1 + e] = v;
+  }
+  __shared__ int s_last;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    s_last = atomicAdd(a.ticket, 1) == (int)gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  select_and_dispatch<4>(a);
+  if (threadIdx.x == 0) *a.ticket = 0;
 }
 }  // namespace hh
 
@@ -607,11 +624,8 @@ namespace hh {
 hipError_t launch_route(const RouteArgs &a, hipStream_t s, Timing tm) {
   if (a.tokens <= RT_TOK) {
     const int pairs = a.tokens * (a.experts + 1);
-    hipExtLaunchKernelGGL(a.router == R_GEMMA ? logits64_kernel<true> : logits64_kernel<false>,
-                          dim3((pairs + 3) / 4), dim3(256), 0, s, tm.start, nullptr, 0, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipExtLaunchKernelGGL(select_small_kernel, dim3(1), dim3(1024), 0, s, nullptr, tm.stop, 0, a);
+    hipExtLaunchKernelGGL(a.router == R_GEMMA ? route_small_kernel<true> : route_small_kernel<false>,
+                          dim3((pairs + 3) / 4), dim3(256), 0, s, tm.start, tm.stop, 0, a);
     return hipGetLastError();
   }
   const int ttiles = (a.tokens + RT_TOK - 1) / RT_TOK;
