@@ -15,7 +15,9 @@ namespace hh {
 hipError_t launch_route(const RouteArgs &a, hipStream_t s, Timing tm = {});
 hipError_t launch_permute(const RouteArgs &a, hipStream_t s);
 hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStream_t s, Timing tm);
-int gemm_rows_per_block(int nt, int quant);
+hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t s, Timing tm_up,
+                        Timing tm_down);
+int gemm_rows_per_block(int quant);
 hipError_t launch_combine(const float *slot_out, int slots, int H, int T, float *y, hipStream_t s,
                           Timing tm);
 hipError_t launch_mxfp4_dequant(const uint8_t *blocks, const uint8_t *scales, int64_t n,
@@ -64,13 +66,17 @@ constexpr int kMaxTokens = 1 << 16;  // tokens per call
 
 // Scratch carve-up for T tokens of a layer shaped like d. All offsets 256-byte aligned.
 struct Scratch {
-  size_t ticket, lg64, lg32, wn, topk_idx, topk_w, slot_w, seg, order, work, n_work, h_hi, h_lo, slot_out, total;
+  size_t lg64, lg32, wn, topk_idx, topk_w, slot_w, seg, order, work, n_work, h_hi, h_lo, slot_out;
+  size_t xq, xs, hq, hs, total;
   int slots, positions, ldh, max_work, tile_tokens, nt;
+  int xld, hld;   // MXFP4: row lengths of the fp8 operand terms (multiples of 512)
 };
 
+constexpr int kSmallT = 16;  // batches up to this size take the decode kernels
+
 int token_tile_nt(const hh_moe_desc &d, int T) {
-  // Decode kernel (16-token tiles) while experts see a handful of tokens, the prefill kernel
-  // (32-token tiles) once batches are large enough for experts to fill them.
+  // Prefill kernel token tiles: 16 tokens while experts see a handful of tokens, 32 once batches
+  // are large enough for experts to fill them.
   return (T >= 64) ? 2 : 1;
 }
 
@@ -92,7 +98,6 @@ Scratch plan(const hh_moe_desc &d, int T) {
     c = align_up(c + bytes, 256);
     return o;
   };
-  s.ticket = take(sizeof(int32_t));   // first: its offset is the same for every T
   s.lg64 = take(sizeof(double) * (size_t)std::min(T, 16) * (E + 1));
   s.lg32 = take(sizeof(float) * (size_t)T * E);
   s.wn = take(sizeof(float) * (size_t)E);
@@ -103,9 +108,16 @@ Scratch plan(const hh_moe_desc &d, int T) {
   s.order = take(sizeof(int32_t) * (size_t)s.positions);
   s.work = take(sizeof(int4) * (size_t)s.max_work);
   s.n_work = take(sizeof(int32_t));
-  s.h_hi = take(sizeof(uint16_t) * (size_t)s.positions * s.ldh);
-  s.h_lo = take(sizeof(uint16_t) * (size_t)s.positions * s.ldh);
-  s.slot_out = take(sizeof(float) * (size_t)T * s.slots * H);
+  const bool mx = d.quant == HH_QUANT_MXFP4;
+  s.h_hi = take(mx ? 0 : sizeof(uint16_t) * (size_t)s.positions * s.ldh);
+  s.h_lo = take(mx ? 0 : sizeof(uint16_t) * (size_t)s.positions * s.ldh);
+  s.xld = (int)align_up((size_t)H, 512);
+  s.hld = (int)align_up((size_t)s.ldh, 512);
+  s.xq = take(mx ? (size_t)T * hh::NTX * s.xld : 0);
+  s.xs = take(mx ? (size_t)T * hh::NTX * (s.xld / 32) : 0);
+  s.hq = take(mx ? (size_t)s.positions * hh::NTH * s.hld : 0);
+  s.hs = take(mx ? (size_t)s.positions * hh::NTH * (s.hld / 32) : 0);
+  s.slot_out = take(T > kSmallT ? sizeof(float) * (size_t)T * s.slots * H : 0);
   s.total = c;
   return s;
 }
@@ -123,8 +135,6 @@ int ensure_arena(hh_ctx *ctx, size_t bytes) {
   if (hipMalloc(&p, bytes) != hipSuccess) return fail(HH_ENOMEM, "scratch arena allocation failed");
   ctx->arena = (uint8_t *)p;
   ctx->arena_bytes = bytes;
-  // The routing ticket (offset 0) starts at zero; every call leaves it at zero.
-  HH_HIP(hipMemsetAsync(p, 0, 256, ctx->stream));
   return HH_OK;
 }
 
@@ -168,7 +178,6 @@ hh::RouteArgs route_args(const hh_moe_desc &d, const hh_moe_weights *w, uint8_t 
   r.want_dispatch = 1;
   r.eps = d.router_eps;
   r.logits = nullptr;
-  r.ticket = (int32_t *)(base + s.ticket);
   r.lg64 = (double *)(base + s.lg64);
   r.lg32 = (float *)(base + s.lg32);
   r.wn = (float *)(base + s.wn);
@@ -181,6 +190,11 @@ hh::RouteArgs route_args(const hh_moe_desc &d, const hh_moe_weights *w, uint8_t 
   r.work = (int4 *)(base + s.work);
   r.n_work = (int32_t *)(base + s.n_work);
   r.max_work = s.max_work;
+  if (d.quant == HH_QUANT_MXFP4 && x) {
+    r.xq = base + s.xq;
+    r.xs = base + s.xs;
+    r.xld = s.xld;
+  }
   return r;
 }
 
@@ -329,8 +343,8 @@ int hh_ctx_reserve(hh_ctx *ctx, const hh_moe_desc *d, int32_t max_tokens) {
   if (max_tokens <= 0 || max_tokens > kMaxTokens) return fail(HH_EINVAL, "max_tokens outside 1..65536");
   // The plan for a batch that switches to 64-token tiles can be smaller than for a batch just
   // below the switch; reserve the larger of the two.
-  size_t need = plan(*d, max_tokens).total;
-  if (max_tokens >= 64) need = std::max(need, plan(*d, 63).total);
+  size_t need = 0;
+  for (int t : {max_tokens, std::min(max_tokens, 63)}) need = std::max(need, plan(*d, t).total);
   return ensure_arena(ctx, need);
 }
 
@@ -394,8 +408,30 @@ int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
   g.h_lo = (uint16_t *)(base + s.h_lo);
   g.slot_w = r.slot_w;
   g.slot_out = (float *)(base + s.slot_out);
+  g.y = y;
+  g.xq = r.xq;
+  g.xs = r.xs;
+  g.xld = s.xld;
+  g.hq = base + s.hq;
+  g.hs = base + s.hs;
+  g.hld = s.hld;
 
-  const int rows = hh::gemm_rows_per_block(s.nt, d->quant);
+  if (T <= kSmallT) {
+    // Decode: exact logits → gate-up (selects the top-k itself) → down with the rank-ordered
+    // combine in its epilogue.
+    hh::Timing tm_down, tm_comb;
+    if ((rc = phase_timing(ctx, &tm))) return rc;
+    if ((rc = phase_timing(ctx, &tm_down))) return rc;
+    if ((rc = phase_timing(ctx, &tm_comb))) return rc;
+    HH_HIP(hh::launch_small(d->quant, g, r, ctx->stream, tm, tm_down));
+    if (tm_comb.start) {   // no combine launch: an empty profiled phase keeps the record aligned
+      HH_HIP(hipEventRecord(tm_comb.start, ctx->stream));
+      HH_HIP(hipEventRecord(tm_comb.stop, ctx->stream));
+    }
+    ctx->dispatches += 3;
+    return HH_OK;
+  }
+  const int rows = hh::gemm_rows_per_block(d->quant);
   g.row_tiles = (s.ldh + rows - 1) / rows;
   if ((rc = phase_timing(ctx, &tm))) return rc;
   HH_HIP(hh::launch_gemm(0, d->quant, s.nt, g, ctx->stream, tm));
@@ -404,7 +440,7 @@ int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
   HH_HIP(hh::launch_gemm(1, d->quant, s.nt, g, ctx->stream, tm));
   if ((rc = phase_timing(ctx, &tm))) return rc;
   HH_HIP(hh::launch_combine(g.slot_out, s.slots, d->hidden, T, y, ctx->stream, tm));
-  ctx->dispatches += (T <= 16 ? 2 : 3) + 3;   // route, gate-up, down, combine
+  ctx->dispatches += 6;   // route logits, select, dispatch, gate-up, down, combine
   return HH_OK;
 }
 
@@ -452,6 +488,7 @@ int hh_router_topk(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
   if (rc) return rc;
   hh::RouteArgs r = route_args(*d, w, ctx->arena, s, x_router, x_router, T);
   r.want_dispatch = 0;
+  r.xq = nullptr;   // no expert products follow
   r.logits = logits;
   r.topk_idx = topk_idx;
   r.topk_w = topk_w;

@@ -48,6 +48,55 @@ __device__ __forceinline__ bf16x8 mxfp4_to_bf16(uint32_t w, float scale) {
   return as_bf16x8(r);
 }
 
+// ---- fp8 e4m3 activation terms for the scaled MXFP4 products ---------------------------------
+// A block of 32 activations (of one token, along K) is written as NTERM fp8 e4m3 terms with an
+// e8m0 scale each: v ≈ Σ_t q_t·2^(b_t-127). b_0 puts the block's largest magnitude in [128, 256)
+// and b_t = b_0 - 4t; each term takes the exact residual of the previous ones (r − dec(q)·2^b is
+// exact in fp32), so NTERM terms keep ~4·NTERM significant bits of every element not far below the
+// block maximum: 2 terms reproduce a bf16 element exactly when it is ≥ 2^-13 of the block maximum,
+// 3 terms keep an fp32 activation to ~2^-13 relative. The block is spread over the 4 lanes
+// l, l^16, l^32, l^48 (lane groups of a wave), 8 values each; the result depends only on the 32
+// values, not on how they are spread.
+constexpr int NTX = 2;   // terms of the expert input x
+constexpr int NTH = 3;   // terms of the activation h
+
+template <int NTERM>
+__device__ __forceinline__ void quant_block(const float (&v)[8], uint32_t (&q)[NTERM][2],
+                                            uint32_t (&sb)[NTERM]) {
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = fmaxf(amax, __shfl_xor(amax, 16));
+  amax = fmaxf(amax, __shfl_xor(amax, 32));
+  const int eb = (int)((__float_as_uint(amax) >> 23) & 0xFF);   // biased exponent (0: zero/tiny)
+  const int b0 = eb > 7 ? eb - 7 : 0;
+  float r[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = v[i];
+#pragma unroll
+  for (int t = 0; t < NTERM; ++t) {
+    const int bt = b0 - 4 * t > 0 ? b0 - 4 * t : 0;
+    sb[t] = (uint32_t)bt;
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = fminf(fmaxf(__builtin_amdgcn_ldexpf(r[i], 127 - bt), -448.f), 448.f);
+    int w0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+    w0 = __builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], w0, true);
+    int w1 = __builtin_amdgcn_cvt_pk_fp8_f32(y[4], y[5], 0, false);
+    w1 = __builtin_amdgcn_cvt_pk_fp8_f32(y[6], y[7], w1, true);
+    q[t][0] = (uint32_t)w0;
+    q[t][1] = (uint32_t)w1;
+    if (t + 1 < NTERM) {
+      const float d[8] = {__builtin_amdgcn_cvt_f32_fp8(w0, 0), __builtin_amdgcn_cvt_f32_fp8(w0, 1),
+                          __builtin_amdgcn_cvt_f32_fp8(w0, 2), __builtin_amdgcn_cvt_f32_fp8(w0, 3),
+                          __builtin_amdgcn_cvt_f32_fp8(w1, 0), __builtin_amdgcn_cvt_f32_fp8(w1, 1),
+                          __builtin_amdgcn_cvt_f32_fp8(w1, 2), __builtin_amdgcn_cvt_f32_fp8(w1, 3)};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) r[i] -= __builtin_amdgcn_ldexpf(d[i], bt - 127);
+    }
+  }
+}
+
 // ---- gated activations (device twins of the oracle's act_pair) ------------------------------
 __device__ __forceinline__ float activate(int act, float g, float u, float alpha, float limit) {
   if (act == A_SWIGLU_OAI) {
@@ -88,12 +137,17 @@ struct GemmArgs {
   int32_t row_tiles;            // workgroup row tiles along the output dimension
   int32_t pad2;
   const uint16_t *x;            // bf16 [T][H]
-  const int32_t *order;         // [positions] slot id (t·slots + r) of each permuted position
+  const int32_t *order;         // [positions] slot id (t·slots + r) of each permuted position (T > 16)
   const int4 *work;             // [max_work] {expert (E = shared), pos0, n, 0}
   const int32_t *n_work;        // device count of valid work items
-  uint16_t *h_hi, *h_lo;        // bf16 [positions][ldh]: activation, hi + lo split
+  uint16_t *h_hi, *h_lo;        // bf16 [T·slots][ldh]: activation of each slot, hi + lo split
+  // MXFP4 (scaled fp4 × fp8 products): the operands as fp8 e4m3 terms with e8m0 block scales.
+  const uint8_t *xq, *xs;       // x: [T][NTX][xld] bytes, scales [T][NTX][xld/32]
+  uint8_t *hq, *hs;             // h: [T·slots][NTH][hld] bytes, scales [T·slots][NTH][hld/32]
+  int32_t xld, hld;             // row lengths (multiples of 128)
   const float *slot_w;          // fp32 [T·slots] routing weight of each slot
-  float *slot_out;              // fp32 [T·slots][H]
+  float *slot_out;              // fp32 [T·slots][H] (T > 16)
+  float *y;                     // fp32 [T][H] layer output (written directly by the decode path)
 };
 
 struct RouteArgs {
@@ -108,6 +162,8 @@ struct RouteArgs {
   float eps;
   double *logits;               // fp64 [T][K] exact logits of the selected experts, or null
   double *lg64;                 // fp64 [T][E+1] exact logits (batches of ≤ 16 tokens; column E: shared gate)
+  uint8_t *xq, *xs;             // MXFP4 layers: x as fp8 terms (GemmArgs::xq), or null
+  int32_t xld;
   float *lg32;                  // fp32 [T][E] screening logits (batches above 16 tokens)
   float *wn;                    // fp32 [E] router row norms
   int32_t *topk_idx;            // [T][K]
@@ -120,7 +176,6 @@ struct RouteArgs {
   int4 *work;                   // [max_work]
   int32_t *n_work;              // [1]
   int32_t max_work;
-  int32_t *ticket;              // [1] workgroup counter of route_small_kernel, 0 between calls
 };
 
 // Optional profiling events of a launch sequence: `start` is attached to the first kernel's

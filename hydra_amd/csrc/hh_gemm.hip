@@ -1,40 +1,53 @@
 // hh_gemm.hip — grouped expert products on gfx950 MFMA, shared by decode and prefill.
 //
-// Two kernels per weight format:
-//   PH_UP   : h[p][i] = act(gate_i · x_t + b, up_i · x_t + b) for every permuted position p
-//             (token t, rank r) of an expert, stored as bf16 hi + lo so the down product sees
-//             the fp32 activation to ~2^-17 relative;
-//   PH_DOWN : slot[t·slots + r][j] = w(t, r) · (down_j · h[p] + b_j), one slot per (token,
-//             rank); the combine then sums slots in rank order.
+// Two products per layer:
+//   PH_UP   : h[s][i] = act(gate_i · x_t + b, up_i · x_t + b) for every slot s = t·slots + r
+//             (token t, rank r; rank `top_k` is the shared expert), stored as bf16 hi + lo so
+//             the down product sees the fp32 activation to ~2^-17 relative;
+//   PH_DOWN : slot value w(t, r) · (down_j · h[s] + b_j); the slots of a token are summed in rank
+//             order into y.
 //
-// Work decomposition. A 1-D grid of (row tile × work item) workgroups of 4 waves. A work item
-// is (expert, first position, tokens ≤ 16·NT) from the device-side dispatch; a wave owns RT
-// tiles of 16 output rows and NT token tiles of 16, and walks the whole K dimension in a fixed
-// order with v_mfma_f32_16x16x32_bf16. The block index is remapped so that consecutive work
-// items of one row tile (the token tiles of one expert, which share its weights) run on the
-// same XCD and hit the same L2.
+// Canonical arithmetic. Every output element (row j, slot s) is TWO accumulation chains over the
+// K dimension, summed at the end (acc_even + acc_odd): chain p takes the chunks c ≡ p (mod 2) in
+// increasing order, each chunk a fixed sequence of v_mfma_f32_16x16x32_bf16 steps (MXFP4/BF16:
+// 128-column chunks, 4 steps; MLX: one 64-column affine group, 2 steps into a group partial P,
+// then acc = fma(s, P, acc), acc = fma(b, Σx, acc)). Two chains halve the dependent-MFMA latency
+// of a decode wave, which owns a single 16-row tile. Decode and prefill kernels differ only in
+// how rows and tokens are tiled over waves and how the B operand reaches the registers; each
+// output element sees the same MFMA sequence with the same operands, so a T-token call equals
+// T one-token calls bit for bit. No split-K across waves, no atomics.
 //
-// Bit-exactness of prefill against token-by-token decode: every output element is produced by
-// the same sequence of MFMAs with the same operands whatever T, NT, RT or the tile placement
-// (no split-K, no atomics, fixed K order, rank-ordered combine); padding token lanes read a
-// valid row and are never stored.
+// Kernels:
+//   up_small / down_small (T ≤ 16, decode): up_small selects the top-k itself from the exact
+//     fp64 logits (every workgroup redundantly, hh_select.hpp), takes the u-th distinct expert of
+//     the batch (in order of first appearance in the (token, rank) table), and computes 32
+//     intermediates of it for all its tokens: 4 waves = {gate, up} × 2 tiles of 16 rows, each
+//     wave issuing its whole weight stream at once (one 16-byte load per lane per chunk), the
+//     tokens' x rows staged in LDS. down_small computes 16 hidden rows of one token for all of
+//     its slots (one wave per slot) and sums them in rank order in the epilogue: no slot buffer,
+//     no combine launch.
+//   prefill_gemm (T > 16): a work list of (expert, first position, ≤ 16·NT tokens) from the
+//     device-side dispatch; 4 waves on different row tiles share the B chunk staged in LDS;
+//     slot values go to slot_out and combine_kernel sums them in rank order.
 //
 // MFMA operand mapping (16x16x32, lane l, lane group g = l/16): A lane l supplies row l%16,
 // B lane l supplies token column l%16, each with 8 consecutive K values; D lane l holds rows
 // 4g..4g+3 of column l%16. The K slots are assigned per format:
-//   MXFP4, BF16: chunk c of 128 columns; MFMA s∈0..3 takes lane group g's columns
-//                128c + 32g + 8s .. +8 (g's 16-byte MXFP4 block 4c+g, or its 64 bytes of bf16)
-//   MLX4/MLX8  : chunk c = affine group c (64 columns); MFMA j∈0..1 takes columns
-//                64c + 16g + 8j .. +8, so both MFMAs stay inside one group and the affine
+//   MXFP4, BF16: chunk c of 128 columns; MFMA step v∈0..3 takes lane group g's columns
+//                128c + 32g + 8v .. +8 (g's 16-byte MXFP4 block 4c+g, or its 64 bytes of bf16)
+//   MLX4/MLX8  : chunk c = affine group c (64 columns); step v∈0..1 takes columns
+//                64c + 16g + 8v .. +8, so both steps stay inside one group and the affine
 //                factorisation s·Σq·x + b·Σx applies per group.
 //
 // Reference kernels replaced: mxfp4_gemv_vectorized (mxfp4.metal:119), mxfp4_gemm_gathered /
 // mxfp4_gemm_tiled (batch.metal:96, tiled.metal:127), bf16_gemv (dense.metal:14),
 // mlx_affine_gemv_t / mlx_affine_gemm_t (gemma.metal:248, :460), swiglu(_batch),
-// qwen_silu_multiply, gelu_mul, write_expert_scaled, scatter_expert(_scaled).
+// qwen_silu_multiply, gelu_mul, write_expert_scaled, scatter_expert(_scaled), sum_expert_slices.
 #include "hh_common.hpp"
+#include "hh_select.hpp"
 
 #include <algorithm>
+#include <mutex>
 
 namespace hh {
 
@@ -87,6 +100,18 @@ template <> struct Fmt<Q_MXFP4> {
   __device__ static bool lane_valid(int c, int g, int K) { return 128 * c + 32 * g < K; }
 };
 
+// ---- MXFP4 blocks without their scales (decode kernels stage a tile's scales in LDS) ----------
+constexpr int Q_MXFP4_W = 4;
+template <> struct Fmt<Q_MXFP4_W> {
+  static constexpr int CHUNK = 128, NB = 4;
+  struct A { u32x4 w; };
+  struct Row { const uint8_t *w; };
+  __device__ static void load(A &a, const Row &rw, int c, int g, int K) {
+    a.w = *(const u32x4 *)(rw.w + min(4 * c + g, K / 32 - 1) * 16);
+  }
+  __device__ static bool lane_valid(int c, int g, int K) { return 128 * c + 32 * g < K; }
+};
+
 // ---- BF16: 128-column chunks, 64 bytes per lane ---------------------------------------------
 template <> struct Fmt<Q_BF16> {
   static constexpr int CHUNK = 128, NB = 4;
@@ -104,12 +129,16 @@ template <> struct Fmt<Q_BF16> {
 };
 
 // ---- MLX affine: 64-column chunks (one group) ------------------------------------------------
+// The lane's stage also carries its row's group scale and bias (bf16 pair); the D rows' values
+// are fetched from the lanes of those rows by shuffle (affine_sb).
 template <int BITS> struct FmtMLX {
   static constexpr int CHUNK = 64, NB = 2;
-  struct A { uint32_t w[BITS / 2]; };  // 4-bit: 2 words (16 values); 8-bit: 4 words
-  struct Row { const uint8_t *w; };
-  __device__ static Row row(const uint8_t *words, int r, int K) {
-    return {words + (size_t)r * (K * BITS / 8)};
+  struct A { uint32_t w[BITS / 2]; uint32_t sb; };  // 4-bit: 2 words (16 values); 8-bit: 4 words
+  struct Row { const uint8_t *w; const uint16_t *sc, *bi; };
+  __device__ static Row row(const uint8_t *words, const uint8_t *scales, const uint8_t *biases,
+                            int r, int K) {
+    return {words + (size_t)r * (K * BITS / 8), (const uint16_t *)scales + (size_t)r * (K / 64),
+            (const uint16_t *)biases + (size_t)r * (K / 64)};
   }
   __device__ static void load(A &a, const Row &rw, int c, int g, int K) {
     const uint8_t *p = rw.w + (64 * c + 16 * g) * BITS / 8;
@@ -120,6 +149,7 @@ template <int BITS> struct FmtMLX {
       u32x4 v = *(const u32x4 *)p;
       a.w[0] = v[0]; a.w[1] = v[1]; a.w[2] = v[2]; a.w[3] = v[3];
     }
+    a.sb = (uint32_t)rw.sc[c] | ((uint32_t)rw.bi[c] << 16);
   }
   __device__ static bf16x8 decode(const A &a, int j) {
     if constexpr (BITS == 4) return mlx4_to_bf16(a.w[j]);
@@ -130,7 +160,9 @@ template <int BITS> struct FmtMLX {
 template <> struct Fmt<Q_MLX4> : FmtMLX<4> {};
 template <> struct Fmt<Q_MLX8> : FmtMLX<8> {};
 
-// ---- the kernel -------------------------------------------------------------------------------
+template <int FMT> constexpr bool is_mlx() { return FMT == Q_MLX4 || FMT == Q_MLX8; }
+
+// ---- shared pieces of the canonical arithmetic -------------------------------------------------
 // Σ of one value held by the 4 lane groups of a token column, in a fixed pairing:
 // (g0 + g1) + (g2 + g3), identical in every lane.
 __device__ __forceinline__ float sum_lane_groups(float v) {
@@ -150,34 +182,179 @@ __device__ __forceinline__ float sum8_bf16(const u32x4 &v) {
   return s;
 }
 
-// Σ of the group's 64 B values of one token column (x, or h_hi + h_lo) from the lane's 2×NH
-// vectors, in a fixed order (hi then lo per MFMA step, steps in order), then across the lane
-// groups. Shared by every kernel so the affine bias term is computed identically.
-template <int NH>
-__device__ __forceinline__ float group_sum(const u32x4 (&bv)[NH][2]) {
-  float v = 0.f;
-#pragma unroll
-  for (int jj = 0; jj < 2; ++jj) {
-    v += sum8_bf16(bv[0][jj]);
-    if (NH > 1) v += sum8_bf16(bv[NH - 1][jj]);
+// One 16-row A tile of a wave: the lane's weight row.
+template <int FMT> struct ATile {
+  typename Fmt<FMT>::Row row;
+};
+
+// Tiles of a wave whose first output row is rb: PH_UP takes RT gate tiles then RT up tiles of
+// intermediates rb + 16q, PH_DOWN RT tiles of hidden rows rb + 16q. Rows past out_dim are
+// clamped into the matrix (their results are never stored).
+// One 16-row A tile: output rows r0 .. r0+15 (lane l16 takes r0 + l16); PH_UP picks the gate
+// (is_up false) or the up matrix.
+template <int PH, int FMT>
+__device__ __forceinline__ ATile<FMT> tile_of(const uint8_t *blob, const ExpertGroup &grp, int r0, bool is_up,
+                                              int K, int l16) {
+  ATile<FMT> t;
+  const int orow = r0 + l16;
+  const int I = grp.inter;
+  if constexpr (FMT == Q_MXFP4) {
+    // GPT-OSS gate_up rows interleave gate and up (ReferenceLayer.swift:11).
+    if (PH == PH_UP) t.row = Fmt<FMT>::row(blob + grp.off[0], blob + grp.off[1], 2 * orow + (is_up ? 1 : 0), K);
+    else t.row = Fmt<FMT>::row(blob + grp.off[3], blob + grp.off[4], orow, K);
+  } else if constexpr (FMT == Q_MXFP4_W) {
+    t.row.w = blob + grp.off[PH == PH_UP ? 0 : 3] + (size_t)(PH == PH_UP ? 2 * orow + (is_up ? 1 : 0) : orow) * (K / 2);
+  } else if constexpr (FMT == Q_BF16) {
+    // Gemma gate_up: gate = rows 0..I-1, up = rows I..2I-1 (Gemma4Weights.swift:107-112).
+    if (PH == PH_UP) t.row = Fmt<FMT>::row(blob + grp.off[0], orow + (is_up ? I : 0), K);
+    else t.row = Fmt<FMT>::row(blob + grp.off[1], orow, K);
+  } else {
+    const int mat = (PH == PH_UP) ? (is_up ? 1 : 0) : 2;
+    t.row = Fmt<FMT>::row(blob + grp.off[3 * mat], blob + grp.off[3 * mat + 1], blob + grp.off[3 * mat + 2],
+                          orow, K);
   }
-  return sum_lane_groups(v);
+  return t;
 }
 
-// The 4 K partials of an output element, summed in partial order.
-__device__ __forceinline__ f32x4 sum_partials4(const f32x4 &p0, const f32x4 &p1, const f32x4 &p2,
-                                               const f32x4 &p3) {
+template <int PH, int FMT, int RT>
+__device__ __forceinline__ void wave_tiles(ATile<FMT> (&t)[(PH == PH_UP ? 2 : 1) * RT],
+                                           const uint8_t *blob, const ExpertGroup &grp, int rb,
+                                           int out_dim, int K, int l16) {
+  constexpr int NM = (PH == PH_UP ? 2 : 1) * RT;
+#pragma unroll
+  for (int m = 0; m < NM; ++m)
+    t[m] = tile_of<PH, FMT>(blob, grp, min(rb + 16 * (m % RT), out_dim - 16), (PH == PH_UP) && (m >= RT), K, l16);
+}
+
+// The MFMA sequence of chunk c for NM A tiles × NT token tiles. `bv(st, hh, v)` returns the
+// lane's 8 B values of token tile st, term hh (x | h_hi, h_lo), step v, at columns
+// Fmt::bcol(c, g, K) + 8v.
+template <int FMT, int NM, int NT, int NH, class BV>
+__device__ __forceinline__ void chunk_mfma(f32x4 (&acc)[NM][NT], const typename Fmt<FMT>::A (&w)[NM],
+                                           const ATile<FMT> (&at)[NM], BV bv, int c, int g, int K) {
+  using F = Fmt<FMT>;
+  if constexpr (!is_mlx<FMT>()) {
+    const bool ok = F::lane_valid(c, g, K);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      u32x4 b[NT][NH];
+#pragma unroll
+      for (int st = 0; st < NT; ++st)
+#pragma unroll
+        for (int hh = 0; hh < NH; ++hh) b[st][hh] = bv(st, hh, v);
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        bf16x8 av;
+        if constexpr (FMT == Q_MXFP4) av = mxfp4_to_bf16(ok ? w[m].w[v] : 0u, e8m0_to_f32(w[m].s));
+        else av = as_bf16x8(ok ? w[m].w[v] : u32x4{0u, 0u, 0u, 0u});
+#pragma unroll
+        for (int st = 0; st < NT; ++st)
+#pragma unroll
+          for (int hh = 0; hh < NH; ++hh) acc[m][st] = mfma(av, as_bf16x8(b[st][hh]), acc[m][st]);
+      }
+    }
+  } else {
+    u32x4 b[NT][NH][2];
+#pragma unroll
+    for (int st = 0; st < NT; ++st)
+#pragma unroll
+      for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+        for (int v = 0; v < 2; ++v) b[st][hh][v] = bv(st, hh, v);
+    f32x4 P[NM][NT];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int st = 0; st < NT; ++st) P[m][st] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int v = 0; v < 2; ++v)
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        const bf16x8 av = F::decode(w[m], v);
+#pragma unroll
+        for (int st = 0; st < NT; ++st)
+#pragma unroll
+          for (int hh = 0; hh < NH; ++hh) P[m][st] = mfma(av, as_bf16x8(b[st][hh][v]), P[m][st]);
+      }
+    // Σ of the group's 64 B values of each token column (x, or h_hi + h_lo), from the operands
+    // in registers: 16 per lane in a fixed order (hi then lo per step, steps in order), then
+    // across the lane groups.
+    float gsum[NT];
+#pragma unroll
+    for (int st = 0; st < NT; ++st) {
+      float s = 0.f;
+#pragma unroll
+      for (int v = 0; v < 2; ++v) {
+        s += sum8_bf16(b[st][0][v]);
+        if (NH > 1) s += sum8_bf16(b[st][NH - 1][v]);
+      }
+      gsum[st] = sum_lane_groups(s);
+    }
+    // acc += s·P + b·Σ per D row (affine factorisation, gemma.metal:234-236); D row 4g + ii is
+    // the A row of lane 4g + ii.
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const uint32_t sbv = (uint32_t)__shfl((int)w[m].sb, 4 * g + ii);
+        const float sc = bf16_bits_to_f32(sbv & 0xFFFF);
+        const float bi = bf16_bits_to_f32(sbv >> 16);
+#pragma unroll
+        for (int st = 0; st < NT; ++st) {
+          acc[m][st][ii] = __builtin_fmaf(sc, P[m][st][ii], acc[m][st][ii]);
+          acc[m][st][ii] = __builtin_fmaf(bi, gsum[st], acc[m][st][ii]);
+        }
+      }
+  }
+}
+
+// Weight stream of one wave over its chunks c = c0, c0 + cs, c0 + 2·cs, ... < nch with a DA-deep
+// register ring: the A operand of the next DA chunks is in flight while a chunk is computed; a
+// wave with at most DA chunks issues its whole stream at once. The loop body is instantiated DA
+// times. Refills are issued only when another round follows (a round's refills past the last
+// chunk reload it, clamped, so the rounds before the last need no per-load test): a duplicate
+// load costs as much of the address/L1 path as a real one.
+template <int FMT, int NM, int DA> struct AStream {
+  typename Fmt<FMT>::A s[DA][NM];
+  int c0, cs, n;   // first chunk, chunk stride, chunks of this wave
+  __device__ __forceinline__ AStream(int first, int stride, int nch)
+      : c0(first), cs(stride), n(nch > first ? (nch - first + stride - 1) / stride : 0) {}
+  __device__ __forceinline__ void load(int slot, const ATile<FMT> (&at)[NM], int i, int nch, int g, int K) {
+    const int c = min(c0 + cs * min(i, max(n - 1, 0)), nch - 1);
+#pragma unroll
+    for (int m = 0; m < NM; ++m) Fmt<FMT>::load(s[slot][m], at[m].row, c, g, K);
+  }
+  __device__ __forceinline__ void fill(const ATile<FMT> (&at)[NM], int nch, int g, int K) {
+#pragma unroll
+    for (int u = 0; u < DA; ++u) load(u, at, u, nch, g, K);
+  }
+  // Runs this wave's chunks through `body(stage, c)`.
+  template <class Body>
+  __device__ __forceinline__ void run(const ATile<FMT> (&at)[NM], int nch, int g, int K, Body body) {
+    for (int i0 = 0; i0 < n; i0 += DA) {
+      const bool more = i0 + DA < n;
+#pragma unroll
+      for (int u = 0; u < DA; ++u) {
+        if (i0 + u < n) body(s[u], c0 + cs * (i0 + u));
+        if (more) load(u, at, i0 + u + DA, nch, g, K);
+      }
+    }
+  }
+};
+
+// acc = p0 + p1 per element (the two chains of the canonical arithmetic).
+__device__ __forceinline__ f32x4 sum_chains(const f32x4 &p0, const f32x4 &p1) {
   f32x4 r;
 #pragma unroll
-  for (int ii = 0; ii < 4; ++ii) r[ii] = ((p0[ii] + p1[ii]) + p2[ii]) + p3[ii];
+  for (int ii = 0; ii < 4; ++ii) r[ii] = p0[ii] + p1[ii];
   return r;
 }
 
-// Gate-up epilogue of 4 intermediates i0..i0+3 of position `pos`: bias, activation, bf16 hi/lo.
+// Activations of 4 intermediates i0..i0+3: bias (GPT-OSS gate_up bias, interleaved like the
+// rows) and the gated activation.
 template <int FMT>
-__device__ __forceinline__ void up_epilogue(const GemmArgs &a, const uint8_t *blob,
-                                            const ExpertGroup &grp, int i0, int pos,
-                                            const f32x4 &gate, const f32x4 &up) {
+__device__ __forceinline__ f32x4 up_values(const GemmArgs &a, const uint8_t *blob, const ExpertGroup &grp,
+                                           int i0, const f32x4 &gate, const f32x4 &up) {
   float gb[4] = {0.f, 0.f, 0.f, 0.f}, ub[4] = {0.f, 0.f, 0.f, 0.f};
   if (FMT == Q_MXFP4 && a.expert_bias) {
     const uint16_t *bias = (const uint16_t *)(blob + grp.off[2]);
@@ -187,25 +364,37 @@ __device__ __forceinline__ void up_epilogue(const GemmArgs &a, const uint8_t *bl
       ub[ii] = bf16_bits_to_f32(bias[2 * (i0 + ii) + 1]);
     }
   }
+  f32x4 y;
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) y[ii] = activate(a.act, gate[ii] + gb[ii], up[ii] + ub[ii], a.alpha, a.limit);
+  return y;
+}
+
+// Gate-up epilogue of 4 intermediates i0..i0+3 of slot `slot`: bias, activation, bf16 hi/lo.
+template <int FMT>
+__device__ __forceinline__ void up_epilogue(const GemmArgs &a, const uint8_t *blob,
+                                            const ExpertGroup &grp, int i0, int slot,
+                                            const f32x4 &gate, const f32x4 &up) {
+  const f32x4 yv = up_values<FMT>(a, blob, grp, i0, gate, up);
   uint32_t hi[4], lo[4];
 #pragma unroll
   for (int ii = 0; ii < 4; ++ii) {
-    const float y = activate(a.act, gate[ii] + gb[ii], up[ii] + ub[ii], a.alpha, a.limit);
+    const float y = yv[ii];
     hi[ii] = f32_to_bf16_bits(y);
     lo[ii] = f32_to_bf16_bits(y - bf16_bits_to_f32(hi[ii]));
   }
-  const size_t o = (size_t)pos * a.ldh + i0;
+  const size_t o = (size_t)slot * a.ldh + i0;
   *(u32x2 *)(a.h_hi + o) = u32x2{hi[0] | (hi[1] << 16), hi[2] | (hi[3] << 16)};
   *(u32x2 *)(a.h_lo + o) = u32x2{lo[0] | (lo[1] << 16), lo[2] | (lo[3] << 16)};
 }
 
-// Down epilogue of hidden rows h0..h0+3 of position `pos`: bias, routing weight, slot store.
+// Slot values of hidden rows h0..h0+3: routing weight × (product + bias)
+// (write_expert_scaled, dense.metal:131-145).
 template <int FMT>
-__device__ __forceinline__ void down_epilogue(const GemmArgs &a, const uint8_t *blob,
-                                              const ExpertGroup &grp, int h0, int pos,
-                                              const f32x4 &r) {
-  const int slot_id = a.order[pos];
-  const float w = a.slot_w[slot_id];
+__device__ __forceinline__ f32x4 down_value(const GemmArgs &a, const uint8_t *blob,
+                                            const ExpertGroup &grp, int h0, int slot,
+                                            const f32x4 &r) {
+  const float w = a.slot_w[slot];
   float db[4] = {0.f, 0.f, 0.f, 0.f};
   if (FMT == Q_MXFP4 && a.expert_bias) {
     const uint16_t *bias = (const uint16_t *)(blob + grp.off[5]);
@@ -215,295 +404,529 @@ __device__ __forceinline__ void down_epilogue(const GemmArgs &a, const uint8_t *
   f32x4 o;
 #pragma unroll
   for (int ii = 0; ii < 4; ++ii) o[ii] = w * (r[ii] + db[ii]);
-  *(f32x4 *)(a.slot_out + (size_t)slot_id * a.hidden + h0) = o;
+  return o;
 }
 
-// KS = K partials per output element: partial p accumulates chunks c ≡ p (mod KS) in increasing
-// order and the partials are summed in p order. The workgroup's 4 waves are 4/KS row groups ×
-// KS partials. Every variant used on one layer shares KS, so a token's result does not depend
-// on which variant (decode or prefill tiling) computed it.
-//
-// Pipeline: the weight (A) operand of the next DA chunks and the B operand of the next DB
-// chunks are in flight while a chunk is computed.
-//
-// TP > 0 (decode): the B rows of up to TP tokens are staged once per workgroup in LDS
-// ([NH][TP][K] bf16, dynamic shared memory) and read from there, so the vector memory unit
-// only carries weight bytes; a work item with more tokens takes several passes.
-template <int PH, int FMT, int RT, int NT, int DA, int DB, int KS, int TP>
-__global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
-  using F = Fmt<FMT>;
-  constexpr bool MLX = (FMT == Q_MLX4 || FMT == Q_MLX8);
-  constexpr int NM = (PH == PH_UP) ? 2 * RT : RT;   // A matrices (row tiles) per wave
-  constexpr int NBV = F::NB;                          // B vectors per token tile per chunk
-  constexpr int NH = (PH == PH_UP) ? 1 : 2;           // B operand terms (x | h_hi, h_lo)
-  constexpr int RG = 4 / KS;                          // row groups per workgroup
-  constexpr int ROWS = RG * 16 * RT;                  // output rows per workgroup
-  constexpr int TOK = TP > 0 ? TP : 16 * NT;          // tokens per pass
-  static_assert(KS == 1 || KS == 2 || KS == 4, "KS divides the 4 waves");
-  static_assert(TP == 0 || (NT == 1 && TP <= 16), "LDS-staged B uses one 16-column tile");
-  extern __shared__ __align__(16) uint16_t s_b[];     // [NH][TP][K] when TP > 0
-  static_assert(DA % DB == 0, "the B ring depth divides the A ring depth");
-
-  // XCD-aware block order: hardware places block b on XCD b % 8; give each XCD a contiguous
-  // range of logical ids, logical = row_tile · max_work + work_item.
-  const int nblk = gridDim.x;
-  const int b = blockIdx.x;
+// XCD-aware block order: hardware places block b on XCD b % 8; give each XCD a contiguous range
+// of logical ids so that neighbouring logical blocks (which share weights or inputs) share an L2.
+__device__ __forceinline__ int xcd_logical(int b, int nblk) {
   const int xcd = b & 7, slot = b >> 3;
   const int per = (nblk + 7) >> 3;
   int rem = nblk & 7;
   if (rem == 0) rem = 8;
-  const int logical = (xcd < rem ? xcd * per : rem * per + (xcd - rem) * (per - 1)) + slot;
-  const int rt = logical / a.max_work;
-  const int wi = logical - rt * a.max_work;
-  if (rt >= a.row_tiles || wi >= *a.n_work) return;
+  return (xcd < rem ? xcd * per : rem * per + (xcd - rem) * (per - 1)) + slot;
+}
 
-  const int4 item = a.work[wi];
-  const int e = item.x, pos0 = item.y, nitem = item.z;
-  const int gsel = (e == a.experts) ? 1 : 0;
-  const ExpertGroup &grp = a.grp[gsel];
-  const uint8_t *blob = grp.blobs + (gsel ? 0 : (size_t)e * grp.stride);
-  const int I = grp.inter, H = a.hidden;
-  const int out_dim = (PH == PH_UP) ? I : H;
-  const int K = (PH == PH_UP) ? H : I;
-  if (rt * ROWS >= out_dim) return;                     // whole workgroup beyond this expert
+// Copies vectors v ∈ [base, base + threads·NB) ∩ [0, n) with `threads` threads (thread index
+// `id`): the loads of the batch are all issued before any store, so a batch costs one memory
+// latency (a load-store loop would wait for each load in turn, and, completion being in order,
+// for every load issued before it).
+template <int NB, class Src, class Dst>
+__device__ __forceinline__ void stage_batch(int base, int id, int threads, int n, Src src, Dst dst) {
+  u32x4 r[NB];
+#pragma unroll
+  for (int k = 0; k < NB; ++k) {
+    const int v = base + id + threads * k;
+    if (v < n) r[k] = src(v);
+  }
+#pragma unroll
+  for (int k = 0; k < NB; ++k) {
+    const int v = base + id + threads * k;
+    if (v < n) dst(v, r[k]);
+  }
+}
+
+// ---- decode prologue -----------------------------------------------------------------------------
+// The expert of a decode workgroup and its tokens, from the exact fp64 logits: every workgroup
+// selects the top-k of every token of the batch itself (wave w: tokens w, w + NW, ...), so the
+// decode step needs no selection or dispatch launch; workgroup 0 also writes the routing outputs.
+// Routed workgroup u takes the u-th entry of the (token, rank) table whose expert does not appear
+// earlier in it; the shared workgroup takes every token. Returns false when the workgroup has no
+// expert (uniform over the workgroup).
+struct SmallPick {
+  int e;          // expert id (E = the shared expert)
+  uint64_t tm;    // its tokens, bit t
+  int ntok;
+};
+
+template <int NW>
+__device__ __forceinline__ bool small_pick(const GemmArgs &a, const RouteArgs &ra, int u, bool shared_wg,
+                                           int *s_idx, SmallPick &pk) {
+  __shared__ double s_lg[NW][64];
+  __shared__ int s_ri[NW][kMaxTopK];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int T = ra.tokens, E = a.experts, K = a.top_k;
+  const bool has_shared = a.slots > K;
+  for (int t = wave; t < T; t += NW) {
+    const double *lg = ra.lg64 + (size_t)t * (E + 1);
+    const TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave]) : topk_exact(lg, E, K);
+    if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
+    if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
+  }
+  __syncthreads();
+  int e = E;
+  if (!shared_wg) {
+    const int n = T * K;   // ≤ 128: entries lane and lane + 64
+    bool first[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int i = lane + 64 * h;
+      first[h] = i < n;
+      if (i < n) {
+        const int ei = s_idx[i];
+        for (int j = 0; j < i; ++j) first[h] = first[h] && s_idx[j] != ei;
+      }
+    }
+    const uint64_t m0 = __ballot(first[0]), m1 = __ballot(first[1]);
+    const int n0 = __popcll(m0);
+    if (u >= n0 + __popcll(m1)) return false;
+    uint64_t mm = u < n0 ? m0 : m1;
+    for (int k = u < n0 ? u : u - n0; k > 0; --k) mm &= mm - 1;
+    e = s_idx[__ffsll((long long)mm) - 1 + (u < n0 ? 0 : 64)];
+  }
+  int r_t = -1;
+  if (lane < T) {
+    if (shared_wg) r_t = K;
+    else
+      for (int r = 0; r < K; ++r)
+        if (s_idx[lane * K + r] == e) r_t = r;
+  }
+  pk.e = e;
+  pk.tm = __ballot(r_t >= 0);
+  pk.ntok = __popcll(pk.tm);
+  return true;
+}
+
+// The j-th set bit of m.
+__device__ __forceinline__ int nth_bit(uint64_t m, int j) {
+  for (int k = 0; k < j; ++k) m &= m - 1;
+  return __ffsll((long long)m) - 1;
+}
+
+// Rank of expert e in token t's selection (the shared expert is rank K).
+__device__ __forceinline__ int rank_of(const int *s_idx, int t, int e, int K, bool shared) {
+  int r = K;
+  if (!shared)
+    for (int rr = 0; rr < K; ++rr)
+      if (s_idx[t * K + rr] == e) r = rr;
+  return r;
+}
+
+// ---- decode: gate-up ----------------------------------------------------------------------------
+constexpr int SMALL_T = 16;       // largest batch of the decode kernels
+constexpr int UP_ROWS = 32;       // intermediates per up_small workgroup (2 tiles × {gate, up})
+constexpr int LDS_PAD = 8;        // bf16 elements of padding per staged row (bank spread)
+
+// Grid: row tile rt (32 intermediates) × u, u < min(E, T·K) the distinct routed experts of the
+// batch, and the last u the shared expert when there is one. 8 waves: wave w takes tile
+// q = w & 1 (16 intermediates), gate (w & 2 = 0) or up rows, and chunk parity p = w >> 2 (the
+// even or odd chain of the canonical arithmetic).
+template <int FMT, int DA>
+__global__ __launch_bounds__(512) void up_small(GemmArgs a, RouteArgs ra) {
+  constexpr int NM = 1;
+  extern __shared__ __align__(16) uint16_t s_x[];   // [ntok][H + LDS_PAD]
+  __shared__ int s_idx[SMALL_T * kMaxTopK];
+  __shared__ f32x4 s_part[3][2][64];                // [gate odd | up even | up odd][q][lane]
 
   const int tid = threadIdx.x, lane = tid & 63;
-  // The wave index is uniform across the wave; readfirstlane lets the compiler keep it (and
-  // the loop bounds derived from it) in scalar registers, so the K loop has scalar control
-  // flow and the load pipeline gets exact wait counts.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, l16 = lane & 15;
-  const int rg = wave / KS, kp = wave % KS;             // row group, K partial
-  const int rb = rt * ROWS + rg * 16 * RT;              // first output row of this wave
+  const int T = ra.tokens, E = a.experts, K = a.top_k, S = a.slots, H = a.hidden;
+  const int rt = blockIdx.x % a.row_tiles, u = blockIdx.x / a.row_tiles;
+  const bool has_shared = S > K;
+  const bool shared_wg = has_shared && u == (int)(gridDim.x / a.row_tiles) - 1;
+  const ExpertGroup &grp = a.grp[shared_wg ? 1 : 0];
+  const int I = grp.inter;
+  if (rt * UP_ROWS >= I) return;                     // whole workgroup past this group's rows
 
-  // A rows of this lane (row l16 of each 16-row tile).
-  typename F::Row arow[NM];
-  const uint8_t *mscale[NM];   // MLX: scales of the matrix of tile m (bf16 [rows][K/64])
-  const uint8_t *mbias[NM];    // MLX: biases
-  int tile_row0[NM];           // first matrix row of tile m (for the D-row scales)
+  SmallPick pk;
+  if (!small_pick<8>(a, ra, u, shared_wg, s_idx, pk)) return;   // uniform over the workgroup
+  const int e = pk.e, ntok = pk.ntok;
+  const uint64_t tm = pk.tm;
+  const uint8_t *blob = grp.blobs + (shared_wg ? 0 : (size_t)e * grp.stride);
+
+  const int q = wave & 1;
+  const bool is_up = (wave & 2) != 0;
+  const int par = wave >> 2;
+  const int rb = rt * UP_ROWS + 16 * q;
+  ATile<FMT> at[NM] = {tile_of<PH_UP, FMT>(blob, grp, rb, is_up, H, l16)};
+  const int nch = (H + Fmt<FMT>::CHUNK - 1) / Fmt<FMT>::CHUNK;
+  const int ldx = H + LDS_PAD;
+  const int per_row = H / 8, nvec = ntok * per_row;
+  auto token_of = [&](int j) { return nth_bit(tm, j); };
+  auto xsrc = [&](int v) {
+    const int j = v / per_row, qq = v - j * per_row;
+    return *(const u32x4 *)(a.x + (size_t)token_of(j) * H + 8 * qq);
+  };
+  auto xdst = [&](int v, const u32x4 &val) {
+    const int j = v / per_row, qq = v - j * per_row;
+    *(u32x4 *)(s_x + (size_t)j * ldx + 8 * qq) = val;
+  };
+  // First batch of x loads, then the weight stream, then the stores (which wait for the x loads
+  // only) and any further batches.
+  constexpr int XB = 2;
+  u32x4 xr[XB];
 #pragma unroll
-  for (int m = 0; m < NM; ++m) {
-    const int q = m % RT;
-    const bool is_up = (PH == PH_UP) && (m >= RT);
-    const int r0 = min(rb + 16 * q, out_dim - 16);
-    const int orow = r0 + l16;   // output row (intermediate or hidden)
-    tile_row0[m] = r0;
-    if constexpr (FMT == Q_MXFP4) {
-      if (PH == PH_UP) arow[m] = F::row(blob + grp.off[0], blob + grp.off[1], 2 * orow + (is_up ? 1 : 0), K);
-      else arow[m] = F::row(blob + grp.off[3], blob + grp.off[4], orow, K);
-    } else if constexpr (FMT == Q_BF16) {
-      if (PH == PH_UP) arow[m] = F::row(blob + grp.off[0], orow + (is_up ? I : 0), K);
-      else arow[m] = F::row(blob + grp.off[1], orow, K);
-    } else {
-      const int mat = (PH == PH_UP) ? (is_up ? 1 : 0) : 2;
-      arow[m] = F::row(blob + grp.off[3 * mat], orow, K);
-      mscale[m] = blob + grp.off[3 * mat + 1];
-      mbias[m] = blob + grp.off[3 * mat + 2];
-    }
+  for (int k = 0; k < XB; ++k)
+    if (tid + 512 * k < nvec) xr[k] = xsrc(tid + 512 * k);
+  AStream<FMT, NM, DA> as(par, 2, nch);
+  as.fill(at, nch, g, H);
+#pragma unroll
+  for (int k = 0; k < XB; ++k)
+    if (tid + 512 * k < nvec) xdst(tid + 512 * k, xr[k]);
+  for (int base = 512 * XB; base < nvec; base += 512 * 4) stage_batch<4>(base, tid, 512, nvec, xsrc, xdst);
+  __syncthreads();
+
+  // Token column l16 = the l16-th token of the expert (padding columns repeat the last one).
+  const int my_t = token_of(min(l16, ntok - 1));
+  const uint16_t *brow = s_x + (size_t)min(l16, ntok - 1) * ldx;
+  f32x4 acc[NM][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
+  as.run(at, nch, g, H, [&](const typename Fmt<FMT>::A (&w)[NM], int c) {
+    const int col = Fmt<FMT>::bcol(c, g, H);
+    chunk_mfma<FMT, NM, 1, 1>(acc, w, at, [&](int, int, int v) { return *(const u32x4 *)(brow + col + 8 * v); },
+                              c, g, H);
+  });
+  // Chains and gate/up meet in the (gate, even) wave of each tile.
+  const int slot_of_part = (is_up ? 1 : 0) * 2 + par;   // 0: gate even (keeps), 1: gate odd, 2: up even, 3: up odd
+  if (slot_of_part > 0) s_part[slot_of_part - 1][q][lane] = acc[0][0];
+  __syncthreads();
+  if (slot_of_part == 0 && l16 < ntok) {
+    const int r = rank_of(s_idx, my_t, e, K, shared_wg);
+    up_epilogue<FMT>(a, blob, grp, rb + 4 * g, my_t * S + r, sum_chains(acc[0][0], s_part[0][q][lane]),
+                     sum_chains(s_part[1][q][lane], s_part[2][q][lane]));
   }
+}
 
-  const int nch = (K + F::CHUNK - 1) / F::CHUNK;
-  // This wave's chunks: c = kp, kp + KS, ...
-  const int my_n = nch > kp ? (nch - kp + KS - 1) / KS : 0;
+// ---- MXFP4 on the scaled MFMA -------------------------------------------------------------------
+typedef int v8i __attribute__((ext_vector_type(8)));
 
-  __shared__ f32x4 s_red[KS > 1 ? 4 : 1][NM][NT][64];
+// D += A·B, v_mfma_scale_f32_16x16x128_f8f6f4 with A = 16 rows × 128 K of fp4 e2m1 and B =
+// 128 K × 16 columns of fp8 e4m3. A lane (g, l16): row l16, the 32 values of K block g (low nibble
+// first: exactly one MXFP4 block as stored) and that block's e8m0 scale. B lane (g, l16): column
+// l16, K 16g..16g+15 in bytes 0-15 and K 64+16g..64+16g+15 in bytes 16-31, and the e8m0 scale of
+// K block g. D as the 16x16 bf16 MFMA.
+__device__ __forceinline__ f32x4 smfma(const u32x4 &a, const u32x4 &blo, const u32x4 &bhi, uint32_t sa,
+                                       uint32_t sb, const f32x4 &c) {
+  const v8i av = {(int)a[0], (int)a[1], (int)a[2], (int)a[3], 0, 0, 0, 0};
+  const v8i bv = {(int)blo[0], (int)blo[1], (int)blo[2], (int)blo[3],
+                  (int)bhi[0], (int)bhi[1], (int)bhi[2], (int)bhi[3]};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 4, 0, 0, (int)sa, 0, (int)sb);
+}
 
-  for (int t0 = 0; t0 < nitem; t0 += TOK) {
-    const int ntok = min(TOK, nitem - t0);
-    // B rows of this lane (token column l16 of each token tile).
-    const uint16_t *brow[NT][NH];
-    int bpos[NT];
+// B operand of chunk c from one term row (bytes, K columns) and its block scales `srow`; columns
+// at or past K read as zero and their blocks' scales as 2^0, so only finite values meet the zeroed
+// weights of a tail chunk.
+struct MxB {
+  u32x4 lo, hi;
+  uint32_t s;
+};
+__device__ __forceinline__ MxB mx_b(const uint8_t *row, const uint8_t *srow, int c, int g, int K) {
+  const int k0 = 128 * c + 16 * g;
+  MxB b;
+  b.lo = *(const u32x4 *)(row + k0);
+  b.hi = *(const u32x4 *)(row + k0 + 64);
+  b.s = srow[4 * c + g];
+  if (k0 >= K) b.lo = u32x4{0u, 0u, 0u, 0u};
+  if (k0 + 64 >= K) b.hi = u32x4{0u, 0u, 0u, 0u};
+  if (128 * c + 32 * g >= K) b.s = 127u;
+  return b;
+}
+
+// One chunk of the canonical MXFP4 arithmetic: acc += A·B_t for the terms t in order.
+template <int NM, int NT, int NTERM, class BF>
+__device__ __forceinline__ void chunk_mx(f32x4 (&acc)[NM][NT], const u32x4 (&w)[NM], const uint32_t (&sa)[NM], BF bf,
+                                         int c, int g, int K) {
+  const bool ok = Fmt<Q_MXFP4>::lane_valid(c, g, K);
+#pragma unroll
+  for (int t = 0; t < NTERM; ++t)
 #pragma unroll
     for (int st = 0; st < NT; ++st) {
-      const int j = 16 * st + l16;
-      const int p = pos0 + t0 + (j < ntok ? j : 0);
-      bpos[st] = p;
-      if (TP > 0) {
-        // LDS rows of the pass; padding columns repeat row 0.
-        brow[st][0] = s_b + (size_t)(j < ntok ? j : 0) * K;
-        if (NH > 1) brow[st][NH - 1] = s_b + (size_t)(TP + (j < ntok ? j : 0)) * K;
-      } else if (PH == PH_UP) {
-        const int slot_id = a.order[p];
-        brow[st][0] = a.x + (size_t)(slot_id / a.slots) * H;
-      } else {
-        brow[st][0] = a.h_hi + (size_t)p * a.ldh;
-        if (NH > 1) brow[st][NH - 1] = a.h_lo + (size_t)p * a.ldh;
-      }
-    }
-    if constexpr (TP > 0) {
-      // Stage the pass's B rows: K/8 16-byte vectors per row, all 256 threads.
-      const int per_row = K / 8;
-      const int total = NH * ntok * per_row;
-      for (int v = tid; v < total; v += 256) {
-        const int hh = v / (ntok * per_row);
-        const int rem2 = v - hh * ntok * per_row;
-        const int j = rem2 / per_row, q = rem2 - j * per_row;
-        const int p = pos0 + t0 + j;
-        const uint16_t *src;
-        if (PH == PH_UP) src = a.x + (size_t)(a.order[p] / a.slots) * H;
-        else src = (hh == 0 ? a.h_hi : a.h_lo) + (size_t)p * a.ldh;
-        *(u32x4 *)(s_b + (size_t)(hh * TP + j) * K + 8 * q) = *(const u32x4 *)(src + 8 * q);
-      }
-      __syncthreads();
-    }
-
-    f32x4 acc[NM][NT];
-#pragma unroll
-    for (int m = 0; m < NM; ++m)
-#pragma unroll
-      for (int st = 0; st < NT; ++st) acc[m][st] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    struct StageA { typename F::A w[NM]; };
-    struct StageB { u32x4 bv[NT][NH][NBV]; };
-    StageA sa[DA];
-    StageB sb[DB];
-
-    // Chunk of pipeline step i, clamped into [0, nch): steps past the wave's last chunk reload
-    // it, and a wave with no chunk at all (K shorter than KS chunks) loads chunk nch - 1, never
-    // a negative one.
-    const int last = my_n > 0 ? my_n - 1 : 0;
-    auto chunk_of = [&](int i) { return min(kp + KS * min(i, last), nch - 1); };
-    auto load_a = [&](StageA &s, int i) {
-      const int c = chunk_of(i);
-#pragma unroll
-      for (int m = 0; m < NM; ++m) F::load(s.w[m], arow[m], c, g, K);
-    };
-    auto load_b = [&](StageB &s, int i) {
-      const int c = chunk_of(i);
-      const int col = F::bcol(c, g, K);
-#pragma unroll
-      for (int st = 0; st < NT; ++st)
-#pragma unroll
-        for (int hh = 0; hh < NH; ++hh) {
-          const u32x4 *p = (const u32x4 *)(brow[st][hh] + col);
-#pragma unroll
-          for (int v = 0; v < NBV; ++v) s.bv[st][hh][v] = p[v];
-        }
-    };
-
-    auto compute_stage = [&](const StageA &s, const StageB &sbv, int i) {
-      const int c = kp + KS * i;
-      if constexpr (!MLX) {
-        const bool ok = F::lane_valid(c, g, K);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-#pragma unroll
-          for (int m = 0; m < NM; ++m) {
-            bf16x8 av;
-            if constexpr (FMT == Q_MXFP4) av = mxfp4_to_bf16(ok ? s.w[m].w[v] : 0u, e8m0_to_f32(s.w[m].s));
-            else av = as_bf16x8(ok ? s.w[m].w[v] : u32x4{0u, 0u, 0u, 0u});
-#pragma unroll
-            for (int st = 0; st < NT; ++st)
-#pragma unroll
-              for (int hh = 0; hh < NH; ++hh) acc[m][st] = mfma(av, as_bf16x8(sbv.bv[st][hh][v]), acc[m][st]);
-          }
-        }
-      } else {
-        f32x4 P[NM][NT];
-#pragma unroll
-        for (int m = 0; m < NM; ++m)
-#pragma unroll
-          for (int st = 0; st < NT; ++st) P[m][st] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj) {
-#pragma unroll
-          for (int m = 0; m < NM; ++m) {
-            const bf16x8 av = F::decode(s.w[m], jj);
-#pragma unroll
-            for (int st = 0; st < NT; ++st)
-#pragma unroll
-              for (int hh = 0; hh < NH; ++hh) P[m][st] = mfma(av, as_bf16x8(sbv.bv[st][hh][jj]), P[m][st]);
-          }
-        }
-        // Σ of the group's 64 B values of each token column (x, or h_hi + h_lo), from the
-        // operands already in registers: 16 per lane in index order, then the lane groups.
-        float gsum[NT];
-#pragma unroll
-        for (int st = 0; st < NT; ++st) {
-          u32x4 gb2[NH][2];
-#pragma unroll
-          for (int hh = 0; hh < NH; ++hh) { gb2[hh][0] = sbv.bv[st][hh][0]; gb2[hh][1] = sbv.bv[st][hh][1]; }
-          gsum[st] = group_sum<NH>(gb2);
-        }
-        // acc += s·P + b·Σ per D row (affine factorisation, gemma.metal:234-236).
-#pragma unroll
-        for (int m = 0; m < NM; ++m) {
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) {
-            const size_t ri = (size_t)(tile_row0[m] + 4 * g + ii) * (K / 64) + c;
-            const float sc = bf16_bits_to_f32(((const uint16_t *)mscale[m])[ri]);
-            const float bi = bf16_bits_to_f32(((const uint16_t *)mbias[m])[ri]);
-#pragma unroll
-            for (int st = 0; st < NT; ++st) {
-              acc[m][st][ii] = __builtin_fmaf(sc, P[m][st][ii], acc[m][st][ii]);
-              acc[m][st][ii] = __builtin_fmaf(bi, gsum[st], acc[m][st][ii]);
-            }
-          }
-        }
-      }
-    };
-
-    // Software pipeline over this wave's chunks. Loads past the last chunk are clamped to it
-    // (valid, already cached) so the steady-state loop has no branches.
-#pragma unroll
-    for (int u = 0; u < DA; ++u) load_a(sa[u], u);
-#pragma unroll
-    for (int u = 0; u < DB; ++u) load_b(sb[u], u);
-    int i0 = 0;
-    for (; i0 + DA <= my_n; i0 += DA) {
-#pragma unroll
-      for (int u = 0; u < DA; ++u) {
-        compute_stage(sa[u], sb[u % DB], i0 + u);
-        load_a(sa[u], i0 + u + DA);
-        load_b(sb[u % DB], i0 + u + DB);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < DA; ++u) {
-      if (i0 + u < my_n) {
-        compute_stage(sa[u], sb[u % DB], i0 + u);
-        if (i0 + u + DB < my_n) load_b(sb[u % DB], i0 + u + DB);
-      }
-    }
-
-    // ---- reduce the KS partials in a fixed order, then the epilogue ----
-    if constexpr (KS > 1) {
+      const MxB b = bf(st, t);
 #pragma unroll
       for (int m = 0; m < NM; ++m)
-#pragma unroll
-        for (int st = 0; st < NT; ++st) s_red[wave][m][st][lane] = acc[m][st];
-      __syncthreads();
+        acc[m][st] = smfma(ok ? w[m] : u32x4{0u, 0u, 0u, 0u}, b.lo, b.hi, sa[m] & 0xFFu, b.s, acc[m][st]);
     }
-    // The waves of a row group finish token tiles st ≡ kp (mod KS).
+}
+
+// Stages the e8m0 scales of `rows` consecutive weight rows (rows · K/32 bytes, 16-byte aligned)
+// into LDS: one 16-byte vector per thread and step.
+__device__ __forceinline__ int scale_vectors(int rows, int K) { return rows * (K / 32) / 16; }
+
+// The NTH fp8 terms of 8 activations of slot `slot` (intermediates ia..ia+3 in q[t][0], ib..ib+3
+// in q[t][1]) and, from lane group 0, the scales of their block blk.
+__device__ __forceinline__ void store_hq(const GemmArgs &a, int slot, int blk, int ia, int ib,
+                                         const uint32_t (&q)[NTH][2], const uint32_t (&sb)[NTH], int g) {
 #pragma unroll
-    for (int st = 0; st < NT; ++st) {
-      if ((st % KS) != kp) continue;
-      const int j = 16 * st + l16;
-      f32x4 r[NM];
+  for (int t = 0; t < NTH; ++t) {
+    uint8_t *row = a.hq + ((size_t)slot * NTH + t) * a.hld;
+    *(uint32_t *)(row + ia) = q[t][0];
+    *(uint32_t *)(row + ib) = q[t][1];
+    if (g == 0) a.hs[((size_t)slot * NTH + t) * (a.hld / 32) + blk] = (uint8_t)sb[t];
+  }
+}
+
+// A staged operand row in LDS: `ld` bytes of one term followed by its ld/32 scale bytes.
+__host__ __device__ __forceinline__ int mx_row_bytes(int ld) { return ld + ld / 32 + 16; }
+
+// Copies the NTERM term rows (and scales) of `nrows` operand rows into LDS rows of
+// mx_row_bytes(ld): LDS row rr = (j, t) ← q + (row_of(j)·NTERM + t)·ld and s + (…)·ld/32, in
+// 16-byte vectors v = id + threads·k. The first NB vectors of each thread can be loaded before
+// other loads are issued (load_first) and stored after them (store_first): completion counts
+// are in order, so stores issued after a weight stream would otherwise wait for all of it.
+template <int NTERM, int NB, class RowOf> struct MxStage {
+  uint8_t *dst;
+  const uint8_t *q, *sc;
+  int ld, n, dv, per_row, RS, id, threads;
+  RowOf row_of;
+  u32x4 r[NB];
+  __device__ __forceinline__ MxStage(uint8_t *dst_, const uint8_t *q_, const uint8_t *sc_, int ld_, int nrows,
+                                     RowOf row_of_, int id_, int threads_)
+      : dst(dst_), q(q_), sc(sc_), ld(ld_), dv(ld_ / 16), per_row(ld_ / 16 + ld_ / 512),
+        RS(mx_row_bytes(ld_)), id(id_), threads(threads_), row_of(row_of_) {
+    n = nrows * NTERM * per_row;
+  }
+  __device__ __forceinline__ u32x4 src(int v) const {
+    const int rr = v / per_row, qq = v - rr * per_row;
+    const size_t grow = (size_t)row_of(rr / NTERM) * NTERM + rr % NTERM;
+    return qq < dv ? *(const u32x4 *)(q + grow * ld + 16 * qq) : *(const u32x4 *)(sc + grow * (ld / 32) + 16 * (qq - dv));
+  }
+  __device__ __forceinline__ void put(int v, const u32x4 &val) const {
+    const int rr = v / per_row, qq = v - rr * per_row;
+    *(u32x4 *)(dst + (size_t)rr * RS + 16 * qq) = val;
+  }
+  // Unconditional (clamped) loads keep the completion counts exact.
+  __device__ __forceinline__ void load_first() {
 #pragma unroll
-      for (int m = 0; m < NM; ++m) {
-        if constexpr (KS == 1) {
-          r[m] = acc[m][st];
-        } else {
-          f32x4 sum = s_red[rg * KS][m][st][lane];
+    for (int k = 0; k < NB; ++k) r[k] = src(min(id + threads * k, n - 1));
+  }
+  __device__ __forceinline__ void store_first() {
 #pragma unroll
-          for (int p = 1; p < KS; ++p) {
-            const f32x4 pp = s_red[rg * KS + p][m][st][lane];
+    for (int k = 0; k < NB; ++k)
+      if (id + threads * k < n) put(id + threads * k, r[k]);
+  }
+  __device__ __forceinline__ void rest() {
+    for (int base = threads * NB; base < n; base += threads * 4)
+      stage_batch<4>(base, id, threads, n, [&](int v) { return src(v); }, [&](int v, const u32x4 &x) { put(v, x); });
+  }
+};
+template <int NTERM, int NB, class RowOf>
+__device__ __forceinline__ MxStage<NTERM, NB, RowOf> mx_stage(uint8_t *dst, const uint8_t *q, const uint8_t *sc,
+                                                               int ld, int nrows, RowOf row_of, int id, int threads) {
+  return MxStage<NTERM, NB, RowOf>(dst, q, sc, ld, nrows, row_of, id, threads);
+}
+
+// Decode gate-up on the scaled MFMA. Grid: row tile rt (32 intermediates) × u (as up_small). 4
+// waves: wave w takes tile q = w & 1 (16 intermediates) and the gate (w < 2) or up rows, over the
+// whole K with both chains; x comes as NTX fp8 terms. The gate waves combine gate and up and write
+// the activations of the 32-intermediate block to LDS; wave 0 writes them as NTH fp8 terms.
+template <int DA>
+__global__ __launch_bounds__(256) void up_small_mx(GemmArgs a, RouteArgs ra) {
+  constexpr int NM = 1;
+  extern __shared__ __align__(16) uint8_t s_xb[];   // [ntok][NTX] rows of mx_row_bytes(xld)
+  __shared__ int s_idx[SMALL_T * kMaxTopK];
+  __shared__ f32x4 s_up[2][64];
+  __shared__ float s_hv[SMALL_T][UP_ROWS];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, l16 = lane & 15;
+  const int K = a.top_k, S = a.slots, H = a.hidden;
+  const int rt = blockIdx.x % a.row_tiles, u = blockIdx.x / a.row_tiles;
+  const bool shared_wg = S > K && u == (int)(gridDim.x / a.row_tiles) - 1;
+  const ExpertGroup &grp = a.grp[shared_wg ? 1 : 0];
+  const int I = grp.inter;
+  if (rt * UP_ROWS >= I) return;
+
+  SmallPick pk;
+  if (!small_pick<4>(a, ra, u, shared_wg, s_idx, pk)) return;
+  const int e = pk.e, ntok = pk.ntok;
+  const uint64_t tm = pk.tm;
+  const uint8_t *blob = grp.blobs + (shared_wg ? 0 : (size_t)e * grp.stride);
+
+  const int q = wave & 1;
+  const bool is_up = wave >= 2;
+  const int rb = rt * UP_ROWS + 16 * q;
+  ATile<Q_MXFP4_W> at[NM] = {tile_of<PH_UP, Q_MXFP4_W>(blob, grp, rb, is_up, H, l16)};
+  const int nch = (H + 127) / 128;
+  const int RS = mx_row_bytes(a.xld);
+  // The workgroup's 64 gate_up rows' scales (contiguous: rows 64·rt ..) and the tokens' x terms:
+  // first loads out before the weight stream, stored after it.
+  const int nsb = H / 32;                            // scale bytes per row
+  uint8_t *s_sc = s_xb + (size_t)ntok * NTX * RS;   // [64][nsb]
+  const int nsv = scale_vectors(64, H);
+  const uint8_t *gsc = blob + grp.off[1] + (size_t)rt * 64 * nsb;
+  u32x4 scv[2];
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii) sum[ii] = sum[ii] + pp[ii];
-          }
-          r[m] = sum;
-        }
-      }
-      if (j >= ntok) continue;
+  for (int k = 0; k < 2; ++k) scv[k] = *(const u32x4 *)(gsc + 16 * min(tid + 256 * k, nsv - 1));
+  auto xs = mx_stage<NTX, 2>(s_xb, a.xq, a.xs, a.xld, ntok, [&](int j) { return nth_bit(tm, j); }, tid, 256);
+  xs.load_first();
+  AStream<Q_MXFP4_W, NM, DA> as(0, 1, nch);
+  as.fill(at, nch, g, H);
 #pragma unroll
-      for (int q = 0; q < RT; ++q) {
-        if (rb + 16 * q >= out_dim) continue;
-        if constexpr (PH == PH_UP) up_epilogue<FMT>(a, blob, grp, rb + 16 * q + 4 * g, bpos[st], r[q], r[RT + q]);
-        else down_epilogue<FMT>(a, blob, grp, rb + 16 * q + 4 * g, bpos[st], r[q]);
-      }
+  for (int k = 0; k < 2; ++k)
+    if (tid + 256 * k < nsv) *(u32x4 *)(s_sc + 16 * (tid + 256 * k)) = scv[k];
+  for (int v = tid + 512; v < nsv; v += 256) *(u32x4 *)(s_sc + 16 * v) = *(const u32x4 *)(gsc + 16 * v);
+  xs.store_first();
+  xs.rest();
+  __syncthreads();
+  const uint8_t *my_sc = s_sc + (2 * (16 * q + l16) + (is_up ? 1 : 0)) * nsb;
+
+  const uint8_t *brow = s_xb + (size_t)min(l16, ntok - 1) * NTX * RS;
+  f32x4 acc[2][NM][1];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) acc[p][0][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+  as.run(at, nch, g, H, [&](const Fmt<Q_MXFP4_W>::A (&w)[NM], int c) {
+    auto bf = [&](int, int t) { return mx_b(brow + t * RS, brow + t * RS + a.xld, c, g, H); };
+    const u32x4 wv[NM] = {w[0].w};
+    const uint32_t sv[NM] = {my_sc[min(4 * c + g, nsb - 1)]};
+    if (c & 1) chunk_mx<NM, 1, NTX>(acc[1], wv, sv, bf, c, g, H);
+    else chunk_mx<NM, 1, NTX>(acc[0], wv, sv, bf, c, g, H);
+  });
+  const f32x4 res = sum_chains(acc[0][0][0], acc[1][0][0]);
+  if (is_up) s_up[q][lane] = res;
+  __syncthreads();
+  if (!is_up && l16 < ntok) {
+    const f32x4 y = up_values<Q_MXFP4>(a, blob, grp, rb + 4 * g, res, s_up[q][lane]);
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) s_hv[l16][16 * q + 4 * g + ii] = y[ii];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // Lane (g, l16): activations 8g .. 8g+7 of the block of token column l16.
+    const int j = min(l16, ntok - 1);
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = s_hv[j][8 * g + i];
+    uint32_t hq[NTH][2], sb[NTH];
+    quant_block<NTH>(v, hq, sb);
+    if (l16 < ntok) {
+      const int t = nth_bit(tm, l16);
+      const int slot = t * S + rank_of(s_idx, t, e, K, shared_wg);
+      store_hq(a, slot, rt, rt * UP_ROWS + 8 * g, rt * UP_ROWS + 8 * g + 4, hq, sb, g);
     }
-    if constexpr (KS > 1 || TP > 0) __syncthreads();   // s_red / s_b are reused by the next pass
+  }
+}
+
+// ---- decode: down + combine -----------------------------------------------------------------------
+// Grid: (16 hidden rows) × token. Wave (r, p): slot r of the token (expert topk_idx[t][r], or the
+// shared expert), chunk parity p when KS = 2 (both chains in one wave when KS = 1). The epilogue
+// sums the chains, then the slots in rank order (sum_expert_slices, dense.metal:147;
+// ReferenceLayer.swift:194-202). SMAX = the most slots a token has under this instantiation.
+template <int FMT, int DA, int SMAX, int KS>
+__global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const int32_t *topk_idx) {
+  constexpr int NM = 1;
+  extern __shared__ __align__(16) uint16_t s_h[];   // [slots][2][ldh + LDS_PAD]
+  __shared__ f32x4 s_odd[KS > 1 ? SMAX : 1][4];     // odd chain, lanes l16 == 0
+  __shared__ float s_o[SMAX][16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, l16 = lane & 15;
+  const int S = a.slots, K = a.top_k, H = a.hidden, E = a.experts;
+  const int T = gridDim.x / a.row_tiles;
+  const int logical = xcd_logical(blockIdx.x, gridDim.x);
+  const int rt = logical / T, t = logical - rt * T;
+  const int r = wave % S, par = wave / S;
+  const int slot = t * S + r;
+  const int e = r < K ? topk_idx[t * K + r] : E;
+  const int gsel = e == E ? 1 : 0;
+  const ExpertGroup &grp = a.grp[gsel];
+  const uint8_t *blob = grp.blobs + (gsel ? 0 : (size_t)e * grp.stride);
+  const int I = grp.inter;
+  const int rb = rt * 16;
+
+  ATile<FMT> at[NM];
+  wave_tiles<PH_DOWN, FMT, 1>(at, blob, grp, rb, H, I, l16);
+  const int nch = (I + Fmt<FMT>::CHUNK - 1) / Fmt<FMT>::CHUNK;
+  f32x4 acc[2][NM][1];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) acc[p][0][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if constexpr (FMT == Q_MXFP4) {
+    // This slot's activation terms and its 16 weight rows' scales into LDS (the slot's waves
+    // share them): first loads out before the weight stream, stored after it.
+    uint8_t *sbm = (uint8_t *)s_h;
+    const int RS = mx_row_bytes(a.hld);
+    const int nsb = I / 32, nsv = scale_vectors(16, I);
+    const int imax = max(a.grp[0].inter, a.grp[1].inter);   // per-slot LDS stride as on the host
+    const int slot_bytes = NTH * RS + 16 * ((16 * (imax / 32) + 15) / 16);
+    uint8_t *my_lds = sbm + (size_t)r * slot_bytes;
+    uint8_t *s_sc = my_lds + NTH * RS;
+    const uint8_t *gsc = blob + grp.off[4] + (size_t)rb * nsb;
+    const int sid = par * 64 + lane, sth = 64 * KS;
+    u32x4 scv[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) scv[k] = *(const u32x4 *)(gsc + 16 * min(sid + sth * k, nsv - 1));
+    auto hs = mx_stage<NTH, 5>(my_lds, a.hq, a.hs, a.hld, 1, [&](int) { return slot; }, sid, sth);
+    hs.load_first();
+    ATile<Q_MXFP4_W> aw[NM] = {tile_of<PH_DOWN, Q_MXFP4_W>(blob, grp, rb, false, I, l16)};
+    AStream<Q_MXFP4_W, NM, DA> as(KS > 1 ? par : 0, KS, nch);
+    as.fill(aw, nch, g, I);
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      if (sid + sth * k < nsv) *(u32x4 *)(s_sc + 16 * (sid + sth * k)) = scv[k];
+    for (int v = sid + 2 * sth; v < nsv; v += sth) *(u32x4 *)(s_sc + 16 * v) = *(const u32x4 *)(gsc + 16 * v);
+    hs.store_first();
+    hs.rest();
+    __syncthreads();
+    const uint8_t *brow = my_lds;
+    const uint8_t *my_sc = s_sc + l16 * nsb;
+    as.run(aw, nch, g, I, [&](const Fmt<Q_MXFP4_W>::A (&w)[NM], int c) {
+      auto bf = [&](int, int t) { return mx_b(brow + t * RS, brow + t * RS + a.hld, c, g, I); };
+      const u32x4 wv[NM] = {w[0].w};
+      const uint32_t sv[NM] = {my_sc[min(4 * c + g, nsb - 1)]};
+      if (KS == 1 && (c & 1)) chunk_mx<NM, 1, NTH>(acc[1], wv, sv, bf, c, g, I);
+      else chunk_mx<NM, 1, NTH>(acc[0], wv, sv, bf, c, g, I);
+    });
+  } else {
+  // This slot's activation (hi, lo) into LDS (the slot's two waves share it): the loads go out
+  // before the weight stream (see stage_batch), the stores after it.
+  const int ldb = a.ldh + LDS_PAD;
+  uint16_t *sb = s_h + (size_t)r * 2 * ldb;
+  const int per_row = I / 8, nvec = 2 * per_row;
+  auto hsrc = [&](int v) {
+    const int hh = v / per_row, qq = v - hh * per_row;
+    return *(const u32x4 *)((hh ? a.h_lo : a.h_hi) + (size_t)slot * a.ldh + 8 * qq);
+  };
+  auto hdst = [&](int v, const u32x4 &val) {
+    const int hh = v / per_row, qq = v - hh * per_row;
+    *(u32x4 *)(sb + hh * ldb + 8 * qq) = val;
+  };
+  // 64·KS·HB vectors in the first batch: both terms of I ≤ 3072 (SMAX 4, KS 2) or I ≤ 1024.
+  constexpr int HB = (SMAX <= 4 && KS == 2) ? 6 : 4;
+  const int sid = par * 64 + lane, sth = 64 * KS;
+  u32x4 hr[HB];
+#pragma unroll
+  for (int k = 0; k < HB; ++k)
+    if (sid + sth * k < nvec) hr[k] = hsrc(sid + sth * k);
+  AStream<FMT, NM, DA> as(KS > 1 ? par : 0, KS, nch);
+  as.fill(at, nch, g, I);
+#pragma unroll
+  for (int k = 0; k < HB; ++k)
+    if (sid + sth * k < nvec) hdst(sid + sth * k, hr[k]);
+  for (int base = sth * HB; base < nvec; base += sth * 4) stage_batch<4>(base, sid, sth, nvec, hsrc, hdst);
+  __syncthreads();
+
+  as.run(at, nch, g, I, [&](const typename Fmt<FMT>::A (&w)[NM], int c) {
+    const int col = Fmt<FMT>::bcol(c, g, I);
+    auto bv = [&](int, int hh, int v) { return *(const u32x4 *)(sb + hh * ldb + col + 8 * v); };
+    if (KS == 1 && (c & 1)) chunk_mfma<FMT, NM, 1, 2>(acc[1], w, at, bv, c, g, I);
+    else chunk_mfma<FMT, NM, 1, 2>(acc[0], w, at, bv, c, g, I);
+  });
+  }
+  if constexpr (KS > 1) {
+    if (par == 1 && l16 == 0) s_odd[r][g] = acc[0][0][0];
+    __syncthreads();
+    if (par == 0 && l16 == 0) acc[1][0][0] = s_odd[r][g];
+  }
+  if (par == 0 && l16 == 0) {
+    const f32x4 o = down_value<FMT>(a, blob, grp, rb + 4 * g, slot, sum_chains(acc[0][0][0], acc[1][0][0]));
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) s_o[r][4 * g + ii] = o[ii];
+  }
+  __syncthreads();
+  if (tid < 16) {
+    float y = s_o[0][tid];
+    for (int qq = 1; qq < S; ++qq) y += s_o[qq][tid];
+    a.y[(size_t)t * H + rb + tid] = y;
   }
 }
 
@@ -511,32 +934,20 @@ __global__ __launch_bounds__(256) void expert_gemm(GemmArgs a) {
 // The 4 waves own 4·RT consecutive 16-row tiles and walk all of K together: the B operand of
 // each chunk (TOK = 16·NT tokens × one chunk of columns, x or h_hi + h_lo) is loaded once by the
 // whole workgroup into LDS (double-buffered, 16-byte segments XOR-swizzled by row so the MFMA
-// reads are bank-conflict free) and shared by the 4 waves. Each wave keeps the 4 K partials
-// (chunk c → partial c mod 4) in separate accumulators and sums them in partial order, which is
-// the arithmetic expert_gemm performs with its 4 waves: a token's result is the same bits
-// whichever kernel computed it.
+// reads are bank-conflict free) and shared by the 4 waves.
 template <int PH, int FMT, int RT, int NT, int DA>
 __global__ __launch_bounds__(256) void prefill_gemm(GemmArgs a) {
   using F = Fmt<FMT>;
-  constexpr bool MLX = (FMT == Q_MLX4 || FMT == Q_MLX8);
   constexpr int NM = (PH == PH_UP) ? 2 * RT : RT;
-  constexpr int NBV = F::NB;                          // B vectors per lane per chunk
   constexpr int NH = (PH == PH_UP) ? 1 : 2;
   constexpr int ROWS = 4 * 16 * RT;
   constexpr int TOK = 16 * NT;
   constexpr int NSEG = F::CHUNK / 8;                  // 16-byte segments per B row chunk
   constexpr int BVEC = NH * TOK * NSEG;               // 16-byte vectors per B chunk
   constexpr int BPT = (BVEC + 255) / 256;             // per thread
-  static_assert(DA == 1 || DA == 2 || DA == 4, "DA divides the 4-chunk unroll");
   __shared__ __align__(16) u32x4 s_bv[2][BVEC];
 
-  const int nblk = gridDim.x;
-  const int b = blockIdx.x;
-  const int xcd = b & 7, slot = b >> 3;
-  const int per = (nblk + 7) >> 3;
-  int rem = nblk & 7;
-  if (rem == 0) rem = 8;
-  const int logical = (xcd < rem ? xcd * per : rem * per + (xcd - rem) * (per - 1)) + slot;
+  const int logical = xcd_logical(blockIdx.x, gridDim.x);
   const int rt = logical / a.max_work;
   const int wi = logical - rt * a.max_work;
   if (rt >= a.row_tiles || wi >= *a.n_work) return;
@@ -556,30 +967,8 @@ __global__ __launch_bounds__(256) void prefill_gemm(GemmArgs a) {
   const int g = lane >> 4, l16 = lane & 15;
   const int rb = rt * ROWS + wave * 16 * RT;
 
-  typename F::Row arow[NM];
-  const uint8_t *mscale[NM];
-  const uint8_t *mbias[NM];
-  int tile_row0[NM];
-#pragma unroll
-  for (int m = 0; m < NM; ++m) {
-    const int q = m % RT;
-    const bool is_up = (PH == PH_UP) && (m >= RT);
-    const int r0 = min(rb + 16 * q, out_dim - 16);
-    const int orow = r0 + l16;
-    tile_row0[m] = r0;
-    if constexpr (FMT == Q_MXFP4) {
-      if (PH == PH_UP) arow[m] = F::row(blob + grp.off[0], blob + grp.off[1], 2 * orow + (is_up ? 1 : 0), K);
-      else arow[m] = F::row(blob + grp.off[3], blob + grp.off[4], orow, K);
-    } else if constexpr (FMT == Q_BF16) {
-      if (PH == PH_UP) arow[m] = F::row(blob + grp.off[0], orow + (is_up ? I : 0), K);
-      else arow[m] = F::row(blob + grp.off[1], orow, K);
-    } else {
-      const int mat = (PH == PH_UP) ? (is_up ? 1 : 0) : 2;
-      arow[m] = F::row(blob + grp.off[3 * mat], orow, K);
-      mscale[m] = blob + grp.off[3 * mat + 1];
-      mbias[m] = blob + grp.off[3 * mat + 2];
-    }
-  }
+  ATile<FMT> at[NM];
+  wave_tiles<PH, FMT, RT>(at, blob, grp, rb, out_dim, K, l16);
   const int nch = (K + F::CHUNK - 1) / F::CHUNK;
 
   for (int t0 = 0; t0 < nitem; t0 += TOK) {
@@ -593,10 +982,10 @@ __global__ __launch_bounds__(256) void prefill_gemm(GemmArgs a) {
       const int hh = v / (TOK * NSEG);
       const int n = (v / NSEG) % TOK;
       const int sg = v % NSEG;
-      const int p = pos0 + t0 + (n < ntok ? n : 0);
+      const int slot = a.order[pos0 + t0 + (n < ntok ? n : 0)];
       const uint16_t *row;
-      if (PH == PH_UP) row = a.x + (size_t)(a.order[p] / a.slots) * H;
-      else row = (hh == 0 ? a.h_hi : a.h_lo) + (size_t)p * a.ldh;
+      if (PH == PH_UP) row = a.x + (size_t)(slot / a.slots) * H;
+      else row = (hh == 0 ? a.h_hi : a.h_lo) + (size_t)slot * a.ldh;
       bsrc[k] = row;
       bcol[k] = 8 * sg;
       bdst[k] = (hh * TOK + n) * NSEG + (sg ^ (n & (NSEG - 1)));
@@ -615,96 +1004,26 @@ __global__ __launch_bounds__(256) void prefill_gemm(GemmArgs a) {
       for (int k = 0; k < BPT; ++k)
         if (tid + 256 * k < BVEC) s_bv[buf][bdst[k]] = breg[k];
     };
-    int bpos[NT];
+    int bslot[NT];
 #pragma unroll
     for (int st = 0; st < NT; ++st) {
       const int j = 16 * st + l16;
-      bpos[st] = pos0 + t0 + (j < ntok ? j : 0);
+      bslot[st] = a.order[pos0 + t0 + (j < ntok ? j : 0)];
     }
 
-    f32x4 acc[4][NM][NT];
+    f32x4 acc[2][NM][NT];
 #pragma unroll
-    for (int pp = 0; pp < 4; ++pp)
+    for (int p = 0; p < 2; ++p)
 #pragma unroll
       for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int st = 0; st < NT; ++st) acc[pp][m][st] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int st = 0; st < NT; ++st) acc[p][m][st] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     typename F::A sa[DA][NM];
     auto load_a = [&](typename F::A (&w)[NM], int c) {
       const int cc = min(c, nch - 1);
 #pragma unroll
-      for (int m = 0; m < NM; ++m) F::load(w[m], arow[m], cc, g, K);
-    };
-
-    // B operand of token tile st, MFMA step v, term hh from LDS buffer buf.
-    auto bvec = [&](int buf, int st, int hh, int v) -> u32x4 {
-      const int n = 16 * st + l16;
-      const int sg = MLX ? (2 * g + v) : (4 * g + v);
-      return s_bv[buf][(hh * TOK + n) * NSEG + (sg ^ (n & (NSEG - 1)))];
-    };
-
-    auto compute = [&](const typename F::A (&w)[NM], int buf, int c, f32x4 (&ac)[NM][NT]) {
-      if constexpr (!MLX) {
-        const bool ok = F::lane_valid(c, g, K);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          u32x4 bv[NT][NH];
-#pragma unroll
-          for (int st = 0; st < NT; ++st)
-#pragma unroll
-            for (int hh = 0; hh < NH; ++hh) bv[st][hh] = bvec(buf, st, hh, v);
-#pragma unroll
-          for (int m = 0; m < NM; ++m) {
-            bf16x8 av;
-            if constexpr (FMT == Q_MXFP4) av = mxfp4_to_bf16(ok ? w[m].w[v] : 0u, e8m0_to_f32(w[m].s));
-            else av = as_bf16x8(ok ? w[m].w[v] : u32x4{0u, 0u, 0u, 0u});
-#pragma unroll
-            for (int st = 0; st < NT; ++st)
-#pragma unroll
-              for (int hh = 0; hh < NH; ++hh) ac[m][st] = mfma(av, as_bf16x8(bv[st][hh]), ac[m][st]);
-          }
-        }
-      } else {
-        u32x4 bv[NT][NH][2];
-#pragma unroll
-        for (int st = 0; st < NT; ++st)
-#pragma unroll
-          for (int hh = 0; hh < NH; ++hh)
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj) bv[st][hh][jj] = bvec(buf, st, hh, jj);
-        f32x4 P[NM][NT];
-#pragma unroll
-        for (int m = 0; m < NM; ++m)
-#pragma unroll
-          for (int st = 0; st < NT; ++st) P[m][st] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-          for (int m = 0; m < NM; ++m) {
-            const bf16x8 av = F::decode(w[m], jj);
-#pragma unroll
-            for (int st = 0; st < NT; ++st)
-#pragma unroll
-              for (int hh = 0; hh < NH; ++hh) P[m][st] = mfma(av, as_bf16x8(bv[st][hh][jj]), P[m][st]);
-          }
-        float gsum[NT];
-#pragma unroll
-        for (int st = 0; st < NT; ++st) gsum[st] = group_sum<NH>(bv[st]);
-#pragma unroll
-        for (int m = 0; m < NM; ++m)
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) {
-            const size_t ri = (size_t)(tile_row0[m] + 4 * g + ii) * (K / 64) + c;
-            const float sc = bf16_bits_to_f32(((const uint16_t *)mscale[m])[ri]);
-            const float bi = bf16_bits_to_f32(((const uint16_t *)mbias[m])[ri]);
-#pragma unroll
-            for (int st = 0; st < NT; ++st) {
-              ac[m][st][ii] = __builtin_fmaf(sc, P[m][st][ii], ac[m][st][ii]);
-              ac[m][st][ii] = __builtin_fmaf(bi, gsum[st], ac[m][st][ii]);
-            }
-          }
-      }
+      for (int m = 0; m < NM; ++m) F::load(w[m], at[m].row, cc, g, K);
     };
 
     // Prologue: B of chunk 0 in LDS, B of chunk 1 in registers, A of chunks 0..DA-1 in flight.
@@ -716,21 +1035,26 @@ __global__ __launch_bounds__(256) void prefill_gemm(GemmArgs a) {
     __syncthreads();
     // Chunk c: compute from LDS buffer c % 2; then stage B of c + 1 into the other buffer and
     // fetch B of c + 2 and A of c + DA; one barrier per chunk.
-    for (int c0 = 0; c0 < nch; c0 += 4) {
+    for (int c0 = 0; c0 < nch; c0 += 2 * DA) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < 2 * DA; ++u) {
         const int c = c0 + u;
         if (c < nch) {
-          compute(sa[u % DA], u & 1, c, acc[u]);
+          const int buf = u & 1;
+          const int seg0 = is_mlx<FMT>() ? 2 * g : 4 * g;
+          chunk_mfma<FMT, NM, NT, NH>(acc[u & 1], sa[u % DA], at, [&](int st, int hh, int v) {
+            const int n = 16 * st + l16;
+            return s_bv[buf][(hh * TOK + n) * NSEG + ((seg0 + v) ^ (n & (NSEG - 1)))];
+          }, c, g, K);
           load_a(sa[u % DA], c + DA);
-          store_b((u + 1) & 1);
+          store_b(buf ^ 1);
           load_b(c + 2);
           __syncthreads();
         }
       }
     }
 
-    // Epilogue: partials summed in order, 4 intermediates / hidden rows per lane.
+    // Epilogue: 4 intermediates / hidden rows per lane.
 #pragma unroll
     for (int st = 0; st < NT; ++st) {
       const int j = 16 * st + l16;
@@ -739,17 +1063,184 @@ __global__ __launch_bounds__(256) void prefill_gemm(GemmArgs a) {
       for (int q = 0; q < RT; ++q) {
         if (rb + 16 * q >= out_dim) continue;
         if constexpr (PH == PH_UP) {
-          const f32x4 gate = sum_partials4(acc[0][q][st], acc[1][q][st], acc[2][q][st], acc[3][q][st]);
-          const f32x4 up = sum_partials4(acc[0][RT + q][st], acc[1][RT + q][st], acc[2][RT + q][st],
-                                         acc[3][RT + q][st]);
-          up_epilogue<FMT>(a, blob, grp, rb + 16 * q + 4 * g, bpos[st], gate, up);
+          up_epilogue<FMT>(a, blob, grp, rb + 16 * q + 4 * g, bslot[st], sum_chains(acc[0][q][st], acc[1][q][st]),
+                           sum_chains(acc[0][RT + q][st], acc[1][RT + q][st]));
         } else {
-          const f32x4 r = sum_partials4(acc[0][q][st], acc[1][q][st], acc[2][q][st], acc[3][q][st]);
-          down_epilogue<FMT>(a, blob, grp, rb + 16 * q + 4 * g, bpos[st], r);
+          const int h0 = rb + 16 * q + 4 * g;
+          *(f32x4 *)(a.slot_out + (size_t)bslot[st] * H + h0) =
+              down_value<FMT>(a, blob, grp, h0, bslot[st], sum_chains(acc[0][q][st], acc[1][q][st]));
         }
       }
     }
     __syncthreads();   // the next pass restages s_bv
+  }
+}
+
+// ---- prefill, MXFP4 on the scaled MFMA -------------------------------------------------------------
+// prefill_gemm's workgroup layout (4 waves × RT 16-row tiles × 16·NT tokens, B chunk shared
+// through LDS, double-buffered) with the fp8 operand terms: a B chunk is, per token and term,
+// 128 bytes (8 segments, XOR-swizzled by token) and the 4 block scales of the chunk. RT = 2, so a
+// gate-up wave holds whole 32-intermediate blocks and quantises its activations itself.
+template <int PH, int RT, int NT, int DA>
+__global__ __launch_bounds__(256) void prefill_mx(GemmArgs a) {
+  using F = Fmt<Q_MXFP4>;
+  constexpr int NM = (PH == PH_UP) ? 2 * RT : RT;
+  constexpr int NTERM = (PH == PH_UP) ? NTX : NTH;
+  constexpr int ROWS = 4 * 16 * RT;
+  constexpr int TOK = 16 * NT;
+  constexpr int BVEC = NTERM * TOK * 8;               // 16-byte segments per B chunk
+  constexpr int BPT = (BVEC + 255) / 256;
+  constexpr int NSC = NTERM * TOK;                    // scale dwords per B chunk
+  static_assert(NSC <= 256, "one scale dword per thread");
+  static_assert(PH == PH_DOWN || RT == 2, "gate-up waves own whole 32-intermediate blocks");
+  __shared__ __align__(16) u32x4 s_bq[2][BVEC];
+  __shared__ uint32_t s_bs[2][NSC];
+
+  const int logical = xcd_logical(blockIdx.x, gridDim.x);
+  const int rt = logical / a.max_work;
+  const int wi = logical - rt * a.max_work;
+  if (rt >= a.row_tiles || wi >= *a.n_work) return;
+
+  const int4 item = a.work[wi];
+  const int e = item.x, pos0 = item.y, nitem = item.z;
+  const int gsel = (e == a.experts) ? 1 : 0;
+  const ExpertGroup &grp = a.grp[gsel];
+  const uint8_t *blob = grp.blobs + (gsel ? 0 : (size_t)e * grp.stride);
+  const int I = grp.inter, H = a.hidden;
+  const int out_dim = (PH == PH_UP) ? I : H;
+  const int K = (PH == PH_UP) ? H : I;
+  if (rt * ROWS >= out_dim) return;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, l16 = lane & 15;
+  const int rb = rt * ROWS + wave * 16 * RT;
+
+  ATile<Q_MXFP4> at[NM];
+  wave_tiles<PH, Q_MXFP4, RT>(at, blob, grp, rb, out_dim, K, l16);
+  const int nch = (K + 127) / 128;
+  const int ld = PH == PH_UP ? a.xld : a.hld;
+  const uint8_t *qbase = PH == PH_UP ? a.xq : a.hq;
+  const uint8_t *sbase = PH == PH_UP ? a.xs : a.hs;
+
+  for (int t0 = 0; t0 < nitem; t0 += TOK) {
+    const int ntok = min(TOK, nitem - t0);
+    // Operand row of token n of the pass: x of its token (gate-up) or h of its slot (down).
+    auto row_of = [&](int n) {
+      const int slot = a.order[pos0 + t0 + (n < ntok ? n : 0)];
+      return PH == PH_UP ? slot / a.slots : slot;
+    };
+    const uint8_t *bsrc[BPT];
+    int bdst[BPT];
+#pragma unroll
+    for (int k = 0; k < BPT; ++k) {
+      const int v = min(tid + 256 * k, BVEC - 1);
+      const int tt = v / (TOK * 8), n = (v / 8) % TOK, sg = v % 8;
+      bsrc[k] = qbase + ((size_t)row_of(n) * NTERM + tt) * ld + 16 * sg;
+      bdst[k] = (tt * TOK + n) * 8 + (sg ^ (n & 7));
+    }
+    const uint8_t *ssrc = sbase + ((size_t)row_of(tid % TOK) * NTERM + min(tid / TOK, NTERM - 1)) * (ld / 32);
+    u32x4 breg[BPT];
+    uint32_t sreg = 0;
+    auto load_b = [&](int c) {
+      const int cc = min(c, nch - 1);
+#pragma unroll
+      for (int k = 0; k < BPT; ++k) breg[k] = *(const u32x4 *)(bsrc[k] + 128 * cc);
+      sreg = *(const uint32_t *)(ssrc + 4 * cc);
+    };
+    auto store_b = [&](int buf) {
+#pragma unroll
+      for (int k = 0; k < BPT; ++k)
+        if (tid + 256 * k < BVEC) s_bq[buf][bdst[k]] = breg[k];
+      if (tid < NSC) s_bs[buf][tid] = sreg;
+    };
+    int bslot[NT];
+#pragma unroll
+    for (int st = 0; st < NT; ++st) {
+      const int j = 16 * st + l16;
+      bslot[st] = a.order[pos0 + t0 + (j < ntok ? j : 0)];
+    }
+
+    f32x4 acc[2][NM][NT];
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int st = 0; st < NT; ++st) acc[p][m][st] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    typename F::A sa[DA][NM];
+    auto load_a = [&](typename F::A (&w)[NM], int c) {
+      const int cc = min(c, nch - 1);
+#pragma unroll
+      for (int m = 0; m < NM; ++m) F::load(w[m], at[m].row, cc, g, K);
+    };
+
+    load_b(0);
+    store_b(0);
+    load_b(1);
+#pragma unroll
+    for (int u = 0; u < DA; ++u) load_a(sa[u], u);
+    __syncthreads();
+    for (int c0 = 0; c0 < nch; c0 += 2 * DA) {
+#pragma unroll
+      for (int u = 0; u < 2 * DA; ++u) {
+        const int c = c0 + u;
+        if (c < nch) {
+          const int buf = u & 1;
+          u32x4 wv[NM];
+          uint32_t sv[NM];
+#pragma unroll
+          for (int m = 0; m < NM; ++m) { wv[m] = sa[u % DA][m].w; sv[m] = sa[u % DA][m].s; }
+          chunk_mx<NM, NT, NTERM>(acc[u & 1], wv, sv, [&](int st, int tt) {
+            const int n = 16 * st + l16;
+            const int k0 = 128 * c + 16 * g;
+            MxB b;
+            b.lo = s_bq[buf][(tt * TOK + n) * 8 + (g ^ (n & 7))];
+            b.hi = s_bq[buf][(tt * TOK + n) * 8 + ((4 + g) ^ (n & 7))];
+            b.s = (s_bs[buf][tt * TOK + n] >> (8 * g)) & 0xFFu;
+            if (k0 >= K) b.lo = u32x4{0u, 0u, 0u, 0u};
+            if (k0 + 64 >= K) b.hi = u32x4{0u, 0u, 0u, 0u};
+            if (128 * c + 32 * g >= K) b.s = 127u;
+            return b;
+          }, c, g, K);
+          load_a(sa[u % DA], c + DA);
+          store_b(buf ^ 1);
+          load_b(c + 2);
+          __syncthreads();
+        }
+      }
+    }
+
+    // Epilogue.
+    if (rb < out_dim) {
+#pragma unroll
+      for (int st = 0; st < NT; ++st) {
+        const int j = 16 * st + l16;
+        if constexpr (PH == PH_UP) {
+          // The wave's 32 intermediates rb .. rb+31 of token column j: one block; every lane takes
+          // part in the block maximum, only real token columns store.
+          const f32x4 y0 = up_values<Q_MXFP4>(a, blob, grp, rb + 4 * g, sum_chains(acc[0][0][st], acc[1][0][st]),
+                                              sum_chains(acc[0][RT][st], acc[1][RT][st]));
+          const f32x4 y1 = up_values<Q_MXFP4>(a, blob, grp, rb + 16 + 4 * g, sum_chains(acc[0][1][st], acc[1][1][st]),
+                                              sum_chains(acc[0][RT + 1][st], acc[1][RT + 1][st]));
+          const float v[8] = {y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
+          uint32_t hq[NTH][2], sb[NTH];
+          quant_block<NTH>(v, hq, sb);
+          if (j < ntok) store_hq(a, bslot[st], rb / 32, rb + 4 * g, rb + 16 + 4 * g, hq, sb, g);
+        } else {
+          if (j >= ntok) continue;
+#pragma unroll
+          for (int q = 0; q < RT; ++q) {
+            if (rb + 16 * q >= out_dim) continue;
+            const int h0 = rb + 16 * q + 4 * g;
+            *(f32x4 *)(a.slot_out + (size_t)bslot[st] * H + h0) =
+                down_value<Q_MXFP4>(a, blob, grp, h0, bslot[st], sum_chains(acc[0][q][st], acc[1][q][st]));
+          }
+        }
+      }
+    }
+    __syncthreads();   // the next pass restages the B buffers
   }
 }
 
@@ -772,27 +1263,32 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *slot_out, int
 
 // ---- launch table -----------------------------------------------------------------------------
 typedef void (*GemmKernel)(GemmArgs);
+typedef void (*UpSmallKernel)(GemmArgs, RouteArgs);
+typedef void (*DownSmallKernel)(GemmArgs, const int32_t *);
 
-// Decode: one 16-row tile and one 16-token tile per workgroup, deep pipelining. Prefill: 32 rows
-// and 64 (gate-up) or 32 (down, whose B operand is twice as wide) tokens per pass.
-constexpr int LAYER_KS = 4;
+// Register ring depth of the decode weight stream, in chunks (per lane per chunk: MXFP4 16 B +
+// a scale, MLX4 8 B, MLX8 16 B (+ a scale|bias pair), BF16 64 B).
+template <int FMT> constexpr int decode_depth() { return FMT == Q_BF16 ? 4 : (FMT == Q_MXFP4 ? 24 : 8); }
 
-constexpr int DECODE_TP = 4;   // tokens per LDS pass in decode
+template <int FMT> static UpSmallKernel up_small_k() {
+  if constexpr (FMT == Q_MXFP4) return up_small_mx<decode_depth<FMT>()>;
+  else return up_small<FMT, decode_depth<FMT>()>;
+}
+template <int FMT> static DownSmallKernel down_small_k(int slots) {
+  return slots <= 4 ? down_small<FMT, decode_depth<FMT>(), 4, 2> : down_small<FMT, decode_depth<FMT>(), kMaxTopK + 1, 1>;
+}
 
 template <int PH, int FMT>
 static GemmKernel pick(int nt) {
-  constexpr int DA_DECODE = (FMT == Q_BF16) ? 2 : 4;
-  if (nt <= 1) return expert_gemm<PH, FMT, 1, 1, DA_DECODE, 1, LAYER_KS, DECODE_TP>;
-  // Prefill: 4 waves × RT 16-row tiles × 32 tokens (BF16 keeps one tile per wave: its
+  if constexpr (FMT == Q_MXFP4) return nt <= 1 ? prefill_mx<PH, 2, 1, 2> : prefill_mx<PH, 2, 2, 2>;
+  // Prefill: 4 waves × RT 16-row tiles × 16·NT tokens (BF16 keeps one tile per wave: its
   // weight operand is 4× wider per chunk).
   constexpr int RT_P = (FMT == Q_BF16) ? 1 : 2;
+  if (nt <= 1) return prefill_gemm<PH, FMT, RT_P, 1, 2>;
   return prefill_gemm<PH, FMT, RT_P, 2, 2>;
 }
 
-int gemm_rows_per_block(int nt, int quant) {
-  if (nt <= 1) return (4 / LAYER_KS) * 16;
-  return 4 * 16 * (quant == Q_BF16 ? 1 : 2);
-}
+int gemm_rows_per_block(int quant) { return 4 * 16 * (quant == Q_BF16 ? 1 : 2); }
 
 static GemmKernel gemm_kernel(int phase, int quant, int nt) {
   switch (quant) {
@@ -806,11 +1302,58 @@ static GemmKernel gemm_kernel(int phase, int quant, int nt) {
 hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStream_t s, Timing tm) {
   const unsigned blocks = (unsigned)a.row_tiles * (unsigned)a.max_work;
   if (blocks == 0) return hipSuccess;
-  // Decode stages DECODE_TP B rows (x, or h_hi and h_lo) of up to K = max(H, ldh) columns.
-  const size_t kmax = (size_t)std::max(a.hidden, a.ldh);
-  const size_t lds = nt <= 1 ? (size_t)DECODE_TP * kmax * 2 * (phase == PH_UP ? 1 : 2) : 0;
-  hipExtLaunchKernelGGL(gemm_kernel(phase, quant, nt), dim3(blocks), dim3(256), lds, s, tm.start,
+  hipExtLaunchKernelGGL(gemm_kernel(phase, quant, nt), dim3(blocks), dim3(256), 0, s, tm.start,
                         tm.stop, 0, a);
+  return hipGetLastError();
+}
+
+// Decode (T ≤ 16). `a.row_tiles` is set here per phase.
+hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t s, Timing tm_up,
+                        Timing tm_down) {
+  const int T = ra.tokens;
+  if (T < 1 || T > SMALL_T) return hipErrorInvalidValue;
+  const int S = a.slots;
+  const int maxu = std::min(a.experts, T * a.top_k) + (S > a.top_k ? 1 : 0);
+  UpSmallKernel up;
+  DownSmallKernel down;
+  switch (quant) {
+  case Q_MXFP4: up = up_small_k<Q_MXFP4>(); down = down_small_k<Q_MXFP4>(S); break;
+  case Q_BF16: up = up_small_k<Q_BF16>(); down = down_small_k<Q_BF16>(S); break;
+  case Q_MLX4: up = up_small_k<Q_MLX4>(); down = down_small_k<Q_MLX4>(S); break;
+  default: up = up_small_k<Q_MLX8>(); down = down_small_k<Q_MLX8>(S); break;
+  }
+  // The decode kernels stage rows in dynamic LDS beyond the default 64 KiB window (gfx950 has
+  // 160 KiB per compute unit).
+  static std::once_flag lds_once;
+  std::call_once(lds_once, [] {
+    const void *ks[] = {(const void *)up_small_k<Q_MXFP4>(), (const void *)up_small_k<Q_BF16>(),
+                        (const void *)up_small_k<Q_MLX4>(), (const void *)up_small_k<Q_MLX8>(),
+                        (const void *)down_small_k<Q_MXFP4>(4), (const void *)down_small_k<Q_BF16>(4),
+                        (const void *)down_small_k<Q_MLX4>(4), (const void *)down_small_k<Q_MLX8>(4),
+                        (const void *)down_small_k<Q_MXFP4>(9), (const void *)down_small_k<Q_BF16>(9),
+                        (const void *)down_small_k<Q_MLX4>(9), (const void *)down_small_k<Q_MLX8>(9)};
+    // Best effort: HIP on gfx950 accepts launches up to the hardware LDS size without it, and
+    // a runtime that rejects the attribute must not leave its error for the launch check below.
+    for (const void *k : ks) {
+      (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      (void)hipGetLastError();
+    }
+  });
+  a.row_tiles = a.ldh / UP_ROWS;
+  const bool mx = quant == Q_MXFP4;
+  const size_t lds_up = mx ? (size_t)T * NTX * mx_row_bytes(a.xld) + 64 * (a.hidden / 32)
+                           : (size_t)T * (a.hidden + LDS_PAD) * 2;
+  hipExtLaunchKernelGGL(up, dim3(a.row_tiles * maxu), dim3(mx ? 256 : 512), lds_up, s, tm_up.start, tm_up.stop, 0,
+                        a, ra);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  a.row_tiles = a.hidden / 16;
+  // MXFP4: per slot the activation terms and 16 rows of weight scales (of the larger group).
+  const int imax = std::max(a.grp[0].inter, a.grp[1].inter);
+  const size_t lds_down = mx ? (size_t)S * (NTH * mx_row_bytes(a.hld) + 16 * ((16 * (imax / 32) + 15) / 16))
+                             : (size_t)S * 2 * (a.ldh + LDS_PAD) * 2;
+  hipExtLaunchKernelGGL(down, dim3(a.row_tiles * T), dim3(64 * S * (S <= 4 ? 2 : 1)), lds_down, s, tm_down.start,
+                        tm_down.stop, 0, a, (const int32_t *)ra.topk_idx);
   return hipGetLastError();
 }
 

@@ -12,18 +12,20 @@
 //   C. Dispatch: the batch's (token, rank) assignments grouped by expert, stable, plus the
 //      work list of the expert products.
 //
-// Batches of at most 16 tokens skip the screening: route_small_kernel computes every logit in
-// fp64 (one wave per (token, expert) pair, spread over many compute units) and the workgroup that
-// finishes last (a ticket counter, with release/acquire fences around it) selects and
-// dispatches. Larger batches run A over a (token tile × expert tile) grid (route_logits_kernel),
-// B one wave per token (route_select_kernel) and C in one workgroup (dispatch_kernel), ordered by
-// the stream.
+// Batches of at most 16 tokens skip the screening: logits_small_kernel computes every logit in
+// fp64 (one wave per (token, expert) pair, spread over many compute units). In the layer, the
+// decode gate-up kernel then selects from those logits itself (hh_select.hpp), so routing a
+// decode step is one launch and needs no dispatch; the operator entry hh_router_topk runs
+// select_small_kernel instead. Larger batches run A over a (token tile × expert tile) grid
+// (route_logits_kernel), B one wave per token (route_select_kernel) and C in one workgroup
+// (dispatch_kernel), ordered by the stream.
 //
 // Reference: router_topk / router_topk_batch (attention.metal:249, batch.metal:430),
 // gemma_router_topk (gemma.metal:158), ReferenceOps.router (ReferenceOps.swift:173-183),
 // QwenReferenceOps.router (:159-179), Gemma4ReferenceOps.router (:131-156),
 // PrefillRunner.assignments (PrefillRunner.swift:224-246).
 #include "hh_common.hpp"
+#include "hh_select.hpp"
 
 namespace hh {
 
@@ -37,34 +39,6 @@ __device__ __forceinline__ double wave_max_f64(double v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o));
   return v;
-}
-
-// Exclusive scan of data[0..n) in place (n ≤ 128·NW), 64·NW threads; returns the total.
-template <int NW>
-__device__ __forceinline__ int block_exclusive_scan(int *data, int n, int *s_wave) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  int a0 = (2 * tid < n) ? data[2 * tid] : 0;
-  int a1 = (2 * tid + 1 < n) ? data[2 * tid + 1] : 0;
-  int v = a0 + a1, inc = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    int y = __shfl_up(inc, o);
-    if (lane >= o) inc += y;
-  }
-  if (lane == 63) s_wave[wave] = inc;
-  __syncthreads();
-  int base = 0, total = 0;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) {
-    base += (w < wave) ? s_wave[w] : 0;
-    total += s_wave[w];
-  }
-  int ex = base + inc - v;
-  __syncthreads();
-  if (2 * tid < n) data[2 * tid] = ex;
-  if (2 * tid + 1 < n) data[2 * tid + 1] = ex + a0;
-  __syncthreads();
-  return total;
 }
 
 // Stable token→expert permutation of the whole batch by one workgroup of NW waves; `idx` is
@@ -284,71 +258,6 @@ struct TokenScreen {
   double norm = 1.0;
 };
 
-// Running exact top-k, descending, ties to the smaller index. Every lane of a wave holds the
-// same copy.
-struct TopK {
-  double v[kMaxTopK];
-  int i[kMaxTopK];
-  __device__ TopK() {
-#pragma unroll
-    for (int r = 0; r < kMaxTopK; ++r) { v[r] = -INFINITY; i[r] = 0x7FFFFFFF; }
-  }
-  // One bubble pass with static indices (registers only). The carried entry (the new one,
-  // then each displaced one) goes ahead of an entry with a smaller value, or an equal value and
-  // a larger index.
-  __device__ void insert(double x, int e, int K) {
-#pragma unroll
-    for (int r = 0; r < kMaxTopK; ++r) {
-      if (r < K && (x > v[r] || (x == v[r] && e < i[r]))) {
-        const double tv = v[r];
-        const int ti = i[r];
-        v[r] = x;
-        i[r] = e;
-        x = tv;
-        e = ti;
-      }
-    }
-  }
-};
-
-// Weights of one token's selection (whole wave; lane r < K handles rank r): tk holds the fp64
-// logits in rank order.
-__device__ __forceinline__ void finish_token(const RouteArgs &a, int t, const TopK &tk, double sg_logit) {
-  const int K = a.top_k, lane = threadIdx.x & 63;
-  double v = -INFINITY;
-  int e = 0;
-#pragma unroll
-  for (int r = 0; r < kMaxTopK; ++r)
-    if (lane == r) { v = tk.v[r]; e = tk.i[r]; }
-  // TOPK_SOFTMAX: softmax over the k selected logits (ReferenceOps.swift:178-182).
-  // SOFTMAX_TOPK_RENORM and GEMMA: softmax over all experts, renormalised over the k
-  // (QwenReferenceOps.swift:159-179, Gemma4ReferenceOps.swift:146-155); the full-softmax
-  // denominator cancels, leaving the same softmax of the k selected logits. The sum runs in
-  // rank order.
-  double w = lane < K ? exp(v - tk.v[0]) : 0.0;
-  double total = 0.0;
-#pragma unroll
-  for (int r = 0; r < kMaxTopK; ++r) {
-    const double wr = __shfl(w, r);
-    if (r < K) total += wr;
-  }
-  w /= total;
-  if (lane < K) {
-    if (a.router == R_GEMMA) w *= (double)bf16_bits_to_f32(a.router_pes[e]);
-    a.topk_idx[(size_t)t * K + lane] = e;
-    a.topk_w[(size_t)t * K + lane] = (float)w;
-    a.slot_w[(size_t)t * a.slots + lane] = (float)w;
-    if (a.logits) a.logits[(size_t)t * K + lane] = v;
-  }
-  if (a.shared_gate && lane == 0) {
-    // σ of the shared gate row, applied to the shared expert's output
-    // (QwenReferenceLayer.swift:399-404).
-    const double sg = 1.0 / (1.0 + exp(-sg_logit));
-    a.slot_w[(size_t)t * a.slots + K] = (float)sg;
-    if (a.shared_w) a.shared_w[t] = (float)sg;
-  }
-}
-
 // Screens token t (one wave): bounds every fp32 logit lgf(e) by err_e, θ = the K-th largest
 // lower bound, and writes the candidates {e : ub_e ≥ θ} to cl[] in ascending order.
 template <bool gemma, class LG, class WN>
@@ -508,124 +417,126 @@ __global__ __launch_bounds__(1024) void dispatch_kernel(RouteArgs a) {
   dispatch_batch<16>(a, a.topk_idx);
 }
 
-// ---- small batches (T ≤ 16): every logit exactly in fp64, one launch ---------------------------
-// The router rows are spread over many workgroups (one compute unit's load path would take several
-// microseconds to stream even a 32-expert router); the last workgroup to finish selects and
-// dispatches, so routing a decode step is one kernel launch.
-
-// Top-k of every token from its exact logits (wave w: tokens w, w + NW, ...), then the dispatch.
-template <int NW>
-__device__ __forceinline__ void select_and_dispatch(const RouteArgs &a) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int E = a.experts, E1 = E + 1, K = a.top_k, T = a.tokens;
-  __shared__ int s_idx[RT_TOK * kMaxTopK];
-  for (int t = wave; t < T; t += NW) {
-    const double *lg = a.lg64 + (size_t)t * E1;
-    double v[8];
+// ---- x as fp8 terms (MXFP4 layers) ----------------------------------------------------------------
+// One wave quantises 16 blocks of 32 columns of token t (quant_block): lane (g, l16) takes block
+// blk0 + l16, columns 8g .. 8g+7 of it.
+__device__ __forceinline__ void quant_x_wave(const RouteArgs &a, int t, int blk0) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, l16 = lane & 15;
+  const int H = a.hidden, nb = H / 32;
+  const int b = blk0 + l16, bc = min(b, nb - 1);
+  const u32x4 xv = *(const u32x4 *)(a.x + (size_t)t * H + bc * 32 + 8 * g);
+  float v[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int e = lane + 64 * j;
-      v[j] = e < E ? lg[e] : -INFINITY;
-    }
-    TopK tk;
-    uint32_t taken = 0;
-#pragma unroll
-    for (int r = 0; r < kMaxTopK; ++r) {
-      if (r < K) {
-        double bv = -INFINITY;
-        int bi = 0x7FFFFFFF;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int e = lane + 64 * j;
-          if (e < E && !(taken & (1u << j)) && (v[j] > bv || bi == 0x7FFFFFFF)) { bv = v[j]; bi = e; }
-        }
-        // Larger value first, smaller index on ties (attention.metal:270,
-        // ReferenceOps.swift:174-176).
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-          const double ov = __shfl_xor(bv, o);
-          const int oi = __shfl_xor(bi, o);
-          if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-        tk.v[r] = bv;
-        tk.i[r] = bi;
-        if (lane == 0) s_idx[t * K + r] = bi;
-      }
-    }
-    finish_token(a, t, tk, a.shared_gate ? lg[E] : 0.0);
+  for (int k = 0; k < 4; ++k) {
+    v[2 * k] = bf_lo(xv[k]);
+    v[2 * k + 1] = bf_hi(xv[k]);
   }
-  __syncthreads();
-  if (a.want_dispatch) dispatch_batch<NW>(a, s_idx);
+  uint32_t q[NTX][2], sb[NTX];
+  quant_block<NTX>(v, q, sb);
+  if (b < nb) {
+#pragma unroll
+    for (int j = 0; j < NTX; ++j) {
+      *(u32x2 *)(a.xq + ((size_t)t * NTX + j) * a.xld + b * 32 + 8 * g) = u32x2{q[j][0], q[j][1]};
+      if (g == 0) a.xs[((size_t)t * NTX + j) * (a.xld / 32) + b] = (uint8_t)sb[j];
+    }
+  }
 }
 
-// A: one wave per (token, expert) pair; expert id E is the shared expert's gate row. B + C: the
-// workgroup that takes the last ticket. Each workgroup releases its logits (fence) before taking
-// a ticket; the last one acquires them (fence) and re-arms the ticket for the next call, which
-// the stream orders after this one.
+__device__ __forceinline__ int quant_x_waves(const RouteArgs &a) {
+  return a.xq ? a.tokens * ((a.hidden / 32 + 15) / 16) : 0;
+}
+
+// Batches above 16 tokens: one wave per 16 blocks of a token.
+__global__ __launch_bounds__(256) void quant_x_kernel(RouteArgs a) {
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int per_t = (a.hidden / 32 + 15) / 16;
+  if (w >= a.tokens * per_t) return;
+  quant_x_wave(a, w / per_t, 16 * (w % per_t));
+}
+
+// ---- small batches (T ≤ 16): every logit exactly in fp64 -----------------------------------------
+// One wave per (token, expert) pair, spread over many compute units (one compute unit's load path
+// would take several microseconds to stream even a 32-expert router); expert id E is the shared
+// expert's gate row. Writes lg64 [T][E+1].
+// Waves past the logits quantise x (MXFP4 layers).
 template <bool gemma>
-__global__ __launch_bounds__(256) void route_small_kernel(RouteArgs a) {
+__global__ __launch_bounds__(256) void logits_small_kernel(RouteArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int E = a.experts, E1 = E + 1, H = a.hidden;
   const int p = blockIdx.x * 4 + wave;
-  const int t = p / E1, e = p - t * E1;
-  if (p < a.tokens * E1 && (e < E || a.shared_gate)) {
-    double v;
-    if (e < E) {
-      const uint16_t *xr = a.xr + (size_t)t * H;
-      double norm = 1.0, root = 1.0;
-      if constexpr (gemma) {
-        double xx = 0.0;
-        for (int base = 0; base < H; base += 2048) {
-          u32x4 xv[4];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int h = base + lane * 8 + 512 * u;
-            xv[u] = *(const u32x4 *)(xr + min(h, H - 8));
-            if (h >= H) xv[u] = u32x4{0u, 0u, 0u, 0u};
-          }
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            double px = 0.0;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-              const float xf = bf16_bits_to_f32((xv[u][k >> 1] >> ((k & 1) * 16)) & 0xFFFF);
-              px += (double)(xf * xf);
-            }
-            xx += px;
-          }
-        }
-        xx = wave_sum_f64(xx);
-        norm = pow(xx / (double)H + (double)a.eps, -0.5);
-        root = pow((double)H, -0.5);
-      }
-      v = exact_logit<gemma>(a, xr, a.router_w + (size_t)e * H, norm, root);
-      if (a.router_b) v += (double)bf16_bits_to_f32(a.router_b[e]);
-    } else {
-      v = exact_logit<false>(a, a.x + (size_t)t * H, a.shared_gate, 1.0, 1.0);
+  if (p >= a.tokens * E1) {
+    const int w = p - a.tokens * E1;
+    if (w < quant_x_waves(a)) {
+      const int per_t = (H / 32 + 15) / 16;
+      quant_x_wave(a, w / per_t, 16 * (w % per_t));
     }
-    if (lane == 0) a.lg64[(size_t)t * E1 + e] = v;
+    return;
   }
-  __shared__ int s_last;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __threadfence();
-    s_last = atomicAdd(a.ticket, 1) == (int)gridDim.x - 1;
+  const int t = p / E1, e = p - t * E1;
+  if (e == E && !a.shared_gate) return;
+  double v;
+  if (e < E) {
+    const uint16_t *xr = a.xr + (size_t)t * H;
+    double norm = 1.0, root = 1.0;
+    if constexpr (gemma) {
+      double xx = 0.0;
+      for (int base = 0; base < H; base += 2048) {
+        u32x4 xv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int h = base + lane * 8 + 512 * u;
+          xv[u] = *(const u32x4 *)(xr + min(h, H - 8));
+          if (h >= H) xv[u] = u32x4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          double px = 0.0;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const float xf = bf16_bits_to_f32((xv[u][k >> 1] >> ((k & 1) * 16)) & 0xFFFF);
+            px += (double)(xf * xf);
+          }
+          xx += px;
+        }
+      }
+      xx = wave_sum_f64(xx);
+      norm = pow(xx / (double)H + (double)a.eps, -0.5);
+      root = pow((double)H, -0.5);
+    }
+    v = exact_logit<gemma>(a, xr, a.router_w + (size_t)e * H, norm, root);
+    if (a.router_b) v += (double)bf16_bits_to_f32(a.router_b[e]);
+  } else {
+    v = exact_logit<false>(a, a.x + (size_t)t * H, a.shared_gate, 1.0, 1.0);
   }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  select_and_dispatch<4>(a);
-  if (threadIdx.x == 0) *a.ticket = 0;
+  if (lane == 0) a.lg64[(size_t)t * E1 + e] = v;
+}
+
+// Top-k and weights of every token from lg64 (operator entry hh_router_topk, T ≤ 16): one
+// workgroup, wave w takes tokens w, w + 4, ...
+__global__ __launch_bounds__(256) void select_small_kernel(RouteArgs a) {
+  const int wave = threadIdx.x >> 6;
+  const int E1 = a.experts + 1;
+  for (int t = wave; t < a.tokens; t += 4) {
+    const double *lg = a.lg64 + (size_t)t * E1;
+    const TopK tk = topk_exact(lg, a.experts, a.top_k);
+    finish_token(a, t, tk, a.shared_gate ? lg[a.experts] : 0.0);
+  }
 }
 }  // namespace hh
 
 namespace hh {
 hipError_t launch_route(const RouteArgs &a, hipStream_t s, Timing tm) {
   if (a.tokens <= RT_TOK) {
-    const int pairs = a.tokens * (a.experts + 1);
-    hipExtLaunchKernelGGL(a.router == R_GEMMA ? route_small_kernel<true> : route_small_kernel<false>,
-                          dim3((pairs + 3) / 4), dim3(256), 0, s, tm.start, tm.stop, 0, a);
+    // The layer (want_dispatch) selects inside its gate-up kernel; the operator entry selects
+    // here.
+    const int waves = a.tokens * (a.experts + 1) + (a.xq ? a.tokens * ((a.hidden / 32 + 15) / 16) : 0);
+    const bool sel = a.want_dispatch == 0;
+    hipExtLaunchKernelGGL(a.router == R_GEMMA ? logits_small_kernel<true> : logits_small_kernel<false>,
+                          dim3((waves + 3) / 4), dim3(256), 0, s, tm.start, sel ? nullptr : tm.stop,
+                          0, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !sel) return e;
+    hipExtLaunchKernelGGL(select_small_kernel, dim3(1), dim3(256), 0, s, nullptr, tm.stop, 0, a);
     return hipGetLastError();
   }
   const int ttiles = (a.tokens + RT_TOK - 1) / RT_TOK;
@@ -636,6 +547,11 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s, Timing tm) {
                         nullptr, 0, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (a.xq) {
+    const int qw = a.tokens * ((a.hidden / 32 + 15) / 16);
+    hipExtLaunchKernelGGL(quant_x_kernel, dim3((qw + 3) / 4), dim3(256), 0, s, nullptr, nullptr, 0, a);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
   hipExtLaunchKernelGGL(g ? route_select_kernel<true> : route_select_kernel<false>, dim3((a.tokens + 3) / 4), dim3(256), 0, s, nullptr,
                         third ? nullptr : tm.stop, 0, a);
   e = hipGetLastError();

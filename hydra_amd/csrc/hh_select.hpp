@@ -1,0 +1,179 @@
+// hh_select.hpp — exact top-k selection and routing weights, shared by the router kernels and by
+// the decode gate-up kernel (which selects redundantly in every workgroup instead of waiting for a
+// separate selection launch).
+//
+// Reference: ReferenceOps.router (ReferenceOps.swift:173-183), QwenReferenceOps.router
+// (QwenReferenceOps.swift:159-179), Gemma4ReferenceOps.router (Gemma4ReferenceOps.swift:131-156),
+// router_topk (attention.metal:249-300: larger value first, smaller index on ties).
+#pragma once
+#include "hh_common.hpp"
+
+namespace hh {
+
+// Exclusive scan of data[0..n) in place (n ≤ 128·NW), 64·NW threads; returns the total.
+template <int NW>
+__device__ __forceinline__ int block_exclusive_scan(int *data, int n, int *s_wave) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int a0 = (2 * tid < n) ? data[2 * tid] : 0;
+  int a1 = (2 * tid + 1 < n) ? data[2 * tid + 1] : 0;
+  int v = a0 + a1, inc = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    int y = __shfl_up(inc, o);
+    if (lane >= o) inc += y;
+  }
+  if (lane == 63) s_wave[wave] = inc;
+  __syncthreads();
+  int base = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    base += (w < wave) ? s_wave[w] : 0;
+    total += s_wave[w];
+  }
+  int ex = base + inc - v;
+  __syncthreads();
+  if (2 * tid < n) data[2 * tid] = ex;
+  if (2 * tid + 1 < n) data[2 * tid + 1] = ex + a0;
+  __syncthreads();
+  return total;
+}
+
+// Running exact top-k, descending, ties to the smaller index. Every lane of a wave holds the
+// same copy.
+struct TopK {
+  double v[kMaxTopK];
+  int i[kMaxTopK];
+  __device__ TopK() {
+#pragma unroll
+    for (int r = 0; r < kMaxTopK; ++r) { v[r] = -INFINITY; i[r] = 0x7FFFFFFF; }
+  }
+  // One bubble pass with static indices (registers only). The carried entry (the new one,
+  // then each displaced one) goes ahead of an entry with a smaller value, or an equal value and
+  // a larger index.
+  __device__ void insert(double x, int e, int K) {
+#pragma unroll
+    for (int r = 0; r < kMaxTopK; ++r) {
+      if (r < K && (x > v[r] || (x == v[r] && e < i[r]))) {
+        const double tv = v[r];
+        const int ti = i[r];
+        v[r] = x;
+        i[r] = e;
+        x = tv;
+        e = ti;
+      }
+    }
+  }
+  // Index of rank r (r < kMaxTopK) read with a static index per case, so the arrays stay in
+  // registers.
+  __device__ int index_of(int r) const {
+    int e = 0;
+#pragma unroll
+    for (int q = 0; q < kMaxTopK; ++q)
+      if (q == r) e = i[q];
+    return e;
+  }
+};
+
+// Top-k of one token from its exact logits lg[0..E) (E ≤ 512), whole wave: K rounds of a wave
+// arg-max, larger value first and the smaller index on ties.
+__device__ __forceinline__ TopK topk_exact(const double *lg, int E, int K) {
+  const int lane = threadIdx.x & 63;
+  double v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int e = lane + 64 * j;
+    v[j] = e < E ? lg[e] : -INFINITY;
+  }
+  TopK tk;
+  uint32_t taken = 0;
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r) {
+    if (r < K) {
+      double bv = -INFINITY;
+      int bi = 0x7FFFFFFF;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int e = lane + 64 * j;
+        if (e < E && !(taken & (1u << j)) && (v[j] > bv || bi == 0x7FFFFFFF)) { bv = v[j]; bi = e; }
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const double ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+      }
+      if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+      tk.v[r] = bv;
+      tk.i[r] = bi;
+    }
+  }
+  return tk;
+}
+
+// The same selection for E ≤ 64 by rank counting: lane e holds logit e and counts the logits
+// that precede it (larger, or equal with a smaller index) from a copy in the wave's LDS row
+// s_lg[64]; the lanes of rank < K publish themselves in s_ri[8]. Independent LDS reads replace
+// the K dependent shuffle chains of topk_exact (the decode critical path).
+__device__ __forceinline__ TopK topk_rank64(const double *lg, int E, int K, double *s_lg, int *s_ri) {
+  const int lane = threadIdx.x & 63;
+  const double v = lane < E ? lg[lane] : -INFINITY;
+  s_lg[lane] = v;
+  __builtin_amdgcn_wave_barrier();
+  int rank = 0;
+#pragma unroll 8
+  for (int j = 0; j < E; ++j) {
+    const double o = s_lg[j];
+    rank += (o > v || (o == v && j < lane)) ? 1 : 0;
+  }
+  if (lane < E && rank < K) s_ri[rank] = lane;
+  __builtin_amdgcn_wave_barrier();
+  TopK tk;
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r) {
+    if (r < K) {
+      tk.i[r] = s_ri[r];
+      tk.v[r] = s_lg[tk.i[r]];
+    }
+  }
+  return tk;
+}
+
+// Weights of one token's selection (whole wave; lane r < K handles rank r): tk holds the fp64
+// logits in rank order. Writes topk_idx/topk_w/slot_w (and logits, shared_w when given).
+__device__ __forceinline__ void finish_token(const RouteArgs &a, int t, const TopK &tk, double sg_logit) {
+  const int K = a.top_k, lane = threadIdx.x & 63;
+  double v = -INFINITY;
+  int e = 0;
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r)
+    if (lane == r) { v = tk.v[r]; e = tk.i[r]; }
+  // TOPK_SOFTMAX: softmax over the k selected logits (ReferenceOps.swift:178-182).
+  // SOFTMAX_TOPK_RENORM and GEMMA: softmax over all experts, renormalised over the k
+  // (QwenReferenceOps.swift:159-179, Gemma4ReferenceOps.swift:146-155); the full-softmax
+  // denominator cancels, leaving the same softmax of the k selected logits. The sum runs in
+  // rank order.
+  double w = lane < K ? exp(v - tk.v[0]) : 0.0;
+  double total = 0.0;
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r) {
+    const double wr = __shfl(w, r);
+    if (r < K) total += wr;
+  }
+  w /= total;
+  if (lane < K) {
+    if (a.router == R_GEMMA) w *= (double)bf16_bits_to_f32(a.router_pes[e]);
+    a.topk_idx[(size_t)t * K + lane] = e;
+    if (a.topk_w) a.topk_w[(size_t)t * K + lane] = (float)w;
+    a.slot_w[(size_t)t * a.slots + lane] = (float)w;
+    if (a.logits) a.logits[(size_t)t * K + lane] = v;
+  }
+  if (a.shared_gate && lane == 0) {
+    // σ of the shared gate row, applied to the shared expert's output
+    // (QwenReferenceLayer.swift:399-404).
+    const double sg = 1.0 / (1.0 + exp(-sg_logit));
+    a.slot_w[(size_t)t * a.slots + K] = (float)sg;
+    if (a.shared_w) a.shared_w[t] = (float)sg;
+  }
+}
+
+}  // namespace hh

@@ -286,9 +286,9 @@ def test_layer_is_deterministic_and_order_independent(torch_dev, ctx):
 # ---- real shapes ----------------------------------------------------------------------------
 
 FULL = {
-    "gpt-oss-20b": (F.GPT_OSS_20B, None, [1, 2, 4, 8]),
+    "gpt-oss-20b": (F.GPT_OSS_20B, None, [1, 2, 4, 8, 16]),
     "gpt-oss-120b-zipf": (F.GPT_OSS_120B, 1.1, [512]),
-    "qwen-q4": (F.QWEN_35B_A3B_Q4, None, [1, 1024]),
+    "qwen-q4": (F.QWEN_35B_A3B_Q4, None, [1, 16, 1024]),
     "qwen-q8": (F.QWEN_35B_A3B_Q8, None, [1, 1024]),
     "gemma-bf16": (F.GEMMA_BF16, None, [1, 2048]),
 }
