@@ -17,7 +17,7 @@ hipError_t launch_permute(const RouteArgs &a, hipStream_t s);
 hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStream_t s, Timing tm);
 hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t s, Timing tm_up,
                         Timing tm_down);
-int gemm_rows_per_block(int quant);
+int gemm_rows_per_block(int quant, int phase);
 hipError_t launch_combine(const float *slot_out, int slots, int H, int T, float *y, hipStream_t s,
                           Timing tm);
 hipError_t launch_mxfp4_dequant(const uint8_t *blocks, const uint8_t *scales, int64_t n,
@@ -75,8 +75,9 @@ struct Scratch {
 constexpr int kSmallT = 16;  // batches up to this size take the decode kernels
 
 int token_tile_nt(const hh_moe_desc &d, int T) {
-  // Prefill kernel token tiles: 16 tokens while experts see a handful of tokens, 32 once batches
-  // are large enough for experts to fill them.
+  // Prefill kernel token tiles of 16: MXFP4 passes of 32 or 64 tokens, the other formats 16 or
+  // 32, the larger once batches are big enough for experts to fill them.
+  if (d.quant == HH_QUANT_MXFP4) return (T >= 128) ? 4 : 2;
   return (T >= 64) ? 2 : 1;
 }
 
@@ -344,7 +345,9 @@ int hh_ctx_reserve(hh_ctx *ctx, const hh_moe_desc *d, int32_t max_tokens) {
   // The plan for a batch that switches to 64-token tiles can be smaller than for a batch just
   // below the switch; reserve the larger of the two.
   size_t need = 0;
-  for (int t : {max_tokens, std::min(max_tokens, 63)}) need = std::max(need, plan(*d, t).total);
+  // Plans just below a token-tile switch can exceed the one for max_tokens.
+  for (int t : {max_tokens, std::min(max_tokens, 63), std::min(max_tokens, 127)})
+    need = std::max(need, plan(*d, t).total);
   return ensure_arena(ctx, need);
 }
 
@@ -431,10 +434,11 @@ int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
     ctx->dispatches += 3;
     return HH_OK;
   }
-  const int rows = hh::gemm_rows_per_block(d->quant);
+  int rows = hh::gemm_rows_per_block(d->quant, 0);
   g.row_tiles = (s.ldh + rows - 1) / rows;
   if ((rc = phase_timing(ctx, &tm))) return rc;
   HH_HIP(hh::launch_gemm(0, d->quant, s.nt, g, ctx->stream, tm));
+  rows = hh::gemm_rows_per_block(d->quant, 1);
   g.row_tiles = (d->hidden + rows - 1) / rows;
   if ((rc = phase_timing(ctx, &tm))) return rc;
   HH_HIP(hh::launch_gemm(1, d->quant, s.nt, g, ctx->stream, tm));

@@ -715,100 +715,163 @@ __device__ __forceinline__ MxStage<NTERM, NB, RowOf> mx_stage(uint8_t *dst, cons
   return MxStage<NTERM, NB, RowOf>(dst, q, sc, ld, nrows, row_of, id, threads);
 }
 
-// Decode gate-up on the scaled MFMA. Grid: row tile rt (32 intermediates) × u (as up_small). 4
-// waves: wave w takes tile q = w & 1 (16 intermediates) and the gate (w < 2) or up rows, over the
-// whole K with both chains; x comes as NTX fp8 terms. The gate waves combine gate and up and write
-// the activations of the 32-intermediate block to LDS; wave 0 writes them as NTH fp8 terms.
+// Decode gate-up on the scaled MFMA, persistent: the grid holds about two workgroups per compute
+// unit; each selects the top-k of the batch once, lists the batch's distinct experts in LDS (in
+// order of first appearance in the (token, rank) table, the shared expert last) and stages every
+// token's x terms, then takes work items it = blockIdx.x, blockIdx.x + gridDim.x, ... An item is
+// 32 intermediates of one expert. 4 waves: wave w takes tile q = w & 1 (16 intermediates) and the
+// gate (w < 2) or up rows over the whole K (both chains); the item's 64 rows' e8m0 scales come
+// through LDS. The gate waves combine gate and up and write the block's activations to LDS; wave
+// 0 writes them as NTH fp8 terms. Each item issues its whole weight stream at once; co-resident
+// workgroups hide one another's latency.
 template <int DA>
-__global__ __launch_bounds__(256) void up_small_mx(GemmArgs a, RouteArgs ra) {
+__global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) {
   constexpr int NM = 1;
-  extern __shared__ __align__(16) uint8_t s_xb[];   // [ntok][NTX] rows of mx_row_bytes(xld)
+  constexpr int NE = SMALL_T * kMaxTopK + 1;
+  extern __shared__ __align__(16) uint8_t s_xb[];   // [T][NTX] rows of mx_row_bytes(xld), then [64][H/32] scales
   __shared__ int s_idx[SMALL_T * kMaxTopK];
+  __shared__ int s_uexp[NE];
+  __shared__ uint64_t s_utm[NE];
+  __shared__ int s_nu;
   __shared__ f32x4 s_up[2][64];
   __shared__ float s_hv[SMALL_T][UP_ROWS];
+  __shared__ double s_lg[4][64];
+  __shared__ int s_ri[4][kMaxTopK];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, l16 = lane & 15;
-  const int K = a.top_k, S = a.slots, H = a.hidden;
-  const int rt = blockIdx.x % a.row_tiles, u = blockIdx.x / a.row_tiles;
-  const bool shared_wg = S > K && u == (int)(gridDim.x / a.row_tiles) - 1;
-  const ExpertGroup &grp = a.grp[shared_wg ? 1 : 0];
-  const int I = grp.inter;
-  if (rt * UP_ROWS >= I) return;
+  const int T = ra.tokens, E = a.experts, K = a.top_k, S = a.slots, H = a.hidden;
+  const bool has_shared = S > K;
 
-  SmallPick pk;
-  if (!small_pick<4>(a, ra, u, shared_wg, s_idx, pk)) return;
-  const int e = pk.e, ntok = pk.ntok;
-  const uint64_t tm = pk.tm;
-  const uint8_t *blob = grp.blobs + (shared_wg ? 0 : (size_t)e * grp.stride);
+  // Top-k of every token (wave w: tokens w, w + 4, ...); workgroup 0 writes the routing outputs.
+  for (int t = wave; t < T; t += 4) {
+    const double *lg = ra.lg64 + (size_t)t * (E + 1);
+    const TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave]) : topk_exact(lg, E, K);
+    if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
+    if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
+  }
+  // x terms of every token: first batch of loads now, stored with the first item.
+  const int RS = mx_row_bytes(a.xld);
+  auto xs = mx_stage<NTX, 2>(s_xb, a.xq, a.xs, a.xld, T, [](int j) { return j; }, tid, 256);
+  xs.load_first();
+  __syncthreads();
+  if (wave == 0) {
+    // Distinct experts in order of first appearance, and the tokens of each.
+    const int n = T * K;   // ≤ 128: entries lane and lane + 64
+    bool first[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int i = lane + 64 * h;
+      first[h] = i < n;
+      if (i < n) {
+        const int ei = s_idx[i];
+        for (int j = 0; j < i; ++j) first[h] = first[h] && s_idx[j] != ei;
+      }
+    }
+    const uint64_t m0 = __ballot(first[0]), m1 = __ballot(first[1]);
+    const uint64_t lt = (1ull << lane) - 1ull;
+    const int n0 = __popcll(m0), nu = n0 + __popcll(m1);
+    if (first[0]) s_uexp[__popcll(m0 & lt)] = s_idx[lane];
+    if (first[1]) s_uexp[n0 + __popcll(m1 & lt)] = s_idx[lane + 64];
+    __builtin_amdgcn_wave_barrier();
+    for (int u = lane; u < nu; u += 64) {
+      const int e = s_uexp[u];
+      uint64_t tm = 0;
+      for (int t = 0; t < T; ++t)
+        for (int r = 0; r < K; ++r)
+          if (s_idx[t * K + r] == e) tm |= 1ull << t;
+      s_utm[u] = tm;
+    }
+    if (lane == 0) {
+      s_nu = nu;
+      s_uexp[nu] = E;                       // the shared expert, every token
+      s_utm[nu] = T >= 64 ? ~0ull : (1ull << T) - 1ull;
+    }
+  }
+  __syncthreads();
+  const int nu = s_nu;
+  const int rtr = a.grp[0].inter / UP_ROWS;
+  const int nitems = nu * rtr + (has_shared ? a.grp[1].inter / UP_ROWS : 0);
 
   const int q = wave & 1;
   const bool is_up = wave >= 2;
-  const int rb = rt * UP_ROWS + 16 * q;
-  ATile<Q_MXFP4_W> at[NM] = {tile_of<PH_UP, Q_MXFP4_W>(blob, grp, rb, is_up, H, l16)};
   const int nch = (H + 127) / 128;
-  const int RS = mx_row_bytes(a.xld);
-  // The workgroup's 64 gate_up rows' scales (contiguous: rows 64·rt ..) and the tokens' x terms:
-  // first loads out before the weight stream, stored after it.
   const int nsb = H / 32;                            // scale bytes per row
-  uint8_t *s_sc = s_xb + (size_t)ntok * NTX * RS;   // [64][nsb]
+  uint8_t *s_sc = s_xb + (size_t)T * NTX * RS;      // [64][nsb]
   const int nsv = scale_vectors(64, H);
-  const uint8_t *gsc = blob + grp.off[1] + (size_t)rt * 64 * nsb;
-  u32x4 scv[2];
-#pragma unroll
-  for (int k = 0; k < 2; ++k) scv[k] = *(const u32x4 *)(gsc + 16 * min(tid + 256 * k, nsv - 1));
-  auto xs = mx_stage<NTX, 2>(s_xb, a.xq, a.xs, a.xld, ntok, [&](int j) { return nth_bit(tm, j); }, tid, 256);
-  xs.load_first();
-  AStream<Q_MXFP4_W, NM, DA> as(0, 1, nch);
-  as.fill(at, nch, g, H);
-#pragma unroll
-  for (int k = 0; k < 2; ++k)
-    if (tid + 256 * k < nsv) *(u32x4 *)(s_sc + 16 * (tid + 256 * k)) = scv[k];
-  for (int v = tid + 512; v < nsv; v += 256) *(u32x4 *)(s_sc + 16 * v) = *(const u32x4 *)(gsc + 16 * v);
-  xs.store_first();
-  xs.rest();
-  __syncthreads();
-  const uint8_t *my_sc = s_sc + (2 * (16 * q + l16) + (is_up ? 1 : 0)) * nsb;
+  bool x_pending = true;
+  for (int it = blockIdx.x; it < nitems; it += gridDim.x) {
+    const bool sh = it >= nu * rtr;
+    const int u = sh ? nu : it / rtr;
+    const int rt = sh ? it - nu * rtr : it % rtr;
+    const int e = s_uexp[u];
+    const uint64_t tm = s_utm[u];
+    const int ntok = __popcll(tm);
+    const ExpertGroup &grp = a.grp[sh ? 1 : 0];
+    const uint8_t *blob = grp.blobs + (sh ? 0 : (size_t)e * grp.stride);
+    const int rb = rt * UP_ROWS + 16 * q;
 
-  const uint8_t *brow = s_xb + (size_t)min(l16, ntok - 1) * NTX * RS;
-  f32x4 acc[2][NM][1];
+    // The item's 64 gate_up rows' scales (contiguous: rows 64·rt ..), first loads out before the
+    // weight stream, stored after it (with the x terms on the first item).
+    const uint8_t *gsc = blob + grp.off[1] + (size_t)rt * 64 * nsb;
+    u32x4 scv[2];
 #pragma unroll
-  for (int p = 0; p < 2; ++p) acc[p][0][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-  as.run(at, nch, g, H, [&](const Fmt<Q_MXFP4_W>::A (&w)[NM], int c) {
-    auto bf = [&](int, int t) { return mx_b(brow + t * RS, brow + t * RS + a.xld, c, g, H); };
-    const u32x4 wv[NM] = {w[0].w};
-    const uint32_t sv[NM] = {my_sc[min(4 * c + g, nsb - 1)]};
-    if (c & 1) chunk_mx<NM, 1, NTX>(acc[1], wv, sv, bf, c, g, H);
-    else chunk_mx<NM, 1, NTX>(acc[0], wv, sv, bf, c, g, H);
-  });
-  const f32x4 res = sum_chains(acc[0][0][0], acc[1][0][0]);
-  if (is_up) s_up[q][lane] = res;
-  __syncthreads();
-  if (!is_up && l16 < ntok) {
-    const f32x4 y = up_values<Q_MXFP4>(a, blob, grp, rb + 4 * g, res, s_up[q][lane]);
-#pragma unroll
-    for (int ii = 0; ii < 4; ++ii) s_hv[l16][16 * q + 4 * g + ii] = y[ii];
-  }
-  __syncthreads();
-  if (wave == 0) {
-    // Lane (g, l16): activations 8g .. 8g+7 of the block of token column l16.
-    const int j = min(l16, ntok - 1);
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = s_hv[j][8 * g + i];
-    uint32_t hq[NTH][2], sb[NTH];
-    quant_block<NTH>(v, hq, sb);
-    if (l16 < ntok) {
-      const int t = nth_bit(tm, l16);
-      const int slot = t * S + rank_of(s_idx, t, e, K, shared_wg);
-      store_hq(a, slot, rt, rt * UP_ROWS + 8 * g, rt * UP_ROWS + 8 * g + 4, hq, sb, g);
+    for (int k = 0; k < 2; ++k) scv[k] = *(const u32x4 *)(gsc + 16 * min(tid + 256 * k, nsv - 1));
+    ATile<Q_MXFP4_W> at[NM] = {tile_of<PH_UP, Q_MXFP4_W>(blob, grp, rb, is_up, H, l16)};
+    AStream<Q_MXFP4_W, NM, DA> as(0, 1, nch);
+    as.fill(at, nch, g, H);
+    if (x_pending) {
+      xs.store_first();
+      xs.rest();
+      x_pending = false;
     }
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      if (tid + 256 * k < nsv) *(u32x4 *)(s_sc + 16 * (tid + 256 * k)) = scv[k];
+    for (int v = tid + 512; v < nsv; v += 256) *(u32x4 *)(s_sc + 16 * v) = *(const u32x4 *)(gsc + 16 * v);
+    __syncthreads();
+
+    const uint8_t *my_sc = s_sc + (2 * (16 * q + l16) + (is_up ? 1 : 0)) * nsb;
+    const int my_t = nth_bit(tm, min(l16, ntok - 1));   // token of column l16 (padding repeats)
+    const uint8_t *brow = s_xb + (size_t)my_t * NTX * RS;
+    f32x4 acc[NM][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
+    as.run(at, nch, g, H, [&](const Fmt<Q_MXFP4_W>::A (&w)[NM], int c) {
+      auto bf = [&](int, int t) { return mx_b(brow + t * RS, brow + t * RS + a.xld, c, g, H); };
+      const u32x4 wv[NM] = {w[0].w};
+      const uint32_t sv[NM] = {my_sc[min(4 * c + g, nsb - 1)]};
+      chunk_mx<NM, 1, NTX>(acc, wv, sv, bf, c, g, H);
+    });
+    const f32x4 res = acc[0][0];
+    if (is_up) s_up[q][lane] = res;
+    __syncthreads();
+    if (!is_up && l16 < ntok) {
+      const f32x4 y = up_values<Q_MXFP4>(a, blob, grp, rb + 4 * g, res, s_up[q][lane]);
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) s_hv[l16][16 * q + 4 * g + ii] = y[ii];
+    }
+    __syncthreads();
+    if (wave == 0) {
+      // Lane (g, l16): activations 8g .. 8g+7 of the block of token column l16.
+      const int j = min(l16, ntok - 1);
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = s_hv[j][8 * g + i];
+      uint32_t hq[NTH][2], sb[NTH];
+      quant_block<NTH>(v, hq, sb);
+      if (l16 < ntok) {
+        const int t = nth_bit(tm, l16);
+        const int slot = t * S + rank_of(s_idx, t, e, K, sh);
+        store_hq(a, slot, rt, rt * UP_ROWS + 8 * g, rt * UP_ROWS + 8 * g + 4, hq, sb, g);
+      }
+    }
+    // s_hv and s_sc are rewritten by the next item only after its first barrier.
   }
 }
 
 // ---- decode: down + combine -----------------------------------------------------------------------
-// Grid: (16 hidden rows) × token. Wave (r, p): slot r of the token (expert topk_idx[t][r], or the
+// Persistent: work items (16 hidden rows, token t) = it = blockIdx.x, blockIdx.x + gridDim.x, ...
+// Wave (r, p): slot r of the token (expert topk_idx[t][r], or the
 // shared expert), chunk parity p when KS = 2 (both chains in one wave when KS = 1). The epilogue
 // sums the chains, then the slots in rank order (sum_expert_slices, dense.metal:147;
 // ReferenceLayer.swift:194-202). SMAX = the most slots a token has under this instantiation.
@@ -822,10 +885,11 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, l16 = lane & 15;
   const int S = a.slots, K = a.top_k, H = a.hidden, E = a.experts;
-  const int T = gridDim.x / a.row_tiles;
-  const int logical = xcd_logical(blockIdx.x, gridDim.x);
-  const int rt = logical / T, t = logical - rt * T;
+  const int T = a.max_work;              // tokens of the batch
+  const int nitems = a.row_tiles * T;
   const int r = wave % S, par = wave / S;
+  for (int it = blockIdx.x; it < nitems; it += gridDim.x) {
+  const int rt = it / T, t = it - rt * T;
   const int slot = t * S + r;
   const int e = r < K ? topk_idx[t * K + r] : E;
   const int gsel = e == E ? 1 : 0;
@@ -873,8 +937,7 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
       auto bf = [&](int, int t) { return mx_b(brow + t * RS, brow + t * RS + a.hld, c, g, I); };
       const u32x4 wv[NM] = {w[0].w};
       const uint32_t sv[NM] = {my_sc[min(4 * c + g, nsb - 1)]};
-      if (KS == 1 && (c & 1)) chunk_mx<NM, 1, NTH>(acc[1], wv, sv, bf, c, g, I);
-      else chunk_mx<NM, 1, NTH>(acc[0], wv, sv, bf, c, g, I);
+      chunk_mx<NM, 1, NTH>(acc[0], wv, sv, bf, c, g, I);   // MXFP4: one chain
     });
   } else {
   // This slot's activation (hi, lo) into LDS (the slot's two waves share it): the loads go out
@@ -918,7 +981,8 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
     if (par == 0 && l16 == 0) acc[1][0][0] = s_odd[r][g];
   }
   if (par == 0 && l16 == 0) {
-    const f32x4 o = down_value<FMT>(a, blob, grp, rb + 4 * g, slot, sum_chains(acc[0][0][0], acc[1][0][0]));
+    const f32x4 o = down_value<FMT>(a, blob, grp, rb + 4 * g, slot,
+                                    FMT == Q_MXFP4 ? acc[0][0][0] : sum_chains(acc[0][0][0], acc[1][0][0]));
 #pragma unroll
     for (int ii = 0; ii < 4; ++ii) s_o[r][4 * g + ii] = o[ii];
   }
@@ -927,6 +991,8 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
     float y = s_o[0][tid];
     for (int qq = 1; qq < S; ++qq) y += s_o[qq][tid];
     a.y[(size_t)t * H + rb + tid] = y;
+  }
+  __syncthreads();   // the next item rewrites the LDS rows and s_o
   }
 }
 
@@ -1244,6 +1310,231 @@ __global__ __launch_bounds__(256) void prefill_mx(GemmArgs a) {
   }
 }
 
+// ---- prefill, MXFP4, producer/consumer workgroups ----------------------------------------------------
+// 8 waves: waves 4-7 load, waves 0-3 multiply. Per 128-column chunk the loaders bring the chunk of
+// the workgroup's 128 weight rows (8 KiB of fp4 blocks) and of the pass's NTOK token operands
+// (NTERM fp8 terms × 128 B each, XOR-swizzled by token, plus their block scales) into a
+// double-buffered LDS stage, keeping R chunks in flight in their registers; the weight rows' e8m0
+// scales for the whole K are staged once. One barrier per chunk. The MFMA waves form a 2 × 2
+// grid of 64 rows × 16·NTW tokens (4 row tiles × NTW token tiles each). Weight rows are the
+// matrix's consecutive rows: for gate_up (gate/up interleaved, ReferenceLayer.swift:11) a tile
+// holds 8 intermediates' gate and up rows, so each lane pairs gate and up in its own D fragment,
+// and a wave's 64 rows are one 32-intermediate block of the activation terms. Per output
+// element the arithmetic is the canonical one (the decode kernels' bits).
+template <int PH, int NTW>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void prefill_mx2(GemmArgs a) {
+  constexpr int NTERM = (PH == PH_UP) ? NTX : NTH;
+  constexpr int NTOK = 32 * NTW;            // tokens per pass
+  constexpr int MR = 128;                   // weight rows per workgroup
+  constexpr int AV = MR * 4;                // 16-byte weight vectors per chunk
+  constexpr int BV = NTERM * NTOK * 8;      // 16-byte operand vectors per chunk
+  constexpr int BS = NTERM * NTOK;          // operand scale dwords per chunk
+  constexpr int APL = AV / 256;             // per loader thread
+  constexpr int BPL = (BV + 255) / 256;
+  // Loader ring depth (chunks in flight), within the 128 registers that let two workgroups
+  // share a compute unit.
+  constexpr int R = (APL + BPL) * 4 * 3 <= 80 ? 3 : 2;
+  static_assert(AV % 256 == 0 && BS <= 256, "loader assignment");
+  __shared__ __align__(16) u32x4 sA[2][AV];
+  __shared__ __align__(16) u32x4 sB[2][BV];
+  __shared__ uint32_t sBs[2][BS];
+  __shared__ float sBias[MR];                       // bias of the workgroup's weight rows
+  extern __shared__ __align__(16) uint8_t sAS[];   // [MR][K/32] weight scales
+
+  const int logical = xcd_logical(blockIdx.x, gridDim.x);
+  const int rt = logical / a.max_work;
+  const int wi = logical - rt * a.max_work;
+  if (rt >= a.row_tiles || wi >= *a.n_work) return;
+  const int4 item = a.work[wi];
+  const int e = item.x, pos0 = item.y, nitem = item.z;
+  const int gsel = (e == a.experts) ? 1 : 0;
+  const ExpertGroup &grp = a.grp[gsel];
+  const uint8_t *blob = grp.blobs + (gsel ? 0 : (size_t)e * grp.stride);
+  const int I = grp.inter, H = a.hidden;
+  const int out_dim = (PH == PH_UP) ? 2 * I : H;    // weight rows of the matrix
+  const int K = (PH == PH_UP) ? H : I;
+  const int r0 = rt * MR;
+  if (r0 >= out_dim) return;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, l16 = lane & 15;
+  const int nch = (K + 127) / 128, nsb = K / 32;
+  const uint8_t *wblk = blob + grp.off[PH == PH_UP ? 0 : 3];
+  const uint8_t *wsc = blob + grp.off[PH == PH_UP ? 1 : 4];
+  const int ld = PH == PH_UP ? a.xld : a.hld;
+  const uint8_t *qbase = PH == PH_UP ? a.xq : a.hq;
+  const uint8_t *sbase = PH == PH_UP ? a.xs : a.hs;
+
+  // Weight scales of the valid rows (16-row granular), whole K, and the rows' biases.
+  const int vrows = min(MR, out_dim - r0);
+  for (int v = tid; v < vrows * nsb / 16; v += 512)
+    *(u32x4 *)(sAS + 16 * v) = *(const u32x4 *)(wsc + (size_t)r0 * nsb + 16 * v);
+  if (tid < MR) {
+    const uint16_t *bias = (const uint16_t *)(blob + grp.off[PH == PH_UP ? 2 : 5]);
+    sBias[tid] = a.expert_bias ? bf16_bits_to_f32(bias[min(r0 + tid, out_dim - 1)]) : 0.f;
+  }
+
+  for (int t0 = 0; t0 < nitem; t0 += NTOK) {
+    const int ntok = min(NTOK, nitem - t0);
+    auto slot_of = [&](int n) { return a.order[pos0 + t0 + min(n, ntok - 1)]; };
+    if (wave >= 4) {
+      // ---- loaders ----
+      const int lt = tid - 256;
+      const uint8_t *asrc[APL];
+      int ag[APL];
+      const uint8_t *bsrc[BPL];
+      const uint8_t *ssrc;
+#pragma unroll
+      for (int k = 0; k < APL; ++k) {
+        // Vector v = (tile j, lane i): row 16j + i%16, block g = i/16 of the chunk.
+        const int v = lt + 256 * k, j = v >> 6, i = v & 63;
+        const int r = min(r0 + 16 * j + (i & 15), out_dim - 1);
+        asrc[k] = wblk + (size_t)r * (K / 2);
+        ag[k] = i >> 4;
+      }
+#pragma unroll
+      for (int k = 0; k < BPL; ++k) {
+        const int v = min(lt + 256 * k, BV - 1);
+        const int tt = v / (NTOK * 8), sl = v % (NTOK * 8), n = sl >> 3, sg = (sl & 7) ^ (n & 7);
+        const int row = PH == PH_UP ? slot_of(n) / a.slots : slot_of(n);
+        bsrc[k] = qbase + ((size_t)row * NTERM + tt) * ld + 16 * sg;
+      }
+      {
+        const int v = min(lt, BS - 1), tt = v / NTOK, n = v % NTOK;
+        const int row = PH == PH_UP ? slot_of(n) / a.slots : slot_of(n);
+        ssrc = sbase + ((size_t)row * NTERM + tt) * (ld / 32);
+      }
+      u32x4 ra[R][APL], rb[R][BPL];
+      uint32_t rs[R];
+      auto issue = [&](int u, int c) {
+        const int cc = min(c, nch - 1);
+#pragma unroll
+        for (int k = 0; k < APL; ++k) ra[u][k] = *(const u32x4 *)(asrc[k] + 16 * min(4 * cc + ag[k], nsb - 1));
+#pragma unroll
+        for (int k = 0; k < BPL; ++k) rb[u][k] = *(const u32x4 *)(bsrc[k] + 128 * cc);
+        rs[u] = *(const uint32_t *)(ssrc + 4 * cc);
+      };
+      auto put = [&](int u, int buf) {
+#pragma unroll
+        for (int k = 0; k < APL; ++k) sA[buf][lt + 256 * k] = ra[u][k];
+#pragma unroll
+        for (int k = 0; k < BPL; ++k)
+          if (lt + 256 * k < BV) sB[buf][lt + 256 * k] = rb[u][k];
+        if (lt < BS) sBs[buf][lt] = rs[u];
+      };
+#pragma unroll
+      for (int u = 0; u < R; ++u) issue(u, u);
+      for (int c0 = 0; c0 < nch; c0 += R) {
+#pragma unroll
+        for (int u = 0; u < R; ++u) {
+          const int c = c0 + u;
+          if (c < nch) {
+            put(u, c & 1);
+            __syncthreads();
+            issue(u, c + R);
+          }
+        }
+      }
+    } else {
+      // ---- MFMA waves ----
+      const int wr = wave & 1, wt = wave >> 1;
+      const int rw = r0 + 64 * wr;              // first weight row of this wave
+      // Epilogue operands fetched now, off the critical path: slot ids and routing weights.
+      int eslot[NTW];
+      float ew[NTW];
+#pragma unroll
+      for (int st = 0; st < NTW; ++st) {
+        eslot[st] = slot_of(16 * NTW * wt + 16 * st + l16);
+        ew[st] = PH == PH_DOWN ? a.slot_w[eslot[st]] : 0.f;
+      }
+      f32x4 acc[4][NTW];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int st = 0; st < NTW; ++st) acc[j][st] = f32x4{0.f, 0.f, 0.f, 0.f};
+      auto compute = [&](int c) {
+        const int buf = c & 1;
+        const bool ok = 128 * c + 32 * g < K;
+        u32x4 w[4];
+        uint32_t sa[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          w[j] = ok ? sA[buf][(4 * wr + j) * 64 + lane] : u32x4{0u, 0u, 0u, 0u};
+          sa[j] = sAS[(64 * wr + 16 * j + l16) * nsb + min(4 * c + g, nsb - 1)];
+        }
+#pragma unroll
+        for (int t = 0; t < NTERM; ++t)
+#pragma unroll
+          for (int st = 0; st < NTW; ++st) {
+            const int n = 16 * NTW * wt + 16 * st + l16;
+            const int k0 = 128 * c + 16 * g;
+            u32x4 blo = sB[buf][(t * NTOK + n) * 8 + (g ^ (n & 7))];
+            u32x4 bhi = sB[buf][(t * NTOK + n) * 8 + ((4 + g) ^ (n & 7))];
+            uint32_t bs = (sBs[buf][t * NTOK + n] >> (8 * g)) & 0xFFu;
+            if (k0 >= K) blo = u32x4{0u, 0u, 0u, 0u};
+            if (k0 + 64 >= K) bhi = u32x4{0u, 0u, 0u, 0u};
+            if (!ok) bs = 127u;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j][st] = smfma(w[j], blo, bhi, sa[j], bs, acc[j][st]);
+          }
+      };
+      for (int c = 0; c < nch; ++c) {
+        __syncthreads();
+        compute(c);
+      }
+      // ---- epilogue ----
+      if (rw < out_dim) {
+#pragma unroll
+        for (int st = 0; st < NTW; ++st) {
+          const int n = 16 * NTW * wt + 16 * st + l16;
+          const int slot = eslot[st];
+          if constexpr (PH == PH_UP) {
+            // Tile j, lane group g: rows rw + 16j + 4g + {0..3} = (gate, up) of intermediates
+            // rw/2 + 8j + 2g + {0, 1}.
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const f32x4 d = acc[j][st];
+              const float *bb = sBias + 64 * wr + 16 * j + 4 * g;
+              v[2 * j] = activate(a.act, d[0] + bb[0], d[1] + bb[1], a.alpha, a.limit);
+              v[2 * j + 1] = activate(a.act, d[2] + bb[2], d[3] + bb[3], a.alpha, a.limit);
+            }
+            uint32_t hq[NTH][2], sb[NTH];
+            quant_block<NTH>(v, hq, sb);
+            if (n < ntok) {
+              const int i0 = rw / 2;
+#pragma unroll
+              for (int t = 0; t < NTH; ++t) {
+                uint8_t *row = a.hq + ((size_t)slot * NTH + t) * a.hld + i0 + 2 * g;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                  *(uint16_t *)(row + 8 * j) = (uint16_t)(hq[t][j >> 1] >> (16 * (j & 1)));
+                if (g == 0) a.hs[((size_t)slot * NTH + t) * (a.hld / 32) + i0 / 32] = (uint8_t)sb[t];
+              }
+            }
+          } else {
+            if (n < ntok) {
+              const float wgt = ew[st];
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const int h0 = rw + 16 * j + 4 * g;
+                const f32x4 r = acc[j][st];
+                const float *bb = sBias + 64 * wr + 16 * j + 4 * g;
+                f32x4 o;
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) o[ii] = wgt * (r[ii] + bb[ii]);   // down_value's arithmetic
+                *(f32x4 *)(a.slot_out + (size_t)slot * H + h0) = o;
+              }
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();   // the next pass restages the buffers
+  }
+}
+
 // y[t][j] = Σ_r slot[t·slots + r][j] in rank order (sum_expert_slices, dense.metal:147; the
 // shared expert's slot comes last as in QwenReferenceLayer.swift:399-404).
 __global__ __launch_bounds__(256) void combine_kernel(const float *slot_out, int slots, int H,
@@ -1271,16 +1562,23 @@ typedef void (*DownSmallKernel)(GemmArgs, const int32_t *);
 template <int FMT> constexpr int decode_depth() { return FMT == Q_BF16 ? 4 : (FMT == Q_MXFP4 ? 24 : 8); }
 
 template <int FMT> static UpSmallKernel up_small_k() {
-  if constexpr (FMT == Q_MXFP4) return up_small_mx<decode_depth<FMT>()>;
+  if constexpr (FMT == Q_MXFP4) return up_small_mx<16>;
   else return up_small<FMT, decode_depth<FMT>()>;
 }
+// Waves per slot of down_small: MXFP4's canonical arithmetic is one chain over K (one wave per
+// slot); the others split K by chunk parity over two waves when the workgroup has room.
+template <int FMT> constexpr int down_ks(int slots) { return (FMT == Q_MXFP4 || slots > 4) ? 1 : 2; }
+
 template <int FMT> static DownSmallKernel down_small_k(int slots) {
-  return slots <= 4 ? down_small<FMT, decode_depth<FMT>(), 4, 2> : down_small<FMT, decode_depth<FMT>(), kMaxTopK + 1, 1>;
+  // Nine waves leave a third of the register file per wave: a shallower ring.
+  constexpr int D9 = decode_depth<FMT>() > 8 ? 8 : decode_depth<FMT>();
+  if (slots > 4) return down_small<FMT, D9, kMaxTopK + 1, 1>;
+  return down_small<FMT, decode_depth<FMT>(), 4, down_ks<FMT>(4)>;
 }
 
 template <int PH, int FMT>
 static GemmKernel pick(int nt) {
-  if constexpr (FMT == Q_MXFP4) return nt <= 1 ? prefill_mx<PH, 2, 1, 2> : prefill_mx<PH, 2, 2, 2>;
+  if constexpr (FMT == Q_MXFP4) return nt <= 2 ? prefill_mx2<PH, 1> : prefill_mx2<PH, 2>;
   // Prefill: 4 waves × RT 16-row tiles × 16·NT tokens (BF16 keeps one tile per wave: its
   // weight operand is 4× wider per chunk).
   constexpr int RT_P = (FMT == Q_BF16) ? 1 : 2;
@@ -1288,7 +1586,12 @@ static GemmKernel pick(int nt) {
   return prefill_gemm<PH, FMT, RT_P, 2, 2>;
 }
 
-int gemm_rows_per_block(int quant) { return 4 * 16 * (quant == Q_BF16 ? 1 : 2); }
+// Output rows per prefill workgroup: intermediates (gate-up) or hidden rows (down). The MXFP4
+// kernel covers 128 weight rows: 64 intermediates of the interleaved gate_up matrix.
+int gemm_rows_per_block(int quant, int phase) {
+  if (quant == Q_MXFP4) return phase == PH_UP ? 64 : 128;
+  return 4 * 16 * (quant == Q_BF16 ? 1 : 2);
+}
 
 static GemmKernel gemm_kernel(int phase, int quant, int nt) {
   switch (quant) {
@@ -1302,7 +1605,10 @@ static GemmKernel gemm_kernel(int phase, int quant, int nt) {
 hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStream_t s, Timing tm) {
   const unsigned blocks = (unsigned)a.row_tiles * (unsigned)a.max_work;
   if (blocks == 0) return hipSuccess;
-  hipExtLaunchKernelGGL(gemm_kernel(phase, quant, nt), dim3(blocks), dim3(256), 0, s, tm.start,
+  const bool mx = quant == Q_MXFP4;
+  // MXFP4: 8 waves, the weight rows' scales (128 rows × K/32 bytes) in dynamic LDS.
+  const size_t lds = mx ? (size_t)128 * ((phase == PH_UP ? a.hidden : a.ldh) / 32) : 0;
+  hipExtLaunchKernelGGL(gemm_kernel(phase, quant, nt), dim3(blocks), dim3(mx ? 512 : 256), lds, s, tm.start,
                         tm.stop, 0, a);
   return hipGetLastError();
 }
@@ -1339,12 +1645,19 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
       (void)hipGetLastError();
     }
   });
+  static int ncu = 0;
+  if (!ncu) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0) ncu = 256;
+  }
   a.row_tiles = a.ldh / UP_ROWS;
   const bool mx = quant == Q_MXFP4;
   const size_t lds_up = mx ? (size_t)T * NTX * mx_row_bytes(a.xld) + 64 * (a.hidden / 32)
                            : (size_t)T * (a.hidden + LDS_PAD) * 2;
-  hipExtLaunchKernelGGL(up, dim3(a.row_tiles * maxu), dim3(mx ? 256 : 512), lds_up, s, tm_up.start, tm_up.stop, 0,
-                        a, ra);
+  // MXFP4: persistent, about two workgroups per compute unit.
+  const int up_grid = mx ? std::min(2 * ncu, a.row_tiles * maxu) : a.row_tiles * maxu;
+  hipExtLaunchKernelGGL(up, dim3(up_grid), dim3(mx ? 256 : 512), lds_up, s, tm_up.start, tm_up.stop, 0, a, ra);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   a.row_tiles = a.hidden / 16;
@@ -1352,7 +1665,10 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
   const int imax = std::max(a.grp[0].inter, a.grp[1].inter);
   const size_t lds_down = mx ? (size_t)S * (NTH * mx_row_bytes(a.hld) + 16 * ((16 * (imax / 32) + 15) / 16))
                              : (size_t)S * 2 * (a.ldh + LDS_PAD) * 2;
-  hipExtLaunchKernelGGL(down, dim3(a.row_tiles * T), dim3(64 * S * (S <= 4 ? 2 : 1)), lds_down, s, tm_down.start,
+  a.max_work = T;
+  const int down_grid = std::min(a.row_tiles * T, 2 * ncu);
+  const int ks = (mx || S > 4) ? 1 : 2;
+  hipExtLaunchKernelGGL(down, dim3(down_grid), dim3(64 * S * ks), lds_down, s, tm_down.start,
                         tm_down.stop, 0, a, (const int32_t *)ra.topk_idx);
   return hipGetLastError();
 }
