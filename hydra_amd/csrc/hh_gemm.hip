@@ -102,12 +102,26 @@ template <> struct Fmt<Q_MXFP4> {
 
 // ---- MXFP4 blocks without their scales (decode kernels stage a tile's scales in LDS) ----------
 constexpr int Q_MXFP4_W = 4;
+// Rows are read through a buffer resource over the whole weight matrix of the expert: the lane's
+// row offset is computed once and a chunk's offset (64 bytes per chunk) goes into the
+// instruction's immediate field, so a stream of chunks costs no address registers. Chunks are
+// not clamped: a lane past K reads the next row (its weights are zeroed by lane_valid) and reads
+// past the matrix return zeros. Streams of this format walk K with stride 1.
 template <> struct Fmt<Q_MXFP4_W> {
   static constexpr int CHUNK = 128, NB = 4;
   struct A { u32x4 w; };
-  struct Row { const uint8_t *w; };
-  __device__ static void load(A &a, const Row &rw, int c, int g, int K) {
-    a.w = *(const u32x4 *)(rw.w + min(4 * c + g, K / 32 - 1) * 16);
+  struct Row {
+    __amdgpu_buffer_rsrc_t rs;
+    int voff;   // row · K/2 + 16·(lane group): the lane's block of chunk 0
+  };
+  __device__ static Row row(const uint8_t *matrix, uint64_t bytes, int r, int K) {
+    Row rw;
+    rw.rs = __builtin_amdgcn_make_buffer_rsrc((void *)matrix, (short)0, (int)bytes, 0x00020000);
+    rw.voff = r * (K / 2) + 16 * ((threadIdx.x & 63) >> 4);
+    return rw;
+  }
+  __device__ static void load(A &a, const Row &rw, int c, int, int) {
+    a.w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw.rs, rw.voff + 64 * c, 0, 0));
   }
   __device__ static bool lane_valid(int c, int g, int K) { return 128 * c + 32 * g < K; }
 };
@@ -203,7 +217,9 @@ __device__ __forceinline__ ATile<FMT> tile_of(const uint8_t *blob, const ExpertG
     if (PH == PH_UP) t.row = Fmt<FMT>::row(blob + grp.off[0], blob + grp.off[1], 2 * orow + (is_up ? 1 : 0), K);
     else t.row = Fmt<FMT>::row(blob + grp.off[3], blob + grp.off[4], orow, K);
   } else if constexpr (FMT == Q_MXFP4_W) {
-    t.row.w = blob + grp.off[PH == PH_UP ? 0 : 3] + (size_t)(PH == PH_UP ? 2 * orow + (is_up ? 1 : 0) : orow) * (K / 2);
+    // The matrix extends to the next sub-tensor of the blob (its scales).
+    if (PH == PH_UP) t.row = Fmt<FMT>::row(blob + grp.off[0], grp.off[1] - grp.off[0], 2 * orow + (is_up ? 1 : 0), K);
+    else t.row = Fmt<FMT>::row(blob + grp.off[3], grp.off[4] - grp.off[3], orow, K);
   } else if constexpr (FMT == Q_BF16) {
     // Gemma gate_up: gate = rows 0..I-1, up = rows I..2I-1 (Gemma4Weights.swift:107-112).
     if (PH == PH_UP) t.row = Fmt<FMT>::row(blob + grp.off[0], orow + (is_up ? I : 0), K);
@@ -314,13 +330,16 @@ __device__ __forceinline__ void chunk_mfma(f32x4 (&acc)[NM][NT], const typename 
 // times. Refills are issued only when another round follows (a round's refills past the last
 // chunk reload it, clamped, so the rounds before the last need no per-load test): a duplicate
 // load costs as much of the address/L1 path as a real one.
+template <int FMT> constexpr bool unit_stride() { return FMT == Q_MXFP4_W; }
 template <int FMT, int NM, int DA> struct AStream {
   typename Fmt<FMT>::A s[DA][NM];
   int c0, cs, n;   // first chunk, chunk stride, chunks of this wave
   __device__ __forceinline__ AStream(int first, int stride, int nch)
       : c0(first), cs(stride), n(nch > first ? (nch - first + stride - 1) / stride : 0) {}
   __device__ __forceinline__ void load(int slot, const ATile<FMT> (&at)[NM], int i, int nch, int g, int K) {
-    const int c = min(c0 + cs * min(i, max(n - 1, 0)), nch - 1);
+    int c;
+    if constexpr (unit_stride<FMT>()) c = c0 + i;
+    else c = min(c0 + cs * min(i, max(n - 1, 0)), nch - 1);
 #pragma unroll
     for (int m = 0; m < NM; ++m) Fmt<FMT>::load(s[slot][m], at[m].row, c, g, K);
   }
@@ -338,6 +357,44 @@ template <int FMT, int NM, int DA> struct AStream {
         if (i0 + u < n) body(s[u], c0 + cs * (i0 + u));
         if (more) load(u, at, i0 + u + DA, nch, g, K);
       }
+    }
+  }
+  // As run, with the chunk's other operands read one chunk ahead: `pre(c)` issues them (LDS
+  // reads) and `body(stage, c, ops)` consumes them, so each chunk's operand latency hides behind
+  // the previous chunk's MFMAs. A wave whose chunks fit the ring (n ≤ DA) runs straight-line code
+  // without refills, which keeps every weight wait exact (a refill inside the loop forces
+  // conservative waits).
+  // ONE: the caller guarantees one round from chunk 0 with stride 1 (n ≤ DA, c0 = 0, cs = 1), and
+  // only that code is generated.
+  template <bool ONE = false, class Pre, class Body>
+  __device__ __forceinline__ void run_pf(const ATile<FMT> (&at)[NM], int nch, int g, int K, Pre pre, Body body) {
+    if (n <= 0) return;
+    if constexpr (ONE) {
+      rounds<true, true>(at, nch, g, K, pre, body);
+    } else {
+      if (n <= DA && c0 == 0 && cs == 1) rounds<true, true>(at, nch, g, K, pre, body);
+      else if (n <= DA) rounds<true, false>(at, nch, g, K, pre, body);
+      else rounds<false, false>(at, nch, g, K, pre, body);
+    }
+  }
+  // UNIT: chunk u of the ring is chunk u of K (one round, first chunk 0, stride 1), so chunk
+  // indices, and the operand offsets derived from them, are compile-time constants.
+  template <bool ONE, bool UNIT, class Pre, class Body>
+  __device__ __forceinline__ void rounds(const ATile<FMT> (&at)[NM], int nch, int g, int K, Pre pre, Body body) {
+    auto op = pre(UNIT ? 0 : c0);
+    for (int i0 = 0; i0 < n; i0 += DA) {
+      const bool more = !ONE && i0 + DA < n;
+#pragma unroll
+      for (int u = 0; u < DA; ++u) {
+        if (i0 + u < n) {
+          const int cn = UNIT ? min(u + 1, DA - 1) : c0 + cs * min(i0 + u + 1, n - 1);
+          const auto nx = pre(cn);
+          body(s[u], UNIT ? u : c0 + cs * (i0 + u), op);
+          op = nx;
+        }
+        if (more) load(u, at, i0 + u + DA, nch, g, K);
+      }
+      if (ONE) break;
     }
   }
 };
@@ -648,6 +705,36 @@ __device__ __forceinline__ void chunk_mx(f32x4 (&acc)[NM][NT], const u32x4 (&w)[
     }
 }
 
+// The operands of one chunk that come from LDS, read unmasked: the B operand of every term and
+// the e8m0 scale of the wave's weight block.
+template <int NTERM> struct MxOps {
+  MxB b[NTERM];
+  uint32_t sa;
+};
+template <int NTERM>
+__device__ __forceinline__ MxOps<NTERM> mx_ops(const uint8_t *brow, int RS, int ld, const uint8_t *my_sc, int nsb,
+                                               int c, int g) {
+  MxOps<NTERM> o;
+  const int k0 = 128 * c + 16 * g;
+#pragma unroll
+  for (int t = 0; t < NTERM; ++t) {
+    o.b[t].lo = *(const u32x4 *)(brow + t * RS + k0);
+    o.b[t].hi = *(const u32x4 *)(brow + t * RS + k0 + 64);
+    o.b[t].s = brow[t * RS + ld + 4 * c + g];
+  }
+  o.sa = my_sc[min(4 * c + g, nsb - 1)];
+  return o;
+}
+// chunk_mx for one tile and one token tile with pre-read operands, which come from rows staged by
+// MxStage (zero past K, scales 2^0 there): the same values mx_b's masks give. Lanes whose weight
+// block lies past K take zero weights, as in chunk_mx.
+template <int NTERM>
+__device__ __forceinline__ void chunk_mx1(f32x4 &acc, const u32x4 &w, const MxOps<NTERM> &o, int c, int g, int K) {
+  const u32x4 wv = Fmt<Q_MXFP4>::lane_valid(c, g, K) ? w : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int t = 0; t < NTERM; ++t) acc = smfma(wv, o.b[t].lo, o.b[t].hi, o.sa & 0xFFu, o.b[t].s, acc);
+}
+
 // Stages the e8m0 scales of `rows` consecutive weight rows (rows · K/32 bytes, 16-byte aligned)
 // into LDS: one 16-byte vector per thread and step.
 __device__ __forceinline__ int scale_vectors(int rows, int K) { return rows * (K / 32) / 16; }
@@ -669,20 +756,22 @@ __device__ __forceinline__ void store_hq(const GemmArgs &a, int slot, int blk, i
 __host__ __device__ __forceinline__ int mx_row_bytes(int ld) { return ld + ld / 32 + 16; }
 
 // Copies the NTERM term rows (and scales) of `nrows` operand rows into LDS rows of
-// mx_row_bytes(ld): LDS row rr = (j, t) ← q + (row_of(j)·NTERM + t)·ld and s + (…)·ld/32, in
-// 16-byte vectors v = id + threads·k. The first NB vectors of each thread can be loaded before
+// mx_row_bytes(ld): LDS row rr = (j, t) ← q + (row_of(j)·NTERM + t)·ld and s + (…)·ld/32, the
+// first `cols` columns only (cols a multiple of 16; the MFMA operand reads mask columns past K),
+// in 16-byte vectors v = id + threads·k. The first NB vectors of each thread can be loaded before
 // other loads are issued (load_first) and stored after them (store_first): completion counts
 // are in order, so stores issued after a weight stream would otherwise wait for all of it.
 template <int NTERM, int NB, class RowOf> struct MxStage {
   uint8_t *dst;
   const uint8_t *q, *sc;
-  int ld, n, dv, per_row, RS, id, threads;
+  int ld, cols, nrows, n, dv, per_row, RS, id, threads;
   RowOf row_of;
   u32x4 r[NB];
-  __device__ __forceinline__ MxStage(uint8_t *dst_, const uint8_t *q_, const uint8_t *sc_, int ld_, int nrows,
-                                     RowOf row_of_, int id_, int threads_)
-      : dst(dst_), q(q_), sc(sc_), ld(ld_), dv(ld_ / 16), per_row(ld_ / 16 + ld_ / 512),
-        RS(mx_row_bytes(ld_)), id(id_), threads(threads_), row_of(row_of_) {
+  __device__ __forceinline__ MxStage(uint8_t *dst_, const uint8_t *q_, const uint8_t *sc_, int ld_, int cols_,
+                                     int nrows_, RowOf row_of_, int id_, int threads_)
+      : dst(dst_), q(q_), sc(sc_), ld(ld_), cols(cols_), nrows(nrows_), dv(cols_ / 16),
+        per_row(cols_ / 16 + (cols_ / 32 + 15) / 16), RS(mx_row_bytes(ld_)), id(id_), threads(threads_),
+        row_of(row_of_) {
     n = nrows * NTERM * per_row;
   }
   __device__ __forceinline__ u32x4 src(int v) const {
@@ -690,9 +779,28 @@ template <int NTERM, int NB, class RowOf> struct MxStage {
     const size_t grow = (size_t)row_of(rr / NTERM) * NTERM + rr % NTERM;
     return qq < dv ? *(const u32x4 *)(q + grow * ld + 16 * qq) : *(const u32x4 *)(sc + grow * (ld / 32) + 16 * (qq - dv));
   }
-  __device__ __forceinline__ void put(int v, const u32x4 &val) const {
+  // Scale bytes of blocks at or past `cols` (the tail of the last scale vector) are stored as 127
+  // (2^0), so the MFMA operands of the last chunk need no masks.
+  __device__ __forceinline__ void put(int v, u32x4 val) const {
     const int rr = v / per_row, qq = v - rr * per_row;
-    *(u32x4 *)(dst + (size_t)rr * RS + 16 * qq) = val;
+    if (qq >= dv) {
+      const int nvalid = cols / 32 - 16 * (qq - dv);
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          if (4 * d + b >= nvalid) val[d] = (val[d] & ~(0xFFu << (8 * b))) | (0x7Fu << (8 * b));
+    }
+    *(u32x4 *)(dst + (size_t)rr * RS + (qq < dv ? 16 * qq : ld + 16 * (qq - dv))) = val;
+  }
+  // Zeros columns cols .. (cols rounded up to 128) of every staged row: the last chunk's operand
+  // past K. Disjoint from the bytes put() writes.
+  __device__ __forceinline__ void pad() const {
+    const int nz = (((cols + 127) & ~127) - cols) / 16;
+    for (int v = id; v < nrows * NTERM * nz; v += threads) {
+      const int rr = v / nz;
+      *(u32x4 *)(dst + (size_t)rr * RS + cols + 16 * (v - rr * nz)) = u32x4{0u, 0u, 0u, 0u};
+    }
   }
   // Unconditional (clamped) loads keep the completion counts exact.
   __device__ __forceinline__ void load_first() {
@@ -711,8 +819,9 @@ template <int NTERM, int NB, class RowOf> struct MxStage {
 };
 template <int NTERM, int NB, class RowOf>
 __device__ __forceinline__ MxStage<NTERM, NB, RowOf> mx_stage(uint8_t *dst, const uint8_t *q, const uint8_t *sc,
-                                                               int ld, int nrows, RowOf row_of, int id, int threads) {
-  return MxStage<NTERM, NB, RowOf>(dst, q, sc, ld, nrows, row_of, id, threads);
+                                                               int ld, int cols, int nrows, RowOf row_of, int id,
+                                                               int threads) {
+  return MxStage<NTERM, NB, RowOf>(dst, q, sc, ld, cols, nrows, row_of, id, threads);
 }
 
 // Decode gate-up on the scaled MFMA, persistent: the grid holds about two workgroups per compute
@@ -724,7 +833,7 @@ __device__ __forceinline__ MxStage<NTERM, NB, RowOf> mx_stage(uint8_t *dst, cons
 // through LDS. The gate waves combine gate and up and write the block's activations to LDS; wave
 // 0 writes them as NTH fp8 terms. Each item issues its whole weight stream at once; co-resident
 // workgroups hide one another's latency.
-template <int DA>
+template <int DA, bool ONE>
 __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) {
   constexpr int NM = 1;
   constexpr int NE = SMALL_T * kMaxTopK + 1;
@@ -753,7 +862,7 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
   }
   // x terms of every token: first batch of loads now, stored with the first item.
   const int RS = mx_row_bytes(a.xld);
-  auto xs = mx_stage<NTX, 2>(s_xb, a.xq, a.xs, a.xld, T, [](int j) { return j; }, tid, 256);
+  auto xs = mx_stage<NTX, 2>(s_xb, a.xq, a.xs, a.xld, a.hidden, T, [](int j) { return j; }, tid, 256);
   xs.load_first();
   __syncthreads();
   if (wave == 0) {
@@ -824,6 +933,7 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
     if (x_pending) {
       xs.store_first();
       xs.rest();
+      xs.pad();
       x_pending = false;
     }
 #pragma unroll
@@ -833,15 +943,19 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
     __syncthreads();
 
     const uint8_t *my_sc = s_sc + (2 * (16 * q + l16) + (is_up ? 1 : 0)) * nsb;
+    // The lane group as a value opaque to the compiler in each item: otherwise every chunk's
+    // item-invariant operand addresses and masks are hoisted out of the item loop and held
+    // (spilled) across it.
+    int gi = g;
+    asm volatile("" : "+v"(gi));
     const int my_t = nth_bit(tm, min(l16, ntok - 1));   // token of column l16 (padding repeats)
     const uint8_t *brow = s_xb + (size_t)my_t * NTX * RS;
     f32x4 acc[NM][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
-    as.run(at, nch, g, H, [&](const Fmt<Q_MXFP4_W>::A (&w)[NM], int c) {
-      auto bf = [&](int, int t) { return mx_b(brow + t * RS, brow + t * RS + a.xld, c, g, H); };
-      const u32x4 wv[NM] = {w[0].w};
-      const uint32_t sv[NM] = {my_sc[min(4 * c + g, nsb - 1)]};
-      chunk_mx<NM, 1, NTX>(acc, wv, sv, bf, c, g, H);
-    });
+    as.template run_pf<ONE>(
+        at, nch, gi, H, [&](int c) { return mx_ops<NTX>(brow, RS, a.xld, my_sc, nsb, c, gi); },
+        [&](const Fmt<Q_MXFP4_W>::A (&w)[NM], int c, const MxOps<NTX> &o) {
+          chunk_mx1<NTX>(acc[0][0], w[0].w, o, c, gi, H);
+        });
     const f32x4 res = acc[0][0];
     if (is_up) s_up[q][lane] = res;
     __syncthreads();
@@ -919,10 +1033,11 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
     u32x4 scv[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) scv[k] = *(const u32x4 *)(gsc + 16 * min(sid + sth * k, nsv - 1));
-    auto hs = mx_stage<NTH, 5>(my_lds, a.hq, a.hs, a.hld, 1, [&](int) { return slot; }, sid, sth);
+    auto hs = mx_stage<NTH, 9>(my_lds, a.hq, a.hs, a.hld, I, 1, [&](int) { return slot; }, sid, sth);
     hs.load_first();
     ATile<Q_MXFP4_W> aw[NM] = {tile_of<PH_DOWN, Q_MXFP4_W>(blob, grp, rb, false, I, l16)};
-    AStream<Q_MXFP4_W, NM, DA> as(KS > 1 ? par : 0, KS, nch);
+    static_assert(KS == 1, "MXFP4 accumulates one chain over K");
+    AStream<Q_MXFP4_W, NM, DA> as(0, 1, nch);
     as.fill(aw, nch, g, I);
 #pragma unroll
     for (int k = 0; k < 2; ++k)
@@ -930,15 +1045,16 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
     for (int v = sid + 2 * sth; v < nsv; v += sth) *(u32x4 *)(s_sc + 16 * v) = *(const u32x4 *)(gsc + 16 * v);
     hs.store_first();
     hs.rest();
+    hs.pad();
     __syncthreads();
     const uint8_t *brow = my_lds;
     const uint8_t *my_sc = s_sc + l16 * nsb;
-    as.run(aw, nch, g, I, [&](const Fmt<Q_MXFP4_W>::A (&w)[NM], int c) {
-      auto bf = [&](int, int t) { return mx_b(brow + t * RS, brow + t * RS + a.hld, c, g, I); };
-      const u32x4 wv[NM] = {w[0].w};
-      const uint32_t sv[NM] = {my_sc[min(4 * c + g, nsb - 1)]};
-      chunk_mx<NM, 1, NTH>(acc[0], wv, sv, bf, c, g, I);   // MXFP4: one chain
-    });
+    // MXFP4: one chain. DA ≥ MX_ONE instantiations run only for rows of at most DA chunks.
+    as.template run_pf<(DA >= 24)>(
+        aw, nch, g, I, [&](int c) { return mx_ops<NTH>(brow, RS, a.hld, my_sc, nsb, c, g); },
+        [&](const Fmt<Q_MXFP4_W>::A (&w)[NM], int c, const MxOps<NTH> &o) {
+          chunk_mx1<NTH>(acc[0][0][0], w[0].w, o, c, g, I);
+        });
   } else {
   // This slot's activation (hi, lo) into LDS (the slot's two waves share it): the loads go out
   // before the weight stream (see stage_batch), the stores after it.
@@ -1561,18 +1677,22 @@ typedef void (*DownSmallKernel)(GemmArgs, const int32_t *);
 // a scale, MLX4 8 B, MLX8 16 B (+ a scale|bias pair), BF16 64 B).
 template <int FMT> constexpr int decode_depth() { return FMT == Q_BF16 ? 4 : (FMT == Q_MXFP4 ? 24 : 8); }
 
-template <int FMT> static UpSmallKernel up_small_k() {
-  if constexpr (FMT == Q_MXFP4) return up_small_mx<16>;
+// MXFP4 streams of at most MX_ONE chunks (K ≤ 3072) run the single-round kernels (the whole row
+// in flight, no ring refills); longer rows take the ring variants.
+constexpr int MX_ONE = 24;
+template <int FMT> static UpSmallKernel up_small_k(bool one) {
+  if constexpr (FMT == Q_MXFP4) return one ? up_small_mx<MX_ONE, true> : up_small_mx<16, false>;
   else return up_small<FMT, decode_depth<FMT>()>;
 }
 // Waves per slot of down_small: MXFP4's canonical arithmetic is one chain over K (one wave per
 // slot); the others split K by chunk parity over two waves when the workgroup has room.
 template <int FMT> constexpr int down_ks(int slots) { return (FMT == Q_MXFP4 || slots > 4) ? 1 : 2; }
 
-template <int FMT> static DownSmallKernel down_small_k(int slots) {
-  // Nine waves leave a third of the register file per wave: a shallower ring.
+template <int FMT> static DownSmallKernel down_small_k(int slots, bool one) {
+  // Nine waves leave a third of the register file per wave: a shallower ring (also the MXFP4
+  // kernel for rows longer than MX_ONE chunks).
   constexpr int D9 = decode_depth<FMT>() > 8 ? 8 : decode_depth<FMT>();
-  if (slots > 4) return down_small<FMT, D9, kMaxTopK + 1, 1>;
+  if (slots > 4 || !one) return down_small<FMT, D9, kMaxTopK + 1, 1>;
   return down_small<FMT, decode_depth<FMT>(), 4, down_ks<FMT>(4)>;
 }
 
@@ -1620,24 +1740,28 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
   if (T < 1 || T > SMALL_T) return hipErrorInvalidValue;
   const int S = a.slots;
   const int maxu = std::min(a.experts, T * a.top_k) + (S > a.top_k ? 1 : 0);
+  const int imax = std::max(a.grp[0].inter, a.grp[1].inter);
+  const bool mx = quant == Q_MXFP4;
+  const bool one_up = !mx || (a.hidden + 127) / 128 <= MX_ONE, one_down = !mx || (imax + 127) / 128 <= MX_ONE;
   UpSmallKernel up;
   DownSmallKernel down;
   switch (quant) {
-  case Q_MXFP4: up = up_small_k<Q_MXFP4>(); down = down_small_k<Q_MXFP4>(S); break;
-  case Q_BF16: up = up_small_k<Q_BF16>(); down = down_small_k<Q_BF16>(S); break;
-  case Q_MLX4: up = up_small_k<Q_MLX4>(); down = down_small_k<Q_MLX4>(S); break;
-  default: up = up_small_k<Q_MLX8>(); down = down_small_k<Q_MLX8>(S); break;
+  case Q_MXFP4: up = up_small_k<Q_MXFP4>(one_up); down = down_small_k<Q_MXFP4>(S, one_down); break;
+  case Q_BF16: up = up_small_k<Q_BF16>(true); down = down_small_k<Q_BF16>(S, true); break;
+  case Q_MLX4: up = up_small_k<Q_MLX4>(true); down = down_small_k<Q_MLX4>(S, true); break;
+  default: up = up_small_k<Q_MLX8>(true); down = down_small_k<Q_MLX8>(S, true); break;
   }
   // The decode kernels stage rows in dynamic LDS beyond the default 64 KiB window (gfx950 has
   // 160 KiB per compute unit).
   static std::once_flag lds_once;
   std::call_once(lds_once, [] {
-    const void *ks[] = {(const void *)up_small_k<Q_MXFP4>(), (const void *)up_small_k<Q_BF16>(),
-                        (const void *)up_small_k<Q_MLX4>(), (const void *)up_small_k<Q_MLX8>(),
-                        (const void *)down_small_k<Q_MXFP4>(4), (const void *)down_small_k<Q_BF16>(4),
-                        (const void *)down_small_k<Q_MLX4>(4), (const void *)down_small_k<Q_MLX8>(4),
-                        (const void *)down_small_k<Q_MXFP4>(9), (const void *)down_small_k<Q_BF16>(9),
-                        (const void *)down_small_k<Q_MLX4>(9), (const void *)down_small_k<Q_MLX8>(9)};
+    const void *ks[] = {(const void *)up_small_k<Q_MXFP4>(true), (const void *)up_small_k<Q_MXFP4>(false),
+                        (const void *)up_small_k<Q_BF16>(true), (const void *)up_small_k<Q_MLX4>(true),
+                        (const void *)up_small_k<Q_MLX8>(true),
+                        (const void *)down_small_k<Q_MXFP4>(4, true), (const void *)down_small_k<Q_BF16>(4, true),
+                        (const void *)down_small_k<Q_MLX4>(4, true), (const void *)down_small_k<Q_MLX8>(4, true),
+                        (const void *)down_small_k<Q_MXFP4>(9, true), (const void *)down_small_k<Q_BF16>(9, true),
+                        (const void *)down_small_k<Q_MLX4>(9, true), (const void *)down_small_k<Q_MLX8>(9, true)};
     // Best effort: HIP on gfx950 accepts launches up to the hardware LDS size without it, and
     // a runtime that rejects the attribute must not leave its error for the launch check below.
     for (const void *k : ks) {
@@ -1652,7 +1776,6 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
     if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0) ncu = 256;
   }
   a.row_tiles = a.ldh / UP_ROWS;
-  const bool mx = quant == Q_MXFP4;
   const size_t lds_up = mx ? (size_t)T * NTX * mx_row_bytes(a.xld) + 64 * (a.hidden / 32)
                            : (size_t)T * (a.hidden + LDS_PAD) * 2;
   // MXFP4: persistent, about two workgroups per compute unit.
@@ -1662,12 +1785,11 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
   if (e != hipSuccess) return e;
   a.row_tiles = a.hidden / 16;
   // MXFP4: per slot the activation terms and 16 rows of weight scales (of the larger group).
-  const int imax = std::max(a.grp[0].inter, a.grp[1].inter);
   const size_t lds_down = mx ? (size_t)S * (NTH * mx_row_bytes(a.hld) + 16 * ((16 * (imax / 32) + 15) / 16))
                              : (size_t)S * 2 * (a.ldh + LDS_PAD) * 2;
   a.max_work = T;
   const int down_grid = std::min(a.row_tiles * T, 2 * ncu);
-  const int ks = (mx || S > 4) ? 1 : 2;
+  const int ks = (mx || S > 4 || !one_down) ? 1 : 2;
   hipExtLaunchKernelGGL(down, dim3(down_grid), dim3(64 * S * ks), lds_down, s, tm_down.start,
                         tm_down.stop, 0, a, (const int32_t *)ra.topk_idx);
   return hipGetLastError();
