@@ -4,7 +4,9 @@
 
 #include <algorithm>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -18,6 +20,10 @@ hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStrea
 hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t s, Timing tm_up,
                         Timing tm_down);
 int gemm_rows_per_block(int quant, int phase);
+size_t decode_fused_lds(const GemmArgs &a, int T);
+bool decode_fused_fits(int H, int I, int E, int K, int shared_inter);
+int decode_fused_flags(int T, int E, int K, int I);
+hipError_t launch_decode_fused(bool gemma, GemmArgs a, const RouteArgs &ra, FuseArgs f, hipStream_t s, Timing tm);
 hipError_t launch_combine(const float *slot_out, int slots, int H, int T, float *y, hipStream_t s,
                           Timing tm);
 hipError_t launch_mxfp4_dequant(const uint8_t *blocks, const uint8_t *scales, int64_t n,
@@ -30,6 +36,10 @@ hipError_t launch_activation(int act, float alpha, float limit, const float *gat
 }  // namespace hh
 
 struct hh_ctx {
+  // Flags of the fused decode kernel: allocated and zeroed once, then only ever written with
+  // flag values; `epoch` is the value of the last call.
+  uint32_t *flags = nullptr;
+  uint32_t epoch = 0;
   int device = 0;
   hipStream_t stream = nullptr;
   uint8_t *arena = nullptr;
@@ -67,7 +77,7 @@ constexpr int kMaxTokens = 1 << 16;  // tokens per call
 // Scratch carve-up for T tokens of a layer shaped like d. All offsets 256-byte aligned.
 struct Scratch {
   size_t lg64, lg32, wn, topk_idx, topk_w, slot_w, seg, order, work, n_work, h_hi, h_lo, slot_out;
-  size_t xq, xs, hq, hs, total;
+  size_t xq, xs, hq, hs, status, total;
   int slots, positions, ldh, max_work, tile_tokens, nt;
   int xld, hld;   // MXFP4: row lengths of the fp8 operand terms (multiples of 512)
 };
@@ -119,6 +129,7 @@ Scratch plan(const hh_moe_desc &d, int T) {
   s.hq = take(mx ? (size_t)s.positions * hh::NTH * s.hld : 0);
   s.hs = take(mx ? (size_t)s.positions * hh::NTH * (s.hld / 32) : 0);
   s.slot_out = take(T > kSmallT ? sizeof(float) * (size_t)T * s.slots * H : 0);
+  s.status = take(sizeof(uint32_t));
   s.total = c;
   return s;
 }
@@ -137,6 +148,33 @@ int ensure_arena(hh_ctx *ctx, size_t bytes) {
   ctx->arena = (uint8_t *)p;
   ctx->arena_bytes = bytes;
   return HH_OK;
+}
+
+// Flag words of the fused decode kernel, per context.
+constexpr size_t kFlagBytes = 256 * 1024;
+
+int ensure_flags(hh_ctx *ctx) {
+  if (ctx->flags) return HH_OK;
+  void *p = nullptr;
+  if (hipMalloc(&p, kFlagBytes) != hipSuccess) return fail(HH_ENOMEM, "flag buffer allocation failed");
+  if (hipMemset(p, 0, kFlagBytes) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+    (void)hipFree(p);
+    return fail(HH_EHIP, "flag buffer initialisation failed");
+  }
+  ctx->flags = (uint32_t *)p;
+  return HH_OK;
+}
+
+// Whether a decode call takes the fused kernel: HH_DECODE_FUSED=1 in the environment turns it
+// on (it is not yet faster than the three-launch decode).
+bool use_fused(const hh_moe_desc &d, int T) {
+  static const bool enabled = [] {
+    const char *v = std::getenv("HH_DECODE_FUSED");
+    return v && v[0] == '1';
+  }();
+  return enabled && d.quant == HH_QUANT_MXFP4 && T <= kSmallT &&
+         hh::decode_fused_fits(d.hidden, d.intermediate, d.experts, d.top_k, d.shared_intermediate) &&
+         sizeof(uint32_t) * (size_t)hh::decode_fused_flags(kSmallT, d.experts, d.top_k, d.intermediate) <= kFlagBytes;
 }
 
 int check_desc(const hh_moe_desc *d) {
@@ -253,6 +291,7 @@ int hh_ctx_destroy(hh_ctx *ctx) {
   hipSetDevice(ctx->device);
   if (ctx->stream) hipStreamSynchronize(ctx->stream);
   if (ctx->arena) hipFree(ctx->arena);
+  if (ctx->flags) hipFree(ctx->flags);
   for (hipEvent_t ev : ctx->events) hipEventDestroy(ev);
   if (ctx->stream) hipStreamDestroy(ctx->stream);
   delete ctx;
@@ -385,7 +424,6 @@ int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
   hh::Timing tm;
   rc = phase_timing(ctx, &tm);
   if (rc) return rc;
-  HH_HIP(hh::launch_route(r, ctx->stream, tm));
 
   hh::GemmArgs g{};
   fill_group(g.grp[0], *d, w->experts, w->expert_stride, d->intermediate);
@@ -418,6 +456,29 @@ int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
   g.hq = base + s.hq;
   g.hs = base + s.hs;
   g.hld = s.hld;
+
+  if (use_fused(*d, T)) {
+    // Decode in one launch (decode_mx): logits and h terms in the arena, flags in the
+    // context's flag buffer.
+    if ((rc = ensure_flags(ctx))) return rc;
+    hh::FuseArgs f{};
+    f.flags = ctx->flags;
+    f.status = (uint32_t *)(base + s.status);
+    if (++ctx->epoch == 0) ++ctx->epoch;   // flags start at 0
+    f.epoch = ctx->epoch;
+    HH_HIP(hh::launch_decode_fused(d->router == HH_ROUTER_GEMMA, g, r, f, ctx->stream, tm));
+    for (int p = 1; p < 4; ++p) {   // the other phases are empty: keep the record aligned
+      hh::Timing te;
+      if ((rc = phase_timing(ctx, &te))) return rc;
+      if (te.start) {
+        HH_HIP(hipEventRecord(te.start, ctx->stream));
+        HH_HIP(hipEventRecord(te.stop, ctx->stream));
+      }
+    }
+    ctx->dispatches += 1;
+    return HH_OK;
+  }
+  HH_HIP(hh::launch_route(r, ctx->stream, tm));
 
   if (T <= kSmallT) {
     // Decode: exact logits → gate-up (selects the top-k itself) → down with the rank-ordered

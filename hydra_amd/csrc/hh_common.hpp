@@ -181,6 +181,19 @@ struct RouteArgs {
 // Optional profiling events of a launch sequence: `start` is attached to the first kernel's
 // dispatch packet and `stop` to the last one's (hipExtLaunchKernelGGL), so the interval covers
 // exactly the kernels' execution, as a kernel trace would. Null events launch normally.
+// Cache policy of device-scope buffer loads and stores on gfx950 (the sc1 bit): a load misses in
+// caches that are not coherent across the device, a store completes once it is visible across
+// the device. Data exchanged between workgroups of one launch moves this way.
+constexpr int kDevScope = 16;
+
+// Fused decode (one launch per MXFP4 layer), see decode_mx.
+struct FuseArgs {
+  uint32_t *flags;    // [R] router workgroups, then the gate-up items
+  uint32_t *status;   // bit 0: a wait timed out
+  uint32_t epoch;     // this call's flag value (never repeats for a buffer)
+  int32_t R, U, D;    // workgroups per role
+};
+
 struct Timing {
   hipEvent_t start = nullptr, stop = nullptr;
 };

@@ -45,6 +45,7 @@
 // qwen_silu_multiply, gelu_mul, write_expert_scaled, scatter_expert(_scaled), sum_expert_slices.
 #include "hh_common.hpp"
 #include "hh_select.hpp"
+#include "hh_logit.hpp"
 
 #include <algorithm>
 #include <mutex>
@@ -427,6 +428,18 @@ __device__ __forceinline__ f32x4 up_values(const GemmArgs &a, const uint8_t *blo
   return y;
 }
 
+// up_values with the GPT-OSS bias of the 4 intermediates already loaded: 16 bytes from the bias
+// row at element 2·i0, (gate, up) bf16 pairs in order.
+__device__ __forceinline__ f32x4 up_values_mx(const GemmArgs &a, const u32x4 &bias, const f32x4 &gate,
+                                              const f32x4 &up) {
+  f32x4 y;
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii)
+    y[ii] = activate(a.act, gate[ii] + bf16_bits_to_f32(bias[ii] & 0xFFFFu), up[ii] + bf16_bits_to_f32(bias[ii] >> 16),
+                     a.alpha, a.limit);
+  return y;
+}
+
 // Gate-up epilogue of 4 intermediates i0..i0+3 of slot `slot`: bias, activation, bf16 hi/lo.
 template <int FMT>
 __device__ __forceinline__ void up_epilogue(const GemmArgs &a, const uint8_t *blob,
@@ -572,6 +585,8 @@ __device__ __forceinline__ int rank_of(const int *s_idx, int t, int e, int K, bo
 // ---- decode: gate-up ----------------------------------------------------------------------------
 constexpr int SMALL_T = 16;       // largest batch of the decode kernels
 constexpr int UP_ROWS = 32;       // intermediates per up_small workgroup (2 tiles × {gate, up})
+constexpr int MX_ONE_CHUNKS = 24; // MXFP4 decode rows of at most this many 128-column chunks stream in one round
+constexpr int kFusedMaxE = 128;   // experts of layers that take the fused decode kernel
 constexpr int LDS_PAD = 8;        // bf16 elements of padding per staged row (bank spread)
 
 // Grid: row tile rt (32 intermediates) × u, u < min(E, T·K) the distinct routed experts of the
@@ -741,14 +756,25 @@ __device__ __forceinline__ int scale_vectors(int rows, int K) { return rows * (K
 
 // The NTH fp8 terms of 8 activations of slot `slot` (intermediates ia..ia+3 in q[t][0], ib..ib+3
 // in q[t][1]) and, from lane group 0, the scales of their block blk.
+template <bool DEV = false>
 __device__ __forceinline__ void store_hq(const GemmArgs &a, int slot, int blk, int ia, int ib,
                                          const uint32_t (&q)[NTH][2], const uint32_t (&sb)[NTH], int g) {
+  // DEV: device-scope stores (sc1) through a buffer resource based at hq (hs lies after it), for
+  // readers in other workgroups of the same launch.
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)a.hq, (short)0, 0x7FFFFFF0, 0x00020000);
 #pragma unroll
   for (int t = 0; t < NTH; ++t) {
     uint8_t *row = a.hq + ((size_t)slot * NTH + t) * a.hld;
-    *(uint32_t *)(row + ia) = q[t][0];
-    *(uint32_t *)(row + ib) = q[t][1];
-    if (g == 0) a.hs[((size_t)slot * NTH + t) * (a.hld / 32) + blk] = (uint8_t)sb[t];
+    uint8_t *srow = a.hs + ((size_t)slot * NTH + t) * (a.hld / 32) + blk;
+    if constexpr (DEV) {
+      __builtin_amdgcn_raw_buffer_store_b32(q[t][0], rs, (int)(row + ia - a.hq), 0, kDevScope);
+      __builtin_amdgcn_raw_buffer_store_b32(q[t][1], rs, (int)(row + ib - a.hq), 0, kDevScope);
+      if (g == 0) __builtin_amdgcn_raw_buffer_store_b8((uint8_t)sb[t], rs, (int)(srow - a.hq), 0, kDevScope);
+    } else {
+      *(uint32_t *)(row + ia) = q[t][0];
+      *(uint32_t *)(row + ib) = q[t][1];
+      if (g == 0) *srow = (uint8_t)sb[t];
+    }
   }
 }
 
@@ -761,7 +787,10 @@ __host__ __device__ __forceinline__ int mx_row_bytes(int ld) { return ld + ld / 
 // in 16-byte vectors v = id + threads·k. The first NB vectors of each thread can be loaded before
 // other loads are issued (load_first) and stored after them (store_first): completion counts
 // are in order, so stores issued after a weight stream would otherwise wait for all of it.
-template <int NTERM, int NB, class RowOf> struct MxStage {
+// DEV: the rows were written by other workgroups of the same launch with device-scope stores;
+// they are read with device-scope loads (sc1), which miss in caches that may hold older
+// contents, through a buffer resource based at q (sc lies after q).
+template <int NTERM, int NB, class RowOf, bool DEV = false> struct MxStage {
   uint8_t *dst;
   const uint8_t *q, *sc;
   int ld, cols, nrows, n, dv, per_row, RS, id, threads;
@@ -777,7 +806,14 @@ template <int NTERM, int NB, class RowOf> struct MxStage {
   __device__ __forceinline__ u32x4 src(int v) const {
     const int rr = v / per_row, qq = v - rr * per_row;
     const size_t grow = (size_t)row_of(rr / NTERM) * NTERM + rr % NTERM;
-    return qq < dv ? *(const u32x4 *)(q + grow * ld + 16 * qq) : *(const u32x4 *)(sc + grow * (ld / 32) + 16 * (qq - dv));
+    // One load from a selected address (two loads under a lane-dependent branch would serialise).
+    const uint8_t *p = qq < dv ? q + grow * ld + 16 * qq : sc + grow * (ld / 32) + 16 * (qq - dv);
+    if constexpr (DEV) {
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)q, (short)0, 0x7FFFFFF0, 0x00020000);
+      return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(p - q), 0, kDevScope));
+    } else {
+      return *(const u32x4 *)p;
+    }
   }
   // Scale bytes of blocks at or past `cols` (the tail of the last scale vector) are stored as 127
   // (2^0), so the MFMA operands of the last chunk need no masks.
@@ -817,12 +853,67 @@ template <int NTERM, int NB, class RowOf> struct MxStage {
       stage_batch<4>(base, id, threads, n, [&](int v) { return src(v); }, [&](int v, const u32x4 &x) { put(v, x); });
   }
 };
-template <int NTERM, int NB, class RowOf>
-__device__ __forceinline__ MxStage<NTERM, NB, RowOf> mx_stage(uint8_t *dst, const uint8_t *q, const uint8_t *sc,
-                                                               int ld, int cols, int nrows, RowOf row_of, int id,
-                                                               int threads) {
-  return MxStage<NTERM, NB, RowOf>(dst, q, sc, ld, cols, nrows, row_of, id, threads);
+template <int NTERM, int NB, bool DEV = false, class RowOf>
+__device__ __forceinline__ MxStage<NTERM, NB, RowOf, DEV> mx_stage(uint8_t *dst, const uint8_t *q, const uint8_t *sc,
+                                                                    int ld, int cols, int nrows, RowOf row_of, int id,
+                                                                    int threads) {
+  return MxStage<NTERM, NB, RowOf, DEV>(dst, q, sc, ld, cols, nrows, row_of, id, threads);
 }
+
+// The decode plan, computed by every wave in registers from the batch's top-k table s_idx
+// [T][K] (LDS): the distinct experts in order of first appearance in (token, rank) order and
+// the tokens of each. Lane l holds entries l and 64 + l (T·K ≤ 128).
+struct Plan {
+  int pe[2];
+  bool pf[2];
+  uint64_t ptm[2];
+  uint64_t m0, m1;
+  int n0, nu, E, T;
+  __device__ __forceinline__ Plan(const int *s_idx, int T_, int K, int E_) : E(E_), T(T_) {
+    const int lane = threadIdx.x & 63, n = T * K;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      pe[h] = lane + 64 * h < n ? s_idx[lane + 64 * h] : -1;
+      pf[h] = lane + 64 * h < n;
+      ptm[h] = 0ull;
+    }
+    for (int j = 0, tj = 0, rj = 0; j < n; ++j) {
+      const int ej = __builtin_amdgcn_readlane(j < 64 ? pe[0] : pe[1], j & 63);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        if (ej == pe[h]) {
+          if (j < lane + 64 * h) pf[h] = false;
+          ptm[h] |= 1ull << tj;
+        }
+      if (++rj == K) { rj = 0; ++tj; }
+    }
+    m0 = __ballot(pf[0]);
+    m1 = __ballot(pf[1]);
+    n0 = __popcll(m0);
+    nu = n0 + __popcll(m1);
+  }
+  // Distinct expert u (< nu) and its token mask; u ≥ nu is the shared expert, every token.
+  __device__ __forceinline__ void entry(int u, int &e, uint64_t &tm) const {
+    if (u >= nu) {
+      e = E;
+      tm = (1ull << T) - 1ull;
+      return;
+    }
+    const int h = u < n0 ? 0 : 1;
+    const int l = nth_bit(h ? m1 : m0, h ? u - n0 : u);
+    const int ev = h ? pe[1] : pe[0];
+    const uint64_t tv = h ? ptm[1] : ptm[0];
+    e = __builtin_amdgcn_readlane(ev, l);
+    tm = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(tv >> 32), l) << 32) |
+         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tv, l);
+  }
+  // Plan index of routed expert e (wave-uniform; e must occur in the table).
+  __device__ __forceinline__ int index_of(int e) const {
+    const uint64_t h0 = __ballot(pf[0] && pe[0] == e), h1 = __ballot(pf[1] && pe[1] == e);
+    if (h0) return __popcll(m0 & ((1ull << (__ffsll((unsigned long long)h0) - 1)) - 1ull));
+    return n0 + __popcll(m1 & ((1ull << (__ffsll((unsigned long long)h1) - 1)) - 1ull));
+  }
+};
 
 // Decode gate-up on the scaled MFMA, persistent: the grid holds about two workgroups per compute
 // unit; each selects the top-k of the batch once, lists the batch's distinct experts in LDS (in
@@ -836,12 +927,8 @@ __device__ __forceinline__ MxStage<NTERM, NB, RowOf> mx_stage(uint8_t *dst, cons
 template <int DA, bool ONE>
 __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) {
   constexpr int NM = 1;
-  constexpr int NE = SMALL_T * kMaxTopK + 1;
   extern __shared__ __align__(16) uint8_t s_xb[];   // [T][NTX] rows of mx_row_bytes(xld), then [64][H/32] scales
   __shared__ int s_idx[SMALL_T * kMaxTopK];
-  __shared__ int s_uexp[NE];
-  __shared__ uint64_t s_utm[NE];
-  __shared__ int s_nu;
   __shared__ f32x4 s_up[2][64];
   __shared__ float s_hv[SMALL_T][UP_ROWS];
   __shared__ double s_lg[4][64];
@@ -853,6 +940,11 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
   const int T = ra.tokens, E = a.experts, K = a.top_k, S = a.slots, H = a.hidden;
   const bool has_shared = S > K;
 
+  // x terms of every token: first batch of loads now (they do not depend on the routing), stored
+  // with the first item.
+  const int RS = mx_row_bytes(a.xld);
+  auto xs = mx_stage<NTX, 2>(s_xb, a.xq, a.xs, a.xld, a.hidden, T, [](int j) { return j; }, tid, 256);
+  xs.load_first();
   // Top-k of every token (wave w: tokens w, w + 4, ...); workgroup 0 writes the routing outputs.
   for (int t = wave; t < T; t += 4) {
     const double *lg = ra.lg64 + (size_t)t * (E + 1);
@@ -860,46 +952,9 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
     if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
     if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
   }
-  // x terms of every token: first batch of loads now, stored with the first item.
-  const int RS = mx_row_bytes(a.xld);
-  auto xs = mx_stage<NTX, 2>(s_xb, a.xq, a.xs, a.xld, a.hidden, T, [](int j) { return j; }, tid, 256);
-  xs.load_first();
   __syncthreads();
-  if (wave == 0) {
-    // Distinct experts in order of first appearance, and the tokens of each.
-    const int n = T * K;   // ≤ 128: entries lane and lane + 64
-    bool first[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int i = lane + 64 * h;
-      first[h] = i < n;
-      if (i < n) {
-        const int ei = s_idx[i];
-        for (int j = 0; j < i; ++j) first[h] = first[h] && s_idx[j] != ei;
-      }
-    }
-    const uint64_t m0 = __ballot(first[0]), m1 = __ballot(first[1]);
-    const uint64_t lt = (1ull << lane) - 1ull;
-    const int n0 = __popcll(m0), nu = n0 + __popcll(m1);
-    if (first[0]) s_uexp[__popcll(m0 & lt)] = s_idx[lane];
-    if (first[1]) s_uexp[n0 + __popcll(m1 & lt)] = s_idx[lane + 64];
-    __builtin_amdgcn_wave_barrier();
-    for (int u = lane; u < nu; u += 64) {
-      const int e = s_uexp[u];
-      uint64_t tm = 0;
-      for (int t = 0; t < T; ++t)
-        for (int r = 0; r < K; ++r)
-          if (s_idx[t * K + r] == e) tm |= 1ull << t;
-      s_utm[u] = tm;
-    }
-    if (lane == 0) {
-      s_nu = nu;
-      s_uexp[nu] = E;                       // the shared expert, every token
-      s_utm[nu] = T >= 64 ? ~0ull : (1ull << T) - 1ull;
-    }
-  }
-  __syncthreads();
-  const int nu = s_nu;
+  const Plan plan(s_idx, T, K, E);
+  const int nu = plan.nu;
   const int rtr = a.grp[0].inter / UP_ROWS;
   const int nitems = nu * rtr + (has_shared ? a.grp[1].inter / UP_ROWS : 0);
 
@@ -914,8 +969,9 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
     const bool sh = it >= nu * rtr;
     const int u = sh ? nu : it / rtr;
     const int rt = sh ? it - nu * rtr : it % rtr;
-    const int e = s_uexp[u];
-    const uint64_t tm = s_utm[u];
+    int e;
+    uint64_t tm;
+    plan.entry(u, e, tm);
     const int ntok = __popcll(tm);
     const ExpertGroup &grp = a.grp[sh ? 1 : 0];
     const uint8_t *blob = grp.blobs + (sh ? 0 : (size_t)e * grp.stride);
@@ -927,6 +983,9 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
     u32x4 scv[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) scv[k] = *(const u32x4 *)(gsc + 16 * min(tid + 256 * k, nsv - 1));
+    // The gate waves' bias (4 intermediates per lane), loaded ahead of the weight stream.
+    u32x4 bias = {0u, 0u, 0u, 0u};
+    if (!is_up && a.expert_bias) bias = *(const u32x4 *)(blob + grp.off[2] + 4 * (rb + 4 * g));
     ATile<Q_MXFP4_W> at[NM] = {tile_of<PH_UP, Q_MXFP4_W>(blob, grp, rb, is_up, H, l16)};
     AStream<Q_MXFP4_W, NM, DA> as(0, 1, nch);
     as.fill(at, nch, g, H);
@@ -960,7 +1019,7 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
     if (is_up) s_up[q][lane] = res;
     __syncthreads();
     if (!is_up && l16 < ntok) {
-      const f32x4 y = up_values<Q_MXFP4>(a, blob, grp, rb + 4 * g, res, s_up[q][lane]);
+      const f32x4 y = up_values_mx(a, bias, res, s_up[q][lane]);
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) s_hv[l16][16 * q + 4 * g + ii] = y[ii];
     }
@@ -1109,6 +1168,307 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
     a.y[(size_t)t * H + rb + tid] = y;
   }
   __syncthreads();   // the next item rewrites the LDS rows and s_o
+  }
+}
+
+// ---- decode, fused: one launch per MXFP4 layer ------------------------------------------------------
+// Workgroups take one of three roles by blockIdx, in dependency order:
+//   [0, R)        router: one wave per (token, expert) pair computes its exact fp64 logit into
+//                 the exchange buffer; then the workgroup's flag.
+//   [R, R+U)      gate-up: quantise x into LDS (every workgroup itself), wait for the router
+//                 flags, select the top-k and build the plan (as up_small_mx), then items
+//                 it = role index, + U, ...; an item's h terms go to the exchange buffer, then
+//                 the item's flag.
+//   [R+U, R+U+D)  down: select the top-k of the batch, then items (16 hidden rows, token),
+//                 wave r = slot r: issue the weight stream and scales, wait for the flags of the
+//                 gate-up items of the slot's expert, stage its h terms and compute; the rank-
+//                 ordered slot sum goes to y.
+// Data passed between workgroups (logits, h terms) is written with device-scope stores and read
+// with device-scope loads (kDevScope); a writer's stores have completed before it stores the
+// flag (flags are device-scope atomics), so a reader that has seen the flag reads the new data on
+// any XCD, without cache maintenance. Workgroups only wait for workgroups of smaller index,
+// which the dispatcher starts first, so every wait is for one that is running or done. Waits are
+// bounded (10 ms): a workgroup that times out sets bit 0 of `status` and its outputs are NaN.
+__device__ __forceinline__ bool flags_ready(const uint32_t *flags, int n, uint32_t epoch) {
+  bool ok = true;
+  for (int i = threadIdx.x & 63; i < n; i += 64)
+    ok = ok && __hip_atomic_load(flags + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch;
+  return __ballot(!ok) == 0ull;
+}
+// Whole wave: true once flags[0..n) all hold `epoch`, false past the deadline (wall clock).
+__device__ __forceinline__ bool wave_wait(const uint32_t *flags, int n, uint32_t epoch, uint64_t deadline) {
+  for (;;) {
+    if (flags_ready(flags, n, epoch)) return true;
+    if (wall_clock64() > deadline) return false;
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+// Whole workgroup: wave 0 waits, the others learn the outcome through LDS.
+__device__ __forceinline__ bool group_wait(const uint32_t *flags, int n, uint32_t epoch, uint64_t deadline,
+                                           int *s_flag) {
+  if (threadIdx.x < 64) {
+    const bool ok = wave_wait(flags, n, epoch, deadline);
+    if (threadIdx.x == 0) *s_flag = ok ? 1 : 0;
+  }
+  __syncthreads();
+  return *s_flag != 0;
+}
+__device__ __forceinline__ void store_flag(uint32_t *flag, uint32_t epoch) {
+  __hip_atomic_store(flag, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Before a flag store: this wave's device-scope data stores have completed.
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// x of every token as NTX fp8 terms into LDS rows (t, j) of RS bytes, the layout MxStage gives:
+// term bytes at their columns, block scales after `xld`, the last chunk's columns past H zero
+// and their scales 2^0. Lane (g, l16) of a wave takes block 16·k + l16, columns 8g .. 8g+7
+// (quant_block).
+__device__ __forceinline__ void quant_x_lds(const uint16_t *x, int T, int H, int xld, uint8_t *s_xb, int RS) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, l16 = lane & 15;
+  const int nb = H / 32, per_t = (nb + 15) / 16;
+  for (int w = wave; w < T * per_t; w += 4) {
+    const int t = w / per_t, b = 16 * (w - t * per_t) + l16, bc = min(b, nb - 1);
+    const u32x4 xv = *(const u32x4 *)(x + (size_t)t * H + bc * 32 + 8 * g);
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[2 * k] = bf_lo(xv[k]);
+      v[2 * k + 1] = bf_hi(xv[k]);
+    }
+    uint32_t q[NTX][2], sb[NTX];
+    quant_block<NTX>(v, q, sb);
+    if (b < nb) {
+#pragma unroll
+      for (int j = 0; j < NTX; ++j) {
+        uint8_t *row = s_xb + (size_t)(t * NTX + j) * RS;
+        *(u32x2 *)(row + b * 32 + 8 * g) = u32x2{q[j][0], q[j][1]};
+        if (g == 0) row[xld + b] = (uint8_t)sb[j];
+      }
+    }
+  }
+  const int hp = (H + 127) & ~127, nz = (hp - H) / 16, ns = (hp - H) / 32;
+  for (int v = tid; v < T * NTX * (nz + ns); v += 256) {
+    const int rr = v / (nz + ns), k = v - rr * (nz + ns);
+    uint8_t *row = s_xb + (size_t)rr * RS;
+    if (k < nz) *(u32x4 *)(row + H + 16 * k) = u32x4{0u, 0u, 0u, 0u};
+    else row[xld + H / 32 + (k - nz)] = 127;
+  }
+}
+
+template <bool GEMMA>
+__global__ __launch_bounds__(256, 2) void decode_mx(GemmArgs a, RouteArgs ra, FuseArgs f) {
+  constexpr int NM = 1, DA = MX_ONE_CHUNKS;
+  extern __shared__ __align__(16) uint8_t s_dyn[];
+  __shared__ int s_idx[SMALL_T * kMaxTopK];
+  __shared__ float s_w[SMALL_T * kMaxTopK];
+  __shared__ f32x4 s_up[2][64];
+  __shared__ float s_hv[SMALL_T][UP_ROWS];
+  __shared__ double s_lg[4][64];
+  __shared__ double s_row[4][kFusedMaxE + 1];
+  __shared__ int s_ri[4][kMaxTopK];
+  __shared__ float s_o[4][16];
+  __shared__ int s_flag, s_bad;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, l16 = lane & 15;
+  const int T = ra.tokens, E = a.experts, E1 = E + 1, K = a.top_k, S = a.slots, H = a.hidden;
+  const int b = blockIdx.x;
+  const uint64_t deadline = wall_clock64() + 1000000;   // 10 ms at 100 MHz
+
+  // ---- router ----
+  if (b < f.R) {
+    const int p = b * 4 + wave;
+    if (p < T * E1) {
+      const int t = p / E1, e = p - t * E1;
+      if (e < E || ra.shared_gate) {
+        const double v = pair_logit<GEMMA>(ra, t, e);
+        if (lane == 0) __hip_atomic_store(ra.lg64 + (size_t)t * E1 + e, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    wait_stores();
+    __syncthreads();
+    if (tid == 0) store_flag(f.flags + b, f.epoch);
+    return;
+  }
+
+  const bool up_role = b < f.R + f.U;
+  if (tid == 0) s_bad = 0;
+  // Gate-up workgroups quantise x while the router runs.
+  const int RS = mx_row_bytes(a.xld);
+  if (up_role) quant_x_lds(ra.x, T, H, a.xld, s_dyn, RS);
+  if (!group_wait(f.flags, f.R, f.epoch, deadline, &s_flag)) {
+    if (tid == 0) atomicOr(f.status, 1u);
+    if (!up_role) {
+      // Down items of this workgroup: NaN rows.
+      for (int it = b - f.R - f.U; it < a.row_tiles * T; it += f.D)
+        if (tid < 16) a.y[(size_t)(it % T) * H + (it / T) * 16 + tid] = __builtin_nanf("");
+    }
+    return;
+  }
+  // Top-k of every token (wave w: tokens w, w + 4, ...). The first gate-up workgroup writes the
+  // routing outputs; down workgroups keep the weights.
+  for (int t = wave; t < T; t += 4) {
+    // The token's logits into LDS with device-scope loads, then the selection from there.
+    double *lg = s_row[wave];
+    for (int e = lane; e < E1; e += 64)
+      lg[e] = __hip_atomic_load(ra.lg64 + (size_t)t * E1 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_wave_barrier();
+    const TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave]) : topk_exact(lg, E, K);
+    if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
+    if (b == f.R) finish_token(ra, t, tk, ra.shared_gate ? lg[E] : 0.0);
+    if (!up_role) {
+      double v;
+      int e;
+      const double w = token_weight(ra, tk, v, e);
+      if (lane < K) s_w[t * K + lane] = (float)w;
+    }
+  }
+  __syncthreads();
+  const Plan plan(s_idx, T, K, E);
+  const int nu = plan.nu;
+  const int rtr = a.grp[0].inter / UP_ROWS;
+  const int nitems = nu * rtr;
+
+  if (up_role) {
+    // ---- gate-up: as up_small_mx with x already in LDS ----
+    const int q = wave & 1;
+    const bool is_up = wave >= 2;
+    const int nch = (H + 127) / 128;
+    const int nsb = H / 32;
+    uint8_t *s_sc = s_dyn + (size_t)T * NTX * RS;   // [64][nsb]
+    const int nsv = scale_vectors(64, H);
+    for (int it = b - f.R; it < nitems; it += f.U) {
+      const int u = it / rtr, rt = it - u * rtr;
+      int e;
+      uint64_t tm;
+      plan.entry(u, e, tm);
+      const int ntok = __popcll(tm);
+      const ExpertGroup &grp = a.grp[0];
+      const uint8_t *blob = grp.blobs + (size_t)e * grp.stride;
+      const int rb = rt * UP_ROWS + 16 * q;
+      const uint8_t *gsc = blob + grp.off[1] + (size_t)rt * 64 * nsb;
+      u32x4 scv[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) scv[k] = *(const u32x4 *)(gsc + 16 * min(tid + 256 * k, nsv - 1));
+      u32x4 bias = {0u, 0u, 0u, 0u};
+      if (!is_up && a.expert_bias) bias = *(const u32x4 *)(blob + grp.off[2] + 4 * (rb + 4 * g));
+      ATile<Q_MXFP4_W> at[NM] = {tile_of<PH_UP, Q_MXFP4_W>(blob, grp, rb, is_up, H, l16)};
+      AStream<Q_MXFP4_W, NM, DA> as(0, 1, nch);
+      as.fill(at, nch, g, H);
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        if (tid + 256 * k < nsv) *(u32x4 *)(s_sc + 16 * (tid + 256 * k)) = scv[k];
+      for (int v = tid + 512; v < nsv; v += 256) *(u32x4 *)(s_sc + 16 * v) = *(const u32x4 *)(gsc + 16 * v);
+      __syncthreads();
+      const uint8_t *my_sc = s_sc + (2 * (16 * q + l16) + (is_up ? 1 : 0)) * nsb;
+      int gi = g;
+      asm volatile("" : "+v"(gi));
+      const int my_t = nth_bit(tm, min(l16, ntok - 1));
+      const uint8_t *brow = s_dyn + (size_t)my_t * NTX * RS;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      as.template run_pf<true>(
+          at, nch, gi, H, [&](int c) { return mx_ops<NTX>(brow, RS, a.xld, my_sc, nsb, c, gi); },
+          [&](const Fmt<Q_MXFP4_W>::A (&w)[NM], int c, const MxOps<NTX> &o) { chunk_mx1<NTX>(acc, w[0].w, o, c, gi, H); });
+      if (is_up) s_up[q][lane] = acc;
+      __syncthreads();
+      if (!is_up && l16 < ntok) {
+        const f32x4 y = up_values_mx(a, bias, acc, s_up[q][lane]);
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) s_hv[l16][16 * q + 4 * g + ii] = y[ii];
+      }
+      __syncthreads();
+      if (wave == 0) {
+        const int j = min(l16, ntok - 1);
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = s_hv[j][8 * g + i];
+        uint32_t hq[NTH][2], sb[NTH];
+        quant_block<NTH>(v, hq, sb);
+        if (l16 < ntok) {
+          const int t = nth_bit(tm, l16);
+          const int slot = t * S + rank_of(s_idx, t, e, K, false);
+          store_hq<true>(a, slot, rt, rt * UP_ROWS + 8 * g, rt * UP_ROWS + 8 * g + 4, hq, sb, g);
+        }
+        wait_stores();
+        if (lane == 0) store_flag(f.flags + f.R + it, f.epoch);
+      }
+    }
+    return;
+  }
+
+  // ---- down: wave r = slot r of the item's token ----
+  const int r = wave;
+  const int I = a.grp[0].inter;
+  const int nch = (I + 127) / 128;
+  const int nsb = I / 32, nsv = scale_vectors(16, I);
+  const int RSH = mx_row_bytes(a.hld);
+  const int slot_bytes = NTH * RSH + 16 * ((16 * nsb + 15) / 16);
+  uint8_t *my_lds = s_dyn + (size_t)r * slot_bytes;
+  uint8_t *s_sc = my_lds + NTH * RSH;
+  for (int it = b - f.R - f.U; it < a.row_tiles * T; it += f.D) {
+    const int rt = it / T, t = it - rt * T;
+    const int rb = rt * 16;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if (r < K) {
+      const int slot = t * S + r;
+      const int e = s_idx[t * K + r];
+      const ExpertGroup &grp = a.grp[0];
+      const uint8_t *blob = grp.blobs + (size_t)e * grp.stride;
+      const uint8_t *gsc = blob + grp.off[4] + (size_t)rb * nsb;
+      u32x4 scv[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) scv[k] = *(const u32x4 *)(gsc + 16 * min(lane + 64 * k, nsv - 1));
+      ATile<Q_MXFP4_W> aw[NM] = {tile_of<PH_DOWN, Q_MXFP4_W>(blob, grp, rb, false, I, l16)};
+      AStream<Q_MXFP4_W, NM, DA> as(0, 1, nch);
+      as.fill(aw, nch, g, I);
+      // The h terms of this slot exist once every gate-up item of its expert is done.
+      const int u = plan.index_of(e);
+      const bool ok = wave_wait(f.flags + f.R + u * rtr, rtr, f.epoch, deadline);
+      if (!ok && lane == 0) {
+        s_bad = 1;
+        atomicOr(f.status, 1u);
+      }
+      // The lane id as a value opaque to the compiler in each item, so the staging addresses are
+      // computed here rather than hoisted out of the item loop and held across it.
+      int li = lane;
+      asm volatile("" : "+v"(li));
+      auto hs = mx_stage<NTH, 9, true>(my_lds, a.hq, a.hs, a.hld, I, 1, [&](int) { return slot; }, li, 64);
+      hs.load_first();
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        if (li + 64 * k < nsv) *(u32x4 *)(s_sc + 16 * (li + 64 * k)) = scv[k];
+      for (int v = li + 128; v < nsv; v += 64) *(u32x4 *)(s_sc + 16 * v) = *(const u32x4 *)(gsc + 16 * v);
+      hs.store_first();
+      hs.rest();
+      hs.pad();
+      __builtin_amdgcn_s_waitcnt(0xc07f);   // this wave's LDS stores (lgkmcnt 0)
+      __builtin_amdgcn_wave_barrier();
+      const uint8_t *my_sc = s_sc + l16 * nsb;
+      int gi = g;
+      asm volatile("" : "+v"(gi));
+      as.template run_pf<true>(
+          aw, nch, gi, I, [&](int c) { return mx_ops<NTH>(my_lds, RSH, a.hld, my_sc, nsb, c, gi); },
+          [&](const Fmt<Q_MXFP4_W>::A (&w)[NM], int c, const MxOps<NTH> &o) { chunk_mx1<NTH>(acc, w[0].w, o, c, gi, I); });
+      if (l16 == 0) {
+        float db[4] = {0.f, 0.f, 0.f, 0.f};
+        if (a.expert_bias) {
+          const uint16_t *bias = (const uint16_t *)(blob + grp.off[5]);
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) db[ii] = bf16_bits_to_f32(bias[rb + 4 * g + ii]);
+        }
+        const float w = s_w[t * K + r];
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) s_o[r][4 * g + ii] = w * (acc[ii] + db[ii]);
+      }
+    }
+    __syncthreads();
+    if (tid < 16) {
+      float y = s_o[0][tid];
+      for (int qq = 1; qq < K; ++qq) y += s_o[qq][tid];
+      a.y[(size_t)t * H + rb + tid] = s_bad ? __builtin_nanf("") : y;
+    }
+    __syncthreads();   // the next item rewrites the LDS rows and s_o
   }
 }
 
@@ -1679,7 +2039,7 @@ template <int FMT> constexpr int decode_depth() { return FMT == Q_BF16 ? 4 : (FM
 
 // MXFP4 streams of at most MX_ONE chunks (K ≤ 3072) run the single-round kernels (the whole row
 // in flight, no ring refills); longer rows take the ring variants.
-constexpr int MX_ONE = 24;
+constexpr int MX_ONE = MX_ONE_CHUNKS;
 template <int FMT> static UpSmallKernel up_small_k(bool one) {
   if constexpr (FMT == Q_MXFP4) return one ? up_small_mx<MX_ONE, true> : up_small_mx<16, false>;
   else return up_small<FMT, decode_depth<FMT>()>;
@@ -1792,6 +2152,50 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
   const int ks = (mx || S > 4 || !one_down) ? 1 : 2;
   hipExtLaunchKernelGGL(down, dim3(down_grid), dim3(64 * S * ks), lds_down, s, tm_down.start,
                         tm_down.stop, 0, a, (const int32_t *)ra.topk_idx);
+  return hipGetLastError();
+}
+
+// Fused decode (MXFP4, T ≤ 16, no shared expert, top_k ≤ 4, H and I ≤ MX_ONE chunks).
+// Dynamic LDS: the larger of the gate-up role (x terms of T tokens + 64 rows of scales) and
+// the down role (4 slots of h terms + 16 rows of scales).
+size_t decode_fused_lds(const GemmArgs &a, int T) {
+  const size_t up = (size_t)T * NTX * mx_row_bytes(a.xld) + 64 * (size_t)(a.hidden / 32);
+  const int nsb = a.grp[0].inter / 32;
+  const size_t down = 4 * ((size_t)NTH * mx_row_bytes(a.hld) + 16 * (size_t)((16 * nsb + 15) / 16));
+  return std::max(up, down);
+}
+bool decode_fused_fits(int H, int I, int E, int K, int shared_inter) {
+  return shared_inter == 0 && K <= 4 && E <= kFusedMaxE && (H + 127) / 128 <= MX_ONE && (I + 127) / 128 <= MX_ONE && H % 32 == 0 &&
+         I % 32 == 0;
+}
+// Router workgroups and gate-up item flags of a T-token call.
+int decode_fused_flags(int T, int E, int K, int I) {
+  return (T * (E + 1) + 3) / 4 + std::min(E, T * K) * (I / UP_ROWS);
+}
+hipError_t launch_decode_fused(bool gemma, GemmArgs a, const RouteArgs &ra, FuseArgs f, hipStream_t s, Timing tm) {
+  const int T = ra.tokens;
+  if (T < 1 || T > SMALL_T) return hipErrorInvalidValue;
+  static int ncu = 0;
+  if (!ncu) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0) ncu = 256;
+  }
+  static std::once_flag lds_once;
+  std::call_once(lds_once, [] {
+    for (const void *k : {(const void *)decode_mx<false>, (const void *)decode_mx<true>}) {
+      (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      (void)hipGetLastError();
+    }
+  });
+  const int nup = std::min(a.experts, T * a.top_k) * (a.grp[0].inter / UP_ROWS);
+  a.row_tiles = a.hidden / 16;
+  f.R = (T * (a.experts + 1) + 3) / 4;
+  f.D = std::min(a.row_tiles * T, ncu);
+  f.U = std::max(1, std::min(nup, 2 * ncu - f.R - f.D));
+  const size_t lds = decode_fused_lds(a, T);
+  hipExtLaunchKernelGGL(gemma ? decode_mx<true> : decode_mx<false>, dim3(f.R + f.U + f.D), dim3(256), lds, s,
+                        tm.start, tm.stop, 0, a, ra, f);
   return hipGetLastError();
 }
 

@@ -26,20 +26,9 @@
 // PrefillRunner.assignments (PrefillRunner.swift:224-246).
 #include "hh_common.hpp"
 #include "hh_select.hpp"
+#include "hh_logit.hpp"
 
 namespace hh {
-
-__device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-
-__device__ __forceinline__ double wave_max_f64(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o));
-  return v;
-}
 
 // Stable token→expert permutation of the whole batch by one workgroup of NW waves; `idx` is
 // the top-k table [T][K] (global or LDS).
@@ -131,9 +120,6 @@ __device__ __forceinline__ void dispatch_batch(const RouteArgs &a, const int32_t
 constexpr int RT_TOK = 16;          // tokens per route workgroup
 constexpr int RT_MAXCAND = 64;      // exact-recompute candidates handled per pass
 
-__device__ __forceinline__ float bf_lo(uint32_t v) { return bf16_bits_to_f32(v & 0xFFFF); }
-__device__ __forceinline__ float bf_hi(uint32_t v) { return bf16_bits_to_f32(v >> 16); }
-
 // Projection input of the router from 8 columns of a token row (xv) and of the GEMMA scale
 // (sv): GEMMA uses u = x·scale split exactly into bf16 hi + lo (x·scale has at most 16
 // significant bits); the other routers use x itself (lo = 0).
@@ -153,51 +139,6 @@ __device__ __forceinline__ void router_operand(bool gemma, const u32x4 &xv, cons
     hi[k] = h0 | (h1 << 16);
     lo[k] = l0 | (l1 << 16);
   }
-}
-
-// Exact (fp64) router logit of expert e for token row xr, in the oracle's arithmetic: one wave.
-// A bf16·bf16 product is exact in fp32, so each term is formed in fp32 and added in fp64:
-// the same value as an fp64 fma. GEMMA: Σ (((x·s)·scale)·root)·w in fp64 with
-// s = (Σx²/H + eps)^-½ passed in `norm`. Each lane issues the loads of four 512-column steps
-// before their products and keeps one accumulator per step, so a dot costs about one memory
-// latency and a short dependency chain.
-template <bool gemma>
-__device__ __forceinline__ double exact_logit(const RouteArgs &a, const uint16_t *xr,
-                                              const uint16_t *wrow, double norm, double root) {
-  const int lane = threadIdx.x & 63, H = a.hidden;
-  double acc[4] = {0.0, 0.0, 0.0, 0.0};
-  for (int base = 0; base < H; base += 2048) {
-    u32x4 xv[4], wv[4], sv[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      // Loads are unconditional (clamped into the row) and masked afterwards: a load under a
-      // lane-dependent branch would be waited for before the next one is issued.
-      const int h = base + lane * 8 + 512 * u;
-      const int hc = min(h, H - 8);
-      const bool ok = h < H;
-      xv[u] = *(const u32x4 *)(xr + hc);
-      wv[u] = *(const u32x4 *)(wrow + hc);
-      sv[u] = gemma ? *(const u32x4 *)(a.router_scale + hc) : u32x4{0u, 0u, 0u, 0u};
-      if (!ok) wv[u] = u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int sh = (k & 1) * 16;
-        const float xf = bf16_bits_to_f32((xv[u][k >> 1] >> sh) & 0xFFFF);
-        const float wf = bf16_bits_to_f32((wv[u][k >> 1] >> sh) & 0xFFFF);
-        if constexpr (gemma) {
-          const double xd = (((double)xf * norm) *
-                             (double)bf16_bits_to_f32((sv[u][k >> 1] >> sh) & 0xFFFF)) * root;
-          acc[u] = fma(xd, (double)wf, acc[u]);
-        } else {
-          acc[u] += (double)(xf * wf);
-        }
-      }
-    }
-  }
-  return wave_sum_f64((acc[0] + acc[1]) + (acc[2] + acc[3]));
 }
 
 // Screening logits of a 16-token × 16-expert tile over the 128-column chunks c ≡ kq (mod nk):
@@ -474,40 +415,7 @@ __global__ __launch_bounds__(256) void logits_small_kernel(RouteArgs a) {
   }
   const int t = p / E1, e = p - t * E1;
   if (e == E && !a.shared_gate) return;
-  double v;
-  if (e < E) {
-    const uint16_t *xr = a.xr + (size_t)t * H;
-    double norm = 1.0, root = 1.0;
-    if constexpr (gemma) {
-      double xx = 0.0;
-      for (int base = 0; base < H; base += 2048) {
-        u32x4 xv[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int h = base + lane * 8 + 512 * u;
-          xv[u] = *(const u32x4 *)(xr + min(h, H - 8));
-          if (h >= H) xv[u] = u32x4{0u, 0u, 0u, 0u};
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          double px = 0.0;
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            const float xf = bf16_bits_to_f32((xv[u][k >> 1] >> ((k & 1) * 16)) & 0xFFFF);
-            px += (double)(xf * xf);
-          }
-          xx += px;
-        }
-      }
-      xx = wave_sum_f64(xx);
-      norm = pow(xx / (double)H + (double)a.eps, -0.5);
-      root = pow((double)H, -0.5);
-    }
-    v = exact_logit<gemma>(a, xr, a.router_w + (size_t)e * H, norm, root);
-    if (a.router_b) v += (double)bf16_bits_to_f32(a.router_b[e]);
-  } else {
-    v = exact_logit<false>(a, a.x + (size_t)t * H, a.shared_gate, 1.0, 1.0);
-  }
+  const double v = pair_logit<gemma>(a, t, e);
   if (lane == 0) a.lg64[(size_t)t * E1 + e] = v;
 }
 

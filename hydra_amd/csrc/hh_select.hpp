@@ -138,20 +138,20 @@ __device__ __forceinline__ TopK topk_rank64(const double *lg, int E, int K, doub
   return tk;
 }
 
-// Weights of one token's selection (whole wave; lane r < K handles rank r): tk holds the fp64
-// logits in rank order. Writes topk_idx/topk_w/slot_w (and logits, shared_w when given).
-__device__ __forceinline__ void finish_token(const RouteArgs &a, int t, const TopK &tk, double sg_logit) {
+// Routing weight of rank `lane` (lanes ≥ K: 0) of one token's selection (whole wave): tk holds
+// the fp64 logits in rank order; `e` returns the lane's expert.
+// TOPK_SOFTMAX: softmax over the k selected logits (ReferenceOps.swift:178-182).
+// SOFTMAX_TOPK_RENORM and GEMMA: softmax over all experts, renormalised over the k
+// (QwenReferenceOps.swift:159-179, Gemma4ReferenceOps.swift:146-155); the full-softmax
+// denominator cancels, leaving the same softmax of the k selected logits. The sum runs in rank
+// order.
+__device__ __forceinline__ double token_weight(const RouteArgs &a, const TopK &tk, double &v, int &e) {
   const int K = a.top_k, lane = threadIdx.x & 63;
-  double v = -INFINITY;
-  int e = 0;
+  v = -INFINITY;
+  e = 0;
 #pragma unroll
   for (int r = 0; r < kMaxTopK; ++r)
     if (lane == r) { v = tk.v[r]; e = tk.i[r]; }
-  // TOPK_SOFTMAX: softmax over the k selected logits (ReferenceOps.swift:178-182).
-  // SOFTMAX_TOPK_RENORM and GEMMA: softmax over all experts, renormalised over the k
-  // (QwenReferenceOps.swift:159-179, Gemma4ReferenceOps.swift:146-155); the full-softmax
-  // denominator cancels, leaving the same softmax of the k selected logits. The sum runs in
-  // rank order.
   double w = lane < K ? exp(v - tk.v[0]) : 0.0;
   double total = 0.0;
 #pragma unroll
@@ -160,8 +160,18 @@ __device__ __forceinline__ void finish_token(const RouteArgs &a, int t, const To
     if (r < K) total += wr;
   }
   w /= total;
+  if (lane < K && a.router == R_GEMMA) w *= (double)bf16_bits_to_f32(a.router_pes[e]);
+  return lane < K ? w : 0.0;
+}
+
+// Weights of one token's selection (whole wave; lane r < K handles rank r). Writes
+// topk_idx/topk_w/slot_w (and logits, shared_w when given).
+__device__ __forceinline__ void finish_token(const RouteArgs &a, int t, const TopK &tk, double sg_logit) {
+  const int K = a.top_k, lane = threadIdx.x & 63;
+  double v;
+  int e;
+  const double w = token_weight(a, tk, v, e);
   if (lane < K) {
-    if (a.router == R_GEMMA) w *= (double)bf16_bits_to_f32(a.router_pes[e]);
     a.topk_idx[(size_t)t * K + lane] = e;
     if (a.topk_w) a.topk_w[(size_t)t * K + lane] = (float)w;
     a.slot_w[(size_t)t * a.slots + lane] = (float)w;
