@@ -40,6 +40,7 @@ struct hh_ctx {
   // flag values; `epoch` is the value of the last call.
   uint32_t *flags = nullptr;
   uint32_t epoch = 0;
+  int decode_fused = -1;   // 1 on, 0 off, -1 the environment's choice
   int device = 0;
   hipStream_t stream = nullptr;
   uint8_t *arena = nullptr;
@@ -167,11 +168,12 @@ int ensure_flags(hh_ctx *ctx) {
 
 // Whether a decode call takes the fused kernel: HH_DECODE_FUSED=1 in the environment turns it
 // on (it is not yet faster than the three-launch decode).
-bool use_fused(const hh_moe_desc &d, int T) {
-  static const bool enabled = [] {
+bool use_fused(const hh_ctx *ctx, const hh_moe_desc &d, int T) {
+  static const bool env_on = [] {
     const char *v = std::getenv("HH_DECODE_FUSED");
     return v && v[0] == '1';
   }();
+  const bool enabled = ctx->decode_fused < 0 ? env_on : ctx->decode_fused != 0;
   return enabled && d.quant == HH_QUANT_MXFP4 && T <= kSmallT &&
          hh::decode_fused_fits(d.hidden, d.intermediate, d.experts, d.top_k, d.shared_intermediate) &&
          sizeof(uint32_t) * (size_t)hh::decode_fused_flags(kSmallT, d.experts, d.top_k, d.intermediate) <= kFlagBytes;
@@ -332,6 +334,13 @@ int hh_ctx_profile_read(hh_ctx *ctx, double *phase_ms, int64_t *calls) {
   return HH_OK;
 }
 
+int hh_ctx_decode_fused(hh_ctx *ctx, int32_t enable) {
+  if (!ctx) return fail(HH_EINVAL, "ctx is NULL");
+  if (enable < -1 || enable > 1) return fail(HH_EINVAL, "enable must be -1, 0 or 1");
+  ctx->decode_fused = enable;
+  return HH_OK;
+}
+
 int hh_desc_check(const hh_moe_desc *desc) { return check_desc(desc); }
 
 int hh_expert_blob_layout(const hh_moe_desc *d, int32_t inter, hh_blob_layout *out) {
@@ -457,7 +466,7 @@ int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
   g.hs = base + s.hs;
   g.hld = s.hld;
 
-  if (use_fused(*d, T)) {
+  if (use_fused(ctx, *d, T)) {
     // Decode in one launch (decode_mx): logits and h terms in the arena, flags in the
     // context's flag buffer.
     if ((rc = ensure_flags(ctx))) return rc;

@@ -1422,6 +1422,12 @@ __global__ __launch_bounds__(256, 2) void decode_mx(GemmArgs a, RouteArgs ra, Fu
       ATile<Q_MXFP4_W> aw[NM] = {tile_of<PH_DOWN, Q_MXFP4_W>(blob, grp, rb, false, I, l16)};
       AStream<Q_MXFP4_W, NM, DA> as(0, 1, nch);
       as.fill(aw, nch, g, I);
+      float db[4] = {0.f, 0.f, 0.f, 0.f};
+      if (a.expert_bias && l16 == 0) {
+        const uint16_t *bias = (const uint16_t *)(blob + grp.off[5]);
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) db[ii] = bf16_bits_to_f32(bias[rb + 4 * g + ii]);
+      }
       // The h terms of this slot exist once every gate-up item of its expert is done.
       const int u = plan.index_of(e);
       const bool ok = wave_wait(f.flags + f.R + u * rtr, rtr, f.epoch, deadline);
@@ -1451,12 +1457,6 @@ __global__ __launch_bounds__(256, 2) void decode_mx(GemmArgs a, RouteArgs ra, Fu
           aw, nch, gi, I, [&](int c) { return mx_ops<NTH>(my_lds, RSH, a.hld, my_sc, nsb, c, gi); },
           [&](const Fmt<Q_MXFP4_W>::A (&w)[NM], int c, const MxOps<NTH> &o) { chunk_mx1<NTH>(acc, w[0].w, o, c, gi, I); });
       if (l16 == 0) {
-        float db[4] = {0.f, 0.f, 0.f, 0.f};
-        if (a.expert_bias) {
-          const uint16_t *bias = (const uint16_t *)(blob + grp.off[5]);
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) db[ii] = bf16_bits_to_f32(bias[rb + 4 * g + ii]);
-        }
         const float w = s_w[t * K + r];
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii) s_o[r][4 * g + ii] = w * (acc[ii] + db[ii]);
@@ -2191,8 +2191,11 @@ hipError_t launch_decode_fused(bool gemma, GemmArgs a, const RouteArgs &ra, Fuse
   const int nup = std::min(a.experts, T * a.top_k) * (a.grp[0].inter / UP_ROWS);
   a.row_tiles = a.hidden / 16;
   f.R = (T * (a.experts + 1) + 3) / 4;
+  // Every gate-up item has its own workgroup: every down item needs all items of its experts, so
+  // a second round of items would hold up the whole layer. Down workgroups beyond the resident
+  // capacity start as earlier ones finish.
+  f.U = std::max(1, nup);
   f.D = std::min(a.row_tiles * T, ncu);
-  f.U = std::max(1, std::min(nup, 2 * ncu - f.R - f.D));
   const size_t lds = decode_fused_lds(a, T);
   hipExtLaunchKernelGGL(gemma ? decode_mx<true> : decode_mx<false>, dim3(f.R + f.U + f.D), dim3(256), lds, s,
                         tm.start, tm.stop, 0, a, ra, f);

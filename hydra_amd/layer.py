@@ -41,6 +41,10 @@ class Context:
         d = desc_c(desc)
         check(lib().hh_ctx_reserve(self.handle, C.byref(d), max_tokens))
 
+    def decode_fused(self, enable: int):
+        """1: MXFP4 decode calls in one fused launch, 0: three launches, -1: the default."""
+        check(lib().hh_ctx_decode_fused(self.handle, int(enable)))
+
     def profile(self, enable: bool = True):
         check(lib().hh_ctx_profile(self.handle, 1 if enable else 0))
 

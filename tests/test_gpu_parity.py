@@ -285,6 +285,39 @@ def test_layer_is_deterministic_and_order_independent(torch_dev, ctx):
 
 # ---- real shapes ----------------------------------------------------------------------------
 
+FUSED_CASES = {
+    "mxfp4": (TINY["mxfp4"], [5, 1, 8, 3, 16, 13, 5, 2]),
+    "mxfp4-ragged": (TINY["mxfp4-ragged"], [3, 16, 1, 7]),
+    "gpt-oss-20b": (F.GPT_OSS_20B, [1, 4, 16, 2, 8, 1]),
+    "gpt-oss-120b": (F.GPT_OSS_120B, [1, 8, 3]),
+}
+
+
+@pytest.mark.parametrize("name", list(FUSED_CASES))
+def test_fused_decode_equals_three_launch_decode(torch_dev, ctx, name):
+    """The one-launch decode (hh_ctx_decode_fused) against the three-launch decode, bit for bit
+    (outputs, top-k indices and weights), over a sequence of batch sizes. The two paths
+    alternate on one context with new tokens at every step, so a fused call that read data left
+    in the scratch by an earlier call (another batch size, other tokens) would show."""
+    from hydra_amd.layer import MoELayer
+    desc, Ts = FUSED_CASES[name]
+    say(f"fused decode {name}")
+    L = MoELayer(synth.make_layer(desc, seed=51), ctx)
+    try:
+        for i, T in enumerate(Ts):
+            x = synth.make_tokens(desc.hidden, T, seed=60 + i)
+            ctx.decode_fused(0)
+            ya, ia, wa = (v.cpu().numpy() for v in L.forward(x))
+            ctx.decode_fused(1)
+            yb, ib, wb = (v.cpu().numpy() for v in L.forward(x))
+            assert np.array_equal(ia, ib), (name, T)
+            assert np.array_equal(wa.view(np.uint32), wb.view(np.uint32)), (name, T)
+            assert not np.isnan(yb).any(), (name, T)
+            assert np.array_equal(ya.view(np.uint32), yb.view(np.uint32)), (name, T)
+    finally:
+        ctx.decode_fused(-1)
+
+
 FULL = {
     "gpt-oss-20b": (F.GPT_OSS_20B, None, [1, 2, 4, 8, 16]),
     "gpt-oss-120b-zipf": (F.GPT_OSS_120B, 1.1, [512]),
