@@ -128,14 +128,23 @@ class Workload:
         self.torch.cuda.empty_cache()
 
 
-def measure_decode(wl, T, steps, warmup):
+def measure_decode(wl, T, steps, warmup, fused=False):
+    """Decode at T tokens: three launches (router logits; gate-up, selecting the top-k itself;
+    down with the rank-ordered combine), or with `fused` the one-launch kernel
+    (hh_ctx_decode_fused), whose profile records the whole layer as the route phase."""
     desc = wl.desc
+    wl.ctx.decode_fused(1 if fused else 0)
     wl.prepare(T, bank=64)
     sec = wl.run(steps, warmup)
     phases = wl.profiled(min(steps, 200))
     U = wl.unique_experts()
     up_b = U * up_bytes(desc) + T * desc.hidden * 2
     layer_b = U * F.streamed_expert_bytes(desc) + desc.experts * desc.hidden * 2
+    wl.ctx.decode_fused(-1)
+    if fused:
+        return {"T": T, "tokens_per_s": T / sec, "ms_per_step": sec * 1e3, "unique_experts": U,
+                "kernel_ms": phases[0], "layer_GBps": layer_b / sec / 1e9,
+                "layer_hbm_frac": layer_b / sec / 1e9 / HBM_PEAK_GBS}
     return {
         "T": T, "tokens_per_s": T / sec, "ms_per_step": sec * 1e3,
         "unique_experts": U, "phase_ms": dict(zip(["route", "gate_up", "down", "combine"], phases)),
@@ -189,8 +198,11 @@ def cpu_baseline(seconds=10.0):
                       f"single-thread T=1: {single:.2f} tokens/s"}
 
 
+TRAFFIC = "profiles/traffic_up_small_mx_gptoss20b_T1.json"
+
+
 def load_traffic():
-    p = os.path.join(ROOT, "profiles", "traffic_gate_up_gptoss20b_T1.json")
+    p = os.path.join(ROOT, TRAFFIC)
     if os.path.exists(p):
         with open(p) as f:
             return json.load(f)
@@ -231,13 +243,17 @@ def main():
     from hydra_amd._lib import lib
     lib()  # fail loudly if the HIP library is missing
 
-    decode = {}
+    decode, fused = {}, {}
     if not args.only_prefill:
         wl = Workload(torch, F.GPT_OSS_20B, copies=args.copies)
         for T in ([1] if args.only_t1 else [1, 2, 4, 8]):
             log(f"decode T={T}")
             steps = args.steps if T == 1 else max(100, args.steps // 4)
             decode[T] = measure_decode(wl, T, steps, args.warmup if T == 1 else 10)
+        if not args.only_t1:
+            for T in [1, 2, 4, 8]:
+                log(f"decode T={T}, one launch")
+                fused[T] = measure_decode(wl, T, max(100, args.steps // 4), 10, fused=True)
         wl.close()
     prefill = {}
     if not args.no_prefill and not args.only_t1:
@@ -271,17 +287,19 @@ def main():
                    "weights": "mxfp4 e2m1 + e8m0/32", "layer_copies": args.copies},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": "expert_gemm gate-up (MXFP4, 16-token tile)",
+                     "kernel": "up_small_mx<24, true>: decode gate-up (MXFP4 weights on the "
+                               "scaled MFMA, top-k selected in every workgroup)",
                      "bytes_per_launch": d1["up_bytes_per_launch"],
                      "avg_launch_ms": d1["phase_ms"]["gate_up"]},
         "cpu_baseline": cpu,
         "decode": {str(T): v for T, v in decode.items()},
+        "decode_one_launch": {str(T): v for T, v in fused.items()},
         "prefill_gpt_oss_120b_zipf": {str(T): v for T, v in prefill.items()},
     }
     tr = load_traffic()
     if tr is not None:
         out["roofline"]["traffic"] = tr.get("bytes_per_launch")
-        out["roofline"]["traffic_source"] = "profiles/traffic_gate_up_gptoss20b_T1.json"
+        out["roofline"]["traffic_source"] = TRAFFIC
     print(json.dumps(out))
 
 
