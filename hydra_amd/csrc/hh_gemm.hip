@@ -477,14 +477,16 @@ __device__ __forceinline__ f32x4 down_value(const GemmArgs &a, const uint8_t *bl
   return o;
 }
 
-// XCD-aware block order: hardware places block b on XCD b % 8; give each XCD a contiguous range
-// of logical ids so that neighbouring logical blocks (which share weights or inputs) share an L2.
-__device__ __forceinline__ int xcd_logical(int b, int nblk) {
-  const int xcd = b & 7, slot = b >> 3;
-  const int per = (nblk + 7) >> 3;
-  int rem = nblk & 7;
-  if (rem == 0) rem = 8;
-  return (xcd < rem ? xcd * per : rem * per + (xcd - rem) * (per - 1)) + slot;
+// Prefill block order: hardware places block b on XCD b % 8. XCD x takes the row tiles
+// [x·rtx, x·rtx + rtx) (rtx = ⌈row_tiles / 8⌉) and walks the work items in order, an item's row
+// tiles consecutively: the item's activation operand is fetched about once per XCD and reused
+// from its L2 by the item's row tiles, and an expert's weight rows by its consecutive items.
+// (Row-tile-major order re-read every item's operand from HBM once per row tile.)
+__device__ __forceinline__ void prefill_tile(int b, int row_tiles, int &rt, int &wi) {
+  const int rtx = (row_tiles + 7) >> 3;
+  const int x = b & 7, j = b >> 3;
+  wi = j / rtx;
+  rt = x * rtx + (j - wi * rtx);
 }
 
 // Copies vectors v ∈ [base, base + threads·NB) ∩ [0, n) with `threads` threads (thread index
@@ -1489,9 +1491,8 @@ __global__ __launch_bounds__(256) void prefill_gemm(GemmArgs a) {
   constexpr int BPT = (BVEC + 255) / 256;             // per thread
   __shared__ __align__(16) u32x4 s_bv[2][BVEC];
 
-  const int logical = xcd_logical(blockIdx.x, gridDim.x);
-  const int rt = logical / a.max_work;
-  const int wi = logical - rt * a.max_work;
+  int rt, wi;
+  prefill_tile(blockIdx.x, a.row_tiles, rt, wi);
   if (rt >= a.row_tiles || wi >= *a.n_work) return;
 
   const int4 item = a.work[wi];
@@ -1638,9 +1639,8 @@ __global__ __launch_bounds__(256) void prefill_mx(GemmArgs a) {
   __shared__ __align__(16) u32x4 s_bq[2][BVEC];
   __shared__ uint32_t s_bs[2][NSC];
 
-  const int logical = xcd_logical(blockIdx.x, gridDim.x);
-  const int rt = logical / a.max_work;
-  const int wi = logical - rt * a.max_work;
+  int rt, wi;
+  prefill_tile(blockIdx.x, a.row_tiles, rt, wi);
   if (rt >= a.row_tiles || wi >= *a.n_work) return;
 
   const int4 item = a.work[wi];
@@ -1817,9 +1817,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   __shared__ float sBias[MR];                       // bias of the workgroup's weight rows
   extern __shared__ __align__(16) uint8_t sAS[];   // [MR][K/32] weight scales
 
-  const int logical = xcd_logical(blockIdx.x, gridDim.x);
-  const int rt = logical / a.max_work;
-  const int wi = logical - rt * a.max_work;
+  int rt, wi;
+  prefill_tile(blockIdx.x, a.row_tiles, rt, wi);
   if (rt >= a.row_tiles || wi >= *a.n_work) return;
   const int4 item = a.work[wi];
   const int e = item.x, pos0 = item.y, nitem = item.z;
@@ -2083,7 +2082,8 @@ static GemmKernel gemm_kernel(int phase, int quant, int nt) {
 }
 
 hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStream_t s, Timing tm) {
-  const unsigned blocks = (unsigned)a.row_tiles * (unsigned)a.max_work;
+  // prefill_tile: 8 XCDs × ⌈row_tiles / 8⌉ row tiles × work items.
+  const unsigned blocks = 8u * (unsigned)((a.row_tiles + 7) / 8) * (unsigned)a.max_work;
   if (blocks == 0) return hipSuccess;
   const bool mx = quant == Q_MXFP4;
   // MXFP4: 8 waves, the weight rows' scales (128 rows × K/32 bytes) in dynamic LDS.
