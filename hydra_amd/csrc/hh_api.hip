@@ -86,9 +86,9 @@ struct Scratch {
 constexpr int kSmallT = 16;  // batches up to this size take the decode kernels
 
 int token_tile_nt(const hh_moe_desc &d, int T) {
-  // Prefill kernel token tiles of 16: MXFP4 passes of 32 or 64 tokens, the other formats 16 or
-  // 32, the larger once batches are big enough for experts to fill them.
-  if (d.quant == HH_QUANT_MXFP4) return (T >= 128) ? 4 : 2;
+  // Prefill kernel token tiles of 16: MXFP4 work items of 32 tokens (prefill_mx3's task), the
+  // other formats 16 or 32, the larger once batches are big enough for experts to fill them.
+  if (d.quant == HH_QUANT_MXFP4) return 2;
   return (T >= 64) ? 2 : 1;
 }
 

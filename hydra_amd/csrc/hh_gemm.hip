@@ -2027,6 +2027,328 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *slot_out, int
   }
 }
 
+// ---- prefill, MXFP4: persistent pipeline with direct-to-LDS loads -----------------------------
+// One 512-thread workgroup per compute unit takes tasks τ = blockIdx.x, + gridDim.x, ... in
+// prefill_tile order (a task: 128 weight rows × one work item of ≤ 32 tokens). Waves 4-7 load,
+// waves 0-3 multiply (2×2: 64 rows × 16 tokens each). The loaders stream every task's 128-column
+// chunks (weight blocks, the rows' block scales, the tokens' fp8 terms and their scales) straight
+// into a ring of S LDS stages with global_load_lds, S−1 chunks ahead of the MFMA waves and across
+// task boundaries, so neither a chunk's memory latency nor a task's start is waited for. Each
+// loader wave issues at least L loads per chunk, so "the oldest chunk has landed" is the fixed wait
+// vmcnt((S−2)·L); the task switches' extra loads (work item and slot ids, fetched into LDS one and
+// two tasks ahead) only make that wait stricter. The arithmetic per output element is
+// prefill_mx2's: one chain over the chunks, the terms in order.
+template <int PH> struct Mx3 {
+  static constexpr int NTERM = PH == PH_UP ? NTX : NTH;
+  static constexpr int NTOK = 32, MR = 128;
+  static constexpr int B_INS = NTERM * NTOK / 8;            // 1 KB operand loads per chunk
+  static constexpr int BPW = B_INS / 4;                     // per loader wave
+  static constexpr int BS_DW = NTERM * NTOK;                // operand scale dwords per chunk
+  static constexpr int L = 2 + BPW + 1 + 1;                 // loads per loader wave per chunk
+  static constexpr int OFF_B = 8192;                        // after 8 weight tiles of 1 KB
+  static constexpr int OFF_BS = OFF_B + B_INS * 1024;
+  static constexpr int OFF_SC = OFF_BS + 256 * ((BS_DW + 63) / 64);
+  static constexpr int STAGE = OFF_SC + 512;                // + 128 rows × 4 block-scale bytes
+  static constexpr int S = PH == PH_UP ? 8 : 7;
+  static constexpr int OFF_INFO = S * STAGE;                // [3][64] work item (4 dwords used)
+  static constexpr int OFF_ORDER = OFF_INFO + 3 * 256;      // [3][64] slot ids (32 used)
+  static constexpr int OFF_JUNK = OFF_ORDER + 3 * 256;      // sink of loads no stage needs
+  static constexpr int LDS = OFF_JUNK + 256;
+  static_assert(B_INS % 4 == 0 && BS_DW <= 256 && (S - 2) * L <= 63, "loader layout");
+};
+
+// Workgroup barrier without __syncthreads' release fence: the fence would make every wave wait for
+// all of its direct-to-LDS loads (vmcnt(0)) before the barrier; the pipeline orders LDS itself
+// with explicit waits. A compiler memory barrier keeps LDS accesses on their side.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+__device__ __forceinline__ void lds_load16(const void *g, uint8_t *l) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)l, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_load4(const void *g, uint8_t *l) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)l, 4, 0, 0);
+}
+
+// Task ids of one workgroup: τ = b, b + G, ... below 8·⌈RT/8⌉·n_work, skipping row tiles ≥ RT.
+struct Mx3Tasks {
+  int b, G, RT, lim;
+  __device__ __forceinline__ int first() const { return fix(b); }
+  __device__ __forceinline__ int next(int tau) const { return fix(tau + G); }
+  __device__ __forceinline__ int fix(int tau) const {
+    for (; tau < lim; tau += G) {
+      int rt, wi;
+      prefill_tile(tau, RT, rt, wi);
+      if (rt < RT) return tau;
+    }
+    return lim;
+  }
+};
+
+template <int PH>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mx3(GemmArgs a) {
+  using C = Mx3<PH>;
+  constexpr int NTERM = C::NTERM, NTOK = C::NTOK, S = C::S, L = C::L;
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, l16 = lane & 15;
+  const ExpertGroup &grp = a.grp[0];
+  const int I = grp.inter, H = a.hidden;
+  const int out_dim = PH == PH_UP ? 2 * I : H;
+  const int K = PH == PH_UP ? H : I;
+  const int nch = (K + 127) / 128, nsb = K / 32;
+  const int ld = PH == PH_UP ? a.xld : a.hld;
+  const uint8_t *qbase = PH == PH_UP ? a.xq : a.hq;
+  const uint8_t *sbase = PH == PH_UP ? a.xs : a.hs;
+  const int RT = a.row_tiles, rtx = (RT + 7) >> 3;
+  const int nwork = *a.n_work;
+  const Mx3Tasks tasks{(int)blockIdx.x, (int)gridDim.x, RT, 8 * rtx * nwork};
+  // Number of chunks this workgroup computes.
+  int nsteps = 0;
+  for (int tau = tasks.first(); tau < tasks.lim; tau = tasks.next(tau)) nsteps += nch;
+  if (nsteps == 0) return;
+  uint8_t *info = lds + C::OFF_INFO, *order = lds + C::OFF_ORDER, *junk = lds + C::OFF_JUNK;
+  auto item_of = [&](int slot) { return *(const int4 *)(info + 256 * slot); };
+
+  if (wave >= 4) {
+    // ---- loaders ----
+    const int lw = wave - 4;
+    // Work item (lanes 0-3) and slot ids (lanes 0-31) of a task into its LDS slot (other lanes
+    // repeat valid entries). Every loader wave fetches them (the same values), so each one's own
+    // vmcnt tells it they have landed.
+    auto fetch_info = [&](int tau, int slot) {
+      int rt, wi;
+      prefill_tile(min(tau, tasks.lim - 1), RT, rt, wi);
+      lds_load4((const int *)(a.work + min(wi, nwork - 1)) + min(lane, 3), info + 256 * slot);
+    };
+    auto fetch_order = [&](int slot) {
+      const int4 it = item_of(slot);
+      lds_load4(a.order + it.y + min(lane, it.z - 1), order + 256 * slot);
+    };
+    // Per-task source pointers.
+    const uint8_t *asrc[2], *bsrc[C::BPW], *bssrc, *scsrc;
+    auto start_task = [&](int tau, int slot) {
+      int rt, wi;
+      prefill_tile(tau, RT, rt, wi);
+      const int4 it = item_of(slot);
+      const int r0 = rt * C::MR;
+      const uint8_t *blob = grp.blobs + (size_t)it.x * grp.stride;
+      const uint8_t *wblk = blob + grp.off[PH == PH_UP ? 0 : 3];
+      const uint8_t *wsc = blob + grp.off[PH == PH_UP ? 1 : 4];
+      const int *ord = (const int *)(order + 256 * slot);
+      auto row_of = [&](int n) {
+        const int sl = ord[min(n, it.z - 1)];
+        return PH == PH_UP ? sl / a.slots : sl;
+      };
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int j = 2 * lw + k;   // 16-row tile of the chunk
+        asrc[k] = wblk + (size_t)min(r0 + 16 * j + l16, out_dim - 1) * (K / 2);
+      }
+#pragma unroll
+      for (int k = 0; k < C::BPW; ++k) {
+        const int v = (lw * C::BPW + k) * 64 + lane;
+        const int t = v / (NTOK * 8), sl = v % (NTOK * 8), n = sl >> 3, sg = (sl & 7) ^ (n & 7);
+        bsrc[k] = qbase + ((size_t)row_of(n) * NTERM + t) * ld + 16 * sg;
+      }
+      {
+        const int d = min(lw * 64 + lane, C::BS_DW - 1), t = d / NTOK, n = d % NTOK;
+        bssrc = sbase + ((size_t)row_of(n) * NTERM + t) * (ld / 32);
+      }
+      // Block scales: one row's 4 bytes of a chunk per lane (4-byte loads from 2-byte-aligned
+      // rows are exact; a 2-byte direct-to-LDS load would write a whole dword per lane).
+      scsrc = wsc + (size_t)min(r0 + min(lw, 1) * 64 + lane, out_dim - 1) * nsb;
+    };
+    // Chunk c of the current task into stage st.
+    auto issue = [&](int c, int st) {
+      uint8_t *stg = lds + st * C::STAGE;
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        lds_load16(asrc[k] + 16 * min(4 * c + g, nsb - 1), stg + 1024 * (2 * lw + k));
+#pragma unroll
+      for (int k = 0; k < C::BPW; ++k) lds_load16(bsrc[k] + 128 * c, stg + C::OFF_B + 1024 * (lw * C::BPW + k));
+      lds_load4(bssrc + 4 * c, lw * 64 < C::BS_DW ? stg + C::OFF_BS + 256 * lw : junk);
+      lds_load4(scsrc + 4 * c, lw < 2 ? stg + C::OFF_SC + 256 * lw : junk);
+    };
+    // Prologue: work items of the first two tasks and the first task's slot ids, then the first
+    // S−1 chunks.
+    int tq[3];   // task ids: issuing, next, the one after
+    tq[0] = tasks.first();
+    tq[1] = tasks.next(tq[0]);
+    tq[2] = tasks.next(tq[1]);
+    fetch_info(tq[0], 0);
+    fetch_info(tq[1], 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    fetch_order(0);
+    fetch_order(1);
+    fetch_info(tq[2], 2);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    int slot = 0, lc = 0;
+    start_task(tq[0], 0);
+    int q = 0;   // chunks issued
+    auto issue_next = [&]() {
+      issue(lc, q % S);
+      ++q;
+      if (++lc == nch) {
+        lc = 0;
+        // Next task: its work item and slot ids have landed (fetched ≥ one task ago).
+        tq[0] = tq[1];
+        tq[1] = tq[2];
+        tq[2] = tasks.next(tq[2]);
+        slot = slot == 2 ? 0 : slot + 1;
+        if (tq[0] < tasks.lim) {
+          start_task(tq[0], slot);
+          const int s1 = slot == 2 ? 0 : slot + 1, s2 = s1 == 2 ? 0 : s1 + 1;
+          fetch_order(s1);            // slot ids of the next task (its work item landed)
+          fetch_info(tq[2], s2);      // work item of the task after it
+        }
+      }
+    };
+    // At every barrier the chunk being computed and the next one (whose operands the MFMA waves
+    // read ahead) have landed: after issuing chunk q, wait until at most S−3 chunks' loads are
+    // outstanding.
+    for (int u = 0; u < S - 1 && q < nsteps; ++u) issue_next();
+    if (q >= S - 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"((S - 3) * L) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    for (int step = 0; step < nsteps; ++step) {
+      ring_barrier();
+      if (q < nsteps) {
+        issue_next();
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((S - 3) * L) : "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+    }
+    return;
+  }
+
+  // ---- MFMA waves ----
+  const int wr = wave & 1, wt = wave >> 1;
+  const int n = 16 * wt + l16;   // token of this lane's B column
+  f32x4 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int tau = tasks.first(), slot = 0, c = 0;
+  int eslot = 0, ntok = 0, r0 = 0;
+  float ew = 0.f;
+  uint16_t braw[4][4];   // bias bits of the lane's rows, loaded at the task's start, used at its end
+  auto task_begin = [&]() {
+    int rt, wi;
+    prefill_tile(tau, RT, rt, wi);
+    const int4 it = item_of(slot);
+    r0 = rt * C::MR;
+    ntok = it.z;
+    eslot = ((const int *)(order + 256 * slot))[min(n, ntok - 1)];
+    ew = PH == PH_DOWN ? a.slot_w[eslot] : 0.f;
+    // Unconditional loads (a branch on expert_bias would make the compiler wait for them here).
+    const uint16_t *bp = (const uint16_t *)(grp.blobs + (size_t)it.x * grp.stride + grp.off[PH == PH_UP ? 2 : 5]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) braw[j][ii] = bp[min(r0 + 64 * wr + 16 * j + 4 * g + ii, out_dim - 1)];
+  };
+  // Operands of a chunk, read from its stage one step ahead of its MFMAs (raw: the chunk's masks
+  // are applied at use).
+  struct Ops {
+    u32x4 w[4], blo[NTERM], bhi[NTERM];
+    uint32_t sa[4], bs[NTERM];
+  };
+  auto read_ops = [&](int st) {
+    const uint8_t *stg = lds + st * C::STAGE;
+    Ops o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      o.w[j] = *(const u32x4 *)(stg + 1024 * (4 * wr + j) + 16 * lane);
+      o.sa[j] = stg[C::OFF_SC + 4 * (64 * wr + 16 * j + l16) + g];
+    }
+    const u32x4 *sb = (const u32x4 *)(stg + C::OFF_B);
+#pragma unroll
+    for (int t = 0; t < NTERM; ++t) {
+      o.blo[t] = sb[(t * NTOK + n) * 8 + (g ^ (n & 7))];
+      o.bhi[t] = sb[(t * NTOK + n) * 8 + ((4 + g) ^ (n & 7))];
+      o.bs[t] = (((const uint32_t *)(stg + C::OFF_BS))[t * NTOK + n] >> (8 * g)) & 0xFFu;
+    }
+    return o;
+  };
+  ring_barrier();
+  Ops cur = read_ops(0);
+  for (int step = 0; step < nsteps; ++step) {
+    if (c == 0) task_begin();
+    Ops nxt;
+    if (step + 1 < nsteps) nxt = read_ops((step + 1) % S);
+    {
+      const bool ok = 128 * c + 32 * g < K;
+      const int k0 = 128 * c + 16 * g;
+#pragma unroll
+      for (int t = 0; t < NTERM; ++t) {
+        // Lanes past K take zero weights; their scale byte may be any byte of the blob, so 2^0
+        // (the product is the same signed zero).
+        const u32x4 blo = k0 >= K ? u32x4{0u, 0u, 0u, 0u} : cur.blo[t];
+        const u32x4 bhi = k0 + 64 >= K ? u32x4{0u, 0u, 0u, 0u} : cur.bhi[t];
+        const uint32_t bs = ok ? cur.bs[t] : 127u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[j] = smfma(ok ? cur.w[j] : u32x4{0u, 0u, 0u, 0u}, blo, bhi, ok ? cur.sa[j] : 127u, bs, acc[j]);
+      }
+    }
+    const bool more = step + 1 < nsteps;
+    if (++c < nch) {
+      if (more) ring_barrier();
+      cur = nxt;
+      continue;
+    }
+    // ---- epilogue of the task ----
+    c = 0;
+    const int rw = r0 + 64 * wr;
+    float bias[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) bias[j][ii] = a.expert_bias ? bf16_bits_to_f32(braw[j][ii]) : 0.f;
+    if (rw < out_dim) {
+      if constexpr (PH == PH_UP) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const f32x4 d = acc[j];
+          v[2 * j] = activate(a.act, d[0] + bias[j][0], d[1] + bias[j][1], a.alpha, a.limit);
+          v[2 * j + 1] = activate(a.act, d[2] + bias[j][2], d[3] + bias[j][3], a.alpha, a.limit);
+        }
+        uint32_t hq[NTH][2], sbq[NTH];
+        quant_block<NTH>(v, hq, sbq);
+        if (n < ntok) {
+          const int i0 = rw / 2;
+#pragma unroll
+          for (int t = 0; t < NTH; ++t) {
+            uint8_t *row = a.hq + ((size_t)eslot * NTH + t) * a.hld + i0 + 2 * g;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) *(uint16_t *)(row + 8 * j) = (uint16_t)(hq[t][j >> 1] >> (16 * (j & 1)));
+            if (g == 0) a.hs[((size_t)eslot * NTH + t) * (a.hld / 32) + i0 / 32] = (uint8_t)sbq[t];
+          }
+        }
+      } else {
+        if (n < ntok) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int h0 = rw + 16 * j + 4 * g;
+            f32x4 o;
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) o[ii] = ew * (acc[j][ii] + bias[j][ii]);   // down_value's arithmetic
+            *(f32x4 *)(a.slot_out + (size_t)eslot * H + h0) = o;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    tau = tasks.next(tau);
+    slot = slot == 2 ? 0 : slot + 1;
+    if (more) ring_barrier();
+    cur = nxt;
+  }
+}
+
 // ---- launch table -----------------------------------------------------------------------------
 typedef void (*GemmKernel)(GemmArgs);
 typedef void (*UpSmallKernel)(GemmArgs, RouteArgs);
@@ -2081,7 +2403,33 @@ static GemmKernel gemm_kernel(int phase, int quant, int nt) {
   }
 }
 
+// Whether prefill_mx3 takes a phase: MXFP4 without a shared expert, 32-token work items, and rows
+// of at least S chunks (task switches are prefetched one task ahead inside the chunk ring).
+static bool use_mx3(int phase, const GemmArgs &a, int nt) {
+  if (a.slots != a.top_k || nt != 2) return false;
+  const int K = phase == PH_UP ? a.hidden : a.grp[0].inter;
+  return (K + 127) / 128 >= (phase == PH_UP ? Mx3<PH_UP>::S : Mx3<PH_DOWN>::S);
+}
+
 hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStream_t s, Timing tm) {
+  if (quant == Q_MXFP4 && use_mx3(phase, a, nt)) {
+    static int ncu = 0;
+    if (!ncu) {
+      int dev = 0;
+      (void)hipGetDevice(&dev);
+      if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu < 8) ncu = 256;
+      ncu &= ~7;   // the task order assumes 8 | gridDim
+      for (const void *k : {(const void *)prefill_mx3<PH_UP>, (const void *)prefill_mx3<PH_DOWN>}) {
+        (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        (void)hipGetLastError();
+      }
+    }
+    if (phase == PH_UP)
+      hipExtLaunchKernelGGL(prefill_mx3<PH_UP>, dim3(ncu), dim3(512), Mx3<PH_UP>::LDS, s, tm.start, tm.stop, 0, a);
+    else
+      hipExtLaunchKernelGGL(prefill_mx3<PH_DOWN>, dim3(ncu), dim3(512), Mx3<PH_DOWN>::LDS, s, tm.start, tm.stop, 0, a);
+    return hipGetLastError();
+  }
   // prefill_tile: 8 XCDs × ⌈row_tiles / 8⌉ row tiles × work items.
   const unsigned blocks = 8u * (unsigned)((a.row_tiles + 7) / 8) * (unsigned)a.max_work;
   if (blocks == 0) return hipSuccess;

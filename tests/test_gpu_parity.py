@@ -222,6 +222,10 @@ TINY = {
     "mxfp4-narrow": F.MoEDesc(hidden=192, intermediate=64, experts=4, top_k=2,
                               quant=F.QUANT_MXFP4, activation=F.ACT_SWIGLU_OAI,
                               router=F.ROUTER_TOPK_SOFTMAX, expert_bias=1),
+    # Rows of ≥ 8 chunks in both products: the persistent LDS-ring prefill kernel.
+    "mxfp4-wide": F.MoEDesc(hidden=1024, intermediate=1024, experts=8, top_k=4,
+                            quant=F.QUANT_MXFP4, activation=F.ACT_SWIGLU_OAI,
+                            router=F.ROUTER_TOPK_SOFTMAX, expert_bias=1),
     "mlx4": F.MoEDesc(hidden=256, intermediate=128, experts=8, top_k=3, quant=F.QUANT_MLX4,
                       activation=F.ACT_SILU, router=F.ROUTER_SOFTMAX_TOPK_RENORM,
                       shared_intermediate=192, group_size=64),
