@@ -9,7 +9,8 @@ several resident copies of the layer (> 256 MB Infinity Cache) and over a bank o
 every step streams its experts from HBM as consecutive layers of a model would.
 
 Also reported: decode at T=2, 4, 8; the GPT-OSS-120B-shaped Zipf-skewed chunked prefill at
-T=512 and T=2048; the roofline of the dominant kernel (the gate-up expert
+T=512 and T=2048; the Qwen-shaped MLX 4-bit and 8-bit layers and the
+BF16 GELU layer at T=1 and in chunked prefill; the roofline of the dominant kernel (the gate-up expert
 product) from HIP events on the library's stream; and the fp64 CPU restatement of the
 reference path timed on this host.
 
@@ -163,7 +164,7 @@ def measure_prefill(wl, T, steps, warmup):
     phases = wl.profiled(min(steps, 20))
     U = wl.unique_experts()
     fl = flops_per_token(desc) * T
-    by = U * F.streamed_expert_bytes(desc)
+    by = U * F.streamed_expert_bytes(desc) + shared_bytes(desc)
     t_exp = (phases[1] + phases[2]) * 1e-3
     return {
         "T": T, "tokens_per_s": T / sec, "ms_per_step": sec * 1e3, "unique_experts": U,
@@ -174,6 +175,34 @@ def measure_prefill(wl, T, steps, warmup):
         "expert_GBps": by / t_exp / 1e9,
         "hbm_frac": by / t_exp / 1e9 / HBM_PEAK_GBS,
     }
+
+
+OTHER = [  # (name, desc, copies, prefill T): BASELINE configs[3] (both bit widths) and [4]
+    ("qwen-35b-a3b-mlx4", F.QWEN_35B_A3B_Q4, 2, 1024),
+    ("qwen-35b-a3b-mlx8", F.QWEN_35B_A3B_Q8, 2, 1024),
+    ("gemma-bf16", F.GEMMA_BF16, 2, 2048),
+]
+
+
+def shared_bytes(desc: F.MoEDesc) -> int:
+    """Bytes of the always-on shared expert (Qwen) plus its gate row."""
+    if not desc.shared_intermediate:
+        return 0
+    return F.streamed_expert_bytes(desc, desc.shared_intermediate) + desc.hidden * 2
+
+
+def measure_other(torch, name, desc, copies, T_prefill, steps):
+    """Decode T=1 and one chunked prefill of another format: whole-layer tokens/s, layer GB/s
+    on the bytes touched (distinct routed experts + shared expert + router), expert-product
+    TFLOP/s for the prefill."""
+    log(f"{name}: decode T=1, prefill T={T_prefill}")
+    wl = Workload(torch, desc, copies=copies)
+    d = measure_decode(wl, 1, steps, 20)
+    d["layer_GBps"] += shared_bytes(desc) / (d["ms_per_step"] * 1e-3) / 1e9
+    d["layer_hbm_frac"] = d["layer_GBps"] / HBM_PEAK_GBS
+    p = measure_prefill(wl, T_prefill, 10, 3)
+    wl.close()
+    return {"decode": {"1": d}, "prefill": {str(T_prefill): p}}
 
 
 def cpu_baseline(seconds=10.0):
@@ -218,6 +247,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--only-t1", action="store_true", help="decode T=1 only (for profiling)")
+    ap.add_argument("--no-other", action="store_true", help="skip the MLX and BF16 configs")
+    ap.add_argument("--only-other", default=None,
+                    help="run only the named other config (qwen-35b-a3b-mlx4, ...; for profiling)")
     ap.add_argument("--only-prefill", action="store_true", help="prefill only (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 256 MiB device-to-device copy and exit (HBM counter calibration)")
@@ -243,6 +275,10 @@ def main():
     from hydra_amd._lib import lib
     lib()  # fail loudly if the HIP library is missing
 
+    if args.only_other:
+        name, desc, copies, Tp = next(o for o in OTHER if o[0] == args.only_other)
+        print(json.dumps({name: measure_other(torch, name, desc, copies, Tp, args.steps)}))
+        return
     decode, fused = {}, {}
     if not args.only_prefill:
         wl = Workload(torch, F.GPT_OSS_20B, copies=args.copies)
@@ -262,6 +298,10 @@ def main():
             log(f"prefill T={T}")
             prefill[T] = measure_prefill(wl, T, 20 if T == 512 else 10, 3)
         wl.close()
+    other = {}
+    if not (args.no_other or args.only_t1 or args.only_prefill):
+        for name, desc, copies, Tp in OTHER:
+            other[name] = measure_other(torch, name, desc, copies, Tp, max(100, args.steps // 4))
     cpu = None if args.no_cpu else cpu_baseline()
     if args.only_prefill:
         print(json.dumps({"prefill_gpt_oss_120b_zipf": {str(T): v for T, v in prefill.items()}}))
@@ -295,6 +335,7 @@ def main():
         "decode": {str(T): v for T, v in decode.items()},
         "decode_one_launch": {str(T): v for T, v in fused.items()},
         "prefill_gpt_oss_120b_zipf": {str(T): v for T, v in prefill.items()},
+        "other_configs": other,
     }
     tr = load_traffic()
     if tr is not None:

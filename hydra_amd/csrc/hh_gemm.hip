@@ -127,27 +127,28 @@ template <> struct Fmt<Q_MXFP4_W> {
   __device__ static bool lane_valid(int c, int g, int K) { return 128 * c + 32 * g < K; }
 };
 
-// ---- BF16: 128-column chunks, 64 bytes per lane ---------------------------------------------
+// ---- BF16: 128-column chunks; step v (32 columns) of a chunk holds, in lane (g, l16), row l16's
+// columns 128c + 32v + 8g .. +7: a lane's four 16-byte pieces lie 64 bytes apart, so a load of
+// one step reads 64 contiguous bytes of each of 16 rows. K is a multiple of 64: a step lies wholly
+// inside or wholly past K, and steps past K are skipped (uniformly) by every kernel.
 template <> struct Fmt<Q_BF16> {
-  static constexpr int CHUNK = 128, NB = 4;
+  static constexpr int CHUNK = 128, NB = 4, VS = 32;   // VS: B columns between steps
   struct A { u32x4 w[4]; };
   struct Row { const uint8_t *w; };
   __device__ static Row row(const uint8_t *base, int r, int K) { return {base + (size_t)r * K * 2}; }
   __device__ static void load(A &a, const Row &rw, int c, int g, int K) {
-    int col = min(128 * c + 32 * g, K - 32);
-    const u32x4 *p = (const u32x4 *)(rw.w + col * 2);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) a.w[s] = p[s];
+    for (int s = 0; s < 4; ++s) a.w[s] = *(const u32x4 *)(rw.w + 2 * min(128 * c + 32 * s + 8 * g, K - 8));
   }
-  __device__ static int bcol(int c, int g, int K) { return min(128 * c + 32 * g, K - 32); }
-  __device__ static bool lane_valid(int c, int g, int K) { return 128 * c + 32 * g < K; }
+  __device__ static int bcol(int c, int g, int) { return 128 * c + 8 * g; }
+  __device__ static bool step_ok(int c, int v, int K) { return 128 * c + 32 * v < K; }
 };
 
 // ---- MLX affine: 64-column chunks (one group) ------------------------------------------------
 // The lane's stage also carries its row's group scale and bias (bf16 pair); the D rows' values
 // are fetched from the lanes of those rows by shuffle (affine_sb).
 template <int BITS> struct FmtMLX {
-  static constexpr int CHUNK = 64, NB = 2;
+  static constexpr int CHUNK = 64, NB = 2, VS = 8;
   struct A { uint32_t w[BITS / 2]; uint32_t sb; };  // 4-bit: 2 words (16 values); 8-bit: 4 words
   struct Row { const uint8_t *w; const uint16_t *sc, *bi; };
   __device__ static Row row(const uint8_t *words, const uint8_t *scales, const uint8_t *biases,
@@ -250,7 +251,23 @@ template <int FMT, int NM, int NT, int NH, class BV>
 __device__ __forceinline__ void chunk_mfma(f32x4 (&acc)[NM][NT], const typename Fmt<FMT>::A (&w)[NM],
                                            const ATile<FMT> (&at)[NM], BV bv, int c, int g, int K) {
   using F = Fmt<FMT>;
-  if constexpr (!is_mlx<FMT>()) {
+  if constexpr (FMT == Q_BF16) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      if (!F::step_ok(c, v, K)) break;
+      u32x4 b[NT][NH];
+#pragma unroll
+      for (int st = 0; st < NT; ++st)
+#pragma unroll
+        for (int hh = 0; hh < NH; ++hh) b[st][hh] = bv(st, hh, v);
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int st = 0; st < NT; ++st)
+#pragma unroll
+          for (int hh = 0; hh < NH; ++hh) acc[m][st] = mfma(as_bf16x8(w[m].w[v]), as_bf16x8(b[st][hh]), acc[m][st]);
+    }
+  } else if constexpr (!is_mlx<FMT>()) {
     const bool ok = F::lane_valid(c, g, K);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -262,8 +279,7 @@ __device__ __forceinline__ void chunk_mfma(f32x4 (&acc)[NM][NT], const typename 
 #pragma unroll
       for (int m = 0; m < NM; ++m) {
         bf16x8 av;
-        if constexpr (FMT == Q_MXFP4) av = mxfp4_to_bf16(ok ? w[m].w[v] : 0u, e8m0_to_f32(w[m].s));
-        else av = as_bf16x8(ok ? w[m].w[v] : u32x4{0u, 0u, 0u, 0u});
+        av = mxfp4_to_bf16(ok ? w[m].w[v] : 0u, e8m0_to_f32(w[m].s));
 #pragma unroll
         for (int st = 0; st < NT; ++st)
 #pragma unroll
@@ -657,7 +673,7 @@ __global__ __launch_bounds__(512) void up_small(GemmArgs a, RouteArgs ra) {
   f32x4 acc[NM][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
   as.run(at, nch, g, H, [&](const typename Fmt<FMT>::A (&w)[NM], int c) {
     const int col = Fmt<FMT>::bcol(c, g, H);
-    chunk_mfma<FMT, NM, 1, 1>(acc, w, at, [&](int, int, int v) { return *(const u32x4 *)(brow + col + 8 * v); },
+    chunk_mfma<FMT, NM, 1, 1>(acc, w, at, [&](int, int, int v) { return *(const u32x4 *)(brow + col + Fmt<FMT>::VS * v); },
                               c, g, H);
   });
   // Chains and gate/up meet in the (gate, even) wave of each tile.
@@ -1147,7 +1163,7 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
 
   as.run(at, nch, g, I, [&](const typename Fmt<FMT>::A (&w)[NM], int c) {
     const int col = Fmt<FMT>::bcol(c, g, I);
-    auto bv = [&](int, int hh, int v) { return *(const u32x4 *)(sb + hh * ldb + col + 8 * v); };
+    auto bv = [&](int, int hh, int v) { return *(const u32x4 *)(sb + hh * ldb + col + Fmt<FMT>::VS * v); };
     if (KS == 1 && (c & 1)) chunk_mfma<FMT, NM, 1, 2>(acc[1], w, at, bv, c, g, I);
     else chunk_mfma<FMT, NM, 1, 2>(acc[0], w, at, bv, c, g, I);
   });
@@ -1471,318 +1487,6 @@ __global__ __launch_bounds__(256, 2) void decode_mx(GemmArgs a, RouteArgs ra, Fu
       a.y[(size_t)t * H + rb + tid] = s_bad ? __builtin_nanf("") : y;
     }
     __syncthreads();   // the next item rewrites the LDS rows and s_o
-  }
-}
-
-// ---- prefill: B chunks staged once per workgroup, waves on different rows ---------------------
-// The 4 waves own 4·RT consecutive 16-row tiles and walk all of K together: the B operand of
-// each chunk (TOK = 16·NT tokens × one chunk of columns, x or h_hi + h_lo) is loaded once by the
-// whole workgroup into LDS (double-buffered, 16-byte segments XOR-swizzled by row so the MFMA
-// reads are bank-conflict free) and shared by the 4 waves.
-template <int PH, int FMT, int RT, int NT, int DA>
-__global__ __launch_bounds__(256) void prefill_gemm(GemmArgs a) {
-  using F = Fmt<FMT>;
-  constexpr int NM = (PH == PH_UP) ? 2 * RT : RT;
-  constexpr int NH = (PH == PH_UP) ? 1 : 2;
-  constexpr int ROWS = 4 * 16 * RT;
-  constexpr int TOK = 16 * NT;
-  constexpr int NSEG = F::CHUNK / 8;                  // 16-byte segments per B row chunk
-  constexpr int BVEC = NH * TOK * NSEG;               // 16-byte vectors per B chunk
-  constexpr int BPT = (BVEC + 255) / 256;             // per thread
-  __shared__ __align__(16) u32x4 s_bv[2][BVEC];
-
-  int rt, wi;
-  prefill_tile(blockIdx.x, a.row_tiles, rt, wi);
-  if (rt >= a.row_tiles || wi >= *a.n_work) return;
-
-  const int4 item = a.work[wi];
-  const int e = item.x, pos0 = item.y, nitem = item.z;
-  const int gsel = (e == a.experts) ? 1 : 0;
-  const ExpertGroup &grp = a.grp[gsel];
-  const uint8_t *blob = grp.blobs + (gsel ? 0 : (size_t)e * grp.stride);
-  const int I = grp.inter, H = a.hidden;
-  const int out_dim = (PH == PH_UP) ? I : H;
-  const int K = (PH == PH_UP) ? H : I;
-  if (rt * ROWS >= out_dim) return;
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = lane >> 4, l16 = lane & 15;
-  const int rb = rt * ROWS + wave * 16 * RT;
-
-  ATile<FMT> at[NM];
-  wave_tiles<PH, FMT, RT>(at, blob, grp, rb, out_dim, K, l16);
-  const int nch = (K + F::CHUNK - 1) / F::CHUNK;
-
-  for (int t0 = 0; t0 < nitem; t0 += TOK) {
-    const int ntok = min(TOK, nitem - t0);
-    // Staging assignment: vector v = tid + 256·k ↦ (term hh, token row n, segment sg).
-    const uint16_t *bsrc[BPT];
-    int bcol[BPT], bdst[BPT];
-#pragma unroll
-    for (int k = 0; k < BPT; ++k) {
-      const int v = min(tid + 256 * k, BVEC - 1);
-      const int hh = v / (TOK * NSEG);
-      const int n = (v / NSEG) % TOK;
-      const int sg = v % NSEG;
-      const int slot = a.order[pos0 + t0 + (n < ntok ? n : 0)];
-      const uint16_t *row;
-      if (PH == PH_UP) row = a.x + (size_t)(slot / a.slots) * H;
-      else row = (hh == 0 ? a.h_hi : a.h_lo) + (size_t)slot * a.ldh;
-      bsrc[k] = row;
-      bcol[k] = 8 * sg;
-      bdst[k] = (hh * TOK + n) * NSEG + (sg ^ (n & (NSEG - 1)));
-    }
-    u32x4 breg[BPT];
-    auto load_b = [&](int c) {
-      // Columns past K (a tail chunk, or K shorter than a chunk) are clamped into the row:
-      // those B values only meet zeroed weights.
-      const int cc = min(c, nch - 1);
-#pragma unroll
-      for (int k = 0; k < BPT; ++k)
-        breg[k] = *(const u32x4 *)(bsrc[k] + min(cc * F::CHUNK + bcol[k], K - 8));
-    };
-    auto store_b = [&](int buf) {
-#pragma unroll
-      for (int k = 0; k < BPT; ++k)
-        if (tid + 256 * k < BVEC) s_bv[buf][bdst[k]] = breg[k];
-    };
-    int bslot[NT];
-#pragma unroll
-    for (int st = 0; st < NT; ++st) {
-      const int j = 16 * st + l16;
-      bslot[st] = a.order[pos0 + t0 + (j < ntok ? j : 0)];
-    }
-
-    f32x4 acc[2][NM][NT];
-#pragma unroll
-    for (int p = 0; p < 2; ++p)
-#pragma unroll
-      for (int m = 0; m < NM; ++m)
-#pragma unroll
-        for (int st = 0; st < NT; ++st) acc[p][m][st] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    typename F::A sa[DA][NM];
-    auto load_a = [&](typename F::A (&w)[NM], int c) {
-      const int cc = min(c, nch - 1);
-#pragma unroll
-      for (int m = 0; m < NM; ++m) F::load(w[m], at[m].row, cc, g, K);
-    };
-
-    // Prologue: B of chunk 0 in LDS, B of chunk 1 in registers, A of chunks 0..DA-1 in flight.
-    load_b(0);
-    store_b(0);
-    load_b(1);
-#pragma unroll
-    for (int u = 0; u < DA; ++u) load_a(sa[u], u);
-    __syncthreads();
-    // Chunk c: compute from LDS buffer c % 2; then stage B of c + 1 into the other buffer and
-    // fetch B of c + 2 and A of c + DA; one barrier per chunk.
-    for (int c0 = 0; c0 < nch; c0 += 2 * DA) {
-#pragma unroll
-      for (int u = 0; u < 2 * DA; ++u) {
-        const int c = c0 + u;
-        if (c < nch) {
-          const int buf = u & 1;
-          const int seg0 = is_mlx<FMT>() ? 2 * g : 4 * g;
-          chunk_mfma<FMT, NM, NT, NH>(acc[u & 1], sa[u % DA], at, [&](int st, int hh, int v) {
-            const int n = 16 * st + l16;
-            return s_bv[buf][(hh * TOK + n) * NSEG + ((seg0 + v) ^ (n & (NSEG - 1)))];
-          }, c, g, K);
-          load_a(sa[u % DA], c + DA);
-          store_b(buf ^ 1);
-          load_b(c + 2);
-          __syncthreads();
-        }
-      }
-    }
-
-    // Epilogue: 4 intermediates / hidden rows per lane.
-#pragma unroll
-    for (int st = 0; st < NT; ++st) {
-      const int j = 16 * st + l16;
-      if (j >= ntok) continue;
-#pragma unroll
-      for (int q = 0; q < RT; ++q) {
-        if (rb + 16 * q >= out_dim) continue;
-        if constexpr (PH == PH_UP) {
-          up_epilogue<FMT>(a, blob, grp, rb + 16 * q + 4 * g, bslot[st], sum_chains(acc[0][q][st], acc[1][q][st]),
-                           sum_chains(acc[0][RT + q][st], acc[1][RT + q][st]));
-        } else {
-          const int h0 = rb + 16 * q + 4 * g;
-          *(f32x4 *)(a.slot_out + (size_t)bslot[st] * H + h0) =
-              down_value<FMT>(a, blob, grp, h0, bslot[st], sum_chains(acc[0][q][st], acc[1][q][st]));
-        }
-      }
-    }
-    __syncthreads();   // the next pass restages s_bv
-  }
-}
-
-// ---- prefill, MXFP4 on the scaled MFMA -------------------------------------------------------------
-// prefill_gemm's workgroup layout (4 waves × RT 16-row tiles × 16·NT tokens, B chunk shared
-// through LDS, double-buffered) with the fp8 operand terms: a B chunk is, per token and term,
-// 128 bytes (8 segments, XOR-swizzled by token) and the 4 block scales of the chunk. RT = 2, so a
-// gate-up wave holds whole 32-intermediate blocks and quantises its activations itself.
-template <int PH, int RT, int NT, int DA>
-__global__ __launch_bounds__(256) void prefill_mx(GemmArgs a) {
-  using F = Fmt<Q_MXFP4>;
-  constexpr int NM = (PH == PH_UP) ? 2 * RT : RT;
-  constexpr int NTERM = (PH == PH_UP) ? NTX : NTH;
-  constexpr int ROWS = 4 * 16 * RT;
-  constexpr int TOK = 16 * NT;
-  constexpr int BVEC = NTERM * TOK * 8;               // 16-byte segments per B chunk
-  constexpr int BPT = (BVEC + 255) / 256;
-  constexpr int NSC = NTERM * TOK;                    // scale dwords per B chunk
-  static_assert(NSC <= 256, "one scale dword per thread");
-  static_assert(PH == PH_DOWN || RT == 2, "gate-up waves own whole 32-intermediate blocks");
-  __shared__ __align__(16) u32x4 s_bq[2][BVEC];
-  __shared__ uint32_t s_bs[2][NSC];
-
-  int rt, wi;
-  prefill_tile(blockIdx.x, a.row_tiles, rt, wi);
-  if (rt >= a.row_tiles || wi >= *a.n_work) return;
-
-  const int4 item = a.work[wi];
-  const int e = item.x, pos0 = item.y, nitem = item.z;
-  const int gsel = (e == a.experts) ? 1 : 0;
-  const ExpertGroup &grp = a.grp[gsel];
-  const uint8_t *blob = grp.blobs + (gsel ? 0 : (size_t)e * grp.stride);
-  const int I = grp.inter, H = a.hidden;
-  const int out_dim = (PH == PH_UP) ? I : H;
-  const int K = (PH == PH_UP) ? H : I;
-  if (rt * ROWS >= out_dim) return;
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = lane >> 4, l16 = lane & 15;
-  const int rb = rt * ROWS + wave * 16 * RT;
-
-  ATile<Q_MXFP4> at[NM];
-  wave_tiles<PH, Q_MXFP4, RT>(at, blob, grp, rb, out_dim, K, l16);
-  const int nch = (K + 127) / 128;
-  const int ld = PH == PH_UP ? a.xld : a.hld;
-  const uint8_t *qbase = PH == PH_UP ? a.xq : a.hq;
-  const uint8_t *sbase = PH == PH_UP ? a.xs : a.hs;
-
-  for (int t0 = 0; t0 < nitem; t0 += TOK) {
-    const int ntok = min(TOK, nitem - t0);
-    // Operand row of token n of the pass: x of its token (gate-up) or h of its slot (down).
-    auto row_of = [&](int n) {
-      const int slot = a.order[pos0 + t0 + (n < ntok ? n : 0)];
-      return PH == PH_UP ? slot / a.slots : slot;
-    };
-    const uint8_t *bsrc[BPT];
-    int bdst[BPT];
-#pragma unroll
-    for (int k = 0; k < BPT; ++k) {
-      const int v = min(tid + 256 * k, BVEC - 1);
-      const int tt = v / (TOK * 8), n = (v / 8) % TOK, sg = v % 8;
-      bsrc[k] = qbase + ((size_t)row_of(n) * NTERM + tt) * ld + 16 * sg;
-      bdst[k] = (tt * TOK + n) * 8 + (sg ^ (n & 7));
-    }
-    const uint8_t *ssrc = sbase + ((size_t)row_of(tid % TOK) * NTERM + min(tid / TOK, NTERM - 1)) * (ld / 32);
-    u32x4 breg[BPT];
-    uint32_t sreg = 0;
-    auto load_b = [&](int c) {
-      const int cc = min(c, nch - 1);
-#pragma unroll
-      for (int k = 0; k < BPT; ++k) breg[k] = *(const u32x4 *)(bsrc[k] + 128 * cc);
-      sreg = *(const uint32_t *)(ssrc + 4 * cc);
-    };
-    auto store_b = [&](int buf) {
-#pragma unroll
-      for (int k = 0; k < BPT; ++k)
-        if (tid + 256 * k < BVEC) s_bq[buf][bdst[k]] = breg[k];
-      if (tid < NSC) s_bs[buf][tid] = sreg;
-    };
-    int bslot[NT];
-#pragma unroll
-    for (int st = 0; st < NT; ++st) {
-      const int j = 16 * st + l16;
-      bslot[st] = a.order[pos0 + t0 + (j < ntok ? j : 0)];
-    }
-
-    f32x4 acc[2][NM][NT];
-#pragma unroll
-    for (int p = 0; p < 2; ++p)
-#pragma unroll
-      for (int m = 0; m < NM; ++m)
-#pragma unroll
-        for (int st = 0; st < NT; ++st) acc[p][m][st] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    typename F::A sa[DA][NM];
-    auto load_a = [&](typename F::A (&w)[NM], int c) {
-      const int cc = min(c, nch - 1);
-#pragma unroll
-      for (int m = 0; m < NM; ++m) F::load(w[m], at[m].row, cc, g, K);
-    };
-
-    load_b(0);
-    store_b(0);
-    load_b(1);
-#pragma unroll
-    for (int u = 0; u < DA; ++u) load_a(sa[u], u);
-    __syncthreads();
-    for (int c0 = 0; c0 < nch; c0 += 2 * DA) {
-#pragma unroll
-      for (int u = 0; u < 2 * DA; ++u) {
-        const int c = c0 + u;
-        if (c < nch) {
-          const int buf = u & 1;
-          u32x4 wv[NM];
-          uint32_t sv[NM];
-#pragma unroll
-          for (int m = 0; m < NM; ++m) { wv[m] = sa[u % DA][m].w; sv[m] = sa[u % DA][m].s; }
-          chunk_mx<NM, NT, NTERM>(acc[u & 1], wv, sv, [&](int st, int tt) {
-            const int n = 16 * st + l16;
-            const int k0 = 128 * c + 16 * g;
-            MxB b;
-            b.lo = s_bq[buf][(tt * TOK + n) * 8 + (g ^ (n & 7))];
-            b.hi = s_bq[buf][(tt * TOK + n) * 8 + ((4 + g) ^ (n & 7))];
-            b.s = (s_bs[buf][tt * TOK + n] >> (8 * g)) & 0xFFu;
-            if (k0 >= K) b.lo = u32x4{0u, 0u, 0u, 0u};
-            if (k0 + 64 >= K) b.hi = u32x4{0u, 0u, 0u, 0u};
-            if (128 * c + 32 * g >= K) b.s = 127u;
-            return b;
-          }, c, g, K);
-          load_a(sa[u % DA], c + DA);
-          store_b(buf ^ 1);
-          load_b(c + 2);
-          __syncthreads();
-        }
-      }
-    }
-
-    // Epilogue.
-    if (rb < out_dim) {
-#pragma unroll
-      for (int st = 0; st < NT; ++st) {
-        const int j = 16 * st + l16;
-        if constexpr (PH == PH_UP) {
-          // The wave's 32 intermediates rb .. rb+31 of token column j: one block; every lane takes
-          // part in the block maximum, only real token columns store.
-          const f32x4 y0 = up_values<Q_MXFP4>(a, blob, grp, rb + 4 * g, sum_chains(acc[0][0][st], acc[1][0][st]),
-                                              sum_chains(acc[0][RT][st], acc[1][RT][st]));
-          const f32x4 y1 = up_values<Q_MXFP4>(a, blob, grp, rb + 16 + 4 * g, sum_chains(acc[0][1][st], acc[1][1][st]),
-                                              sum_chains(acc[0][RT + 1][st], acc[1][RT + 1][st]));
-          const float v[8] = {y0[0], y0[1], y0[2], y0[3], y1[0], y1[1], y1[2], y1[3]};
-          uint32_t hq[NTH][2], sb[NTH];
-          quant_block<NTH>(v, hq, sb);
-          if (j < ntok) store_hq(a, bslot[st], rb / 32, rb + 4 * g, rb + 16 + 4 * g, hq, sb, g);
-        } else {
-          if (j >= ntok) continue;
-#pragma unroll
-          for (int q = 0; q < RT; ++q) {
-            if (rb + 16 * q >= out_dim) continue;
-            const int h0 = rb + 16 * q + 4 * g;
-            *(f32x4 *)(a.slot_out + (size_t)bslot[st] * H + h0) =
-                down_value<Q_MXFP4>(a, blob, grp, h0, bslot[st], sum_chains(acc[0][q][st], acc[1][q][st]));
-          }
-        }
-      }
-    }
-    __syncthreads();   // the next pass restages the B buffers
   }
 }
 
@@ -2349,6 +2053,346 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
+// ---- prefill, BF16 and MLX affine: an LDS ring filled by loader waves -----------------------------
+// 8 waves, one workgroup per compute unit, persistent over the tasks τ = blockIdx, + gridDim, ...
+// (a task = one work item of ≤ 32 tokens × one row tile, in prefill_tile's XCD-aware order).
+// Waves 4-7 load: each stage (SCOLS columns of K) brings, by direct-to-LDS loads, the weight
+// operand of the row tile (per MFMA wave: NM tiles of 16 rows, laid out exactly as that wave's
+// lanes read them), the MLX group scales and biases, and the TOK token rows of the activation
+// (x, or h_hi and h_lo) in 16-byte segments XOR-swizzled by token so the MFMA reads are
+// bank-conflict free. S stages are in flight; the ring runs on across task boundaries (each
+// task's work item and slot ids also travel by direct-to-LDS loads, ahead of its first stage).
+// Waves 0-3 multiply: wave w owns output rows rb .. rb + 16·RT of the tile (gate and up tiles of
+// the same intermediates for gate-up) for all 32 tokens, and reads each stage's operands one
+// stage ahead of its MFMAs. The arithmetic per output element is chunk_mfma's, the decode
+// kernels' bits: two chains over the chunks (even / odd), steps in order.
+template <int PH, int FMT, int RT> struct Ring {
+  static constexpr int NT = 2, TOK = 16 * NT;
+  static constexpr int NM = (PH == PH_UP ? 2 : 1) * RT;
+  static constexpr int NH = PH == PH_UP ? 1 : 2;
+  static constexpr bool MLX = is_mlx<FMT>();
+  static constexpr int SCOLS = MLX ? 128 : 64;                  // K columns per stage
+  static constexpr int SEGS = SCOLS / 8;                        // 16-byte segments per token row
+  static constexpr int RPI = 1024 / (SCOLS * 2);                // token rows per 1 KiB load
+  static constexpr int A_INS = FMT == Q_MLX4 ? 1 : 2;           // 1 KiB weight loads per tile
+  static constexpr int B_INS = NH * TOK / RPI;                  // 1 KiB operand loads per stage
+  static constexpr int BPW = B_INS / 4;
+  static constexpr int SB_INS = MLX ? 4 : 0;                    // {scale, bias} × 2 groups
+  static constexpr int L = NM * A_INS + BPW + SB_INS;           // loads per loader wave per stage
+  static constexpr int OFF_B = 4 * NM * A_INS * 1024;
+  static constexpr int OFF_SB = OFF_B + B_INS * 1024;
+  static constexpr int STAGE = OFF_SB + (MLX ? 4096 : 0);
+  static constexpr int S_LDS = (148 * 1024) / STAGE, S_CNT = 3 + 63 / L;
+  static constexpr int S = S_LDS < S_CNT ? (S_LDS < 8 ? S_LDS : 8) : (S_CNT < 8 ? S_CNT : 8);
+  static constexpr int NSLOT = S + 1;                           // task info slots (≤ S tasks ahead)
+  static constexpr int OFF_INFO = S * STAGE;                    // [NSLOT][work item 256 B | slots 256 B]
+  static constexpr int LDS = OFF_INFO + NSLOT * 512;
+  static constexpr int ROWS = 64 * RT;
+  static_assert(B_INS % 4 == 0 && S >= 3 && NM <= 4 && LDS <= 160 * 1024, "ring layout");
+  __device__ static int swz(int n) { return SEGS == 16 ? (n & 15) : ((n >> 1) & 7); }
+};
+
+__device__ __forceinline__ void lds_load2(const void *g, uint8_t *l) {
+  __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)l, 2, 0, 0);
+}
+template <int N> __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+template <int PH, int FMT, int RT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_ring(GemmArgs a) {
+  using C = Ring<PH, FMT, RT>;
+  using F = Fmt<FMT>;
+  constexpr int NM = C::NM, NT = C::NT, NH = C::NH, TOK = C::TOK, S = C::S, L = C::L;
+  constexpr int SCOLS = C::SCOLS, SEGS = C::SEGS;
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, l16 = lane & 15;
+  const int H = a.hidden, E = a.experts;
+  const int RTL = a.row_tiles, rtx = (RTL + 7) >> 3;
+  const int nwork = *a.n_work;
+  const Mx3Tasks tasks{(int)blockIdx.x, (int)gridDim.x, RTL, 8 * rtx * nwork};
+  if (tasks.first() >= tasks.lim) return;
+  auto group_of = [&](int e) -> const ExpertGroup & { return a.grp[e == E ? 1 : 0]; };
+  auto k_of = [&](int e) { return PH == PH_UP ? H : group_of(e).inter; };
+  auto nst_of = [&](int e) { return (k_of(e) + SCOLS - 1) / SCOLS; };
+  auto work_of = [&](int tau) {
+    int rt, wi;
+    prefill_tile(min(tau, tasks.lim - 1), RTL, rt, wi);
+    return a.work[wi];
+  };
+
+  if (wave >= 4) {
+    // ---- loaders ----
+    const int lw = wave - 4;
+    int tau = tasks.first(), slot = 0;
+    int4 wn = work_of(tau), wnn = work_of(tasks.next(tau));
+    int on = a.order[wn.y + min(lane, wn.z - 1)];
+    int4 cur;
+    int K = 0, nst = 0, ls = 0, q = 0;     // task K, its stages, stage within it, stages issued
+    ATile<FMT> at[NM];
+    const uint16_t *brow[C::BPW];
+    bool more = true;
+    {
+      // The first task's copy, waited for here.
+      int rt0, wi0;
+      prefill_tile(tau, RTL, rt0, wi0);
+      lds_load4((const int *)(a.work + wi0) + min(lane, 3), lds + C::OFF_INFO);
+      lds_load4(a.order + wn.y + min(lane, wn.z - 1), lds + C::OFF_INFO + 256);
+      wait_vm<0>();
+    }
+    auto begin_task = [&]() {
+      cur = wn;
+      const int o = on;
+      int rt, wi;
+      prefill_tile(tau, RTL, rt, wi);
+      // The MFMA waves' copy of a task's work item and slot ids, sent one task ahead (the first
+      // task's with it): it lands long before the task's first stage is read.
+      const int t1 = tasks.next(tau);
+      const int nslot = slot == C::NSLOT - 1 ? 0 : slot + 1;
+      if (t1 < tasks.lim) {
+        int rt1, wi1;
+        prefill_tile(t1, RTL, rt1, wi1);
+        uint8_t *info = lds + C::OFF_INFO + 512 * nslot;
+        lds_load4((const int *)(a.work + wi1) + min(lane, 3), info);
+        lds_load4(a.order + wnn.y + min(lane, wnn.z - 1), info + 256);
+      }
+      const int e = cur.x;
+      const ExpertGroup &grp = group_of(e);
+      const uint8_t *blob = grp.blobs + (e == E ? 0 : (size_t)e * grp.stride);
+      K = k_of(e);
+      nst = nst_of(e);
+      const int out_dim = PH == PH_UP ? grp.inter : H;
+      wave_tiles<PH, FMT, RT>(at, blob, grp, rt * C::ROWS + lw * 16 * RT, out_dim, K, l16);
+#pragma unroll
+      for (int i = 0; i < C::BPW; ++i) {
+        const int j = lw * C::BPW + i;
+        const int hh = j / (TOK / C::RPI);
+        const int n = C::RPI * (j % (TOK / C::RPI)) + lane / SEGS;
+        const int sl = __shfl(o, min(n, cur.z - 1));
+        brow[i] = PH == PH_UP ? a.x + (size_t)(sl / a.slots) * H : (hh ? a.h_lo : a.h_hi) + (size_t)sl * a.ldh;
+      }
+      // Prefetch: the next task's slot ids, the work item of the one after.
+      wn = wnn;
+      on = a.order[wn.y + min(lane, wn.z - 1)];
+      wnn = work_of(tasks.next(t1));
+      ls = 0;
+    };
+    auto issue = [&](int s, int st) {
+      uint8_t *stg = lds + st * C::STAGE;
+#pragma unroll
+      for (int m = 0; m < NM; ++m) {
+        uint8_t *dst = stg + (lw * NM + m) * C::A_INS * 1024;
+        const uint8_t *w = at[m].row.w;
+        if constexpr (FMT == Q_BF16) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) lds_load16(w + 2 * min(64 * s + 32 * j + 8 * g, K - 8), dst + 1024 * j);
+        } else if constexpr (FMT == Q_MLX4) {
+          lds_load16(w + min(64 * s + 16 * g, K / 2 - 16), dst);
+        } else {
+#pragma unroll
+          for (int p = 0; p < 2; ++p) lds_load16(w + min(128 * s + 64 * p + 16 * g, K - 16), dst + 1024 * p);
+        }
+      }
+      if constexpr (C::MLX) {
+        // Group scales and biases of the wave's rows: lane (m, r) holds tile m's row r (one
+        // dword per lane; tiles past NM repeat the last).
+        typename F::Row r = at[0].row;
+#pragma unroll
+        for (int m = 1; m < NM; ++m)
+          if ((lane >> 4) >= m) r = at[m].row;
+        const int ng = K / 64;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const int gi = min(2 * s + p, ng - 1);
+          lds_load2(r.sc + gi, stg + C::OFF_SB + lw * 1024 + p * 256);
+          lds_load2(r.bi + gi, stg + C::OFF_SB + lw * 1024 + 512 + p * 256);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < C::BPW; ++i) {
+        const int j = lw * C::BPW + i;
+        const int n = C::RPI * (j % (TOK / C::RPI)) + lane / SEGS;
+        const int seg = (lane % SEGS) ^ C::swz(n);
+        lds_load16(brow[i] + min(SCOLS * s + 8 * seg, K - 8), stg + C::OFF_B + 1024 * j);
+      }
+    };
+    auto issue_next = [&]() {
+      if (ls == 0) begin_task();
+      issue(ls, q % S);
+      asm volatile("" ::: "memory");   // stages (and task copies) issue in program order
+      ++q;
+      if (++ls == nst) {
+        ls = 0;
+        tau = tasks.next(tau);
+        slot = slot == C::NSLOT - 1 ? 0 : slot + 1;
+        more = tau < tasks.lim;
+      }
+    };
+    for (int u = 0; u < S - 1 && more; ++u) issue_next();
+    if (q >= S - 1) wait_vm<(S - 3) * L>();
+    else wait_vm<0>();
+    for (int step = 0; more || step < q; ++step) {
+      ring_barrier();
+      if (more) {
+        issue_next();
+        wait_vm<(S - 3) * L>();
+      } else {
+        wait_vm<0>();
+      }
+    }
+    return;
+  }
+
+  // ---- MFMA waves ----
+  struct Ops {
+    typename F::A w[C::MLX ? 2 : 1][NM];
+    u32x4 b[C::MLX ? 2 : 1][NT][NH][2];
+  };
+  auto read_ops = [&](int st) {
+    const uint8_t *stg = lds + st * C::STAGE;
+    Ops o;
+    constexpr int NP = C::MLX ? 2 : 1;
+#pragma unroll
+    for (int m = 0; m < NM; ++m) {
+      const uint8_t *ab = stg + (wave * NM + m) * C::A_INS * 1024;
+      if constexpr (FMT == Q_BF16) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) o.w[0][m].w[j] = *(const u32x4 *)(ab + 1024 * j + 16 * lane);
+      } else {
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          if constexpr (FMT == Q_MLX4) {
+            const u32x2 v = *(const u32x2 *)(ab + 16 * ((2 * p + (g >> 1)) * 16 + l16) + 8 * (g & 1));
+            o.w[p][m].w[0] = v[0];
+            o.w[p][m].w[1] = v[1];
+          } else {
+            const u32x4 v = *(const u32x4 *)(ab + 1024 * p + 16 * lane);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o.w[p][m].w[k] = v[k];
+          }
+          const uint8_t *sbp = stg + C::OFF_SB + wave * 1024 + p * 256 + 4 * (16 * m + l16);
+          o.w[p][m].sb = (*(const uint32_t *)sbp & 0xFFFFu) | (*(const uint32_t *)(sbp + 512) << 16);
+        }
+      }
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+#pragma unroll
+      for (int st = 0; st < NT; ++st)
+#pragma unroll
+        for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+          for (int v = 0; v < 2; ++v) {
+            const int n = 16 * st + l16;
+            const int seg = C::MLX ? 8 * p + 2 * g + v : 4 * v + g;
+            o.b[p][st][hh][v] =
+                *(const u32x4 *)(stg + C::OFF_B + (hh * TOK + n) * (SCOLS * 2) + 16 * (seg ^ C::swz(n)));
+          }
+    return o;
+  };
+
+  f32x4 acc[2][NM][NT];
+  auto zero = [&]() {
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int st = 0; st < NT; ++st) acc[p][m][st] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+  zero();
+  int tau = tasks.first(), slot = 0, ls = 0, nst = 0, K = 0, e = 0, ntok = 0, rt = 0;
+  int eslot[NT];
+  float ew[NT];
+  const ATile<FMT> at_unused[NM] = {};
+  ring_barrier();
+  Ops cur = read_ops(0);
+  for (int step = 0;; ++step) {
+    if (ls == 0) {
+      const uint8_t *info = lds + C::OFF_INFO + 512 * slot;
+      const int4 it = *(const int4 *)info;
+      e = it.x;
+      ntok = it.z;
+      K = k_of(e);
+      nst = nst_of(e);
+      int wi;
+      prefill_tile(tau, RTL, rt, wi);
+#pragma unroll
+      for (int st = 0; st < NT; ++st) {
+        eslot[st] = ((const int *)(info + 256))[min(16 * st + l16, ntok - 1)];
+        ew[st] = PH == PH_DOWN ? a.slot_w[eslot[st]] : 0.f;
+      }
+    }
+    // Is there a stage after this one (this task's next, or the next task's first)?
+    const bool last_stage = ls + 1 == nst;
+    const int tau_n = last_stage ? tasks.next(tau) : tau;
+    const bool more = !last_stage || tau_n < tasks.lim;
+    Ops nxt;
+    if (more) nxt = read_ops((step + 1) % S);
+    if constexpr (FMT == Q_BF16) {
+      const int c = ls >> 1;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int v = 2 * (ls & 1) + j;
+        if (!F::step_ok(c, v, K)) break;
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+          for (int st = 0; st < NT; ++st)
+#pragma unroll
+            for (int hh = 0; hh < NH; ++hh)
+              acc[c & 1][m][st] = mfma(as_bf16x8(cur.w[0][m].w[j]), as_bf16x8(cur.b[0][st][hh][j]), acc[c & 1][m][st]);
+      }
+    } else {
+#pragma unroll
+      for (int p = 0; p < 2; ++p) {
+        const int c = 2 * ls + p;
+        if (64 * c >= K) break;
+        chunk_mfma<FMT, NM, NT, NH>(acc[c & 1], cur.w[p], at_unused,
+                                    [&](int st, int hh, int v) { return cur.b[p][st][hh][v]; }, c, g, K);
+      }
+    }
+    if (last_stage) {
+      // ---- epilogue of the task ----
+      const ExpertGroup &grp = group_of(e);
+      const int out_dim = PH == PH_UP ? grp.inter : H;
+      const int rb = rt * C::ROWS + wave * 16 * RT;
+#pragma unroll
+      for (int st = 0; st < NT; ++st) {
+        if (16 * st + l16 >= ntok) continue;
+#pragma unroll
+        for (int q = 0; q < RT; ++q) {
+          if (rb + 16 * q >= out_dim) continue;
+          if constexpr (PH == PH_UP) {
+            up_epilogue<FMT>(a, nullptr, grp, rb + 16 * q + 4 * g, eslot[st],
+                             sum_chains(acc[0][q][st], acc[1][q][st]), sum_chains(acc[0][RT + q][st], acc[1][RT + q][st]));
+          } else {
+            const f32x4 r = sum_chains(acc[0][q][st], acc[1][q][st]);
+            f32x4 o;
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) o[ii] = ew[st] * (r[ii] + 0.f);   // down_value's arithmetic
+            *(f32x4 *)(a.slot_out + (size_t)eslot[st] * H + rb + 16 * q + 4 * g) = o;
+          }
+        }
+      }
+      zero();
+      tau = tau_n;
+      slot = slot == C::NSLOT - 1 ? 0 : slot + 1;
+      ls = 0;
+    } else {
+      ++ls;
+    }
+    if (!more) break;
+    ring_barrier();
+    cur = nxt;
+  }
+}
+
+// Row tiles per MFMA wave of the ring kernel: gate-up one (a gate and an up tile), down two.
+template <int PH, int FMT> constexpr int ring_rt() {
+  return PH == PH_DOWN ? 2 : 1;
+}
+
 // ---- launch table -----------------------------------------------------------------------------
 typedef void (*GemmKernel)(GemmArgs);
 typedef void (*UpSmallKernel)(GemmArgs, RouteArgs);
@@ -2380,18 +2424,21 @@ template <int FMT> static DownSmallKernel down_small_k(int slots, bool one) {
 template <int PH, int FMT>
 static GemmKernel pick(int nt) {
   if constexpr (FMT == Q_MXFP4) return nt <= 2 ? prefill_mx2<PH, 1> : prefill_mx2<PH, 2>;
-  // Prefill: 4 waves × RT 16-row tiles × 16·NT tokens (BF16 keeps one tile per wave: its
-  // weight operand is 4× wider per chunk).
-  constexpr int RT_P = (FMT == Q_BF16) ? 1 : 2;
-  if (nt <= 1) return prefill_gemm<PH, FMT, RT_P, 1, 2>;
-  return prefill_gemm<PH, FMT, RT_P, 2, 2>;
+  else return prefill_ring<PH, FMT, ring_rt<PH, FMT>()>;
 }
 
 // Output rows per prefill workgroup: intermediates (gate-up) or hidden rows (down). The MXFP4
 // kernel covers 128 weight rows: 64 intermediates of the interleaved gate_up matrix.
 int gemm_rows_per_block(int quant, int phase) {
   if (quant == Q_MXFP4) return phase == PH_UP ? 64 : 128;
-  return 4 * 16 * (quant == Q_BF16 ? 1 : 2);
+  switch (quant) {
+  case Q_BF16: return phase == PH_UP ? Ring<PH_UP, Q_BF16, ring_rt<PH_UP, Q_BF16>()>::ROWS
+                                     : Ring<PH_DOWN, Q_BF16, ring_rt<PH_DOWN, Q_BF16>()>::ROWS;
+  case Q_MLX4: return phase == PH_UP ? Ring<PH_UP, Q_MLX4, ring_rt<PH_UP, Q_MLX4>()>::ROWS
+                                     : Ring<PH_DOWN, Q_MLX4, ring_rt<PH_DOWN, Q_MLX4>()>::ROWS;
+  default: return phase == PH_UP ? Ring<PH_UP, Q_MLX8, ring_rt<PH_UP, Q_MLX8>()>::ROWS
+                                 : Ring<PH_DOWN, Q_MLX8, ring_rt<PH_DOWN, Q_MLX8>()>::ROWS;
+  }
 }
 
 static GemmKernel gemm_kernel(int phase, int quant, int nt) {
@@ -2401,6 +2448,29 @@ static GemmKernel gemm_kernel(int phase, int quant, int nt) {
   case Q_MLX4: return phase == PH_UP ? pick<PH_UP, Q_MLX4>(nt) : pick<PH_DOWN, Q_MLX4>(nt);
   default: return phase == PH_UP ? pick<PH_UP, Q_MLX8>(nt) : pick<PH_DOWN, Q_MLX8>(nt);
   }
+}
+
+// Dynamic LDS of the ring kernel of (phase, quant).
+static size_t ring_lds(int phase, int quant) {
+  switch (quant) {
+  case Q_BF16: return phase == PH_UP ? Ring<PH_UP, Q_BF16, ring_rt<PH_UP, Q_BF16>()>::LDS
+                                     : Ring<PH_DOWN, Q_BF16, ring_rt<PH_DOWN, Q_BF16>()>::LDS;
+  case Q_MLX4: return phase == PH_UP ? Ring<PH_UP, Q_MLX4, ring_rt<PH_UP, Q_MLX4>()>::LDS
+                                     : Ring<PH_DOWN, Q_MLX4, ring_rt<PH_DOWN, Q_MLX4>()>::LDS;
+  default: return phase == PH_UP ? Ring<PH_UP, Q_MLX8, ring_rt<PH_UP, Q_MLX8>()>::LDS
+                                 : Ring<PH_DOWN, Q_MLX8, ring_rt<PH_DOWN, Q_MLX8>()>::LDS;
+  }
+}
+
+static int device_cus() {
+  static int ncu = 0;
+  if (!ncu) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu < 8) ncu = 256;
+    ncu &= ~7;   // prefill_tile's order assumes 8 | gridDim for persistent grids
+  }
+  return ncu;
 }
 
 // Whether prefill_mx3 takes a phase: MXFP4 without a shared expert, 32-token work items, and rows
@@ -2428,6 +2498,22 @@ hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStrea
       hipExtLaunchKernelGGL(prefill_mx3<PH_UP>, dim3(ncu), dim3(512), Mx3<PH_UP>::LDS, s, tm.start, tm.stop, 0, a);
     else
       hipExtLaunchKernelGGL(prefill_mx3<PH_DOWN>, dim3(ncu), dim3(512), Mx3<PH_DOWN>::LDS, s, tm.start, tm.stop, 0, a);
+    return hipGetLastError();
+  }
+  if (quant != Q_MXFP4) {
+    // BF16 / MLX: the persistent ring kernel, one workgroup per compute unit.
+    static std::once_flag once;
+    std::call_once(once, [] {
+      for (int ph = 0; ph < 2; ++ph)
+        for (int q : {Q_BF16, Q_MLX4, Q_MLX8}) {
+          (void)hipFuncSetAttribute((const void *)gemm_kernel(ph, q, 2), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    160 * 1024);
+          (void)hipGetLastError();
+        }
+    });
+    if (a.max_work == 0) return hipSuccess;
+    hipExtLaunchKernelGGL(gemm_kernel(phase, quant, nt), dim3(device_cus()), dim3(512), ring_lds(phase, quant), s,
+                          tm.start, tm.stop, 0, a);
     return hipGetLastError();
   }
   // prefill_tile: 8 XCDs × ⌈row_tiles / 8⌉ row tiles × work items.
