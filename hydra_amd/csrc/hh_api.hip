@@ -86,10 +86,10 @@ struct Scratch {
 constexpr int kSmallT = 16;  // batches up to this size take the decode kernels
 
 int token_tile_nt(const hh_moe_desc &d, int T) {
-  // Prefill kernel token tiles of 16: MXFP4 work items of 32 tokens (prefill_mx3's task), the
-  // other formats 16 or 32, the larger once batches are big enough for experts to fill them.
-  if (d.quant == HH_QUANT_MXFP4) return 2;
-  return (T >= 64) ? 2 : 1;
+  // Prefill work items of 16·nt tokens: MXFP4 32 (prefill_mx2/mx3), BF16 64 once experts
+  // average 64 tokens or more (the weight tile is then read once per 64 tokens), else 32.
+  if (d.quant == HH_QUANT_BF16 && (int64_t)T * d.top_k >= 64 * (int64_t)d.experts) return 4;
+  return 2;
 }
 
 Scratch plan(const hh_moe_desc &d, int T) {

@@ -2066,15 +2066,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // the same intermediates for gate-up) for all 32 tokens, and reads each stage's operands one
 // stage ahead of its MFMAs. The arithmetic per output element is chunk_mfma's, the decode
 // kernels' bits: two chains over the chunks (even / odd), steps in order.
-template <int PH, int FMT, int RT> struct Ring {
-  static constexpr int NT = 2, TOK = 16 * NT;
+template <int PH, int FMT, int RT, int NT_> struct Ring {
+  static constexpr int NT = NT_, TOK = 16 * NT;
   static constexpr int NM = (PH == PH_UP ? 2 : 1) * RT;
   static constexpr int NH = PH == PH_UP ? 1 : 2;
   static constexpr bool MLX = is_mlx<FMT>();
-  static constexpr int SCOLS = MLX ? 128 : 64;                  // K columns per stage
+  // K columns per stage: two MLX groups; BF16 two 32-column steps, one for wide token tiles.
+  static constexpr int SCOLS = MLX ? 128 : (NT >= 4 ? 32 : 64);
+  static constexpr int SPS = MLX ? 2 : SCOLS / 32;              // MLX groups / BF16 steps per stage
   static constexpr int SEGS = SCOLS / 8;                        // 16-byte segments per token row
   static constexpr int RPI = 1024 / (SCOLS * 2);                // token rows per 1 KiB load
-  static constexpr int A_INS = FMT == Q_MLX4 ? 1 : 2;           // 1 KiB weight loads per tile
+  static constexpr int A_INS = FMT == Q_MLX4 ? 1 : SPS;         // 1 KiB weight loads per tile
   static constexpr int B_INS = NH * TOK / RPI;                  // 1 KiB operand loads per stage
   static constexpr int BPW = B_INS / 4;
   static constexpr int SB_INS = MLX ? 4 : 0;                    // {scale, bias} × 2 groups
@@ -2082,14 +2084,20 @@ template <int PH, int FMT, int RT> struct Ring {
   static constexpr int OFF_B = 4 * NM * A_INS * 1024;
   static constexpr int OFF_SB = OFF_B + B_INS * 1024;
   static constexpr int STAGE = OFF_SB + (MLX ? 4096 : 0);
+  static constexpr int NO = (TOK + 63) / 64;                    // slot-id registers per lane
+  static constexpr int INFO = 256 + 256 * NO;                   // work item, slot ids
   static constexpr int S_LDS = (148 * 1024) / STAGE, S_CNT = 3 + 63 / L;
   static constexpr int S = S_LDS < S_CNT ? (S_LDS < 8 ? S_LDS : 8) : (S_CNT < 8 ? S_CNT : 8);
   static constexpr int NSLOT = S + 1;                           // task info slots (≤ S tasks ahead)
-  static constexpr int OFF_INFO = S * STAGE;                    // [NSLOT][work item 256 B | slots 256 B]
-  static constexpr int LDS = OFF_INFO + NSLOT * 512;
+  static constexpr int OFF_INFO = S * STAGE;
+  static constexpr int LDS = OFF_INFO + NSLOT * INFO;
   static constexpr int ROWS = 64 * RT;
+  // The B operand of the next stage is read ahead too, except for wide token tiles (registers).
+  static constexpr bool RA_B = NT <= 2;
   static_assert(B_INS % 4 == 0 && S >= 3 && NM <= 4 && LDS <= 160 * 1024, "ring layout");
-  __device__ static int swz(int n) { return SEGS == 16 ? (n & 15) : ((n >> 1) & 7); }
+  __device__ static int swz(int n) {
+    return SEGS == 16 ? (n & 15) : (SEGS == 8 ? ((n >> 1) & 7) : ((n >> 2) & 3));
+  }
 };
 
 __device__ __forceinline__ void lds_load2(const void *g, uint8_t *l) {
@@ -2097,12 +2105,12 @@ __device__ __forceinline__ void lds_load2(const void *g, uint8_t *l) {
 }
 template <int N> __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
 
-template <int PH, int FMT, int RT>
+template <int PH, int FMT, int RT, int NT_>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_ring(GemmArgs a) {
-  using C = Ring<PH, FMT, RT>;
+  using C = Ring<PH, FMT, RT, NT_>;
   using F = Fmt<FMT>;
   constexpr int NM = C::NM, NT = C::NT, NH = C::NH, TOK = C::TOK, S = C::S, L = C::L;
-  constexpr int SCOLS = C::SCOLS, SEGS = C::SEGS;
+  constexpr int SCOLS = C::SCOLS, SEGS = C::SEGS, SPS = C::SPS, NO = C::NO;
   extern __shared__ __align__(16) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -2120,42 +2128,41 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     prefill_tile(min(tau, tasks.lim - 1), RTL, rt, wi);
     return a.work[wi];
   };
+  // A task's copy for the MFMA waves: its work item, then its slot ids.
+  auto send_info = [&](int tau, const int4 &w, int slot) {
+    int rt, wi;
+    prefill_tile(tau, RTL, rt, wi);
+    uint8_t *info = lds + C::OFF_INFO + C::INFO * slot;
+    lds_load4((const int *)(a.work + wi) + min(lane, 3), info);
+#pragma unroll
+    for (int k = 0; k < NO; ++k) lds_load4(a.order + w.y + min(64 * k + lane, w.z - 1), info + 256 * (k + 1));
+  };
 
   if (wave >= 4) {
     // ---- loaders ----
     const int lw = wave - 4;
     int tau = tasks.first(), slot = 0;
     int4 wn = work_of(tau), wnn = work_of(tasks.next(tau));
-    int on = a.order[wn.y + min(lane, wn.z - 1)];
-    int4 cur;
+    int on[NO];
+#pragma unroll
+    for (int k = 0; k < NO; ++k) on[k] = a.order[wn.y + min(64 * k + lane, wn.z - 1)];
     int K = 0, nst = 0, ls = 0, q = 0;     // task K, its stages, stage within it, stages issued
     ATile<FMT> at[NM];
     const uint16_t *brow[C::BPW];
     bool more = true;
-    {
-      // The first task's copy, waited for here.
-      int rt0, wi0;
-      prefill_tile(tau, RTL, rt0, wi0);
-      lds_load4((const int *)(a.work + wi0) + min(lane, 3), lds + C::OFF_INFO);
-      lds_load4(a.order + wn.y + min(lane, wn.z - 1), lds + C::OFF_INFO + 256);
-      wait_vm<0>();
-    }
+    send_info(tau, wn, 0);   // the first task's copy, waited for here
+    wait_vm<0>();
     auto begin_task = [&]() {
-      cur = wn;
-      const int o = on;
+      const int4 cur = wn;
+      int o[NO];
+#pragma unroll
+      for (int k = 0; k < NO; ++k) o[k] = on[k];
       int rt, wi;
       prefill_tile(tau, RTL, rt, wi);
-      // The MFMA waves' copy of a task's work item and slot ids, sent one task ahead (the first
-      // task's with it): it lands long before the task's first stage is read.
+      // The next task's copy goes out a task ahead: it lands long before that task's first stage
+      // is read.
       const int t1 = tasks.next(tau);
-      const int nslot = slot == C::NSLOT - 1 ? 0 : slot + 1;
-      if (t1 < tasks.lim) {
-        int rt1, wi1;
-        prefill_tile(t1, RTL, rt1, wi1);
-        uint8_t *info = lds + C::OFF_INFO + 512 * nslot;
-        lds_load4((const int *)(a.work + wi1) + min(lane, 3), info);
-        lds_load4(a.order + wnn.y + min(lane, wnn.z - 1), info + 256);
-      }
+      if (t1 < tasks.lim) send_info(t1, wnn, slot == C::NSLOT - 1 ? 0 : slot + 1);
       const int e = cur.x;
       const ExpertGroup &grp = group_of(e);
       const uint8_t *blob = grp.blobs + (e == E ? 0 : (size_t)e * grp.stride);
@@ -2167,15 +2174,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int i = 0; i < C::BPW; ++i) {
         const int j = lw * C::BPW + i;
         const int hh = j / (TOK / C::RPI);
-        const int n = C::RPI * (j % (TOK / C::RPI)) + lane / SEGS;
-        const int sl = __shfl(o, min(n, cur.z - 1));
+        const int n = min(C::RPI * (j % (TOK / C::RPI)) + lane / SEGS, cur.z - 1);
+        int sl = 0;
+#pragma unroll
+        for (int k = 0; k < NO; ++k) {
+          const int v = __shfl(o[k], n & 63);
+          if ((n >> 6) == k) sl = v;
+        }
         brow[i] = PH == PH_UP ? a.x + (size_t)(sl / a.slots) * H : (hh ? a.h_lo : a.h_hi) + (size_t)sl * a.ldh;
       }
       // Prefetch: the next task's slot ids, the work item of the one after.
       wn = wnn;
-      on = a.order[wn.y + min(lane, wn.z - 1)];
+#pragma unroll
+      for (int k = 0; k < NO; ++k) on[k] = a.order[wn.y + min(64 * k + lane, wn.z - 1)];
       wnn = work_of(tasks.next(t1));
-      ls = 0;
     };
     auto issue = [&](int s, int st) {
       uint8_t *stg = lds + st * C::STAGE;
@@ -2185,7 +2197,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const uint8_t *w = at[m].row.w;
         if constexpr (FMT == Q_BF16) {
 #pragma unroll
-          for (int j = 0; j < 2; ++j) lds_load16(w + 2 * min(64 * s + 32 * j + 8 * g, K - 8), dst + 1024 * j);
+          for (int j = 0; j < SPS; ++j) lds_load16(w + 2 * min(SCOLS * s + 32 * j + 8 * g, K - 8), dst + 1024 * j);
         } else if constexpr (FMT == Q_MLX4) {
           lds_load16(w + min(64 * s + 16 * g, K / 2 - 16), dst);
         } else {
@@ -2244,20 +2256,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 
   // ---- MFMA waves ----
-  struct Ops {
-    typename F::A w[C::MLX ? 2 : 1][NM];
-    u32x4 b[C::MLX ? 2 : 1][NT][NH][2];
-  };
-  auto read_ops = [&](int st) {
+  constexpr int NP = C::MLX ? 2 : 1;
+  struct AOps { typename F::A w[NP][NM]; };
+  struct BOps { u32x4 b[NP][NT][NH][C::MLX ? 2 : SPS]; };
+  auto read_a = [&](int st) {
     const uint8_t *stg = lds + st * C::STAGE;
-    Ops o;
-    constexpr int NP = C::MLX ? 2 : 1;
+    AOps o;
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
       const uint8_t *ab = stg + (wave * NM + m) * C::A_INS * 1024;
       if constexpr (FMT == Q_BF16) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) o.w[0][m].w[j] = *(const u32x4 *)(ab + 1024 * j + 16 * lane);
+        for (int j = 0; j < SPS; ++j) o.w[0][m].w[j] = *(const u32x4 *)(ab + 1024 * j + 16 * lane);
       } else {
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
@@ -2275,17 +2285,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
       }
     }
+    return o;
+  };
+  auto read_b = [&](int st) {
+    const uint8_t *stg = lds + st * C::STAGE;
+    BOps o;
 #pragma unroll
     for (int p = 0; p < NP; ++p)
 #pragma unroll
-      for (int st = 0; st < NT; ++st)
+      for (int st2 = 0; st2 < NT; ++st2)
 #pragma unroll
         for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
-          for (int v = 0; v < 2; ++v) {
-            const int n = 16 * st + l16;
+          for (int v = 0; v < (C::MLX ? 2 : SPS); ++v) {
+            const int n = 16 * st2 + l16;
             const int seg = C::MLX ? 8 * p + 2 * g + v : 4 * v + g;
-            o.b[p][st][hh][v] =
+            o.b[p][st2][hh][v] =
                 *(const u32x4 *)(stg + C::OFF_B + (hh * TOK + n) * (SCOLS * 2) + 16 * (seg ^ C::swz(n)));
           }
     return o;
@@ -2302,14 +2317,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   };
   zero();
   int tau = tasks.first(), slot = 0, ls = 0, nst = 0, K = 0, e = 0, ntok = 0, rt = 0;
-  int eslot[NT];
-  float ew[NT];
+  float ew[PH == PH_DOWN ? NT : 1];
   const ATile<FMT> at_unused[NM] = {};
   ring_barrier();
-  Ops cur = read_ops(0);
+  AOps cur = read_a(0);
+  BOps curb;
+  if constexpr (C::RA_B) curb = read_b(0);
   for (int step = 0;; ++step) {
     if (ls == 0) {
-      const uint8_t *info = lds + C::OFF_INFO + 512 * slot;
+      const uint8_t *info = lds + C::OFF_INFO + C::INFO * slot;
       const int4 it = *(const int4 *)info;
       e = it.x;
       ntok = it.z;
@@ -2317,39 +2333,49 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       nst = nst_of(e);
       int wi;
       prefill_tile(tau, RTL, rt, wi);
+      if constexpr (PH == PH_DOWN) {
 #pragma unroll
-      for (int st = 0; st < NT; ++st) {
-        eslot[st] = ((const int *)(info + 256))[min(16 * st + l16, ntok - 1)];
-        ew[st] = PH == PH_DOWN ? a.slot_w[eslot[st]] : 0.f;
+        for (int st = 0; st < NT; ++st) ew[st] = a.slot_w[((const int *)(info + 256))[min(16 * st + l16, ntok - 1)]];
       }
     }
     // Is there a stage after this one (this task's next, or the next task's first)?
     const bool last_stage = ls + 1 == nst;
     const int tau_n = last_stage ? tasks.next(tau) : tau;
     const bool more = !last_stage || tau_n < tasks.lim;
-    Ops nxt;
-    if (more) nxt = read_ops((step + 1) % S);
+    const int st_n = (step + 1) % S;
+    AOps nxt;
+    BOps nxtb;
+    if (more) {
+      nxt = read_a(st_n);
+      if constexpr (C::RA_B) nxtb = read_b(st_n);
+    }
+    if constexpr (!C::RA_B) curb = read_b(step % S);
     if constexpr (FMT == Q_BF16) {
-      const int c = ls >> 1;
+      const int c = (SCOLS * ls) >> 7;
+      auto steps = [&](f32x4 (&ac)[NM][NT]) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int v = 2 * (ls & 1) + j;
-        if (!F::step_ok(c, v, K)) break;
+        for (int j = 0; j < SPS; ++j) {
+          const int v = ((SCOLS * ls) & 127) / 32 + j;
+          if (!F::step_ok(c, v, K)) break;
 #pragma unroll
-        for (int m = 0; m < NM; ++m)
+          for (int m = 0; m < NM; ++m)
 #pragma unroll
-          for (int st = 0; st < NT; ++st)
+            for (int st = 0; st < NT; ++st)
 #pragma unroll
-            for (int hh = 0; hh < NH; ++hh)
-              acc[c & 1][m][st] = mfma(as_bf16x8(cur.w[0][m].w[j]), as_bf16x8(cur.b[0][st][hh][j]), acc[c & 1][m][st]);
-      }
+              for (int hh = 0; hh < NH; ++hh)
+                ac[m][st] = mfma(as_bf16x8(cur.w[0][m].w[j]), as_bf16x8(curb.b[0][st][hh][j]), ac[m][st]);
+        }
+      };
+      // Chain by chunk parity, with static register indices.
+      if (c & 1) steps(acc[1]);
+      else steps(acc[0]);
     } else {
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
         const int c = 2 * ls + p;
         if (64 * c >= K) break;
         chunk_mfma<FMT, NM, NT, NH>(acc[c & 1], cur.w[p], at_unused,
-                                    [&](int st, int hh, int v) { return cur.b[p][st][hh][v]; }, c, g, K);
+                                    [&](int st, int hh, int v) { return curb.b[p][st][hh][v]; }, c, g, K);
       }
     }
     if (last_stage) {
@@ -2357,21 +2383,23 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const ExpertGroup &grp = group_of(e);
       const int out_dim = PH == PH_UP ? grp.inter : H;
       const int rb = rt * C::ROWS + wave * 16 * RT;
+      const int *slots = (const int *)(lds + C::OFF_INFO + C::INFO * slot + 256);   // still this task's
 #pragma unroll
       for (int st = 0; st < NT; ++st) {
         if (16 * st + l16 >= ntok) continue;
+        const int es = slots[16 * st + l16];
 #pragma unroll
         for (int q = 0; q < RT; ++q) {
           if (rb + 16 * q >= out_dim) continue;
           if constexpr (PH == PH_UP) {
-            up_epilogue<FMT>(a, nullptr, grp, rb + 16 * q + 4 * g, eslot[st],
+            up_epilogue<FMT>(a, nullptr, grp, rb + 16 * q + 4 * g, es,
                              sum_chains(acc[0][q][st], acc[1][q][st]), sum_chains(acc[0][RT + q][st], acc[1][RT + q][st]));
           } else {
             const f32x4 r = sum_chains(acc[0][q][st], acc[1][q][st]);
             f32x4 o;
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) o[ii] = ew[st] * (r[ii] + 0.f);   // down_value's arithmetic
-            *(f32x4 *)(a.slot_out + (size_t)eslot[st] * H + rb + 16 * q + 4 * g) = o;
+            *(f32x4 *)(a.slot_out + (size_t)es * H + rb + 16 * q + 4 * g) = o;
           }
         }
       }
@@ -2385,6 +2413,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (!more) break;
     ring_barrier();
     cur = nxt;
+    if constexpr (C::RA_B) curb = nxtb;
   }
 }
 
@@ -2421,24 +2450,31 @@ template <int FMT> static DownSmallKernel down_small_k(int slots, bool one) {
   return down_small<FMT, decode_depth<FMT>(), 4, down_ks<FMT>(4)>;
 }
 
+// The ring kernel of a BF16 / MLX phase: 64-token work items (BF16 layers whose experts average
+// 64 or more tokens) or 32-token ones.
+template <int PH, int FMT> static GemmKernel ring_pick(int nt, size_t *lds) {
+  constexpr int RT = ring_rt<PH, FMT>();
+  if constexpr (FMT == Q_BF16) {
+    if (nt > 2) {
+      if (lds) *lds = Ring<PH, FMT, RT, 4>::LDS;
+      return prefill_ring<PH, FMT, RT, 4>;
+    }
+  }
+  if (lds) *lds = Ring<PH, FMT, RT, 2>::LDS;
+  return prefill_ring<PH, FMT, RT, 2>;
+}
+
 template <int PH, int FMT>
 static GemmKernel pick(int nt) {
   if constexpr (FMT == Q_MXFP4) return nt <= 2 ? prefill_mx2<PH, 1> : prefill_mx2<PH, 2>;
-  else return prefill_ring<PH, FMT, ring_rt<PH, FMT>()>;
+  else return ring_pick<PH, FMT>(nt, nullptr);
 }
 
 // Output rows per prefill workgroup: intermediates (gate-up) or hidden rows (down). The MXFP4
 // kernel covers 128 weight rows: 64 intermediates of the interleaved gate_up matrix.
 int gemm_rows_per_block(int quant, int phase) {
   if (quant == Q_MXFP4) return phase == PH_UP ? 64 : 128;
-  switch (quant) {
-  case Q_BF16: return phase == PH_UP ? Ring<PH_UP, Q_BF16, ring_rt<PH_UP, Q_BF16>()>::ROWS
-                                     : Ring<PH_DOWN, Q_BF16, ring_rt<PH_DOWN, Q_BF16>()>::ROWS;
-  case Q_MLX4: return phase == PH_UP ? Ring<PH_UP, Q_MLX4, ring_rt<PH_UP, Q_MLX4>()>::ROWS
-                                     : Ring<PH_DOWN, Q_MLX4, ring_rt<PH_DOWN, Q_MLX4>()>::ROWS;
-  default: return phase == PH_UP ? Ring<PH_UP, Q_MLX8, ring_rt<PH_UP, Q_MLX8>()>::ROWS
-                                 : Ring<PH_DOWN, Q_MLX8, ring_rt<PH_DOWN, Q_MLX8>()>::ROWS;
-  }
+  return 64 * (phase == PH_UP ? ring_rt<PH_UP, Q_BF16>() : ring_rt<PH_DOWN, Q_BF16>());
 }
 
 static GemmKernel gemm_kernel(int phase, int quant, int nt) {
@@ -2450,16 +2486,15 @@ static GemmKernel gemm_kernel(int phase, int quant, int nt) {
   }
 }
 
-// Dynamic LDS of the ring kernel of (phase, quant).
-static size_t ring_lds(int phase, int quant) {
+// Dynamic LDS of the ring kernel of (phase, quant, token tile).
+static size_t ring_lds(int phase, int quant, int nt) {
+  size_t lds = 0;
   switch (quant) {
-  case Q_BF16: return phase == PH_UP ? Ring<PH_UP, Q_BF16, ring_rt<PH_UP, Q_BF16>()>::LDS
-                                     : Ring<PH_DOWN, Q_BF16, ring_rt<PH_DOWN, Q_BF16>()>::LDS;
-  case Q_MLX4: return phase == PH_UP ? Ring<PH_UP, Q_MLX4, ring_rt<PH_UP, Q_MLX4>()>::LDS
-                                     : Ring<PH_DOWN, Q_MLX4, ring_rt<PH_DOWN, Q_MLX4>()>::LDS;
-  default: return phase == PH_UP ? Ring<PH_UP, Q_MLX8, ring_rt<PH_UP, Q_MLX8>()>::LDS
-                                 : Ring<PH_DOWN, Q_MLX8, ring_rt<PH_DOWN, Q_MLX8>()>::LDS;
+  case Q_BF16: (void)(phase == PH_UP ? ring_pick<PH_UP, Q_BF16>(nt, &lds) : ring_pick<PH_DOWN, Q_BF16>(nt, &lds)); break;
+  case Q_MLX4: (void)(phase == PH_UP ? ring_pick<PH_UP, Q_MLX4>(nt, &lds) : ring_pick<PH_DOWN, Q_MLX4>(nt, &lds)); break;
+  default: (void)(phase == PH_UP ? ring_pick<PH_UP, Q_MLX8>(nt, &lds) : ring_pick<PH_DOWN, Q_MLX8>(nt, &lds)); break;
   }
+  return lds;
 }
 
 static int device_cus() {
@@ -2505,14 +2540,15 @@ hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStrea
     static std::once_flag once;
     std::call_once(once, [] {
       for (int ph = 0; ph < 2; ++ph)
-        for (int q : {Q_BF16, Q_MLX4, Q_MLX8}) {
-          (void)hipFuncSetAttribute((const void *)gemm_kernel(ph, q, 2), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    160 * 1024);
-          (void)hipGetLastError();
-        }
+        for (int q : {Q_BF16, Q_MLX4, Q_MLX8})
+          for (int nt : {2, 4}) {
+            (void)hipFuncSetAttribute((const void *)gemm_kernel(ph, q, nt), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      160 * 1024);
+            (void)hipGetLastError();
+          }
     });
     if (a.max_work == 0) return hipSuccess;
-    hipExtLaunchKernelGGL(gemm_kernel(phase, quant, nt), dim3(device_cus()), dim3(512), ring_lds(phase, quant), s,
+    hipExtLaunchKernelGGL(gemm_kernel(phase, quant, nt), dim3(device_cus()), dim3(512), ring_lds(phase, quant, nt), s,
                           tm.start, tm.stop, 0, a);
     return hipGetLastError();
   }
