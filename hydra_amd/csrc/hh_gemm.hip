@@ -1742,23 +1742,25 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *slot_out, int
 // vmcnt((S−2)·L); the task switches' extra loads (work item and slot ids, fetched into LDS one and
 // two tasks ahead) only make that wait stricter. The arithmetic per output element is
 // prefill_mx2's: one chain over the chunks, the terms in order.
-template <int PH> struct Mx3 {
+// RR: 128-row halves of the weight tile (MR = 128·RR rows); TT: 32-token halves of the token tile.
+template <int PH, int RR, int TT> struct Mx3 {
   static constexpr int NTERM = PH == PH_UP ? NTX : NTH;
-  static constexpr int NTOK = 32, MR = 128;
+  static constexpr int NTOK = 32 * TT, MR = 128 * RR;
   static constexpr int B_INS = NTERM * NTOK / 8;            // 1 KB operand loads per chunk
   static constexpr int BPW = B_INS / 4;                     // per loader wave
   static constexpr int BS_DW = NTERM * NTOK;                // operand scale dwords per chunk
-  static constexpr int L = 2 + BPW + 1 + 1;                 // loads per loader wave per chunk
-  static constexpr int OFF_B = 8192;                        // after 8 weight tiles of 1 KB
+  static constexpr int L = 2 * RR + BPW + 1 + 1;            // loads per loader wave per chunk
+  static constexpr int OFF_B = 8192 * RR;                   // after 8·RR weight tiles of 1 KB
   static constexpr int OFF_BS = OFF_B + B_INS * 1024;
   static constexpr int OFF_SC = OFF_BS + 256 * ((BS_DW + 63) / 64);
-  static constexpr int STAGE = OFF_SC + 512;                // + 128 rows × 4 block-scale bytes
-  static constexpr int S = PH == PH_UP ? 8 : 7;
+  static constexpr int STAGE = OFF_SC + 512 * RR;           // + MR rows × 4 block-scale bytes
+  static constexpr int S_FIT = (150 * 1024 - 1792) / STAGE;
+  static constexpr int S = S_FIT > 8 ? 8 : S_FIT;
   static constexpr int OFF_INFO = S * STAGE;                // [3][64] work item (4 dwords used)
   static constexpr int OFF_ORDER = OFF_INFO + 3 * 256;      // [3][64] slot ids (32 used)
   static constexpr int OFF_JUNK = OFF_ORDER + 3 * 256;      // sink of loads no stage needs
   static constexpr int LDS = OFF_JUNK + 256;
-  static_assert(B_INS % 4 == 0 && BS_DW <= 256 && (S - 2) * L <= 63, "loader layout");
+  static_assert(B_INS % 4 == 0 && BS_DW <= 256 && NTOK <= 64 && S >= 3 && (S - 2) * L <= 63, "loader layout");
 };
 
 // Workgroup barrier without __syncthreads' release fence: the fence would make every wave wait for
@@ -1789,9 +1791,9 @@ struct Mx3Tasks {
   }
 };
 
-template <int PH>
+template <int PH, int RR, int TT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mx3(GemmArgs a) {
-  using C = Mx3<PH>;
+  using C = Mx3<PH, RR, TT>;
   constexpr int NTERM = C::NTERM, NTOK = C::NTOK, S = C::S, L = C::L;
   extern __shared__ __align__(16) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1831,7 +1833,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       lds_load4(a.order + it.y + min(lane, it.z - 1), order + 256 * slot);
     };
     // Per-task source pointers.
-    const uint8_t *asrc[2], *bsrc[C::BPW], *bssrc, *scsrc;
+    const uint8_t *asrc[2 * RR], *bsrc[C::BPW], *bssrc, *scsrc;
     auto start_task = [&](int tau, int slot) {
       int rt, wi;
       prefill_tile(tau, RT, rt, wi);
@@ -1846,8 +1848,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         return PH == PH_UP ? sl / a.slots : sl;
       };
 #pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int j = 2 * lw + k;   // 16-row tile of the chunk
+      for (int k = 0; k < 2 * RR; ++k) {
+        const int j = 2 * RR * lw + k;   // 16-row tile of the chunk
         asrc[k] = wblk + (size_t)min(r0 + 16 * j + l16, out_dim - 1) * (K / 2);
       }
 #pragma unroll
@@ -1862,18 +1864,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       // Block scales: one row's 4 bytes of a chunk per lane (4-byte loads from 2-byte-aligned
       // rows are exact; a 2-byte direct-to-LDS load would write a whole dword per lane).
-      scsrc = wsc + (size_t)min(r0 + min(lw, 1) * 64 + lane, out_dim - 1) * nsb;
+      scsrc = wsc + (size_t)min(r0 + min(lw, 2 * RR - 1) * 64 + lane, out_dim - 1) * nsb;
     };
     // Chunk c of the current task into stage st.
     auto issue = [&](int c, int st) {
       uint8_t *stg = lds + st * C::STAGE;
 #pragma unroll
-      for (int k = 0; k < 2; ++k)
-        lds_load16(asrc[k] + 16 * min(4 * c + g, nsb - 1), stg + 1024 * (2 * lw + k));
+      for (int k = 0; k < 2 * RR; ++k)
+        lds_load16(asrc[k] + 16 * min(4 * c + g, nsb - 1), stg + 1024 * (2 * RR * lw + k));
 #pragma unroll
       for (int k = 0; k < C::BPW; ++k) lds_load16(bsrc[k] + 128 * c, stg + C::OFF_B + 1024 * (lw * C::BPW + k));
       lds_load4(bssrc + 4 * c, lw * 64 < C::BS_DW ? stg + C::OFF_BS + 256 * lw : junk);
-      lds_load4(scsrc + 4 * c, lw < 2 ? stg + C::OFF_SC + 256 * lw : junk);
+      lds_load4(scsrc + 4 * c, lw < 2 * RR ? stg + C::OFF_SC + 256 * lw : junk);
     };
     // Prologue: work items of the first two tasks and the first task's slot ids, then the first
     // S−1 chunks.
@@ -1928,51 +1930,61 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 
   // ---- MFMA waves ----
+  // Wave (wr, wt): weight rows r0 + 64·RR·wr + 16j (j < 4·RR), tokens 16·TT·wt + 16·tt + l16.
   const int wr = wave & 1, wt = wave >> 1;
-  const int n = 16 * wt + l16;   // token of this lane's B column
-  f32x4 acc[4];
+  constexpr int NJ = 4 * RR;
+  f32x4 acc[NJ][TT];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) acc[j][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
   int tau = tasks.first(), slot = 0, c = 0;
-  int eslot = 0, ntok = 0, r0 = 0;
-  float ew = 0.f;
-  uint16_t braw[4][4];   // bias bits of the lane's rows, loaded at the task's start, used at its end
+  int ntok = 0, r0 = 0;
+  int eslot[TT];
+  float ew[TT];
+  uint16_t braw[NJ][4];   // bias bits of the lane's rows, loaded at the task's start, used at its end
   auto task_begin = [&]() {
     int rt, wi;
     prefill_tile(tau, RT, rt, wi);
     const int4 it = item_of(slot);
     r0 = rt * C::MR;
     ntok = it.z;
-    eslot = ((const int *)(order + 256 * slot))[min(n, ntok - 1)];
-    ew = PH == PH_DOWN ? a.slot_w[eslot] : 0.f;
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      eslot[tt] = ((const int *)(order + 256 * slot))[min(16 * TT * wt + 16 * tt + l16, ntok - 1)];
+      ew[tt] = PH == PH_DOWN ? a.slot_w[eslot[tt]] : 0.f;
+    }
     // Unconditional loads (a branch on expert_bias would make the compiler wait for them here).
     const uint16_t *bp = (const uint16_t *)(grp.blobs + (size_t)it.x * grp.stride + grp.off[PH == PH_UP ? 2 : 5]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) braw[j][ii] = bp[min(r0 + 64 * wr + 16 * j + 4 * g + ii, out_dim - 1)];
+      for (int ii = 0; ii < 4; ++ii) braw[j][ii] = bp[min(r0 + 64 * RR * wr + 16 * j + 4 * g + ii, out_dim - 1)];
   };
   // Operands of a chunk, read from its stage one step ahead of its MFMAs (raw: the chunk's masks
   // are applied at use).
   struct Ops {
-    u32x4 w[4], blo[NTERM], bhi[NTERM];
-    uint32_t sa[4], bs[NTERM];
+    u32x4 w[NJ], blo[NTERM][TT], bhi[NTERM][TT];
+    uint32_t sa[NJ], bs[NTERM][TT];
   };
   auto read_ops = [&](int st) {
     const uint8_t *stg = lds + st * C::STAGE;
     Ops o;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      o.w[j] = *(const u32x4 *)(stg + 1024 * (4 * wr + j) + 16 * lane);
-      o.sa[j] = stg[C::OFF_SC + 4 * (64 * wr + 16 * j + l16) + g];
+    for (int j = 0; j < NJ; ++j) {
+      o.w[j] = *(const u32x4 *)(stg + 1024 * (NJ * wr + j) + 16 * lane);
+      o.sa[j] = stg[C::OFF_SC + 4 * (64 * RR * wr + 16 * j + l16) + g];
     }
     const u32x4 *sb = (const u32x4 *)(stg + C::OFF_B);
 #pragma unroll
-    for (int t = 0; t < NTERM; ++t) {
-      o.blo[t] = sb[(t * NTOK + n) * 8 + (g ^ (n & 7))];
-      o.bhi[t] = sb[(t * NTOK + n) * 8 + ((4 + g) ^ (n & 7))];
-      o.bs[t] = (((const uint32_t *)(stg + C::OFF_BS))[t * NTOK + n] >> (8 * g)) & 0xFFu;
-    }
+    for (int t = 0; t < NTERM; ++t)
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+        const int n = 16 * TT * wt + 16 * tt + l16;
+        o.blo[t][tt] = sb[(t * NTOK + n) * 8 + (g ^ (n & 7))];
+        o.bhi[t][tt] = sb[(t * NTOK + n) * 8 + ((4 + g) ^ (n & 7))];
+        o.bs[t][tt] = (((const uint32_t *)(stg + C::OFF_BS))[t * NTOK + n] >> (8 * g)) & 0xFFu;
+      }
     return o;
   };
   ring_barrier();
@@ -1985,16 +1997,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const bool ok = 128 * c + 32 * g < K;
       const int k0 = 128 * c + 16 * g;
 #pragma unroll
-      for (int t = 0; t < NTERM; ++t) {
-        // Lanes past K take zero weights; their scale byte may be any byte of the blob, so 2^0
-        // (the product is the same signed zero).
-        const u32x4 blo = k0 >= K ? u32x4{0u, 0u, 0u, 0u} : cur.blo[t];
-        const u32x4 bhi = k0 + 64 >= K ? u32x4{0u, 0u, 0u, 0u} : cur.bhi[t];
-        const uint32_t bs = ok ? cur.bs[t] : 127u;
+      for (int t = 0; t < NTERM; ++t)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[j] = smfma(ok ? cur.w[j] : u32x4{0u, 0u, 0u, 0u}, blo, bhi, ok ? cur.sa[j] : 127u, bs, acc[j]);
-      }
+        for (int tt = 0; tt < TT; ++tt) {
+          // Lanes past K take zero weights; their scale byte may be any byte of the blob, so 2^0
+          // (the product is the same signed zero).
+          const u32x4 blo = k0 >= K ? u32x4{0u, 0u, 0u, 0u} : cur.blo[t][tt];
+          const u32x4 bhi = k0 + 64 >= K ? u32x4{0u, 0u, 0u, 0u} : cur.bhi[t][tt];
+          const uint32_t bs = ok ? cur.bs[t][tt] : 127u;
+#pragma unroll
+          for (int j = 0; j < NJ; ++j)
+            acc[j][tt] = smfma(ok ? cur.w[j] : u32x4{0u, 0u, 0u, 0u}, blo, bhi, ok ? cur.sa[j] : 127u, bs, acc[j][tt]);
+        }
     }
     const bool more = step + 1 < nsteps;
     if (++c < nch) {
@@ -2004,48 +2018,56 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     // ---- epilogue of the task ----
     c = 0;
-    const int rw = r0 + 64 * wr;
-    float bias[4][4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int tt = 0; tt < TT; ++tt) {
+      const int n = 16 * TT * wt + 16 * tt + l16;
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) bias[j][ii] = a.expert_bias ? bf16_bits_to_f32(braw[j][ii]) : 0.f;
-    if (rw < out_dim) {
-      if constexpr (PH == PH_UP) {
-        float v[8];
+      for (int h = 0; h < RR; ++h) {
+        const int rw = r0 + 64 * RR * wr + 64 * h;   // a 64-row block: 32 intermediates of gate-up
+        if (rw >= out_dim) continue;
+        float bias[4][4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const f32x4 d = acc[j];
-          v[2 * j] = activate(a.act, d[0] + bias[j][0], d[1] + bias[j][1], a.alpha, a.limit);
-          v[2 * j + 1] = activate(a.act, d[2] + bias[j][2], d[3] + bias[j][3], a.alpha, a.limit);
-        }
-        uint32_t hq[NTH][2], sbq[NTH];
-        quant_block<NTH>(v, hq, sbq);
-        if (n < ntok) {
-          const int i0 = rw / 2;
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-          for (int t = 0; t < NTH; ++t) {
-            uint8_t *row = a.hq + ((size_t)eslot * NTH + t) * a.hld + i0 + 2 * g;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) *(uint16_t *)(row + 8 * j) = (uint16_t)(hq[t][j >> 1] >> (16 * (j & 1)));
-            if (g == 0) a.hs[((size_t)eslot * NTH + t) * (a.hld / 32) + i0 / 32] = (uint8_t)sbq[t];
-          }
-        }
-      } else {
-        if (n < ntok) {
+          for (int ii = 0; ii < 4; ++ii) bias[j][ii] = a.expert_bias ? bf16_bits_to_f32(braw[4 * h + j][ii]) : 0.f;
+        if constexpr (PH == PH_UP) {
+          float v[8];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const int h0 = rw + 16 * j + 4 * g;
-            f32x4 o;
+            const f32x4 d = acc[4 * h + j][tt];
+            v[2 * j] = activate(a.act, d[0] + bias[j][0], d[1] + bias[j][1], a.alpha, a.limit);
+            v[2 * j + 1] = activate(a.act, d[2] + bias[j][2], d[3] + bias[j][3], a.alpha, a.limit);
+          }
+          uint32_t hq[NTH][2], sbq[NTH];
+          quant_block<NTH>(v, hq, sbq);
+          if (n < ntok) {
+            const int i0 = rw / 2;
 #pragma unroll
-            for (int ii = 0; ii < 4; ++ii) o[ii] = ew * (acc[j][ii] + bias[j][ii]);   // down_value's arithmetic
-            *(f32x4 *)(a.slot_out + (size_t)eslot * H + h0) = o;
+            for (int t = 0; t < NTH; ++t) {
+              uint8_t *row = a.hq + ((size_t)eslot[tt] * NTH + t) * a.hld + i0 + 2 * g;
+#pragma unroll
+              for (int j = 0; j < 4; ++j) *(uint16_t *)(row + 8 * j) = (uint16_t)(hq[t][j >> 1] >> (16 * (j & 1)));
+              if (g == 0) a.hs[((size_t)eslot[tt] * NTH + t) * (a.hld / 32) + i0 / 32] = (uint8_t)sbq[t];
+            }
+          }
+        } else {
+          if (n < ntok) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int h0 = rw + 16 * j + 4 * g;
+              f32x4 o;
+#pragma unroll
+              for (int ii = 0; ii < 4; ++ii) o[ii] = ew[tt] * (acc[4 * h + j][tt][ii] + bias[j][ii]);   // down_value's arithmetic
+              *(f32x4 *)(a.slot_out + (size_t)eslot[tt] * H + h0) = o;
+            }
           }
         }
       }
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) acc[j][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
     tau = tasks.next(tau);
     slot = slot == 2 ? 0 : slot + 1;
     if (more) ring_barrier();
@@ -2508,32 +2530,40 @@ static int device_cus() {
   return ncu;
 }
 
-// Whether prefill_mx3 takes a phase: MXFP4 without a shared expert, 32-token work items, and rows
-// of at least S chunks (task switches are prefetched one task ahead inside the chunk ring).
+// Whether prefill_mx3 takes a phase: MXFP4 without a shared expert, work items of 32 tokens, and
+// rows of at least S chunks (task switches are prefetched one task ahead inside the chunk ring).
+// Gate-up over batches of 64 or more work items takes 256-row tiles (twice the products per staged
+// byte); down, and smaller batches, 128-row tiles (down's deeper ring measured faster).
+template <int PH, int RR, int TT> static bool mx3_fits(const GemmArgs &a) {
+  const int K = PH == PH_UP ? a.hidden : a.grp[0].inter;
+  return (K + 127) / 128 >= Mx3<PH, RR, TT>::S;
+}
+static bool mx3_wide(int phase, const GemmArgs &a) { return phase == PH_UP && a.max_work >= 64; }
 static bool use_mx3(int phase, const GemmArgs &a, int nt) {
   if (a.slots != a.top_k || nt != 2) return false;
-  const int K = phase == PH_UP ? a.hidden : a.grp[0].inter;
-  return (K + 127) / 128 >= (phase == PH_UP ? Mx3<PH_UP>::S : Mx3<PH_DOWN>::S);
+  if (!mx3_wide(phase, a)) return phase == PH_UP ? mx3_fits<PH_UP, 1, 1>(a) : mx3_fits<PH_DOWN, 1, 1>(a);
+  return mx3_fits<PH_UP, 2, 1>(a);
+}
+
+template <int PH, int RR, int TT> static hipError_t launch_mx3(GemmArgs a, hipStream_t s, Timing tm) {
+  static std::once_flag once;
+  std::call_once(once, [] {
+    (void)hipFuncSetAttribute((const void *)prefill_mx3<PH, RR, TT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024);
+    (void)hipGetLastError();
+  });
+  // Row tiles of this variant: MR weight rows (MR / 2 intermediates of the interleaved gate_up).
+  constexpr int rows = PH == PH_UP ? Mx3<PH, RR, TT>::MR / 2 : Mx3<PH, RR, TT>::MR;
+  a.row_tiles = ((PH == PH_UP ? a.ldh : a.hidden) + rows - 1) / rows;
+  hipExtLaunchKernelGGL(prefill_mx3<PH, RR, TT>, dim3(device_cus()), dim3(512), Mx3<PH, RR, TT>::LDS, s, tm.start,
+                        tm.stop, 0, a);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStream_t s, Timing tm) {
   if (quant == Q_MXFP4 && use_mx3(phase, a, nt)) {
-    static int ncu = 0;
-    if (!ncu) {
-      int dev = 0;
-      (void)hipGetDevice(&dev);
-      if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu < 8) ncu = 256;
-      ncu &= ~7;   // the task order assumes 8 | gridDim
-      for (const void *k : {(const void *)prefill_mx3<PH_UP>, (const void *)prefill_mx3<PH_DOWN>}) {
-        (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        (void)hipGetLastError();
-      }
-    }
-    if (phase == PH_UP)
-      hipExtLaunchKernelGGL(prefill_mx3<PH_UP>, dim3(ncu), dim3(512), Mx3<PH_UP>::LDS, s, tm.start, tm.stop, 0, a);
-    else
-      hipExtLaunchKernelGGL(prefill_mx3<PH_DOWN>, dim3(ncu), dim3(512), Mx3<PH_DOWN>::LDS, s, tm.start, tm.stop, 0, a);
-    return hipGetLastError();
+    if (!mx3_wide(phase, a)) return phase == PH_UP ? launch_mx3<PH_UP, 1, 1>(a, s, tm) : launch_mx3<PH_DOWN, 1, 1>(a, s, tm);
+    return launch_mx3<PH_UP, 2, 1>(a, s, tm);
   }
   if (quant != Q_MXFP4) {
     // BF16 / MLX: the persistent ring kernel, one workgroup per compute unit.

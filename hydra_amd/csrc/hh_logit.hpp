@@ -111,4 +111,54 @@ __device__ __forceinline__ double pair_logit(const RouteArgs &a, int t, int e) {
   return v;
 }
 
+// exact_logit of R rows at once (the loads of all R rows of a 2048-column pass in flight
+// together): for each row the same per-lane arithmetic, so the same values bit for bit.
+template <bool gemma, int R>
+__device__ __forceinline__ void exact_logits_rows(const RouteArgs &a, const uint16_t *xr,
+                                                  const uint16_t *const (&wrow)[R], double norm,
+                                                  double root, double (&out)[R]) {
+  const int lane = threadIdx.x & 63, H = a.hidden;
+  double acc[R][4];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[r][u] = 0.0;
+  for (int base = 0; base < H; base += 2048) {
+    u32x4 xv[4], sv[4], wv[R][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int h = base + lane * 8 + 512 * u;
+      const int hc = min(h, H - 8);
+      const bool ok = h < H;
+      xv[u] = *(const u32x4 *)(xr + hc);
+      sv[u] = gemma ? *(const u32x4 *)(a.router_scale + hc) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        wv[r][u] = *(const u32x4 *)(wrow[r] + hc);
+        if (!ok) wv[r][u] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int sh = (k & 1) * 16;
+          const float xf = bf16_bits_to_f32((xv[u][k >> 1] >> sh) & 0xFFFF);
+          const float wf = bf16_bits_to_f32((wv[r][u][k >> 1] >> sh) & 0xFFFF);
+          if constexpr (gemma) {
+            const double xd = (((double)xf * norm) *
+                               (double)bf16_bits_to_f32((sv[u][k >> 1] >> sh) & 0xFFFF)) * root;
+            acc[r][u] = fma(xd, (double)wf, acc[r][u]);
+          } else {
+            acc[r][u] += (double)(xf * wf);
+          }
+        }
+      }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) out[r] = wave_sum_f64((acc[r][0] + acc[r][1]) + (acc[r][2] + acc[r][3]));
+}
+
 }  // namespace hh

@@ -291,17 +291,6 @@ __device__ __forceinline__ TokenScreen screen_token(const RouteArgs &a, int t, L
   return ts;
 }
 
-// Exact logit (bias included) of candidate e of token t (one wave).
-template <bool gemma>
-__device__ __forceinline__ double exact_candidate(const RouteArgs &a, int t, int e,
-                                                  const TokenScreen &ts) {
-  const double root = gemma ? pow((double)a.hidden, -0.5) : 1.0;
-  double v = exact_logit<gemma>(a, a.xr + (size_t)t * a.hidden, a.router_w + (size_t)e * a.hidden,
-                                ts.norm, root);
-  if (a.router_b) v += (double)bf16_bits_to_f32(a.router_b[e]);
-  return v;
-}
-
 // ---- large batches ---------------------------------------------------------------------------
 // A: one workgroup per (16-token tile, 16-expert tile), the 4 waves splitting K; writes the
 // screening logits lg32 [T][E] and, from the first token tile, ‖w_e‖.
@@ -344,10 +333,27 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
   const float *wn = a.wn;
   const TokenScreen ts = screen_token<gemma>(a, t, [&](int e) { return lg[e]; },
                                       [&](int e) { return wn[e]; }, s_cl[wave]);
+  // Exact logits of the candidates, four at a time (one memory latency per batch), inserted in
+  // ascending expert order.
   TopK tk;
-  for (int ci = 0; ci < ts.nc; ++ci) {
-    const int e = s_cl[wave][ci];
-    tk.insert(exact_candidate<gemma>(a, t, e, ts), e, a.top_k);
+  const double root = gemma ? pow((double)a.hidden, -0.5) : 1.0;
+  const uint16_t *xr = a.xr + (size_t)t * a.hidden;
+  for (int c0 = 0; c0 < ts.nc; c0 += 4) {
+    int e[4];
+    const uint16_t *rows[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      e[r] = s_cl[wave][min(c0 + r, ts.nc - 1)];
+      rows[r] = a.router_w + (size_t)e[r] * a.hidden;
+    }
+    double v[4];
+    exact_logits_rows<gemma, 4>(a, xr, rows, ts.norm, root, v);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (c0 + r >= ts.nc) break;
+      if (a.router_b) v[r] += (double)bf16_bits_to_f32(a.router_b[e[r]]);
+      tk.insert(v[r], e[r], a.top_k);
+    }
   }
   const double sg = a.shared_gate ? exact_logit<false>(a, a.x + (size_t)t * a.hidden, a.shared_gate, 1.0, 1.0) : 0.0;
   finish_token(a, t, tk, sg);

@@ -272,6 +272,25 @@ def test_prefill_equals_token_by_token_bit_for_bit(torch_dev, ctx, name):
     assert np.array_equal(np.concatenate(parts).view(np.uint32), y_all.view(np.uint32))
 
 
+def test_wide_prefill_tiles_equal_token_by_token_bit_for_bit(torch_dev, ctx):
+    """Batches of 64+ work items take the 256-row MXFP4 prefill tiles: still the decode bits."""
+    from hydra_amd.layer import MoELayer
+    desc = TINY["mxfp4-wide"]
+    say("prefill==decode mxfp4-wide T=300 (256-row tiles)")
+    layer = synth.make_layer(desc, seed=43)
+    T = 300                                  # 1200 assignments: ≥ 64 work items of 32 tokens
+    x = synth.make_tokens(desc.hidden, T, seed=44)
+    L = MoELayer(layer, ctx)
+    y_all, idx_all, _ = L.forward(x)
+    y_all = y_all.cpu().numpy()
+    ry, ridx, _, _ = O.moe_forward(layer, x[:8])
+    assert np.array_equal(idx_all.cpu().numpy()[:8], ridx)
+    assert rel_l2(y_all[:8], ry) < REL_L2
+    for t in range(0, T, 7):
+        y1 = L.forward(x[t:t + 1])[0].cpu().numpy()[0]
+        assert np.array_equal(y1.view(np.uint32), y_all[t].view(np.uint32)), t
+
+
 def test_layer_is_deterministic_and_order_independent(torch_dev, ctx):
     from hydra_amd.layer import MoELayer
     desc = TINY["mxfp4"]
