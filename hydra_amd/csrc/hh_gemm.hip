@@ -2075,6 +2075,330 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
+// ---- prefill, MXFP4: weight rows in registers, token operand through an LDS ring -----------------
+// prefill_mx3's persistent task order and loader protocol, with the weight operand taken out of
+// LDS: each MFMA wave owns 64 distinct weight rows of the task's 256-row tile (one 32-intermediate
+// block of gate-up) and streams them straight into a DA-deep register ring that runs across task
+// boundaries (the wave reads the next task's work item from the loaders' LDS copy when its stream
+// crosses into it). The loaders only stage the 32 tokens' fp8 terms, their scales and the weight
+// rows' block scales, so a stage is ~9 KB and the ring holds S = 12 of them: with the weight
+// rows in the register file, about twice as many bytes are in flight per compute unit as when
+// everything passes through LDS. Per output element the arithmetic is the canonical one.
+template <int PH> struct MxA {   // PH_UP (down's three terms leave too few registers)
+  static constexpr int NTERM = PH == PH_UP ? NTX : NTH;
+  static constexpr int NTOK = 32, MR = 256, NJ = 4, DA = 6;
+  static constexpr int B_INS = NTERM * NTOK / 8;            // 1 KB operand loads per chunk
+  static constexpr int BPW = B_INS / 4;                     // per loader wave
+  static constexpr int BS_DW = NTERM * NTOK;                // operand scale dwords per chunk
+  static constexpr int L = BPW + 1 + 1;                     // loads per loader wave per chunk
+  static constexpr int OFF_BS = B_INS * 1024;
+  static constexpr int OFF_SC = OFF_BS + 256 * ((BS_DW + 63) / 64);
+  static constexpr int STAGE = OFF_SC + 4 * 256;            // + 256 rows × 4 block-scale bytes
+  static constexpr int S = 12;
+  static constexpr int OFF_INFO = S * STAGE;                // [3][64] work item (4 dwords used)
+  static constexpr int OFF_ORDER = OFF_INFO + 3 * 256;      // [3][64] slot ids (32 used)
+  static constexpr int OFF_BIAS = OFF_ORDER + 3 * 256;      // [3][256] bf16 bias of the tile's rows
+  static constexpr int OFF_JUNK = OFF_BIAS + 3 * 512;       // sink of loads no stage needs
+  static constexpr int LDS = OFF_JUNK + 256;
+  static_assert(B_INS % 4 == 0 && BS_DW <= 256 && (S - 2) * L <= 63 && DA % 2 == 0 && LDS <= 160 * 1024, "loader layout");
+};
+
+template <int PH>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mxa(GemmArgs a) {
+  using C = MxA<PH>;
+  constexpr int NTERM = C::NTERM, NTOK = C::NTOK, S = C::S, L = C::L, NJ = C::NJ, DA = C::DA;
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, l16 = lane & 15;
+  const ExpertGroup &grp = a.grp[0];
+  const int I = grp.inter, H = a.hidden;
+  const int out_dim = PH == PH_UP ? 2 * I : H;
+  const int K = PH == PH_UP ? H : I;
+  const int nch = (K + 127) / 128, nsb = K / 32;
+  const int ld = PH == PH_UP ? a.xld : a.hld;
+  const uint8_t *qbase = PH == PH_UP ? a.xq : a.hq;
+  const uint8_t *sbase = PH == PH_UP ? a.xs : a.hs;
+  const int RT = a.row_tiles, rtx = (RT + 7) >> 3;
+  const int nwork = *a.n_work;
+  const Mx3Tasks tasks{(int)blockIdx.x, (int)gridDim.x, RT, 8 * rtx * nwork};
+  int nsteps = 0;
+  for (int tau = tasks.first(); tau < tasks.lim; tau = tasks.next(tau)) nsteps += nch;
+  if (nsteps == 0) return;
+  uint8_t *info = lds + C::OFF_INFO, *order = lds + C::OFF_ORDER, *junk = lds + C::OFF_JUNK;
+  auto item_of = [&](int slot) { return *(const int4 *)(info + 256 * slot); };
+
+  if (wave >= 4) {
+    // ---- loaders (prefill_mx3's, without the weight blocks) ----
+    const int lw = wave - 4;
+    auto fetch_info = [&](int tau, int slot) {
+      int rt, wi;
+      prefill_tile(min(tau, tasks.lim - 1), RT, rt, wi);
+      lds_load4((const int *)(a.work + min(wi, nwork - 1)) + min(lane, 3), info + 256 * slot);
+    };
+    // Slot ids and the tile rows' bias of a task whose work item has landed.
+    auto fetch_order = [&](int tau, int slot) {
+      const int4 it = item_of(slot);
+      lds_load4(a.order + it.y + min(lane, it.z - 1), order + 256 * slot);
+      int rt, wi;
+      prefill_tile(min(tau, tasks.lim - 1), RT, rt, wi);
+      const uint8_t *bp = grp.blobs + (size_t)it.x * grp.stride + grp.off[PH == PH_UP ? 2 : 5];
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        lds_load4(bp + 2 * min(rt * C::MR + 2 * (64 * k + lane), out_dim - 2), lds + C::OFF_BIAS + 512 * slot + 256 * k);
+    };
+    const uint8_t *bsrc[C::BPW], *bssrc, *scsrc;
+    auto start_task = [&](int tau, int slot) {
+      int rt, wi;
+      prefill_tile(tau, RT, rt, wi);
+      const int4 it = item_of(slot);
+      const int r0 = rt * C::MR;
+      const uint8_t *wsc = grp.blobs + (size_t)it.x * grp.stride + grp.off[PH == PH_UP ? 1 : 4];
+      const int *ord = (const int *)(order + 256 * slot);
+      auto row_of = [&](int n) {
+        const int sl = ord[min(n, it.z - 1)];
+        return PH == PH_UP ? sl / a.slots : sl;
+      };
+#pragma unroll
+      for (int k = 0; k < C::BPW; ++k) {
+        const int v = (lw * C::BPW + k) * 64 + lane;
+        const int t = v / (NTOK * 8), sl = v % (NTOK * 8), n = sl >> 3, sg = (sl & 7) ^ (n & 7);
+        bsrc[k] = qbase + ((size_t)row_of(n) * NTERM + t) * ld + 16 * sg;
+      }
+      {
+        const int d = min(lw * 64 + lane, C::BS_DW - 1), t = d / NTOK, n = d % NTOK;
+        bssrc = sbase + ((size_t)row_of(n) * NTERM + t) * (ld / 32);
+      }
+      // Block scales of rows r0 + 64·lw + lane: one row's 4 bytes of a chunk per lane.
+      scsrc = wsc + (size_t)min(r0 + lw * 64 + lane, out_dim - 1) * nsb;
+    };
+    auto issue = [&](int c, int st) {
+      uint8_t *stg = lds + st * C::STAGE;
+#pragma unroll
+      for (int k = 0; k < C::BPW; ++k) lds_load16(bsrc[k] + 128 * c, stg + 1024 * (lw * C::BPW + k));
+      lds_load4(bssrc + 4 * c, lw * 64 < C::BS_DW ? stg + C::OFF_BS + 256 * lw : junk);
+      lds_load4(scsrc + 4 * c, stg + C::OFF_SC + 256 * lw);
+    };
+    int tq[3];
+    tq[0] = tasks.first();
+    tq[1] = tasks.next(tq[0]);
+    tq[2] = tasks.next(tq[1]);
+    fetch_info(tq[0], 0);
+    fetch_info(tq[1], 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    fetch_order(tq[0], 0);
+    fetch_order(tq[1], 1);
+    fetch_info(tq[2], 2);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    int slot = 0, lc = 0;
+    start_task(tq[0], 0);
+    int q = 0;
+    auto issue_next = [&]() {
+      issue(lc, q % S);
+      ++q;
+      if (++lc == nch) {
+        lc = 0;
+        tq[0] = tq[1];
+        tq[1] = tq[2];
+        tq[2] = tasks.next(tq[2]);
+        slot = slot == 2 ? 0 : slot + 1;
+        if (tq[0] < tasks.lim) {
+          start_task(tq[0], slot);
+          const int s1 = slot == 2 ? 0 : slot + 1, s2 = s1 == 2 ? 0 : s1 + 1;
+          fetch_order(tq[1], s1);
+          fetch_info(tq[2], s2);
+        }
+      }
+    };
+    // One barrier per two chunks: at barrier k chunks 2k and 2k+1 have landed; after it the
+    // slots of chunks 2k−2 and 2k−1 (computed before it) take chunks 2k+S−2 and 2k+S−1.
+    for (int u = 0; u < S - 2 && q < nsteps; ++u) issue_next();
+    if (q >= S - 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"((S - 4) * L) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const int nbar = (nsteps + 1) / 2;
+    for (int k = 0; k < nbar; ++k) {
+      ring_barrier();
+      if (q + 2 <= nsteps) {
+        issue_next();
+        issue_next();
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"((S - 4) * L) : "memory");
+      } else {
+        while (q < nsteps) issue_next();
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+    }
+    return;
+  }
+
+  // ---- MFMA waves: rows 64·wave .. +63 of the tile (NJ = 4 tiles of 16), tokens 0..31 ----
+  constexpr int TT = 2;
+  f32x4 acc[NJ][TT];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) acc[j][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Weight stream: chunk qa (of this workgroup's flat chunk sequence) of the load task.
+  int la_tau = tasks.first(), la_slot = 0, la_c = 0;
+  const uint8_t *arow[NJ];
+  auto la_rows = [&]() {
+    int rt, wi;
+    prefill_tile(la_tau, RT, rt, wi);
+    const int4 it = item_of(la_slot);
+    const uint8_t *wblk = grp.blobs + (size_t)it.x * grp.stride + grp.off[PH == PH_UP ? 0 : 3];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      arow[j] = wblk + (size_t)min(rt * C::MR + 64 * wave + 16 * j + l16, out_dim - 1) * (K / 2);
+  };
+  u32x4 ar[DA][NJ];
+  // Unconditional: past the last task the stream re-reads the last task's rows (never used). A
+  // load under a branch becomes a copy at the merge, which waits for the data: the ring would be
+  // one chunk deep.
+  auto load_a = [&](u32x4 (&dst)[NJ]) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) dst[j] = *(const u32x4 *)(arow[j] + 16 * min(4 * la_c + g, nsb - 1));
+    if (la_tau >= tasks.lim) return;
+    if (++la_c == nch) {
+      la_c = 0;
+      la_tau = tasks.next(la_tau);
+      la_slot = la_slot == 2 ? 0 : la_slot + 1;
+      if (la_tau < tasks.lim) la_rows();
+    }
+  };
+  int tau = tasks.first(), slot = 0, c = 0;
+  int ntok = 0, r0 = 0;
+  int eslot[TT];
+  float ew[TT];
+  auto task_begin = [&]() {
+    int rt, wi;
+    prefill_tile(tau, RT, rt, wi);
+    const int4 it = item_of(slot);
+    r0 = rt * C::MR;
+    ntok = it.z;
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      eslot[tt] = ((const int *)(order + 256 * slot))[min(16 * tt + l16, ntok - 1)];
+      ew[tt] = PH == PH_DOWN ? a.slot_w[eslot[tt]] : 0.f;
+    }
+  };
+  struct Ops {
+    u32x4 blo[NTERM][TT], bhi[NTERM][TT];
+    uint32_t sa[NJ], bs[NTERM][TT];
+  };
+  auto read_ops = [&](int st) {
+    const uint8_t *stg = lds + st * C::STAGE;
+    Ops o;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) o.sa[j] = stg[C::OFF_SC + 4 * (64 * wave + 16 * j + l16) + g];
+    const u32x4 *sb = (const u32x4 *)stg;
+#pragma unroll
+    for (int t = 0; t < NTERM; ++t)
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) {
+        const int n = 16 * tt + l16;
+        o.blo[t][tt] = sb[(t * NTOK + n) * 8 + (g ^ (n & 7))];
+        o.bhi[t][tt] = sb[(t * NTOK + n) * 8 + ((4 + g) ^ (n & 7))];
+        o.bs[t][tt] = (((const uint32_t *)(stg + C::OFF_BS))[t * NTOK + n] >> (8 * g)) & 0xFFu;
+      }
+    return o;
+  };
+  ring_barrier();   // the loaders' first task copies have landed
+  la_rows();
+#pragma unroll
+  for (int u = 0; u < DA; ++u) load_a(ar[u]);
+  bool done = false;
+  for (int k0 = 0; !done; k0 += DA) {
+#pragma unroll
+    for (int u = 0; u < DA; ++u) {
+      const int step = k0 + u;
+      if (c == 0) task_begin();
+      // The step's token operands (read after its barrier: registers go to the weight ring).
+      const Ops cur = read_ops(step % S);
+      const bool more = step + 1 < nsteps;
+      {
+        const bool ok = 128 * c + 32 * g < K;
+        const int kk = 128 * c + 16 * g;
+#pragma unroll
+        for (int t = 0; t < NTERM; ++t)
+#pragma unroll
+          for (int tt = 0; tt < TT; ++tt) {
+            const u32x4 blo = kk >= K ? u32x4{0u, 0u, 0u, 0u} : cur.blo[t][tt];
+            const u32x4 bhi = kk + 64 >= K ? u32x4{0u, 0u, 0u, 0u} : cur.bhi[t][tt];
+            const uint32_t bs = ok ? cur.bs[t][tt] : 127u;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+              acc[j][tt] = smfma(ok ? ar[u][j] : u32x4{0u, 0u, 0u, 0u}, blo, bhi, ok ? cur.sa[j] : 127u, bs, acc[j][tt]);
+          }
+      }
+      load_a(ar[u]);   // the chunk DA ahead into the slot just consumed
+      if (++c == nch) {
+        // ---- epilogue of the task ----
+        c = 0;
+        const int rw = r0 + 64 * wave;   // a 64-row block: 32 intermediates of gate-up
+        if (rw < out_dim) {
+          // The tile rows' bias from the task's LDS copy (rows past out_dim: another row's, never
+          // stored).
+          const uint8_t *bl = lds + C::OFF_BIAS + 512 * slot;
+          float bias[NJ][4];
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            const u32x2 bw = *(const u32x2 *)(bl + 2 * (64 * wave + 16 * j + 4 * g));
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii)
+              bias[j][ii] = a.expert_bias ? bf16_bits_to_f32((bw[ii >> 1] >> (16 * (ii & 1))) & 0xFFFFu) : 0.f;
+          }
+#pragma unroll
+          for (int tt = 0; tt < TT; ++tt) {
+            const int n = 16 * tt + l16;
+            if constexpr (PH == PH_UP) {
+              float v[8];
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const f32x4 d = acc[j][tt];
+                v[2 * j] = activate(a.act, d[0] + bias[j][0], d[1] + bias[j][1], a.alpha, a.limit);
+                v[2 * j + 1] = activate(a.act, d[2] + bias[j][2], d[3] + bias[j][3], a.alpha, a.limit);
+              }
+              uint32_t hq[NTH][2], sbq[NTH];
+              quant_block<NTH>(v, hq, sbq);
+              if (n < ntok) {
+                const int i0 = rw / 2;
+#pragma unroll
+                for (int t = 0; t < NTH; ++t) {
+                  uint8_t *row = a.hq + ((size_t)eslot[tt] * NTH + t) * a.hld + i0 + 2 * g;
+#pragma unroll
+                  for (int j = 0; j < 4; ++j) *(uint16_t *)(row + 8 * j) = (uint16_t)(hq[t][j >> 1] >> (16 * (j & 1)));
+                  if (g == 0) a.hs[((size_t)eslot[tt] * NTH + t) * (a.hld / 32) + i0 / 32] = (uint8_t)sbq[t];
+                }
+              }
+            } else {
+              if (n < ntok) {
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                  const int h0 = rw + 16 * j + 4 * g;
+                  f32x4 o;
+#pragma unroll
+                  for (int ii = 0; ii < 4; ++ii) o[ii] = ew[tt] * (acc[j][tt][ii] + bias[j][ii]);   // down_value's arithmetic
+                  *(f32x4 *)(a.slot_out + (size_t)eslot[tt] * H + h0) = o;
+                }
+              }
+            }
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int tt = 0; tt < TT; ++tt) acc[j][tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        tau = tasks.next(tau);
+        slot = slot == 2 ? 0 : slot + 1;
+      }
+      if (!more) {
+        done = true;
+        break;
+      }
+      if (step & 1) ring_barrier();   // one barrier per two chunks
+    }
+  }
+}
+
 // ---- prefill, BF16 and MLX affine: an LDS ring filled by loader waves -----------------------------
 // 8 waves, one workgroup per compute unit, persistent over the tasks τ = blockIdx, + gridDim, ...
 // (a task = one work item of ≤ 32 tokens × one row tile, in prefill_tile's XCD-aware order).
@@ -2560,7 +2884,30 @@ template <int PH, int RR, int TT> static hipError_t launch_mx3(GemmArgs a, hipSt
   return hipGetLastError();
 }
 
+// Whether prefill_mxa takes a phase: as prefill_mx3's wide variant, with rows of at least S
+// chunks (a wave's weight stream reads the next task's copy, which the loaders rewrite S chunks
+// later).
+static bool use_mxa(int phase, const GemmArgs &a, int nt) {
+  // Gate-up only: down's three operand terms leave too few registers for the weight ring.
+  if (phase != PH_UP || a.slots != a.top_k || nt != 2 || a.max_work < 64) return false;
+  const int K = phase == PH_UP ? a.hidden : a.grp[0].inter;
+  return (K + 127) / 128 >= MxA<PH_UP>::S;
+}
+
+template <int PH> static hipError_t launch_mxa(GemmArgs a, hipStream_t s, Timing tm) {
+  static std::once_flag once;
+  std::call_once(once, [] {
+    (void)hipFuncSetAttribute((const void *)prefill_mxa<PH>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    (void)hipGetLastError();
+  });
+  constexpr int rows = PH == PH_UP ? MxA<PH>::MR / 2 : MxA<PH>::MR;
+  a.row_tiles = ((PH == PH_UP ? a.ldh : a.hidden) + rows - 1) / rows;
+  hipExtLaunchKernelGGL(prefill_mxa<PH>, dim3(device_cus()), dim3(512), MxA<PH>::LDS, s, tm.start, tm.stop, 0, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStream_t s, Timing tm) {
+  if (quant == Q_MXFP4 && use_mxa(phase, a, nt)) return launch_mxa<PH_UP>(a, s, tm);
   if (quant == Q_MXFP4 && use_mx3(phase, a, nt)) {
     if (!mx3_wide(phase, a)) return phase == PH_UP ? launch_mx3<PH_UP, 1, 1>(a, s, tm) : launch_mx3<PH_DOWN, 1, 1>(a, s, tm);
     return launch_mx3<PH_UP, 2, 1>(a, s, tm);

@@ -272,11 +272,20 @@ def test_prefill_equals_token_by_token_bit_for_bit(torch_dev, ctx, name):
     assert np.array_equal(np.concatenate(parts).view(np.uint32), y_all.view(np.uint32))
 
 
-def test_wide_prefill_tiles_equal_token_by_token_bit_for_bit(torch_dev, ctx):
+WIDE = {
+    "mxfp4-wide": TINY["mxfp4-wide"],
+    # Gate-up rows of ≥ 12 chunks: the register-ring gate-up kernel.
+    "mxfp4-deep": F.MoEDesc(hidden=2048, intermediate=1024, experts=8, top_k=4, quant=F.QUANT_MXFP4,
+                            activation=F.ACT_SWIGLU_OAI, router=F.ROUTER_TOPK_SOFTMAX, expert_bias=1),
+}
+
+
+@pytest.mark.parametrize("name", list(WIDE))
+def test_wide_prefill_tiles_equal_token_by_token_bit_for_bit(torch_dev, ctx, name):
     """Batches of 64+ work items take the 256-row MXFP4 prefill tiles: still the decode bits."""
     from hydra_amd.layer import MoELayer
-    desc = TINY["mxfp4-wide"]
-    say("prefill==decode mxfp4-wide T=300 (256-row tiles)")
+    desc = WIDE[name]
+    say(f"prefill==decode {name} T=300 (256-row tiles)")
     layer = synth.make_layer(desc, seed=43)
     T = 300                                  # 1200 assignments: ≥ 64 work items of 32 tokens
     x = synth.make_tokens(desc.hidden, T, seed=44)
