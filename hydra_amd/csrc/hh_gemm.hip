@@ -287,55 +287,76 @@ __device__ __forceinline__ void chunk_mfma(f32x4 (&acc)[NM][NT], const typename 
       }
     }
   } else {
+    // MLX affine, one 64-column group: P = Σ q·x on the bf16 MFMA (steps v = 0, 1: word v of the
+    // lane's codes), G = Σ x on the MFMA with an all-ones A operand (every row of its D holds the
+    // column sums, so each lane gets its column's), then acc += s·P + b·G per D row
+    // (gemma.metal:234-236's factorisation). 4-bit codes enter the MFMA as bf16 (128 + q), two
+    // per instruction pair: ((w >> 4k) & 0x000F000F) | 0x43004300 holds codes k and k+4, so the
+    // B values are paired the same way (x_k, x_{k+4}) and the 128·G term goes into the bias:
+    // acc += s·P' + (b − 128·s)·G.
     u32x4 b[NT][NH][2];
 #pragma unroll
     for (int st = 0; st < NT; ++st)
 #pragma unroll
       for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
-        for (int v = 0; v < 2; ++v) b[st][hh][v] = bv(st, hh, v);
-    f32x4 P[NM][NT];
+        for (int v = 0; v < 2; ++v) {
+          const u32x4 raw = bv(st, hh, v);
+          if constexpr (FMT == Q_MLX4) {
+            // (x0,x1)(x2,x3)(x4,x5)(x6,x7) → (x0,x4)(x1,x5)(x2,x6)(x3,x7)
+            b[st][hh][v] = u32x4{__builtin_amdgcn_perm(raw[2], raw[0], 0x05040100u),
+                                 __builtin_amdgcn_perm(raw[2], raw[0], 0x07060302u),
+                                 __builtin_amdgcn_perm(raw[3], raw[1], 0x05040100u),
+                                 __builtin_amdgcn_perm(raw[3], raw[1], 0x07060302u)};
+          } else {
+            b[st][hh][v] = raw;
+          }
+        }
+    f32x4 P[NM][NT], G[NT];
 #pragma unroll
-    for (int m = 0; m < NM; ++m)
+    for (int st = 0; st < NT; ++st) {
+      G[st] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int st = 0; st < NT; ++st) P[m][st] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int m = 0; m < NM; ++m) P[m][st] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};   // bf16 1.0
 #pragma unroll
-    for (int v = 0; v < 2; ++v)
+    for (int v = 0; v < 2; ++v) {
+#pragma unroll
+      for (int st = 0; st < NT; ++st)
+#pragma unroll
+        for (int hh = 0; hh < NH; ++hh) G[st] = mfma(as_bf16x8(ones), as_bf16x8(b[st][hh][v]), G[st]);
 #pragma unroll
       for (int m = 0; m < NM; ++m) {
-        const bf16x8 av = F::decode(w[m], v);
+        bf16x8 av;
+        if constexpr (FMT == Q_MLX4) {
+          const uint32_t wv = w[m].w[v];
+          u32x4 r;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) r[k] = ((wv >> (4 * k)) & 0x000F000Fu) | 0x43004300u;
+          av = as_bf16x8(r);
+        } else {
+          av = F::decode(w[m], v);
+        }
 #pragma unroll
         for (int st = 0; st < NT; ++st)
 #pragma unroll
           for (int hh = 0; hh < NH; ++hh) P[m][st] = mfma(av, as_bf16x8(b[st][hh][v]), P[m][st]);
       }
-    // Σ of the group's 64 B values of each token column (x, or h_hi + h_lo), from the operands
-    // in registers: 16 per lane in a fixed order (hi then lo per step, steps in order), then
-    // across the lane groups.
-    float gsum[NT];
-#pragma unroll
-    for (int st = 0; st < NT; ++st) {
-      float s = 0.f;
-#pragma unroll
-      for (int v = 0; v < 2; ++v) {
-        s += sum8_bf16(b[st][0][v]);
-        if (NH > 1) s += sum8_bf16(b[st][NH - 1][v]);
-      }
-      gsum[st] = sum_lane_groups(s);
     }
-    // acc += s·P + b·Σ per D row (affine factorisation, gemma.metal:234-236); D row 4g + ii is
-    // the A row of lane 4g + ii.
+    // D row 4g + ii is the A row of lane 4g + ii: its scale and bias by shuffle.
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
         const uint32_t sbv = (uint32_t)__shfl((int)w[m].sb, 4 * g + ii);
         const float sc = bf16_bits_to_f32(sbv & 0xFFFF);
-        const float bi = bf16_bits_to_f32(sbv >> 16);
+        const float bi0 = bf16_bits_to_f32(sbv >> 16);
+        const float bi = FMT == Q_MLX4 ? __builtin_fmaf(-128.f, sc, bi0) : bi0;
 #pragma unroll
         for (int st = 0; st < NT; ++st) {
           acc[m][st][ii] = __builtin_fmaf(sc, P[m][st][ii], acc[m][st][ii]);
-          acc[m][st][ii] = __builtin_fmaf(bi, gsum[st], acc[m][st][ii]);
+          acc[m][st][ii] = __builtin_fmaf(bi, G[st][ii], acc[m][st][ii]);
         }
       }
   }
