@@ -563,12 +563,16 @@ __device__ __forceinline__ bool small_pick(const GemmArgs &a, const RouteArgs &r
                                            int *s_idx, SmallPick &pk) {
   __shared__ double s_lg[NW][64];
   __shared__ int s_ri[NW][kMaxTopK];
+  __shared__ int s_ci[NW][kFastCand];
+  __shared__ double s_cv[NW][kFastCand];
+  __shared__ double s_rv[NW][kMaxTopK];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = ra.tokens, E = a.experts, K = a.top_k;
   const bool has_shared = a.slots > K;
   for (int t = wave; t < T; t += NW) {
     const double *lg = ra.lg64 + (size_t)t * (E + 1);
-    const TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave]) : topk_exact(lg, E, K);
+    const TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave])
+                            : topk_fast(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave]);
     if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
     if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
   }
@@ -650,6 +654,23 @@ __global__ __launch_bounds__(512) void up_small(GemmArgs a, RouteArgs ra) {
   const int I = grp.inter;
   if (rt * UP_ROWS >= I) return;                     // whole workgroup past this group's rows
 
+  // Every token's x into LDS (row t), independent of the routing: the first batch of loads
+  // goes out before the selection.
+  const int ldx = H + LDS_PAD;
+  const int per_row = H / 8, nvec = T * per_row;
+  auto xsrc = [&](int v) {
+    const int t = v / per_row, qq = v - t * per_row;
+    return *(const u32x4 *)(a.x + (size_t)t * H + 8 * qq);
+  };
+  auto xdst = [&](int v, const u32x4 &val) {
+    const int t = v / per_row, qq = v - t * per_row;
+    *(u32x4 *)(s_x + (size_t)t * ldx + 8 * qq) = val;
+  };
+  constexpr int XB = 2;
+  u32x4 xr[XB];
+#pragma unroll
+  for (int k = 0; k < XB; ++k)
+    if (tid + 512 * k < nvec) xr[k] = xsrc(tid + 512 * k);
   SmallPick pk;
   if (!small_pick<8>(a, ra, u, shared_wg, s_idx, pk)) return;   // uniform over the workgroup
   const int e = pk.e, ntok = pk.ntok;
@@ -662,24 +683,8 @@ __global__ __launch_bounds__(512) void up_small(GemmArgs a, RouteArgs ra) {
   const int rb = rt * UP_ROWS + 16 * q;
   ATile<FMT> at[NM] = {tile_of<PH_UP, FMT>(blob, grp, rb, is_up, H, l16)};
   const int nch = (H + Fmt<FMT>::CHUNK - 1) / Fmt<FMT>::CHUNK;
-  const int ldx = H + LDS_PAD;
-  const int per_row = H / 8, nvec = ntok * per_row;
   auto token_of = [&](int j) { return nth_bit(tm, j); };
-  auto xsrc = [&](int v) {
-    const int j = v / per_row, qq = v - j * per_row;
-    return *(const u32x4 *)(a.x + (size_t)token_of(j) * H + 8 * qq);
-  };
-  auto xdst = [&](int v, const u32x4 &val) {
-    const int j = v / per_row, qq = v - j * per_row;
-    *(u32x4 *)(s_x + (size_t)j * ldx + 8 * qq) = val;
-  };
-  // First batch of x loads, then the weight stream, then the stores (which wait for the x loads
-  // only) and any further batches.
-  constexpr int XB = 2;
-  u32x4 xr[XB];
-#pragma unroll
-  for (int k = 0; k < XB; ++k)
-    if (tid + 512 * k < nvec) xr[k] = xsrc(tid + 512 * k);
+  // The weight stream, then the x stores (which wait for the x loads only) and any further batches.
   AStream<FMT, NM, DA> as(par, 2, nch);
   as.fill(at, nch, g, H);
 #pragma unroll
@@ -690,7 +695,7 @@ __global__ __launch_bounds__(512) void up_small(GemmArgs a, RouteArgs ra) {
 
   // Token column l16 = the l16-th token of the expert (padding columns repeat the last one).
   const int my_t = token_of(min(l16, ntok - 1));
-  const uint16_t *brow = s_x + (size_t)min(l16, ntok - 1) * ldx;
+  const uint16_t *brow = s_x + (size_t)my_t * ldx;
   f32x4 acc[NM][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
   as.run(at, nch, g, H, [&](const typename Fmt<FMT>::A (&w)[NM], int c) {
     const int col = Fmt<FMT>::bcol(c, g, H);
@@ -972,6 +977,9 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
   __shared__ float s_hv[SMALL_T][UP_ROWS];
   __shared__ double s_lg[4][64];
   __shared__ int s_ri[4][kMaxTopK];
+  __shared__ int s_ci[4][kFastCand];
+  __shared__ double s_cv[4][kFastCand];
+  __shared__ double s_rv[4][kMaxTopK];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -987,7 +995,8 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
   // Top-k of every token (wave w: tokens w, w + 4, ...); workgroup 0 writes the routing outputs.
   for (int t = wave; t < T; t += 4) {
     const double *lg = ra.lg64 + (size_t)t * (E + 1);
-    const TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave]) : topk_exact(lg, E, K);
+    const TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave])
+                            : topk_fast(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave]);
     if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
     if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
   }
@@ -3081,3 +3090,4 @@ hipError_t launch_combine(const float *slot_out, int slots, int H, int T, float 
 }
 
 }  // namespace hh
+

@@ -430,9 +430,13 @@ __global__ __launch_bounds__(256) void logits_small_kernel(RouteArgs a) {
 __global__ __launch_bounds__(256) void select_small_kernel(RouteArgs a) {
   const int wave = threadIdx.x >> 6;
   const int E1 = a.experts + 1;
+  __shared__ int s_ri[4][kMaxTopK];
+  __shared__ double s_rv[4][kMaxTopK];
+  __shared__ int s_ci[4][kFastCand];
+  __shared__ double s_cv[4][kFastCand];
   for (int t = wave; t < a.tokens; t += 4) {
     const double *lg = a.lg64 + (size_t)t * E1;
-    const TopK tk = topk_exact(lg, a.experts, a.top_k);
+    const TopK tk = topk_fast(lg, a.experts, a.top_k, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave]);
     finish_token(a, t, tk, a.shared_gate ? lg[a.experts] : 0.0);
   }
 }

@@ -138,6 +138,100 @@ __device__ __forceinline__ TopK topk_rank64(const double *lg, int E, int K, doub
   return tk;
 }
 
+// The value of lane l's v (wave-uniform l), without memory.
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// The same selection for E ≤ 512 (one wave; lane l holds logits l, l + 64, ...) without K
+// dependent rounds of shuffles. τ = the K-th largest of the 64 lane maxima bounds the K-th
+// largest logit from below (the K lanes with the largest maxima hold K logits ≥ τ), so every
+// selected logit is ≥ τ and a candidate's rank among the candidates {v ≥ τ} is its rank among
+// all logits (a logit < τ is never ahead of one ≥ τ). Both rankings count the values ahead
+// (larger, or equal with a smaller index) from registers by readlane, so ties resolve exactly as
+// topk_exact's. s_ri / s_rv[kMaxTopK] and s_ci[kFastCand] / s_cv[kFastCand] are the wave's LDS
+// scratch; more candidates than 64 (heavy ties) rank from LDS, more than kFastCand take
+// topk_exact.
+constexpr int kFastCand = 128;
+__device__ __forceinline__ TopK topk_fast(const double *lg, int E, int K, int *s_ri, double *s_rv, int *s_ci,
+                                          double *s_cv) {
+  const int lane = threadIdx.x & 63;
+  double v[8];
+  double m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int e = lane + 64 * j;
+    v[j] = e < E ? lg[min(e, E - 1)] : -INFINITY;
+    m = fmax(m, v[j]);
+  }
+  // τ: the lane maximum of rank K−1 among the 64 (ties by lane).
+  int rank = 0;
+  for (int j = 0; j < 64; ++j) {
+    const double o = readlane_f64(m, j);
+    rank += (o > m || (o == m && j < lane)) ? 1 : 0;
+  }
+  const uint64_t at_k = __ballot(rank == K - 1);
+  const double tau = readlane_f64(m, __ffsll((unsigned long long)at_k) - 1);
+  // Candidates v ≥ τ, compacted into LDS (lane-major within each j).
+  int nc = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) nc += __popcll(__ballot(lane + 64 * j < E && v[j] >= tau));
+  if (nc > kFastCand) return topk_exact(lg, E, K);
+  nc = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int e = lane + 64 * j;
+    const bool c = e < E && v[j] >= tau;
+    const uint64_t bm = __ballot(c);
+    if (c) {
+      const int pos = nc + __popcll(bm & ((1ull << lane) - 1ull));
+      s_ci[pos] = e;
+      s_cv[pos] = v[j];
+    }
+    nc += __popcll(bm);
+  }
+  __builtin_amdgcn_wave_barrier();
+  // Rank of each candidate among the candidates; ranks < K publish index and value.
+  for (int c0 = 0; c0 < nc; c0 += 64) {
+    const int ci = c0 + lane;
+    const bool mine = ci < nc;
+    const double cv = mine ? s_cv[ci] : 0.0;
+    const int ce = mine ? s_ci[ci] : 0;
+    int r = 0;
+    if (nc <= 64) {
+      for (int j = 0; j < nc; ++j) {
+        const double o = readlane_f64(cv, j);
+        const int oe = __builtin_amdgcn_readlane(ce, j);
+        r += (o > cv || (o == cv && oe < ce)) ? 1 : 0;
+      }
+    } else {
+      for (int j = 0; j < nc; ++j) {
+        const double o = s_cv[j];
+        const int oe = s_ci[j];
+        r += (o > cv || (o == cv && oe < ce)) ? 1 : 0;
+      }
+    }
+    if (mine && r < K) {
+      s_ri[r] = ce;
+      s_rv[r] = cv;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  TopK tk;
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r) {
+    if (r < K) {
+      tk.i[r] = s_ri[r];
+      tk.v[r] = s_rv[r];
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  return tk;
+}
+
 // Routing weight of rank `lane` (lanes ≥ K: 0) of one token's selection (whole wave): tk holds
 // the fp64 logits in rank order; `e` returns the lane's expert.
 // TOPK_SOFTMAX: softmax over the k selected logits (ReferenceOps.swift:178-182).
