@@ -2023,7 +2023,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (c == 0) task_begin();
     Ops nxt;
     if (step + 1 < nsteps) nxt = read_ops((step + 1) % S);
-    {
+    if (128 * (c + 1) <= K) {
+      // A whole chunk (every chunk but a partial last one): no lane masks.
+#pragma unroll
+      for (int t = 0; t < NTERM; ++t)
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+          for (int j = 0; j < NJ; ++j)
+            acc[j][tt] = smfma(cur.w[j], cur.blo[t][tt], cur.bhi[t][tt], cur.sa[j], cur.bs[t][tt], acc[j][tt]);
+    } else {
       const bool ok = 128 * c + 32 * g < K;
       const int k0 = 128 * c + 16 * g;
 #pragma unroll
@@ -2344,7 +2353,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // The step's token operands (read after its barrier: registers go to the weight ring).
       const Ops cur = read_ops(step % S);
       const bool more = step + 1 < nsteps;
-      {
+      if (128 * (c + 1) <= K) {
+        // A whole chunk (every chunk but a partial last one): no lane masks.
+#pragma unroll
+        for (int t = 0; t < NTERM; ++t)
+#pragma unroll
+          for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+              acc[j][tt] = smfma(ar[u][j], cur.blo[t][tt], cur.bhi[t][tt], cur.sa[j], cur.bs[t][tt], acc[j][tt]);
+      } else {
         const bool ok = 128 * c + 32 * g < K;
         const int kk = 128 * c + 16 * g;
 #pragma unroll
