@@ -31,68 +31,76 @@
 namespace hh {
 
 // Stable token→expert permutation of the whole batch by one workgroup of NW waves; `idx` is
-// the top-k table [T][K] (global or LDS).
+// the top-k table [T][K] (global or LDS). Wave w owns the contiguous assignment range
+// [w·R, (w+1)·R): pass 1 counts its assignments per expert, a scan over (expert, wave) gives every
+// wave its first position inside each expert's segment, pass 2 writes the positions (a lane's rank
+// among the earlier lanes of its 64-assignment chunk with the same expert, found by ballots over
+// the expert id's bits, plus the wave's running count). Two barriers in all, and (t, r) order is
+// kept inside each expert.
 template <int NW>
 __device__ __forceinline__ void dispatch_batch(const RouteArgs &a, const int32_t *idx) {
   constexpr int NT = 64 * NW;
   __shared__ int s_cnt[kMaxExperts + 1];
   __shared__ int s_off[kMaxExperts + 1];
   __shared__ int s_tiles[kMaxExperts + 1];
-  __shared__ int s_run[kMaxExperts];
-  __shared__ int s_wcnt[NW][kMaxExperts];
+  __shared__ int s_wc[NW][kMaxExperts];   // pass 1: count per (wave, expert); then running position
   __shared__ int s_wave[NW];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int E = a.experts, K = a.top_k, T = a.tokens, A = T * K;
   const int TN = a.tile_tokens;
-  for (int e = tid; e <= E; e += NT) s_cnt[e] = 0;
-  for (int e = tid; e < E; e += NT) {
-    s_run[e] = 0;
-    for (int w = 0; w < NW; ++w) s_wcnt[w][e] = 0;
+  const int R = ((A + NW - 1) / NW + 63) & ~63;     // assignments per wave, whole chunks
+  const int lo = min(wave * R, A), hi = min(lo + R, A);
+  for (int e = tid; e < NW * kMaxExperts; e += NT) (&s_wc[0][0])[e] = 0;
+  __syncthreads();
+  const int nbits = E > 1 ? 32 - __clz(E - 1) : 1;
+  // Peers of the lane's assignment inside its chunk (same expert), as a lane mask.
+  auto peers_of = [&](bool valid, int e) {
+    uint64_t peers = __ballot(valid);
+    for (int bb = 0; bb < nbits; ++bb) {
+      const uint64_t m = __ballot(valid && ((e >> bb) & 1));
+      peers &= ((e >> bb) & 1) ? m : ~m;
+    }
+    return peers;
+  };
+  for (int base = lo; base < hi; base += 64) {
+    const int i = base + lane;
+    const bool valid = i < hi;
+    const int e = valid ? idx[i] : 0;
+    const uint64_t peers = peers_of(valid, e);
+    if (valid && __popcll(peers & ((1ull << lane) - 1ull)) == 0) s_wc[wave][e] += __popcll(peers);
+    __builtin_amdgcn_wave_barrier();
   }
   __syncthreads();
-  for (int i = tid; i < A; i += NT) atomicAdd(&s_cnt[idx[i]], 1);
-  __syncthreads();
+  // Per expert: total count, and each wave's first position relative to the expert's segment.
   for (int e = tid; e < E; e += NT) {
-    s_off[e] = s_cnt[e];
-    s_tiles[e] = (s_cnt[e] + TN - 1) / TN;
+    int run = 0;
+    for (int w = 0; w < NW; ++w) {
+      const int c = s_wc[w][e];
+      s_wc[w][e] = run;
+      run += c;
+    }
+    s_cnt[e] = run;
+    s_off[e] = run;
+    s_tiles[e] = (run + TN - 1) / TN;
   }
   __syncthreads();
   block_exclusive_scan<NW>(s_off, E, s_wave);
   const int routed_tiles = block_exclusive_scan<NW>(s_tiles, E, s_wave);
-  // Stable scatter in chunks of NT assignments, (t, r) order preserved inside each expert:
-  // a lane's rank among the lanes of its wave with the same expert (matched by ballots over
-  // the expert id's bits), plus the counts of earlier waves and earlier chunks.
-  const int nbits = E > 1 ? 32 - __clz(E - 1) : 1;
-  for (int base = 0; base < A; base += NT) {
-    const int i = base + tid;
-    const bool valid = i < A;
+  for (int base = lo; base < hi; base += 64) {
+    const int i = base + lane;
+    const bool valid = i < hi;
     const int e = valid ? idx[i] : 0;
-    uint64_t peers = __ballot(valid);
-    for (int b = 0; b < nbits; ++b) {
-      uint64_t m = __ballot(valid && ((e >> b) & 1));
-      peers &= ((e >> b) & 1) ? m : ~m;
-    }
+    const uint64_t peers = peers_of(valid, e);
     const int rank = __popcll(peers & ((1ull << lane) - 1ull));
-    if (valid && rank == 0) s_wcnt[wave][e] = __popcll(peers);
-    __syncthreads();
     if (valid) {
-      int pos = s_off[e] + s_run[e] + rank;
-      for (int w = 0; w < wave; ++w) pos += s_wcnt[w][e];
       const int t = i / K, r = i - t * K;
-      a.order[pos] = t * a.slots + r;
+      a.order[s_off[e] + s_wc[wave][e] + rank] = t * a.slots + r;
     }
-    __syncthreads();
-    for (int x = tid; x < E; x += NT) {
-      int add = 0;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        add += s_wcnt[w][x];
-        s_wcnt[w][x] = 0;
-      }
-      s_run[x] += add;
-    }
-    __syncthreads();
+    __builtin_amdgcn_wave_barrier();
+    if (valid && rank == 0) s_wc[wave][e] += __popcll(peers);
+    __builtin_amdgcn_wave_barrier();
   }
+  __syncthreads();
   // Segments and work items (expert, first position, tokens), ascending expert order.
   for (int e = tid; e < E; e += NT) {
     a.seg[e] = s_off[e];
@@ -258,25 +266,48 @@ __device__ __forceinline__ TokenScreen screen_token(const RouteArgs &a, int t, L
       ub[j] = -INFINITY;
     }
   }
-  uint32_t taken = 0;
-  float theta = INFINITY;
-  for (int r = 0; r < K; ++r) {
-    float bv = -INFINITY;
-    int bi = 0x7FFFFFFF;
+  // θ = the K-th largest lower bound. τ = the K-th largest of the 64 lane maxima is ≤ θ (the K
+  // lanes with the largest maxima hold K bounds ≥ τ), so θ is the K-th largest of the bounds ≥ τ,
+  // ranked (larger, or equal and earlier) by readlane from lanes; cl[] is the scratch.
+  float mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int e = lane + 64 * j;
-      if (e < E && !(taken & (1u << j)) && (lb[j] > bv || bi == 0x7FFFFFFF)) { bv = lb[j]; bi = e; }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float ov = __shfl_xor(bv, o);
-      const int oi = __shfl_xor(bi, o);
-      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-    }
-    if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
-    theta = bv;
+  for (int j = 0; j < 8; ++j) mx = fmaxf(mx, lb[j]);
+  int rk = 0;
+  for (int j = 0; j < 64; ++j) {
+    const float o = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx), j));
+    rk += (o > mx || (o == mx && j < lane)) ? 1 : 0;
   }
+  const float tau = __builtin_bit_cast(
+      float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx), __ffsll((unsigned long long)__ballot(rk == K - 1)) - 1));
+  int nq = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const bool q = lane + 64 * j < E && lb[j] >= tau;
+    const uint64_t bm = __ballot(q);
+    if (q) cl[nq + __popcll(bm & ((1ull << lane) - 1ull))] = __builtin_bit_cast(int, lb[j]);
+    nq += __popcll(bm);
+  }
+  __builtin_amdgcn_wave_barrier();
+  float theta = -INFINITY;
+  for (int c0 = 0; c0 < nq; c0 += 64) {
+    const int ci = c0 + lane;
+    const float cv = ci < nq ? __builtin_bit_cast(float, cl[ci]) : -INFINITY;
+    int r = 0;
+    if (nq <= 64) {
+      for (int j = 0; j < nq; ++j) {
+        const float o = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cv), j));
+        r += (o > cv || (o == cv && j < ci)) ? 1 : 0;
+      }
+    } else {
+      for (int j = 0; j < nq; ++j) {
+        const float o = __builtin_bit_cast(float, cl[j]);
+        r += (o > cv || (o == cv && j < ci)) ? 1 : 0;
+      }
+    }
+    const uint64_t hit = __ballot(ci < nq && r == K - 1);
+    if (hit) theta = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cv), __ffsll((unsigned long long)hit) - 1));
+  }
+  __builtin_amdgcn_wave_barrier();
   int nc = 0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
