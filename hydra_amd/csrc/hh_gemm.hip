@@ -2123,9 +2123,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // rows' block scales, so a stage is ~9 KB and the ring holds S = 12 of them: with the weight
 // rows in the register file, about twice as many bytes are in flight per compute unit as when
 // everything passes through LDS. Per output element the arithmetic is the canonical one.
-template <int PH> struct MxA {   // PH_UP (down's three terms leave too few registers)
+// TT: 16-token tiles per wave (the whole token tile): 2 (32-token work items) or 4 (64).
+template <int PH, int TT_ = 2> struct MxA {   // PH_UP (down's three terms leave too few registers)
   static constexpr int NTERM = PH == PH_UP ? NTX : NTH;
-  static constexpr int NTOK = 32, MR = 256, NJ = 4, DA = 6;
+  static constexpr int TT = TT_, NTOK = 16 * TT, MR = 256, NJ = 4, DA = TT == 2 ? 6 : 2;
   static constexpr int B_INS = NTERM * NTOK / 8;            // 1 KB operand loads per chunk
   static constexpr int BPW = B_INS / 4;                     // per loader wave
   static constexpr int BS_DW = NTERM * NTOK;                // operand scale dwords per chunk
@@ -2133,18 +2134,18 @@ template <int PH> struct MxA {   // PH_UP (down's three terms leave too few regi
   static constexpr int OFF_BS = B_INS * 1024;
   static constexpr int OFF_SC = OFF_BS + 256 * ((BS_DW + 63) / 64);
   static constexpr int STAGE = OFF_SC + 4 * 256;            // + 256 rows × 4 block-scale bytes
-  static constexpr int S = 12;
+  static constexpr int S = TT == 2 ? 12 : 8;
   static constexpr int OFF_INFO = S * STAGE;                // [3][64] work item (4 dwords used)
-  static constexpr int OFF_ORDER = OFF_INFO + 3 * 256;      // [3][64] slot ids (32 used)
+  static constexpr int OFF_ORDER = OFF_INFO + 3 * 256;      // [3][64] slot ids (NTOK used)
   static constexpr int OFF_BIAS = OFF_ORDER + 3 * 256;      // [3][256] bf16 bias of the tile's rows
   static constexpr int OFF_JUNK = OFF_BIAS + 3 * 512;       // sink of loads no stage needs
   static constexpr int LDS = OFF_JUNK + 256;
   static_assert(B_INS % 4 == 0 && BS_DW <= 256 && (S - 2) * L <= 63 && DA % 2 == 0 && LDS <= 160 * 1024, "loader layout");
 };
 
-template <int PH>
+template <int PH, int TT_>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mxa(GemmArgs a) {
-  using C = MxA<PH>;
+  using C = MxA<PH, TT_>;
   constexpr int NTERM = C::NTERM, NTOK = C::NTOK, S = C::S, L = C::L, NJ = C::NJ, DA = C::DA;
   extern __shared__ __align__(16) uint8_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -2269,8 +2270,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     return;
   }
 
-  // ---- MFMA waves: rows 64·wave .. +63 of the tile (NJ = 4 tiles of 16), tokens 0..31 ----
-  constexpr int TT = 2;
+  // ---- MFMA waves: rows 64·wave .. +63 of the tile (NJ = 4 tiles of 16), every token ----
+  constexpr int TT = C::TT;
   f32x4 acc[NJ][TT];
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
@@ -2351,32 +2352,34 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const int step = k0 + u;
       if (c == 0) task_begin();
       // The step's token operands (read after its barrier: registers go to the weight ring).
-      const Ops cur = read_ops(step % S);
+      Ops cur = read_ops(step % S);
       const bool more = step + 1 < nsteps;
-      if (128 * (c + 1) <= K) {
-        // A whole chunk (every chunk but a partial last one): no lane masks.
-#pragma unroll
-        for (int t = 0; t < NTERM; ++t)
-#pragma unroll
-          for (int tt = 0; tt < TT; ++tt)
-#pragma unroll
-            for (int j = 0; j < NJ; ++j)
-              acc[j][tt] = smfma(ar[u][j], cur.blo[t][tt], cur.bhi[t][tt], cur.sa[j], cur.bs[t][tt], acc[j][tt]);
-      } else {
+      if (128 * (c + 1) > K) {
+        // A partial last chunk: lanes past K take zero weights and operand terms; their scale
+        // bytes may be any bytes, so 2^0 (the product is the same signed zero). Masked in place.
         const bool ok = 128 * c + 32 * g < K;
         const int kk = 128 * c + 16 * g;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+          if (!ok) ar[u][j] = u32x4{0u, 0u, 0u, 0u};
+          if (!ok) cur.sa[j] = 127u;
+        }
 #pragma unroll
         for (int t = 0; t < NTERM; ++t)
 #pragma unroll
           for (int tt = 0; tt < TT; ++tt) {
-            const u32x4 blo = kk >= K ? u32x4{0u, 0u, 0u, 0u} : cur.blo[t][tt];
-            const u32x4 bhi = kk + 64 >= K ? u32x4{0u, 0u, 0u, 0u} : cur.bhi[t][tt];
-            const uint32_t bs = ok ? cur.bs[t][tt] : 127u;
-#pragma unroll
-            for (int j = 0; j < NJ; ++j)
-              acc[j][tt] = smfma(ok ? ar[u][j] : u32x4{0u, 0u, 0u, 0u}, blo, bhi, ok ? cur.sa[j] : 127u, bs, acc[j][tt]);
+            if (kk >= K) cur.blo[t][tt] = u32x4{0u, 0u, 0u, 0u};
+            if (kk + 64 >= K) cur.bhi[t][tt] = u32x4{0u, 0u, 0u, 0u};
+            if (!ok) cur.bs[t][tt] = 127u;
           }
       }
+#pragma unroll
+      for (int t = 0; t < NTERM; ++t)
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt)
+#pragma unroll
+          for (int j = 0; j < NJ; ++j)
+            acc[j][tt] = smfma(ar[u][j], cur.blo[t][tt], cur.bhi[t][tt], cur.sa[j], cur.bs[t][tt], acc[j][tt]);
       load_a(ar[u]);   // the chunk DA ahead into the slot just consumed
       if (++c == nch) {
         // ---- epilogue of the task ----
@@ -2932,30 +2935,36 @@ template <int PH, int RR, int TT> static hipError_t launch_mx3(GemmArgs a, hipSt
   return hipGetLastError();
 }
 
-// Whether prefill_mxa takes a phase: as prefill_mx3's wide variant, with rows of at least S
-// chunks (a wave's weight stream reads the next task's copy, which the loaders rewrite S chunks
-// later).
+// Whether prefill_mxa takes a phase: gate-up of MXFP4 layers without a shared expert, 32-token
+// work items in batches of 64 or more, or 64-token ones; rows of at least S chunks (a wave's
+// weight stream reads the next task's copy, which the loaders rewrite S chunks later). Down's three
+// operand terms leave too few registers for the weight ring.
 static bool use_mxa(int phase, const GemmArgs &a, int nt) {
-  // Gate-up only: down's three operand terms leave too few registers for the weight ring.
-  if (phase != PH_UP || a.slots != a.top_k || nt != 2 || a.max_work < 64) return false;
-  const int K = phase == PH_UP ? a.hidden : a.grp[0].inter;
-  return (K + 127) / 128 >= MxA<PH_UP>::S;
+  if (phase != PH_UP || a.slots != a.top_k) return false;
+  if (nt == 2) return a.max_work >= 64 && (a.hidden + 127) / 128 >= MxA<PH_UP, 2>::S;
+  return nt == 4 && (a.hidden + 127) / 128 >= MxA<PH_UP, 4>::S;
 }
 
-template <int PH> static hipError_t launch_mxa(GemmArgs a, hipStream_t s, Timing tm) {
+template <int PH, int TT> static hipError_t launch_mxa(GemmArgs a, hipStream_t s, Timing tm) {
   static std::once_flag once;
   std::call_once(once, [] {
-    (void)hipFuncSetAttribute((const void *)prefill_mxa<PH>, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    (void)hipFuncSetAttribute((const void *)prefill_mxa<PH, TT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              160 * 1024);
     (void)hipGetLastError();
   });
-  constexpr int rows = PH == PH_UP ? MxA<PH>::MR / 2 : MxA<PH>::MR;
+  constexpr int rows = PH == PH_UP ? MxA<PH, TT>::MR / 2 : MxA<PH, TT>::MR;
   a.row_tiles = ((PH == PH_UP ? a.ldh : a.hidden) + rows - 1) / rows;
-  hipExtLaunchKernelGGL(prefill_mxa<PH>, dim3(device_cus()), dim3(512), MxA<PH>::LDS, s, tm.start, tm.stop, 0, a);
+  hipExtLaunchKernelGGL(prefill_mxa<PH, TT>, dim3(device_cus()), dim3(512), MxA<PH, TT>::LDS, s, tm.start, tm.stop, 0,
+                        a);
   return hipGetLastError();
 }
 
 hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStream_t s, Timing tm) {
-  if (quant == Q_MXFP4 && use_mxa(phase, a, nt)) return launch_mxa<PH_UP>(a, s, tm);
+  if (quant == Q_MXFP4 && use_mxa(phase, a, nt))
+    return nt == 2 ? launch_mxa<PH_UP, 2>(a, s, tm) : launch_mxa<PH_UP, 4>(a, s, tm);
+  if (quant == Q_MXFP4 && nt == 4 && phase == PH_DOWN && a.slots == a.top_k &&
+      (a.grp[0].inter + 127) / 128 >= Mx3<PH_DOWN, 1, 2>::S)
+    return launch_mx3<PH_DOWN, 1, 2>(a, s, tm);
   if (quant == Q_MXFP4 && use_mx3(phase, a, nt)) {
     if (!mx3_wide(phase, a)) return phase == PH_UP ? launch_mx3<PH_UP, 1, 1>(a, s, tm) : launch_mx3<PH_DOWN, 1, 1>(a, s, tm);
     return launch_mx3<PH_UP, 2, 1>(a, s, tm);

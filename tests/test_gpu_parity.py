@@ -274,15 +274,21 @@ def test_prefill_equals_token_by_token_bit_for_bit(torch_dev, ctx, name):
 
 WIDE = {
     "mxfp4-wide": TINY["mxfp4-wide"],
-    # Gate-up rows of ≥ 12 chunks: the register-ring gate-up kernel.
+    # Gate-up rows of ≥ 12 chunks: the register-ring gate-up kernel (64-token items at T=300: the
+    # experts average 150 tokens).
     "mxfp4-deep": F.MoEDesc(hidden=2048, intermediate=1024, experts=8, top_k=4, quant=F.QUANT_MXFP4,
+                            activation=F.ACT_SWIGLU_OAI, router=F.ROUTER_TOPK_SOFTMAX, expert_bias=1),
+    # Many experts (≈ 19 tokens each at T=300): 32-token items, the register-ring gate-up kernel's
+    # 32-token tiles and the 128-row down tiles.
+    "mxfp4-many": F.MoEDesc(hidden=2048, intermediate=1024, experts=64, top_k=4, quant=F.QUANT_MXFP4,
                             activation=F.ACT_SWIGLU_OAI, router=F.ROUTER_TOPK_SOFTMAX, expert_bias=1),
 }
 
 
 @pytest.mark.parametrize("name", list(WIDE))
 def test_wide_prefill_tiles_equal_token_by_token_bit_for_bit(torch_dev, ctx, name):
-    """Batches of 64+ work items take the 256-row MXFP4 prefill tiles: still the decode bits."""
+    """Large MXFP4 batches take the 256-row prefill tiles (32- or 64-token items): still the
+    decode bits."""
     from hydra_amd.layer import MoELayer
     desc = WIDE[name]
     say(f"prefill==decode {name} T=300 (256-row tiles)")
