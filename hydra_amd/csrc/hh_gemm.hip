@@ -632,12 +632,14 @@ constexpr int MX_ONE_CHUNKS = 24; // MXFP4 decode rows of at most this many 128-
 constexpr int kFusedMaxE = 128;   // experts of layers that take the fused decode kernel
 constexpr int LDS_PAD = 8;        // bf16 elements of padding per staged row (bank spread)
 
-// Grid: row tile rt (32 intermediates) × u, u < min(E, T·K) the distinct routed experts of the
-// batch, and the last u the shared expert when there is one. 8 waves: wave w takes tile
-// q = w & 1 (16 intermediates), gate (w & 2 = 0) or up rows, and chunk parity p = w >> 2 (the
-// even or odd chain of the canonical arithmetic).
-template <int FMT, int DA>
-__global__ __launch_bounds__(512) void up_small(GemmArgs a, RouteArgs ra) {
+// Grid: row tile rt (16·TPW intermediates) × u, u < min(E, T·K) the distinct routed experts of
+// the batch, and the last u the shared expert when there is one. 4·TPW waves: wave w takes tile
+// q (16 intermediates; w & 1 when TPW = 2), gate or up rows, and chunk parity p (the even or odd
+// chain of the canonical arithmetic). TPW = 1 gives twice the workgroups of half the size, which
+// spreads a decode step's few experts over more compute units.
+template <int FMT, int DA, int TPW = 2>
+__global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) {
+  constexpr int NTH = 256 * TPW, NWV = 4 * TPW, ROWS = 16 * TPW;
   constexpr int NM = 1;
   extern __shared__ __align__(16) uint16_t s_x[];   // [ntok][H + LDS_PAD]
   __shared__ int s_idx[SMALL_T * kMaxTopK];
@@ -652,7 +654,7 @@ __global__ __launch_bounds__(512) void up_small(GemmArgs a, RouteArgs ra) {
   const bool shared_wg = has_shared && u == (int)(gridDim.x / a.row_tiles) - 1;
   const ExpertGroup &grp = a.grp[shared_wg ? 1 : 0];
   const int I = grp.inter;
-  if (rt * UP_ROWS >= I) return;                     // whole workgroup past this group's rows
+  if (rt * ROWS >= I) return;                        // whole workgroup past this group's rows
 
   // Every token's x into LDS (row t), independent of the routing: the first batch of loads
   // goes out before the selection.
@@ -670,17 +672,17 @@ __global__ __launch_bounds__(512) void up_small(GemmArgs a, RouteArgs ra) {
   u32x4 xr[XB];
 #pragma unroll
   for (int k = 0; k < XB; ++k)
-    if (tid + 512 * k < nvec) xr[k] = xsrc(tid + 512 * k);
+    if (tid + NTH * k < nvec) xr[k] = xsrc(tid + NTH * k);
   SmallPick pk;
-  if (!small_pick<8>(a, ra, u, shared_wg, s_idx, pk)) return;   // uniform over the workgroup
+  if (!small_pick<NWV>(a, ra, u, shared_wg, s_idx, pk)) return;   // uniform over the workgroup
   const int e = pk.e, ntok = pk.ntok;
   const uint64_t tm = pk.tm;
   const uint8_t *blob = grp.blobs + (shared_wg ? 0 : (size_t)e * grp.stride);
 
-  const int q = wave & 1;
-  const bool is_up = (wave & 2) != 0;
-  const int par = wave >> 2;
-  const int rb = rt * UP_ROWS + 16 * q;
+  const int q = TPW == 2 ? (wave & 1) : 0;
+  const bool is_up = TPW == 2 ? (wave & 2) != 0 : (wave & 1) != 0;
+  const int par = TPW == 2 ? wave >> 2 : wave >> 1;
+  const int rb = rt * ROWS + 16 * q;
   ATile<FMT> at[NM] = {tile_of<PH_UP, FMT>(blob, grp, rb, is_up, H, l16)};
   const int nch = (H + Fmt<FMT>::CHUNK - 1) / Fmt<FMT>::CHUNK;
   auto token_of = [&](int j) { return nth_bit(tm, j); };
@@ -689,8 +691,8 @@ __global__ __launch_bounds__(512) void up_small(GemmArgs a, RouteArgs ra) {
   as.fill(at, nch, g, H);
 #pragma unroll
   for (int k = 0; k < XB; ++k)
-    if (tid + 512 * k < nvec) xdst(tid + 512 * k, xr[k]);
-  for (int base = 512 * XB; base < nvec; base += 512 * 4) stage_batch<4>(base, tid, 512, nvec, xsrc, xdst);
+    if (tid + NTH * k < nvec) xdst(tid + NTH * k, xr[k]);
+  for (int base = NTH * XB; base < nvec; base += NTH * 4) stage_batch<4>(base, tid, NTH, nvec, xsrc, xdst);
   __syncthreads();
 
   // Token column l16 = the l16-th token of the expert (padding columns repeat the last one).
@@ -2833,7 +2835,7 @@ template <int FMT> constexpr int decode_depth() { return FMT == Q_BF16 ? 4 : (FM
 constexpr int MX_ONE = MX_ONE_CHUNKS;
 template <int FMT> static UpSmallKernel up_small_k(bool one) {
   if constexpr (FMT == Q_MXFP4) return one ? up_small_mx<MX_ONE, true> : up_small_mx<16, false>;
-  else return up_small<FMT, decode_depth<FMT>()>;
+  else return up_small<FMT, decode_depth<FMT>(), 1>;
 }
 // Waves per slot of down_small: MXFP4's canonical arithmetic is one chain over K (one wave per
 // slot); the others split K by chunk parity over two waves when the workgroup has room.
@@ -3039,12 +3041,12 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
     (void)hipGetDevice(&dev);
     if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0) ncu = 256;
   }
-  a.row_tiles = a.ldh / UP_ROWS;
+  a.row_tiles = a.ldh / (mx ? UP_ROWS : 16);   // up_small: one 16-intermediate tile per workgroup
   const size_t lds_up = mx ? (size_t)T * NTX * mx_row_bytes(a.xld) + 64 * (a.hidden / 32)
                            : (size_t)T * (a.hidden + LDS_PAD) * 2;
   // MXFP4: persistent, about two workgroups per compute unit.
   const int up_grid = mx ? std::min(2 * ncu, a.row_tiles * maxu) : a.row_tiles * maxu;
-  hipExtLaunchKernelGGL(up, dim3(up_grid), dim3(mx ? 256 : 512), lds_up, s, tm_up.start, tm_up.stop, 0, a, ra);
+  hipExtLaunchKernelGGL(up, dim3(up_grid), dim3(256), lds_up, s, tm_up.start, tm_up.stop, 0, a, ra);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   a.row_tiles = a.hidden / 16;
