@@ -381,9 +381,10 @@ template <int FMT, int NM, int DA> struct AStream {
 #pragma unroll
     for (int m = 0; m < NM; ++m) Fmt<FMT>::load(s[slot][m], at[m].row, c, g, K);
   }
-  __device__ __forceinline__ void fill(const ATile<FMT> (&at)[NM], int nch, int g, int K) {
+  // The first P (default: all DA) stages; run_pf<ONE, P> issues the rest as it goes.
+  template <int P = DA> __device__ __forceinline__ void fill(const ATile<FMT> (&at)[NM], int nch, int g, int K) {
 #pragma unroll
-    for (int u = 0; u < DA; ++u) load(u, at, u, nch, g, K);
+    for (int u = 0; u < P; ++u) load(u, at, u, nch, g, K);
   }
   // Runs this wave's chunks through `body(stage, c)`.
   template <class Body>
@@ -404,11 +405,17 @@ template <int FMT, int NM, int DA> struct AStream {
   // conservative waits).
   // ONE: the caller guarantees one round from chunk 0 with stride 1 (n ≤ DA, c0 = 0, cs = 1), and
   // only that code is generated.
-  template <bool ONE = false, class Pre, class Body>
+  // P < DA (ONE only): the stream was filled with its first P chunks and chunk u + P is issued
+  // after chunk u is computed, so at most P loads of the wave are in flight. The memory system
+  // returns a saturating stream at the rate it accepts new loads, so the later chunks' data is
+  // not delayed, while the MFMAs of the early chunks overlap the stream and the workgroup's
+  // staging barrier (before the first chunk) waits only for loads issued ahead of it.
+  template <bool ONE = false, int P = DA, class Pre, class Body>
   __device__ __forceinline__ void run_pf(const ATile<FMT> (&at)[NM], int nch, int g, int K, Pre pre, Body body) {
+    static_assert(P == DA || ONE, "a partial fill needs the single-round stream");
     if (n <= 0) return;
     if constexpr (ONE) {
-      rounds<true, true>(at, nch, g, K, pre, body);
+      rounds<true, true, P>(at, nch, g, K, pre, body);
     } else {
       if (n <= DA && c0 == 0 && cs == 1) rounds<true, true>(at, nch, g, K, pre, body);
       else if (n <= DA) rounds<true, false>(at, nch, g, K, pre, body);
@@ -417,7 +424,7 @@ template <int FMT, int NM, int DA> struct AStream {
   }
   // UNIT: chunk u of the ring is chunk u of K (one round, first chunk 0, stride 1), so chunk
   // indices, and the operand offsets derived from them, are compile-time constants.
-  template <bool ONE, bool UNIT, class Pre, class Body>
+  template <bool ONE, bool UNIT, int P = DA, class Pre, class Body>
   __device__ __forceinline__ void rounds(const ATile<FMT> (&at)[NM], int nch, int g, int K, Pre pre, Body body) {
     auto op = pre(UNIT ? 0 : c0);
     for (int i0 = 0; i0 < n; i0 += DA) {
@@ -429,6 +436,9 @@ template <int FMT, int NM, int DA> struct AStream {
           const auto nx = pre(cn);
           body(s[u], UNIT ? u : c0 + cs * (i0 + u), op);
           op = nx;
+        }
+        if constexpr (P < DA) {
+          if (u + P < DA) load(u + P, at, u + P, nch, g, K);
         }
         if (more) load(u, at, i0 + u + DA, nch, g, K);
       }
@@ -629,6 +639,10 @@ __device__ __forceinline__ int rank_of(const int *s_idx, int t, int e, int K, bo
 constexpr int SMALL_T = 16;       // largest batch of the decode kernels
 constexpr int UP_ROWS = 32;       // intermediates per up_small workgroup (2 tiles × {gate, up})
 constexpr int MX_ONE_CHUNKS = 24; // MXFP4 decode rows of at most this many 128-column chunks stream in one round
+#ifndef HH_MX_PF
+#define HH_MX_PF 6
+#endif
+constexpr int MX_PF = HH_MX_PF;   // chunks a single-round MXFP4 decode wave issues before its staging barrier
 constexpr int kFusedMaxE = 128;   // experts of layers that take the fused decode kernel
 constexpr int LDS_PAD = 8;        // bf16 elements of padding per staged row (bank spread)
 
@@ -1037,8 +1051,9 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
     u32x4 bias = {0u, 0u, 0u, 0u};
     if (!is_up && a.expert_bias) bias = *(const u32x4 *)(blob + grp.off[2] + 4 * (rb + 4 * g));
     ATile<Q_MXFP4_W> at[NM] = {tile_of<PH_UP, Q_MXFP4_W>(blob, grp, rb, is_up, H, l16)};
+    constexpr int PF = ONE ? MX_PF : DA;
     AStream<Q_MXFP4_W, NM, DA> as(0, 1, nch);
-    as.fill(at, nch, g, H);
+    as.template fill<PF>(at, nch, g, H);
     if (x_pending) {
       xs.store_first();
       xs.rest();
@@ -1060,7 +1075,7 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
     const int my_t = nth_bit(tm, min(l16, ntok - 1));   // token of column l16 (padding repeats)
     const uint8_t *brow = s_xb + (size_t)my_t * NTX * RS;
     f32x4 acc[NM][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
-    as.template run_pf<ONE>(
+    as.template run_pf<ONE, PF>(
         at, nch, gi, H, [&](int c) { return mx_ops<NTX>(brow, RS, a.xld, my_sc, nsb, c, gi); },
         [&](const Fmt<Q_MXFP4_W>::A (&w)[NM], int c, const MxOps<NTX> &o) {
           chunk_mx1<NTX>(acc[0][0], w[0].w, o, c, gi, H);
@@ -1093,6 +1108,17 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
 }
 
 // ---- decode: down + combine -----------------------------------------------------------------------
+// Item order of down_small, XCD-aware: workgroups are dealt to the 8 XCDs round robin by index
+// and the grid is a multiple of 8, so item it runs on XCD it % 8. The T tokens of row tile rt
+// are consecutive items of one XCD (rt ≡ it (mod 8)): the tokens that share an expert read its
+// 16 rows at about the same time through the same L2 instead of once per token from HBM. Row
+// tiles are padded to a multiple of 8; padding items have rt ≥ the row tile count.
+__host__ __device__ constexpr int down_small_items(int row_tiles, int T) { return 8 * ((row_tiles + 7) / 8) * T; }
+__device__ __forceinline__ void down_small_item(int it, int T, int &rt, int &t) {
+  const int x = it & 7, j = it >> 3, jt = j / T;
+  t = j - jt * T;
+  rt = x + 8 * jt;
+}
 // Persistent: work items (16 hidden rows, token t) = it = blockIdx.x, blockIdx.x + gridDim.x, ...
 // Wave (r, p): slot r of the token (expert topk_idx[t][r], or the
 // shared expert), chunk parity p when KS = 2 (both chains in one wave when KS = 1). The epilogue
@@ -1109,10 +1135,12 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
   const int g = lane >> 4, l16 = lane & 15;
   const int S = a.slots, K = a.top_k, H = a.hidden, E = a.experts;
   const int T = a.max_work;              // tokens of the batch
-  const int nitems = a.row_tiles * T;
+  const int nitems = down_small_items(a.row_tiles, T);
   const int r = wave % S, par = wave / S;
   for (int it = blockIdx.x; it < nitems; it += gridDim.x) {
-  const int rt = it / T, t = it - rt * T;
+  int rt, t;
+  down_small_item(it, T, rt, t);
+  if (rt >= a.row_tiles) continue;       // padding item (uniform over the workgroup)
   const int slot = t * S + r;
   const int e = r < K ? topk_idx[t * K + r] : E;
   const int gsel = e == E ? 1 : 0;
@@ -1146,8 +1174,9 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
     hs.load_first();
     ATile<Q_MXFP4_W> aw[NM] = {tile_of<PH_DOWN, Q_MXFP4_W>(blob, grp, rb, false, I, l16)};
     static_assert(KS == 1, "MXFP4 accumulates one chain over K");
+    constexpr int PF = DA >= MX_ONE_CHUNKS ? MX_PF : DA;
     AStream<Q_MXFP4_W, NM, DA> as(0, 1, nch);
-    as.fill(aw, nch, g, I);
+    as.template fill<PF>(aw, nch, g, I);
 #pragma unroll
     for (int k = 0; k < 2; ++k)
       if (sid + sth * k < nsv) *(u32x4 *)(s_sc + 16 * (sid + sth * k)) = scv[k];
@@ -1159,7 +1188,7 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
     const uint8_t *brow = my_lds;
     const uint8_t *my_sc = s_sc + l16 * nsb;
     // MXFP4: one chain. DA ≥ MX_ONE instantiations run only for rows of at most DA chunks.
-    as.template run_pf<(DA >= 24)>(
+    as.template run_pf<(DA >= MX_ONE_CHUNKS), PF>(
         aw, nch, g, I, [&](int c) { return mx_ops<NTH>(brow, RS, a.hld, my_sc, nsb, c, g); },
         [&](const Fmt<Q_MXFP4_W>::A (&w)[NM], int c, const MxOps<NTH> &o) {
           chunk_mx1<NTH>(acc[0][0][0], w[0].w, o, c, g, I);
@@ -3054,7 +3083,7 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
   const size_t lds_down = mx ? (size_t)S * (NTH * mx_row_bytes(a.hld) + 16 * ((16 * (imax / 32) + 15) / 16))
                              : (size_t)S * 2 * (a.ldh + LDS_PAD) * 2;
   a.max_work = T;
-  const int down_grid = std::min(a.row_tiles * T, 2 * ncu);
+  const int down_grid = std::min(down_small_items(a.row_tiles, T), std::max(8, (2 * ncu) & ~7));   // a multiple of 8
   const int ks = (mx || S > 4 || !one_down) ? 1 : 2;
   hipExtLaunchKernelGGL(down, dim3(down_grid), dim3(64 * S * ks), lds_down, s, tm_down.start,
                         tm_down.stop, 0, a, (const int32_t *)ra.topk_idx);

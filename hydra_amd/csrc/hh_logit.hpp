@@ -27,43 +27,61 @@ __device__ __forceinline__ float bf_hi(uint32_t v) { return bf16_bits_to_f32(v >
 // Exact (fp64) router logit of expert e for token row xr, in the oracle's arithmetic: one wave.
 // A bf16·bf16 product is exact in fp32, so each term is formed in fp32 and added in fp64:
 // the same value as an fp64 fma. GEMMA: Σ (((x·s)·scale)·root)·w in fp64 with
-// s = (Σx²/H + eps)^-½ passed in `norm`. Each lane issues the loads of four 512-column steps
-// before their products and keeps one accumulator per step, so a dot costs about one memory
-// latency and a short dependency chain.
+// s = (Σx²/H + eps)^-½ passed in `norm`. Lane l takes columns 2048·i + 512·u + 8l .. +7 into
+// accumulator u (i ascending), and the logit is (acc0 + acc1) + (acc2 + acc3). Rows of at most
+// 4096 columns issue all their loads (two 2048-column steps) before the first product, so a dot
+// costs one memory latency and a short dependency chain.
 template <bool gemma>
 __device__ __forceinline__ double exact_logit(const RouteArgs &a, const uint16_t *xr,
                                               const uint16_t *wrow, double norm, double root) {
   const int lane = threadIdx.x & 63, H = a.hidden;
   double acc[4] = {0.0, 0.0, 0.0, 0.0};
-  for (int base = 0; base < H; base += 2048) {
+  struct Step {
     u32x4 xv[4], wv[4], sv[4];
+  };
+  // Loads are unconditional (clamped into the row) and masked afterwards: a load under a
+  // lane-dependent branch would be waited for before the next one is issued.
+  auto load = [&](Step &st, int base) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      // Loads are unconditional (clamped into the row) and masked afterwards: a load under a
-      // lane-dependent branch would be waited for before the next one is issued.
       const int h = base + lane * 8 + 512 * u;
       const int hc = min(h, H - 8);
-      const bool ok = h < H;
-      xv[u] = *(const u32x4 *)(xr + hc);
-      wv[u] = *(const u32x4 *)(wrow + hc);
-      sv[u] = gemma ? *(const u32x4 *)(a.router_scale + hc) : u32x4{0u, 0u, 0u, 0u};
-      if (!ok) wv[u] = u32x4{0u, 0u, 0u, 0u};
+      st.xv[u] = *(const u32x4 *)(xr + hc);
+      st.wv[u] = *(const u32x4 *)(wrow + hc);
+      st.sv[u] = gemma ? *(const u32x4 *)(a.router_scale + hc) : u32x4{0u, 0u, 0u, 0u};
+      if (h >= H) st.wv[u] = u32x4{0u, 0u, 0u, 0u};
     }
+  };
+  auto add = [&](const Step &st) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const int sh = (k & 1) * 16;
-        const float xf = bf16_bits_to_f32((xv[u][k >> 1] >> sh) & 0xFFFF);
-        const float wf = bf16_bits_to_f32((wv[u][k >> 1] >> sh) & 0xFFFF);
+        const float xf = bf16_bits_to_f32((st.xv[u][k >> 1] >> sh) & 0xFFFF);
+        const float wf = bf16_bits_to_f32((st.wv[u][k >> 1] >> sh) & 0xFFFF);
         if constexpr (gemma) {
           const double xd = (((double)xf * norm) *
-                             (double)bf16_bits_to_f32((sv[u][k >> 1] >> sh) & 0xFFFF)) * root;
+                             (double)bf16_bits_to_f32((st.sv[u][k >> 1] >> sh) & 0xFFFF)) * root;
           acc[u] = fma(xd, (double)wf, acc[u]);
         } else {
           acc[u] += (double)(xf * wf);
         }
       }
+    }
+  };
+  if (H <= 4096) {
+    // Both steps' loads first (the second clamped into the row when H ≤ 2048, and not added).
+    Step s0, s1;
+    load(s0, 0);
+    load(s1, 2048);
+    add(s0);
+    if (H > 2048) add(s1);
+  } else {
+    for (int base = 0; base < H; base += 2048) {
+      Step st;
+      load(st, base);
+      add(st);
     }
   }
   return wave_sum_f64((acc[0] + acc[1]) + (acc[2] + acc[3]));
