@@ -1,0 +1,217 @@
+"""Checkpoint expert tensors straight into HBM.
+
+The reference installs a checkpoint by repacking it into a `.hydra` file: every stacked expert
+tensor of a layer (one safetensors entry holding all E experts' copies of one blob slot) is
+scattered into E expert blobs at the slot's offset (`RepackPlan.swift:198-230` for GPT-OSS,
+`GemmaRepackPlan.swift:137-155` for Gemma 4 BF16, `QwenRepackPlan.swift:97-126` for Qwen
+MLX), and the runtime later reads those blobs through the SSD slot cache. Here every expert is
+resident, so the same scatter goes from the safetensors bytes directly into the device blob
+buffer the kernels read (`hh_scatter_expert_tensor`, one strided copy per tensor), and the
+router tensors are copied as they are. The result is an `MoELayer` whose weights are
+byte-for-byte the blobs the installer would have written.
+
+Tensor names and shapes follow the reference's configs: `GptOssConfig.swift:164-165` and the
+expert suffixes of `RepackPlan.swift:208-215`; `Gemma4Config.swift:183-208` (router
+`router.proj.weight`, `router.scale`, `router.per_expert_scale`; experts `experts.gate_up_proj`
+[E][2I][H], gate rows first, as `Gemma4Weights.swift:103-113` reads them, and
+`experts.down_proj`); `Qwen35MoeConfig.swift:155-158, 341-368` (prefix
+`language_model.model`, experts `mlp.switch_mlp.{gate,up,down}_proj.{weight,scales,biases}`,
+shared expert `mlp.shared_expert.*`, router `mlp.gate`, shared gate `mlp.shared_expert_gate`).
+
+The layer's router takes bf16 weights (`hh_moe_weights.router_weight`). Published Qwen MLX
+builds quantise `mlp.gate` and `mlp.shared_expert_gate` to 8 bits (`Qwen35MoeConfig.swift:341-342`);
+their dequantised values are not bf16 numbers, so loading one raises `CheckpointError` instead
+of rounding them silently. A checkpoint that stores those two as BF16 loads.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import glob
+import json
+import os
+import struct
+
+import numpy as np
+import torch
+
+from . import formats as F
+from ._lib import check, desc_c, lib
+from .layer import Context, MoELayer
+
+_ITEM = {"U8": 1, "I8": 1, "BF16": 2, "F16": 2, "U16": 2, "I16": 2, "F32": 4, "U32": 4,
+         "I32": 4, "F64": 8, "I64": 8, "U64": 8, "BOOL": 1}
+
+
+class CheckpointError(ValueError):
+    """A tensor is missing, or its dtype or shape is not what the layer description implies."""
+
+
+class SafetensorsFile:
+    """One .safetensors file: the JSON header (8-byte little-endian length, then the header),
+    and the data section mapped read-only."""
+
+    def __init__(self, path: str):
+        self.path = path
+        with open(path, "rb") as f:
+            (n,) = struct.unpack("<Q", f.read(8))
+            header = json.loads(f.read(n))
+        self.meta = header.pop("__metadata__", None)
+        self.entries = header
+        self._base = 8 + n
+        self._map = None
+
+    def names(self):
+        return list(self.entries)
+
+    def tensor(self, name: str):
+        """(dtype, shape, uint8 view of the tensor's bytes)."""
+        e = self.entries[name]
+        lo, hi = e["data_offsets"]
+        shape = tuple(int(v) for v in e["shape"])
+        if hi - lo != int(np.prod(shape, dtype=np.int64)) * _ITEM[e["dtype"]]:
+            raise CheckpointError(f"{self.path}: {name}: byte range does not match its shape")
+        if self._map is None:
+            self._map = np.memmap(self.path, dtype=np.uint8, mode="r")
+        return e["dtype"], shape, self._map[self._base + lo:self._base + hi]
+
+
+class Checkpoint:
+    """A checkpoint directory (or one file): tensor name → the file that holds it."""
+
+    def __init__(self, path: str):
+        if os.path.isdir(path):
+            index = os.path.join(path, "model.safetensors.index.json")
+            if os.path.exists(index):
+                with open(index) as f:
+                    wm = json.load(f)["weight_map"]
+                files = sorted(set(wm.values()))
+                self.files = {fn: SafetensorsFile(os.path.join(path, fn)) for fn in files}
+                self.where = {k: self.files[v] for k, v in wm.items()}
+            else:
+                paths = sorted(glob.glob(os.path.join(path, "*.safetensors")))
+                self.files = {os.path.basename(p): SafetensorsFile(p) for p in paths}
+                self.where = {n: f for f in self.files.values() for n in f.names()}
+        else:
+            f = SafetensorsFile(path)
+            self.files = {os.path.basename(path): f}
+            self.where = {n: f for n in f.names()}
+
+    def __contains__(self, name):
+        return name in self.where
+
+    def tensor(self, name: str, dtype: str, shape: tuple):
+        """The bytes of `name`, checked against the expected dtype and shape."""
+        if name not in self.where:
+            raise CheckpointError(f"missing tensor {name}")
+        dt, sh, data = self.where[name].tensor(name)
+        if dt != dtype or sh != tuple(shape):
+            raise CheckpointError(f"{name}: {dt}{list(sh)}, expected {dtype}{list(shape)}")
+        return data
+
+
+# ---- per-family tensor maps ------------------------------------------------------------------
+
+def expert_sources(desc: F.MoEDesc, family: str, layer: int, shared: bool = False):
+    """[(blob slot, tensor name, dtype, shape)] of the layer's stacked expert tensors, in blob
+    slot order, or of the shared expert's tensors (Qwen, `shared=True`: no expert axis)."""
+    H, E = desc.hidden, desc.experts
+    I = desc.shared_intermediate if shared else desc.intermediate
+    lead = () if shared else (E,)
+    if family == "gpt-oss":
+        if desc.quant != F.QUANT_MXFP4 or shared:
+            raise CheckpointError("gpt-oss checkpoints hold MXFP4 routed experts")
+        p = f"model.layers.{layer}.mlp.experts"
+        spec = [("gate_up_proj_blocks", "U8", (2 * I, H // 32, 16)),
+                ("gate_up_proj_scales", "U8", (2 * I, H // 32)),
+                ("gate_up_proj_bias", "BF16", (2 * I,)),
+                ("down_proj_blocks", "U8", (H, I // 32, 16)),
+                ("down_proj_scales", "U8", (H, I // 32)),
+                ("down_proj_bias", "BF16", (H,))]
+    elif family == "gemma4":
+        if desc.quant != F.QUANT_BF16 or shared:
+            raise CheckpointError("gemma4 checkpoints hold BF16 routed experts")
+        p = f"model.language_model.layers.{layer}.experts"
+        spec = [("gate_up_proj", "BF16", (2 * I, H)), ("down_proj", "BF16", (H, I))]
+    elif family == "qwen3.5-moe":
+        if desc.quant not in (F.QUANT_MLX4, F.QUANT_MLX8):
+            raise CheckpointError("qwen3.5-moe checkpoints hold MLX affine experts")
+        vpw, g = 32 // desc.bits, desc.group_size
+        p = f"language_model.model.layers.{layer}.mlp." + ("shared_expert" if shared else "switch_mlp")
+        spec = []
+        for proj, (rows, cols) in [("gate_proj", (I, H)), ("up_proj", (I, H)), ("down_proj", (H, I))]:
+            spec += [(f"{proj}.weight", "U32", (rows, cols // vpw)),
+                     (f"{proj}.scales", "BF16", (rows, cols // g)),
+                     (f"{proj}.biases", "BF16", (rows, cols // g))]
+    else:
+        raise CheckpointError(f"unknown family {family!r} (gpt-oss, gemma4, qwen3.5-moe)")
+    return [(slot, f"{p}.{suffix}", dt, lead + shape) for slot, (suffix, dt, shape) in enumerate(spec)]
+
+
+def router_sources(desc: F.MoEDesc, family: str, layer: int):
+    """{MoELayer tensor key: (tensor name, dtype, shape, required)}."""
+    H, E = desc.hidden, desc.experts
+    if family == "gpt-oss":
+        p = f"model.layers.{layer}.mlp.router"
+        return {"router_weight": (f"{p}.weight", "BF16", (E, H), True),
+                "router_bias": (f"{p}.bias", "BF16", (E,), bool(desc.expert_bias))}
+    if family == "gemma4":
+        p = f"model.language_model.layers.{layer}.router"
+        return {"router_weight": (f"{p}.proj.weight", "BF16", (E, H), True),
+                "router_scale": (f"{p}.scale", "BF16", (H,), True),
+                "router_expert_scale": (f"{p}.per_expert_scale", "BF16", (E,), True)}
+    if family == "qwen3.5-moe":
+        p = f"language_model.model.layers.{layer}.mlp"
+        out = {"router_weight": (f"{p}.gate.weight", "BF16", (E, H), True)}
+        if desc.shared_intermediate:
+            out["shared_gate"] = (f"{p}.shared_expert_gate.weight", "BF16", (1, H), True)
+        return out
+    raise CheckpointError(f"unknown family {family!r}")
+
+
+def _quantised_router(ck: Checkpoint, name: str) -> bool:
+    stem = name[:-len(".weight")]
+    return name in ck and ck.where[name].entries[name]["dtype"] == "U32" and f"{stem}.scales" in ck
+
+
+def load_moe_layer(path_or_ckpt, desc: F.MoEDesc, family: str, layer: int,
+                   ctx: Context | None = None, device: int = 0) -> MoELayer:
+    """The MoE half of decoder layer `layer` of a checkpoint, resident in HBM in the reference's
+    expert blob layout. Checks every tensor's dtype and shape against `desc` first."""
+    ck = path_or_ckpt if isinstance(path_or_ckpt, Checkpoint) else Checkpoint(path_or_ckpt)
+    routed = expert_sources(desc, family, layer)
+    shared = expert_sources(desc, family, layer, shared=True) if desc.shared_intermediate else []
+    routers = router_sources(desc, family, layer)
+    for key, (name, dt, shape, required) in routers.items():
+        if _quantised_router(ck, name):
+            raise CheckpointError(f"{name} is MLX-quantised; the layer's router takes bf16 weights")
+    # Every tensor is checked before any device memory is touched.
+    routed_data = [(slot, ck.tensor(n, dt, sh)) for slot, n, dt, sh in routed]
+    shared_data = [(slot, ck.tensor(n, dt, sh)) for slot, n, dt, sh in shared]
+    router_data = {k: ck.tensor(n, dt, sh) for k, (n, dt, sh, req) in routers.items()
+                   if req or n in ck}
+
+    ctx = ctx or Context(device)
+    dev = torch.device(f"cuda:{ctx.device}")
+    d = desc_c(desc)
+    lay = F.blob_layout(desc)
+    torch.cuda.synchronize(dev)
+    experts = torch.zeros((desc.experts, lay.stride), dtype=torch.uint8, device=dev)
+    for slot, data in routed_data:
+        check(lib().hh_scatter_expert_tensor(ctx.handle, C.byref(d), desc.intermediate, slot,
+                                             desc.experts, C.c_void_p(data.ctypes.data),
+                                             data.nbytes, C.c_void_p(experts.data_ptr()),
+                                             lay.stride))
+    tensors = {}
+    if shared_data:
+        slay = F.blob_layout(desc, desc.shared_intermediate)
+        blob = torch.zeros((slay.stride,), dtype=torch.uint8, device=dev)
+        for slot, data in shared_data:
+            check(lib().hh_scatter_expert_tensor(ctx.handle, C.byref(d), desc.shared_intermediate,
+                                                 slot, 1, C.c_void_p(data.ctypes.data),
+                                                 data.nbytes, C.c_void_p(blob.data_ptr()),
+                                                 slay.stride))
+        tensors["shared_expert"] = blob
+    for key, data in router_data.items():
+        tensors[key] = torch.from_numpy(np.array(data).view(np.int16)).to(dev)
+    torch.cuda.synchronize(dev)
+    return MoELayer.resident(desc, experts, lay.stride, tensors, ctx)

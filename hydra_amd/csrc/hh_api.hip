@@ -524,6 +524,32 @@ int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
   return HH_OK;
 }
 
+int hh_scatter_expert_tensor(hh_ctx *ctx, const hh_moe_desc *d, int32_t inter, int32_t slot,
+                             int32_t experts, const void *src, int64_t src_bytes, void *blobs,
+                             uint64_t stride) {
+  if (!ctx || !d || !src || !blobs) return fail(HH_EINVAL, "NULL argument");
+  int rc = check_desc(d);
+  if (rc) return rc;
+  hh_blob_layout lay;
+  if ((rc = hh_expert_blob_layout(d, inter, &lay))) return rc;
+  if (slot < 0 || slot >= lay.slot_count) return fail(HH_EINVAL, "slot outside the format's blob slots");
+  if (experts <= 0) return fail(HH_EINVAL, "experts must be positive");
+  if (stride == 0) stride = lay.stride_bytes;
+  if (stride < lay.payload_bytes) return fail(HH_ESHAPE, "expert_stride is smaller than one blob");
+  if (stride % 256 || ((uintptr_t)blobs & 255)) return fail(HH_EALIGN, "blobs and expert_stride must be 256-byte aligned");
+  const size_t bytes = lay.bytes[slot];
+  if (src_bytes != (int64_t)bytes * experts)
+    return fail(HH_ESHAPE, "src_bytes is not experts x the slot's byte count");
+  HH_HIP(hipSetDevice(ctx->device));
+  HH_HIP(hipMemcpy2DAsync((uint8_t *)blobs + lay.offset[slot], stride, src, bytes, bytes, experts,
+                          hipMemcpyDefault, ctx->stream));
+  // Loading is off the hot path: return with the copy complete, so a host source can be
+  // released at once.
+  HH_HIP(hipStreamSynchronize(ctx->stream));
+  ctx->dispatches += 1;
+  return HH_OK;
+}
+
 int hh_mxfp4_dequant(hh_ctx *ctx, const uint8_t *blocks, const uint8_t *scales, int64_t n,
                      float *out) {
   if (!ctx || !blocks || !scales || !out) return fail(HH_EINVAL, "NULL argument");

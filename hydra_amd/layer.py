@@ -100,6 +100,21 @@ class MoELayer:
         self._desc_c = desc_c(self.desc)
         self._weights_c = self.weights_c()
 
+    @classmethod
+    def resident(cls, desc: F.MoEDesc, experts: torch.Tensor, expert_stride: int,
+                 tensors: dict, ctx: Context) -> "MoELayer":
+        """A layer over weights already in HBM: `experts` uint8 [E][expert_stride] in the blob
+        layout, `tensors` the device router / shared-expert tensors by name (absent = None)."""
+        self = cls.__new__(cls)
+        self.desc, self.ctx = desc, ctx
+        self.experts, self.expert_stride = experts, int(expert_stride)
+        self.tensors = {k: tensors.get(k) for k in
+                        ["shared_expert", "router_weight", "router_bias", "router_scale",
+                         "router_expert_scale", "shared_gate"]}
+        self._desc_c = desc_c(desc)
+        self._weights_c = self.weights_c()
+        return self
+
     def weights_c(self, experts: torch.Tensor | None = None) -> MoEWeightsC:
         t = self.tensors
         ex = self.experts if experts is None else experts

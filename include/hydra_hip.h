@@ -171,6 +171,18 @@ int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *desc, const hh_moe_weights *w
                    const uint16_t *x, const uint16_t *x_router, int32_t tokens,
                    float *y, int32_t *topk_idx, float *topk_w);
 
+/* Checkpoint expert tensors straight into HBM: copies one stacked checkpoint tensor, the E
+ * experts' copies of blob slot `slot` back to back (E × bytes[slot] bytes, e.g. GPT-OSS's
+ * model.layers.L.mlp.experts.gate_up_proj_blocks [E][2I][H/32][16]), into the E blobs at
+ * `blobs`: blob e's bytes offset[slot] .. + bytes[slot] (offsets and sizes of
+ * hh_expert_blob_layout(desc, intermediate)) = src[e·bytes[slot] ..]. One strided copy on the
+ * context's stream, complete when the call returns; `src` may be host or device memory. Replaces the installer's expert ScatterCopy operations (RepackPlan.swift:198-230,
+ * GemmaRepackPlan.swift:137-155, QwenRepackPlan.swift:97-126), writing the blob layout the
+ * kernels read in place of a .hydra file. HH_ESHAPE if src_bytes ≠ experts × bytes[slot].    */
+int hh_scatter_expert_tensor(hh_ctx *ctx, const hh_moe_desc *desc, int32_t intermediate,
+                             int32_t slot, int32_t experts, const void *src, int64_t src_bytes,
+                             void *blobs, uint64_t expert_stride);
+
 /* ---- operator-level entry points (parity tests mirror the encoder passes) ----------------- */
 /* MXFP4 → fp32 (MXFP4.swift:67-99; GPU mxfp4_dequantize, mxfp4.metal:25). `blocks` is
  * nblocks×16 bytes, `scales` nblocks bytes, `out` nblocks×32 floats. Uses the same decode
