@@ -157,6 +157,39 @@ def measure_decode(wl, T, steps, warmup, fused=False):
     }
 
 
+def measure_stack(wl, T, layers, steps, warmup):
+    """A decode layer stack (GPT-OSS-20B has 24 MoE layers) at T tokens: `layers` calls per
+    step over the resident weight copies in turn, run eagerly and as one captured HIP graph
+    (hh_ctx_capture_begin / hh_graph_launch). Returns µs per layer of both."""
+    torch = wl.torch
+    wl.ctx.decode_fused(0)
+    wl.prepare(T, bank=max(layers, 8))
+    calls = [(wl.bank[l], wl.idx[l], wl.wc[l % len(wl.wc)]) for l in range(layers)]
+
+    def record():
+        for x, idx, wc in calls:
+            wl.layer.forward_into(x, wl.y, idx, wl.w, weights_c=wc)
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        wl.ctx.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            fn()
+        wl.ctx.synchronize()
+        return (time.perf_counter() - t0) / steps
+
+    eager = timed(record)
+    graph = wl.ctx.capture(record)
+    replay = timed(graph.launch)
+    graph.close()
+    wl.ctx.decode_fused(-1)
+    return {"T": T, "layers": layers, "eager_us_per_layer": eager / layers * 1e6,
+            "graph_us_per_layer": replay / layers * 1e6, "graph_tokens_per_s": T / replay,
+            "eager_tokens_per_s": T / eager}
+
+
 def measure_prefill(wl, T, steps, warmup):
     desc = wl.desc
     wl.prepare(T, bank=4)
@@ -279,7 +312,7 @@ def main():
         name, desc, copies, Tp = next(o for o in OTHER if o[0] == args.only_other)
         print(json.dumps({name: measure_other(torch, name, desc, copies, Tp, args.steps)}))
         return
-    decode, fused = {}, {}
+    decode, fused, stack = {}, {}, {}
     if not args.only_prefill:
         wl = Workload(torch, F.GPT_OSS_20B, copies=args.copies)
         for T in ([1] if args.only_t1 else [1, 2, 4, 8]):
@@ -287,6 +320,9 @@ def main():
             steps = args.steps if T == 1 else max(100, args.steps // 4)
             decode[T] = measure_decode(wl, T, steps, args.warmup if T == 1 else 10)
         if not args.only_t1:
+            for T in [1, 8]:
+                log(f"decode stack of 24 layers, T={T}: eager and one HIP graph")
+                stack[T] = measure_stack(wl, T, 24, 40, 5)
             for T in [1, 2, 4, 8]:
                 log(f"decode T={T}, one launch")
                 fused[T] = measure_decode(wl, T, max(100, args.steps // 4), 10, fused=True)
@@ -334,6 +370,7 @@ def main():
         "cpu_baseline": cpu,
         "decode": {str(T): v for T, v in decode.items()},
         "decode_one_launch": {str(T): v for T, v in fused.items()},
+        "decode_stack_24_layers": {str(T): v for T, v in stack.items()},
         "prefill_gpt_oss_120b_zipf": {str(T): v for T, v in prefill.items()},
         "other_configs": other,
     }

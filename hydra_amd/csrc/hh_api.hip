@@ -50,6 +50,17 @@ struct hh_ctx {
   bool profile = false;
   std::vector<hipEvent_t> events;
   size_t events_used = 0;
+  // Graph capture: calls are recorded, not run; dispatches counted while recording are moved
+  // to the graph and added back per launch.
+  bool capturing = false;
+  int64_t capture_base = 0;
+};
+
+struct hh_graph {
+  hh_ctx *ctx = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  int64_t dispatches = 0;
 };
 
 namespace {
@@ -143,6 +154,8 @@ Scratch plan(const hh_moe_desc &d, int T) {
 
 int ensure_arena(hh_ctx *ctx, size_t bytes) {
   if (ctx->arena_bytes >= bytes) return HH_OK;
+  if (ctx->capturing)
+    return fail(HH_EINVAL, "the scratch arena must cover the call before capture (hh_ctx_reserve)");
   HH_HIP(hipSetDevice(ctx->device));
   if (ctx->arena) {
     HH_HIP(hipStreamSynchronize(ctx->stream));
@@ -180,7 +193,8 @@ bool use_fused(const hh_ctx *ctx, const hh_moe_desc &d, int T) {
     return v && v[0] == '1';
   }();
   const bool enabled = ctx->decode_fused < 0 ? env_on : ctx->decode_fused != 0;
-  return enabled && d.quant == HH_QUANT_MXFP4 && T <= kSmallT &&
+  // Under capture the fused kernel's per-call flag epoch would be frozen into the graph.
+  return enabled && !ctx->capturing && d.quant == HH_QUANT_MXFP4 && T <= kSmallT &&
          hh::decode_fused_fits(d.hidden, d.intermediate, d.experts, d.top_k, d.shared_intermediate) &&
          sizeof(uint32_t) * (size_t)hh::decode_fused_flags(kSmallT, d.experts, d.top_k, d.intermediate) <= kFlagBytes;
 }
@@ -297,6 +311,11 @@ int hh_ctx_create(hh_ctx **out, int32_t device) {
 int hh_ctx_destroy(hh_ctx *ctx) {
   if (!ctx) return HH_OK;
   hipSetDevice(ctx->device);
+  if (ctx->capturing) {   // abandon an unfinished capture
+    hipGraph_t g = nullptr;
+    if (hipStreamEndCapture(ctx->stream, &g) == hipSuccess && g) hipGraphDestroy(g);
+    ctx->capturing = false;
+  }
   if (ctx->stream) hipStreamSynchronize(ctx->stream);
   if (ctx->arena) hipFree(ctx->arena);
   if (ctx->flags) hipFree(ctx->flags);
@@ -310,6 +329,7 @@ void *hh_ctx_stream(hh_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
 
 int hh_ctx_synchronize(hh_ctx *ctx) {
   if (!ctx) return fail(HH_EINVAL, "ctx is NULL");
+  if (ctx->capturing) return fail(HH_EINVAL, "the context is capturing a graph");
   HH_HIP(hipSetDevice(ctx->device));
   HH_HIP(hipStreamSynchronize(ctx->stream));
   return HH_OK;
@@ -319,6 +339,7 @@ int64_t hh_dispatch_count(const hh_ctx *ctx) { return ctx ? ctx->dispatches : 0;
 
 int hh_ctx_profile(hh_ctx *ctx, int32_t enable) {
   if (!ctx) return fail(HH_EINVAL, "ctx is NULL");
+  if (ctx->capturing) return fail(HH_EINVAL, "the context is capturing a graph");
   ctx->profile = enable != 0;
   return HH_OK;
 }
@@ -524,10 +545,66 @@ int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
   return HH_OK;
 }
 
+int hh_ctx_capture_begin(hh_ctx *ctx) {
+  if (!ctx) return fail(HH_EINVAL, "ctx is NULL");
+  if (ctx->capturing) return fail(HH_EINVAL, "the context is already capturing");
+  if (ctx->profile) return fail(HH_EINVAL, "profiling is on: turn it off before capture");
+  HH_HIP(hipSetDevice(ctx->device));
+  HH_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeRelaxed));
+  ctx->capturing = true;
+  ctx->capture_base = ctx->dispatches;
+  return HH_OK;
+}
+
+int hh_ctx_capture_end(hh_ctx *ctx, hh_graph **out) {
+  if (!ctx || !out) return fail(HH_EINVAL, "NULL argument");
+  *out = nullptr;
+  if (!ctx->capturing) return fail(HH_EINVAL, "the context is not capturing");
+  HH_HIP(hipSetDevice(ctx->device));
+  ctx->capturing = false;
+  const int64_t recorded = ctx->dispatches - ctx->capture_base;
+  ctx->dispatches = ctx->capture_base;
+  hipGraph_t graph = nullptr;
+  HH_HIP(hipStreamEndCapture(ctx->stream, &graph));
+  hipGraphExec_t exec = nullptr;
+  const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    hipGraphDestroy(graph);
+    return hip_fail(e, "hipGraphInstantiate");
+  }
+  hh_graph *g = new hh_graph;
+  g->ctx = ctx;
+  g->graph = graph;
+  g->exec = exec;
+  g->dispatches = recorded;
+  *out = g;
+  return HH_OK;
+}
+
+int hh_graph_launch(hh_graph *g) {
+  if (!g) return fail(HH_EINVAL, "graph is NULL");
+  if (g->ctx->capturing) return fail(HH_EINVAL, "the context is capturing a graph");
+  HH_HIP(hipSetDevice(g->ctx->device));
+  HH_HIP(hipGraphLaunch(g->exec, g->ctx->stream));
+  g->ctx->dispatches += g->dispatches;
+  return HH_OK;
+}
+
+int hh_graph_destroy(hh_graph *g) {
+  if (!g) return HH_OK;
+  hipSetDevice(g->ctx->device);
+  hipStreamSynchronize(g->ctx->stream);
+  if (g->exec) hipGraphExecDestroy(g->exec);
+  if (g->graph) hipGraphDestroy(g->graph);
+  delete g;
+  return HH_OK;
+}
+
 int hh_scatter_expert_tensor(hh_ctx *ctx, const hh_moe_desc *d, int32_t inter, int32_t slot,
                              int32_t experts, const void *src, int64_t src_bytes, void *blobs,
                              uint64_t stride) {
   if (!ctx || !d || !src || !blobs) return fail(HH_EINVAL, "NULL argument");
+  if (ctx->capturing) return fail(HH_EINVAL, "the context is capturing a graph");
   int rc = check_desc(d);
   if (rc) return rc;
   hh_blob_layout lay;

@@ -55,6 +55,18 @@ class Context:
         check(lib().hh_ctx_profile_read(self.handle, ms, C.byref(calls)))
         return list(ms), calls.value
 
+    def capture(self, record) -> "Graph":
+        """Runs `record()` (hh_moe_forward calls on this context) under graph capture and
+        returns the graph; nothing runs until `Graph.launch`."""
+        check(lib().hh_ctx_capture_begin(self.handle))
+        try:
+            record()
+        finally:
+            g = C.c_void_p()
+            rc = lib().hh_ctx_capture_end(self.handle, C.byref(g))
+        check(rc)
+        return Graph(g, self)
+
     @property
     def dispatches(self) -> int:
         return lib().hh_dispatch_count(self.handle)
@@ -63,6 +75,29 @@ class Context:
         if self.handle:
             lib().hh_ctx_destroy(self.handle)
             self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Graph:
+    """A recorded sequence of layer calls (hh_graph); `launch` replays it on the context's
+    stream."""
+
+    def __init__(self, handle, ctx: Context):
+        self.handle, self.ctx = handle, ctx
+
+    def launch(self):
+        check(lib().hh_graph_launch(self.handle))
+
+    def close(self):
+        # A graph outlived by its context was freed with nothing: its context is gone.
+        if self.handle and self.ctx.handle:
+            lib().hh_graph_destroy(self.handle)
+        self.handle = None
 
     def __del__(self):
         try:

@@ -171,6 +171,22 @@ int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *desc, const hh_moe_weights *w
                    const uint16_t *x, const uint16_t *x_router, int32_t tokens,
                    float *y, int32_t *topk_idx, float *topk_w);
 
+/* A layer stack as one HIP graph (the per-layer-stack graphs a HIP-backed
+ * ModelRunner.forward / TextModelRunner would replay in place of encoding every layer's passes
+ * per token, ModelRunner.swift:110-230): between hh_ctx_capture_begin and hh_ctx_capture_end
+ * the context's hh_moe_forward calls are recorded, not run, with the buffers they were given;
+ * hh_graph_launch replays them on the context's stream. The scratch arena must already cover
+ * every recorded call (hh_ctx_reserve; a call that would grow it fails), profiling must be off,
+ * and while recording the context accepts no call that synchronises (hh_ctx_synchronize,
+ * hh_scatter_expert_tensor); the one-launch decode (hh_ctx_decode_fused) is not used for
+ * recorded calls. A graph's calls share the context's arena, so replays of graphs of one
+ * context are ordered by its stream, like eager calls.                                      */
+typedef struct hh_graph hh_graph;
+int hh_ctx_capture_begin(hh_ctx *ctx);
+int hh_ctx_capture_end(hh_ctx *ctx, hh_graph **out);
+int hh_graph_launch(hh_graph *graph);
+int hh_graph_destroy(hh_graph *graph);
+
 /* Checkpoint expert tensors straight into HBM: copies one stacked checkpoint tensor, the E
  * experts' copies of blob slot `slot` back to back (E × bytes[slot] bytes, e.g. GPT-OSS's
  * model.layers.L.mlp.experts.gate_up_proj_blocks [E][2I][H/32][16]), into the E blobs at
