@@ -24,6 +24,9 @@
  *                             the reference's full-layer fixture gemma4_operators.json["layer"]
  *   hho_blob_layout           the reference's own byte counts (MXFP4Tests.swift:106-119) and
  *                             closed-form alignment rules
+ *   hho_attention_decode      reference fixtures reference_ops.json["sdpa_full"],
+ *                             ["sdpa_sliding"] (every query row as one decode step), a sink of
+ *                             -inf against plain softmax attention, one key = its value row
  */
 #include "hh_oracle.h"
 
@@ -475,4 +478,43 @@ void hho_router_logits(const hho_desc *d, const hho_weights *w, const double *x,
     free((void *)w64.router_weight); free((void *)w64.router_bias);
     free((void *)w64.router_scale); free((void *)w64.router_expert_scale);
     free((void *)w64.shared_gate);
+}
+
+/* Decode attention over a key/value history with per-head sinks (ReferenceLayer.swift:150-180;
+ * GPU attention_decode_split + attention_decode_merge, attention.metal:307-450). Keys
+ * start_position .. start_position + key_count - 1 are visible; a key at position p lives in
+ * cache row p % ring_size (ring_size 0: row p). Caches are [rows][kv_heads][head_dim], query and
+ * out [q_heads][head_dim]; query head h reads kv head h / (q_heads / kv_heads). The sink enters
+ * the softmax denominator only. */
+void hho_attention_decode(const double *q, const double *k_cache, const double *v_cache,
+                          const double *sinks, int q_heads, int kv_heads, int head_dim,
+                          int key_count, int ring_size, int start_position, double sm_scale,
+                          double *out) {
+    const int q_mult = q_heads / kv_heads;
+    double *logits = (double *)malloc(sizeof(double) * (size_t)(key_count > 0 ? key_count : 1));
+    for (int h = 0; h < q_heads; ++h) {
+        const int kvh = h / q_mult;
+        const double sink = sinks[h];
+        double peak = sink;
+        for (int j = 0; j < key_count; ++j) {
+            const long pos = (long)start_position + j;
+            const long row = ring_size > 0 ? pos % ring_size : pos;
+            const double *kr = k_cache + ((size_t)row * kv_heads + kvh) * head_dim;
+            double dot = 0.0;
+            for (int i = 0; i < head_dim; ++i) dot += q[(size_t)h * head_dim + i] * kr[i];
+            logits[j] = dot * sm_scale;
+            if (logits[j] > peak) peak = logits[j];
+        }
+        double den = exp(sink - peak);
+        for (int j = 0; j < key_count; ++j) den += exp(logits[j] - peak);
+        for (int i = 0; i < head_dim; ++i) out[(size_t)h * head_dim + i] = 0.0;
+        for (int j = 0; j < key_count; ++j) {
+            const long pos = (long)start_position + j;
+            const long row = ring_size > 0 ? pos % ring_size : pos;
+            const double *vr = v_cache + ((size_t)row * kv_heads + kvh) * head_dim;
+            const double w = exp(logits[j] - peak) / den;
+            for (int i = 0; i < head_dim; ++i) out[(size_t)h * head_dim + i] += w * vr[i];
+        }
+    }
+    free(logits);
 }

@@ -89,4 +89,9 @@ int hho_moe_forward(const hho_desc *d, const hho_weights *w, const uint16_t *x,
 #ifdef __cplusplus
 }
 #endif
+void hho_attention_decode(const double *q, const double *k_cache, const double *v_cache,
+                          const double *sinks, int q_heads, int kv_heads, int head_dim,
+                          int key_count, int ring_size, int start_position, double sm_scale,
+                          double *out);
+
 #endif

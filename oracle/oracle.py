@@ -275,3 +275,22 @@ def moe_forward_f64(desc, blobs, x, router_weight, x_router=None, router_bias=No
     if rc != 0:
         raise ValueError(f"oracle rejected the layer (code {rc})")
     return y, idx, wts, sw
+
+
+def attention_decode(q, k_cache, v_cache, sinks, kv_heads, key_count, start_position=0,
+                     ring_size=0, sm_scale=None):
+    """fp64 decode attention with sinks (ReferenceLayer.swift:150-180). q [q_heads][d];
+    caches [rows][kv_heads][d]; returns out [q_heads][d]."""
+    q = np.ascontiguousarray(q, np.float64)
+    qh, d = q.shape
+    k = np.ascontiguousarray(k_cache, np.float64)
+    v = np.ascontiguousarray(v_cache, np.float64)
+    s = np.ascontiguousarray(sinks, np.float64)
+    if sm_scale is None:
+        sm_scale = 1.0 / np.sqrt(d)
+    out = np.zeros((qh, d), np.float64)
+    L = lib()
+    L.hho_attention_decode.argtypes = [C.c_void_p] * 4 + [C.c_int] * 6 + [C.c_double, C.c_void_p]
+    L.hho_attention_decode(_p(q), _p(k), _p(v), _p(s), qh, kv_heads, d, key_count, ring_size,
+                           start_position, float(sm_scale), _p(out))
+    return out

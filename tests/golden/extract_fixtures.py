@@ -7,6 +7,8 @@ Only data is copied (inputs and expected outputs the reference's tests hold):
   * Tests/HydraFormatTests/Fixtures/mxfp4_{packed.bin,scales.bin,expected.f32}
     (written by the reference's tools/gen_mxfp4_fixture.py; used by MXFP4Tests.swift:19-47)
   * reference_ops.json keys "router", "swiglu"          (ReferenceOpsTests.swift:127-216)
+  * reference_ops.json keys "sdpa_full", "sdpa_sliding"  (attention with sinks; written by the
+    reference's tools/gen_reference_fixtures.py:100-128, 217-220)
   * gemma4_operators.json keys "gelu_tanh", "router", "rms_norm", "rms_norm_unscaled",
     "layer"                                              (Gemma4ReferenceTests.swift)
 Nothing at test time reads the reference.
@@ -28,6 +30,8 @@ def main(ref: str) -> None:
         ops = json.load(f)
     with open(os.path.join(HERE, "reference_ops_moe.json"), "w") as f:
         json.dump({k: ops[k] for k in ["router", "swiglu"]}, f)
+    with open(os.path.join(HERE, "reference_ops_attention.json"), "w") as f:
+        json.dump({k: ops[k] for k in ["sdpa_full", "sdpa_sliding"]}, f)
     with open(os.path.join(rfx, "gemma4_operators.json")) as f:
         gem = json.load(f)
     with open(os.path.join(HERE, "gemma4_moe.json"), "w") as f:

@@ -329,3 +329,48 @@ def test_full_size_expert_matches_dense_formulation():
     got = O.expert_ffn(d, layer["experts"][0], x)
     ref = D.expert_ffn(d, layer["experts"][0], x)
     assert np.max(np.abs(got - ref)) / np.max(np.abs(ref)) < 1e-12
+
+
+# ---- decode attention with sinks --------------------------------------------------------------
+
+@pytest.mark.parametrize("key", ["sdpa_full", "sdpa_sliding"])
+def test_attention_decode_matches_reference_sdpa_fixture(golden_dir, key):
+    """reference_ops.json sdpa fixtures (gen_reference_fixtures.py:100-128): every query row t
+    is one decode step over the keys its causal (and sliding) mask leaves visible."""
+    f = _golden(golden_dir, "reference_ops_attention.json")[key]
+    kv, m, d, W = f["kv_heads"], f["q_mult"], f["head_dim"], f["sliding_window"]
+    Q, K, V = np.array(f["q"]), np.array(f["k"]), np.array(f["v"])
+    for t in range(f["tokens"]):
+        first = max(0, t - W + 1) if W > 0 else 0
+        out = O.attention_decode(Q[t].reshape(kv * m, d), K, V, f["sinks"], kv, t - first + 1,
+                                 first, 0, f["sm_scale"])
+        np.testing.assert_allclose(out.reshape(-1), f["expected"][t], rtol=0, atol=1e-12)
+
+
+def test_attention_decode_closed_forms():
+    rng = np.random.default_rng(5)
+    qh, kv, d, n = 6, 2, 16, 9
+    q = rng.standard_normal((qh, d))
+    k = rng.standard_normal((n, kv, d))
+    v = rng.standard_normal((n, kv, d))
+    # A sink of -inf is plain softmax attention.
+    out = O.attention_decode(q, k, v, np.full(qh, -np.inf), kv, n)
+    for h in range(qh):
+        g = h // (qh // kv)
+        lg = k[:, g, :] @ q[h] / np.sqrt(d)
+        w = np.exp(lg - lg.max()); w /= w.sum()
+        np.testing.assert_allclose(out[h], w @ v[:, g, :], rtol=1e-12, atol=1e-12)
+    # One key and a sink far below it: the value row itself.
+    out1 = O.attention_decode(q, k, v, np.full(qh, -1e3), kv, 1, start_position=4)
+    for h in range(qh):
+        np.testing.assert_allclose(out1[h], v[4, h // 3], rtol=1e-12)
+    # A ring of R rows holding positions p at row p % R equals the linear history.
+    R, start = 5, 7
+    ring_k, ring_v = np.zeros((R, kv, d)), np.zeros((R, kv, d))
+    lin_k, lin_v = rng.standard_normal((start + R, kv, d)), rng.standard_normal((start + R, kv, d))
+    for p in range(start, start + R):
+        ring_k[p % R], ring_v[p % R] = lin_k[p], lin_v[p]
+    sinks = rng.standard_normal(qh)
+    a = O.attention_decode(q, ring_k, ring_v, sinks, kv, R, start, R)
+    b = O.attention_decode(q, lin_k, lin_v, sinks, kv, R, start, 0)
+    np.testing.assert_allclose(a, b, rtol=0, atol=0)
