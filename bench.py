@@ -190,6 +190,41 @@ def measure_stack(wl, T, layers, steps, warmup):
             "eager_tokens_per_s": T / eager}
 
 
+def measure_attention(torch, keys, q_heads=64, kv_heads=8, head_dim=64, reps=50, steps=20):
+    """Decode attention with sinks (hh_attention_decode) on GPT-OSS's attention shape over an
+    fp16 history of `keys` positions: `reps` calls recorded as one HIP graph, replayed `steps`
+    times. Bytes = the key and value rows read once (keys · kv_heads · head_dim · 2 B · 2)."""
+    from hydra_amd.attention import attention_decode_into
+    from hydra_amd.layer import Context
+    dev = "cuda:0"
+    g = torch.Generator(device=dev).manual_seed(keys)
+    ctx = Context(0)
+    q = torch.randn((q_heads, head_dim), device=dev, generator=g)
+    # Two histories used in turn, each larger than the 256 MB memory-side cache at 64k keys.
+    caches = [(torch.randn((keys, kv_heads, head_dim), device=dev, generator=g).half(),
+               torch.randn((keys, kv_heads, head_dim), device=dev, generator=g).half())
+              for _ in range(2)]
+    sinks = torch.randn(q_heads, device=dev, generator=g).bfloat16().view(torch.int16)
+    out = torch.empty((q_heads, head_dim), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    attention_decode_into(ctx, q, caches[0][0], caches[0][1], sinks, keys, out=out)
+    ctx.synchronize()
+    graph = ctx.capture(lambda: [attention_decode_into(ctx, q, *caches[i % 2], sinks, keys, out=out)
+                                 for i in range(reps)])
+    graph.launch()
+    ctx.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.launch()
+    ctx.synchronize()
+    sec = (time.perf_counter() - t0) / (steps * reps)
+    graph.close()
+    ctx.close()
+    by = keys * kv_heads * head_dim * 2 * 2
+    return {"keys": keys, "q_heads": q_heads, "kv_heads": kv_heads, "head_dim": head_dim,
+            "us_per_call": sec * 1e6, "GBps": by / sec / 1e9, "hbm_frac": by / sec / 1e9 / HBM_PEAK_GBS}
+
+
 def measure_prefill(wl, T, steps, warmup):
     desc = wl.desc
     wl.prepare(T, bank=4)
@@ -284,6 +319,8 @@ def main():
     ap.add_argument("--only-other", default=None,
                     help="run only the named other config (qwen-35b-a3b-mlx4, ...; for profiling)")
     ap.add_argument("--only-prefill", action="store_true", help="prefill only (for profiling)")
+    ap.add_argument("--only-attention", action="store_true",
+                    help="decode attention only (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 256 MiB device-to-device copy and exit (HBM counter calibration)")
     args = ap.parse_args()
@@ -308,6 +345,10 @@ def main():
     from hydra_amd._lib import lib
     lib()  # fail loudly if the HIP library is missing
 
+    if args.only_attention:
+        print(json.dumps({"decode_attention_gpt_oss": {
+            str(k): measure_attention(torch, k) for k in [4096, 32768, 131072]}}))
+        return
     if args.only_other:
         name, desc, copies, Tp = next(o for o in OTHER if o[0] == args.only_other)
         print(json.dumps({name: measure_other(torch, name, desc, copies, Tp, args.steps)}))
@@ -327,6 +368,11 @@ def main():
                 log(f"decode T={T}, one launch")
                 fused[T] = measure_decode(wl, T, max(100, args.steps // 4), 10, fused=True)
         wl.close()
+    attention = {}
+    if not (args.only_t1 or args.only_prefill or args.no_other):
+        for keys in [4096, 32768, 131072]:
+            log(f"decode attention, {keys} keys")
+            attention[keys] = measure_attention(torch, keys)
     prefill = {}
     if not args.no_prefill and not args.only_t1:
         wl = Workload(torch, F.GPT_OSS_120B, copies=2, zipf=1.1)
@@ -371,6 +417,7 @@ def main():
         "decode": {str(T): v for T, v in decode.items()},
         "decode_one_launch": {str(T): v for T, v in fused.items()},
         "decode_stack_24_layers": {str(T): v for T, v in stack.items()},
+        "decode_attention_gpt_oss": {str(k): v for k, v in attention.items()},
         "prefill_gpt_oss_120b_zipf": {str(T): v for T, v in prefill.items()},
         "other_configs": other,
     }

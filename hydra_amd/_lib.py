@@ -18,6 +18,7 @@ EXPORTS = [
     "hh_moe_forward", "hh_mxfp4_dequant", "hh_mlx_dequant", "hh_router_topk", "hh_activation",
     "hh_permute", "hh_ctx_profile", "hh_ctx_profile_read", "hh_ctx_decode_fused", "hh_scatter_expert_tensor",
     "hh_ctx_capture_begin", "hh_ctx_capture_end", "hh_graph_launch", "hh_graph_destroy",
+    "hh_attention_decode",
 ]
 
 CODES = {0: "HH_OK", -1: "HH_EINVAL", -2: "HH_EALIGN", -3: "HH_ETOPK", -4: "HH_EHIP",
@@ -82,6 +83,7 @@ def lib() -> C.CDLL:
     L.hh_permute.argtypes = [vp, vp, i32, i32, i32, vp, vp]
     L.hh_ctx_profile.argtypes = [vp, i32]
     L.hh_ctx_capture_begin.argtypes = [vp]
+    L.hh_attention_decode.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32, C.c_float, vp]
     L.hh_ctx_capture_end.argtypes = [vp, C.POINTER(vp)]
     L.hh_graph_launch.argtypes = [vp]
     L.hh_graph_destroy.argtypes = [vp]

@@ -26,6 +26,7 @@ int decode_fused_flags(int T, int E, int K, int I);
 hipError_t launch_decode_fused(bool gemma, GemmArgs a, const RouteArgs &ra, FuseArgs f, hipStream_t s, Timing tm);
 hipError_t launch_combine(const float *slot_out, int slots, int H, int T, float *y, hipStream_t s,
                           Timing tm);
+hipError_t launch_attention_decode(const AttnArgs &a, hipStream_t s);
 hipError_t launch_mxfp4_dequant(const uint8_t *blocks, const uint8_t *scales, int64_t n,
                                 float *out, hipStream_t s);
 hipError_t launch_mlx_dequant(const uint32_t *words, const uint16_t *scales,
@@ -54,6 +55,9 @@ struct hh_ctx {
   // to the graph and added back per launch.
   bool capturing = false;
   int64_t capture_base = 0;
+  // Decode attention partials (per query head and chunk), grown on demand.
+  float *attn = nullptr;
+  size_t attn_bytes = 0;
 };
 
 struct hh_graph {
@@ -318,6 +322,7 @@ int hh_ctx_destroy(hh_ctx *ctx) {
   }
   if (ctx->stream) hipStreamSynchronize(ctx->stream);
   if (ctx->arena) hipFree(ctx->arena);
+  if (ctx->attn) hipFree(ctx->attn);
   if (ctx->flags) hipFree(ctx->flags);
   for (hipEvent_t ev : ctx->events) hipEventDestroy(ev);
   if (ctx->stream) hipStreamDestroy(ctx->stream);
@@ -624,6 +629,61 @@ int hh_scatter_expert_tensor(hh_ctx *ctx, const hh_moe_desc *d, int32_t inter, i
   // released at once.
   HH_HIP(hipStreamSynchronize(ctx->stream));
   ctx->dispatches += 1;
+  return HH_OK;
+}
+
+int hh_attention_decode(hh_ctx *ctx, const float *q, const uint16_t *k_cache,
+                        const uint16_t *v_cache, const uint16_t *sinks, int32_t q_heads,
+                        int32_t kv_heads, int32_t head_dim, int32_t key_count, int32_t ring_size,
+                        int32_t start_position, float sm_scale, float *out) {
+  if (!ctx || !q || !k_cache || !v_cache || !sinks || !out) return fail(HH_EINVAL, "NULL argument");
+  if (head_dim != 64 && head_dim != 128) return fail(HH_ESHAPE, "head_dim must be 64 or 128");
+  if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads || q_heads / kv_heads > hh::kAttnQM)
+    return fail(HH_ESHAPE, "q_heads must be kv_heads x 1..8");
+  if (key_count < 0 || ring_size < 0 || start_position < 0 || (ring_size > 0 && key_count > ring_size))
+    return fail(HH_EINVAL, "key_count, ring_size and start_position must be >= 0, keys within the ring");
+  if (((uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)q) & 15)
+    return fail(HH_EALIGN, "q and the caches must be 16-byte aligned");
+  // Chunks of at least 256 keys (one 64-key tile per wave), up to ~1024 workgroups.
+  const int chunks = std::max(1, std::min(key_count / 256, std::max(1, 1024 / kv_heads)));
+  const int per_chunk = std::max(1, (key_count + chunks - 1) / chunks);
+  const size_t slots = (size_t)q_heads * chunks;
+  const size_t need = sizeof(float) * slots * (2 + (size_t)head_dim);
+  HH_HIP(hipSetDevice(ctx->device));
+  if (ctx->attn_bytes < need) {
+    if (ctx->capturing)
+      return fail(HH_EINVAL, "attention partials must be sized before capture (one eager call)");
+    if (ctx->attn) {
+      HH_HIP(hipStreamSynchronize(ctx->stream));
+      HH_HIP(hipFree(ctx->attn));
+      ctx->attn = nullptr;
+      ctx->attn_bytes = 0;
+    }
+    void *p = nullptr;
+    if (hipMalloc(&p, need) != hipSuccess) return fail(HH_ENOMEM, "attention partials allocation failed");
+    ctx->attn = (float *)p;
+    ctx->attn_bytes = need;
+  }
+  hh::AttnArgs a{};
+  a.q = q;
+  a.k = k_cache;
+  a.v = v_cache;
+  a.sinks = sinks;
+  a.qh = q_heads;
+  a.kvh = kv_heads;
+  a.d = head_dim;
+  a.keys = key_count;
+  a.ring = ring_size;
+  a.start = start_position;
+  a.chunks = chunks;
+  a.per_chunk = per_chunk;
+  a.scale = sm_scale;
+  a.pmax = ctx->attn;
+  a.pden = ctx->attn + slots;
+  a.pout = ctx->attn + 2 * slots;
+  a.out = out;
+  HH_HIP(hh::launch_attention_decode(a, ctx->stream));
+  ctx->dispatches += 2;
   return HH_OK;
 }
 

@@ -150,6 +150,18 @@ struct GemmArgs {
   float *y;                     // fp32 [T][H] layer output (written directly by the decode path)
 };
 
+// Decode attention (hh_attn.hip).
+struct AttnArgs {
+  const float *q;              // [qh][d]
+  const uint16_t *k, *v;       // fp16 [rows][kvh][d]
+  const uint16_t *sinks;       // bf16 [qh]
+  int qh, kvh, d, keys, ring, start, chunks, per_chunk;
+  float scale;
+  float *pmax, *pden, *pout;   // [qh][chunks], [qh][chunks], [qh][chunks][d]
+  float *out;                  // [qh][d]
+};
+constexpr int kAttnQM = 8;     // most query heads per kv head
+
 struct RouteArgs {
   const uint16_t *x;            // bf16 [T][H] expert input (and shared-gate input)
   const uint16_t *xr;           // bf16 [T][H] router input

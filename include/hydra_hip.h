@@ -171,6 +171,21 @@ int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *desc, const hh_moe_weights *w
                    const uint16_t *x, const uint16_t *x_router, int32_t tokens,
                    float *y, int32_t *topk_idx, float *topk_w);
 
+/* Decode attention with per-head sinks over an fp16 key/value history (the step before the
+ * router in every layer): ForwardEncoder.attention (ForwardEncoder.swift:1107-1160) with
+ * attention_decode_split/attention_decode_merge (attention.metal:307-450); semantics of
+ * ReferenceLayer.decode (ReferenceLayer.swift:150-180).
+ *   q        fp32 [q_heads][head_dim]
+ *   k_cache, v_cache  fp16 bits [rows][kv_heads][head_dim]; key position p is row p % ring_size
+ *            (ring_size 0: row p); keys start_position .. start_position + key_count - 1
+ *   sinks    bf16 [q_heads], in the softmax denominator only
+ *   out      fp32 [q_heads][head_dim]
+ * head_dim 64 or 128, q_heads = kv_heads × 1..8 (HH_ESHAPE otherwise).                     */
+int hh_attention_decode(hh_ctx *ctx, const float *q, const uint16_t *k_cache,
+                        const uint16_t *v_cache, const uint16_t *sinks, int32_t q_heads,
+                        int32_t kv_heads, int32_t head_dim, int32_t key_count, int32_t ring_size,
+                        int32_t start_position, float sm_scale, float *out);
+
 /* A layer stack as one HIP graph (the per-layer-stack graphs a HIP-backed
  * ModelRunner.forward / TextModelRunner would replay in place of encoding every layer's passes
  * per token, ModelRunner.swift:110-230): between hh_ctx_capture_begin and hh_ctx_capture_end
