@@ -645,7 +645,7 @@ int hh_attention_decode(hh_ctx *ctx, const float *q, const uint16_t *k_cache,
   if (((uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)q) & 15)
     return fail(HH_EALIGN, "q and the caches must be 16-byte aligned");
   // Chunks of at least 256 keys (one 64-key tile per wave), up to ~1024 workgroups.
-  const int chunks = std::max(1, std::min(key_count / 256, std::max(1, 1024 / kv_heads)));
+  const int chunks = std::max(1, std::min(key_count / 256, std::max(1, hh::kAttnMaxChunks / kv_heads)));
   const int per_chunk = std::max(1, (key_count + chunks - 1) / chunks);
   const size_t slots = (size_t)q_heads * chunks;
   const size_t need = sizeof(float) * slots * (2 + (size_t)head_dim);

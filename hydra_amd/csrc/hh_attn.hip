@@ -41,8 +41,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 template <int D>
 __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
   constexpr int QM = kAttnQM, DG = D / 8, JG = 64 / DG, KPL = 64 / JG;
-  __shared__ float s_q[QM][D];
-  __shared__ float s_p[4][64][QM];
+  __shared__ __align__(16) float s_q[QM][D];
+  __shared__ __align__(16) float s_p[4][64][QM];
   __shared__ float s_m[4][QM], s_l[4][QM];
   __shared__ float s_acc[4][QM][D];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -74,19 +74,41 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     // Phase 1: lane = key base + lane.
     const int key = base + lane;
     const bool valid = key < last;
+    // The tile's key rows (lane = key) and value rows (lane = key group, dims) are both issued
+    // before any arithmetic: one memory latency per tile. Rows past the chunk read row `first`
+    // (in bounds) and are masked.
+    f16x8 kr[DG], vr[KPL];
+    {
+      const f16x8 *kp = (const f16x8 *)(a.k + row_of(valid ? key : first) * row_stride + (size_t)kvh * D);
+#pragma unroll
+      for (int c = 0; c < DG; ++c) kr[c] = kp[c];
+#pragma unroll
+      for (int i = 0; i < KPL; ++i) {
+        const int j = base + jg * KPL + i;
+        vr[i] = *(const f16x8 *)(a.v + row_of(j < last ? j : first) * row_stride + (size_t)kvh * D + 8 * dg);
+      }
+    }
     float s[QM];
 #pragma unroll
     for (int h = 0; h < QM; ++h) s[h] = 0.f;
     if (valid) {
-      const f16x8 *kr = (const f16x8 *)(a.k + row_of(key) * row_stride + (size_t)kvh * D);
 #pragma unroll
       for (int c = 0; c < DG; ++c) {
-        const f16x8 kv = kr[c];
+        float kf[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float kf = (float)kv[e];
+        for (int e = 0; e < 8; ++e) kf[e] = (float)kr[c][e];
 #pragma unroll
-          for (int h = 0; h < QM; ++h) s[h] = fmaf(s_q[h][8 * c + e], kf, s[h]);
+        for (int h = 0; h < QM; ++h) {
+          // 16-byte broadcast reads of the query (every lane reads the same address).
+          const f32x4 qa = *(const f32x4 *)&s_q[h][8 * c], qb = *(const f32x4 *)&s_q[h][8 * c + 4];
+          s[h] = fmaf(qa[0], kf[0], s[h]);
+          s[h] = fmaf(qa[1], kf[1], s[h]);
+          s[h] = fmaf(qa[2], kf[2], s[h]);
+          s[h] = fmaf(qa[3], kf[3], s[h]);
+          s[h] = fmaf(qb[0], kf[4], s[h]);
+          s[h] = fmaf(qb[1], kf[5], s[h]);
+          s[h] = fmaf(qb[2], kf[6], s[h]);
+          s[h] = fmaf(qb[3], kf[7], s[h]);
         }
       }
     }
@@ -105,14 +127,12 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     // Phase 2: lane = (key group jg, dims 8·dg .. 8·dg + 7).
-#pragma unroll 4
+#pragma unroll
     for (int i = 0; i < KPL; ++i) {
       const int j = jg * KPL + i;
-      if (base + j >= last) break;
-      const f16x8 vv = *(const f16x8 *)(a.v + row_of(base + j) * row_stride + (size_t)kvh * D + 8 * dg);
-      float pj[QM];
-#pragma unroll
-      for (int h = 0; h < QM; ++h) pj[h] = s_p[wave][j][h];
+      const f16x8 vv = vr[i];   // a masked key has p = 0
+      const f32x4 pa = *(const f32x4 *)&s_p[wave][j][0], pb = *(const f32x4 *)&s_p[wave][j][4];
+      const float pj[QM] = {pa[0], pa[1], pa[2], pa[3], pb[0], pb[1], pb[2], pb[3]};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float vf = (float)vv[e];
@@ -163,21 +183,38 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
   }
 }
 
-// One workgroup of 64 per query head: the chunks in order.
+// One workgroup of 64 per query head. Lanes take chunks for the maximum and the denominator
+// (wave reductions), the chunk weights go to LDS, then lane i sums dimension i (and i + 64) over
+// the chunks in order, loads issued eight chunks at a time.
 template <int D>
 __global__ __launch_bounds__(64) void attn_merge_kernel(AttnArgs a) {
+  __shared__ float s_f[kAttnMaxChunks];
   const int h = blockIdx.x, lane = threadIdx.x;
   const float *pm = a.pmax + (size_t)h * a.chunks, *pd = a.pden + (size_t)h * a.chunks;
   float g = -INFINITY;
-  for (int c = 0; c < a.chunks; ++c) g = fmaxf(g, pm[c]);
+  for (int c = lane; c < a.chunks; c += 64) g = fmaxf(g, pm[c]);
+  g = wave_max(g);
   float den = 0.f;
-  for (int c = 0; c < a.chunks; ++c) den += pd[c] * __expf(pm[c] - g);
+  for (int c = lane; c < a.chunks; c += 64) den += pd[c] * __expf(pm[c] - g);
+  den = wave_sum(den);
   const float inv = 1.f / den;
-  for (int i = lane; i < D; i += 64) {
+  for (int c = lane; c < a.chunks; c += 64) s_f[c] = __expf(pm[c] - g) * inv;
+  __syncthreads();
+  const float *po = a.pout + (size_t)h * a.chunks * D;
+#pragma unroll
+  for (int r = 0; r < D / 64; ++r) {
+    const int i = lane + 64 * r;
     float sum = 0.f;
-    for (int c = 0; c < a.chunks; ++c)
-      sum += a.pout[((size_t)h * a.chunks + c) * D + i] * __expf(pm[c] - g);
-    a.out[(size_t)h * D + i] = sum * inv;
+    int c = 0;
+    for (; c + 8 <= a.chunks; c += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = po[(size_t)(c + u) * D + i];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) sum = fmaf(v[u], s_f[c + u], sum);
+    }
+    for (; c < a.chunks; ++c) sum = fmaf(po[(size_t)c * D + i], s_f[c], sum);
+    a.out[(size_t)h * D + i] = sum;
   }
 }
 

@@ -161,6 +161,7 @@ struct AttnArgs {
   float *out;                  // [qh][d]
 };
 constexpr int kAttnQM = 8;     // most query heads per kv head
+constexpr int kAttnMaxChunks = 1024;
 
 struct RouteArgs {
   const uint16_t *x;            // bf16 [T][H] expert input (and shared-gate input)
