@@ -27,15 +27,33 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 
 
+// Wave reductions on DPP (register moves, no LDS round trip): row_shr 1, 2, 4, 8 leave each
+// 16-lane row's result in its lane 15, row_bcast 15 and 31 carry it to lane 63, read back
+// with readlane. Lanes whose DPP source is outside the row or masked take the identity.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_f(float identity, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, identity),
+                                                               __builtin_bit_cast(int, v), CTRL, ROWS,
+                                                               0xf, false));
+}
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
+  const float id = -INFINITY;
+  v = fmaxf(v, dpp_f<0x111, 0xf>(id, v));
+  v = fmaxf(v, dpp_f<0x112, 0xf>(id, v));
+  v = fmaxf(v, dpp_f<0x114, 0xf>(id, v));
+  v = fmaxf(v, dpp_f<0x118, 0xf>(id, v));
+  v = fmaxf(v, dpp_f<0x142, 0xa>(id, v));
+  v = fmaxf(v, dpp_f<0x143, 0xc>(id, v));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  v += dpp_f<0x111, 0xf>(0.f, v);
+  v += dpp_f<0x112, 0xf>(0.f, v);
+  v += dpp_f<0x114, 0xf>(0.f, v);
+  v += dpp_f<0x118, 0xf>(0.f, v);
+  v += dpp_f<0x142, 0xa>(0.f, v);
+  v += dpp_f<0x143, 0xc>(0.f, v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 template <int D>
