@@ -85,13 +85,15 @@ class Workload:
         self.bank = [to_device(synth.make_tokens(self.desc.hidden, T, seed=1000 + i), dev)
                      for i in range(bank)]
         self.y = torch.empty((T, self.desc.hidden), dtype=torch.float32, device=dev)
-        self.idx = torch.empty((bank, T, self.desc.top_k), dtype=torch.int32, device=dev)
+        self.idx = torch.full((bank, T, self.desc.top_k), -1, dtype=torch.int32, device=dev)
+        self.written = set()
         self.w = torch.empty((T, self.desc.top_k), dtype=torch.float32, device=dev)
         self.ctx.reserve(self.desc, T)
         torch.cuda.synchronize()
 
     def step(self, i):
         b = i % len(self.bank)
+        self.written.add(b)
         self.layer.forward_into(self.bank[b], self.y, self.idx[b], self.w,
                                 weights_c=self.wc[i % len(self.wc)])
 
@@ -118,9 +120,13 @@ class Workload:
         return [m / max(calls, 1) for m in ms]
 
     def unique_experts(self):
-        """Mean distinct experts per step over the bank's routing."""
+        """Mean distinct experts per step over the routing of the bank entries this run has
+        actually routed (entries never stepped hold -1 and are left out)."""
         idx = self.idx.cpu().numpy()
-        return float(np.mean([np.unique(idx[i]).size for i in range(idx.shape[0])]))
+        rows = sorted(self.written)
+        assert rows, "no step has run"
+        assert all((idx[i] >= 0).all() for i in rows), "a routed bank entry holds no indices"
+        return float(np.mean([np.unique(idx[i]).size for i in rows]))
 
     def close(self):
         self.copies = self.wc = self.bank = None
@@ -139,6 +145,8 @@ def measure_decode(wl, T, steps, warmup, fused=False):
     sec = wl.run(steps, warmup)
     phases = wl.profiled(min(steps, 200))
     U = wl.unique_experts()
+    if T == 1:
+        assert U == desc.top_k, f"T=1 must touch exactly top_k experts, got {U}"
     up_b = U * up_bytes(desc) + T * desc.hidden * 2
     layer_b = U * F.streamed_expert_bytes(desc) + desc.experts * desc.hidden * 2
     wl.ctx.decode_fused(-1)
@@ -273,26 +281,38 @@ def measure_other(torch, name, desc, copies, T_prefill, steps):
     return {"decode": {"1": d}, "prefill": {str(T_prefill): p}}
 
 
-def cpu_baseline(seconds=10.0):
+def cpu_baseline(runs=5, seconds=2.5):
     """The fp64 restatement of the reference's CPU path (oracle/), GPT-OSS-20B shape
-    (configs[0]), timed on this host: T=16 tokens per call, OpenMP over rows."""
+    (configs[0]), timed on this host: `runs` timed runs of T=16 tokens per call with OpenMP over
+    rows (each about `seconds` long) and `runs` single-thread T=1 calls; the medians are
+    reported."""
     from oracle import oracle as O
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     layer = synth.make_layer(F.GPT_OSS_20B, seed=0)
     x = synth.make_tokens(F.GPT_OSS_20B.hidden, 16, seed=0)
     O.moe_forward(layer, x[:1], nthreads=threads)           # warm
-    done, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        O.moe_forward(layer, x, nthreads=threads)
-        done += 16
-    rate = done / (time.perf_counter() - t0)
-    t1 = time.perf_counter()
-    O.moe_forward(layer, x[:1], nthreads=1)
-    single = 1.0 / (time.perf_counter() - t1)
-    return {"value": rate, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"gpt-oss-20b MXFP4 MoE layer (BASELINE configs[0]), T=16 per call, "
-                      f"fp64 oracle with OpenMP over rows, {done} tokens in ~{seconds:.0f}s; "
-                      f"single-thread T=1: {single:.2f} tokens/s"}
+    omp, total = [], 0
+    for _ in range(runs):
+        done, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            O.moe_forward(layer, x, nthreads=threads)
+            done += 16
+        omp.append(done / (time.perf_counter() - t0))
+        total += done
+    single = []
+    for r in range(runs):
+        t1 = time.perf_counter()
+        O.moe_forward(layer, x[r:r + 1], nthreads=1)
+        single.append(1.0 / (time.perf_counter() - t1))
+    med = float(np.median(omp))
+    return {"value": med, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "runs": runs, "openmp_tokens_per_s": omp, "openmp_threads": threads,
+            "single_thread_tokens_per_s": float(np.median(single)),
+            "single_thread_runs": single,
+            "sample": f"gpt-oss-20b MXFP4 MoE layer (BASELINE configs[0]), fp64 oracle: median of "
+                      f"{runs} runs of T=16 calls with OpenMP over rows on {threads} threads "
+                      f"({total} tokens in ~{runs * seconds:.0f}s), and median of {runs} "
+                      f"single-thread T=1 calls"}
 
 
 TRAFFIC = "profiles/traffic_up_small_mx_gptoss20b_T1.json"
@@ -402,7 +422,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "mxfp4 weights x fp8-e4m3 activation terms (x: 2 terms, h: 3), fp32 accumulation",
         "data": "synthetic",
         "config": {"workload": "gpt-oss-20b-shaped MXFP4 MoE layer, decode T=1 (BASELINE configs[1])",
                    "hidden": 2880, "intermediate": 2880, "experts": 32, "top_k": 4,

@@ -58,6 +58,9 @@ struct hh_ctx {
   // Decode attention partials (per query head and chunk), grown on demand.
   float *attn = nullptr;
   size_t attn_bytes = 0;
+  // Instantiated graphs of this context that are not yet destroyed: they hold the arena's and
+  // the attention partials' device addresses, so neither may be reallocated while any exist.
+  int live_graphs = 0;
 };
 
 struct hh_graph {
@@ -160,6 +163,9 @@ int ensure_arena(hh_ctx *ctx, size_t bytes) {
   if (ctx->arena_bytes >= bytes) return HH_OK;
   if (ctx->capturing)
     return fail(HH_EINVAL, "the scratch arena must cover the call before capture (hh_ctx_reserve)");
+  if (ctx->live_graphs > 0)
+    return fail(HH_EINVAL, "the call needs a larger scratch arena, but graphs of this context still "
+                           "use the current one (reserve before capture, or destroy the graphs)");
   HH_HIP(hipSetDevice(ctx->device));
   if (ctx->arena) {
     HH_HIP(hipStreamSynchronize(ctx->stream));
@@ -582,6 +588,7 @@ int hh_ctx_capture_end(hh_ctx *ctx, hh_graph **out) {
   g->graph = graph;
   g->exec = exec;
   g->dispatches = recorded;
+  ctx->live_graphs += 1;
   *out = g;
   return HH_OK;
 }
@@ -601,6 +608,7 @@ int hh_graph_destroy(hh_graph *g) {
   hipStreamSynchronize(g->ctx->stream);
   if (g->exec) hipGraphExecDestroy(g->exec);
   if (g->graph) hipGraphDestroy(g->graph);
+  g->ctx->live_graphs -= 1;
   delete g;
   return HH_OK;
 }
@@ -653,6 +661,9 @@ int hh_attention_decode(hh_ctx *ctx, const float *q, const uint16_t *k_cache,
   if (ctx->attn_bytes < need) {
     if (ctx->capturing)
       return fail(HH_EINVAL, "attention partials must be sized before capture (one eager call)");
+    if (ctx->live_graphs > 0)
+      return fail(HH_EINVAL, "the call needs larger attention partials, but graphs of this context "
+                             "still use the current ones (destroy the graphs first)");
     if (ctx->attn) {
       HH_HIP(hipStreamSynchronize(ctx->stream));
       HH_HIP(hipFree(ctx->attn));

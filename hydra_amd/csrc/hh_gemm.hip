@@ -1277,7 +1277,11 @@ __device__ __forceinline__ bool flags_ready(const uint32_t *flags, int n, uint32
 // Whole wave: true once flags[0..n) all hold `epoch`, false past the deadline (wall clock).
 __device__ __forceinline__ bool wave_wait(const uint32_t *flags, int n, uint32_t epoch, uint64_t deadline) {
   for (;;) {
-    if (flags_ready(flags, n, epoch)) return true;
+    if (flags_ready(flags, n, epoch)) {
+      // Acquire: the data reads that follow are ordered after the flag reads.
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      return true;
+    }
     if (wall_clock64() > deadline) return false;
     __builtin_amdgcn_s_sleep(2);
   }
@@ -1293,6 +1297,8 @@ __device__ __forceinline__ bool group_wait(const uint32_t *flags, int n, uint32_
   return *s_flag != 0;
 }
 __device__ __forceinline__ void store_flag(uint32_t *flag, uint32_t epoch) {
+  // Release: the writer's data stores are ordered before the flag store.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   __hip_atomic_store(flag, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Before a flag store: this wave's device-scope data stores have completed.

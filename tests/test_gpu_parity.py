@@ -358,11 +358,36 @@ def test_fused_decode_equals_three_launch_decode(torch_dev, ctx, name):
 
 FULL = {
     "gpt-oss-20b": (F.GPT_OSS_20B, None, [1, 2, 4, 8, 16]),
-    "gpt-oss-120b-zipf": (F.GPT_OSS_120B, 1.1, [512]),
+    "gpt-oss-120b-zipf": (F.GPT_OSS_120B, 1.1, [512, 2048]),
     "qwen-q4": (F.QWEN_35B_A3B_Q4, None, [1, 16, 1024]),
     "qwen-q8": (F.QWEN_35B_A3B_Q8, None, [1, 1024]),
     "gemma-bf16": (F.GEMMA_BF16, None, [1, 2048]),
 }
+
+
+def tile_edge_sample(idx, experts, T, seed=0):
+    """At least 16 tokens (all of them when T < 16): the first and last token of the batch, a
+    few random ones, and the tokens at the 32- and 64-token tile edges of the prefill work
+    items (positions 0, 31, 32, 63, 64, 95, 96, 127, 128 and the last of an expert's segment in
+    the stable (token, rank) order) of the busiest experts and of random ones."""
+    if T <= 16:
+        return list(range(T))
+    rng = np.random.default_rng(T + seed)
+    flat = idx.ravel()
+    counts = np.bincount(flat, minlength=experts)
+    picks = set([0, T - 1]) | set(rng.choice(T, 4, replace=False).tolist())
+    busy = list(np.argsort(-counts, kind="stable")[:3])
+    used = [e for e in range(experts) if counts[e] > 0]
+    others = list(rng.choice(used, min(3, len(used)), replace=False))
+    for e in busy + others:
+        toks = np.nonzero(flat == e)[0] // idx.shape[1]     # stable (token, rank) order
+        n = len(toks)
+        for p in (0, 31, 32, 63, 64, 95, 96, 127, 128, n - 1):
+            if 0 <= p < n:
+                picks.add(int(toks[p]))
+    while len(picks) < 16:
+        picks.add(int(rng.integers(T)))
+    return sorted(picks)
 
 
 @pytest.mark.parametrize("name", list(FULL))
@@ -388,7 +413,7 @@ def test_full_size_layers_against_oracle_sample(torch_dev, ctx, name):
             else:
                 ri, _ = O.router_softmax_topk_renorm(logits[t], desc.top_k)
             assert np.array_equal(idx[t], ri), t
-        sample = sorted(set([0, T - 1] + list(np.random.default_rng(T).choice(T, min(T, 3), replace=False))))
+        sample = tile_edge_sample(idx, desc.experts, T)
         ry, _, _, _ = O.moe_forward(layer, x[sample], nthreads=min(16, os.cpu_count() or 1))
         assert rel_l2(y[sample], ry) < REL_L2
         # the batch equals one-token calls, bit for bit, on a sample of tokens

@@ -76,3 +76,34 @@ def test_capture_rules_are_enforced_without_a_gpu_call():
     assert L.hh_ctx_capture_end(None, C.byref(g)) != 0
     assert L.hh_graph_launch(None) != 0
     assert L.hh_graph_destroy(None) == 0
+
+
+@pytest.mark.gpu
+def test_growing_scratch_is_refused_while_a_graph_lives():
+    """A live graph holds the context's arena and attention-partial addresses: an eager call
+    that would reallocate either fails with HH_EINVAL until the graph is destroyed; a call
+    that fits still runs, and after destruction the growing call succeeds."""
+    import torch
+    from hydra_amd._lib import HydraHIPError
+    from hydra_amd.layer import Context, MoELayer
+    print("[gpu] graph blocks arena growth", flush=True)
+    ctx = Context(0)
+    try:
+        d = STACK[0]
+        layer = MoELayer(synth.make_layer(d, seed=55), ctx)
+        ctx.reserve(d, 1)
+        x = torch.zeros((1, d.hidden), dtype=torch.int16, device="cuda:0")
+        y = torch.empty((1, d.hidden), dtype=torch.float32, device="cuda:0")
+        torch.cuda.synchronize()
+        graph = ctx.capture(lambda: layer.forward_into(x, y))
+        layer.forward(synth.make_tokens(d.hidden, 1, seed=5))          # fits: runs
+        with pytest.raises(HydraHIPError) as e:
+            layer.forward(synth.make_tokens(d.hidden, 200, seed=6))    # would grow the arena
+        assert e.value.code == -1 and "graph" in str(e.value)
+        graph.launch()
+        ctx.synchronize()
+        graph.close()
+        y2, _, _ = layer.forward(synth.make_tokens(d.hidden, 200, seed=6))
+        assert torch.isfinite(y2).all()
+    finally:
+        ctx.close()
