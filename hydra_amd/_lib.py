@@ -18,7 +18,7 @@ EXPORTS = [
     "hh_moe_forward", "hh_mxfp4_dequant", "hh_mlx_dequant", "hh_router_topk", "hh_activation",
     "hh_permute", "hh_ctx_profile", "hh_ctx_profile_read", "hh_ctx_decode_fused", "hh_scatter_expert_tensor",
     "hh_ctx_capture_begin", "hh_ctx_capture_end", "hh_graph_launch", "hh_graph_destroy",
-    "hh_attention_decode",
+    "hh_attention_decode", "hh_moe_forward_noalloc",
 ]
 
 CODES = {0: "HH_OK", -1: "HH_EINVAL", -2: "HH_EALIGN", -3: "HH_ETOPK", -4: "HH_EHIP",
@@ -75,6 +75,7 @@ def lib() -> C.CDLL:
     L.hh_expert_blob_layout.argtypes = [C.POINTER(MoEDescC), i32, C.POINTER(BlobLayoutC)]
     L.hh_moe_forward.argtypes = [vp, C.POINTER(MoEDescC), C.POINTER(MoEWeightsC), vp, vp, i32,
                                  vp, vp, vp]
+    L.hh_moe_forward_noalloc.argtypes = L.hh_moe_forward.argtypes
     L.hh_mxfp4_dequant.argtypes = [vp, vp, vp, i64, vp]
     L.hh_mlx_dequant.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, vp]
     L.hh_router_topk.argtypes = [vp, C.POINTER(MoEDescC), C.POINTER(MoEWeightsC), vp, i32, vp,

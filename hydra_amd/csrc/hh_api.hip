@@ -61,6 +61,10 @@ struct hh_ctx {
   // Instantiated graphs of this context that are not yet destroyed: they hold the arena's and
   // the attention partials' device addresses, so neither may be reallocated while any exist.
   int live_graphs = 0;
+  // This device's copy of the static scratch array (hh_moe_forward_noalloc), or NULL when its
+  // address could not be resolved (scratch_error then says why).
+  uint8_t *scratch = nullptr;
+  std::string scratch_error;
 };
 
 struct hh_graph {
@@ -70,9 +74,38 @@ struct hh_graph {
   int64_t dispatches = 0;
 };
 
+// Scratch of hh_moe_forward_noalloc: a fixed array in every device's memory, held from module
+// load until the process ends. Host code never uses this name as an address (on the host it is
+// only a stand-in for the symbol); static_scratch() resolves each device's copy once.
+static __device__ __align__(256) uint8_t scratch[HH_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 thread_local std::string g_error;
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t *g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device `device`, resolved by
+// hipGetSymbolAddress on the first call per device and kept; NULL (with *err set) on failure.
+uint8_t *static_scratch(int device, std::string *err) {
+  if (device < 0 || device >= kMaxDevices) {
+    *err = "device index beyond the static scratch table";
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      *err = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+      return nullptr;
+    }
+    g_scratch_ptr[device] = (uint8_t *)p;
+  }
+  return g_scratch_ptr[device];
+}
 
 int fail(int code, const std::string &msg) {
   g_error = msg;
@@ -280,9 +313,9 @@ void fill_group(hh::ExpertGroup &g, const hh_moe_desc &d, const void *blobs, siz
 }
 
 // The timing events of the next phase when profiling is on (none otherwise).
-int phase_timing(hh_ctx *ctx, hh::Timing *tm) {
+int phase_timing(hh_ctx *ctx, hh::Timing *tm, bool off = false) {
   *tm = hh::Timing{};
-  if (!ctx->profile) return HH_OK;
+  if (!ctx->profile || off) return HH_OK;
   while (ctx->events_used + 2 > ctx->events.size()) {
     hipEvent_t ev;
     HH_HIP(hipEventCreate(&ev));
@@ -292,6 +325,130 @@ int phase_timing(hh_ctx *ctx, hh::Timing *tm) {
   tm->stop = ctx->events[ctx->events_used++];
   return HH_OK;
 }
+
+// Argument checks shared by the layer entry points (HH_OK or the error code).
+int check_forward(const hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
+                  const uint16_t *x, const uint16_t *x_router, int32_t T, const float *y) {
+  if (!ctx) return fail(HH_EINVAL, "ctx is NULL");
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (!w || !w->experts || !w->router_weight || !x || !y)
+    return fail(HH_EINVAL, "experts, router_weight, x and y are required");
+  if (d->router == HH_ROUTER_GEMMA && (!w->router_scale || !w->router_expert_scale))
+    return fail(HH_EINVAL, "the GEMMA router needs router_scale and router_expert_scale");
+  if (d->shared_intermediate > 0 && (!w->shared_expert || !w->shared_gate))
+    return fail(HH_EINVAL, "a shared expert needs shared_expert and shared_gate");
+  if (T < 0 || T > kMaxTokens) return fail(HH_EINVAL, "token count outside 0..65536");
+  if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)w->experts | (uintptr_t)w->router_weight |
+       (uintptr_t)(x_router ? x_router : x)) & 15)
+    return fail(HH_EALIGN, "x, x_router, y, experts and router_weight must be 16-byte aligned");
+  if (w->expert_stride % 256) return fail(HH_EALIGN, "expert_stride must be a multiple of 256");
+  if (w->shared_expert && ((uintptr_t)w->shared_expert & 255))
+    return fail(HH_EALIGN, "shared_expert must be 256-byte aligned");
+  if ((uintptr_t)w->experts & 255) return fail(HH_EALIGN, "experts must be 256-byte aligned");
+
+  return HH_OK;
+}
+
+// One layer over T ≥ 1 tokens with its scratch at `base` (laid out by plan(*d, T)). With
+// `noalloc` the call takes neither the one-launch decode (its flag buffer is allocated on first
+// use) nor profiling events.
+int forward_layer(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w, const uint16_t *x,
+                  const uint16_t *x_router, int32_t T, float *y, int32_t *topk_idx, float *topk_w,
+                  uint8_t *base, const Scratch &s, bool noalloc) {
+  int rc;
+
+  hh::RouteArgs r = route_args(*d, w, base, s, x, x_router, T);
+  if (topk_idx) r.topk_idx = topk_idx;
+  if (topk_w) r.topk_w = topk_w;
+  hh::Timing tm;
+  rc = phase_timing(ctx, &tm, noalloc);
+  if (rc) return rc;
+
+  hh::GemmArgs g{};
+  fill_group(g.grp[0], *d, w->experts, w->expert_stride, d->intermediate);
+  if (d->shared_intermediate > 0) fill_group(g.grp[1], *d, w->shared_expert, 0, d->shared_intermediate);
+  else g.grp[1] = g.grp[0];
+  g.hidden = d->hidden;
+  g.experts = d->experts;
+  g.top_k = d->top_k;
+  g.slots = s.slots;
+  g.quant = d->quant;
+  g.act = d->activation;
+  g.expert_bias = d->expert_bias;
+  g.group = d->group_size;
+  g.alpha = d->swiglu_alpha;
+  g.limit = d->swiglu_limit;
+  g.ldh = s.ldh;
+  g.max_work = s.max_work;
+  g.x = x;
+  g.order = r.order;
+  g.work = r.work;
+  g.n_work = r.n_work;
+  g.h_hi = (uint16_t *)(base + s.h_hi);
+  g.h_lo = (uint16_t *)(base + s.h_lo);
+  g.slot_w = r.slot_w;
+  g.slot_out = (float *)(base + s.slot_out);
+  g.y = y;
+  g.xq = r.xq;
+  g.xs = r.xs;
+  g.xld = s.xld;
+  g.hq = base + s.hq;
+  g.hs = base + s.hs;
+  g.hld = s.hld;
+
+  if (!noalloc && use_fused(ctx, *d, T)) {
+    // Decode in one launch (decode_mx): logits and h terms in the arena, flags in the
+    // context's flag buffer.
+    if ((rc = ensure_flags(ctx))) return rc;
+    hh::FuseArgs f{};
+    f.flags = ctx->flags;
+    f.status = (uint32_t *)(base + s.status);
+    if (++ctx->epoch == 0) ++ctx->epoch;   // flags start at 0
+    f.epoch = ctx->epoch;
+    HH_HIP(hh::launch_decode_fused(d->router == HH_ROUTER_GEMMA, g, r, f, ctx->stream, tm));
+    for (int p = 1; p < 4; ++p) {   // the other phases are empty: keep the record aligned
+      hh::Timing te;
+      if ((rc = phase_timing(ctx, &te, noalloc))) return rc;
+      if (te.start) {
+        HH_HIP(hipEventRecord(te.start, ctx->stream));
+        HH_HIP(hipEventRecord(te.stop, ctx->stream));
+      }
+    }
+    ctx->dispatches += 1;
+    return HH_OK;
+  }
+  HH_HIP(hh::launch_route(r, ctx->stream, tm));
+
+  if (T <= kSmallT) {
+    // Decode: exact logits → gate-up (selects the top-k itself) → down with the rank-ordered
+    // combine in its epilogue.
+    hh::Timing tm_down, tm_comb;
+    if ((rc = phase_timing(ctx, &tm, noalloc))) return rc;
+    if ((rc = phase_timing(ctx, &tm_down, noalloc))) return rc;
+    if ((rc = phase_timing(ctx, &tm_comb, noalloc))) return rc;
+    HH_HIP(hh::launch_small(d->quant, g, r, ctx->stream, tm, tm_down));
+    if (tm_comb.start) {   // no combine launch: an empty profiled phase keeps the record aligned
+      HH_HIP(hipEventRecord(tm_comb.start, ctx->stream));
+      HH_HIP(hipEventRecord(tm_comb.stop, ctx->stream));
+    }
+    ctx->dispatches += 3;
+    return HH_OK;
+  }
+  int rows = hh::gemm_rows_per_block(d->quant, 0);
+  g.row_tiles = (s.ldh + rows - 1) / rows;
+  if ((rc = phase_timing(ctx, &tm, noalloc))) return rc;
+  HH_HIP(hh::launch_gemm(0, d->quant, s.nt, g, ctx->stream, tm));
+  rows = hh::gemm_rows_per_block(d->quant, 1);
+  g.row_tiles = (d->hidden + rows - 1) / rows;
+  if ((rc = phase_timing(ctx, &tm, noalloc))) return rc;
+  HH_HIP(hh::launch_gemm(1, d->quant, s.nt, g, ctx->stream, tm));
+  if ((rc = phase_timing(ctx, &tm, noalloc))) return rc;
+  HH_HIP(hh::launch_combine(g.slot_out, s.slots, d->hidden, T, y, ctx->stream, tm));
+  ctx->dispatches += 6;   // route logits, select, dispatch, gate-up, down, combine
+  return HH_OK;
+}
+
 
 }  // namespace
 
@@ -308,6 +465,7 @@ int hh_ctx_create(hh_ctx **out, int32_t device) {
   HH_HIP(hipSetDevice(device));
   hh_ctx *c = new hh_ctx();
   c->device = device;
+  c->scratch = static_scratch(device, &c->scratch_error);   // device is current
   // Default priority, non-blocking with respect to the legacy default stream.
   hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
@@ -440,120 +598,29 @@ int hh_ctx_reserve(hh_ctx *ctx, const hh_moe_desc *d, int32_t max_tokens) {
 int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
                    const uint16_t *x, const uint16_t *x_router, int32_t T, float *y,
                    int32_t *topk_idx, float *topk_w) {
-  if (!ctx) return fail(HH_EINVAL, "ctx is NULL");
-  int rc = check_desc(d);
+  int rc = check_forward(ctx, d, w, x, x_router, T, y);
   if (rc) return rc;
-  if (!w || !w->experts || !w->router_weight || !x || !y)
-    return fail(HH_EINVAL, "experts, router_weight, x and y are required");
-  if (d->router == HH_ROUTER_GEMMA && (!w->router_scale || !w->router_expert_scale))
-    return fail(HH_EINVAL, "the GEMMA router needs router_scale and router_expert_scale");
-  if (d->shared_intermediate > 0 && (!w->shared_expert || !w->shared_gate))
-    return fail(HH_EINVAL, "a shared expert needs shared_expert and shared_gate");
-  if (T < 0 || T > kMaxTokens) return fail(HH_EINVAL, "token count outside 0..65536");
   if (T == 0) return HH_OK;
-  if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)w->experts | (uintptr_t)w->router_weight |
-       (uintptr_t)(x_router ? x_router : x)) & 15)
-    return fail(HH_EALIGN, "x, x_router, y, experts and router_weight must be 16-byte aligned");
-  if (w->expert_stride % 256) return fail(HH_EALIGN, "expert_stride must be a multiple of 256");
-  if (w->shared_expert && ((uintptr_t)w->shared_expert & 255))
-    return fail(HH_EALIGN, "shared_expert must be 256-byte aligned");
-  if ((uintptr_t)w->experts & 255) return fail(HH_EALIGN, "experts must be 256-byte aligned");
-
   HH_HIP(hipSetDevice(ctx->device));
   const Scratch s = plan(*d, T);
-  rc = ensure_arena(ctx, s.total);
+  if ((rc = ensure_arena(ctx, s.total))) return rc;
+  return forward_layer(ctx, d, w, x, x_router, T, y, topk_idx, topk_w, ctx->arena, s, false);
+}
+
+int hh_moe_forward_noalloc(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
+                           const uint16_t *x, const uint16_t *x_router, int32_t T, float *y,
+                           int32_t *topk_idx, float *topk_w) {
+  int rc = check_forward(ctx, d, w, x, x_router, T, y);
   if (rc) return rc;
-  uint8_t *base = ctx->arena;
-
-  hh::RouteArgs r = route_args(*d, w, base, s, x, x_router, T);
-  if (topk_idx) r.topk_idx = topk_idx;
-  if (topk_w) r.topk_w = topk_w;
-  hh::Timing tm;
-  rc = phase_timing(ctx, &tm);
-  if (rc) return rc;
-
-  hh::GemmArgs g{};
-  fill_group(g.grp[0], *d, w->experts, w->expert_stride, d->intermediate);
-  if (d->shared_intermediate > 0) fill_group(g.grp[1], *d, w->shared_expert, 0, d->shared_intermediate);
-  else g.grp[1] = g.grp[0];
-  g.hidden = d->hidden;
-  g.experts = d->experts;
-  g.top_k = d->top_k;
-  g.slots = s.slots;
-  g.quant = d->quant;
-  g.act = d->activation;
-  g.expert_bias = d->expert_bias;
-  g.group = d->group_size;
-  g.alpha = d->swiglu_alpha;
-  g.limit = d->swiglu_limit;
-  g.ldh = s.ldh;
-  g.max_work = s.max_work;
-  g.x = x;
-  g.order = r.order;
-  g.work = r.work;
-  g.n_work = r.n_work;
-  g.h_hi = (uint16_t *)(base + s.h_hi);
-  g.h_lo = (uint16_t *)(base + s.h_lo);
-  g.slot_w = r.slot_w;
-  g.slot_out = (float *)(base + s.slot_out);
-  g.y = y;
-  g.xq = r.xq;
-  g.xs = r.xs;
-  g.xld = s.xld;
-  g.hq = base + s.hq;
-  g.hs = base + s.hs;
-  g.hld = s.hld;
-
-  if (use_fused(ctx, *d, T)) {
-    // Decode in one launch (decode_mx): logits and h terms in the arena, flags in the
-    // context's flag buffer.
-    if ((rc = ensure_flags(ctx))) return rc;
-    hh::FuseArgs f{};
-    f.flags = ctx->flags;
-    f.status = (uint32_t *)(base + s.status);
-    if (++ctx->epoch == 0) ++ctx->epoch;   // flags start at 0
-    f.epoch = ctx->epoch;
-    HH_HIP(hh::launch_decode_fused(d->router == HH_ROUTER_GEMMA, g, r, f, ctx->stream, tm));
-    for (int p = 1; p < 4; ++p) {   // the other phases are empty: keep the record aligned
-      hh::Timing te;
-      if ((rc = phase_timing(ctx, &te))) return rc;
-      if (te.start) {
-        HH_HIP(hipEventRecord(te.start, ctx->stream));
-        HH_HIP(hipEventRecord(te.stop, ctx->stream));
-      }
-    }
-    ctx->dispatches += 1;
-    return HH_OK;
-  }
-  HH_HIP(hh::launch_route(r, ctx->stream, tm));
-
-  if (T <= kSmallT) {
-    // Decode: exact logits → gate-up (selects the top-k itself) → down with the rank-ordered
-    // combine in its epilogue.
-    hh::Timing tm_down, tm_comb;
-    if ((rc = phase_timing(ctx, &tm))) return rc;
-    if ((rc = phase_timing(ctx, &tm_down))) return rc;
-    if ((rc = phase_timing(ctx, &tm_comb))) return rc;
-    HH_HIP(hh::launch_small(d->quant, g, r, ctx->stream, tm, tm_down));
-    if (tm_comb.start) {   // no combine launch: an empty profiled phase keeps the record aligned
-      HH_HIP(hipEventRecord(tm_comb.start, ctx->stream));
-      HH_HIP(hipEventRecord(tm_comb.stop, ctx->stream));
-    }
-    ctx->dispatches += 3;
-    return HH_OK;
-  }
-  int rows = hh::gemm_rows_per_block(d->quant, 0);
-  g.row_tiles = (s.ldh + rows - 1) / rows;
-  if ((rc = phase_timing(ctx, &tm))) return rc;
-  HH_HIP(hh::launch_gemm(0, d->quant, s.nt, g, ctx->stream, tm));
-  rows = hh::gemm_rows_per_block(d->quant, 1);
-  g.row_tiles = (d->hidden + rows - 1) / rows;
-  if ((rc = phase_timing(ctx, &tm))) return rc;
-  HH_HIP(hh::launch_gemm(1, d->quant, s.nt, g, ctx->stream, tm));
-  if ((rc = phase_timing(ctx, &tm))) return rc;
-  HH_HIP(hh::launch_combine(g.slot_out, s.slots, d->hidden, T, y, ctx->stream, tm));
-  ctx->dispatches += 6;   // route logits, select, dispatch, gate-up, down, combine
-  return HH_OK;
+  if (T == 0) return HH_OK;
+  if (!ctx->scratch) return fail(HH_EHIP, "static scratch unavailable: " + ctx->scratch_error);
+  const Scratch s = plan(*d, T);
+  if (s.total > HH_NOALLOC_SCRATCH_BYTES)
+    return fail(HH_ENOMEM, "the call needs " + std::to_string(s.total) +
+                               " bytes of scratch; the allocation-free entry point has " +
+                               std::to_string((size_t)HH_NOALLOC_SCRATCH_BYTES) + " (use fewer tokens)");
+  HH_HIP(hipSetDevice(ctx->device));
+  return forward_layer(ctx, d, w, x, x_router, T, y, topk_idx, topk_w, ctx->scratch, s, true);
 }
 
 int hh_ctx_capture_begin(hh_ctx *ctx) {

@@ -171,6 +171,25 @@ int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *desc, const hh_moe_weights *w
                    const uint16_t *x, const uint16_t *x_router, int32_t tokens,
                    float *y, int32_t *topk_idx, float *topk_w);
 
+/* Allocation-free variant of hh_moe_forward, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference, whose decode path relies on scratch preallocated at start-up
+ * (LayerRunner.swift:6-10); this entry needs no reservation at all. Same arguments, results
+ * bit for bit equal to hh_moe_forward's. Its scratch is a fixed array of
+ * HH_NOALLOC_SCRATCH_BYTES in each device's memory, held from library load until the process
+ * ends, instead of the context's arena; the call makes no hipMalloc/hipFree, never takes the
+ * one-launch decode and records no profiling events. A call whose scratch plan exceeds the
+ * array returns HH_ENOMEM before enqueuing anything (decode of every family fits; prefill fits
+ * while T·(K+shared)·H·4 bytes of slot outputs and the routing tables stay under the limit,
+ * e.g. up to a few hundred tokens of a GPT-OSS layer). Every call on a device shares that
+ * device's array, so calls that overlap on one device (from two contexts or streams) race:
+ * serialise them on one stream. The array keeps the last call's contents; no kernel reads
+ * scratch it has not written in the same call, so nothing needs clearing between calls.    */
+#define HH_NOALLOC_SCRATCH_BYTES (16u << 20)
+int hh_moe_forward_noalloc(hh_ctx *ctx, const hh_moe_desc *desc, const hh_moe_weights *w,
+                           const uint16_t *x, const uint16_t *x_router, int32_t tokens,
+                           float *y, int32_t *topk_idx, float *topk_w);
+
 /* Decode attention with per-head sinks over an fp16 key/value history (the step before the
  * router in every layer): ForwardEncoder.attention (ForwardEncoder.swift:1107-1160) with
  * attention_decode_split/attention_decode_merge (attention.metal:307-450); semantics of
