@@ -18,7 +18,7 @@ EXPORTS = [
     "hh_moe_forward", "hh_mxfp4_dequant", "hh_mlx_dequant", "hh_router_topk", "hh_activation",
     "hh_permute", "hh_ctx_profile", "hh_ctx_profile_read", "hh_ctx_decode_fused", "hh_scatter_expert_tensor",
     "hh_ctx_capture_begin", "hh_ctx_capture_end", "hh_graph_launch", "hh_graph_destroy",
-    "hh_attention_decode", "hh_moe_forward_noalloc",
+    "hh_attention_decode", "hh_moe_forward_noalloc", "hh_moe_block_forward",
 ]
 
 CODES = {0: "HH_OK", -1: "HH_EINVAL", -2: "HH_EALIGN", -3: "HH_ETOPK", -4: "HH_EHIP",
@@ -44,6 +44,12 @@ class MoEWeightsC(C.Structure):
                 ("shared_expert", C.c_void_p), ("router_weight", C.c_void_p),
                 ("router_bias", C.c_void_p), ("router_scale", C.c_void_p),
                 ("router_expert_scale", C.c_void_p), ("shared_gate", C.c_void_p)]
+
+
+class BlockNormsC(C.Structure):
+    _fields_ = [("pre_norm", C.c_void_p), ("post_expert_norm", C.c_void_p),
+                ("post_dense_norm", C.c_void_p), ("post_norm", C.c_void_p),
+                ("layer_scalar", C.c_void_p), ("eps", C.c_float)]
 
 
 class BlobLayoutC(C.Structure):
@@ -76,6 +82,8 @@ def lib() -> C.CDLL:
     L.hh_moe_forward.argtypes = [vp, C.POINTER(MoEDescC), C.POINTER(MoEWeightsC), vp, vp, i32,
                                  vp, vp, vp]
     L.hh_moe_forward_noalloc.argtypes = L.hh_moe_forward.argtypes
+    L.hh_moe_block_forward.argtypes = [vp, C.POINTER(MoEDescC), C.POINTER(MoEWeightsC),
+                                       C.POINTER(BlockNormsC), vp, vp, i32, vp, vp]
     L.hh_mxfp4_dequant.argtypes = [vp, vp, vp, i64, vp]
     L.hh_mlx_dequant.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, vp]
     L.hh_router_topk.argtypes = [vp, C.POINTER(MoEDescC), C.POINTER(MoEWeightsC), vp, i32, vp,

@@ -24,8 +24,14 @@ size_t decode_fused_lds(const GemmArgs &a, int T);
 bool decode_fused_fits(int H, int I, int E, int K, int shared_inter);
 int decode_fused_flags(int T, int E, int K, int I);
 hipError_t launch_decode_fused(bool gemma, GemmArgs a, const RouteArgs &ra, FuseArgs f, hipStream_t s, Timing tm);
-hipError_t launch_combine(const float *slot_out, int slots, int H, int T, float *y, hipStream_t s,
-                          Timing tm);
+hipError_t launch_combine(const float *slot_out, int slots, int H, int T, float *y,
+                          const float *resid, hipStream_t s, Timing tm);
+hipError_t launch_block_norm(const float *hidden, const uint16_t *weight, int H, float eps,
+                             int pow_form, int T, uint16_t *xn, uint16_t *xr, hipStream_t s);
+hipError_t launch_block_gemma_finish(float *hidden, const float *mix, const float *dense,
+                                     const uint16_t *n1, const uint16_t *n2, const uint16_t *n,
+                                     const uint16_t *scalar, int H, float eps, int T,
+                                     hipStream_t s);
 hipError_t launch_attention_decode(const AttnArgs &a, hipStream_t s);
 hipError_t launch_mxfp4_dequant(const uint8_t *blocks, const uint8_t *scales, int64_t n,
                                 float *out, hipStream_t s);
@@ -355,7 +361,7 @@ int check_forward(const hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights 
 // use) nor profiling events.
 int forward_layer(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w, const uint16_t *x,
                   const uint16_t *x_router, int32_t T, float *y, int32_t *topk_idx, float *topk_w,
-                  uint8_t *base, const Scratch &s, bool noalloc) {
+                  uint8_t *base, const Scratch &s, bool noalloc, const float *resid = nullptr) {
   int rc;
 
   hh::RouteArgs r = route_args(*d, w, base, s, x, x_router, T);
@@ -390,6 +396,7 @@ int forward_layer(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w, co
   g.slot_w = r.slot_w;
   g.slot_out = (float *)(base + s.slot_out);
   g.y = y;
+  g.resid = resid;
   g.xq = r.xq;
   g.xs = r.xs;
   g.xld = s.xld;
@@ -397,7 +404,7 @@ int forward_layer(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w, co
   g.hs = base + s.hs;
   g.hld = s.hld;
 
-  if (!noalloc && use_fused(ctx, *d, T)) {
+  if (!noalloc && !resid && use_fused(ctx, *d, T)) {
     // Decode in one launch (decode_mx): logits and h terms in the arena, flags in the
     // context's flag buffer.
     if ((rc = ensure_flags(ctx))) return rc;
@@ -444,7 +451,7 @@ int forward_layer(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w, co
   if ((rc = phase_timing(ctx, &tm, noalloc))) return rc;
   HH_HIP(hh::launch_gemm(1, d->quant, s.nt, g, ctx->stream, tm));
   if ((rc = phase_timing(ctx, &tm, noalloc))) return rc;
-  HH_HIP(hh::launch_combine(g.slot_out, s.slots, d->hidden, T, y, ctx->stream, tm));
+  HH_HIP(hh::launch_combine(g.slot_out, s.slots, d->hidden, T, y, resid, ctx->stream, tm));
   ctx->dispatches += 6;   // route logits, select, dispatch, gate-up, down, combine
   return HH_OK;
 }
@@ -605,6 +612,47 @@ int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
   const Scratch s = plan(*d, T);
   if ((rc = ensure_arena(ctx, s.total))) return rc;
   return forward_layer(ctx, d, w, x, x_router, T, y, topk_idx, topk_w, ctx->arena, s, false);
+}
+
+int hh_moe_block_forward(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
+                         const hh_block_norms *nm, float *hidden, const float *dense_out,
+                         int32_t T, int32_t *topk_idx, float *topk_w) {
+  if (!nm || !nm->pre_norm) return fail(HH_EINVAL, "norms and norms->pre_norm are required");
+  const bool gemma = nm->post_expert_norm != nullptr;
+  if (gemma && (!nm->post_dense_norm || !nm->post_norm || !dense_out))
+    return fail(HH_EINVAL, "Gemma branches need post_dense_norm, post_norm and dense_out");
+  if (!hidden) return fail(HH_EINVAL, "hidden is NULL");
+  // The layer's checks, with the bf16 input the block writes standing in for x.
+  int rc = check_forward(ctx, d, w, (const uint16_t *)hidden, nullptr, T, hidden);
+  if (rc) return rc;
+  if (d->hidden > 8192) return fail(HH_ESHAPE, "the block entry takes hidden <= 8192");
+  if (dense_out && ((uintptr_t)dense_out & 15)) return fail(HH_EALIGN, "dense_out must be 16-byte aligned");
+  if (T == 0) return HH_OK;
+  HH_HIP(hipSetDevice(ctx->device));
+  const Scratch s = plan(*d, T);
+  // After the layer's scratch: the bf16 layer input, the GEMMA router's bf16 residual, and (Gemma
+  // branches) the expert branch's fp32 output.
+  const size_t row16 = align_up(sizeof(uint16_t) * (size_t)T * d->hidden, 256);
+  const size_t row32 = align_up(sizeof(float) * (size_t)T * d->hidden, 256);
+  const bool router_resid = d->router == HH_ROUTER_GEMMA;
+  const size_t o_xn = s.total, o_xr = o_xn + row16, o_mix = o_xr + (router_resid ? row16 : 0);
+  const size_t total = o_mix + (gemma ? row32 : 0);
+  if ((rc = ensure_arena(ctx, total))) return rc;
+  uint8_t *base = ctx->arena;
+  uint16_t *xn = (uint16_t *)(base + o_xn);
+  uint16_t *xr = router_resid ? (uint16_t *)(base + o_xr) : nullptr;
+  HH_HIP(hh::launch_block_norm(hidden, nm->pre_norm, d->hidden, nm->eps, router_resid ? 1 : 0, T,
+                               xn, xr, ctx->stream));
+  ctx->dispatches += 1;
+  if (!gemma)
+    return forward_layer(ctx, d, w, xn, xr, T, hidden, topk_idx, topk_w, base, s, false, hidden);
+  float *mix = (float *)(base + o_mix);
+  if ((rc = forward_layer(ctx, d, w, xn, xr, T, mix, topk_idx, topk_w, base, s, false))) return rc;
+  HH_HIP(hh::launch_block_gemma_finish(hidden, mix, dense_out, nm->post_dense_norm,
+                                       nm->post_expert_norm, nm->post_norm, nm->layer_scalar,
+                                       d->hidden, nm->eps, T, ctx->stream));
+  ctx->dispatches += 1;
+  return HH_OK;
 }
 
 int hh_moe_forward_noalloc(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,

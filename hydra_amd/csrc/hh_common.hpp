@@ -148,6 +148,7 @@ struct GemmArgs {
   const float *slot_w;          // fp32 [T·slots] routing weight of each slot
   float *slot_out;              // fp32 [T·slots][H] (T > 16)
   float *y;                     // fp32 [T][H] layer output (written directly by the decode path)
+  const float *resid;           // fp32 [T][H] residual added to the mixture (y = resid + Σ slots), or null
 };
 
 // Decode attention (hh_attn.hip).

@@ -1244,7 +1244,9 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
   if (tid < 16) {
     float y = s_o[0][tid];
     for (int qq = 1; qq < S; ++qq) y += s_o[qq][tid];
-    a.y[(size_t)t * H + rb + tid] = y;
+    const size_t o = (size_t)t * H + rb + tid;
+    if (a.resid) y = a.resid[o] + y;
+    a.y[o] = y;
   }
   __syncthreads();   // the next item rewrites the LDS rows and s_o
   }
@@ -1784,7 +1786,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 // y[t][j] = Σ_r slot[t·slots + r][j] in rank order (sum_expert_slices, dense.metal:147; the
 // shared expert's slot comes last as in QwenReferenceLayer.swift:399-404).
 __global__ __launch_bounds__(256) void combine_kernel(const float *slot_out, int slots, int H,
-                                                      int T, float *y) {
+                                                      int T, float *y, const float *resid) {
   const size_t n4 = (size_t)T * H / 4;
   for (size_t q = blockIdx.x * 256ull + threadIdx.x; q < n4; q += (size_t)gridDim.x * 256) {
     const size_t t = (q * 4) / H, j = (q * 4) % H;
@@ -1793,6 +1795,10 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *slot_out, int
     for (int r = 1; r < slots; ++r) {
       const f32x4 v = src[(size_t)r * H / 4];
       s[0] += v[0]; s[1] += v[1]; s[2] += v[2]; s[3] += v[3];
+    }
+    if (resid) {   // the residual stream: y = resid + mixture (ReferenceLayer.swift:202)
+      const f32x4 r = *(const f32x4 *)(resid + t * H + j);
+      s[0] = r[0] + s[0]; s[1] = r[1] + s[1]; s[2] = r[2] + s[2]; s[3] = r[3] + s[3];
     }
     *(f32x4 *)(y + t * H + j) = s;
   }
@@ -3143,13 +3149,13 @@ hipError_t launch_decode_fused(bool gemma, GemmArgs a, const RouteArgs &ra, Fuse
   return hipGetLastError();
 }
 
-hipError_t launch_combine(const float *slot_out, int slots, int H, int T, float *y, hipStream_t s,
-                          Timing tm) {
+hipError_t launch_combine(const float *slot_out, int slots, int H, int T, float *y,
+                          const float *resid, hipStream_t s, Timing tm) {
   const size_t n4 = (size_t)T * H / 4;
   unsigned blocks = (unsigned)std::min<size_t>((n4 + 255) / 256, 4096);
   if (blocks == 0) return hipSuccess;
   hipExtLaunchKernelGGL(combine_kernel, dim3(blocks), dim3(256), 0, s, tm.start, tm.stop, 0,
-                        slot_out, slots, H, T, y);
+                        slot_out, slots, H, T, y, resid);
   return hipGetLastError();
 }
 

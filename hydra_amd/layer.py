@@ -17,7 +17,7 @@ import numpy as np
 import torch
 
 from . import formats as F
-from ._lib import MoEWeightsC, check, desc_c, lib
+from ._lib import BlockNormsC, MoEWeightsC, check, desc_c, lib
 
 
 def _ptr(t):
@@ -166,6 +166,19 @@ class MoELayer:
         check(lib().hh_moe_forward(self.ctx.handle, C.byref(self._desc_c),
                                    C.byref(weights_c or self._weights_c), _ptr(x),
                                    _ptr(x_router), T, _ptr(y), _ptr(idx), _ptr(w)))
+
+    def block_forward_into(self, norms: dict, hidden: torch.Tensor,
+                           dense_out: torch.Tensor | None = None, idx: torch.Tensor | None = None,
+                           w: torch.Tensor | None = None) -> None:
+        """The FFN block on the fp32 residual stream `hidden` [T][H], updated in place
+        (hh_moe_block_forward): `norms` maps pre_norm / post_expert_norm / post_dense_norm /
+        post_norm / layer_scalar to device bf16 tensors (absent = NULL) and eps to a float."""
+        nc = BlockNormsC(_ptr(norms.get("pre_norm")), _ptr(norms.get("post_expert_norm")),
+                         _ptr(norms.get("post_dense_norm")), _ptr(norms.get("post_norm")),
+                         _ptr(norms.get("layer_scalar")), float(norms.get("eps", 1e-5)))
+        check(lib().hh_moe_block_forward(self.ctx.handle, C.byref(self._desc_c),
+                                         C.byref(self._weights_c), C.byref(nc), _ptr(hidden),
+                                         _ptr(dense_out), hidden.shape[0], _ptr(idx), _ptr(w)))
 
     def forward(self, x, x_router=None):
         """x: bf16 bits [T][H] (numpy uint16 or device int16). Returns (y fp32 [T][H],

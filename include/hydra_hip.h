@@ -171,6 +171,41 @@ int hh_moe_forward(hh_ctx *ctx, const hh_moe_desc *desc, const hh_moe_weights *w
                    const uint16_t *x, const uint16_t *x_router, int32_t tokens,
                    float *y, int32_t *topk_idx, float *topk_w);
 
+/* The whole FFN block around the MoE layer, on the fp32 residual stream `hidden` [T][H]
+ * (updated in place), with the RMSNorms and residual adds fused around hh_moe_forward's
+ * kernels. Two structures, chosen by norms->post_expert_norm:
+ *
+ *   pre-norm (post_expert_norm NULL; GPT-OSS, Qwen):
+ *       x = bf16(rmsnorm(hidden, pre_norm));  hidden += moe(x)
+ *     ReferenceLayer.decode (ReferenceLayer.swift:189-202), QwenLayerRunner
+ *     (QwenLayerRunner.swift:11-14); the GPU sequence rmsNorm → router → experts → addInPlace
+ *     of LayerRunner.swift:202-216 and :279-301. rmsnorm(v, w) = v·(mean v² + eps)^-½·w
+ *     (ReferenceOps.swift:20-25). The residual add is done by the layer's last kernel.
+ *   Gemma's parallel branches (post_expert_norm set; dense_out, post_dense_norm, post_norm
+ *   required): the expert branch reads x = bf16(rmsnorm(hidden, pre_norm)) (the
+ *   pre_feedforward_layernorm_2), the GEMMA router reads bf16(hidden) (the residual), and
+ *       hidden = (hidden + rmsnorm(rmsnorm(dense_out, post_dense_norm)
+ *                                  + rmsnorm(moe(x), post_expert_norm), post_norm)) · scalar
+ *     Gemma4ReferenceLayer.forward (Gemma4ReferenceLayer.swift:175-214),
+ *     Gemma4LayerRunner.encodeCombineBranches (Gemma4LayerRunner.swift:683-723). dense_out is
+ *     the dense MLP's output before its post-norm (post_feedforward_layernorm_1).
+ *
+ * Norms and sums are computed in fp64 and x is rounded once to bf16 (the layer's input format,
+ * as for hh_moe_forward). H ≤ 8192. Norm weights are bf16 [H]; layer_scalar bf16 [1] or NULL
+ * (1). The pow form (mean + eps)^-½ of Gemma4ReferenceOps.swift:28 is used for the GEMMA
+ * router's layers, 1/√(mean + eps) otherwise.                                                */
+typedef struct hh_block_norms {
+    const uint16_t *pre_norm;          /* the expert input's RMSNorm weight (required)          */
+    const uint16_t *post_expert_norm;  /* Gemma post_feedforward_layernorm_2, or NULL          */
+    const uint16_t *post_dense_norm;   /* Gemma post_feedforward_layernorm_1                   */
+    const uint16_t *post_norm;         /* Gemma post_feedforward_layernorm                     */
+    const uint16_t *layer_scalar;      /* Gemma layer_scalar (bf16 [1]) or NULL                */
+    float eps;                         /* the model's rms_norm_eps                             */
+} hh_block_norms;
+int hh_moe_block_forward(hh_ctx *ctx, const hh_moe_desc *desc, const hh_moe_weights *w,
+                         const hh_block_norms *norms, float *hidden, const float *dense_out,
+                         int32_t tokens, int32_t *topk_idx, float *topk_w);
+
 /* Allocation-free variant of hh_moe_forward, for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
  * counterpart in the reference, whose decode path relies on scratch preallocated at start-up

@@ -294,3 +294,88 @@ def attention_decode(q, k_cache, v_cache, sinks, kv_heads, key_count, start_posi
     L.hho_attention_decode(_p(q), _p(k), _p(v), _p(s), qh, kv_heads, d, key_count, ring_size,
                            start_position, float(sm_scale), _p(out))
     return out
+
+
+# ---- the FFN block around the MoE layer (RMSNorm, residual, Gemma's branch norms) ------------
+
+def rms_norm(x, weight, eps, pow_form=False) -> np.ndarray:
+    """RMSNorm of each row in fp64: x·f·w with f = 1/√(mean(x²)+eps) (ReferenceOps.rmsNorm,
+    ReferenceOps.swift:20-25) or, with `pow_form`, f = (mean(x²)+eps)^-½ (Gemma4ReferenceOps
+    .rmsNorm, Gemma4ReferenceOps.swift:25-31); `weight` None = unscaled. The mean of squares is
+    numpy's (pairwise) sum, which differs from the reference's left-to-right sum only in the
+    last bits of fp64."""
+    x = np.asarray(x, np.float64)
+    m = np.mean(x * x, axis=-1, keepdims=True) + eps
+    f = m ** -0.5 if pow_form else 1.0 / np.sqrt(m)
+    out = x * f
+    return out if weight is None else out * np.asarray(weight, np.float64)
+
+
+def f64_to_bf16(x) -> np.ndarray:
+    """fp64 → bf16 bits, one round to nearest even (NaN → quiet NaN). Normal results round
+    the fp64 significand at bf16's last bit directly; results below bf16's normal range go
+    through exact rational arithmetic."""
+    from fractions import Fraction
+    x = np.ascontiguousarray(x, np.float64)
+    bits = x.view(np.uint64)
+    lsb = (bits >> np.uint64(45)) & np.uint64(1)
+    r = (bits + np.uint64((1 << 44) - 1) + lsb) & ~np.uint64((1 << 45) - 1)
+    with np.errstate(over="ignore"):            # past bf16's range: inf, as RNE gives
+        out = (r.view(np.float64).astype(np.float32).view(np.uint32) >> np.uint32(16)).astype(np.uint16)
+    tiny = np.abs(x) < 2.0 ** -126
+    for i in zip(*np.nonzero(tiny)):
+        v = Fraction(float(x[i]))
+        q = v / Fraction(2) ** -133            # bf16 subnormal step 2^-133
+        n = int(q)                              # toward zero
+        rem = q - n
+        if abs(rem) > Fraction(1, 2) or (abs(rem) == Fraction(1, 2) and n % 2):
+            n += 1 if q > 0 else -1
+        out[i] = (0x8000 if (x[i] < 0 or (x[i] == 0 and np.signbit(x[i]))) else 0) | abs(n)
+    out[np.isnan(x)] = 0x7FC0
+    return out
+
+
+def block_forward(desc, norms, hidden, moe, dense_out=None, bf16_input=True):
+    """The FFN block around the MoE layer on an fp32/fp64 residual stream `hidden` [T][H]:
+    returns (new hidden fp64 [T][H], idx, w, the layer input x).
+
+    Pre-norm (no post_expert_norm; GPT-OSS ReferenceLayer.swift:189-202, Qwen
+    QwenLayerRunner.swift:11-14): x = rmsnorm(hidden, pre_norm); hidden + moe(x).
+    Gemma (Gemma4ReferenceLayer.swift:175-214): the router reads the residual, the experts
+    x = rmsnorm(hidden, pre_norm); hidden + rmsnorm(rmsnorm(dense_out, post_dense_norm) +
+    rmsnorm(moe(x), post_expert_norm), post_norm), times layer_scalar.
+
+    `norms` holds fp64 weights (layer_scalar: one value, or None) and eps. `moe(x, x_router)`
+    returns (y, idx, w). With `bf16_input` the layer input x (and the GEMMA router's residual)
+    is rounded to bf16 bits, the format the layer's C ABI takes (x through f64_to_bf16, the
+    fp32 residual through f32_to_bf16); without it the fp64 values go to `moe` as they are."""
+    hidden = np.atleast_2d(np.asarray(hidden, np.float64))
+    eps = float(norms["eps"])
+    gemma_router = desc.router == 2
+    xn = rms_norm(hidden, norms["pre_norm"], eps, pow_form=gemma_router)
+    if bf16_input:
+        x = f64_to_bf16(xn)
+        xr = f32_to_bf16(hidden.astype(np.float32)) if gemma_router else None
+    else:
+        x, xr = xn, (hidden if gemma_router else None)
+    y, idx, wts = moe(x, xr)
+    if norms.get("post_expert_norm") is None:
+        return hidden + y, idx, wts, x
+    b1 = rms_norm(np.asarray(dense_out, np.float64), norms["post_dense_norm"], eps, pow_form=True)
+    b2 = rms_norm(y, norms["post_expert_norm"], eps, pow_form=True)
+    c = rms_norm(b1 + b2, norms["post_norm"], eps, pow_form=True)
+    ls = 1.0 if norms.get("layer_scalar") is None else float(np.ravel(norms["layer_scalar"])[0])
+    return (hidden + c) * ls, idx, wts, x
+
+
+def block_forward_layer(layer, norms_bf16, hidden, dense_out=None, nthreads=1):
+    """block_forward over a synthetic/quantised layer (moe_forward), with the norm weights
+    given as bf16 bits, as the C ABI takes them."""
+    desc = layer["desc"]
+    to64 = lambda v: None if v is None else bf16_to_f32(v).astype(np.float64)
+    norms = {k: (to64(v) if k != "eps" else v) for k, v in norms_bf16.items()}
+
+    def moe(x, xr):
+        y, idx, w, _ = moe_forward(layer, x, x_router=xr, nthreads=nthreads)
+        return y, idx, w
+    return block_forward(desc, norms, hidden, moe, dense_out)

@@ -6,7 +6,7 @@ Run once in a container where the reference is mounted:
 Only data is copied (inputs and expected outputs the reference's tests hold):
   * Tests/HydraFormatTests/Fixtures/mxfp4_{packed.bin,scales.bin,expected.f32}
     (written by the reference's tools/gen_mxfp4_fixture.py; used by MXFP4Tests.swift:19-47)
-  * reference_ops.json keys "router", "swiglu"          (ReferenceOpsTests.swift:127-216)
+  * reference_ops.json keys "router", "swiglu", "rms_norm" (ReferenceOpsTests.swift)
   * reference_ops.json keys "sdpa_full", "sdpa_sliding"  (attention with sinks; written by the
     reference's tools/gen_reference_fixtures.py:100-128, 217-220)
   * gemma4_operators.json keys "gelu_tanh", "router", "rms_norm", "rms_norm_unscaled",
@@ -29,7 +29,7 @@ def main(ref: str) -> None:
     with open(os.path.join(rfx, "reference_ops.json")) as f:
         ops = json.load(f)
     with open(os.path.join(HERE, "reference_ops_moe.json"), "w") as f:
-        json.dump({k: ops[k] for k in ["router", "swiglu"]}, f)
+        json.dump({k: ops[k] for k in ["router", "swiglu", "rms_norm"]}, f)
     with open(os.path.join(HERE, "reference_ops_attention.json"), "w") as f:
         json.dump({k: ops[k] for k in ["sdpa_full", "sdpa_sliding"]}, f)
     with open(os.path.join(rfx, "gemma4_operators.json")) as f:
