@@ -43,7 +43,11 @@ class MoEWeightsC(C.Structure):
     _fields_ = [("experts", C.c_void_p), ("expert_stride", C.c_size_t),
                 ("shared_expert", C.c_void_p), ("router_weight", C.c_void_p),
                 ("router_bias", C.c_void_p), ("router_scale", C.c_void_p),
-                ("router_expert_scale", C.c_void_p), ("shared_gate", C.c_void_p)]
+                ("router_expert_scale", C.c_void_p), ("shared_gate", C.c_void_p),
+                ("router_bits", C.c_int32), ("router_words", C.c_void_p),
+                ("router_scales", C.c_void_p), ("router_biases", C.c_void_p),
+                ("shared_gate_words", C.c_void_p), ("shared_gate_scales", C.c_void_p),
+                ("shared_gate_biases", C.c_void_p)]
 
 
 class BlockNormsC(C.Structure):

@@ -18,10 +18,11 @@ expert suffixes of `RepackPlan.swift:208-215`; `Gemma4Config.swift:183-208` (rou
 `language_model.model`, experts `mlp.switch_mlp.{gate,up,down}_proj.{weight,scales,biases}`,
 shared expert `mlp.shared_expert.*`, router `mlp.gate`, shared gate `mlp.shared_expert_gate`).
 
-The layer's router takes bf16 weights (`hh_moe_weights.router_weight`). Published Qwen MLX
-builds quantise `mlp.gate` and `mlp.shared_expert_gate` to 8 bits (`Qwen35MoeConfig.swift:341-342`);
-their dequantised values are not bf16 numbers, so loading one raises `CheckpointError` instead
-of rounding them silently. A checkpoint that stores those two as BF16 loads.
+Published Qwen MLX builds quantise `mlp.gate` and `mlp.shared_expert_gate` to 8 bits
+(`Qwen35MoeConfig.swift:340-342`: `.weight` U32 words, `.scales` and `.biases` BF16, group 64);
+they load as the layer's MLX-affine router (`hh_moe_weights.router_bits`, exact fp64 logits),
+with the bit width read from the word count. A checkpoint that stores them as BF16 loads as a
+bf16 router.
 """
 from __future__ import annotations
 
@@ -147,8 +148,9 @@ def expert_sources(desc: F.MoEDesc, family: str, layer: int, shared: bool = Fals
     return [(slot, f"{p}.{suffix}", dt, lead + shape) for slot, (suffix, dt, shape) in enumerate(spec)]
 
 
-def router_sources(desc: F.MoEDesc, family: str, layer: int):
-    """{MoELayer tensor key: (tensor name, dtype, shape, required)}."""
+def router_sources(desc: F.MoEDesc, family: str, layer: int, router_bits: int = 0):
+    """{MoELayer tensor key: (tensor name, dtype, shape, required)}; `router_bits` 4 or 8 names
+    Qwen's MLX-affine router and shared-gate tensors instead of bf16 ones."""
     H, E = desc.hidden, desc.experts
     if family == "gpt-oss":
         p = f"model.layers.{layer}.mlp.router"
@@ -161,6 +163,15 @@ def router_sources(desc: F.MoEDesc, family: str, layer: int):
                 "router_expert_scale": (f"{p}.per_expert_scale", "BF16", (E,), True)}
     if family == "qwen3.5-moe":
         p = f"language_model.model.layers.{layer}.mlp"
+        if router_bits:
+            out = {}
+            for key, stem, rows in [("router", f"{p}.gate", E), ("shared_gate", f"{p}.shared_expert_gate", 1)]:
+                if key == "shared_gate" and not desc.shared_intermediate:
+                    continue
+                out[f"{key}_words"] = (f"{stem}.weight", "U32", (rows, H * router_bits // 32), True)
+                out[f"{key}_scales"] = (f"{stem}.scales", "BF16", (rows, H // 64), True)
+                out[f"{key}_biases"] = (f"{stem}.biases", "BF16", (rows, H // 64), True)
+            return out
         out = {"router_weight": (f"{p}.gate.weight", "BF16", (E, H), True)}
         if desc.shared_intermediate:
             out["shared_gate"] = (f"{p}.shared_expert_gate.weight", "BF16", (1, H), True)
@@ -168,9 +179,19 @@ def router_sources(desc: F.MoEDesc, family: str, layer: int):
     raise CheckpointError(f"unknown family {family!r}")
 
 
-def _quantised_router(ck: Checkpoint, name: str) -> bool:
+def _quantised_router_bits(ck: Checkpoint, desc: F.MoEDesc, family: str, layer: int) -> int:
+    """The MLX bit width of the layer's router tensor, 0 when it is stored as bf16."""
+    name = router_sources(desc, family, layer)["router_weight"][0]
     stem = name[:-len(".weight")]
-    return name in ck and ck.where[name].entries[name]["dtype"] == "U32" and f"{stem}.scales" in ck
+    if name not in ck or ck.where[name].entries[name]["dtype"] != "U32" or f"{stem}.scales" not in ck:
+        return 0
+    if family != "qwen3.5-moe":
+        raise CheckpointError(f"{name} is MLX-quantised; only Qwen layers take an MLX router")
+    words = ck.where[name].entries[name]["shape"][-1]
+    bits = words * 32 // desc.hidden
+    if bits not in (4, 8) or words * 32 != bits * desc.hidden:
+        raise CheckpointError(f"{name}: {words} words per row of {desc.hidden} is neither 4- nor 8-bit")
+    return bits
 
 
 def load_moe_layer(path_or_ckpt, desc: F.MoEDesc, family: str, layer: int,
@@ -180,10 +201,8 @@ def load_moe_layer(path_or_ckpt, desc: F.MoEDesc, family: str, layer: int,
     ck = path_or_ckpt if isinstance(path_or_ckpt, Checkpoint) else Checkpoint(path_or_ckpt)
     routed = expert_sources(desc, family, layer)
     shared = expert_sources(desc, family, layer, shared=True) if desc.shared_intermediate else []
-    routers = router_sources(desc, family, layer)
-    for key, (name, dt, shape, required) in routers.items():
-        if _quantised_router(ck, name):
-            raise CheckpointError(f"{name} is MLX-quantised; the layer's router takes bf16 weights")
+    router_bits = _quantised_router_bits(ck, desc, family, layer)
+    routers = router_sources(desc, family, layer, router_bits)
     # Every tensor is checked before any device memory is touched.
     routed_data = [(slot, ck.tensor(n, dt, sh)) for slot, n, dt, sh in routed]
     shared_data = [(slot, ck.tensor(n, dt, sh)) for slot, n, dt, sh in shared]
@@ -212,6 +231,8 @@ def load_moe_layer(path_or_ckpt, desc: F.MoEDesc, family: str, layer: int,
                                                  slay.stride))
         tensors["shared_expert"] = blob
     for key, data in router_data.items():
-        tensors[key] = torch.from_numpy(np.array(data).view(np.int16)).to(dev)
+        a = np.array(data)
+        a = a.view(np.int32) if key.endswith("_words") else a.view(np.int16)
+        tensors[key] = torch.from_numpy(a).to(dev)
     torch.cuda.synchronize(dev)
-    return MoELayer.resident(desc, experts, lay.stride, tensors, ctx)
+    return MoELayer.resident(desc, experts, lay.stride, tensors, ctx, router_bits=router_bits)

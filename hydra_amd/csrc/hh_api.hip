@@ -192,7 +192,11 @@ Scratch plan(const hh_moe_desc &d, int T) {
   s.xs = take(mx ? (size_t)T * hh::NTX * (s.xld / 32) : 0);
   s.hq = take(mx ? (size_t)s.positions * hh::NTH * s.hld : 0);
   s.hs = take(mx ? (size_t)s.positions * hh::NTH * (s.hld / 32) : 0);
-  s.slot_out = take(T > kSmallT ? sizeof(float) * (size_t)T * s.slots * H : 0);
+  // Above 16 tokens the slot outputs are written only after routing, so an MLX router's fp64
+  // logits [T][E+1] share their region.
+  s.slot_out = take(T > kSmallT ? std::max(sizeof(float) * (size_t)T * s.slots * H,
+                                           sizeof(double) * (size_t)T * (E + 1))
+                                : 0);
   s.status = take(sizeof(uint32_t));
   s.total = c;
   return s;
@@ -278,6 +282,20 @@ hh::RouteArgs route_args(const hh_moe_desc &d, const hh_moe_weights *w, uint8_t 
   r.router_scale = w ? w->router_scale : nullptr;
   r.router_pes = w ? w->router_expert_scale : nullptr;
   r.shared_gate = (w && d.shared_intermediate > 0) ? w->shared_gate : nullptr;
+  if (w && w->router_bits) {
+    r.router_bits = w->router_bits;
+    r.rq_words = w->router_words;
+    r.rq_scales = w->router_scales;
+    r.rq_biases = w->router_biases;
+    if (d.shared_intermediate > 0) {
+      r.sg_words = w->shared_gate_words;
+      r.sg_scales = w->shared_gate_scales;
+      r.sg_biases = w->shared_gate_biases;
+      // shared_gate marks "a shared expert is present" for the selection and dispatch code;
+      // the MLX kernels read the sg_* tensors, never it.
+      r.shared_gate = (const uint16_t *)w->shared_gate_words;
+    }
+  }
   r.tokens = T;
   r.hidden = d.hidden;
   r.experts = d.experts;
@@ -288,7 +306,7 @@ hh::RouteArgs route_args(const hh_moe_desc &d, const hh_moe_weights *w, uint8_t 
   r.want_dispatch = 1;
   r.eps = d.router_eps;
   r.logits = nullptr;
-  r.lg64 = (double *)(base + s.lg64);
+  r.lg64 = (double *)(base + (T > kSmallT && w && w->router_bits ? s.slot_out : s.lg64));
   r.lg32 = (float *)(base + s.lg32);
   r.wn = (float *)(base + s.wn);
   r.topk_idx = (int32_t *)(base + s.topk_idx);
@@ -332,22 +350,46 @@ int phase_timing(hh_ctx *ctx, hh::Timing *tm, bool off = false) {
   return HH_OK;
 }
 
+// The router tensors: bf16 router_weight (+ shared_gate), or an MLX-affine router.
+int check_router(const hh_moe_desc *d, const hh_moe_weights *w, const uint16_t *x,
+                 const uint16_t *x_router) {
+  if (w->router_bits == 0) {
+    if (!w->router_weight) return fail(HH_EINVAL, "router_weight is required");
+    if ((uintptr_t)w->router_weight & 15) return fail(HH_EALIGN, "router_weight must be 16-byte aligned");
+    if (d->shared_intermediate > 0 && !w->shared_gate)
+      return fail(HH_EINVAL, "a shared expert needs shared_gate");
+    return HH_OK;
+  }
+  if (w->router_bits != 4 && w->router_bits != 8) return fail(HH_EINVAL, "router_bits must be 0, 4 or 8");
+  if (!w->router_words || !w->router_scales || !w->router_biases)
+    return fail(HH_EINVAL, "an MLX router needs router_words, router_scales and router_biases");
+  if (d->router == HH_ROUTER_GEMMA) return fail(HH_EINVAL, "the GEMMA router takes a bf16 projection");
+  if (((uintptr_t)w->router_words | (uintptr_t)w->shared_gate_words) & 15)
+    return fail(HH_EALIGN, "router_words and shared_gate_words must be 16-byte aligned");
+  if (d->shared_intermediate > 0) {
+    if (!w->shared_gate_words || !w->shared_gate_scales || !w->shared_gate_biases)
+      return fail(HH_EINVAL, "a shared expert with an MLX router needs shared_gate_words/scales/biases");
+    if (x_router && x_router != x)
+      return fail(HH_EINVAL, "an MLX router with a shared expert routes on x (x_router NULL or x)");
+  }
+  return HH_OK;
+}
+
 // Argument checks shared by the layer entry points (HH_OK or the error code).
 int check_forward(const hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
                   const uint16_t *x, const uint16_t *x_router, int32_t T, const float *y) {
   if (!ctx) return fail(HH_EINVAL, "ctx is NULL");
   int rc = check_desc(d);
   if (rc) return rc;
-  if (!w || !w->experts || !w->router_weight || !x || !y)
-    return fail(HH_EINVAL, "experts, router_weight, x and y are required");
+  if (!w || !w->experts || !x || !y) return fail(HH_EINVAL, "experts, x and y are required");
+  if (int rc = check_router(d, w, x, x_router)) return rc;
   if (d->router == HH_ROUTER_GEMMA && (!w->router_scale || !w->router_expert_scale))
     return fail(HH_EINVAL, "the GEMMA router needs router_scale and router_expert_scale");
-  if (d->shared_intermediate > 0 && (!w->shared_expert || !w->shared_gate))
-    return fail(HH_EINVAL, "a shared expert needs shared_expert and shared_gate");
+  if (d->shared_intermediate > 0 && !w->shared_expert)
+    return fail(HH_EINVAL, "a shared expert needs shared_expert");
   if (T < 0 || T > kMaxTokens) return fail(HH_EINVAL, "token count outside 0..65536");
-  if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)w->experts | (uintptr_t)w->router_weight |
-       (uintptr_t)(x_router ? x_router : x)) & 15)
-    return fail(HH_EALIGN, "x, x_router, y, experts and router_weight must be 16-byte aligned");
+  if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)w->experts | (uintptr_t)(x_router ? x_router : x)) & 15)
+    return fail(HH_EALIGN, "x, x_router, y and experts must be 16-byte aligned");
   if (w->expert_stride % 256) return fail(HH_EALIGN, "expert_stride must be a multiple of 256");
   if (w->shared_expert && ((uintptr_t)w->shared_expert & 255))
     return fail(HH_EALIGN, "shared_expert must be 256-byte aligned");
@@ -404,7 +446,7 @@ int forward_layer(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w, co
   g.hs = base + s.hs;
   g.hld = s.hld;
 
-  if (!noalloc && !resid && use_fused(ctx, *d, T)) {
+  if (!noalloc && !resid && w->router_bits == 0 && use_fused(ctx, *d, T)) {
     // Decode in one launch (decode_mx): logits and h terms in the arena, flags in the
     // context's flag buffer.
     if ((rc = ensure_flags(ctx))) return rc;
@@ -843,12 +885,19 @@ int hh_router_topk(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
   if (!ctx) return fail(HH_EINVAL, "ctx is NULL");
   int rc = check_desc(d);
   if (rc) return rc;
-  if (!w || !w->router_weight || !x_router || !topk_idx || !topk_w)
-    return fail(HH_EINVAL, "router_weight, x_router, topk_idx and topk_w are required");
+  if (!w || !x_router || !topk_idx || !topk_w)
+    return fail(HH_EINVAL, "the weights, x_router, topk_idx and topk_w are required");
   if (d->router == HH_ROUTER_GEMMA && (!w->router_scale || !w->router_expert_scale))
     return fail(HH_EINVAL, "the GEMMA router needs router_scale and router_expert_scale");
-  if (((uintptr_t)x_router | (uintptr_t)w->router_weight) & 15)
-    return fail(HH_EALIGN, "x_router and router_weight must be 16-byte aligned");
+  if ((uintptr_t)x_router & 15) return fail(HH_EALIGN, "x_router must be 16-byte aligned");
+  if (w->router_bits == 0 && !w->router_weight) return fail(HH_EINVAL, "router_weight is required");
+  if (w->router_bits == 0 && ((uintptr_t)w->router_weight & 15))
+    return fail(HH_EALIGN, "router_weight must be 16-byte aligned");
+  if (w->router_bits) {
+    hh_moe_desc dd = *d;
+    if (!shared_w) dd.shared_intermediate = 0;   // no shared gate wanted
+    if (int rc2 = check_router(&dd, w, x_router, x_router)) return rc2;
+  }
   if (T < 0 || T > kMaxTokens) return fail(HH_EINVAL, "token count outside 0..65536");
   if (T == 0) return HH_OK;
   HH_HIP(hipSetDevice(ctx->device));
@@ -862,7 +911,9 @@ int hh_router_topk(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
   r.topk_idx = topk_idx;
   r.topk_w = topk_w;
   r.shared_w = shared_w;
-  if (d->shared_intermediate > 0 && !w->shared_gate) r.shared_gate = nullptr;
+  if (d->shared_intermediate > 0 &&
+      (w->router_bits ? (!shared_w || !w->shared_gate_words) : !w->shared_gate))
+    r.shared_gate = nullptr;
   HH_HIP(hh::launch_route(r, ctx->stream));
   ctx->dispatches += 2;
   return HH_OK;

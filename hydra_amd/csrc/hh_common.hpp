@@ -172,10 +172,17 @@ struct RouteArgs {
   const uint16_t *router_scale; // bf16 [H] (GEMMA)
   const uint16_t *router_pes;   // bf16 [E] (GEMMA)
   const uint16_t *shared_gate;  // bf16 [H] or null
+  // MLX-affine router (router_bits 4 or 8; 0 = the bf16 router above): words [E][H·bits/32],
+  // scales / biases bf16 [E][H/64]; the shared gate row in the same format (sg_*), or null.
+  int32_t router_bits;
+  const uint32_t *rq_words;
+  const uint16_t *rq_scales, *rq_biases;
+  const uint32_t *sg_words;
+  const uint16_t *sg_scales, *sg_biases;
   int32_t tokens, hidden, experts, top_k, slots, router, tile_tokens, want_dispatch;
   float eps;
   double *logits;               // fp64 [T][K] exact logits of the selected experts, or null
-  double *lg64;                 // fp64 [T][E+1] exact logits (batches of ≤ 16 tokens; column E: shared gate)
+  double *lg64;                 // fp64 [T][E+1] exact logits (batches of ≤ 16 tokens, or any batch with an MLX router; column E: shared gate)
   uint8_t *xq, *xs;             // MXFP4 layers: x as fp8 terms (GemmArgs::xq), or null
   int32_t xld;
   float *lg32;                  // fp32 [T][E] screening logits (batches above 16 tokens)

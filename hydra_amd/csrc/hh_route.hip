@@ -471,10 +471,119 @@ __global__ __launch_bounds__(256) void select_small_kernel(RouteArgs a) {
     finish_token(a, t, tk, a.shared_gate ? lg[a.experts] : 0.0);
   }
 }
+
+// ---- MLX-affine router: exact logits of every (token, row) pair on the fp64 MFMA -------------
+// One wave per (16-token tile, 16-row tile), rows 0..E-1 the router, row E the shared gate.
+// Per 64-column chunk c (one MLX group) lane (g, l16) takes row r0 + l16 and token t0 + l16 at
+// columns 64c + 16g + s, s = 0..15: step s of the chunk is one v_mfma_f64_16x16x4_f64 whose
+// k index g stands for column 64c + 16g + s in both operands, so the 16 steps cover the
+// chunk's 64 columns once. A = q·scale + bias and B = x are exact in fp64 (an 8-bit code times
+// a bf16 scale has 16 significant bits, the bias aligns within fp64's 53), so each product is
+// exact and the dot is an fp64 sum like the reference's (MLXAffine.matvec,
+// Gemma4ReferenceOps.swift:224-239). D: lane (g, l16) holds rows r0 + g + 4i (i = 0..3) of
+// token t0 + l16 (the f64 MFMA's output layout, unlike the f32 16x16 ones).
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+template <int BITS>
+__device__ __forceinline__ uint32_t mlx_code(const u32x4 &q, int s) {
+  if constexpr (BITS == 8) return (q[s >> 2] >> (8 * (s & 3))) & 0xFFu;
+  else return (q[s >> 3] >> (4 * (s & 7))) & 0xFu;
+}
+
+template <int BITS>
+__global__ __launch_bounds__(64) void mlx_router_logits_kernel(RouteArgs a) {
+  const int lane = threadIdx.x, g = lane >> 4, l16 = lane & 15;
+  const int E = a.experts, H = a.hidden, T = a.tokens;
+  const int rows = E + (a.shared_gate ? 1 : 0);
+  const int rtiles = (rows + 15) / 16;
+  const int tt = blockIdx.x / rtiles, rt = blockIdx.x - tt * rtiles;
+  const int t0 = tt * 16, r0 = rt * 16;
+  const int row = min(r0 + l16, rows - 1), tok = min(t0 + l16, T - 1);
+  const bool sg = row == E;
+  const int wpr = H * BITS / 32, gpr = H / 64;   // words and groups per row
+  const uint32_t *qrow = sg ? a.sg_words : a.rq_words + (size_t)row * wpr;
+  const uint16_t *srow = sg ? a.sg_scales : a.rq_scales + (size_t)row * gpr;
+  const uint16_t *brow = sg ? a.sg_biases : a.rq_biases + (size_t)row * gpr;
+  const uint16_t *xrow = (sg ? a.x : a.xr) + (size_t)tok * H;
+  f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+  for (int c = 0; c < gpr; ++c) {
+    const int col = 64 * c + 16 * g;
+    u32x4 q;
+    if constexpr (BITS == 8) q = *(const u32x4 *)(qrow + col / 4);
+    else {
+      const u32x2 h = *(const u32x2 *)(qrow + col / 8);
+      q = u32x4{h[0], h[1], 0u, 0u};
+    }
+    const u32x4 x0 = *(const u32x4 *)(xrow + col), x1 = *(const u32x4 *)(xrow + col + 8);
+    const double sc = (double)bf16_bits_to_f32(srow[c]), bi = (double)bf16_bits_to_f32(brow[c]);
+#pragma unroll
+    for (int st = 0; st < 16; ++st) {
+      const double w = fma((double)mlx_code<BITS>(q, st), sc, bi);
+      const u32x4 &xv = st < 8 ? x0 : x1;
+      const uint32_t xb = (xv[(st & 7) >> 1] >> (16 * (st & 1))) & 0xFFFFu;
+      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(w, (double)bf16_bits_to_f32(xb), acc, 0, 0, 0);
+    }
+  }
+  const int t = t0 + l16;
+  if (t < T) {
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const int r = r0 + g + 4 * ii;
+      if (r < rows) {
+        double v = acc[ii];
+        if (r < E && a.router_b) v += (double)bf16_bits_to_f32(a.router_b[r]);
+        a.lg64[(size_t)t * (E + 1) + r] = v;
+      }
+    }
+  }
+}
+
+// Top-k and weights of every token from lg64, one wave per token (batches with an MLX router).
+__global__ __launch_bounds__(256) void select_lg64_kernel(RouteArgs a) {
+  const int wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wave;
+  __shared__ int s_ri[4][kMaxTopK];
+  __shared__ double s_rv[4][kMaxTopK];
+  __shared__ int s_ci[4][kFastCand];
+  __shared__ double s_cv[4][kFastCand];
+  if (t >= a.tokens) return;
+  const double *lg = a.lg64 + (size_t)t * (a.experts + 1);
+  const TopK tk = topk_fast(lg, a.experts, a.top_k, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave]);
+  finish_token(a, t, tk, a.shared_gate ? lg[a.experts] : 0.0);
+}
+
+// The MLX-router sequence: exact logits, x terms (MXFP4 layers), selection (unless the layer's
+// decode gate-up kernel selects), dispatch (layers above 16 tokens).
+hipError_t launch_route_mlx(const RouteArgs &a, hipStream_t s, Timing tm) {
+  const int rows = a.experts + (a.shared_gate ? 1 : 0);
+  const int blocks = ((a.tokens + 15) / 16) * ((rows + 15) / 16);
+  const bool small = a.tokens <= RT_TOK;
+  const bool sel = !small || a.want_dispatch == 0;
+  const bool disp = !small && a.want_dispatch != 0;
+  const bool quant = a.xq != nullptr;
+  hipExtLaunchKernelGGL(a.router_bits == 8 ? mlx_router_logits_kernel<8> : mlx_router_logits_kernel<4>,
+                        dim3(blocks), dim3(64), 0, s, tm.start,
+                        (sel || quant) ? nullptr : tm.stop, 0, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (quant) {
+    const int qw = a.tokens * ((a.hidden / 32 + 15) / 16);
+    hipExtLaunchKernelGGL(quant_x_kernel, dim3((qw + 3) / 4), dim3(256), 0, s, nullptr,
+                          sel ? nullptr : tm.stop, 0, a);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (!sel) return hipSuccess;
+  hipExtLaunchKernelGGL(select_lg64_kernel, dim3((a.tokens + 3) / 4), dim3(256), 0, s, nullptr,
+                        disp ? nullptr : tm.stop, 0, a);
+  if ((e = hipGetLastError()) != hipSuccess || !disp) return e;
+  hipExtLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, nullptr, tm.stop, 0, a);
+  return hipGetLastError();
+}
 }  // namespace hh
 
 namespace hh {
 hipError_t launch_route(const RouteArgs &a, hipStream_t s, Timing tm) {
+  if (a.router_bits) return launch_route_mlx(a, s, tm);
   if (a.tokens <= RT_TOK) {
     // The layer (want_dispatch) selects inside its gate-up kernel; the operator entry selects
     // here.

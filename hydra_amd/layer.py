@@ -20,6 +20,12 @@ from . import formats as F
 from ._lib import BlockNormsC, MoEWeightsC, check, desc_c, lib
 
 
+# Device tensors of a layer besides its expert blobs (absent ones are None).
+TENSORS = ["shared_expert", "router_weight", "router_bias", "router_scale", "router_expert_scale",
+           "shared_gate", "router_words", "router_scales", "router_biases", "shared_gate_words",
+           "shared_gate_scales", "shared_gate_biases"]
+
+
 def _ptr(t):
     return None if t is None else C.c_void_p(t.data_ptr())
 
@@ -128,24 +134,22 @@ class MoELayer:
         torch.cuda.synchronize(dev)
         self.experts = to_device(layer["experts"], dev)
         self.expert_stride = int(layer["experts"].shape[1])
-        self.tensors = {k: to_device(layer.get(k), dev) for k in
-                        ["shared_expert", "router_weight", "router_bias", "router_scale",
-                         "router_expert_scale", "shared_gate"]}
+        self.tensors = {k: to_device(layer.get(k), dev) for k in TENSORS}
+        self.router_bits = int(layer.get("router_bits", 0))
         torch.cuda.synchronize(dev)
         self._desc_c = desc_c(self.desc)
         self._weights_c = self.weights_c()
 
     @classmethod
     def resident(cls, desc: F.MoEDesc, experts: torch.Tensor, expert_stride: int,
-                 tensors: dict, ctx: Context) -> "MoELayer":
+                 tensors: dict, ctx: Context, router_bits: int = 0) -> "MoELayer":
         """A layer over weights already in HBM: `experts` uint8 [E][expert_stride] in the blob
         layout, `tensors` the device router / shared-expert tensors by name (absent = None)."""
         self = cls.__new__(cls)
         self.desc, self.ctx = desc, ctx
         self.experts, self.expert_stride = experts, int(expert_stride)
-        self.tensors = {k: tensors.get(k) for k in
-                        ["shared_expert", "router_weight", "router_bias", "router_scale",
-                         "router_expert_scale", "shared_gate"]}
+        self.tensors = {k: tensors.get(k) for k in TENSORS}
+        self.router_bits = int(router_bits)
         self._desc_c = desc_c(desc)
         self._weights_c = self.weights_c()
         return self
@@ -156,7 +160,10 @@ class MoELayer:
         return MoEWeightsC(ex.data_ptr(), self.expert_stride, _ptr(t["shared_expert"]),
                            _ptr(t["router_weight"]), _ptr(t["router_bias"]),
                            _ptr(t["router_scale"]), _ptr(t["router_expert_scale"]),
-                           _ptr(t["shared_gate"]))
+                           _ptr(t["shared_gate"]), self.router_bits, _ptr(t["router_words"]),
+                           _ptr(t["router_scales"]), _ptr(t["router_biases"]),
+                           _ptr(t["shared_gate_words"]), _ptr(t["shared_gate_scales"]),
+                           _ptr(t["shared_gate_biases"]))
 
     def forward_into(self, x: torch.Tensor, y: torch.Tensor, idx: torch.Tensor | None = None,
                      w: torch.Tensor | None = None, x_router: torch.Tensor | None = None,

@@ -137,8 +137,26 @@ def zipf_router_bias(seed: int, experts: int, s: float = 1.1) -> np.ndarray:
     return f32_to_bf16((-s * np.log1p(rank)).astype(np.float32))
 
 
-def make_layer(desc: F.MoEDesc, seed: int = 0, zipf: float | None = None) -> dict:
-    """Synthetic weights of one layer as host arrays, in the reference blob layout."""
+def mlx_router_rows(seed: int, name: str, rows: int, hidden: int, bits: int):
+    """An MLX-affine router matrix [rows][hidden] (group 64): uniform codes, scales chosen so
+    the dequantised rows have std ≈ 1/√H (logits ≈ N(0, 1) for N(0, 1) inputs), group biases
+    −centre·scale. Returns (words uint32 [rows][H·bits/32], scales, biases bf16 [rows][H/64])."""
+    centre = 7.5 if bits == 4 else 127.5
+    code_std = (2 ** bits - 1) / np.sqrt(12.0)
+    nw = rows * hidden * bits // 32
+    words = random_bytes(seed, f"{name}_words", nw * 4).view(np.uint32).reshape(rows, -1)
+    ng = rows * hidden // 64
+    s0 = 1.0 / (np.sqrt(hidden) * code_std)
+    scales = f32_to_bf16(np.abs(s0 + 0.2 * s0 * normal(seed, f"{name}_scales", ng)).astype(np.float32))
+    biases = f32_to_bf16(-centre * bf16_to_f32(scales))
+    return words, scales.reshape(rows, -1), biases.reshape(rows, -1)
+
+
+def make_layer(desc: F.MoEDesc, seed: int = 0, zipf: float | None = None,
+               router_bits: int = 0) -> dict:
+    """Synthetic weights of one layer as host arrays, in the reference blob layout. With
+    `router_bits` 4 or 8 the router (and shared gate) are MLX-affine matrices, as Qwen's
+    published builds store mlp.gate and mlp.shared_expert_gate (Qwen35MoeConfig.swift:340-342)."""
     H, E = desc.hidden, desc.experts
     lay, tens = _expert_tensors(desc, seed, "experts", E, desc.intermediate)
     layer = {"desc": desc, "layout": lay, "experts": pack_blobs(lay, tens)}
@@ -146,6 +164,18 @@ def make_layer(desc: F.MoEDesc, seed: int = 0, zipf: float | None = None) -> dic
         slay, stens = _expert_tensors(desc, seed, "shared", 1, desc.shared_intermediate)
         layer["shared_expert"] = pack_blobs(slay, stens)[0]
         layer["shared_gate"] = bf16_normal(seed, "shared_gate", H, 0.0, 1.0 / np.sqrt(H))
+    if router_bits:
+        assert desc.router != F.ROUTER_GEMMA, "the GEMMA router takes a bf16 projection"
+        layer["router_bits"] = router_bits
+        (layer["router_words"], layer["router_scales"],
+         layer["router_biases"]) = mlx_router_rows(seed, "router", E, H, router_bits)
+        if desc.shared_intermediate:
+            del layer["shared_gate"]
+            (layer["shared_gate_words"], layer["shared_gate_scales"],
+             layer["shared_gate_biases"]) = mlx_router_rows(seed, "shared_gate", 1, H, router_bits)
+        if desc.expert_bias:
+            layer["router_bias"] = bf16_normal(seed, "router_bias", E, 0.0, 0.02)
+        return layer
     if desc.router == F.ROUTER_GEMMA:
         # Unit router scales: the normalised input has unit rms, so N(0, 1) projection rows
         # give ≈ N(0, 1) logits after the H^-½ factor.

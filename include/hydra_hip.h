@@ -86,11 +86,28 @@ typedef struct hh_moe_weights {
     const void *experts;             /* E expert blobs, reference blob layout for desc->quant  */
     size_t      expert_stride;       /* bytes between blobs; 0 = the reference stride (16 KiB aligned) */
     const void *shared_expert;       /* one blob of shared_intermediate, same format, or NULL   */
-    const uint16_t *router_weight;   /* bf16 [E][H]                                             */
+    const uint16_t *router_weight;   /* bf16 [E][H] (NULL with an MLX router, below)            */
     const uint16_t *router_bias;     /* bf16 [E] or NULL (GPT-OSS router bias)                  */
     const uint16_t *router_scale;    /* bf16 [H], GEMMA router only                             */
     const uint16_t *router_expert_scale; /* bf16 [E], GEMMA router only                         */
     const uint16_t *shared_gate;     /* bf16 [H]: the shared expert's sigmoid gate row          */
+    /* MLX-affine router (Qwen's published builds quantise mlp.gate and
+     * mlp.shared_expert_gate to 8 bits: Qwen35MoeConfig.swift:340-342; applied by
+     * QwenMixtureBlock.encodeRouterAndShared, QwenMixtureBlock.swift:153-177). router_bits 0:
+     * the bf16 router_weight / shared_gate above are used. 4 or 8: router_words uint32
+     * [E][H·bits/32], router_scales / router_biases bf16 [E][H/64] (group 64) replace
+     * router_weight, and, for a shared expert, shared_gate_words/scales/biases ([1][H] in the
+     * same format) replace shared_gate. Logits are exact: every weight q·s + b and every
+     * product with the bf16 input is formed exactly in fp64 (Gemma4ReferenceOps.swift:210-239),
+     * so top-k indices equal the fp64 reference's. Not with the GEMMA router; the router input
+     * must be x (x_router NULL or equal to x) when a shared expert is present.               */
+    int32_t         router_bits;
+    const uint32_t *router_words;
+    const uint16_t *router_scales;
+    const uint16_t *router_biases;
+    const uint32_t *shared_gate_words;
+    const uint16_t *shared_gate_scales;
+    const uint16_t *shared_gate_biases;
 } hh_moe_weights;
 
 /* Byte layout of one expert blob (offsets from the blob start). Slots in consumption order:

@@ -451,14 +451,32 @@ static double *widen(const uint16_t *b, size_t n) {
     return o;
 }
 
+/* The router (rows = E) or shared gate (rows = 1) as fp64 [rows][H]: bf16 values widened, or an
+ * MLX-affine matrix (group 64) dequantised row by row as QwenReferenceMixture receives it. */
+static double *widen_router(const hho_weights *w, int shared_gate, size_t rows, size_t H) {
+    const uint32_t *words = shared_gate ? w->shared_gate_words : w->router_words;
+    const uint16_t *sc = shared_gate ? w->shared_gate_scales : w->router_scales;
+    const uint16_t *bi = shared_gate ? w->shared_gate_biases : w->router_biases;
+    if (!w->router_bits || !words) return widen(shared_gate ? w->shared_gate : w->router_weight, rows * H);
+    const size_t wpr = H * (size_t)w->router_bits / 32, gpr = H / 64;
+    double *o = (double *)malloc(sizeof(double) * rows * H);
+    double *sd = (double *)malloc(sizeof(double) * gpr), *bd = (double *)malloc(sizeof(double) * gpr);
+    for (size_t r = 0; r < rows; ++r) {
+        for (size_t g = 0; g < gpr; ++g) { sd[g] = bf(sc[r * gpr + g]); bd[g] = bf(bi[r * gpr + g]); }
+        hho_mlx_dequant(words + r * wpr, sd, bd, (int)H, w->router_bits, 64, o + r * H);
+    }
+    free(sd); free(bd);
+    return o;
+}
+
 int hho_moe_forward(const hho_desc *d, const hho_weights *w, const uint16_t *x,
                     const uint16_t *x_router, int tokens, double *y, int32_t *idx, double *wts,
                     double *shared_w, int nthreads) {
     size_t H = (size_t)d->hidden, E = (size_t)d->experts, T = (size_t)tokens;
     hho_weights_f64 w64 = {w->experts, w->expert_stride, w->shared_expert,
-                           widen(w->router_weight, E * H), widen(w->router_bias, E),
+                           widen_router(w, 0, E, H), widen(w->router_bias, E),
                            widen(w->router_scale, H), widen(w->router_expert_scale, E),
-                           widen(w->shared_gate, H)};
+                           widen_router(w, 1, 1, H)};
     double *xd = widen(x, T * H);
     double *xr = widen(x_router, T * H);
     int rc = hho_moe_forward_f64(d, &w64, xd, xr, tokens, y, idx, wts, shared_w, nthreads);
@@ -471,9 +489,9 @@ int hho_moe_forward(const hho_desc *d, const hho_weights *w, const uint16_t *x,
 void hho_router_logits(const hho_desc *d, const hho_weights *w, const double *x, double *logits) {
     size_t H = (size_t)d->hidden, E = (size_t)d->experts;
     hho_weights_f64 w64 = {w->experts, w->expert_stride, w->shared_expert,
-                           widen(w->router_weight, E * H), widen(w->router_bias, E),
+                           widen_router(w, 0, E, H), widen(w->router_bias, E),
                            widen(w->router_scale, H), widen(w->router_expert_scale, E),
-                           widen(w->shared_gate, H)};
+                           widen_router(w, 1, 1, H)};
     hho_router_logits_f64(d, &w64, x, logits);
     free((void *)w64.router_weight); free((void *)w64.router_bias);
     free((void *)w64.router_scale); free((void *)w64.router_expert_scale);

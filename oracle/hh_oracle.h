@@ -34,6 +34,11 @@ typedef struct hho_weights {
     const uint8_t *experts; size_t expert_stride;
     const uint8_t *shared_expert;
     const uint16_t *router_weight, *router_bias, *router_scale, *router_expert_scale, *shared_gate;
+    /* MLX-affine router (router_bits 4 or 8, group 64): replaces router_weight / shared_gate,
+     * dequantised to fp64 q·scale + bias (Gemma4ReferenceOps.swift:210-221). */
+    int32_t router_bits;
+    const uint32_t *router_words; const uint16_t *router_scales, *router_biases;
+    const uint32_t *shared_gate_words; const uint16_t *shared_gate_scales, *shared_gate_biases;
 } hho_weights;
 
 typedef struct hho_weights_f64 {

@@ -28,7 +28,11 @@ class Weights(C.Structure):
     _fields_ = [("experts", C.c_void_p), ("expert_stride", C.c_size_t),
                 ("shared_expert", C.c_void_p), ("router_weight", C.c_void_p),
                 ("router_bias", C.c_void_p), ("router_scale", C.c_void_p),
-                ("router_expert_scale", C.c_void_p), ("shared_gate", C.c_void_p)]
+                ("router_expert_scale", C.c_void_p), ("shared_gate", C.c_void_p),
+                ("router_bits", C.c_int32), ("router_words", C.c_void_p),
+                ("router_scales", C.c_void_p), ("router_biases", C.c_void_p),
+                ("shared_gate_words", C.c_void_p), ("shared_gate_scales", C.c_void_p),
+                ("shared_gate_biases", C.c_void_p)]
 
 
 def build() -> str:
@@ -179,7 +183,11 @@ def _weights(layer):
     w = Weights(arr("experts", np.uint8), C.c_size_t(layer["experts"].shape[1]),
                 arr("shared_expert", np.uint8), arr("router_weight", np.uint16),
                 arr("router_bias", np.uint16), arr("router_scale", np.uint16),
-                arr("router_expert_scale", np.uint16), arr("shared_gate", np.uint16))
+                arr("router_expert_scale", np.uint16), arr("shared_gate", np.uint16),
+                int(layer.get("router_bits", 0)), arr("router_words", np.uint32),
+                arr("router_scales", np.uint16), arr("router_biases", np.uint16),
+                arr("shared_gate_words", np.uint32), arr("shared_gate_scales", np.uint16),
+                arr("shared_gate_biases", np.uint16))
     return w, keep
 
 

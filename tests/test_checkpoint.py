@@ -26,6 +26,8 @@ CASES = {
                              activation=F.ACT_SILU, router=F.ROUTER_SOFTMAX_TOPK_RENORM,
                              shared_intermediate=192, group_size=64),
 }
+# Qwen's published builds store the router and shared gate as 8-bit MLX (Qwen35MoeConfig.swift:340-342).
+ROUTER_BITS = {"qwen3.5-moe": 8}
 LAYER = 3
 SEED = 41
 
@@ -47,9 +49,10 @@ def write_safetensors(path, tensors):
             f.write(b.tobytes())
 
 
-def checkpoint_tensors(desc, family, layer_idx=LAYER, seed=SEED):
+def checkpoint_tensors(desc, family, layer_idx=LAYER, seed=SEED, router_bits=None):
     """The synthetic layer as checkpoint tensors, and the layer dict itself."""
-    layer = synth.make_layer(desc, seed=seed)
+    rb = ROUTER_BITS.get(family, 0) if router_bits is None else router_bits
+    layer = synth.make_layer(desc, seed=seed, router_bits=rb)
     _, routed = synth._expert_tensors(desc, seed, "experts", desc.experts, desc.intermediate)
     out = {}
     for slot, name, dt, shape in CK.expert_sources(desc, family, layer_idx):
@@ -58,7 +61,7 @@ def checkpoint_tensors(desc, family, layer_idx=LAYER, seed=SEED):
         _, shared = synth._expert_tensors(desc, seed, "shared", 1, desc.shared_intermediate)
         for slot, name, dt, shape in CK.expert_sources(desc, family, layer_idx, shared=True):
             out[name] = (dt, shape, shared[slot])
-    for key, (name, dt, shape, req) in CK.router_sources(desc, family, layer_idx).items():
+    for key, (name, dt, shape, req) in CK.router_sources(desc, family, layer_idx, rb).items():
         if key in layer:
             out[name] = (dt, shape, layer[key])
     return out, layer
@@ -103,10 +106,10 @@ def test_scatter_plan_rebuilds_the_packed_blobs(tmp_path, family, shards):
             blob[slay.offsets[slot]:slay.offsets[slot] + slay.sizes[slot]] = \
                 np.asarray(ck.tensor(name, dt, shape)).reshape(-1)
         assert np.array_equal(blob, layer["shared_expert"])
-    for key, (name, dt, shape, req) in CK.router_sources(desc, family, LAYER).items():
+    for key, (name, dt, shape, req) in CK.router_sources(desc, family, LAYER, ROUTER_BITS.get(family, 0)).items():
         if key in layer:
-            got = np.asarray(ck.tensor(name, dt, shape)).view(np.uint16).reshape(-1)
-            assert np.array_equal(got, np.asarray(layer[key]).reshape(-1))
+            got = np.asarray(ck.tensor(name, dt, shape)).reshape(-1)
+            assert np.array_equal(got, np.asarray(layer[key]).view(np.uint8).reshape(-1))
 
 
 def test_shape_and_dtype_mismatches_are_errors(tmp_path):
@@ -133,18 +136,37 @@ def test_shape_and_dtype_mismatches_are_errors(tmp_path):
                           "gemma4", LAYER)
 
 
-def test_quantised_qwen_router_is_refused(tmp_path):
+def test_router_format_is_read_from_the_checkpoint(tmp_path):
+    """Qwen's router loads from MLX words (bit width from the word count) or from BF16; an
+    MLX-quantised router of another family, or a word count of neither width, is an error."""
     desc = CASES["qwen3.5-moe"]
-    tens, _ = checkpoint_tensors(desc, "qwen3.5-moe")
     stem = f"language_model.model.layers.{LAYER}.mlp.gate"
+    ck8, _ = checkpoint_tensors(desc, "qwen3.5-moe", router_bits=8)
+    write_safetensors(tmp_path / "q8.safetensors", ck8)
+    assert CK._quantised_router_bits(CK.Checkpoint(str(tmp_path / "q8.safetensors")), desc,
+                                     "qwen3.5-moe", LAYER) == 8
+    ck4, _ = checkpoint_tensors(desc, "qwen3.5-moe", router_bits=4)
+    write_safetensors(tmp_path / "q4.safetensors", ck4)
+    assert CK._quantised_router_bits(CK.Checkpoint(str(tmp_path / "q4.safetensors")), desc,
+                                     "qwen3.5-moe", LAYER) == 4
+    bf, _ = checkpoint_tensors(desc, "qwen3.5-moe", router_bits=0)
+    write_safetensors(tmp_path / "bf.safetensors", bf)
+    assert CK._quantised_router_bits(CK.Checkpoint(str(tmp_path / "bf.safetensors")), desc,
+                                     "qwen3.5-moe", LAYER) == 0
     E, H = desc.experts, desc.hidden
-    del tens[f"{stem}.weight"]
-    tens[f"{stem}.weight"] = ("U32", (E, H // 4), np.zeros(E * H, np.uint8))
-    tens[f"{stem}.scales"] = ("BF16", (E, H // 64), np.zeros(E * H // 32, np.uint8))
-    tens[f"{stem}.biases"] = ("BF16", (E, H // 64), np.zeros(E * H // 32, np.uint8))
-    write_safetensors(tmp_path / "q.safetensors", tens)
-    with pytest.raises(CK.CheckpointError, match="MLX-quantised"):
-        CK.load_moe_layer(str(tmp_path / "q.safetensors"), desc, "qwen3.5-moe", LAYER)
+    bad = dict(ck8)
+    bad[f"{stem}.weight"] = ("U32", (E, H // 16), np.zeros(E * H // 4, np.uint8))   # 2-bit
+    write_safetensors(tmp_path / "bad.safetensors", bad)
+    with pytest.raises(CK.CheckpointError, match="neither 4- nor 8-bit"):
+        CK.load_moe_layer(str(tmp_path / "bad.safetensors"), desc, "qwen3.5-moe", LAYER)
+    g = CASES["gpt-oss"]
+    tens, _ = checkpoint_tensors(g, "gpt-oss")
+    rs = f"model.layers.{LAYER}.mlp.router"
+    tens[f"{rs}.weight"] = ("U32", (g.experts, g.hidden // 4), np.zeros(g.experts * g.hidden, np.uint8))
+    tens[f"{rs}.scales"] = ("BF16", (g.experts, g.hidden // 64), np.zeros(g.experts * g.hidden // 32, np.uint8))
+    write_safetensors(tmp_path / "g.safetensors", tens)
+    with pytest.raises(CK.CheckpointError, match="only Qwen"):
+        CK.load_moe_layer(str(tmp_path / "g.safetensors"), g, "gpt-oss", LAYER)
 
 
 def test_truncated_byte_range_is_an_error(tmp_path):
