@@ -19,6 +19,7 @@ EXPORTS = [
     "hh_permute", "hh_ctx_profile", "hh_ctx_profile_read", "hh_ctx_decode_fused", "hh_scatter_expert_tensor",
     "hh_ctx_capture_begin", "hh_ctx_capture_end", "hh_graph_launch", "hh_graph_destroy",
     "hh_attention_decode", "hh_moe_forward_noalloc", "hh_moe_block_forward",
+    "hh_expert_gemv", "hh_expert_gemm", "hh_combine",
 ]
 
 CODES = {0: "HH_OK", -1: "HH_EINVAL", -2: "HH_EALIGN", -3: "HH_ETOPK", -4: "HH_EHIP",
@@ -56,6 +57,12 @@ class BlockNormsC(C.Structure):
                 ("layer_scalar", C.c_void_p), ("eps", C.c_float)]
 
 
+class MatrixC(C.Structure):
+    _fields_ = [("quant", C.c_int32), ("rows", C.c_int32), ("cols", C.c_int32),
+                ("group_size", C.c_int32), ("weights", C.c_void_p), ("scales", C.c_void_p),
+                ("biases", C.c_void_p), ("bias", C.c_void_p)]
+
+
 class BlobLayoutC(C.Structure):
     _fields_ = [("slot_count", C.c_int32), ("offset", C.c_size_t * 9), ("bytes", C.c_size_t * 9),
                 ("payload_bytes", C.c_size_t), ("stride_bytes", C.c_size_t)]
@@ -88,6 +95,9 @@ def lib() -> C.CDLL:
     L.hh_moe_forward_noalloc.argtypes = L.hh_moe_forward.argtypes
     L.hh_moe_block_forward.argtypes = [vp, C.POINTER(MoEDescC), C.POINTER(MoEWeightsC),
                                        C.POINTER(BlockNormsC), vp, vp, i32, vp, vp]
+    L.hh_expert_gemv.argtypes = [vp, C.POINTER(MatrixC), vp, vp]
+    L.hh_expert_gemm.argtypes = [vp, C.POINTER(MatrixC), vp, i32, vp]
+    L.hh_combine.argtypes = [vp, vp, vp, i32, i32, i32, vp]
     L.hh_mxfp4_dequant.argtypes = [vp, vp, vp, i64, vp]
     L.hh_mlx_dequant.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, vp]
     L.hh_router_topk.argtypes = [vp, C.POINTER(MoEDescC), C.POINTER(MoEWeightsC), vp, i32, vp,

@@ -33,6 +33,12 @@ hipError_t launch_block_gemma_finish(float *hidden, const float *mix, const floa
                                      const uint16_t *scalar, int H, float eps, int T,
                                      hipStream_t s);
 hipError_t launch_attention_decode(const AttnArgs &a, hipStream_t s);
+hipError_t launch_down_small(int quant, GemmArgs a, const int32_t *topk_idx, int T, hipStream_t s,
+                             Timing tm_down);
+hipError_t launch_proj_prepare(const GemmArgs &a, const float *x, int T, int cols, int32_t *topk,
+                               int32_t *order, int tile_tokens, hipStream_t s);
+hipError_t launch_combine_weighted(const float *slots, const float *w, int T, int count, int size,
+                                   float *y, hipStream_t s);
 hipError_t launch_mxfp4_dequant(const uint8_t *blocks, const uint8_t *scales, int64_t n,
                                 float *out, hipStream_t s);
 hipError_t launch_mlx_dequant(const uint32_t *words, const uint16_t *scales,
@@ -950,6 +956,105 @@ int hh_permute(hh_ctx *ctx, const int32_t *topk_idx, int32_t T, int32_t K, int32
   ctx->dispatches += 1;
   HH_HIP(hipMemcpyAsync(seg_offsets, r.seg, sizeof(int32_t) * (E + 1), hipMemcpyDeviceToDevice,
                         ctx->stream));
+  return HH_OK;
+}
+
+int hh_expert_gemm(hh_ctx *ctx, const hh_matrix *m, const float *x, int32_t T, float *y) {
+  if (!ctx || !m || !x || !y || !m->weights) return fail(HH_EINVAL, "NULL argument");
+  const int R = m->rows, Kc = m->cols, q = m->quant;
+  if (q < HH_QUANT_MXFP4 || q > HH_QUANT_BF16) return fail(HH_EINVAL, "unknown quant");
+  if (R <= 0 || Kc <= 0 || R % 64 || Kc % 64) return fail(HH_ESHAPE, "rows and cols must be positive multiples of 64");
+  if (T < 0 || T > kMaxTokens) return fail(HH_EINVAL, "token count outside 0..65536");
+  const bool mlx = q == HH_QUANT_MLX4 || q == HH_QUANT_MLX8;
+  if (q != HH_QUANT_BF16 && !m->scales) return fail(HH_EINVAL, "MXFP4 and MLX matrices need scales");
+  if (mlx && (!m->biases || m->group_size != 64)) return fail(HH_ESHAPE, "MLX matrices need biases and group_size 64");
+  if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)m->weights) & 15)
+    return fail(HH_EALIGN, "x, y and weights must be 16-byte aligned");
+  if (q == HH_QUANT_MXFP4 && (size_t)R * Kc / 2 > 0x7FFFFFF0u) return fail(HH_ESHAPE, "MXFP4 matrix above 2 GiB");
+  if (T == 0) return HH_OK;
+  HH_HIP(hipSetDevice(ctx->device));
+  // Scratch: the activation operand of T rows, routing (topk, weights, order) and the work list.
+  const int tile = 32;
+  const size_t ldh = align_up((size_t)Kc, 64), hld = align_up(ldh, 512);
+  const bool mx = q == HH_QUANT_MXFP4;
+  const int items = (T + tile - 1) / tile;
+  size_t c = 0;
+  auto take = [&](size_t bytes) { size_t o = c; c = align_up(c + bytes, 256); return o; };
+  const size_t o_hi = take(mx ? 0 : 2 * (size_t)T * ldh), o_lo = take(mx ? 0 : 2 * (size_t)T * ldh);
+  const size_t o_hq = take(mx ? (size_t)T * hh::NTH * hld : 0), o_hs = take(mx ? (size_t)T * hh::NTH * (hld / 32) : 0);
+  const size_t o_w = take(4 * (size_t)T), o_k = take(4 * (size_t)T), o_ord = take(4 * (size_t)T);
+  const size_t o_work = take(sizeof(int4) * (size_t)items), o_nw = take(4);
+  int rc = ensure_arena(ctx, c);
+  if (rc) return rc;
+  uint8_t *base = ctx->arena;
+  // The matrix as the down tensors of a one-expert blob: offsets from the lowest pointer.
+  const uint8_t *p[3] = {(const uint8_t *)m->weights, (const uint8_t *)m->scales,
+                         (const uint8_t *)(mx ? m->bias : m->biases)};
+  const uint8_t *lo = p[0];
+  for (const uint8_t *v : p)
+    if (v && v < lo) lo = v;
+  hh::GemmArgs g{};
+  hh::ExpertGroup &e = g.grp[0];
+  e.blobs = lo;
+  e.stride = 0;
+  e.inter = Kc;
+  auto off = [&](const uint8_t *v) { return (uint64_t)(v ? v - lo : 0); };
+  if (mx) {
+    e.off[3] = off(p[0]); e.off[4] = off(p[1]); e.off[5] = off(p[2]);
+    e.down_bytes = (uint32_t)((size_t)R * Kc / 2);
+  } else if (q == HH_QUANT_BF16) {
+    e.off[1] = off(p[0]);
+  } else {
+    e.off[6] = off(p[0]); e.off[7] = off(p[1]); e.off[8] = off(p[2]);
+  }
+  g.grp[1] = g.grp[0];
+  g.hidden = R;
+  g.experts = 1;
+  g.top_k = 1;
+  g.slots = 1;
+  g.quant = q;
+  g.act = HH_ACT_SILU;
+  g.expert_bias = (mx && m->bias) ? 1 : 0;
+  g.group = m->group_size;
+  g.ldh = (int)ldh;
+  g.hld = (int)hld;
+  g.xld = (int)hld;
+  g.h_hi = (uint16_t *)(base + o_hi);
+  g.h_lo = (uint16_t *)(base + o_lo);
+  g.hq = base + o_hq;
+  g.hs = base + o_hs;
+  g.slot_w = (const float *)(base + o_w);
+  g.order = (const int32_t *)(base + o_ord);
+  g.work = (const int4 *)(base + o_work);
+  g.n_work = (const int32_t *)(base + o_nw);
+  g.y = y;
+  g.slot_out = y;   // one slot per token: the slot rows are the output rows
+  int32_t *topk = (int32_t *)(base + o_k);
+  HH_HIP(hh::launch_proj_prepare(g, x, T, Kc, topk, (int32_t *)(base + o_ord), tile, ctx->stream));
+  if (T <= kSmallT) {
+    HH_HIP(hh::launch_down_small(q, g, topk, T, ctx->stream, hh::Timing{}));
+  } else {
+    const int rows = hh::gemm_rows_per_block(q, 1);
+    g.row_tiles = (R + rows - 1) / rows;
+    g.max_work = items;
+    HH_HIP(hh::launch_gemm(1, q, 2, g, ctx->stream, hh::Timing{}));
+  }
+  ctx->dispatches += 2;
+  return HH_OK;
+}
+
+int hh_expert_gemv(hh_ctx *ctx, const hh_matrix *m, const float *x, float *y) {
+  return hh_expert_gemm(ctx, m, x, 1, y);
+}
+
+int hh_combine(hh_ctx *ctx, const float *slots, const float *weights, int32_t T, int32_t count,
+               int32_t size, float *y) {
+  if (!ctx || !slots || !y) return fail(HH_EINVAL, "NULL argument");
+  if (T < 0 || count < 1 || size < 0) return fail(HH_EINVAL, "tokens, count and size must be non-negative (count ≥ 1)");
+  if ((int64_t)T * size == 0) return HH_OK;
+  HH_HIP(hipSetDevice(ctx->device));
+  HH_HIP(hh::launch_combine_weighted(slots, weights, T, count, size, y, ctx->stream));
+  ctx->dispatches += 1;
   return HH_OK;
 }
 

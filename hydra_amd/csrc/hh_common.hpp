@@ -123,7 +123,8 @@ struct ExpertGroup {
   const uint8_t *blobs;   // blob of expert 0 of the group
   uint64_t stride;        // bytes between consecutive blobs
   int32_t inter;          // I of the group
-  int32_t pad;
+  uint32_t down_bytes;    // MXFP4: the down matrix's bytes when its tensors are not one blob (an
+                          // operator-level projection); 0: the blob's off[4] − off[3]
   uint64_t off[9];        // sub-tensor offsets inside a blob (reference blob layout)
 };
 

@@ -221,7 +221,7 @@ __device__ __forceinline__ ATile<FMT> tile_of(const uint8_t *blob, const ExpertG
   } else if constexpr (FMT == Q_MXFP4_W) {
     // The matrix extends to the next sub-tensor of the blob (its scales).
     if (PH == PH_UP) t.row = Fmt<FMT>::row(blob + grp.off[0], grp.off[1] - grp.off[0], 2 * orow + (is_up ? 1 : 0), K);
-    else t.row = Fmt<FMT>::row(blob + grp.off[3], grp.off[4] - grp.off[3], orow, K);
+    else t.row = Fmt<FMT>::row(blob + grp.off[3], grp.down_bytes ? grp.down_bytes : grp.off[4] - grp.off[3], orow, K);
   } else if constexpr (FMT == Q_BF16) {
     // Gemma gate_up: gate = rows 0..I-1, up = rows I..2I-1 (Gemma4Weights.swift:107-112).
     if (PH == PH_UP) t.row = Fmt<FMT>::row(blob + grp.off[0], orow + (is_up ? I : 0), K);
@@ -3040,6 +3040,9 @@ hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStrea
   return hipGetLastError();
 }
 
+hipError_t launch_down_small(int quant, GemmArgs a, const int32_t *topk_idx, int T, hipStream_t s,
+                             Timing tm_down);
+
 // Decode (T ≤ 16). `a.row_tiles` is set here per phase.
 hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t s, Timing tm_up,
                         Timing tm_down) {
@@ -3090,6 +3093,41 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
   hipExtLaunchKernelGGL(up, dim3(up_grid), dim3(256), lds_up, s, tm_up.start, tm_up.stop, 0, a, ra);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  return launch_down_small(quant, a, ra.topk_idx, T, s, tm_down);
+}
+
+// The decode down product alone (the second launch of launch_small): slot values of T ≤ 16
+// tokens summed in rank order into a.y. Also the operator-level projection's T ≤ 16 path.
+hipError_t launch_down_small(int quant, GemmArgs a, const int32_t *topk_idx, int T, hipStream_t s,
+                             Timing tm_down) {
+  if (T < 1 || T > SMALL_T) return hipErrorInvalidValue;
+  const int S = a.slots;
+  const int imax = std::max(a.grp[0].inter, a.grp[1].inter);
+  const bool mx = quant == Q_MXFP4;
+  const bool one_down = !mx || (imax + 127) / 128 <= MX_ONE;
+  DownSmallKernel down;
+  switch (quant) {
+  case Q_MXFP4: down = down_small_k<Q_MXFP4>(S, one_down); break;
+  case Q_BF16: down = down_small_k<Q_BF16>(S, true); break;
+  case Q_MLX4: down = down_small_k<Q_MLX4>(S, true); break;
+  default: down = down_small_k<Q_MLX8>(S, true); break;
+  }
+  static std::once_flag lds_once;
+  std::call_once(lds_once, [] {
+    for (int sl : {1, 2, 3, 4, 5, 6, 7, 8, 9})
+      for (const void *k : {(const void *)down_small_k<Q_MXFP4>(sl, true), (const void *)down_small_k<Q_MXFP4>(sl, false),
+                            (const void *)down_small_k<Q_BF16>(sl, true), (const void *)down_small_k<Q_MLX4>(sl, true),
+                            (const void *)down_small_k<Q_MLX8>(sl, true)}) {
+        (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        (void)hipGetLastError();
+      }
+  });
+  static int ncu = 0;
+  if (!ncu) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0) ncu = 256;
+  }
   a.row_tiles = a.hidden / 16;
   // MXFP4: per slot the activation terms and 16 rows of weight scales (of the larger group).
   const size_t lds_down = mx ? (size_t)S * (NTH * mx_row_bytes(a.hld) + 16 * ((16 * (imax / 32) + 15) / 16))
@@ -3098,7 +3136,7 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
   const int down_grid = std::min(down_small_items(a.row_tiles, T), std::max(8, (2 * ncu) & ~7));   // a multiple of 8
   const int ks = (mx || S > 4 || !one_down) ? 1 : 2;
   hipExtLaunchKernelGGL(down, dim3(down_grid), dim3(64 * S * ks), lds_down, s, tm_down.start,
-                        tm_down.stop, 0, a, (const int32_t *)ra.topk_idx);
+                        tm_down.stop, 0, a, topk_idx);
   return hipGetLastError();
 }
 

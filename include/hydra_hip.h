@@ -315,6 +315,42 @@ int hh_activation(hh_ctx *ctx, const hh_moe_desc *desc, const float *gate, const
 int hh_permute(hh_ctx *ctx, const int32_t *topk_idx, int32_t tokens, int32_t top_k,
                int32_t experts, int32_t *seg_offsets, int32_t *order);
 
+/* One weight matrix in an expert format, for the projection entries below. All pointers are
+ * device memory; rows and cols are multiples of 64.
+ *   MXFP4: weights = blocks [rows][cols/32][16] (low nibble = even column), scales = e8m0 bytes
+ *          [rows][cols/32], bias = bf16 [rows] or NULL (MXFP4.swift:67-99)
+ *   BF16 : weights = bf16 [rows][cols]
+ *   MLX4/MLX8: weights = words [rows][cols·bits/32] (low-order value first), scales and biases
+ *          bf16 [rows][cols/group_size] (MLXAffineLayout.swift:22-66), group_size 64           */
+typedef struct hh_matrix {
+    int32_t quant;            /* hh_quant                                                       */
+    int32_t rows, cols;
+    int32_t group_size;       /* MLX: 64                                                        */
+    const void *weights;
+    const void *scales;       /* MXFP4 / MLX; NULL for BF16                                     */
+    const uint16_t *biases;   /* MLX group biases; NULL otherwise                               */
+    const uint16_t *bias;     /* MXFP4: per-row bf16 bias added to y, or NULL                   */
+} hh_matrix;
+
+/* y = W·x (+ bias) for one fp32 input vector x [cols] → y fp32 [rows]: the operator-level
+ * expert projection of ForwardEncoder.expertProjection (ForwardEncoder.swift:947-972, MXFP4
+ * with bias), mlxAffineProjection (:328-365) and encodeProjection(.bf16) (:300-313), run on
+ * the layer's own down-product kernels (the input in the layer's activation operand: MXFP4 as
+ * three fp8 terms per 32-column block, ~2^-13 relative; BF16/MLX as a bf16 hi + lo pair).   */
+int hh_expert_gemv(hh_ctx *ctx, const hh_matrix *m, const float *x, float *y);
+/* The same for `tokens` input rows x [tokens][cols] → y [tokens][rows] (BatchEncoder
+ * .expertProjection, BatchEncoder.swift:147-173; mlxAffineBatchedProjection,
+ * ForwardEncoder.swift:456-487): the layer's decode down kernel up to 16 tokens, its prefill
+ * kernels above. Row t equals hh_expert_gemv of x[t] bit for bit.                           */
+int hh_expert_gemm(hh_ctx *ctx, const hh_matrix *m, const float *x, int32_t tokens, float *y);
+/* Weighted combine in rank order: y[t][j] = Σ_{r<count} weights[t][r]·slots[t][r][j], each
+ * product rounded to fp32 and the sum taken from r = 0 (write_expert_scaled then
+ * sum_expert_slices, dense.metal:131-158, as LayerRunner.encodeCombineSlices,
+ * LayerRunner.swift:279-301, encodes them). slots fp32 [tokens][count][size]; weights fp32
+ * [tokens][count], or NULL for a plain sum of the slots.                                     */
+int hh_combine(hh_ctx *ctx, const float *slots, const float *weights, int32_t tokens,
+               int32_t count, int32_t size, float *y);
+
 #ifdef __cplusplus
 }
 #endif

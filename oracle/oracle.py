@@ -387,3 +387,27 @@ def block_forward_layer(layer, norms_bf16, hidden, dense_out=None, nthreads=1):
         y, idx, w, _ = moe_forward(layer, x, x_router=xr, nthreads=nthreads)
         return y, idx, w
     return block_forward(desc, norms, hidden, moe, dense_out)
+
+
+def matvec(quant, rows, cols, weights, scales=None, biases=None, bias=None, x=None,
+           group=64) -> np.ndarray:
+    """y[t] = W·x[t] (+ bias) in fp64 with W dequantised exactly: MXFP4 through mxfp4_decode
+    (MXFP4.swift:67-99), MLX through mlx_dequant (Gemma4ReferenceOps.swift:210-239), BF16
+    widened; the projection of ReferenceLayer.matVec (ReferenceLayer.swift:104-113) and
+    MLXAffine.matvec. x fp32/fp64 [T][cols] → y fp64 [T][rows]."""
+    x = np.atleast_2d(np.asarray(x, np.float64))
+    if quant == 0:
+        W = mxfp4_decode(np.asarray(weights, np.uint8).reshape(-1, 16),
+                         np.asarray(scales, np.uint8).reshape(-1)).reshape(rows, cols).astype(np.float64)
+    elif quant == 3:
+        W = bf16_to_f32(np.asarray(weights, np.uint16).reshape(rows, cols)).astype(np.float64)
+    else:
+        bits = 4 if quant == 1 else 8
+        wd = np.asarray(weights, np.uint32).reshape(rows, -1)
+        sc = bf16_to_f32(np.asarray(scales, np.uint16)).astype(np.float64).reshape(rows, -1)
+        bi = bf16_to_f32(np.asarray(biases, np.uint16)).astype(np.float64).reshape(rows, -1)
+        W = np.stack([mlx_dequant(wd[r], sc[r], bi[r], cols, bits, group) for r in range(rows)])
+    y = x @ W.T
+    if bias is not None:
+        y = y + bf16_to_f32(np.asarray(bias, np.uint16)).astype(np.float64)
+    return y
