@@ -39,9 +39,12 @@ FLAGS = [
 ]
 
 
+DEFINES: list = []   # extra -D flags (development variants, e.g. HH_TRACE); none by default
+
+
 def compile_one(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *FLAGS, "-I", os.path.join(ROOT, "include"), "-I", CSRC, "-c",
+    cmd = [hipcc(), *FLAGS, *[f"-D{d}" for d in DEFINES], "-I", os.path.join(ROOT, "include"), "-I", CSRC, "-c",
            os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -65,4 +68,8 @@ def build(jobs: int = 4) -> str:
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=4)
-    print(build(ap.parse_args().jobs))
+    ap.add_argument("--define", action="append", default=[],
+                    help="extra preprocessor definition (development variants)")
+    args = ap.parse_args()
+    DEFINES.extend(args.define)
+    print(build(args.jobs))

@@ -33,6 +33,10 @@ hipError_t launch_block_gemma_finish(float *hidden, const float *mix, const floa
                                      const uint16_t *scalar, int H, float eps, int T,
                                      hipStream_t s);
 hipError_t launch_attention_decode(const AttnArgs &a, hipStream_t s);
+#ifdef HH_TRACE
+hipError_t trace_read(void *out, size_t bytes);
+hipError_t trace_clear();
+#endif
 hipError_t launch_down_small(int quant, GemmArgs a, const int32_t *topk_idx, int T, hipStream_t s,
                              Timing tm_down);
 hipError_t launch_proj_prepare(const GemmArgs &a, const float *x, int T, int cols, int32_t *topk,
@@ -1042,6 +1046,12 @@ int hh_expert_gemm(hh_ctx *ctx, const hh_matrix *m, const float *x, int32_t T, f
   ctx->dispatches += 2;
   return HH_OK;
 }
+
+#ifdef HH_TRACE
+// Development build only: the decode kernels' timeline of the last call (hh_gemm.hip).
+int hh_debug_trace_read(void *out, size_t bytes) { return hh::trace_read(out, bytes) == hipSuccess ? HH_OK : HH_EHIP; }
+int hh_debug_trace_clear(void) { return hh::trace_clear() == hipSuccess ? HH_OK : HH_EHIP; }
+#endif
 
 int hh_expert_gemv(hh_ctx *ctx, const hh_matrix *m, const float *x, float *y) {
   return hh_expert_gemm(ctx, m, x, 1, y);

@@ -344,12 +344,17 @@ __device__ __forceinline__ void chunk_mfma(f32x4 (&acc)[NM][NT], const typename 
           for (int hh = 0; hh < NH; ++hh) P[m][st] = mfma(av, as_bf16x8(b[st][hh][v]), P[m][st]);
       }
     }
-    // D row 4g + ii is the A row of lane 4g + ii: its scale and bias by shuffle.
+    // D row 4g + ii is the A row of lane 4g + ii: its scale and bias by shuffle (all four
+    // shuffles issued before the first is used).
 #pragma unroll
-    for (int m = 0; m < NM; ++m)
+    for (int m = 0; m < NM; ++m) {
+      const int sbl = (int)w[m].sb;
+      uint32_t sbs[4];
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) sbs[ii] = (uint32_t)__shfl(sbl, 4 * g + ii);
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
-        const uint32_t sbv = (uint32_t)__shfl((int)w[m].sb, 4 * g + ii);
+        const uint32_t sbv = sbs[ii];
         const float sc = bf16_bits_to_f32(sbv & 0xFFFF);
         const float bi0 = bf16_bits_to_f32(sbv >> 16);
         const float bi = FMT == Q_MLX4 ? __builtin_fmaf(-128.f, sc, bi0) : bi0;
@@ -359,6 +364,7 @@ __device__ __forceinline__ void chunk_mfma(f32x4 (&acc)[NM][NT], const typename 
           acc[m][st][ii] = __builtin_fmaf(bi, G[st][ii], acc[m][st][ii]);
         }
       }
+    }
   }
 }
 
@@ -636,6 +642,20 @@ __device__ __forceinline__ int rank_of(const int *s_idx, int t, int e, int K, bo
 }
 
 // ---- decode: gate-up ----------------------------------------------------------------------------
+// Development timeline (built only with -DHH_TRACE): per workgroup, wall-clock stamps (100 MHz)
+// at fixed points of the decode kernels, [kernel][block][point]; the last call's values.
+#ifdef HH_TRACE
+constexpr int kTraceBlocks = 4096, kTracePoints = 8;
+static __device__ uint64_t hh_trace_buf[3 * kTraceBlocks * kTracePoints];
+#define HH_TR(kern, point)                                                                     \
+  do {                                                                                         \
+    if (threadIdx.x == 0 && blockIdx.x < kTraceBlocks)                                         \
+      hh_trace_buf[((kern) * kTraceBlocks + blockIdx.x) * kTracePoints + (point)] = wall_clock64(); \
+  } while (0)
+#else
+#define HH_TR(kern, point) do {} while (0)
+#endif
+
 constexpr int SMALL_T = 16;       // largest batch of the decode kernels
 constexpr int UP_ROWS = 32;       // intermediates per up_small workgroup (2 tiles × {gate, up})
 constexpr int MX_ONE_CHUNKS = 24; // MXFP4 decode rows of at most this many 128-column chunks stream in one round
@@ -687,8 +707,10 @@ __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) 
 #pragma unroll
   for (int k = 0; k < XB; ++k)
     if (tid + NTH * k < nvec) xr[k] = xsrc(tid + NTH * k);
+  HH_TR(1, 0);
   SmallPick pk;
   if (!small_pick<NWV>(a, ra, u, shared_wg, s_idx, pk)) return;   // uniform over the workgroup
+  HH_TR(1, 1);
   const int e = pk.e, ntok = pk.ntok;
   const uint64_t tm = pk.tm;
   const uint8_t *blob = grp.blobs + (shared_wg ? 0 : (size_t)e * grp.stride);
@@ -708,6 +730,7 @@ __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) 
     if (tid + NTH * k < nvec) xdst(tid + NTH * k, xr[k]);
   for (int base = NTH * XB; base < nvec; base += NTH * 4) stage_batch<4>(base, tid, NTH, nvec, xsrc, xdst);
   __syncthreads();
+  HH_TR(1, 2);
 
   // Token column l16 = the l16-th token of the expert (padding columns repeat the last one).
   const int my_t = token_of(min(l16, ntok - 1));
@@ -722,11 +745,13 @@ __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) 
   const int slot_of_part = (is_up ? 1 : 0) * 2 + par;   // 0: gate even (keeps), 1: gate odd, 2: up even, 3: up odd
   if (slot_of_part > 0) s_part[slot_of_part - 1][q][lane] = acc[0][0];
   __syncthreads();
+  HH_TR(1, 3);
   if (slot_of_part == 0 && l16 < ntok) {
     const int r = rank_of(s_idx, my_t, e, K, shared_wg);
     up_epilogue<FMT>(a, blob, grp, rb + 4 * g, my_t * S + r, sum_chains(acc[0][0], s_part[0][q][lane]),
                      sum_chains(s_part[1][q][lane], s_part[2][q][lane]));
   }
+  HH_TR(1, 4);
 }
 
 // ---- MXFP4 on the scaled MFMA -------------------------------------------------------------------
@@ -1006,17 +1031,23 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
   // x terms of every token: first batch of loads now (they do not depend on the routing), stored
   // with the first item.
   const int RS = mx_row_bytes(a.xld);
+  HH_TR(1, 0);
   auto xs = mx_stage<NTX, 2>(s_xb, a.xq, a.xs, a.xld, a.hidden, T, [](int j) { return j; }, tid, 256);
   xs.load_first();
   // Top-k of every token (wave w: tokens w, w + 4, ...); workgroup 0 writes the routing outputs.
   for (int t = wave; t < T; t += 4) {
     const double *lg = ra.lg64 + (size_t)t * (E + 1);
+#ifdef HH_TRACE
+    { volatile double first = lg[lane % E]; (void)first; if (t == 0) HH_TR(1, 6); }
+#endif
     const TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave])
                             : topk_fast(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave]);
+    if (t == 0) HH_TR(1, 7);
     if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
     if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
   }
   __syncthreads();
+  HH_TR(1, 1);
   const Plan plan(s_idx, T, K, E);
   const int nu = plan.nu;
   const int rtr = a.grp[0].inter / UP_ROWS;
@@ -1065,6 +1096,7 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
       if (tid + 256 * k < nsv) *(u32x4 *)(s_sc + 16 * (tid + 256 * k)) = scv[k];
     for (int v = tid + 512; v < nsv; v += 256) *(u32x4 *)(s_sc + 16 * v) = *(const u32x4 *)(gsc + 16 * v);
     __syncthreads();
+    if (it == (int)blockIdx.x) HH_TR(1, 2);
 
     const uint8_t *my_sc = s_sc + (2 * (16 * q + l16) + (is_up ? 1 : 0)) * nsb;
     // The lane group as a value opaque to the compiler in each item: otherwise every chunk's
@@ -1083,6 +1115,7 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
     const f32x4 res = acc[0][0];
     if (is_up) s_up[q][lane] = res;
     __syncthreads();
+    if (it == (int)blockIdx.x) HH_TR(1, 3);
     if (!is_up && l16 < ntok) {
       const f32x4 y = up_values_mx(a, bias, res, s_up[q][lane]);
 #pragma unroll
@@ -1103,8 +1136,10 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
         store_hq(a, slot, rt, rt * UP_ROWS + 8 * g, rt * UP_ROWS + 8 * g + 4, hq, sb, g);
       }
     }
+    if (it == (int)blockIdx.x) HH_TR(1, 4);
     // s_hv and s_sc are rewritten by the next item only after its first barrier.
   }
+  HH_TR(1, 5);
 }
 
 // ---- decode: down + combine -----------------------------------------------------------------------
@@ -1137,6 +1172,7 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
   const int T = a.max_work;              // tokens of the batch
   const int nitems = down_small_items(a.row_tiles, T);
   const int r = wave % S, par = wave / S;
+  HH_TR(2, 0);
   for (int it = blockIdx.x; it < nitems; it += gridDim.x) {
   int rt, t;
   down_small_item(it, T, rt, t);
@@ -1182,9 +1218,11 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
       if (sid + sth * k < nsv) *(u32x4 *)(s_sc + 16 * (sid + sth * k)) = scv[k];
     for (int v = sid + 2 * sth; v < nsv; v += sth) *(u32x4 *)(s_sc + 16 * v) = *(const u32x4 *)(gsc + 16 * v);
     hs.store_first();
+    if (it == (int)blockIdx.x) HH_TR(2, 4);
     hs.rest();
     hs.pad();
     __syncthreads();
+    if (it == (int)blockIdx.x) HH_TR(2, 1);
     const uint8_t *brow = my_lds;
     const uint8_t *my_sc = s_sc + l16 * nsb;
     // MXFP4: one chain. DA ≥ MX_ONE instantiations run only for rows of at most DA chunks.
@@ -1221,6 +1259,7 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
     if (sid + sth * k < nvec) hdst(sid + sth * k, hr[k]);
   for (int base = sth * HB; base < nvec; base += sth * 4) stage_batch<4>(base, sid, sth, nvec, hsrc, hdst);
   __syncthreads();
+  if (it == (int)blockIdx.x) HH_TR(2, 1);
 
   as.run(at, nch, g, I, [&](const typename Fmt<FMT>::A (&w)[NM], int c) {
     const int col = Fmt<FMT>::bcol(c, g, I);
@@ -1241,6 +1280,7 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
     for (int ii = 0; ii < 4; ++ii) s_o[r][4 * g + ii] = o[ii];
   }
   __syncthreads();
+  if (it == (int)blockIdx.x) HH_TR(2, 2);
   if (tid < 16) {
     float y = s_o[0][tid];
     for (int qq = 1; qq < S; ++qq) y += s_o[qq][tid];
@@ -1250,6 +1290,7 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
   }
   __syncthreads();   // the next item rewrites the LDS rows and s_o
   }
+  HH_TR(2, 3);
 }
 
 // ---- decode, fused: one launch per MXFP4 layer ------------------------------------------------------
@@ -3098,6 +3139,17 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
 
 // The decode down product alone (the second launch of launch_small): slot values of T ≤ 16
 // tokens summed in rank order into a.y. Also the operator-level projection's T ≤ 16 path.
+#ifdef HH_TRACE
+hipError_t trace_read(void *out, size_t bytes) {
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(hh_trace_buf), std::min(bytes, sizeof(hh_trace_buf)), 0,
+                             hipMemcpyDeviceToHost);
+}
+hipError_t trace_clear() {
+  static uint64_t zeros[3 * kTraceBlocks * kTracePoints];
+  return hipMemcpyToSymbol(HIP_SYMBOL(hh_trace_buf), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
+}
+#endif
+
 hipError_t launch_down_small(int quant, GemmArgs a, const int32_t *topk_idx, int T, hipStream_t s,
                              Timing tm_down) {
   if (T < 1 || T > SMALL_T) return hipErrorInvalidValue;
