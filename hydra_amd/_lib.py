@@ -20,7 +20,12 @@ EXPORTS = [
     "hh_ctx_capture_begin", "hh_ctx_capture_end", "hh_graph_launch", "hh_graph_destroy",
     "hh_attention_decode", "hh_moe_forward_noalloc", "hh_moe_block_forward",
     "hh_expert_gemv", "hh_expert_gemm", "hh_combine",
+    "hh_runner_create", "hh_runner_destroy", "hh_runner_set_layer", "hh_runner_reserve",
+    "hh_runner_forward", "hh_runner_capture",
 ]
+
+# int (*hh_layer_hook)(void *user, int32_t layer, void *stream)
+LAYER_HOOK = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_int32, C.c_void_p)
 
 CODES = {0: "HH_OK", -1: "HH_EINVAL", -2: "HH_EALIGN", -3: "HH_ETOPK", -4: "HH_EHIP",
          -5: "HH_ENOMEM", -6: "HH_ESHAPE"}
@@ -98,6 +103,13 @@ def lib() -> C.CDLL:
     L.hh_expert_gemv.argtypes = [vp, C.POINTER(MatrixC), vp, vp]
     L.hh_expert_gemm.argtypes = [vp, C.POINTER(MatrixC), vp, i32, vp]
     L.hh_combine.argtypes = [vp, vp, vp, i32, i32, i32, vp]
+    L.hh_runner_create.argtypes = [vp, i32, C.POINTER(vp)]
+    L.hh_runner_destroy.argtypes = [vp]
+    L.hh_runner_set_layer.argtypes = [vp, i32, C.POINTER(MoEDescC), C.POINTER(MoEWeightsC),
+                                      C.POINTER(BlockNormsC), vp]
+    L.hh_runner_reserve.argtypes = [vp, i32]
+    L.hh_runner_forward.argtypes = [vp, vp, i32, LAYER_HOOK, vp]
+    L.hh_runner_capture.argtypes = [vp, vp, i32, LAYER_HOOK, vp, C.POINTER(vp)]
     L.hh_mxfp4_dequant.argtypes = [vp, vp, vp, i64, vp]
     L.hh_mlx_dequant.argtypes = [vp, vp, vp, vp, i32, i32, i32, i32, vp]
     L.hh_router_topk.argtypes = [vp, C.POINTER(MoEDescC), C.POINTER(MoEWeightsC), vp, i32, vp,

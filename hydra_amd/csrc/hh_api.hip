@@ -385,6 +385,22 @@ int check_router(const hh_moe_desc *d, const hh_moe_weights *w, const uint16_t *
   return HH_OK;
 }
 
+// The FFN block's scratch after the layer's: the bf16 layer input, the GEMMA router's bf16
+// residual, and (Gemma branches) the expert branch's fp32 output.
+struct BlockScratch {
+  size_t xn, xr, mix, total;
+};
+BlockScratch block_plan(const hh_moe_desc &d, const Scratch &s, int T, bool gemma) {
+  const size_t row16 = align_up(sizeof(uint16_t) * (size_t)T * d.hidden, 256);
+  const size_t row32 = align_up(sizeof(float) * (size_t)T * d.hidden, 256);
+  BlockScratch b;
+  b.xn = s.total;
+  b.xr = b.xn + row16;
+  b.mix = b.xr + (d.router == HH_ROUTER_GEMMA ? row16 : 0);
+  b.total = b.mix + (gemma ? row32 : 0);
+  return b;
+}
+
 // Argument checks shared by the layer entry points (HH_OK or the error code).
 int check_forward(const hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w,
                   const uint16_t *x, const uint16_t *x_router, int32_t T, const float *y) {
@@ -682,14 +698,10 @@ int hh_moe_block_forward(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights
   if (T == 0) return HH_OK;
   HH_HIP(hipSetDevice(ctx->device));
   const Scratch s = plan(*d, T);
-  // After the layer's scratch: the bf16 layer input, the GEMMA router's bf16 residual, and (Gemma
-  // branches) the expert branch's fp32 output.
-  const size_t row16 = align_up(sizeof(uint16_t) * (size_t)T * d->hidden, 256);
-  const size_t row32 = align_up(sizeof(float) * (size_t)T * d->hidden, 256);
+  const BlockScratch bs = block_plan(*d, s, T, gemma);
   const bool router_resid = d->router == HH_ROUTER_GEMMA;
-  const size_t o_xn = s.total, o_xr = o_xn + row16, o_mix = o_xr + (router_resid ? row16 : 0);
-  const size_t total = o_mix + (gemma ? row32 : 0);
-  if ((rc = ensure_arena(ctx, total))) return rc;
+  const size_t o_xn = bs.xn, o_xr = bs.xr, o_mix = bs.mix;
+  if ((rc = ensure_arena(ctx, bs.total))) return rc;
   uint8_t *base = ctx->arena;
   uint16_t *xn = (uint16_t *)(base + o_xn);
   uint16_t *xr = router_resid ? (uint16_t *)(base + o_xr) : nullptr;
@@ -1066,6 +1078,102 @@ int hh_combine(hh_ctx *ctx, const float *slots, const float *weights, int32_t T,
   HH_HIP(hh::launch_combine_weighted(slots, weights, T, count, size, y, ctx->stream));
   ctx->dispatches += 1;
   return HH_OK;
+}
+
+// ---- the model's MoE halves as one runner ----------------------------------------------------
+
+}  // extern "C"
+
+struct hh_runner {
+  hh_ctx *ctx = nullptr;
+  struct Layer {
+    bool set = false;
+    hh_moe_desc desc{};
+    hh_moe_weights w{};
+    hh_block_norms norms{};
+    const float *dense_out = nullptr;
+  };
+  std::vector<Layer> layers;
+};
+
+extern "C" {
+
+int hh_runner_create(hh_ctx *ctx, int32_t layers, hh_runner **out) {
+  if (!ctx || !out) return fail(HH_EINVAL, "NULL argument");
+  *out = nullptr;
+  if (layers <= 0 || layers > 4096) return fail(HH_EINVAL, "layers outside 1..4096");
+  hh_runner *r = new hh_runner;
+  r->ctx = ctx;
+  r->layers.resize((size_t)layers);
+  *out = r;
+  return HH_OK;
+}
+
+int hh_runner_destroy(hh_runner *r) {
+  delete r;
+  return HH_OK;
+}
+
+int hh_runner_set_layer(hh_runner *r, int32_t layer, const hh_moe_desc *d, const hh_moe_weights *w,
+                        const hh_block_norms *norms, const float *dense_out) {
+  if (!r || !d || !w || !norms) return fail(HH_EINVAL, "NULL argument");
+  if (layer < 0 || layer >= (int32_t)r->layers.size()) return fail(HH_EINVAL, "no such layer");
+  int rc = check_desc(d);
+  if (rc) return rc;
+  if (!norms->pre_norm) return fail(HH_EINVAL, "norms->pre_norm is required");
+  if (norms->post_expert_norm && (!norms->post_dense_norm || !norms->post_norm || !dense_out))
+    return fail(HH_EINVAL, "Gemma branches need post_dense_norm, post_norm and dense_out");
+  hh_runner::Layer &L = r->layers[(size_t)layer];
+  L.set = true;
+  L.desc = *d;
+  L.w = *w;
+  L.norms = *norms;
+  L.dense_out = dense_out;
+  return HH_OK;
+}
+
+int hh_runner_reserve(hh_runner *r, int32_t max_tokens) {
+  if (!r) return fail(HH_EINVAL, "runner is NULL");
+  if (max_tokens <= 0 || max_tokens > kMaxTokens) return fail(HH_EINVAL, "max_tokens outside 1..65536");
+  size_t need = 0;
+  for (const hh_runner::Layer &L : r->layers) {
+    if (!L.set) return fail(HH_EINVAL, "a layer of the runner is not set");
+    const bool gemma = L.norms.post_expert_norm != nullptr;
+    for (int t : {max_tokens, std::min(max_tokens, 63), std::min(max_tokens, 127)})
+      need = std::max(need, block_plan(L.desc, plan(L.desc, t), t, gemma).total);
+  }
+  return ensure_arena(r->ctx, need);
+}
+
+int hh_runner_forward(hh_runner *r, float *hidden, int32_t T, hh_layer_hook hook, void *user) {
+  if (!r || !hidden) return fail(HH_EINVAL, "NULL argument");
+  for (size_t l = 0; l < r->layers.size(); ++l) {
+    const hh_runner::Layer &L = r->layers[l];
+    if (!L.set) return fail(HH_EINVAL, "layer " + std::to_string(l) + " of the runner is not set");
+    if (hook) {
+      const int hrc = hook(user, (int32_t)l, (void *)r->ctx->stream);
+      if (hrc) return fail(hrc, "the layer hook failed at layer " + std::to_string(l));
+    }
+    const int rc = hh_moe_block_forward(r->ctx, &L.desc, &L.w, &L.norms, hidden, L.dense_out, T,
+                                        nullptr, nullptr);
+    if (rc) return rc;
+  }
+  return HH_OK;
+}
+
+int hh_runner_capture(hh_runner *r, float *hidden, int32_t T, hh_layer_hook hook, void *user,
+                      hh_graph **out) {
+  if (!r || !out) return fail(HH_EINVAL, "NULL argument");
+  int rc = hh_ctx_capture_begin(r->ctx);
+  if (rc) return rc;
+  const int frc = hh_runner_forward(r, hidden, T, hook, user);
+  const std::string ferr = g_error;
+  rc = hh_ctx_capture_end(r->ctx, out);
+  if (frc) {
+    if (*out) { hh_graph_destroy(*out); *out = nullptr; }
+    return fail(frc, ferr);
+  }
+  return rc;
 }
 
 }  // extern "C"

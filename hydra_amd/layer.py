@@ -17,7 +17,7 @@ import numpy as np
 import torch
 
 from . import formats as F
-from ._lib import BlockNormsC, MoEWeightsC, check, desc_c, lib
+from ._lib import LAYER_HOOK, BlockNormsC, MoEWeightsC, check, desc_c, lib
 
 
 # Device tensors of a layer besides its expert blobs (absent ones are None).
@@ -80,6 +80,69 @@ class Context:
     def close(self):
         if self.handle:
             lib().hh_ctx_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def block_norms_c(norms: dict) -> BlockNormsC:
+    """hh_block_norms from {pre_norm, post_expert_norm, post_dense_norm, post_norm, layer_scalar:
+    device bf16 tensors (absent = NULL), eps: float}."""
+    return BlockNormsC(_ptr(norms.get("pre_norm")), _ptr(norms.get("post_expert_norm")),
+                       _ptr(norms.get("post_dense_norm")), _ptr(norms.get("post_norm")),
+                       _ptr(norms.get("layer_scalar")), float(norms.get("eps", 1e-5)))
+
+
+class Runner:
+    """hh_runner: the MoE halves (FFN blocks) of a layer stack on one context. `hook(layer)`
+    (optional) runs before each layer's block and may only enqueue work on the context's
+    stream (the token mixer)."""
+
+    def __init__(self, ctx: Context, layers: list):
+        """layers: [(MoELayer, norms dict, dense_out tensor or None)]."""
+        self.ctx = ctx
+        h = C.c_void_p()
+        check(lib().hh_runner_create(ctx.handle, len(layers), C.byref(h)))
+        self.handle = h
+        self._keep = []
+        for i, (ml, norms, dense) in enumerate(layers):
+            nc = block_norms_c(norms)
+            self._keep.append((ml, norms, dense, nc))
+            check(lib().hh_runner_set_layer(h, i, C.byref(ml._desc_c), C.byref(ml._weights_c),
+                                            C.byref(nc), _ptr(dense)))
+
+    def reserve(self, max_tokens: int):
+        check(lib().hh_runner_reserve(self.handle, max_tokens))
+
+    def _hook(self, hook):
+        if hook is None:
+            return LAYER_HOOK()
+        def fn(user, layer, stream):
+            try:
+                hook(layer)
+                return 0
+            except Exception:
+                return -1
+        return LAYER_HOOK(fn)
+
+    def forward(self, hidden: torch.Tensor, hook=None):
+        cb = self._hook(hook)
+        check(lib().hh_runner_forward(self.handle, _ptr(hidden), hidden.shape[0], cb, None))
+
+    def capture(self, hidden: torch.Tensor, hook=None) -> "Graph":
+        cb = self._hook(hook)
+        g = C.c_void_p()
+        check(lib().hh_runner_capture(self.handle, _ptr(hidden), hidden.shape[0], cb, None,
+                                      C.byref(g)))
+        return Graph(g, self.ctx)
+
+    def close(self):
+        if self.handle:
+            lib().hh_runner_destroy(self.handle)
             self.handle = None
 
     def __del__(self):
@@ -180,9 +243,7 @@ class MoELayer:
         """The FFN block on the fp32 residual stream `hidden` [T][H], updated in place
         (hh_moe_block_forward): `norms` maps pre_norm / post_expert_norm / post_dense_norm /
         post_norm / layer_scalar to device bf16 tensors (absent = NULL) and eps to a float."""
-        nc = BlockNormsC(_ptr(norms.get("pre_norm")), _ptr(norms.get("post_expert_norm")),
-                         _ptr(norms.get("post_dense_norm")), _ptr(norms.get("post_norm")),
-                         _ptr(norms.get("layer_scalar")), float(norms.get("eps", 1e-5)))
+        nc = block_norms_c(norms)
         check(lib().hh_moe_block_forward(self.ctx.handle, C.byref(self._desc_c),
                                          C.byref(self._weights_c), C.byref(nc), _ptr(hidden),
                                          _ptr(dense_out), hidden.shape[0], _ptr(idx), _ptr(w)))

@@ -273,6 +273,30 @@ int hh_ctx_capture_end(hh_ctx *ctx, hh_graph **out);
 int hh_graph_launch(hh_graph *graph);
 int hh_graph_destroy(hh_graph *graph);
 
+/* The MoE halves of a whole model behind a HIP-backed ModelRunner (ModelRunner.forward /
+ * prefill, ModelRunner.swift:110-230, 418-547; QwenLayerRunner.swift:11-14): per layer the
+ * caller's token mixer (attention), enqueued by `hook` on the context's stream, then the
+ * layer's FFN block (hh_moe_block_forward) — router, experts and residual on the device with no
+ * host synchronisation between layers (the reference waits for a router readback before it can
+ * fetch each layer's experts, ModelRunner.swift:164-170). hh_runner_capture records the whole
+ * stack, hooks included, as one HIP graph for a fixed token count (the hooks must only enqueue
+ * work on the stream they are given). Layers are set once with their description, weights,
+ * norms and, for Gemma's parallel branches, the buffer the hook fills with the dense MLP's
+ * output. hh_runner_reserve sizes the context's scratch for every layer up to max_tokens
+ * (required before capture).                                                                 */
+typedef struct hh_runner hh_runner;
+typedef int (*hh_layer_hook)(void *user, int32_t layer, void *stream);
+int hh_runner_create(hh_ctx *ctx, int32_t layers, hh_runner **out);
+int hh_runner_destroy(hh_runner *runner);
+int hh_runner_set_layer(hh_runner *runner, int32_t layer, const hh_moe_desc *desc,
+                        const hh_moe_weights *w, const hh_block_norms *norms,
+                        const float *dense_out);
+int hh_runner_reserve(hh_runner *runner, int32_t max_tokens);
+int hh_runner_forward(hh_runner *runner, float *hidden, int32_t tokens, hh_layer_hook hook,
+                      void *user);
+int hh_runner_capture(hh_runner *runner, float *hidden, int32_t tokens, hh_layer_hook hook,
+                      void *user, hh_graph **out);
+
 /* Checkpoint expert tensors straight into HBM: copies one stacked checkpoint tensor, the E
  * experts' copies of blob slot `slot` back to back (E × bytes[slot] bytes, e.g. GPT-OSS's
  * model.layers.L.mlp.experts.gate_up_proj_blocks [E][2I][H/32][16]), into the E blobs at

@@ -43,6 +43,10 @@ CASES = {
     "mlx8-down": (F.QUANT_MLX8, 2048, 512, False),
     "bf16-gate-up": (F.QUANT_BF16, 1408, 2816, False),
     "bf16-down": (F.QUANT_BF16, 2816, 704, False),
+    "bf16-small": (F.QUANT_BF16, 64, 256, False),
+    "bf16-square": (F.QUANT_BF16, 256, 256, False),
+    "mlx4-small": (F.QUANT_MLX4, 64, 256, False),
+    "mxfp4-small": (F.QUANT_MXFP4, 64, 256, True),
 }
 
 

@@ -1,0 +1,115 @@
+"""hh_runner: a layer stack's MoE halves (FFN blocks) with the caller's per-layer hook in front
+of each, eager and recorded as one HIP graph, against the same calls made one by one.
+
+Three layers share one fp32 residual stream (H = 256): an MXFP4 GPT-OSS-style pre-norm block, a
+Qwen-style MLX-4 block with a shared expert and an 8-bit MLX router, and a Gemma-style BF16
+block with parallel branches whose dense output the hook writes. The hook enqueues a projection
+of the current residual stream (hh_expert_gemm) before every layer, so the order of hooks and
+blocks shows in its outputs. Bars: bit for bit."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from hydra_amd import formats as F
+from hydra_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+H = 256
+DESCS = [
+    (F.MoEDesc(hidden=H, intermediate=128, experts=6, top_k=2, quant=F.QUANT_MXFP4,
+               activation=F.ACT_SWIGLU_OAI, router=F.ROUTER_TOPK_SOFTMAX, expert_bias=1), 0),
+    (F.MoEDesc(hidden=H, intermediate=128, experts=8, top_k=3, quant=F.QUANT_MLX4,
+               activation=F.ACT_SILU, router=F.ROUTER_SOFTMAX_TOPK_RENORM,
+               shared_intermediate=128, group_size=64), 8),
+    (F.MoEDesc(hidden=H, intermediate=128, experts=5, top_k=2, quant=F.QUANT_BF16,
+               activation=F.ACT_GELU_TANH, router=F.ROUTER_GEMMA), 0),
+]
+
+
+def _norms(rng, gemma):
+    nb = lambda: synth.f32_to_bf16(rng.uniform(0.5, 1.5, H).astype(np.float32))
+    n = {"pre_norm": nb(), "eps": 1e-6 if gemma else 1e-5}
+    if gemma:
+        n.update(post_expert_norm=nb(), post_dense_norm=nb(), post_norm=nb(),
+                 layer_scalar=synth.f32_to_bf16(np.array([0.5], np.float32)))
+    return n
+
+
+@pytest.mark.parametrize("T", [1, 24])
+def test_runner_equals_calls_one_by_one(T):
+    import torch
+    from hydra_amd._lib import MatrixC, check, lib
+    from hydra_amd.layer import Context, MoELayer, Runner, to_device
+    print(f"[gpu] runner T={T}", flush=True)
+    dev = "cuda:0"
+    ctx = Context(0)
+    try:
+        rng = np.random.default_rng(71)
+        layers, mats, probes = [], [], []
+        dense = torch.zeros((T, H), dtype=torch.float32, device=dev)
+        for i, (d, rb) in enumerate(DESCS):
+            ml = MoELayer(synth.make_layer(d, seed=72 + i, router_bits=rb), ctx)
+            gemma = d.router == F.ROUTER_GEMMA
+            norms = {k: (v if k == "eps" else to_device(v, dev)) for k, v in _norms(rng, gemma).items()}
+            layers.append((ml, norms, dense if gemma else None))
+            rows = H if gemma else 64
+            w = to_device(synth.bf16_normal(80 + i, "hook", rows * H, 0.0, 0.05), dev)
+            mats.append((MatrixC(F.QUANT_BF16, rows, H, 64, C.c_void_p(w.data_ptr()), None, None, None), w))
+            probes.append(dense if gemma else torch.empty((T, rows), dtype=torch.float32, device=dev))
+        runner = Runner(ctx, layers)
+        runner.reserve(T)
+
+        def hook(l, hidden):
+            out = probes[l]
+            check(lib().hh_expert_gemm(ctx.handle, C.byref(mats[l][0]), C.c_void_p(hidden.data_ptr()),
+                                       T, C.c_void_p(out.data_ptr())))
+
+        def snapshot(hidden):
+            return [hidden.cpu().numpy().copy()] + [p.cpu().numpy().copy() for p in probes]
+
+        x0 = (rng.standard_normal((T, H)) * 2).astype(np.float32)
+        # one by one
+        hid = torch.from_numpy(x0.copy()).to(dev)
+        torch.cuda.synchronize()
+        for l, (ml, norms, dn) in enumerate(layers):
+            hook(l, hid)
+            ml.block_forward_into(norms, hid, dn)
+        ctx.synchronize()
+        ref = snapshot(hid)
+        assert np.isfinite(ref[0]).all()
+        # the runner, eager
+        for p in probes:
+            p.fill_(float("nan"))
+        hid2 = torch.from_numpy(x0.copy()).to(dev)
+        torch.cuda.synchronize()
+        seen = []
+        runner.forward(hid2, hook=lambda l: (seen.append(l), hook(l, hid2)))
+        ctx.synchronize()
+        assert seen == [0, 1, 2]
+        for a, b in zip(snapshot(hid2), ref):
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        # one graph for the stack, replayed on new inputs
+        buf = torch.empty((T, H), dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        graph = runner.capture(buf, hook=lambda l: hook(l, buf))
+        for rep in range(3):
+            xr = (rng.standard_normal((T, H)) * 2).astype(np.float32)
+            e = torch.from_numpy(xr.copy()).to(dev)
+            torch.cuda.synchronize()
+            runner.forward(e, hook=lambda l: hook(l, e))   # eager work between the replays
+            ctx.synchronize()
+            expect = snapshot(e)
+            buf.copy_(torch.from_numpy(xr))
+            for p in probes:
+                p.fill_(float("nan"))
+            torch.cuda.synchronize()
+            graph.launch()
+            ctx.synchronize()
+            for a, b in zip(snapshot(buf), expect):
+                assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), rep
+        graph.close()
+        runner.close()
+    finally:
+        ctx.close()
