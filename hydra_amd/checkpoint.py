@@ -236,3 +236,127 @@ def load_moe_layer(path_or_ckpt, desc: F.MoEDesc, family: str, layer: int,
         tensors[key] = torch.from_numpy(a).to(dev)
     torch.cuda.synchronize(dev)
     return MoELayer.resident(desc, experts, lay.stride, tensors, ctx, router_bits=router_bits)
+
+
+# ---- .hydra installations ----------------------------------------------------------------------
+# A .hydra directory (HydraLayout.swift:4-20): manifest.json (format "hydra/1", the model's
+# counts, the expert stride; Manifest.swift:9-80), resident.bin (the resident tensors in the
+# model's declared order, each at a 256-byte aligned offset, HydraLayout.swift:52-70),
+# experts/layer_NN.bin (E expert blobs at the blob stride, RepackPlan.swift:21, the exact bytes the
+# kernels read).
+
+HYDRA_FORMAT = "hydra/1"      # HydraManifest.currentFormat (Manifest.swift:13)
+
+
+def hydra_manifest(path: str) -> dict:
+    with open(os.path.join(path, "manifest.json")) as f:
+        m = json.load(f)
+    if m.get("format") != HYDRA_FORMAT:
+        raise CheckpointError(f"{path}: manifest format {m.get('format')!r}, expected {HYDRA_FORMAT!r}")
+    return m
+
+
+def gpt_oss_resident_tensors(hidden: int, experts: int, layers: int, heads: int = 64,
+                             head_dim: int = 64, kv_heads: int = 8):
+    """GPT-OSS's resident tensor list in declaration order, (name, bytes), for layers
+    0..layers-1 (GptOssConfig.residentTensorNames, GptOssConfig.swift:148-166; all BF16)."""
+    q, kv = heads * head_dim, kv_heads * head_dim
+    out = []
+    for l in range(layers):
+        p = f"model.layers.{l}"
+        out += [(f"{p}.input_layernorm.weight", 2 * hidden),
+                (f"{p}.self_attn.q_proj.weight", 2 * q * hidden), (f"{p}.self_attn.q_proj.bias", 2 * q),
+                (f"{p}.self_attn.k_proj.weight", 2 * kv * hidden), (f"{p}.self_attn.k_proj.bias", 2 * kv),
+                (f"{p}.self_attn.v_proj.weight", 2 * kv * hidden), (f"{p}.self_attn.v_proj.bias", 2 * kv),
+                (f"{p}.self_attn.o_proj.weight", 2 * hidden * q), (f"{p}.self_attn.o_proj.bias", 2 * hidden),
+                (f"{p}.self_attn.sinks", 2 * heads),
+                (f"{p}.post_attention_layernorm.weight", 2 * hidden),
+                (f"{p}.mlp.router.weight", 2 * experts * hidden), (f"{p}.mlp.router.bias", 2 * experts)]
+    return out
+
+
+def resident_placements(tensors):
+    """{name: (offset, bytes)}: each tensor at the next 256-byte aligned offset, in order
+    (HydraLayout.init, HydraLayout.swift:52-70)."""
+    out, cursor = {}, 0
+    for name, nbytes in tensors:
+        cursor = F._align(cursor, F.TENSOR_ALIGNMENT)
+        out[name] = (cursor, nbytes)
+        cursor += nbytes
+    return out
+
+
+def load_hydra_layer(path: str, desc: F.MoEDesc, family: str, layer: int,
+                     ctx: Context | None = None, device: int = 0, router_checkpoint=None,
+                     attention=(64, 64, 8)) -> MoELayer:
+    """The MoE half of layer `layer` of a .hydra installation, resident in HBM. The experts come
+    from experts/layer_NN.bin as they are (checked against the manifest's count and stride and
+    this build's blob layout). The router: for GPT-OSS from resident.bin at the placement of
+    `model.layers.L.mlp.router.{weight,bias}` (resident order of GptOssConfig, attention dims
+    (heads, head_dim, kv_heads) = `attention`); for the other families from
+    `router_checkpoint` (a safetensors checkpoint or directory), as load_moe_layer reads it."""
+    m = hydra_manifest(path)
+    model, lay_m = m["model"], m["layout"]
+    lay = F.blob_layout(desc)
+    if model["expertCount"] != desc.experts or model["hiddenSize"] != desc.hidden:
+        raise CheckpointError(f"{path}: manifest has {model['expertCount']} experts of hidden "
+                              f"{model['hiddenSize']}, the description {desc.experts} / {desc.hidden}")
+    if lay_m["expertStrideBytes"] != lay.stride or lay_m["expertPayloadBytes"] != lay.payload:
+        raise CheckpointError(f"{path}: expert stride/payload {lay_m['expertStrideBytes']}/"
+                              f"{lay_m['expertPayloadBytes']} differ from the blob layout {lay.stride}/{lay.payload}")
+    if not 0 <= layer < model["layerCount"]:
+        raise CheckpointError(f"{path}: no layer {layer} (layerCount {model['layerCount']})")
+    fn = os.path.join(path, "experts", f"layer_{layer:02d}.bin")
+    if not os.path.exists(fn) or os.path.getsize(fn) != desc.experts * lay.stride:
+        raise CheckpointError(f"{fn}: missing or not {desc.experts} blobs of {lay.stride} bytes")
+    blobs = np.memmap(fn, dtype=np.uint8, mode="r", shape=(desc.experts, lay.stride))
+    tensors = {}
+    if family == "gpt-oss":
+        heads, head_dim, kv_heads = attention
+        place = resident_placements(gpt_oss_resident_tensors(desc.hidden, desc.experts,
+                                                             model["layerCount"], heads, head_dim,
+                                                             kv_heads))
+        rfn = os.path.join(path, "resident.bin")
+        res = np.memmap(rfn, dtype=np.uint8, mode="r")
+        for key, suffix in [("router_weight", "weight"), ("router_bias", "bias")]:
+            if key == "router_bias" and not desc.expert_bias:
+                continue
+            off, nb = place[f"model.layers.{layer}.mlp.router.{suffix}"]
+            if off + nb > res.size:
+                raise CheckpointError(f"{rfn}: shorter than the router placement of layer {layer}")
+            tensors[key] = np.array(res[off:off + nb]).view(np.uint16)
+        router_bits = 0
+    else:
+        if router_checkpoint is None:
+            raise CheckpointError(f"{family}: the router comes from router_checkpoint (its resident "
+                                  f"placement is not described here)")
+        ck = router_checkpoint if isinstance(router_checkpoint, Checkpoint) else Checkpoint(router_checkpoint)
+        router_bits = _quantised_router_bits(ck, desc, family, layer)
+        for key, (name, dt, shape, req) in router_sources(desc, family, layer, router_bits).items():
+            if req or name in ck:
+                tensors[key] = np.array(ck.tensor(name, dt, shape))
+    ctx = ctx or Context(device)
+    dev = torch.device(f"cuda:{ctx.device}")
+    torch.cuda.synchronize(dev)
+    experts = torch.from_numpy(np.array(blobs)).to(dev)
+    dt = {}
+    for key, data in tensors.items():
+        a = np.ascontiguousarray(data)
+        if key.endswith("_words"):
+            a = a.view(np.int32)
+        elif a.dtype == np.uint8:
+            a = a.view(np.int16)
+        elif a.dtype == np.uint16:
+            a = a.view(np.int16)
+        dt[key] = torch.from_numpy(a.copy()).to(dev)
+    if desc.shared_intermediate:
+        shared = expert_sources(desc, family, layer, shared=True)
+        ck = router_checkpoint if isinstance(router_checkpoint, Checkpoint) else Checkpoint(router_checkpoint)
+        slay = F.blob_layout(desc, desc.shared_intermediate)
+        blob = np.zeros(slay.stride, np.uint8)
+        for slot, name, dtn, shape in shared:
+            blob[slay.offsets[slot]:slay.offsets[slot] + slay.sizes[slot]] = \
+                np.asarray(ck.tensor(name, dtn, shape)).reshape(-1)
+        dt["shared_expert"] = torch.from_numpy(blob).to(dev)
+    torch.cuda.synchronize(dev)
+    return MoELayer.resident(desc, experts, lay.stride, dt, ctx, router_bits=router_bits)
