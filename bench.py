@@ -166,17 +166,25 @@ def measure_decode(wl, T, steps, warmup, fused=False):
 
 
 def measure_stack(wl, T, layers, steps, warmup):
-    """A decode layer stack (GPT-OSS-20B has 24 MoE layers) at T tokens: `layers` calls per
-    step over the resident weight copies in turn, run eagerly and as one captured HIP graph
-    (hh_ctx_capture_begin / hh_graph_launch). Returns µs per layer of both."""
+    """The MoE halves of a GPT-OSS-20B decode stack (24 layers) at T tokens through hh_runner:
+    per layer the FFN block (RMSNorm, router, experts, residual) on one fp32 residual stream,
+    layer l on weight copy l % copies, no host synchronisation between layers; run eagerly and
+    as one captured HIP graph. Returns µs per layer of both."""
+    from hydra_amd.layer import MoELayer, Runner
     torch = wl.torch
+    dev = "cuda:0"
+    desc = wl.desc
     wl.ctx.decode_fused(0)
-    wl.prepare(T, bank=max(layers, 8))
-    calls = [(wl.bank[l], wl.idx[l], wl.wc[l % len(wl.wc)]) for l in range(layers)]
-
-    def record():
-        for x, idx, wc in calls:
-            wl.layer.forward_into(x, wl.y, idx, wl.w, weights_c=wc)
+    g = torch.Generator(device=dev).manual_seed(7)
+    norm = {"pre_norm": (torch.rand(desc.hidden, device=dev, generator=g) + 0.5).bfloat16().view(torch.int16),
+            "eps": 1e-5}
+    mls = [MoELayer.resident(desc, wl.copies[l % len(wl.copies)], wl.layer.expert_stride,
+                             wl.layer.tensors, wl.ctx) for l in range(layers)]
+    runner = Runner(wl.ctx, [(ml, norm, None) for ml in mls])
+    runner.reserve(T)
+    hidden = torch.randn((T, desc.hidden), device=dev, generator=g) * 3
+    base = hidden.clone()
+    torch.cuda.synchronize()
 
     def timed(fn):
         for _ in range(warmup):
@@ -188,14 +196,18 @@ def measure_stack(wl, T, layers, steps, warmup):
         wl.ctx.synchronize()
         return (time.perf_counter() - t0) / steps
 
-    eager = timed(record)
-    graph = wl.ctx.capture(record)
+    eager = timed(lambda: runner.forward(hidden))
+    hidden.copy_(base)
+    torch.cuda.synchronize()
+    graph = runner.capture(hidden)
     replay = timed(graph.launch)
     graph.close()
+    runner.close()
     wl.ctx.decode_fused(-1)
     return {"T": T, "layers": layers, "eager_us_per_layer": eager / layers * 1e6,
             "graph_us_per_layer": replay / layers * 1e6, "graph_tokens_per_s": T / replay,
-            "eager_tokens_per_s": T / eager}
+            "eager_tokens_per_s": T / eager,
+            "what": "hh_runner FFN blocks (RMSNorm + MoE + residual) of 24 GPT-OSS-20B layers"}
 
 
 def measure_attention(torch, keys, q_heads=64, kv_heads=8, head_dim=64, reps=50, steps=20):
@@ -339,6 +351,8 @@ def main():
     ap.add_argument("--only-other", default=None,
                     help="run only the named other config (qwen-35b-a3b-mlx4, ...; for profiling)")
     ap.add_argument("--only-prefill", action="store_true", help="prefill only (for profiling)")
+    ap.add_argument("--only-stack", action="store_true",
+                    help="the 24-layer FFN-block decode stack only (for profiling)")
     ap.add_argument("--only-attention", action="store_true",
                     help="decode attention only (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -365,6 +379,11 @@ def main():
     from hydra_amd._lib import lib
     lib()  # fail loudly if the HIP library is missing
 
+    if args.only_stack:
+        wl = Workload(torch, F.GPT_OSS_20B, copies=args.copies)
+        print(json.dumps({"decode_stack_24_layers": {"1": measure_stack(wl, 1, 24, args.steps, args.warmup)}}))
+        wl.close()
+        return
     if args.only_attention:
         print(json.dumps({"decode_attention_gpt_oss": {
             str(k): measure_attention(torch, k) for k in [4096, 32768, 131072]}}))

@@ -427,14 +427,30 @@ int check_forward(const hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights 
 // One layer over T ≥ 1 tokens with its scratch at `base` (laid out by plan(*d, T)). With
 // `noalloc` the call takes neither the one-launch decode (its flag buffer is allocated on first
 // use) nor profiling events.
+// The FFN block's norm when the small-batch router kernel forms the layer input itself.
+struct BlockIn {
+  const float *hidden;
+  const uint16_t *norm_w;
+  float eps;
+  int pow_form;
+};
+
 int forward_layer(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w, const uint16_t *x,
                   const uint16_t *x_router, int32_t T, float *y, int32_t *topk_idx, float *topk_w,
-                  uint8_t *base, const Scratch &s, bool noalloc, const float *resid = nullptr) {
+                  uint8_t *base, const Scratch &s, bool noalloc, const float *resid = nullptr,
+                  const BlockIn *bin = nullptr) {
   int rc;
 
   hh::RouteArgs r = route_args(*d, w, base, s, x, x_router, T);
   if (topk_idx) r.topk_idx = topk_idx;
   if (topk_w) r.topk_w = topk_w;
+  if (bin) {
+    r.resid = bin->hidden;
+    r.norm_w = bin->norm_w;
+    r.norm_eps = bin->eps;
+    r.norm_pow = bin->pow_form;
+    r.xn_out = d->quant == HH_QUANT_MXFP4 ? nullptr : const_cast<uint16_t *>(x);
+  }
   hh::Timing tm;
   rc = phase_timing(ctx, &tm, noalloc);
   if (rc) return rc;
@@ -705,13 +721,23 @@ int hh_moe_block_forward(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights
   uint8_t *base = ctx->arena;
   uint16_t *xn = (uint16_t *)(base + o_xn);
   uint16_t *xr = router_resid ? (uint16_t *)(base + o_xr) : nullptr;
-  HH_HIP(hh::launch_block_norm(hidden, nm->pre_norm, d->hidden, nm->eps, router_resid ? 1 : 0, T,
-                               xn, xr, ctx->stream));
-  ctx->dispatches += 1;
+  // Up to 16 tokens with a bf16 (non-GEMMA) router and H ≤ 4096, the router kernel forms the layer
+  // input itself (one launch fewer); otherwise a norm kernel writes it first. Both round the same
+  // fp64 values (row_sumsq's canonical sum).
+  const BlockIn bin{hidden, nm->pre_norm, nm->eps, router_resid ? 1 : 0};
+  const bool fused = T <= kSmallT && w->router_bits == 0 && !router_resid && d->hidden <= 4096;
+  if (!fused) {
+    HH_HIP(hh::launch_block_norm(hidden, nm->pre_norm, d->hidden, nm->eps, router_resid ? 1 : 0, T,
+                                 xn, xr, ctx->stream));
+    ctx->dispatches += 1;
+  }
   if (!gemma)
-    return forward_layer(ctx, d, w, xn, xr, T, hidden, topk_idx, topk_w, base, s, false, hidden);
+    return forward_layer(ctx, d, w, xn, xr, T, hidden, topk_idx, topk_w, base, s, false, hidden,
+                         fused ? &bin : nullptr);
   float *mix = (float *)(base + o_mix);
-  if ((rc = forward_layer(ctx, d, w, xn, xr, T, mix, topk_idx, topk_w, base, s, false))) return rc;
+  if ((rc = forward_layer(ctx, d, w, xn, xr, T, mix, topk_idx, topk_w, base, s, false, nullptr,
+                          fused ? &bin : nullptr)))
+    return rc;
   HH_HIP(hh::launch_block_gemma_finish(hidden, mix, dense_out, nm->post_dense_norm,
                                        nm->post_expert_norm, nm->post_norm, nm->layer_scalar,
                                        d->hidden, nm->eps, T, ctx->stream));

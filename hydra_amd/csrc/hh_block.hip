@@ -12,23 +12,9 @@
 // Arithmetic: every reduction and product is fp64 (squares of fp32 values are exact in fp64), as
 // in the fp64 reference; the bf16 layer input is the fp64 value rounded once to bf16.
 #include "hh_common.hpp"
+#include "hh_norm.hpp"
 
 namespace hh {
-
-// fp64 → bf16 bits, round to nearest even, one rounding: the value is first narrowed to fp32
-// with round-to-odd (truncate, then set the last bit when inexact), which keeps the information
-// a later rounding to 8 significant bits needs, then rounded to bf16 by RNE.
-__device__ __forceinline__ uint32_t f64_to_bf16_bits(double v) {
-  float f = (float)v;
-  if (f != f) return f32_to_bf16_bits(f);
-  const double back = (double)f;
-  if (back != v) {
-    uint32_t b = __float_as_uint(f);
-    if (fabs(back) > fabs(v)) b -= 1;   // the truncation: one step toward zero
-    f = __uint_as_float(b | 1u);
-  }
-  return f32_to_bf16_bits(f);
-}
 
 constexpr int kBlockThreads = 256;
 
@@ -45,32 +31,14 @@ __device__ __forceinline__ double block_sum_f64(double v, double *s_red) {
   return t;
 }
 
-// The norm's factor (mean(x²) + eps)^-½ in the family's form: 1/√(·) (ReferenceOps.rmsNorm) or
-// pow(·, -½) (Gemma4ReferenceOps.rmsNorm).
-__device__ __forceinline__ double norm_factor(double sumsq, int H, double eps, int pow_form) {
-  const double m = sumsq / (double)H + eps;
-  return pow_form ? pow(m, -0.5) : 1.0 / sqrt(m);
-}
-
-// One workgroup per token: xn[t] = bf16(hidden[t]·f·w) (the layer's expert and router input),
-// and, when xr is given, xr[t] = bf16(hidden[t]) (the residual the GEMMA router reads).
-__global__ __launch_bounds__(kBlockThreads) void block_norm_kernel(
-    const float *hidden, const uint16_t *weight, int H, float eps, int pow_form, uint16_t *xn,
-    uint16_t *xr) {
-  __shared__ double s_red[kBlockThreads / 64];
+// One wave per token: xn[t] = bf16(hidden[t]·f·w) (the layer's expert and router input), and,
+// when xr is given, xr[t] = bf16(hidden[t]) (the residual the GEMMA router reads). The same
+// arithmetic as the small-batch router kernel's own rows (norm_row_bf16).
+__global__ __launch_bounds__(64) void block_norm_kernel(const float *hidden, const uint16_t *weight,
+                                                        int H, float eps, int pow_form, uint16_t *xn,
+                                                        uint16_t *xr) {
   const size_t t = blockIdx.x;
-  const float *x = hidden + t * H;
-  double ss = 0.0;
-  for (int h = threadIdx.x; h < H; h += kBlockThreads) {
-    const double v = x[h];
-    ss += v * v;
-  }
-  const double f = norm_factor(block_sum_f64(ss, s_red), H, (double)eps, pow_form);
-  for (int h = threadIdx.x; h < H; h += kBlockThreads) {
-    const double v = x[h];
-    xn[t * H + h] = (uint16_t)f64_to_bf16_bits(v * f * (double)bf16_bits_to_f32(weight[h]));
-    if (xr) xr[t * H + h] = (uint16_t)f32_to_bf16_bits(x[h]);
-  }
+  norm_row_bf16(hidden + t * H, weight, H, eps, pow_form, xn + t * H, xr ? xr + t * H : nullptr);
 }
 
 // One workgroup per token, Gemma's parallel branches:
@@ -112,8 +80,8 @@ __global__ __launch_bounds__(kBlockThreads) void block_gemma_finish_kernel(
 
 hipError_t launch_block_norm(const float *hidden, const uint16_t *weight, int H, float eps,
                              int pow_form, int T, uint16_t *xn, uint16_t *xr, hipStream_t s) {
-  hipLaunchKernelGGL(block_norm_kernel, dim3(T), dim3(kBlockThreads), 0, s, hidden, weight, H,
-                     eps, pow_form, xn, xr);
+  hipLaunchKernelGGL(block_norm_kernel, dim3(T), dim3(64), 0, s, hidden, weight, H, eps,
+                     pow_form, xn, xr);
   return hipGetLastError();
 }
 

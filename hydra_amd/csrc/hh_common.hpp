@@ -182,6 +182,14 @@ struct RouteArgs {
   const uint16_t *sg_scales, *sg_biases;
   int32_t tokens, hidden, experts, top_k, slots, router, tile_tokens, want_dispatch;
   float eps;
+  // FFN block, batches of ≤ 16 tokens with a bf16 router: the router kernel forms the layer input
+  // itself from the fp32 residual stream, rmsnorm(resid)·norm_w rounded to bf16 (norm_row_bf16),
+  // and writes it to xn_out for the expert products (non-MXFP4 layers); null otherwise.
+  const float *resid;
+  const uint16_t *norm_w;
+  float norm_eps;
+  int32_t norm_pow;
+  uint16_t *xn_out;
   double *logits;               // fp64 [T][K] exact logits of the selected experts, or null
   double *lg64;                 // fp64 [T][E+1] exact logits (batches of ≤ 16 tokens, or any batch with an MLX router; column E: shared gate)
   uint8_t *xq, *xs;             // MXFP4 layers: x as fp8 terms (GemmArgs::xq), or null

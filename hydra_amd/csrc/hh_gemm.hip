@@ -1184,6 +1184,8 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
   const uint8_t *blob = grp.blobs + (gsel ? 0 : (size_t)e * grp.stride);
   const int I = grp.inter;
   const int rb = rt * 16;
+  // The residual of the item's 16 rows (FFN block), loaded ahead of the weight stream.
+  const float rv = (a.resid && tid < 16) ? a.resid[(size_t)t * H + rb + tid] : 0.f;
 
   ATile<FMT> at[NM];
   wave_tiles<PH_DOWN, FMT, 1>(at, blob, grp, rb, H, I, l16);
@@ -1285,7 +1287,7 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
     float y = s_o[0][tid];
     for (int qq = 1; qq < S; ++qq) y += s_o[qq][tid];
     const size_t o = (size_t)t * H + rb + tid;
-    if (a.resid) y = a.resid[o] + y;
+    if (a.resid) y = rv + y;
     a.y[o] = y;
   }
   __syncthreads();   // the next item rewrites the LDS rows and s_o

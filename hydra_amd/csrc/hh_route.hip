@@ -27,6 +27,9 @@
 #include "hh_common.hpp"
 #include "hh_select.hpp"
 #include "hh_logit.hpp"
+#include "hh_norm.hpp"
+
+#include <mutex>
 
 namespace hh {
 
@@ -437,6 +440,104 @@ __global__ __launch_bounds__(256) void quant_x_kernel(RouteArgs a) {
 // would take several microseconds to stream even a 32-expert router); expert id E is the shared
 // expert's gate row. Writes lg64 [T][E+1].
 // Waves past the logits quantise x (MXFP4 layers).
+// FFN block (a.resid set, bf16 router, H ≤ 4096): the layer input x = bf16(resid·f·norm_w) of
+// token t, formed in registers in the canonical row layout (row_sumsq's), and its exact logit
+// against row `wrow` in exact_logit's arithmetic (bf16·bf16 products exact in fp32, added in fp64
+// per u, (acc0 + acc1) + (acc2 + acc3), wave sum): the values the block's norm kernel followed by
+// exact_logit give. All loads (residual row, norm weights, projection row) go out together. When
+// xn_out is given the lanes also store x there.
+__device__ __forceinline__ double block_pair_logit(const RouteArgs &a, int t, const uint16_t *wrow,
+                                                   uint16_t *xn_out) {
+  const int lane = threadIdx.x & 63, H = a.hidden;
+  const float *x = a.resid + (size_t)t * H;
+  f32x4 xv[2][4][2];
+  u32x4 nv[2][4], wv[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int h = 2048 * i + 512 * u + 8 * lane;
+      const int hc = min(h, H - 8);
+      xv[i][u][0] = *(const f32x4 *)(x + hc);
+      xv[i][u][1] = *(const f32x4 *)(x + hc + 4);
+      nv[i][u] = *(const u32x4 *)(a.norm_w + hc);
+      wv[i][u] = *(const u32x4 *)(wrow + hc);
+      if (h >= H) {
+        xv[i][u][0] = xv[i][u][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        wv[i][u] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  double ss = 0.0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (2048 * i >= H) break;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const double d = xv[i][u][k >> 2][k & 3];
+        ss += d * d;
+      }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  const double f = norm_factor(ss, H, (double)a.norm_eps, a.norm_pow);
+  double acc[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (2048 * i >= H) break;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      uint32_t xb[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t nb = (nv[i][u][k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+        xb[k] = f64_to_bf16_bits((double)xv[i][u][k >> 2][k & 3] * f * (double)bf16_bits_to_f32(nb));
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float xf = bf16_bits_to_f32(xb[k]);
+        const float wf = bf16_bits_to_f32((wv[i][u][k >> 1] >> (16 * (k & 1))) & 0xFFFFu);
+        acc[u] += (double)(xf * wf);
+      }
+      const int h = 2048 * i + 512 * u + 8 * lane;
+      if (xn_out && h < H)
+        *(u32x4 *)(xn_out + (size_t)t * H + h) =
+            u32x4{xb[0] | (xb[1] << 16), xb[2] | (xb[3] << 16), xb[4] | (xb[5] << 16), xb[6] | (xb[7] << 16)};
+    }
+  }
+  return wave_sum_f64((acc[0] + acc[1]) + (acc[2] + acc[3]));
+}
+
+// The FFN block's x terms (MXFP4 layers): as quant_x_wave over token t's layer input, formed
+// from the residual stream (norm factor from the whole row, values rounded as norm_row_bf16).
+__device__ __forceinline__ void quant_x_wave_block(const RouteArgs &a, int t, int blk0) {
+  const int lane = threadIdx.x & 63, g = lane >> 4, l16 = lane & 15;
+  const int H = a.hidden, nb = H / 32;
+  const int b = blk0 + l16, bc = min(b, nb - 1);
+  const float *x = a.resid + (size_t)t * H;
+  const int c0 = bc * 32 + 8 * g;
+  const f32x4 x0 = *(const f32x4 *)(x + c0), x1 = *(const f32x4 *)(x + c0 + 4);
+  const u32x4 nw = *(const u32x4 *)(a.norm_w + c0);
+  const double f = norm_factor(row_sumsq(x, H), H, (double)a.norm_eps, a.norm_pow);
+  float v[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t nbits = (nw[k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
+    const float xv = k < 4 ? x0[k] : x1[k - 4];
+    v[k] = bf16_bits_to_f32(f64_to_bf16_bits((double)xv * f * (double)bf16_bits_to_f32(nbits)));
+  }
+  uint32_t q[NTX][2], sb[NTX];
+  quant_block<NTX>(v, q, sb);
+  if (b < nb) {
+#pragma unroll
+    for (int j = 0; j < NTX; ++j) {
+      *(u32x2 *)(a.xq + ((size_t)t * NTX + j) * a.xld + b * 32 + 8 * g) = u32x2{q[j][0], q[j][1]};
+      if (g == 0) a.xs[((size_t)t * NTX + j) * (a.xld / 32) + b] = (uint8_t)sb[j];
+    }
+  }
+}
+
 template <bool gemma>
 __global__ __launch_bounds__(256) void logits_small_kernel(RouteArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -446,13 +547,22 @@ __global__ __launch_bounds__(256) void logits_small_kernel(RouteArgs a) {
     const int w = p - a.tokens * E1;
     if (w < quant_x_waves(a)) {
       const int per_t = (H / 32 + 15) / 16;
-      quant_x_wave(a, w / per_t, 16 * (w % per_t));
+      if (!gemma && a.resid) quant_x_wave_block(a, w / per_t, 16 * (w % per_t));
+      else quant_x_wave(a, w / per_t, 16 * (w % per_t));
     }
     return;
   }
   const int t = p / E1, e = p - t * E1;
   if (e == E && !a.shared_gate) return;
-  const double v = pair_logit<gemma>(a, t, e);
+  double v;
+  if (!gemma && a.resid) {
+    // The FFN block: the (t, 0) wave also stores the layer input for the expert products.
+    v = block_pair_logit(a, t, e < E ? a.router_w + (size_t)e * H : a.shared_gate,
+                         e == 0 ? a.xn_out : nullptr);
+    if (e < E && a.router_b) v += (double)bf16_bits_to_f32(a.router_b[e]);
+  } else {
+    v = pair_logit<gemma>(a, t, e);
+  }
   if (lane == 0) a.lg64[(size_t)t * E1 + e] = v;
 }
 
@@ -589,7 +699,8 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s, Timing tm) {
     // here.
     const int waves = a.tokens * (a.experts + 1) + (a.xq ? a.tokens * ((a.hidden / 32 + 15) / 16) : 0);
     const bool sel = a.want_dispatch == 0;
-    hipExtLaunchKernelGGL(a.router == R_GEMMA ? logits_small_kernel<true> : logits_small_kernel<false>,
+    const bool g = a.router == R_GEMMA;
+    hipExtLaunchKernelGGL(g ? logits_small_kernel<true> : logits_small_kernel<false>,
                           dim3((waves + 3) / 4), dim3(256), 0, s, tm.start, sel ? nullptr : tm.stop,
                           0, a);
     hipError_t e = hipGetLastError();
