@@ -279,18 +279,21 @@ def shared_bytes(desc: F.MoEDesc) -> int:
     return F.streamed_expert_bytes(desc, desc.shared_intermediate) + desc.hidden * 2
 
 
-def measure_other(torch, name, desc, copies, T_prefill, steps):
-    """Decode T=1 and one chunked prefill of another format: whole-layer tokens/s, layer GB/s
-    on the bytes touched (distinct routed experts + shared expert + router), expert-product
-    TFLOP/s for the prefill."""
-    log(f"{name}: decode T=1, prefill T={T_prefill}")
+def measure_other(torch, name, desc, copies, T_prefill, steps, prefill=True):
+    """Decode T=1 and T=8 and one chunked prefill of another format: whole-layer tokens/s,
+    layer GB/s on the bytes touched (distinct routed experts + shared expert + router),
+    expert-product TFLOP/s for the prefill."""
+    log(f"{name}: decode T=1 and 8, prefill T={T_prefill}")
     wl = Workload(torch, desc, copies=copies)
-    d = measure_decode(wl, 1, steps, 20)
-    d["layer_GBps"] += shared_bytes(desc) / (d["ms_per_step"] * 1e-3) / 1e9
-    d["layer_hbm_frac"] = d["layer_GBps"] / HBM_PEAK_GBS
-    p = measure_prefill(wl, T_prefill, 10, 3)
+    dec = {}
+    for T in (1, 8):
+        d = measure_decode(wl, T, steps if T == 1 else max(50, steps // 4), 20)
+        d["layer_GBps"] += shared_bytes(desc) / (d["ms_per_step"] * 1e-3) / 1e9
+        d["layer_hbm_frac"] = d["layer_GBps"] / HBM_PEAK_GBS
+        dec[str(T)] = d
+    p = measure_prefill(wl, T_prefill, 10, 3) if prefill else None
     wl.close()
-    return {"decode": {"1": d}, "prefill": {str(T_prefill): p}}
+    return {"decode": dec, "prefill": {str(T_prefill): p} if p else {}}
 
 
 def cpu_baseline(runs=5, seconds=2.5):
@@ -390,7 +393,8 @@ def main():
         return
     if args.only_other:
         name, desc, copies, Tp = next(o for o in OTHER if o[0] == args.only_other)
-        print(json.dumps({name: measure_other(torch, name, desc, copies, Tp, args.steps)}))
+        print(json.dumps({name: measure_other(torch, name, desc, copies, Tp, args.steps,
+                                              prefill=not args.no_prefill)}))
         return
     decode, fused, stack = {}, {}, {}
     if not args.only_prefill:

@@ -562,27 +562,17 @@ __device__ __forceinline__ void stage_batch(int base, int id, int threads, int n
 }
 
 // ---- decode prologue -----------------------------------------------------------------------------
-// The expert of a decode workgroup and its tokens, from the exact fp64 logits: every workgroup
-// selects the top-k of every token of the batch itself (wave w: tokens w, w + NW, ...), so the
-// decode step needs no selection or dispatch launch; workgroup 0 also writes the routing outputs.
-// Routed workgroup u takes the u-th entry of the (token, rank) table whose expert does not appear
-// earlier in it; the shared workgroup takes every token. Returns false when the workgroup has no
-// expert (uniform over the workgroup).
-struct SmallPick {
-  int e;          // expert id (E = the shared expert)
-  uint64_t tm;    // its tokens, bit t
-  int ntok;
-};
-
+// Every decode gate-up workgroup selects the top-k of every token of the batch itself from the
+// exact fp64 logits (wave w: tokens w, w + NW, ...) into s_idx [T][K], so the decode step needs no
+// selection or dispatch launch; workgroup 0 also writes the routing outputs.
 template <int NW>
-__device__ __forceinline__ bool small_pick(const GemmArgs &a, const RouteArgs &ra, int u, bool shared_wg,
-                                           int *s_idx, SmallPick &pk) {
+__device__ __forceinline__ void select_batch(const GemmArgs &a, const RouteArgs &ra, int *s_idx) {
   __shared__ double s_lg[NW][64];
   __shared__ int s_ri[NW][kMaxTopK];
   __shared__ int s_ci[NW][kFastCand];
   __shared__ double s_cv[NW][kFastCand];
   __shared__ double s_rv[NW][kMaxTopK];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int T = ra.tokens, E = a.experts, K = a.top_k;
   const bool has_shared = a.slots > K;
   for (int t = wave; t < T; t += NW) {
@@ -593,37 +583,6 @@ __device__ __forceinline__ bool small_pick(const GemmArgs &a, const RouteArgs &r
     if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
   }
   __syncthreads();
-  int e = E;
-  if (!shared_wg) {
-    const int n = T * K;   // ≤ 128: entries lane and lane + 64
-    bool first[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int i = lane + 64 * h;
-      first[h] = i < n;
-      if (i < n) {
-        const int ei = s_idx[i];
-        for (int j = 0; j < i; ++j) first[h] = first[h] && s_idx[j] != ei;
-      }
-    }
-    const uint64_t m0 = __ballot(first[0]), m1 = __ballot(first[1]);
-    const int n0 = __popcll(m0);
-    if (u >= n0 + __popcll(m1)) return false;
-    uint64_t mm = u < n0 ? m0 : m1;
-    for (int k = u < n0 ? u : u - n0; k > 0; --k) mm &= mm - 1;
-    e = s_idx[__ffsll((long long)mm) - 1 + (u < n0 ? 0 : 64)];
-  }
-  int r_t = -1;
-  if (lane < T) {
-    if (shared_wg) r_t = K;
-    else
-      for (int r = 0; r < K; ++r)
-        if (s_idx[lane * K + r] == e) r_t = r;
-  }
-  pk.e = e;
-  pk.tm = __ballot(r_t >= 0);
-  pk.ntok = __popcll(pk.tm);
-  return true;
 }
 
 // The j-th set bit of m.
@@ -631,6 +590,61 @@ __device__ __forceinline__ int nth_bit(uint64_t m, int j) {
   for (int k = 0; k < j; ++k) m &= m - 1;
   return __ffsll((long long)m) - 1;
 }
+
+// The decode plan, computed by every wave in registers from the batch's top-k table s_idx
+// [T][K] (LDS): the distinct experts in order of first appearance in (token, rank) order and
+// the tokens of each. Lane l holds entries l and 64 + l (T·K ≤ 128).
+struct Plan {
+  int pe[2];
+  bool pf[2];
+  uint64_t ptm[2];
+  uint64_t m0, m1;
+  int n0, nu, E, T;
+  __device__ __forceinline__ Plan(const int *s_idx, int T_, int K, int E_) : E(E_), T(T_) {
+    const int lane = threadIdx.x & 63, n = T * K;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      pe[h] = lane + 64 * h < n ? s_idx[lane + 64 * h] : -1;
+      pf[h] = lane + 64 * h < n;
+      ptm[h] = 0ull;
+    }
+    for (int j = 0, tj = 0, rj = 0; j < n; ++j) {
+      const int ej = __builtin_amdgcn_readlane(j < 64 ? pe[0] : pe[1], j & 63);
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        if (ej == pe[h]) {
+          if (j < lane + 64 * h) pf[h] = false;
+          ptm[h] |= 1ull << tj;
+        }
+      if (++rj == K) { rj = 0; ++tj; }
+    }
+    m0 = __ballot(pf[0]);
+    m1 = __ballot(pf[1]);
+    n0 = __popcll(m0);
+    nu = n0 + __popcll(m1);
+  }
+  // Distinct expert u (< nu) and its token mask; u ≥ nu is the shared expert, every token.
+  __device__ __forceinline__ void entry(int u, int &e, uint64_t &tm) const {
+    if (u >= nu) {
+      e = E;
+      tm = (1ull << T) - 1ull;
+      return;
+    }
+    const int h = u < n0 ? 0 : 1;
+    const int l = nth_bit(h ? m1 : m0, h ? u - n0 : u);
+    const int ev = h ? pe[1] : pe[0];
+    const uint64_t tv = h ? ptm[1] : ptm[0];
+    e = __builtin_amdgcn_readlane(ev, l);
+    tm = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(tv >> 32), l) << 32) |
+         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tv, l);
+  }
+  // Plan index of routed expert e (wave-uniform; e must occur in the table).
+  __device__ __forceinline__ int index_of(int e) const {
+    const uint64_t h0 = __ballot(pf[0] && pe[0] == e), h1 = __ballot(pf[1] && pe[1] == e);
+    if (h0) return __popcll(m0 & ((1ull << (__ffsll((unsigned long long)h0) - 1)) - 1ull));
+    return n0 + __popcll(m1 & ((1ull << (__ffsll((unsigned long long)h1) - 1)) - 1ull));
+  }
+};
 
 // Rank of expert e in token t's selection (the shared expert is rank K).
 __device__ __forceinline__ int rank_of(const int *s_idx, int t, int e, int K, bool shared) {
@@ -666,11 +680,13 @@ constexpr int MX_PF = HH_MX_PF;   // chunks a single-round MXFP4 decode wave iss
 constexpr int kFusedMaxE = 128;   // experts of layers that take the fused decode kernel
 constexpr int LDS_PAD = 8;        // bf16 elements of padding per staged row (bank spread)
 
-// Grid: row tile rt (16·TPW intermediates) × u, u < min(E, T·K) the distinct routed experts of
-// the batch, and the last u the shared expert when there is one. 4·TPW waves: wave w takes tile
-// q (16 intermediates; w & 1 when TPW = 2), gate or up rows, and chunk parity p (the even or odd
-// chain of the canonical arithmetic). TPW = 1 gives twice the workgroups of half the size, which
-// spreads a decode step's few experts over more compute units.
+// Persistent: work items (row tile rt of 16·TPW intermediates, u) with u < nu the batch's
+// distinct routed experts in order of first appearance in the (token, rank) table and u = nu the
+// shared expert when there is one; item it = blockIdx.x, blockIdx.x + gridDim.x, ... Every
+// workgroup selects the batch's top-k once (at T = 1 the grid holds one workgroup per item).
+// 4·TPW waves: wave w takes tile q (16 intermediates; w & 1 when TPW = 2), gate or up rows, and
+// chunk parity p (the even or odd chain of the canonical arithmetic). TPW = 1 gives twice the
+// workgroups of half the size, which spreads a decode step's few experts over more compute units.
 template <int FMT, int DA, int TPW = 2>
 __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) {
   constexpr int NTH = 256 * TPW, NWV = 4 * TPW, ROWS = 16 * TPW;
@@ -683,15 +699,10 @@ __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, l16 = lane & 15;
   const int T = ra.tokens, E = a.experts, K = a.top_k, S = a.slots, H = a.hidden;
-  const int rt = blockIdx.x % a.row_tiles, u = blockIdx.x / a.row_tiles;
   const bool has_shared = S > K;
-  const bool shared_wg = has_shared && u == (int)(gridDim.x / a.row_tiles) - 1;
-  const ExpertGroup &grp = a.grp[shared_wg ? 1 : 0];
-  const int I = grp.inter;
-  if (rt * ROWS >= I) return;                        // whole workgroup past this group's rows
 
   // Every token's x into LDS (row t), independent of the routing: the first batch of loads
-  // goes out before the selection.
+  // goes out before the selection and is stored with the first item.
   const int ldx = H + LDS_PAD;
   const int per_row = H / 8, nvec = T * per_row;
   auto xsrc = [&](int v) {
@@ -708,50 +719,65 @@ __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) 
   for (int k = 0; k < XB; ++k)
     if (tid + NTH * k < nvec) xr[k] = xsrc(tid + NTH * k);
   HH_TR(1, 0);
-  SmallPick pk;
-  if (!small_pick<NWV>(a, ra, u, shared_wg, s_idx, pk)) return;   // uniform over the workgroup
+  select_batch<NWV>(a, ra, s_idx);
   HH_TR(1, 1);
-  const int e = pk.e, ntok = pk.ntok;
-  const uint64_t tm = pk.tm;
-  const uint8_t *blob = grp.blobs + (shared_wg ? 0 : (size_t)e * grp.stride);
+  const Plan plan(s_idx, T, K, E);
+  const int rtr = (a.grp[0].inter + ROWS - 1) / ROWS;
+  const int nitems = plan.nu * rtr + (has_shared ? (a.grp[1].inter + ROWS - 1) / ROWS : 0);
 
   const int q = TPW == 2 ? (wave & 1) : 0;
   const bool is_up = TPW == 2 ? (wave & 2) != 0 : (wave & 1) != 0;
   const int par = TPW == 2 ? wave >> 2 : wave >> 1;
-  const int rb = rt * ROWS + 16 * q;
-  ATile<FMT> at[NM] = {tile_of<PH_UP, FMT>(blob, grp, rb, is_up, H, l16)};
   const int nch = (H + Fmt<FMT>::CHUNK - 1) / Fmt<FMT>::CHUNK;
-  auto token_of = [&](int j) { return nth_bit(tm, j); };
-  // The weight stream, then the x stores (which wait for the x loads only) and any further batches.
-  AStream<FMT, NM, DA> as(par, 2, nch);
-  as.fill(at, nch, g, H);
+  bool x_pending = true;
+  for (int it = blockIdx.x; it < nitems; it += gridDim.x) {
+    const bool sh = it >= plan.nu * rtr;
+    const int u = sh ? plan.nu : it / rtr;
+    const int rt = sh ? it - plan.nu * rtr : it % rtr;
+    int e;
+    uint64_t tm;
+    plan.entry(u, e, tm);
+    const int ntok = __popcll(tm);
+    const ExpertGroup &grp = a.grp[sh ? 1 : 0];
+    const uint8_t *blob = grp.blobs + (sh ? 0 : (size_t)e * grp.stride);
+    const int rb = rt * ROWS + 16 * q;
+    ATile<FMT> at[NM] = {tile_of<PH_UP, FMT>(blob, grp, rb, is_up, H, l16)};
+    // The weight stream, then (first item) the x stores, which wait for the x loads only, and
+    // any further batches.
+    AStream<FMT, NM, DA> as(par, 2, nch);
+    as.fill(at, nch, g, H);
+    if (x_pending) {
 #pragma unroll
-  for (int k = 0; k < XB; ++k)
-    if (tid + NTH * k < nvec) xdst(tid + NTH * k, xr[k]);
-  for (int base = NTH * XB; base < nvec; base += NTH * 4) stage_batch<4>(base, tid, NTH, nvec, xsrc, xdst);
-  __syncthreads();
-  HH_TR(1, 2);
+      for (int k = 0; k < XB; ++k)
+        if (tid + NTH * k < nvec) xdst(tid + NTH * k, xr[k]);
+      for (int base = NTH * XB; base < nvec; base += NTH * 4) stage_batch<4>(base, tid, NTH, nvec, xsrc, xdst);
+      x_pending = false;
+    }
+    __syncthreads();
+    if (it == (int)blockIdx.x) HH_TR(1, 2);
 
-  // Token column l16 = the l16-th token of the expert (padding columns repeat the last one).
-  const int my_t = token_of(min(l16, ntok - 1));
-  const uint16_t *brow = s_x + (size_t)my_t * ldx;
-  f32x4 acc[NM][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
-  as.run(at, nch, g, H, [&](const typename Fmt<FMT>::A (&w)[NM], int c) {
-    const int col = Fmt<FMT>::bcol(c, g, H);
-    chunk_mfma<FMT, NM, 1, 1>(acc, w, at, [&](int, int, int v) { return *(const u32x4 *)(brow + col + Fmt<FMT>::VS * v); },
-                              c, g, H);
-  });
-  // Chains and gate/up meet in the (gate, even) wave of each tile.
-  const int slot_of_part = (is_up ? 1 : 0) * 2 + par;   // 0: gate even (keeps), 1: gate odd, 2: up even, 3: up odd
-  if (slot_of_part > 0) s_part[slot_of_part - 1][q][lane] = acc[0][0];
-  __syncthreads();
-  HH_TR(1, 3);
-  if (slot_of_part == 0 && l16 < ntok) {
-    const int r = rank_of(s_idx, my_t, e, K, shared_wg);
-    up_epilogue<FMT>(a, blob, grp, rb + 4 * g, my_t * S + r, sum_chains(acc[0][0], s_part[0][q][lane]),
-                     sum_chains(s_part[1][q][lane], s_part[2][q][lane]));
+    // Token column l16 = the l16-th token of the expert (padding columns repeat the last one).
+    const int my_t = nth_bit(tm, min(l16, ntok - 1));
+    const uint16_t *brow = s_x + (size_t)my_t * ldx;
+    f32x4 acc[NM][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
+    as.run(at, nch, g, H, [&](const typename Fmt<FMT>::A (&w)[NM], int c) {
+      const int col = Fmt<FMT>::bcol(c, g, H);
+      chunk_mfma<FMT, NM, 1, 1>(acc, w, at, [&](int, int, int v) { return *(const u32x4 *)(brow + col + Fmt<FMT>::VS * v); },
+                                c, g, H);
+    });
+    // Chains and gate/up meet in the (gate, even) wave of each tile. The next item's partials
+    // are written only after its first barrier, which this item's epilogue wave reaches last.
+    const int slot_of_part = (is_up ? 1 : 0) * 2 + par;   // 0: gate even (keeps), 1: gate odd, 2: up even, 3: up odd
+    if (slot_of_part > 0) s_part[slot_of_part - 1][q][lane] = acc[0][0];
+    __syncthreads();
+    if (it == (int)blockIdx.x) HH_TR(1, 3);
+    if (slot_of_part == 0 && l16 < ntok) {
+      const int r = rank_of(s_idx, my_t, e, K, sh);
+      up_epilogue<FMT>(a, blob, grp, rb + 4 * g, my_t * S + r, sum_chains(acc[0][0], s_part[0][q][lane]),
+                       sum_chains(s_part[1][q][lane], s_part[2][q][lane]));
+    }
+    if (it == (int)blockIdx.x) HH_TR(1, 4);
   }
-  HH_TR(1, 4);
 }
 
 // ---- MXFP4 on the scaled MFMA -------------------------------------------------------------------
@@ -944,61 +970,6 @@ __device__ __forceinline__ MxStage<NTERM, NB, RowOf, DEV> mx_stage(uint8_t *dst,
                                                                     int threads) {
   return MxStage<NTERM, NB, RowOf, DEV>(dst, q, sc, ld, cols, nrows, row_of, id, threads);
 }
-
-// The decode plan, computed by every wave in registers from the batch's top-k table s_idx
-// [T][K] (LDS): the distinct experts in order of first appearance in (token, rank) order and
-// the tokens of each. Lane l holds entries l and 64 + l (T·K ≤ 128).
-struct Plan {
-  int pe[2];
-  bool pf[2];
-  uint64_t ptm[2];
-  uint64_t m0, m1;
-  int n0, nu, E, T;
-  __device__ __forceinline__ Plan(const int *s_idx, int T_, int K, int E_) : E(E_), T(T_) {
-    const int lane = threadIdx.x & 63, n = T * K;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      pe[h] = lane + 64 * h < n ? s_idx[lane + 64 * h] : -1;
-      pf[h] = lane + 64 * h < n;
-      ptm[h] = 0ull;
-    }
-    for (int j = 0, tj = 0, rj = 0; j < n; ++j) {
-      const int ej = __builtin_amdgcn_readlane(j < 64 ? pe[0] : pe[1], j & 63);
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-        if (ej == pe[h]) {
-          if (j < lane + 64 * h) pf[h] = false;
-          ptm[h] |= 1ull << tj;
-        }
-      if (++rj == K) { rj = 0; ++tj; }
-    }
-    m0 = __ballot(pf[0]);
-    m1 = __ballot(pf[1]);
-    n0 = __popcll(m0);
-    nu = n0 + __popcll(m1);
-  }
-  // Distinct expert u (< nu) and its token mask; u ≥ nu is the shared expert, every token.
-  __device__ __forceinline__ void entry(int u, int &e, uint64_t &tm) const {
-    if (u >= nu) {
-      e = E;
-      tm = (1ull << T) - 1ull;
-      return;
-    }
-    const int h = u < n0 ? 0 : 1;
-    const int l = nth_bit(h ? m1 : m0, h ? u - n0 : u);
-    const int ev = h ? pe[1] : pe[0];
-    const uint64_t tv = h ? ptm[1] : ptm[0];
-    e = __builtin_amdgcn_readlane(ev, l);
-    tm = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(tv >> 32), l) << 32) |
-         (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)tv, l);
-  }
-  // Plan index of routed expert e (wave-uniform; e must occur in the table).
-  __device__ __forceinline__ int index_of(int e) const {
-    const uint64_t h0 = __ballot(pf[0] && pe[0] == e), h1 = __ballot(pf[1] && pe[1] == e);
-    if (h0) return __popcll(m0 & ((1ull << (__ffsll((unsigned long long)h0) - 1)) - 1ull));
-    return n0 + __popcll(m1 & ((1ull << (__ffsll((unsigned long long)h1) - 1)) - 1ull));
-  }
-};
 
 // Decode gate-up on the scaled MFMA, persistent: the grid holds about two workgroups per compute
 // unit; each selects the top-k of the batch once, lists the batch's distinct experts in LDS (in
@@ -2609,7 +2580,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   auto work_of = [&](int tau) {
     int rt, wi;
     prefill_tile(min(tau, tasks.lim - 1), RTL, rt, wi);
-    return a.work[wi];
+    return a.work[min(wi, nwork - 1)];
   };
   // A task's copy for the MFMA waves: its work item, then its slot ids.
   auto send_info = [&](int tau, const int4 &w, int slot) {
@@ -3131,8 +3102,10 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
   a.row_tiles = a.ldh / (mx ? UP_ROWS : 16);   // up_small: one 16-intermediate tile per workgroup
   const size_t lds_up = mx ? (size_t)T * NTX * mx_row_bytes(a.xld) + 64 * (a.hidden / 32)
                            : (size_t)T * (a.hidden + LDS_PAD) * 2;
-  // MXFP4: persistent, about two workgroups per compute unit.
-  const int up_grid = mx ? std::min(2 * ncu, a.row_tiles * maxu) : a.row_tiles * maxu;
+  // Persistent: about two workgroups per compute unit (MXFP4), or as many as the staged x rows
+  // leave room for in LDS, up to four (the others).
+  const int up_per_cu = mx ? 2 : (int)std::max<size_t>(1, std::min<size_t>(4, (size_t)(160 << 10) / lds_up));
+  const int up_grid = std::min(up_per_cu * ncu, a.row_tiles * maxu);
   hipExtLaunchKernelGGL(up, dim3(up_grid), dim3(256), lds_up, s, tm_up.start, tm_up.stop, 0, a, ra);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
