@@ -136,7 +136,7 @@ struct GemmArgs {
   int32_t ldh;                  // row stride (elements) of h_hi / h_lo; multiple of 64
   int32_t max_work;             // grid rows of work items
   int32_t row_tiles;            // workgroup row tiles along the output dimension
-  int32_t pad2;
+  int32_t xcd_rows;             // persistent prefill: row-tile parts P of the 8 XCDs (1, 2, 4, 8; 0 = 8)
   const uint16_t *x;            // bf16 [T][H]
   const int32_t *order;         // [positions] slot id (t·slots + r) of each permuted position (T > 16)
   const int4 *work;             // [max_work] {expert (E = shared), pos0, n, 0}

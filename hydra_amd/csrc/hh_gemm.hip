@@ -1863,16 +1863,32 @@ __device__ __forceinline__ void lds_load4(const void *g, uint8_t *l) {
   __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)l, 4, 0, 0);
 }
 
-// Task ids of one workgroup: τ = b, b + G, ... below 8·⌈RT/8⌉·n_work, skipping row tiles ≥ RT.
+// Task ids of one workgroup of a persistent prefill kernel: τ = b, b + G, ... (G a multiple of
+// 8, so τ mod 8 is the workgroup's XCD), skipping tasks past the row tiles or the work items.
+// The 8 XCDs form P row-tile parts × 8/P work-item parts: XCD x takes row tiles of part x mod P
+// and work items of part x / P, work item by work item (each item's row tiles consecutively).
+// An expert's slice of weight rows stays in the XCD's L2 across the expert's consecutive items,
+// and an item's operand rows are fetched by the P XCDs of its item part.
 struct Mx3Tasks {
-  int b, G, RT, lim;
+  int b, G, RT, nwork, P, rtp, nq, lim;
+  __device__ __forceinline__ Mx3Tasks(int b_, int G_, int RT_, int nwork_, int P_)
+      : b(b_), G(G_), RT(RT_), nwork(nwork_), P(P_ == 1 || P_ == 2 || P_ == 4 ? P_ : 8) {
+    rtp = (RT + P - 1) / P;
+    nq = (nwork + 8 / P - 1) / (8 / P);
+    lim = 8 * rtp * nq;
+  }
+  __device__ __forceinline__ void tile(int tau, int &rt, int &wi) const {
+    const int x = tau & 7, j = tau >> 3, q = j / rtp;
+    rt = (x & (P - 1)) * rtp + (j - q * rtp);
+    wi = (x / P) * nq + q;
+  }
   __device__ __forceinline__ int first() const { return fix(b); }
   __device__ __forceinline__ int next(int tau) const { return fix(tau + G); }
   __device__ __forceinline__ int fix(int tau) const {
     for (; tau < lim; tau += G) {
       int rt, wi;
-      prefill_tile(tau, RT, rt, wi);
-      if (rt < RT) return tau;
+      tile(tau, rt, wi);
+      if (rt < RT && wi < nwork) return tau;
     }
     return lim;
   }
@@ -1896,7 +1912,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const uint8_t *sbase = PH == PH_UP ? a.xs : a.hs;
   const int RT = a.row_tiles, rtx = (RT + 7) >> 3;
   const int nwork = *a.n_work;
-  const Mx3Tasks tasks{(int)blockIdx.x, (int)gridDim.x, RT, 8 * rtx * nwork};
+  const Mx3Tasks tasks((int)blockIdx.x, (int)gridDim.x, RT, nwork, a.xcd_rows);
   // Number of chunks this workgroup computes.
   int nsteps = 0;
   for (int tau = tasks.first(); tau < tasks.lim; tau = tasks.next(tau)) nsteps += nch;
@@ -1912,7 +1928,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // vmcnt tells it they have landed.
     auto fetch_info = [&](int tau, int slot) {
       int rt, wi;
-      prefill_tile(min(tau, tasks.lim - 1), RT, rt, wi);
+      tasks.tile(min(tau, tasks.lim - 1), rt, wi);
       lds_load4((const int *)(a.work + min(wi, nwork - 1)) + min(lane, 3), info + 256 * slot);
     };
     auto fetch_order = [&](int slot) {
@@ -1923,7 +1939,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const uint8_t *asrc[2 * RR], *bsrc[C::BPW], *bssrc, *scsrc;
     auto start_task = [&](int tau, int slot) {
       int rt, wi;
-      prefill_tile(tau, RT, rt, wi);
+      tasks.tile(tau, rt, wi);
       const int4 it = item_of(slot);
       const int r0 = rt * C::MR;
       const uint8_t *blob = grp.blobs + (size_t)it.x * grp.stride;
@@ -2032,7 +2048,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   uint16_t braw[NJ][4];   // bias bits of the lane's rows, loaded at the task's start, used at its end
   auto task_begin = [&]() {
     int rt, wi;
-    prefill_tile(tau, RT, rt, wi);
+    tasks.tile(tau, rt, wi);
     const int4 it = item_of(slot);
     r0 = rt * C::MR;
     ntok = it.z;
@@ -2218,7 +2234,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const uint8_t *sbase = PH == PH_UP ? a.xs : a.hs;
   const int RT = a.row_tiles, rtx = (RT + 7) >> 3;
   const int nwork = *a.n_work;
-  const Mx3Tasks tasks{(int)blockIdx.x, (int)gridDim.x, RT, 8 * rtx * nwork};
+  const Mx3Tasks tasks((int)blockIdx.x, (int)gridDim.x, RT, nwork, a.xcd_rows);
   int nsteps = 0;
   for (int tau = tasks.first(); tau < tasks.lim; tau = tasks.next(tau)) nsteps += nch;
   if (nsteps == 0) return;
@@ -2230,7 +2246,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int lw = wave - 4;
     auto fetch_info = [&](int tau, int slot) {
       int rt, wi;
-      prefill_tile(min(tau, tasks.lim - 1), RT, rt, wi);
+      tasks.tile(min(tau, tasks.lim - 1), rt, wi);
       lds_load4((const int *)(a.work + min(wi, nwork - 1)) + min(lane, 3), info + 256 * slot);
     };
     // Slot ids and the tile rows' bias of a task whose work item has landed.
@@ -2238,7 +2254,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       const int4 it = item_of(slot);
       lds_load4(a.order + it.y + min(lane, it.z - 1), order + 256 * slot);
       int rt, wi;
-      prefill_tile(min(tau, tasks.lim - 1), RT, rt, wi);
+      tasks.tile(min(tau, tasks.lim - 1), rt, wi);
       const uint8_t *bp = grp.blobs + (size_t)it.x * grp.stride + grp.off[PH == PH_UP ? 2 : 5];
 #pragma unroll
       for (int k = 0; k < 2; ++k)
@@ -2247,7 +2263,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const uint8_t *bsrc[C::BPW], *bssrc, *scsrc;
     auto start_task = [&](int tau, int slot) {
       int rt, wi;
-      prefill_tile(tau, RT, rt, wi);
+      tasks.tile(tau, rt, wi);
       const int4 it = item_of(slot);
       const int r0 = rt * C::MR;
       const uint8_t *wsc = grp.blobs + (size_t)it.x * grp.stride + grp.off[PH == PH_UP ? 1 : 4];
@@ -2339,7 +2355,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const uint8_t *arow[NJ];
   auto la_rows = [&]() {
     int rt, wi;
-    prefill_tile(la_tau, RT, rt, wi);
+    tasks.tile(la_tau, rt, wi);
     const int4 it = item_of(la_slot);
     const uint8_t *wblk = grp.blobs + (size_t)it.x * grp.stride + grp.off[PH == PH_UP ? 0 : 3];
 #pragma unroll
@@ -2367,7 +2383,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   float ew[TT];
   auto task_begin = [&]() {
     int rt, wi;
-    prefill_tile(tau, RT, rt, wi);
+    tasks.tile(tau, rt, wi);
     const int4 it = item_of(slot);
     r0 = rt * C::MR;
     ntok = it.z;
@@ -2572,20 +2588,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int H = a.hidden, E = a.experts;
   const int RTL = a.row_tiles, rtx = (RTL + 7) >> 3;
   const int nwork = *a.n_work;
-  const Mx3Tasks tasks{(int)blockIdx.x, (int)gridDim.x, RTL, 8 * rtx * nwork};
+  const Mx3Tasks tasks((int)blockIdx.x, (int)gridDim.x, RTL, nwork, a.xcd_rows);
   if (tasks.first() >= tasks.lim) return;
   auto group_of = [&](int e) -> const ExpertGroup & { return a.grp[e == E ? 1 : 0]; };
   auto k_of = [&](int e) { return PH == PH_UP ? H : group_of(e).inter; };
   auto nst_of = [&](int e) { return (k_of(e) + SCOLS - 1) / SCOLS; };
   auto work_of = [&](int tau) {
     int rt, wi;
-    prefill_tile(min(tau, tasks.lim - 1), RTL, rt, wi);
+    tasks.tile(min(tau, tasks.lim - 1), rt, wi);
     return a.work[min(wi, nwork - 1)];
   };
   // A task's copy for the MFMA waves: its work item, then its slot ids.
   auto send_info = [&](int tau, const int4 &w, int slot) {
     int rt, wi;
-    prefill_tile(tau, RTL, rt, wi);
+    tasks.tile(tau, rt, wi);
     uint8_t *info = lds + C::OFF_INFO + C::INFO * slot;
     lds_load4((const int *)(a.work + wi) + min(lane, 3), info);
 #pragma unroll
@@ -2612,7 +2628,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int k = 0; k < NO; ++k) o[k] = on[k];
       int rt, wi;
-      prefill_tile(tau, RTL, rt, wi);
+      tasks.tile(tau, rt, wi);
       // The next task's copy goes out a task ahead: it lands long before that task's first stage
       // is read.
       const int t1 = tasks.next(tau);
@@ -2786,7 +2802,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       K = k_of(e);
       nst = nst_of(e);
       int wi;
-      prefill_tile(tau, RTL, rt, wi);
+      tasks.tile(tau, rt, wi);
       if constexpr (PH == PH_DOWN) {
 #pragma unroll
         for (int st = 0; st < NT; ++st) ew[st] = a.slot_w[((const int *)(info + 256))[min(16 * st + l16, ntok - 1)]];
@@ -3016,7 +3032,13 @@ template <int PH, int TT> static hipError_t launch_mxa(GemmArgs a, hipStream_t s
   return hipGetLastError();
 }
 
-hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStream_t s, Timing tm) {
+hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &args, hipStream_t s, Timing tm) {
+  // Persistent kernels: XCD split into row-tile parts × work-item parts (Mx3Tasks). Measured on
+  // the benchmark layers (prefill T = 512..2048) against 8 row-tile parts: BF16 gate-up 832 →
+  // 615 µs with 4 or 2 parts, BF16 down 414 → 371 µs with 2; MLX 3-5 % faster with 4; MXFP4
+  // within ±2 % (its down fetches 18 % fewer bytes with 4).
+  GemmArgs a = args;
+  a.xcd_rows = (quant == Q_BF16 && phase == PH_DOWN) ? 2 : 4;
   if (quant == Q_MXFP4 && use_mxa(phase, a, nt))
     return nt == 2 ? launch_mxa<PH_UP, 2>(a, s, tm) : launch_mxa<PH_UP, 4>(a, s, tm);
   if (quant == Q_MXFP4 && nt == 4 && phase == PH_DOWN && a.slots == a.top_k &&
