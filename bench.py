@@ -279,14 +279,14 @@ def shared_bytes(desc: F.MoEDesc) -> int:
     return F.streamed_expert_bytes(desc, desc.shared_intermediate) + desc.hidden * 2
 
 
-def measure_other(torch, name, desc, copies, T_prefill, steps, prefill=True):
-    """Decode T=1 and T=8 and one chunked prefill of another format: whole-layer tokens/s,
+def measure_other(torch, name, desc, copies, T_prefill, steps, prefill=True, decode_tokens=(1, 8)):
+    """Decode at the given batch sizes and one chunked prefill of another format: whole-layer tokens/s,
     layer GB/s on the bytes touched (distinct routed experts + shared expert + router),
     expert-product TFLOP/s for the prefill."""
-    log(f"{name}: decode T=1 and 8, prefill T={T_prefill}")
+    log(f"{name}: decode T={list(decode_tokens)}, prefill T={T_prefill}")
     wl = Workload(torch, desc, copies=copies)
     dec = {}
-    for T in (1, 8):
+    for T in decode_tokens:
         d = measure_decode(wl, T, steps if T == 1 else max(50, steps // 4), 20)
         d["layer_GBps"] += shared_bytes(desc) / (d["ms_per_step"] * 1e-3) / 1e9
         d["layer_hbm_frac"] = d["layer_GBps"] / HBM_PEAK_GBS
@@ -349,6 +349,8 @@ def main():
     ap.add_argument("--copies", type=int, default=8, help="resident layer copies (decode)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--decode-tokens", default="1,8",
+                    help="decode batch sizes of the --only-other measurement (comma list)")
     ap.add_argument("--only-t1", action="store_true", help="decode T=1 only (for profiling)")
     ap.add_argument("--no-other", action="store_true", help="skip the MLX and BF16 configs")
     ap.add_argument("--only-other", default=None,
@@ -394,7 +396,8 @@ def main():
     if args.only_other:
         name, desc, copies, Tp = next(o for o in OTHER if o[0] == args.only_other)
         print(json.dumps({name: measure_other(torch, name, desc, copies, Tp, args.steps,
-                                              prefill=not args.no_prefill)}))
+                                              prefill=not args.no_prefill,
+                                              decode_tokens=[int(t) for t in args.decode_tokens.split(",") if t])}))
         return
     decode, fused, stack = {}, {}, {}
     if not args.only_prefill:

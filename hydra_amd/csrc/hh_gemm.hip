@@ -687,7 +687,7 @@ constexpr int LDS_PAD = 8;        // bf16 elements of padding per staged row (ba
 // 4·TPW waves: wave w takes tile q (16 intermediates; w & 1 when TPW = 2), gate or up rows, and
 // chunk parity p (the even or odd chain of the canonical arithmetic). TPW = 1 gives twice the
 // workgroups of half the size, which spreads a decode step's few experts over more compute units.
-template <int FMT, int DA, int TPW = 2>
+template <int FMT, int DA, int TPW, int XB>
 __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) {
   constexpr int NTH = 256 * TPW, NWV = 4 * TPW, ROWS = 16 * TPW;
   constexpr int NM = 1;
@@ -702,7 +702,8 @@ __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) 
   const bool has_shared = S > K;
 
   // Every token's x into LDS (row t), independent of the routing: the first batch of loads
-  // goes out before the selection and is stored with the first item.
+  // (XB vectors per thread) goes out before the selection and is stored with the first item, or,
+  // for batches of several tokens, right after the selection (before any weight stream).
   const int ldx = H + LDS_PAD;
   const int per_row = H / 8, nvec = T * per_row;
   auto xsrc = [&](int v) {
@@ -713,7 +714,6 @@ __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) 
     const int t = v / per_row, qq = v - t * per_row;
     *(u32x4 *)(s_x + (size_t)t * ldx + 8 * qq) = val;
   };
-  constexpr int XB = 2;
   u32x4 xr[XB];
 #pragma unroll
   for (int k = 0; k < XB; ++k)
@@ -730,6 +730,14 @@ __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) 
   const int par = TPW == 2 ? wave >> 2 : wave >> 1;
   const int nch = (H + Fmt<FMT>::CHUNK - 1) / Fmt<FMT>::CHUNK;
   bool x_pending = true;
+  auto store_x = [&]() {
+#pragma unroll
+    for (int k = 0; k < XB; ++k)
+      if (tid + NTH * k < nvec) xdst(tid + NTH * k, xr[k]);
+    for (int base = NTH * XB; base < nvec; base += NTH * 4) stage_batch<4>(base, tid, NTH, nvec, xsrc, xdst);
+    x_pending = false;
+  };
+  if constexpr (XB > 2) store_x();
   for (int it = blockIdx.x; it < nitems; it += gridDim.x) {
     const bool sh = it >= plan.nu * rtr;
     const int u = sh ? plan.nu : it / rtr;
@@ -746,13 +754,7 @@ __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) 
     // any further batches.
     AStream<FMT, NM, DA> as(par, 2, nch);
     as.fill(at, nch, g, H);
-    if (x_pending) {
-#pragma unroll
-      for (int k = 0; k < XB; ++k)
-        if (tid + NTH * k < nvec) xdst(tid + NTH * k, xr[k]);
-      for (int base = NTH * XB; base < nvec; base += NTH * 4) stage_batch<4>(base, tid, NTH, nvec, xsrc, xdst);
-      x_pending = false;
-    }
+    if (x_pending) store_x();
     __syncthreads();
     if (it == (int)blockIdx.x) HH_TR(1, 2);
 
@@ -980,7 +982,7 @@ __device__ __forceinline__ MxStage<NTERM, NB, RowOf, DEV> mx_stage(uint8_t *dst,
 // through LDS. The gate waves combine gate and up and write the block's activations to LDS; wave
 // 0 writes them as NTH fp8 terms. Each item issues its whole weight stream at once; co-resident
 // workgroups hide one another's latency.
-template <int DA, bool ONE>
+template <int DA, bool ONE, int XB>
 __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) {
   constexpr int NM = 1;
   extern __shared__ __align__(16) uint8_t s_xb[];   // [T][NTX] rows of mx_row_bytes(xld), then [64][H/32] scales
@@ -1003,7 +1005,7 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
   // with the first item.
   const int RS = mx_row_bytes(a.xld);
   HH_TR(1, 0);
-  auto xs = mx_stage<NTX, 2>(s_xb, a.xq, a.xs, a.xld, a.hidden, T, [](int j) { return j; }, tid, 256);
+  auto xs = mx_stage<NTX, XB>(s_xb, a.xq, a.xs, a.xld, a.hidden, T, [](int j) { return j; }, tid, 256);
   xs.load_first();
   // Top-k of every token (wave w: tokens w, w + 4, ...); workgroup 0 writes the routing outputs.
   for (int t = wave; t < T; t += 4) {
@@ -1031,6 +1033,14 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
   uint8_t *s_sc = s_xb + (size_t)T * NTX * RS;      // [64][nsb]
   const int nsv = scale_vectors(64, H);
   bool x_pending = true;
+  if constexpr (XB > 2) {
+    // Batches of several tokens: the x terms landed during the selection; they are stored before
+    // the first item's weight stream takes its registers.
+    xs.store_first();
+    xs.rest();
+    xs.pad();
+    x_pending = false;
+  }
   for (int it = blockIdx.x; it < nitems; it += gridDim.x) {
     const bool sh = it >= nu * rtr;
     const int u = sh ? nu : it / rtr;
@@ -2904,9 +2914,18 @@ template <int FMT> constexpr int decode_depth() { return FMT == Q_BF16 ? 4 : (FM
 // MXFP4 streams of at most MX_ONE chunks (K ≤ 3072) run the single-round kernels (the whole row
 // in flight, no ring refills); longer rows take the ring variants.
 constexpr int MX_ONE = MX_ONE_CHUNKS;
-template <int FMT> static UpSmallKernel up_small_k(bool one) {
-  if constexpr (FMT == Q_MXFP4) return one ? up_small_mx<MX_ONE, true> : up_small_mx<16, false>;
-  else return up_small<FMT, decode_depth<FMT>(), 1>;
+// One token's x (MXFP4: 2 terms × (H/16 + scale vectors) 16-byte vectors, 372 at H = 2880; the
+// others: H/8 vectors) fits the first round of staging loads at two vectors per thread; larger
+// batches issue twelve per thread before the selection, so T ≤ 8 stages in one round (T = 8 took
+// four).
+constexpr int MX_XB_WIDE = 12;
+template <int FMT> static UpSmallKernel up_small_k(bool one, int T) {
+  if constexpr (FMT == Q_MXFP4) {
+    if (T == 1) return one ? up_small_mx<MX_ONE, true, 2> : up_small_mx<16, false, 2>;
+    return one ? up_small_mx<MX_ONE, true, MX_XB_WIDE> : up_small_mx<16, false, MX_XB_WIDE>;
+  }
+  else if (T == 1) return up_small<FMT, decode_depth<FMT>(), 1, 2>;
+  else return up_small<FMT, decode_depth<FMT>(), 1, MX_XB_WIDE>;
 }
 // Waves per slot of down_small: MXFP4's canonical arithmetic is one chain over K (one wave per
 // slot); the others split K by chunk parity over two waves when the workgroup has room.
@@ -3092,18 +3111,20 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
   UpSmallKernel up;
   DownSmallKernel down;
   switch (quant) {
-  case Q_MXFP4: up = up_small_k<Q_MXFP4>(one_up); down = down_small_k<Q_MXFP4>(S, one_down); break;
-  case Q_BF16: up = up_small_k<Q_BF16>(true); down = down_small_k<Q_BF16>(S, true); break;
-  case Q_MLX4: up = up_small_k<Q_MLX4>(true); down = down_small_k<Q_MLX4>(S, true); break;
-  default: up = up_small_k<Q_MLX8>(true); down = down_small_k<Q_MLX8>(S, true); break;
+  case Q_MXFP4: up = up_small_k<Q_MXFP4>(one_up, T); down = down_small_k<Q_MXFP4>(S, one_down); break;
+  case Q_BF16: up = up_small_k<Q_BF16>(true, T); down = down_small_k<Q_BF16>(S, true); break;
+  case Q_MLX4: up = up_small_k<Q_MLX4>(true, T); down = down_small_k<Q_MLX4>(S, true); break;
+  default: up = up_small_k<Q_MLX8>(true, T); down = down_small_k<Q_MLX8>(S, true); break;
   }
   // The decode kernels stage rows in dynamic LDS beyond the default 64 KiB window (gfx950 has
   // 160 KiB per compute unit).
   static std::once_flag lds_once;
   std::call_once(lds_once, [] {
-    const void *ks[] = {(const void *)up_small_k<Q_MXFP4>(true), (const void *)up_small_k<Q_MXFP4>(false),
-                        (const void *)up_small_k<Q_BF16>(true), (const void *)up_small_k<Q_MLX4>(true),
-                        (const void *)up_small_k<Q_MLX8>(true),
+    const void *ks[] = {(const void *)up_small_k<Q_MXFP4>(true, 1), (const void *)up_small_k<Q_MXFP4>(false, 1),
+                        (const void *)up_small_k<Q_MXFP4>(true, SMALL_T), (const void *)up_small_k<Q_MXFP4>(false, SMALL_T),
+                        (const void *)up_small_k<Q_BF16>(true, 1), (const void *)up_small_k<Q_MLX4>(true, 1),
+                        (const void *)up_small_k<Q_MLX8>(true, 1), (const void *)up_small_k<Q_BF16>(true, SMALL_T),
+                        (const void *)up_small_k<Q_MLX4>(true, SMALL_T), (const void *)up_small_k<Q_MLX8>(true, SMALL_T),
                         (const void *)down_small_k<Q_MXFP4>(4, true), (const void *)down_small_k<Q_BF16>(4, true),
                         (const void *)down_small_k<Q_MLX4>(4, true), (const void *)down_small_k<Q_MLX8>(4, true),
                         (const void *)down_small_k<Q_MXFP4>(9, true), (const void *)down_small_k<Q_BF16>(9, true),
