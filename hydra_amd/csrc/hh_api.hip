@@ -36,6 +36,8 @@ hipError_t launch_attention_decode(const AttnArgs &a, hipStream_t s);
 #ifdef HH_TRACE
 hipError_t trace_read(void *out, size_t bytes);
 hipError_t trace_clear();
+hipError_t trace_read_route(void *out, size_t bytes);
+hipError_t trace_clear_route();
 #endif
 hipError_t launch_down_small(int quant, GemmArgs a, const int32_t *topk_idx, int T, hipStream_t s,
                              Timing tm_down);
@@ -1087,8 +1089,14 @@ int hh_expert_gemm(hh_ctx *ctx, const hh_matrix *m, const float *x, int32_t T, f
 
 #ifdef HH_TRACE
 // Development build only: the decode kernels' timeline of the last call (hh_gemm.hip).
-int hh_debug_trace_read(void *out, size_t bytes) { return hh::trace_read(out, bytes) == hipSuccess ? HH_OK : HH_EHIP; }
-int hh_debug_trace_clear(void) { return hh::trace_clear() == hipSuccess ? HH_OK : HH_EHIP; }
+// [kernel][block][point]: kernel 0 the small-batch router (hh_route.hip), 1 gate-up, 2 down.
+int hh_debug_trace_read(void *out, size_t bytes) {
+  if (hh::trace_read(out, bytes) != hipSuccess) return HH_EHIP;
+  return hh::trace_read_route(out, bytes) == hipSuccess ? HH_OK : HH_EHIP;
+}
+int hh_debug_trace_clear(void) {
+  return hh::trace_clear() == hipSuccess && hh::trace_clear_route() == hipSuccess ? HH_OK : HH_EHIP;
+}
 #endif
 
 int hh_expert_gemv(hh_ctx *ctx, const hh_matrix *m, const float *x, float *y) {

@@ -36,27 +36,32 @@ __device__ __forceinline__ double norm_factor(double sumsq, int H, double eps, i
 // Σ x² of row x[0..H) by one wave in the canonical lane layout of a row (that of exact_logit):
 // lane l holds columns 2048i + 512u + 8l .. +7 (u = 0..3) of each 2048-column step i, and adds
 // their squares in (i, u, column) order; then the lanes by a fixed butterfly. Every lane returns
-// the sum. H is a multiple of 8, x 16-byte aligned.
+// the sum. H is a multiple of 8, x 16-byte aligned. Two steps' loads go out together (columns
+// past H read as zero, whose squares add nothing).
 __device__ __forceinline__ double row_sumsq(const float *x, int H) {
   const int lane = threadIdx.x & 63;
   double s = 0.0;
-  for (int base = 0; base < H; base += 2048) {
-    f32x4 v[4][2];
+  for (int base = 0; base < H; base += 4096) {
+    f32x4 v[2][4][2];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int h = base + 512 * u + 8 * lane;
-      const int hc = min(h, H - 8);
-      v[u][0] = *(const f32x4 *)(x + hc);
-      v[u][1] = *(const f32x4 *)(x + hc + 4);
-      if (h >= H) v[u][0] = v[u][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const double d = v[u][k >> 2][k & 3];
-        s += d * d;
+      for (int u = 0; u < 4; ++u) {
+        const int h = base + 2048 * i + 512 * u + 8 * lane;
+        const int hc = min(h, H - 8);
+        v[i][u][0] = *(const f32x4 *)(x + hc);
+        v[i][u][1] = *(const f32x4 *)(x + hc + 4);
+        if (h >= H) v[i][u][0] = v[i][u][1] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const double d = v[i][u][k >> 2][k & 3];
+          s += d * d;
+        }
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);

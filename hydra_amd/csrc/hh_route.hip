@@ -435,80 +435,33 @@ __global__ __launch_bounds__(256) void quant_x_kernel(RouteArgs a) {
   quant_x_wave(a, w / per_t, 16 * (w % per_t));
 }
 
+// Development timeline (built only with -DHH_TRACE): wall-clock stamps (100 MHz) of the small-batch
+// router kernel per workgroup, [block][point], read as kernel 0 of the decode kernels' timeline.
+#ifdef HH_TRACE
+constexpr int kRtTraceBlocks = 4096, kRtTracePoints = 8;
+static __device__ uint64_t hh_trace_rt[kRtTraceBlocks * kRtTracePoints];
+#define HH_RT(point)                                                                               \
+  do {                                                                                             \
+    if ((threadIdx.x & 63) == 0 && blockIdx.x < kRtTraceBlocks)                                    \
+      hh_trace_rt[blockIdx.x * kRtTracePoints + (point)] = wall_clock64();                         \
+  } while (0)
+hipError_t trace_read_route(void *out, size_t bytes) {
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(hh_trace_rt), std::min(bytes, sizeof(hh_trace_rt)), 0,
+                             hipMemcpyDeviceToHost);
+}
+hipError_t trace_clear_route() {
+  static uint64_t zeros[kRtTraceBlocks * kRtTracePoints];
+  return hipMemcpyToSymbol(HIP_SYMBOL(hh_trace_rt), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
+}
+#else
+#define HH_RT(point) do {} while (0)
+#endif
+
 // ---- small batches (T ≤ 16): every logit exactly in fp64 -----------------------------------------
 // One wave per (token, expert) pair, spread over many compute units (one compute unit's load path
 // would take several microseconds to stream even a 32-expert router); expert id E is the shared
 // expert's gate row. Writes lg64 [T][E+1].
 // Waves past the logits quantise x (MXFP4 layers).
-// FFN block (a.resid set, bf16 router, H ≤ 4096): the layer input x = bf16(resid·f·norm_w) of
-// token t, formed in registers in the canonical row layout (row_sumsq's), and its exact logit
-// against row `wrow` in exact_logit's arithmetic (bf16·bf16 products exact in fp32, added in fp64
-// per u, (acc0 + acc1) + (acc2 + acc3), wave sum): the values the block's norm kernel followed by
-// exact_logit give. All loads (residual row, norm weights, projection row) go out together. When
-// xn_out is given the lanes also store x there.
-__device__ __forceinline__ double block_pair_logit(const RouteArgs &a, int t, const uint16_t *wrow,
-                                                   uint16_t *xn_out) {
-  const int lane = threadIdx.x & 63, H = a.hidden;
-  const float *x = a.resid + (size_t)t * H;
-  f32x4 xv[2][4][2];
-  u32x4 nv[2][4], wv[2][4];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int h = 2048 * i + 512 * u + 8 * lane;
-      const int hc = min(h, H - 8);
-      xv[i][u][0] = *(const f32x4 *)(x + hc);
-      xv[i][u][1] = *(const f32x4 *)(x + hc + 4);
-      nv[i][u] = *(const u32x4 *)(a.norm_w + hc);
-      wv[i][u] = *(const u32x4 *)(wrow + hc);
-      if (h >= H) {
-        xv[i][u][0] = xv[i][u][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-        wv[i][u] = u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-  double ss = 0.0;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    if (2048 * i >= H) break;
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const double d = xv[i][u][k >> 2][k & 3];
-        ss += d * d;
-      }
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-  const double f = norm_factor(ss, H, (double)a.norm_eps, a.norm_pow);
-  double acc[4] = {0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    if (2048 * i >= H) break;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      uint32_t xb[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const uint32_t nb = (nv[i][u][k >> 1] >> (16 * (k & 1))) & 0xFFFFu;
-        xb[k] = f64_to_bf16_bits((double)xv[i][u][k >> 2][k & 3] * f * (double)bf16_bits_to_f32(nb));
-      }
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float xf = bf16_bits_to_f32(xb[k]);
-        const float wf = bf16_bits_to_f32((wv[i][u][k >> 1] >> (16 * (k & 1))) & 0xFFFFu);
-        acc[u] += (double)(xf * wf);
-      }
-      const int h = 2048 * i + 512 * u + 8 * lane;
-      if (xn_out && h < H)
-        *(u32x4 *)(xn_out + (size_t)t * H + h) =
-            u32x4{xb[0] | (xb[1] << 16), xb[2] | (xb[3] << 16), xb[4] | (xb[5] << 16), xb[6] | (xb[7] << 16)};
-    }
-  }
-  return wave_sum_f64((acc[0] + acc[1]) + (acc[2] + acc[3]));
-}
-
 // The FFN block's x terms (MXFP4 layers): as quant_x_wave over token t's layer input, formed
 // from the residual stream (norm factor from the whole row, values rounded as norm_row_bf16).
 __device__ __forceinline__ void quant_x_wave_block(const RouteArgs &a, int t, int blk0) {
@@ -543,27 +496,134 @@ __global__ __launch_bounds__(256) void logits_small_kernel(RouteArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int E = a.experts, E1 = E + 1, H = a.hidden;
   const int p = blockIdx.x * 4 + wave;
+  if (wave == 0) HH_RT(0);
   if (p >= a.tokens * E1) {
     const int w = p - a.tokens * E1;
     if (w < quant_x_waves(a)) {
       const int per_t = (H / 32 + 15) / 16;
-      if (!gemma && a.resid) quant_x_wave_block(a, w / per_t, 16 * (w % per_t));
-      else quant_x_wave(a, w / per_t, 16 * (w % per_t));
+      quant_x_wave(a, w / per_t, 16 * (w % per_t));
     }
+    if (wave == 0) HH_RT(2);
     return;
   }
   const int t = p / E1, e = p - t * E1;
   if (e == E && !a.shared_gate) return;
-  double v;
-  if (!gemma && a.resid) {
-    // The FFN block: the (t, 0) wave also stores the layer input for the expert products.
-    v = block_pair_logit(a, t, e < E ? a.router_w + (size_t)e * H : a.shared_gate,
-                         e == 0 ? a.xn_out : nullptr);
-    if (e < E && a.router_b) v += (double)bf16_bits_to_f32(a.router_b[e]);
-  } else {
-    v = pair_logit<gemma>(a, t, e);
-  }
+  const double v = pair_logit<gemma>(a, t, e);
   if (lane == 0) a.lg64[(size_t)t * E1 + e] = v;
+  if (wave == 0) HH_RT(1);
+}
+
+// The FFN block's router (a.resid set, bf16 non-GEMMA router, T ≤ 16, H ≤ 4096): workgroup (t, g)
+// of BLK_W waves forms token t's layer input x = bf16(resid·f·norm_w) once, into LDS (its threads
+// splitting the columns; the norm factor f from every wave's own canonical Σ resid², row_sumsq's
+// order), then wave w computes the exact logit of row BLK_W·g + w against it (row E: the shared
+// gate) in exact_logit's arithmetic (lane l: columns 2048i + 512u + 8l .. +7, bf16·bf16 products
+// exact in fp32 added in fp64 per u, (acc0 + acc1) + (acc2 + acc3), wave sum): the values the
+// block's norm kernel followed by the plain router give. Every global load of a wave (router
+// row, residual row, its share of the norm weights) goes out before the first arithmetic, so the
+// workgroup costs one memory latency. Workgroup (t, 0) also stores x for the expert products;
+// workgroups past T·G quantise x (MXFP4 layers).
+constexpr int BLK_W = 8;
+__host__ __device__ constexpr int block_logit_groups(int E) { return (E + 1 + BLK_W - 1) / BLK_W; }
+__global__ __launch_bounds__(64 * BLK_W) void logits_block_kernel(RouteArgs a) {
+  __shared__ __align__(16) uint16_t s_xn[4096];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int E = a.experts, E1 = E + 1, H = a.hidden;
+  const int G = block_logit_groups(E);
+  if (wave == 0) HH_RT(0);
+  if ((int)blockIdx.x >= a.tokens * G) {
+    const int w = ((int)blockIdx.x - a.tokens * G) * BLK_W + wave;
+    if (w < quant_x_waves(a)) {
+      const int per_t = (H / 32 + 15) / 16;
+      quant_x_wave_block(a, w / per_t, 16 * (w % per_t));
+    }
+    if (wave == 0) HH_RT(2);
+    return;
+  }
+  const int t = blockIdx.x / G, g = blockIdx.x - t * G, e = g * BLK_W + wave;
+  const bool live = e < E || (e == E && a.shared_gate);
+  const uint16_t *wrow = (e < E || !live) ? a.router_w + (size_t)min(e, E - 1) * H : a.shared_gate;
+  const float *x = a.resid + (size_t)t * H;
+  // Loads: the router row and the residual row in the canonical layout, and this thread's share
+  // of the row (4 columns per step) with its norm weights.
+  u32x4 wv[2][4];
+  f32x4 xv[2][4][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int h = 2048 * i + 512 * u + 8 * lane;
+      const int hc = min(h, H - 8);
+      wv[i][u] = *(const u32x4 *)(wrow + hc);
+      xv[i][u][0] = *(const f32x4 *)(x + hc);
+      xv[i][u][1] = *(const f32x4 *)(x + hc + 4);
+      if (h >= H) {
+        wv[i][u] = u32x4{0u, 0u, 0u, 0u};
+        xv[i][u][0] = xv[i][u][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  constexpr int NS = 4096 / 4 / (64 * BLK_W);   // 4-column groups per thread (H ≤ 4096)
+  const int n4 = H / 4;
+  f32x4 sx[NS];
+  u32x2 sn[NS];
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    const int j = min(tid + 64 * BLK_W * k, n4 - 1);
+    sx[k] = ((const f32x4 *)x)[j];
+    sn[k] = ((const u32x2 *)a.norm_w)[j];
+  }
+  // Σ resid² in row_sumsq's order, then the thread's columns of x.
+  double ss = 0.0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const double d = xv[i][u][k >> 2][k & 3];
+        ss += d * d;
+      }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  const double f = norm_factor(ss, H, (double)a.norm_eps, a.norm_pow);
+  uint16_t *xn_g = (g == 0 && a.xn_out) ? a.xn_out + (size_t)t * H : nullptr;
+#pragma unroll
+  for (int k = 0; k < NS; ++k) {
+    const int j = tid + 64 * BLK_W * k;
+    if (j < n4) {
+      uint32_t o[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t nb = (sn[k][c >> 1] >> (16 * (c & 1))) & 0xFFFFu;
+        o[c] = f64_to_bf16_bits((double)sx[k][c] * f * (double)bf16_bits_to_f32(nb));
+      }
+      const u32x2 pk = {o[0] | (o[1] << 16), o[2] | (o[3] << 16)};
+      *(u32x2 *)(s_xn + 4 * j) = pk;
+      if (xn_g) *(u32x2 *)(xn_g + 4 * j) = pk;
+    }
+  }
+  __syncthreads();
+  if (!live) return;
+  double acc[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (2048 * i >= H) break;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const u32x4 xb = *(const u32x4 *)(s_xn + min(2048 * i + 512 * u + 8 * lane, H - 8));
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int sh = (k & 1) * 16;
+        const float xf = bf16_bits_to_f32((xb[k >> 1] >> sh) & 0xFFFF);
+        const float wf = bf16_bits_to_f32((wv[i][u][k >> 1] >> sh) & 0xFFFF);
+        acc[u] += (double)(xf * wf);
+      }
+    }
+  }
+  double v = wave_sum_f64((acc[0] + acc[1]) + (acc[2] + acc[3]));
+  if (e < E && a.router_b) v += (double)bf16_bits_to_f32(a.router_b[e]);
+  if (lane == 0) a.lg64[(size_t)t * E1 + e] = v;
+  if (wave == 0) HH_RT(1);
 }
 
 // Top-k and weights of every token from lg64 (operator entry hh_router_topk, T ≤ 16): one
@@ -697,12 +757,21 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s, Timing tm) {
   if (a.tokens <= RT_TOK) {
     // The layer (want_dispatch) selects inside its gate-up kernel; the operator entry selects
     // here.
-    const int waves = a.tokens * (a.experts + 1) + (a.xq ? a.tokens * ((a.hidden / 32 + 15) / 16) : 0);
+    const int qwaves = a.xq ? a.tokens * ((a.hidden / 32 + 15) / 16) : 0;
     const bool sel = a.want_dispatch == 0;
     const bool g = a.router == R_GEMMA;
-    hipExtLaunchKernelGGL(g ? logits_small_kernel<true> : logits_small_kernel<false>,
-                          dim3((waves + 3) / 4), dim3(256), 0, s, tm.start, sel ? nullptr : tm.stop,
-                          0, a);
+    if (a.resid) {
+      // The FFN block's router (the caller admits only bf16 non-GEMMA routers, H ≤ 4096).
+      if (g || a.hidden > 4096) return hipErrorInvalidValue;
+      const int blocks = a.tokens * block_logit_groups(a.experts) + (qwaves + BLK_W - 1) / BLK_W;
+      hipExtLaunchKernelGGL(logits_block_kernel, dim3(blocks), dim3(64 * BLK_W), 0, s, tm.start,
+                            sel ? nullptr : tm.stop, 0, a);
+    } else {
+      const int waves = a.tokens * (a.experts + 1) + qwaves;
+      hipExtLaunchKernelGGL(g ? logits_small_kernel<true> : logits_small_kernel<false>,
+                            dim3((waves + 3) / 4), dim3(256), 0, s, tm.start, sel ? nullptr : tm.stop,
+                            0, a);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || !sel) return e;
     hipExtLaunchKernelGGL(select_small_kernel, dim3(1), dim3(256), 0, s, nullptr, tm.stop, 0, a);
