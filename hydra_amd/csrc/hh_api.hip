@@ -859,6 +859,11 @@ int hh_attention_decode(hh_ctx *ctx, const float *q, const uint16_t *k_cache,
     return fail(HH_EINVAL, "key_count, ring_size and start_position must be >= 0, keys within the ring");
   if (((uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)q) & 15)
     return fail(HH_EALIGN, "q and the caches must be 16-byte aligned");
+  // The key count and ring position are kernel arguments: a recorded graph would replay them
+  // unchanged at every later step.
+  if (ctx->capturing)
+    return fail(HH_EINVAL, "hh_attention_decode cannot be recorded in a graph (its key count and "
+                           "ring position change every step); call it eagerly");
   // Chunks of at least 256 keys (one 64-key tile per wave), up to ~1024 workgroups.
   const int chunks = std::max(1, std::min(key_count / 256, std::max(1, hh::kAttnMaxChunks / kv_heads)));
   const int per_chunk = std::max(1, (key_count + chunks - 1) / chunks);
@@ -866,8 +871,6 @@ int hh_attention_decode(hh_ctx *ctx, const float *q, const uint16_t *k_cache,
   const size_t need = sizeof(float) * slots * (2 + (size_t)head_dim);
   HH_HIP(hipSetDevice(ctx->device));
   if (ctx->attn_bytes < need) {
-    if (ctx->capturing)
-      return fail(HH_EINVAL, "attention partials must be sized before capture (one eager call)");
     if (ctx->live_graphs > 0)
       return fail(HH_EINVAL, "the call needs larger attention partials, but graphs of this context "
                              "still use the current ones (destroy the graphs first)");

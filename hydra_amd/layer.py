@@ -67,10 +67,15 @@ class Context:
         check(lib().hh_ctx_capture_begin(self.handle))
         try:
             record()
-        finally:
+        except BaseException:
+            # end the capture and drop what it recorded: a graph left alive would keep the
+            # context's scratch from growing
             g = C.c_void_p()
-            rc = lib().hh_ctx_capture_end(self.handle, C.byref(g))
-        check(rc)
+            lib().hh_ctx_capture_end(self.handle, C.byref(g))
+            lib().hh_graph_destroy(g)
+            raise
+        g = C.c_void_p()
+        check(lib().hh_ctx_capture_end(self.handle, C.byref(g)))
         return Graph(g, self)
 
     @property

@@ -251,7 +251,9 @@ int hh_moe_forward_noalloc(hh_ctx *ctx, const hh_moe_desc *desc, const hh_moe_we
  *            (ring_size 0: row p); keys start_position .. start_position + key_count - 1
  *   sinks    bf16 [q_heads], in the softmax denominator only
  *   out      fp32 [q_heads][head_dim]
- * head_dim 64 or 128, q_heads = kv_heads × 1..8 (HH_ESHAPE otherwise).                     */
+ * head_dim 64 or 128, q_heads = kv_heads × 1..8 (HH_ESHAPE otherwise). Refused (HH_EINVAL)
+ * while the context captures a graph: key_count and start_position change every decode step,
+ * and a graph would replay the recorded values.                                             */
 int hh_attention_decode(hh_ctx *ctx, const float *q, const uint16_t *k_cache,
                         const uint16_t *v_cache, const uint16_t *sinks, int32_t q_heads,
                         int32_t kv_heads, int32_t head_dim, int32_t key_count, int32_t ring_size,

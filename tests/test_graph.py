@@ -107,3 +107,32 @@ def test_growing_scratch_is_refused_while_a_graph_lives():
         assert torch.isfinite(y2).all()
     finally:
         ctx.close()
+
+
+@pytest.mark.gpu
+def test_attention_is_refused_inside_a_capture():
+    """hh_attention_decode takes the key count and ring position as per-step arguments, which a
+    graph would replay unchanged: it fails with HH_EINVAL while the context captures, the
+    capture still ends cleanly, and the same call runs eagerly afterwards."""
+    import torch
+    from hydra_amd._lib import HydraHIPError
+    from hydra_amd.attention import attention_decode_into
+    from hydra_amd.layer import Context
+    print("[gpu] attention refused under capture", flush=True)
+    ctx = Context(0)
+    try:
+        dev = "cuda:0"
+        q = torch.randn((8, 64), device=dev)
+        k = torch.randn((512, 1, 64), device=dev).half()
+        v = torch.randn((512, 1, 64), device=dev).half()
+        sinks = torch.zeros(8, dtype=torch.int16, device=dev)
+        out = torch.empty((8, 64), dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        with pytest.raises(HydraHIPError) as e:
+            ctx.capture(lambda: attention_decode_into(ctx, q, k, v, sinks, 300, out=out))
+        assert e.value.code == -1 and "graph" in str(e.value)
+        attention_decode_into(ctx, q, k, v, sinks, 300, out=out)
+        ctx.synchronize()
+        assert torch.isfinite(out).all()
+    finally:
+        ctx.close()
