@@ -212,8 +212,10 @@ def measure_stack(wl, T, layers, steps, warmup):
 
 def measure_attention(torch, keys, q_heads=64, kv_heads=8, head_dim=64, reps=50, steps=20):
     """Decode attention with sinks (hh_attention_decode) on GPT-OSS's attention shape over an
-    fp16 history of `keys` positions: `reps` calls recorded as one HIP graph, replayed `steps`
-    times. Bytes = the key and value rows read once (keys · kv_heads · head_dim · 2 B · 2)."""
+    fp16 history of `keys` positions: `steps` rounds of `reps` back-to-back calls, timed with
+    events on the context's stream; a spin kernel queued ahead of each round lets the host
+    enqueue the round's calls before the first runs, so the events bracket GPU work only.
+    Bytes = the key and value rows read once (keys · kv_heads · head_dim · 2 B · 2)."""
     from hydra_amd.attention import attention_decode_into
     from hydra_amd.layer import Context
     dev = "cuda:0"
@@ -227,18 +229,21 @@ def measure_attention(torch, keys, q_heads=64, kv_heads=8, head_dim=64, reps=50,
     sinks = torch.randn(q_heads, device=dev, generator=g).bfloat16().view(torch.int16)
     out = torch.empty((q_heads, head_dim), dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
-    attention_decode_into(ctx, q, caches[0][0], caches[0][1], sinks, keys, out=out)
+    for i in range(4):
+        attention_decode_into(ctx, q, *caches[i % 2], sinks, keys, out=out)
     ctx.synchronize()
-    graph = ctx.capture(lambda: [attention_decode_into(ctx, q, *caches[i % 2], sinks, keys, out=out)
-                                 for i in range(reps)])
-    graph.launch()
-    ctx.synchronize()
-    t0 = time.perf_counter()
+    total = 0.0
     for _ in range(steps):
-        graph.launch()
-    ctx.synchronize()
-    sec = (time.perf_counter() - t0) / (steps * reps)
-    graph.close()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(ctx.stream):
+            torch.cuda._sleep(20_000_000)
+            start.record(ctx.stream)
+        for i in range(reps):
+            attention_decode_into(ctx, q, *caches[i % 2], sinks, keys, out=out)
+        stop.record(ctx.stream)
+        stop.synchronize()
+        total += start.elapsed_time(stop) * 1e-3
+    sec = total / (steps * reps)
     ctx.close()
     by = keys * kv_heads * head_dim * 2 * 2
     return {"keys": keys, "q_heads": q_heads, "kv_heads": kv_heads, "head_dim": head_dim,

@@ -49,6 +49,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <vector>
 
 namespace hh {
 
@@ -3099,6 +3100,24 @@ hipError_t launch_down_small(int quant, GemmArgs a, const int32_t *topk_idx, int
                              Timing tm_down);
 
 // Decode (T ≤ 16). `a.row_tiles` is set here per phase.
+// Workgroups of `kernel` resident per compute unit at `threads` threads and `lds` bytes of dynamic
+// LDS (at least 1), from the runtime's occupancy calculator, cached per (kernel, lds).
+static int resident_per_cu(const void *kernel, int threads, size_t lds) {
+  struct Entry { const void *k; size_t lds; int n; };
+  static std::mutex mu;
+  static std::vector<Entry> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const Entry &en : cache)
+    if (en.k == kernel && en.lds == lds) return en.n;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, threads, lds) != hipSuccess || n < 1) {
+    (void)hipGetLastError();
+    n = 1;
+  }
+  cache.push_back({kernel, lds, n});
+  return n;
+}
+
 hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t s, Timing tm_up,
                         Timing tm_down) {
   const int T = ra.tokens;
@@ -3145,9 +3164,10 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
   a.row_tiles = a.ldh / (mx ? UP_ROWS : 16);   // up_small: one 16-intermediate tile per workgroup
   const size_t lds_up = mx ? (size_t)T * NTX * mx_row_bytes(a.xld) + 64 * (a.hidden / 32)
                            : (size_t)T * (a.hidden + LDS_PAD) * 2;
-  // Persistent: about two workgroups per compute unit (MXFP4), or as many as the staged x rows
-  // leave room for in LDS, up to four (the others).
-  const int up_per_cu = mx ? 2 : (int)std::max<size_t>(1, std::min<size_t>(4, (size_t)(160 << 10) / lds_up));
+  // Persistent: as many workgroups per compute unit as are co-resident (registers, and the staged
+  // x rows in LDS), up to two (MXFP4, whose launch bounds hold two) or four (the others): a grid
+  // larger than that leaves workgroups waiting for earlier ones to exit.
+  const int up_per_cu = std::min(mx ? 2 : 4, resident_per_cu((const void *)up, 256, lds_up));
   const int up_grid = std::min(up_per_cu * ncu, a.row_tiles * maxu);
   hipExtLaunchKernelGGL(up, dim3(up_grid), dim3(256), lds_up, s, tm_up.start, tm_up.stop, 0, a, ra);
   hipError_t e = hipGetLastError();
@@ -3203,8 +3223,10 @@ hipError_t launch_down_small(int quant, GemmArgs a, const int32_t *topk_idx, int
   const size_t lds_down = mx ? (size_t)S * (NTH * mx_row_bytes(a.hld) + 16 * ((16 * (imax / 32) + 15) / 16))
                              : (size_t)S * 2 * (a.ldh + LDS_PAD) * 2;
   a.max_work = T;
-  const int down_grid = std::min(down_small_items(a.row_tiles, T), std::max(8, (2 * ncu) & ~7));   // a multiple of 8
   const int ks = (mx || S > 4 || !one_down) ? 1 : 2;
+  // Persistent, a multiple of 8 workgroups: up to two per compute unit, as many as are co-resident.
+  const int down_per_cu = std::min(2, resident_per_cu((const void *)down, 64 * S * ks, lds_down));
+  const int down_grid = std::min(down_small_items(a.row_tiles, T), std::max(8, (down_per_cu * ncu) & ~7));
   hipExtLaunchKernelGGL(down, dim3(down_grid), dim3(64 * S * ks), lds_down, s, tm_down.start,
                         tm_down.stop, 0, a, topk_idx);
   return hipGetLastError();
