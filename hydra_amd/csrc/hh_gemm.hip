@@ -667,8 +667,16 @@ static __device__ uint64_t hh_trace_buf[3 * kTraceBlocks * kTracePoints];
     if (threadIdx.x == 0 && blockIdx.x < kTraceBlocks)                                         \
       hh_trace_buf[((kern) * kTraceBlocks + blockIdx.x) * kTracePoints + (point)] = wall_clock64(); \
   } while (0)
+// Per-step stamps (core clock) of MFMA wave 0 of workgroup 0 of the MXFP4 prefill gate-up:
+// hh_trace_buf[2][step][point], steps < kTraceBlocks.
+#define HH_TRS(step, point)                                                                      \
+  do {                                                                                           \
+    if (threadIdx.x == 0 && blockIdx.x == 0 && (step) < kTraceBlocks)                            \
+      hh_trace_buf[(2 * kTraceBlocks + (step)) * kTracePoints + (point)] = clock64();            \
+  } while (0)
 #else
 #define HH_TR(kern, point) do {} while (0)
+#define HH_TRS(step, point) do {} while (0)
 #endif
 
 constexpr int SMALL_T = 16;       // largest batch of the decode kernels
@@ -2208,9 +2216,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // rows in the register file, about twice as many bytes are in flight per compute unit as when
 // everything passes through LDS. Per output element the arithmetic is the canonical one.
 // TT: 16-token tiles per wave (the whole token tile): 2 (32-token work items) or 4 (64).
+#ifndef HH_MXA_DA
+#define HH_MXA_DA 4
+#endif
+#ifndef HH_MXA_RA
+#define HH_MXA_RA 1
+#endif
 template <int PH, int TT_ = 2> struct MxA {   // PH_UP (down's three terms leave too few registers)
   static constexpr int NTERM = PH == PH_UP ? NTX : NTH;
-  static constexpr int TT = TT_, NTOK = 16 * TT, MR = 256, NJ = 4, DA = TT == 2 ? 6 : 2;
+  static constexpr int TT = TT_, NTOK = 16 * TT, MR = 256, NJ = 4;
+  // RA: an even step also reads the next step's operands (32-token items; 64-token items leave
+  // no registers for a second set). DA: the weight ring's depth in chunks.
+  static constexpr bool RA = TT == 2 && HH_MXA_RA;
+  static constexpr int DA = TT == 2 ? HH_MXA_DA : 2;
   static constexpr int B_INS = NTERM * NTOK / 8;            // 1 KB operand loads per chunk
   static constexpr int BPW = B_INS / 4;                     // per loader wave
   static constexpr int BS_DW = NTERM * NTOK;                // operand scale dwords per chunk
@@ -2430,13 +2448,27 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
   for (int u = 0; u < DA; ++u) load_a(ar[u]);
   bool done = false;
+  // Barrier k lands chunks 2k and 2k + 1: with RA an even step reads its own operands and the
+  // next (odd) step's, whose LDS latency then passes under the even step's MFMAs. DA is even and
+  // k0 a multiple of DA, so the parity of `step` is that of the unrolled copy u.
+  Ops nx;
   for (int k0 = 0; !done; k0 += DA) {
 #pragma unroll
     for (int u = 0; u < DA; ++u) {
       const int step = k0 + u;
+      if (PH == PH_UP) HH_TRS(step, 0);
       if (c == 0) task_begin();
-      // The step's token operands (read after its barrier: registers go to the weight ring).
-      Ops cur = read_ops(step % S);
+      Ops cur;
+      if (C::RA && (u & 1)) {
+        cur = nx;
+      } else {
+        cur = read_ops(step % S);
+        if (C::RA) nx = read_ops((step + 1) % S);   // past the last step: a stage no step reads
+      }
+#ifdef HH_TRACE_STEPS
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#endif
+      if (PH == PH_UP) HH_TRS(step, 1);
       const bool more = step + 1 < nsteps;
       if (128 * (c + 1) > K) {
         // A partial last chunk: lanes past K take zero weights and operand terms; their scale
@@ -2464,7 +2496,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
           for (int j = 0; j < NJ; ++j)
             acc[j][tt] = smfma(ar[u][j], cur.blo[t][tt], cur.bhi[t][tt], cur.sa[j], cur.bs[t][tt], acc[j][tt]);
+      if (PH == PH_UP) HH_TRS(step, 2);
       load_a(ar[u]);   // the chunk DA ahead into the slot just consumed
+      if (PH == PH_UP) HH_TRS(step, 3);
       if (++c == nch) {
         // ---- epilogue of the task ----
         c = 0;
@@ -2529,7 +2563,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         done = true;
         break;
       }
+      if (PH == PH_UP) HH_TRS(step, 4);
       if (step & 1) ring_barrier();   // one barrier per two chunks
+      if (PH == PH_UP) HH_TRS(step, 5);
     }
   }
 }
