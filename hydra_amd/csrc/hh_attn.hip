@@ -10,9 +10,10 @@
 // q_mult heads of a kv head each read the same key/value rows. Here a workgroup owns (kv head,
 // chunk of keys) and computes all q_mult (≤ 8) query heads of that kv head from one read of
 // each row, so HBM sees the history once per call. Each of the 4 waves takes 64-key tiles:
-//   phase 1, lane = key: the key row (head_dim fp16, 16-byte loads) against the q_mult queries
-//            (LDS broadcast reads), one fp32 logit per head; online softmax per head across the
-//            wave (max and sum reductions);
+//   phase 1, on the fp16 MFMA: S [64 keys × 16 head columns] = K·q^T with the key rows as the A
+//            operand (fp16, as stored) and the scaled queries as an fp16 pair hi + lo held in
+//            registers for the whole call (every product exact in fp32, q to ~2^-22); online
+//            softmax per head column (16 logits per lane, then the 4 lane groups);
 //   phase 2, lane = (key group, 8 dims): the value rows of its keys (16-byte loads), weighted by
 //            the tile's probabilities (LDS), into q_mult × 8 fp32 accumulators.
 // The waves' states merge in LDS and the workgroup writes an unnormalised partial (max, sum,
@@ -58,12 +59,13 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 template <int D>
 __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
-  constexpr int QM = kAttnQM, DG = D / 8, JG = 64 / DG, KPL = 64 / JG;
+  constexpr int QM = kAttnQM, DG = D / 8, JG = 64 / DG, KPL = 64 / JG, NDC = D / 32;
   __shared__ __align__(16) float s_q[QM][D];
   __shared__ __align__(16) float s_p[4][64][QM];
   __shared__ float s_m[4][QM], s_l[4][QM];
   __shared__ float s_acc[4][QM][D];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, l16 = lane & 15;
   const int kvh = blockIdx.x % a.kvh, chunk = blockIdx.x / a.kvh;
   const int qm = a.qh / a.kvh;
   const int h0 = kvh * qm;
@@ -72,16 +74,29 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     s_q[h][c] = h < qm ? a.q[(size_t)(h0 + h) * D + c] * a.scale : 0.f;
   }
   __syncthreads();
+  // The scaled queries as the B operand of the QK^T MFMAs: lane (g, l16) holds head l16's
+  // dimensions 32·dc + 8g .. +7 as an fp16 pair hi + lo (the fp32 value to ~2^-22 relative;
+  // each product with an fp16 key is exact in fp32); zero for heads ≥ qm.
+  f16x8 qhi[NDC], qlo[NDC];
+#pragma unroll
+  for (int dc = 0; dc < NDC; ++dc)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = l16 < QM ? s_q[l16][32 * dc + 8 * g + e] : 0.f;
+      const _Float16 hi = (_Float16)x;
+      qhi[dc][e] = hi;
+      qlo[dc][e] = (_Float16)(x - (float)hi);
+    }
   const int first = chunk * a.per_chunk;
   const int last = min(first + a.per_chunk, a.keys);
-  float M[QM], L[QM], acc[QM][8];
+  // Running maximum and denominator of head l16 (every lane group holds the same values).
+  float M = l16 < qm ? bf16_bits_to_f32(a.sinks[h0 + l16]) : 0.f;
+  float L = (chunk == 0 && wave == 0) ? 1.f : 0.f;
+  float acc[QM][8];
 #pragma unroll
-  for (int h = 0; h < QM; ++h) {
-    M[h] = h < qm ? bf16_bits_to_f32(a.sinks[h0 + h]) : 0.f;
-    L[h] = (chunk == 0 && wave == 0) ? 1.f : 0.f;
+  for (int h = 0; h < QM; ++h)
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[h][i] = 0.f;
-  }
   const size_t row_stride = (size_t)a.kvh * D;   // elements between cache rows
   auto row_of = [&](int key) -> size_t {
     const long long pos = (long long)a.start + key;
@@ -89,58 +104,66 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
   };
   const int jg = lane / DG, dg = lane - jg * DG;
   for (int base = first + 64 * wave; base < last; base += 256) {
-    // Phase 1: lane = key base + lane.
-    const int key = base + lane;
-    const bool valid = key < last;
-    // The tile's key rows (lane = key) and value rows (lane = key group, dims) are both issued
-    // before any arithmetic: one memory latency per tile. Rows past the chunk read row `first`
-    // (in bounds) and are masked.
-    f16x8 kr[DG], vr[KPL];
-    {
-      const f16x8 *kp = (const f16x8 *)(a.k + row_of(valid ? key : first) * row_stride + (size_t)kvh * D);
+    // The tile's key rows (16-key subtile st, lane (g, l16): key base + 16·st + l16, dimensions
+    // 32·dc + 8g .. +7) and value rows (lane = key group, dims) are all issued before any
+    // arithmetic: one memory latency per tile. Rows past the chunk read row `first` (in bounds)
+    // and are masked.
+    f16x8 kr[4][NDC], vr[KPL];
 #pragma unroll
-      for (int c = 0; c < DG; ++c) kr[c] = kp[c];
+    for (int st = 0; st < 4; ++st) {
+      const int key = base + 16 * st + l16;
+      const f16x8 *kp = (const f16x8 *)(a.k + row_of(key < last ? key : first) * row_stride + (size_t)kvh * D);
 #pragma unroll
-      for (int i = 0; i < KPL; ++i) {
-        const int j = base + jg * KPL + i;
-        vr[i] = *(const f16x8 *)(a.v + row_of(j < last ? j : first) * row_stride + (size_t)kvh * D + 8 * dg);
+      for (int dc = 0; dc < NDC; ++dc) kr[st][dc] = kp[4 * dc + g];
+    }
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      const int j = base + jg * KPL + i;
+      vr[i] = *(const f16x8 *)(a.v + row_of(j < last ? j : first) * row_stride + (size_t)kvh * D + 8 * dg);
+    }
+    // Phase 1: S = K·q^T on the fp16 MFMA; sc[st][i] is the logit of key base + 16·st + 4g + i
+    // for head l16.
+    f32x4 sc[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      sc[st] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int dc = 0; dc < NDC; ++dc) {
+        sc[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[st][dc], qhi[dc], sc[st], 0, 0, 0);
+        sc[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[st][dc], qlo[dc], sc[st], 0, 0, 0);
       }
     }
-    float s[QM];
+    // Online softmax of head l16 over the tile's 64 keys: 16 per lane, then the 4 lane groups.
+    float mt = -INFINITY;
 #pragma unroll
-    for (int h = 0; h < QM; ++h) s[h] = 0.f;
-    if (valid) {
+    for (int st = 0; st < 4; ++st)
 #pragma unroll
-      for (int c = 0; c < DG; ++c) {
-        float kf[8];
+      for (int i = 0; i < 4; ++i)
+        if (base + 16 * st + 4 * g + i < last) mt = fmaxf(mt, sc[st][i]);
+    mt = fmaxf(mt, __shfl_xor(mt, 16));
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    const float mn = fmaxf(M, mt);
+    const float corr = __expf(M - mn);
+    float ps = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) kf[e] = (float)kr[c][e];
+    for (int st = 0; st < 4; ++st)
 #pragma unroll
-        for (int h = 0; h < QM; ++h) {
-          // 16-byte broadcast reads of the query (every lane reads the same address).
-          const f32x4 qa = *(const f32x4 *)&s_q[h][8 * c], qb = *(const f32x4 *)&s_q[h][8 * c + 4];
-          s[h] = fmaf(qa[0], kf[0], s[h]);
-          s[h] = fmaf(qa[1], kf[1], s[h]);
-          s[h] = fmaf(qa[2], kf[2], s[h]);
-          s[h] = fmaf(qa[3], kf[3], s[h]);
-          s[h] = fmaf(qb[0], kf[4], s[h]);
-          s[h] = fmaf(qb[1], kf[5], s[h]);
-          s[h] = fmaf(qb[2], kf[6], s[h]);
-          s[h] = fmaf(qb[3], kf[7], s[h]);
-        }
+      for (int i = 0; i < 4; ++i) {
+        const int k = 16 * st + 4 * g + i;
+        const float p = base + k < last ? __expf(sc[st][i] - mn) : 0.f;
+        ps += p;
+        if (l16 < QM) s_p[wave][k][l16] = p;
       }
-    }
+    ps += __shfl_xor(ps, 16);
+    ps += __shfl_xor(ps, 32);
+    L = L * corr + ps;
+    M = mn;
+    // Every lane rescales its accumulators by each head's factor (lane h holds head h's).
 #pragma unroll
     for (int h = 0; h < QM; ++h) {
-      const float mt = wave_max(valid ? s[h] : -INFINITY);
-      const float mn = fmaxf(M[h], mt);
-      const float corr = __expf(M[h] - mn);
-      const float p = valid ? __expf(s[h] - mn) : 0.f;
-      L[h] = L[h] * corr + wave_sum(p);
-      M[h] = mn;
-      s_p[wave][lane][h] = p;
+      const float ch = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), h));
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[h][i] *= corr;
+      for (int i = 0; i < 8; ++i) acc[h][i] *= ch;
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -167,13 +190,9 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     for (int e = 0; e < 8; ++e)
 #pragma unroll
       for (int o = DG; o < 64; o <<= 1) acc[h][e] += __shfl_xor(acc[h][e], o);
-  if (lane < QM) {
-#pragma unroll
-    for (int h = 0; h < QM; ++h)
-      if (lane == h) {
-        s_m[wave][h] = M[h];
-        s_l[wave][h] = L[h];
-      }
+  if (lane < QM) {   // lane h: head h's state
+    s_m[wave][lane] = M;
+    s_l[wave][lane] = L;
   }
   if (jg == 0) {
 #pragma unroll
