@@ -14,8 +14,10 @@
 //            operand (fp16, as stored) and the scaled queries as an fp16 pair hi + lo held in
 //            registers for the whole call (every product exact in fp32, q to ~2^-22); online
 //            softmax per head column (16 logits per lane, then the 4 lane groups);
-//   phase 2, lane = (key group, 8 dims): the value rows of its keys (16-byte loads), weighted by
-//            the tile's probabilities (LDS), into q_mult × 8 fp32 accumulators.
+//   phase 2, on the fp16 MFMA: O [16 head rows × head_dim] += P·V, with the probabilities as an
+//            fp16 pair hi + lo straight from the phase-1 registers (the MFMA's k order follows
+//            the lanes' keys) and the value tile staged in the wave's LDS rows (16-byte loads in,
+//            column reads out).
 // The waves' states merge in LDS and the workgroup writes an unnormalised partial (max, sum,
 // head_dim sums) per (query head, chunk); attn_merge_kernel combines the chunks of a head in
 // chunk order. As in the reference, every partial starts from the sink as its running maximum
@@ -59,9 +61,10 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 template <int D>
 __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
-  constexpr int QM = kAttnQM, DG = D / 8, JG = 64 / DG, KPL = 64 / JG, NDC = D / 32;
+  constexpr int QM = kAttnQM, DG = D / 8, JG = 64 / DG, KPL = 64 / JG, NDC = D / 32, NN = D / 16;
+  constexpr int VST = D + 4;   // halves per staged value row: rows 4 keys apart land 8 banks apart
   __shared__ __align__(16) float s_q[QM][D];
-  __shared__ __align__(16) float s_p[4][64][QM];
+  __shared__ __align__(16) _Float16 s_v[4][64 * VST];
   __shared__ float s_m[4][QM], s_l[4][QM];
   __shared__ float s_acc[4][QM][D];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -92,22 +95,22 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
   // Running maximum and denominator of head l16 (every lane group holds the same values).
   float M = l16 < qm ? bf16_bits_to_f32(a.sinks[h0 + l16]) : 0.f;
   float L = (chunk == 0 && wave == 0) ? 1.f : 0.f;
-  float acc[QM][8];
+  // Unnormalised output: acc[n][i] = head 4g + i, dimension 16n + l16 (the PV MFMA's layout).
+  f32x4 acc[NN];
 #pragma unroll
-  for (int h = 0; h < QM; ++h)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[h][i] = 0.f;
+  for (int n = 0; n < NN; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
   const size_t row_stride = (size_t)a.kvh * D;   // elements between cache rows
   auto row_of = [&](int key) -> size_t {
     const long long pos = (long long)a.start + key;
     return (size_t)(a.ring > 0 ? pos % a.ring : pos);
   };
   const int jg = lane / DG, dg = lane - jg * DG;
+  _Float16 *sv = s_v[wave];
   for (int base = first + 64 * wave; base < last; base += 256) {
     // The tile's key rows (16-key subtile st, lane (g, l16): key base + 16·st + l16, dimensions
-    // 32·dc + 8g .. +7) and value rows (lane = key group, dims) are all issued before any
-    // arithmetic: one memory latency per tile. Rows past the chunk read row `first` (in bounds)
-    // and are masked.
+    // 32·dc + 8g .. +7) and value rows (lane (jg, dg): keys jg·KPL .. +KPL−1, dimensions
+    // 8·dg .. +7) are all issued before any arithmetic: one memory latency per tile. Rows past
+    // the chunk read row `first` (in bounds) and are masked (their probabilities are zero).
     f16x8 kr[4][NDC], vr[KPL];
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
@@ -133,6 +136,14 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
         sc[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[st][dc], qlo[dc], sc[st], 0, 0, 0);
       }
     }
+    // The value tile into the wave's LDS rows (row = key − base), read back column-wise below.
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      const u32x4 w = __builtin_bit_cast(u32x4, vr[i]);
+      u32x2 *dst = (u32x2 *)(sv + (jg * KPL + i) * VST + 8 * dg);
+      dst[0] = u32x2{w[0], w[1]};
+      dst[1] = u32x2{w[2], w[3]};
+    }
     // Online softmax of head l16 over the tile's 64 keys: 16 per lane, then the 4 lane groups.
     float mt = -INFINITY;
 #pragma unroll
@@ -145,76 +156,71 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     const float mn = fmaxf(M, mt);
     const float corr = __expf(M - mn);
     float ps = 0.f;
+    // P as the A operand of the PV MFMAs (head l16's row; k index (kc, g, e) stands for key
+    // 16·(2kc + e/4) + 4g + e%4, the lane's own logits), as an fp16 pair hi + lo.
+    f16x8 phi[2], plo[2];
 #pragma unroll
     for (int st = 0; st < 4; ++st)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int k = 16 * st + 4 * g + i;
-        const float p = base + k < last ? __expf(sc[st][i] - mn) : 0.f;
+        const float p = base + 16 * st + 4 * g + i < last ? __expf(sc[st][i] - mn) : 0.f;
         ps += p;
-        if (l16 < QM) s_p[wave][k][l16] = p;
+        const _Float16 hi = (_Float16)p;
+        phi[st >> 1][4 * (st & 1) + i] = hi;
+        plo[st >> 1][4 * (st & 1) + i] = (_Float16)(p - (float)hi);
       }
     ps += __shfl_xor(ps, 16);
     ps += __shfl_xor(ps, 32);
     L = L * corr + ps;
     M = mn;
-    // Every lane rescales its accumulators by each head's factor (lane h holds head h's).
+    // Lane (g, l16) holds output rows 4g .. 4g + 3: their heads' rescale factors.
 #pragma unroll
-    for (int h = 0; h < QM; ++h) {
-      const float ch = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), h));
+    for (int i = 0; i < 4; ++i) {
+      const float ci = __shfl(corr, 4 * g + i);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[h][i] *= ch;
+      for (int n = 0; n < NN; ++n) acc[n][i] *= ci;
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    // Phase 2: lane = (key group jg, dims 8·dg .. 8·dg + 7).
+    // Phase 2: O[h][d] += Σ_key P[h][key]·V[key][d] on the fp16 MFMA; B = the value column
+    // 16n + l16 at the lane's keys (the k order of P), read from the staged rows.
 #pragma unroll
-    for (int i = 0; i < KPL; ++i) {
-      const int j = jg * KPL + i;
-      const f16x8 vv = vr[i];   // a masked key has p = 0
-      const f32x4 pa = *(const f32x4 *)&s_p[wave][j][0], pb = *(const f32x4 *)&s_p[wave][j][4];
-      const float pj[QM] = {pa[0], pa[1], pa[2], pa[3], pb[0], pb[1], pb[2], pb[3]};
+    for (int n = 0; n < NN; ++n)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float vf = (float)vv[e];
+      for (int kc = 0; kc < 2; ++kc) {
+        f16x8 vb;
 #pragma unroll
-        for (int h = 0; h < QM; ++h) acc[h][e] = fmaf(pj[h], vf, acc[h][e]);
+        for (int e = 0; e < 8; ++e) vb[e] = sv[(16 * (2 * kc + (e >> 2)) + 4 * g + (e & 3)) * VST + 16 * n + l16];
+        acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(phi[kc], vb, acc[n], 0, 0, 0);
+        acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(plo[kc], vb, acc[n], 0, 0, 0);
       }
-    }
-    __builtin_amdgcn_wave_barrier();   // s_p is rewritten by the next tile
+    __builtin_amdgcn_wave_barrier();   // the staged rows are rewritten by the next tile
   }
-  // Sum the key groups of the wave (lanes with the same dg), then merge the waves in LDS.
-#pragma unroll
-  for (int h = 0; h < QM; ++h)
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-#pragma unroll
-      for (int o = DG; o < 64; o <<= 1) acc[h][e] += __shfl_xor(acc[h][e], o);
+  // The waves' states merge in LDS.
   if (lane < QM) {   // lane h: head h's state
     s_m[wave][lane] = M;
     s_l[wave][lane] = L;
   }
-  if (jg == 0) {
 #pragma unroll
-    for (int h = 0; h < QM; ++h)
+  for (int i = 0; i < 4; ++i)
+    if (4 * g + i < QM)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s_acc[wave][h][8 * dg + e] = acc[h][e];
-  }
+      for (int n = 0; n < NN; ++n) s_acc[wave][4 * g + i][16 * n + l16] = acc[n][i];
   __syncthreads();
   for (int i = tid; i < qm * D; i += 256) {
     const int h = i / D, c = i - h * D;
-    float g = s_m[0][h];
-    for (int w = 1; w < 4; ++w) g = fmaxf(g, s_m[w][h]);
+    float gm = s_m[0][h];
+    for (int w = 1; w < 4; ++w) gm = fmaxf(gm, s_m[w][h]);
     float den = 0.f, o = 0.f;
     for (int w = 0; w < 4; ++w) {
-      const float f = __expf(s_m[w][h] - g);
+      const float f = __expf(s_m[w][h] - gm);
       den += s_l[w][h] * f;
       o += s_acc[w][h][c] * f;
     }
     const size_t slot = (size_t)(h0 + h) * a.chunks + chunk;
     a.pout[slot * D + c] = o;
     if (c == 0) {
-      a.pmax[slot] = g;
+      a.pmax[slot] = gm;
       a.pden[slot] = den;
     }
   }
