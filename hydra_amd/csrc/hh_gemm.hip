@@ -2823,7 +2823,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     return o;
   };
 
+  // The two chains of the canonical arithmetic. MLX: acc[c & 1] with c static per half-stage.
+  // BF16 (a stage is part of one chunk): acc[0] holds the chain of chunk parity cpar and acc[1] the
+  // other; they trade places when the parity changes (at most once per chunk), so the MFMAs
+  // address fixed registers, and the epilogue's acc[0] + acc[1] is the same sum either way (fp
+  // addition commutes).
   f32x4 acc[2][NM][NT];
+  int cpar = 0;
   auto zero = [&]() {
 #pragma unroll
     for (int p = 0; p < 2; ++p)
@@ -2831,6 +2837,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int m = 0; m < NM; ++m)
 #pragma unroll
         for (int st = 0; st < NT; ++st) acc[p][m][st] = f32x4{0.f, 0.f, 0.f, 0.f};
+    cpar = 0;
   };
   zero();
   int tau = tasks.first(), slot = 0, ls = 0, nst = 0, K = 0, e = 0, ntok = 0, rt = 0;
@@ -2841,6 +2848,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   BOps curb;
   if constexpr (C::RA_B) curb = read_b(0);
   for (int step = 0;; ++step) {
+    if (PH == PH_UP) HH_TRS(step, 0);
     if (ls == 0) {
       const uint8_t *info = lds + C::OFF_INFO + C::INFO * slot;
       const int4 it = *(const int4 *)info;
@@ -2867,6 +2875,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       if constexpr (C::RA_B) nxtb = read_b(st_n);
     }
     if constexpr (!C::RA_B) curb = read_b(step % S);
+#ifdef HH_TRACE_STEPS
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#endif
+    if (PH == PH_UP) HH_TRS(step, 1);
     if constexpr (FMT == Q_BF16) {
       const int c = (SCOLS * ls) >> 7;
       auto steps = [&](f32x4 (&ac)[NM][NT]) {
@@ -2883,9 +2895,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                 ac[m][st] = mfma(as_bf16x8(cur.w[0][m].w[j]), as_bf16x8(curb.b[0][st][hh][j]), ac[m][st]);
         }
       };
-      // Chain by chunk parity, with static register indices.
-      if (c & 1) steps(acc[1]);
-      else steps(acc[0]);
+      if ((c & 1) != cpar) {
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+          for (int st = 0; st < NT; ++st) {
+            const f32x4 t = acc[0][m][st];
+            acc[0][m][st] = acc[1][m][st];
+            acc[1][m][st] = t;
+          }
+        cpar ^= 1;
+      }
+      steps(acc[0]);
     } else {
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
@@ -2927,8 +2948,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     } else {
       ++ls;
     }
+    if (PH == PH_UP) HH_TRS(step, 2);
     if (!more) break;
     ring_barrier();
+    if (PH == PH_UP) HH_TRS(step, 3);
     cur = nxt;
     if constexpr (C::RA_B) curb = nxtb;
   }
