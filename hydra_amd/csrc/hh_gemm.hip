@@ -2588,8 +2588,9 @@ template <int PH, int FMT, int RT, int NT_> struct Ring {
   static constexpr int NM = (PH == PH_UP ? 2 : 1) * RT;
   static constexpr int NH = PH == PH_UP ? 1 : 2;
   static constexpr bool MLX = is_mlx<FMT>();
-  // K columns per stage: two MLX groups; BF16 two 32-column steps, one for wide token tiles.
-  static constexpr int SCOLS = MLX ? 128 : (NT >= 4 ? 32 : 64);
+  // K columns per stage: two MLX groups; BF16 two 32-column steps (128-column stages leave
+  // 64-token tiles too few stages in LDS).
+  static constexpr int SCOLS = MLX ? 128 : 64;
   static constexpr int SPS = MLX ? 2 : SCOLS / 32;              // MLX groups / BF16 steps per stage
   static constexpr int SEGS = SCOLS / 8;                        // 16-byte segments per token row
   static constexpr int RPI = 1024 / (SCOLS * 2);                // token rows per 1 KiB load
@@ -2609,7 +2610,8 @@ template <int PH, int FMT, int RT, int NT_> struct Ring {
   static constexpr int OFF_INFO = S * STAGE;
   static constexpr int LDS = OFF_INFO + NSLOT * INFO;
   static constexpr int ROWS = 64 * RT;
-  // The B operand of the next stage is read ahead too, except for wide token tiles (registers).
+  // The B operand of the next stage is read ahead too, except for wide token tiles (measured
+  // slower there: gate-up 567 → 617 µs).
   static constexpr bool RA_B = NT <= 2;
   static_assert(B_INS % 4 == 0 && S >= 3 && NM <= 4 && LDS <= 160 * 1024, "ring layout");
   __device__ static int swz(int n) {
