@@ -417,12 +417,15 @@ template <int FMT, int NM, int DA> struct AStream {
   // returns a saturating stream at the rate it accepts new loads, so the later chunks' data is
   // not delayed, while the MFMAs of the early chunks overlap the stream and the workgroup's
   // staging barrier (before the first chunk) waits only for loads issued ahead of it.
-  template <bool ONE = false, int P = DA, class Pre, class Body>
+  // NC > 0 (ONE only): the stream's chunk count is NC, known at compile time, so the per-chunk
+  // guards vanish and the unrolled chunks form one straight block (no register copies at merges).
+  template <bool ONE = false, int P = DA, int NC = 0, class Pre, class Body>
   __device__ __forceinline__ void run_pf(const ATile<FMT> (&at)[NM], int nch, int g, int K, Pre pre, Body body) {
     static_assert(P == DA || ONE, "a partial fill needs the single-round stream");
+    static_assert(NC == 0 || (ONE && NC <= DA), "a static chunk count needs the single-round stream");
     if (n <= 0) return;
     if constexpr (ONE) {
-      rounds<true, true, P>(at, nch, g, K, pre, body);
+      rounds<true, true, P, NC>(at, nch, g, K, pre, body);
     } else {
       if (n <= DA && c0 == 0 && cs == 1) rounds<true, true>(at, nch, g, K, pre, body);
       else if (n <= DA) rounds<true, false>(at, nch, g, K, pre, body);
@@ -431,21 +434,21 @@ template <int FMT, int NM, int DA> struct AStream {
   }
   // UNIT: chunk u of the ring is chunk u of K (one round, first chunk 0, stride 1), so chunk
   // indices, and the operand offsets derived from them, are compile-time constants.
-  template <bool ONE, bool UNIT, int P = DA, class Pre, class Body>
+  template <bool ONE, bool UNIT, int P = DA, int NC = 0, class Pre, class Body>
   __device__ __forceinline__ void rounds(const ATile<FMT> (&at)[NM], int nch, int g, int K, Pre pre, Body body) {
     auto op = pre(UNIT ? 0 : c0);
     for (int i0 = 0; i0 < n; i0 += DA) {
       const bool more = !ONE && i0 + DA < n;
 #pragma unroll
       for (int u = 0; u < DA; ++u) {
-        if (i0 + u < n) {
+        if (NC > 0 ? u < NC : i0 + u < n) {
           const int cn = UNIT ? min(u + 1, DA - 1) : c0 + cs * min(i0 + u + 1, n - 1);
           const auto nx = pre(cn);
           body(s[u], UNIT ? u : c0 + cs * (i0 + u), op);
           op = nx;
         }
         if constexpr (P < DA) {
-          if (u + P < DA) load(u + P, at, u + P, nch, g, K);
+          if (u + P < (NC > 0 ? NC : DA)) load(u + P, at, u + P, nch, g, K);
         }
         if (more) load(u, at, i0 + u + DA, nch, g, K);
       }
@@ -865,9 +868,11 @@ __device__ __forceinline__ MxOps<NTERM> mx_ops(const uint8_t *brow, int RS, int 
 // chunk_mx for one tile and one token tile with pre-read operands, which come from rows staged by
 // MxStage (zero past K, scales 2^0 there): the same values mx_b's masks give. Lanes whose weight
 // block lies past K take zero weights, as in chunk_mx.
+// `full`: the chunk lies wholly inside K (no lane needs the test).
 template <int NTERM>
-__device__ __forceinline__ void chunk_mx1(f32x4 &acc, const u32x4 &w, const MxOps<NTERM> &o, int c, int g, int K) {
-  const u32x4 wv = Fmt<Q_MXFP4>::lane_valid(c, g, K) ? w : u32x4{0u, 0u, 0u, 0u};
+__device__ __forceinline__ void chunk_mx1(f32x4 &acc, const u32x4 &w, const MxOps<NTERM> &o, int c, int g, int K,
+                                          bool full = false) {
+  const u32x4 wv = (full || Fmt<Q_MXFP4>::lane_valid(c, g, K)) ? w : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
   for (int t = 0; t < NTERM; ++t) acc = smfma(wv, o.b[t].lo, o.b[t].hi, o.sa & 0xFFu, o.b[t].s, acc);
 }
@@ -991,7 +996,8 @@ __device__ __forceinline__ MxStage<NTERM, NB, RowOf, DEV> mx_stage(uint8_t *dst,
 // through LDS. The gate waves combine gate and up and write the block's activations to LDS; wave
 // 0 writes them as NTH fp8 terms. Each item issues its whole weight stream at once; co-resident
 // workgroups hide one another's latency.
-template <int DA, bool ONE, int XB>
+// NCH > 0 (ONE only): every row of the layer has exactly NCH chunks (checked on the host).
+template <int DA, bool ONE, int XB, int NCH = 0>
 __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) {
   constexpr int NM = 1;
   extern __shared__ __align__(16) uint8_t s_xb[];   // [T][NTX] rows of mx_row_bytes(xld), then [64][H/32] scales
@@ -1097,10 +1103,10 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
     const int my_t = nth_bit(tm, min(l16, ntok - 1));   // token of column l16 (padding repeats)
     const uint8_t *brow = s_xb + (size_t)my_t * NTX * RS;
     f32x4 acc[NM][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
-    as.template run_pf<ONE, PF>(
+    as.template run_pf<ONE, PF, NCH>(
         at, nch, gi, H, [&](int c) { return mx_ops<NTX>(brow, RS, a.xld, my_sc, nsb, c, gi); },
         [&](const Fmt<Q_MXFP4_W>::A (&w)[NM], int c, const MxOps<NTX> &o) {
-          chunk_mx1<NTX>(acc[0][0], w[0].w, o, c, gi, H);
+          chunk_mx1<NTX>(acc[0][0], w[0].w, o, c, gi, H, NCH > 0 && c < NCH - 1);
         });
     const f32x4 res = acc[0][0];
     if (is_up) s_up[q][lane] = res;
@@ -1149,7 +1155,8 @@ __device__ __forceinline__ void down_small_item(int it, int T, int &rt, int &t) 
 // shared expert), chunk parity p when KS = 2 (both chains in one wave when KS = 1). The epilogue
 // sums the chains, then the slots in rank order (sum_expert_slices, dense.metal:147;
 // ReferenceLayer.swift:194-202). SMAX = the most slots a token has under this instantiation.
-template <int FMT, int DA, int SMAX, int KS>
+// NCH > 0 (MXFP4, single round): every slot's row has exactly NCH chunks (checked on the host).
+template <int FMT, int DA, int SMAX, int KS, int NCH = 0>
 __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const int32_t *topk_idx) {
   constexpr int NM = 1;
   extern __shared__ __align__(16) uint16_t s_h[];   // [slots][2][ldh + LDS_PAD]
@@ -1218,10 +1225,10 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
     const uint8_t *brow = my_lds;
     const uint8_t *my_sc = s_sc + l16 * nsb;
     // MXFP4: one chain. DA ≥ MX_ONE instantiations run only for rows of at most DA chunks.
-    as.template run_pf<(DA >= MX_ONE_CHUNKS), PF>(
+    as.template run_pf<(DA >= MX_ONE_CHUNKS), PF, NCH>(
         aw, nch, g, I, [&](int c) { return mx_ops<NTH>(brow, RS, a.hld, my_sc, nsb, c, g); },
         [&](const Fmt<Q_MXFP4_W>::A (&w)[NM], int c, const MxOps<NTH> &o) {
-          chunk_mx1<NTH>(acc[0][0][0], w[0].w, o, c, g, I);
+          chunk_mx1<NTH>(acc[0][0][0], w[0].w, o, c, g, I, NCH > 0 && c < NCH - 1);
         });
   } else {
   // This slot's activation (hi, lo) into LDS (the slot's two waves share it): the loads go out
@@ -2981,8 +2988,12 @@ constexpr int MX_ONE = MX_ONE_CHUNKS;
 // batches issue twelve per thread before the selection, so T ≤ 8 stages in one round (T = 8 took
 // four).
 constexpr int MX_XB_WIDE = 12;
-template <int FMT> static UpSmallKernel up_small_k(bool one, int T) {
+// Rows of exactly MX_STATIC chunks (K = 2817..2944: GPT-OSS's 2880) take variants with the chunk
+// count compiled in (`st`).
+constexpr int MX_STATIC = 23;
+template <int FMT> static UpSmallKernel up_small_k(bool one, int T, bool st = false) {
   if constexpr (FMT == Q_MXFP4) {
+    if (one && st) return T == 1 ? up_small_mx<MX_ONE, true, 2, MX_STATIC> : up_small_mx<MX_ONE, true, MX_XB_WIDE, MX_STATIC>;
     if (T == 1) return one ? up_small_mx<MX_ONE, true, 2> : up_small_mx<16, false, 2>;
     return one ? up_small_mx<MX_ONE, true, MX_XB_WIDE> : up_small_mx<16, false, MX_XB_WIDE>;
   }
@@ -2993,11 +3004,13 @@ template <int FMT> static UpSmallKernel up_small_k(bool one, int T) {
 // slot); the others split K by chunk parity over two waves when the workgroup has room.
 template <int FMT> constexpr int down_ks(int slots) { return (FMT == Q_MXFP4 || slots > 4) ? 1 : 2; }
 
-template <int FMT> static DownSmallKernel down_small_k(int slots, bool one) {
+template <int FMT> static DownSmallKernel down_small_k(int slots, bool one, bool st = false) {
   // Nine waves leave a third of the register file per wave: a shallower ring (also the MXFP4
   // kernel for rows longer than MX_ONE chunks).
   constexpr int D9 = decode_depth<FMT>() > 8 ? 8 : decode_depth<FMT>();
   if (slots > 4 || !one) return down_small<FMT, D9, kMaxTopK + 1, 1>;
+  if constexpr (FMT == Q_MXFP4)
+    if (st) return down_small<FMT, decode_depth<FMT>(), 4, down_ks<FMT>(4), MX_STATIC>;
   return down_small<FMT, decode_depth<FMT>(), 4, down_ks<FMT>(4)>;
 }
 
@@ -3191,7 +3204,17 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
   UpSmallKernel up;
   DownSmallKernel down;
   switch (quant) {
-  case Q_MXFP4: up = up_small_k<Q_MXFP4>(one_up, T); down = down_small_k<Q_MXFP4>(S, one_down); break;
+  case Q_MXFP4: {
+    // The static-count variants need every row of the phase at MX_STATIC chunks: the up rows run
+    // over H, the down rows over each expert group's intermediate size (the second group only
+    // when a shared slot exists).
+    const bool st_up = (a.hidden + 127) / 128 == MX_STATIC;
+    const bool st_down = (a.grp[0].inter + 127) / 128 == MX_STATIC &&
+                         (S == a.top_k || (a.grp[1].inter + 127) / 128 == MX_STATIC);
+    up = up_small_k<Q_MXFP4>(one_up, T, st_up);
+    down = down_small_k<Q_MXFP4>(S, one_down, st_down);
+    break;
+  }
   case Q_BF16: up = up_small_k<Q_BF16>(true, T); down = down_small_k<Q_BF16>(S, true); break;
   case Q_MLX4: up = up_small_k<Q_MLX4>(true, T); down = down_small_k<Q_MLX4>(S, true); break;
   default: up = up_small_k<Q_MLX8>(true, T); down = down_small_k<Q_MLX8>(S, true); break;
@@ -3208,7 +3231,9 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
                         (const void *)down_small_k<Q_MXFP4>(4, true), (const void *)down_small_k<Q_BF16>(4, true),
                         (const void *)down_small_k<Q_MLX4>(4, true), (const void *)down_small_k<Q_MLX8>(4, true),
                         (const void *)down_small_k<Q_MXFP4>(9, true), (const void *)down_small_k<Q_BF16>(9, true),
-                        (const void *)down_small_k<Q_MLX4>(9, true), (const void *)down_small_k<Q_MLX8>(9, true)};
+                        (const void *)down_small_k<Q_MLX4>(9, true), (const void *)down_small_k<Q_MLX8>(9, true),
+                        (const void *)up_small_k<Q_MXFP4>(true, 1, true), (const void *)up_small_k<Q_MXFP4>(true, SMALL_T, true),
+                        (const void *)down_small_k<Q_MXFP4>(4, true, true)};
     // Best effort: HIP on gfx950 accepts launches up to the hardware LDS size without it, and
     // a runtime that rejects the attribute must not leave its error for the launch check below.
     for (const void *k : ks) {
