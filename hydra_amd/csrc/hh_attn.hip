@@ -61,6 +61,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 template <int D>
 __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
+  warm_kernargs<sizeof(AttnArgs)>();
   constexpr int QM = kAttnQM, DG = D / 8, JG = 64 / DG, KPL = 64 / JG, NDC = D / 32, NN = D / 16;
   constexpr int VST = D + 4;   // halves per staged value row: rows 4 keys apart land 8 banks apart
   __shared__ __align__(16) float s_q[QM][D];
@@ -231,6 +232,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
 // the chunks in order, loads issued eight chunks at a time.
 template <int D>
 __global__ __launch_bounds__(64) void attn_merge_kernel(AttnArgs a) {
+  warm_kernargs<sizeof(AttnArgs)>();
   __shared__ float s_f[kAttnMaxChunks];
   const int h = blockIdx.x, lane = threadIdx.x;
   const float *pm = a.pmax + (size_t)h * a.chunks, *pd = a.pden + (size_t)h * a.chunks;

@@ -208,6 +208,20 @@ struct RouteArgs {
   int32_t max_work;
 };
 
+// The kernel's argument block into the scalar cache in one round: one dword of each 64-byte line
+// is read at entry and the reads are awaited together. Otherwise each field is read where it is
+// first used, and every line's first touch is a round trip of its own on a cold compute unit
+// (the argument reads of a decode kernel form chains of several).
+template <size_t BYTES> __device__ __forceinline__ void warm_kernargs() {
+  const uint32_t *k = (const uint32_t *)__builtin_amdgcn_kernarg_segment_ptr();
+  uint32_t x = 0;
+#pragma unroll
+  for (size_t i = 0; i < (BYTES + 63) / 64; ++i) x ^= k[16 * i];
+  __builtin_amdgcn_sched_barrier(0);   // nothing that waits on a field is scheduled among the reads
+  asm volatile("" ::"s"(x));
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // Optional profiling events of a launch sequence: `start` is attached to the first kernel's
 // dispatch packet and `stop` to the last one's (hipExtLaunchKernelGGL), so the interval covers
 // exactly the kernels' execution, as a kernel trace would. Null events launch normally.

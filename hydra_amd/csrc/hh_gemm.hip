@@ -701,6 +701,7 @@ constexpr int LDS_PAD = 8;        // bf16 elements of padding per staged row (ba
 // workgroups of half the size, which spreads a decode step's few experts over more compute units.
 template <int FMT, int DA, int TPW, int XB>
 __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) {
+  warm_kernargs<sizeof(GemmArgs) + sizeof(RouteArgs)>();
   constexpr int NTH = 256 * TPW, NWV = 4 * TPW, ROWS = 16 * TPW;
   constexpr int NM = 1;
   extern __shared__ __align__(16) uint16_t s_x[];   // [ntok][H + LDS_PAD]
@@ -931,7 +932,11 @@ template <int NTERM, int NB, class RowOf, bool DEV = false> struct MxStage {
     n = nrows * NTERM * per_row;
   }
   __device__ __forceinline__ u32x4 src(int v) const {
-    const int rr = v / per_row, qq = v - rr * per_row;
+    const int rr = v / per_row;
+    return src_at(rr, v - rr * per_row);
+  }
+  // Vector qq of staged row rr.
+  __device__ __forceinline__ u32x4 src_at(int rr, int qq) const {
     const size_t grow = (size_t)row_of(rr / NTERM) * NTERM + rr % NTERM;
     // One load from a selected address (two loads under a lane-dependent branch would serialise).
     const uint8_t *p = qq < dv ? q + grow * ld + 16 * qq : sc + grow * (ld / 32) + 16 * (qq - dv);
@@ -945,7 +950,10 @@ template <int NTERM, int NB, class RowOf, bool DEV = false> struct MxStage {
   // Scale bytes of blocks at or past `cols` (the tail of the last scale vector) are stored as 127
   // (2^0), so the MFMA operands of the last chunk need no masks.
   __device__ __forceinline__ void put(int v, u32x4 val) const {
-    const int rr = v / per_row, qq = v - rr * per_row;
+    const int rr = v / per_row;
+    put_at(rr, v - rr * per_row, val);
+  }
+  __device__ __forceinline__ void put_at(int rr, int qq, u32x4 val) const {
     if (qq >= dv) {
       const int nvalid = cols / 32 - 16 * (qq - dv);
 #pragma unroll
@@ -965,15 +973,46 @@ template <int NTERM, int NB, class RowOf, bool DEV = false> struct MxStage {
       *(u32x4 *)(dst + (size_t)rr * RS + cols + 16 * (v - rr * nz)) = u32x4{0u, 0u, 0u, 0u};
     }
   }
+  // The (row, vector) coordinates of vectors id, id + threads, ...: one division, then a step of
+  // `threads` vectors (under a row when threads < per_row, so one carry at most; otherwise the
+  // whole rows of the step are added first).
+  struct Walk {
+    int rr, qq, dr, dq;
+  };
+  __device__ __forceinline__ Walk walk() const {
+    Walk w;
+    w.rr = id / per_row;
+    w.qq = id - w.rr * per_row;
+    w.dr = threads / per_row;
+    w.dq = threads - w.dr * per_row;
+    return w;
+  }
+  __device__ __forceinline__ void step(Walk &w) const {
+    w.rr += w.dr;
+    w.qq += w.dq;
+    if (w.qq >= per_row) {
+      w.qq -= per_row;
+      ++w.rr;
+    }
+  }
   // Unconditional (clamped) loads keep the completion counts exact.
   __device__ __forceinline__ void load_first() {
+    const int rl = (n - 1) / per_row, ql = n - 1 - rl * per_row;
+    Walk w = walk();
 #pragma unroll
-    for (int k = 0; k < NB; ++k) r[k] = src(min(id + threads * k, n - 1));
+    for (int k = 0; k < NB; ++k) {
+      const bool in = id + threads * k < n;
+      r[k] = src_at(in ? w.rr : rl, in ? w.qq : ql);
+      step(w);
+    }
   }
   __device__ __forceinline__ void store_first() {
+    Walk w = walk();
 #pragma unroll
-    for (int k = 0; k < NB; ++k)
-      if (id + threads * k < n) put(id + threads * k, r[k]);
+    for (int k = 0; k < NB; ++k) {
+      if (id + threads * k < n) put_at(w.rr, w.qq, r[k]);
+      step(w);
+    }
   }
   __device__ __forceinline__ void rest() {
     for (int base = threads * NB; base < n; base += threads * 4)
@@ -999,6 +1038,7 @@ __device__ __forceinline__ MxStage<NTERM, NB, RowOf, DEV> mx_stage(uint8_t *dst,
 // NCH > 0 (ONE only): every row of the layer has exactly NCH chunks (checked on the host).
 template <int DA, bool ONE, int XB, int NCH = 0>
 __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) {
+  warm_kernargs<sizeof(GemmArgs) + sizeof(RouteArgs)>();
   constexpr int NM = 1;
   extern __shared__ __align__(16) uint8_t s_xb[];   // [T][NTX] rows of mx_row_bytes(xld), then [64][H/32] scales
   __shared__ int s_idx[SMALL_T * kMaxTopK];
@@ -1158,6 +1198,7 @@ __device__ __forceinline__ void down_small_item(int it, int T, int &rt, int &t) 
 // NCH > 0 (MXFP4, single round): every slot's row has exactly NCH chunks (checked on the host).
 template <int FMT, int DA, int SMAX, int KS, int NCH = 0>
 __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const int32_t *topk_idx) {
+  warm_kernargs<sizeof(GemmArgs) + sizeof(void *)>();
   constexpr int NM = 1;
   extern __shared__ __align__(16) uint16_t s_h[];   // [slots][2][ldh + LDS_PAD]
   __shared__ f32x4 s_odd[KS > 1 ? SMAX : 1][4];     // odd chain, lanes l16 == 0
@@ -1175,6 +1216,7 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
   down_small_item(it, T, rt, t);
   if (rt >= a.row_tiles) continue;       // padding item (uniform over the workgroup)
   const int slot = t * S + r;
+  if (it == (int)blockIdx.x) HH_TR(2, 6);
   const int e = r < K ? topk_idx[t * K + r] : E;
   const int gsel = e == E ? 1 : 0;
   const ExpertGroup &grp = a.grp[gsel];
@@ -1212,6 +1254,7 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
     constexpr int PF = DA >= MX_ONE_CHUNKS ? MX_PF : DA;
     AStream<Q_MXFP4_W, NM, DA> as(0, 1, nch);
     as.template fill<PF>(aw, nch, g, I);
+    if (it == (int)blockIdx.x) HH_TR(2, 5);
 #pragma unroll
     for (int k = 0; k < 2; ++k)
       if (sid + sth * k < nsv) *(u32x4 *)(s_sc + 16 * (sid + sth * k)) = scv[k];

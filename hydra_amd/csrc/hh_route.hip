@@ -493,6 +493,7 @@ __device__ __forceinline__ void quant_x_wave_block(const RouteArgs &a, int t, in
 
 template <bool gemma>
 __global__ __launch_bounds__(256) void logits_small_kernel(RouteArgs a) {
+  warm_kernargs<sizeof(RouteArgs)>();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int E = a.experts, E1 = E + 1, H = a.hidden;
   const int p = blockIdx.x * 4 + wave;
@@ -526,6 +527,7 @@ __global__ __launch_bounds__(256) void logits_small_kernel(RouteArgs a) {
 constexpr int BLK_W = 8;
 __host__ __device__ constexpr int block_logit_groups(int E) { return (E + 1 + BLK_W - 1) / BLK_W; }
 __global__ __launch_bounds__(64 * BLK_W) void logits_block_kernel(RouteArgs a) {
+  warm_kernargs<sizeof(RouteArgs)>();
   __shared__ __align__(16) uint16_t s_xn[4096];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int E = a.experts, E1 = E + 1, H = a.hidden;
@@ -629,6 +631,7 @@ __global__ __launch_bounds__(64 * BLK_W) void logits_block_kernel(RouteArgs a) {
 // Top-k and weights of every token from lg64 (operator entry hh_router_topk, T ≤ 16): one
 // workgroup, wave w takes tokens w, w + 4, ...
 __global__ __launch_bounds__(256) void select_small_kernel(RouteArgs a) {
+  warm_kernargs<sizeof(RouteArgs)>();
   const int wave = threadIdx.x >> 6;
   const int E1 = a.experts + 1;
   __shared__ int s_ri[4][kMaxTopK];
@@ -662,6 +665,7 @@ __device__ __forceinline__ uint32_t mlx_code(const u32x4 &q, int s) {
 
 template <int BITS>
 __global__ __launch_bounds__(64) void mlx_router_logits_kernel(RouteArgs a) {
+  warm_kernargs<sizeof(RouteArgs)>();
   const int lane = threadIdx.x, g = lane >> 4, l16 = lane & 15;
   const int E = a.experts, H = a.hidden, T = a.tokens;
   const int rows = E + (a.shared_gate ? 1 : 0);
@@ -710,6 +714,7 @@ __global__ __launch_bounds__(64) void mlx_router_logits_kernel(RouteArgs a) {
 
 // Top-k and weights of every token from lg64, one wave per token (batches with an MLX router).
 __global__ __launch_bounds__(256) void select_lg64_kernel(RouteArgs a) {
+  warm_kernargs<sizeof(RouteArgs)>();
   const int wave = threadIdx.x >> 6;
   const int t = blockIdx.x * 4 + wave;
   __shared__ int s_ri[4][kMaxTopK];
