@@ -212,8 +212,11 @@ struct TokenScreen {
 
 // Screens token t (one wave): bounds every fp32 logit lgf(e) by err_e, θ = the K-th largest
 // lower bound, and writes the candidates {e : ub_e ≥ θ} to cl[] in ascending order.
-template <bool gemma, class LG, class WN>
-__device__ __forceinline__ TokenScreen screen_token(const RouteArgs &a, int t, LG lgf, WN wnf, int *cl) {
+// NW > 1: the NW waves of the workgroup screen the same token together (identical results in
+// every wave); the 64-lane ranking splits over them through s_rk [NW][64].
+template <bool gemma, int NW = 1, class LG, class WN>
+__device__ __forceinline__ TokenScreen screen_token(const RouteArgs &a, int t, LG lgf, WN wnf, int *cl,
+                                                    int (*s_rk)[64] = nullptr) {
   const int lane = threadIdx.x & 63;
   const int E = a.experts, H = a.hidden, K = a.top_k;
   const uint16_t *xr = a.xr + (size_t)t * H;
@@ -276,9 +279,21 @@ __device__ __forceinline__ TokenScreen screen_token(const RouteArgs &a, int t, L
 #pragma unroll
   for (int j = 0; j < 8; ++j) mx = fmaxf(mx, lb[j]);
   int rk = 0;
-  for (int j = 0; j < 64; ++j) {
-    const float o = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx), j));
-    rk += (o > mx || (o == mx && j < lane)) ? 1 : 0;
+  {
+    const int j0 = NW > 1 ? (64 / NW) * (int)(threadIdx.x >> 6) : 0;
+#pragma unroll 4
+    for (int jj = 0; jj < 64 / NW; ++jj) {
+      const int j = j0 + jj;
+      const float o = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx), j));
+      rk += (o > mx || (o == mx && j < lane)) ? 1 : 0;
+    }
+  }
+  if constexpr (NW > 1) {
+    s_rk[threadIdx.x >> 6][lane] = rk;
+    __syncthreads();
+    rk = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) rk += s_rk[w][lane];
   }
   const float tau = __builtin_bit_cast(
       float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx), __ffsll((unsigned long long)__ballot(rk == K - 1)) - 1));
@@ -325,79 +340,6 @@ __device__ __forceinline__ TokenScreen screen_token(const RouteArgs &a, int t, L
   return ts;
 }
 
-// ---- large batches ---------------------------------------------------------------------------
-// A: one workgroup per (16-token tile, 16-expert tile), the 4 waves splitting K; writes the
-// screening logits lg32 [T][E] and, from the first token tile, ‖w_e‖.
-template <bool gemma>
-__global__ __launch_bounds__(256) void route_logits_kernel(RouteArgs a) {
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int g = lane >> 4, l16 = lane & 15;
-  const int E = a.experts, T = a.tokens;
-  const int ntiles = (E + 15) / 16;
-  const int tt = blockIdx.x / ntiles, et = blockIdx.x - tt * ntiles;
-  const int t0 = tt * RT_TOK;
-  const int ntok = min(RT_TOK, T - t0);
-  __shared__ float s_part[4][16][16];   // [wave][expert in tile][token]
-  __shared__ float s_wpart[4][16];
-  float wsq;
-  const f32x4 acc = tile_logits<gemma>(a, t0, ntok, et, wave, 4, wsq);
-#pragma unroll
-  for (int ii = 0; ii < 4; ++ii) s_part[wave][4 * g + ii][l16] = acc[ii];
-  if (g == (l16 >> 2)) s_wpart[wave][l16] = wsq;
-  __syncthreads();
-  const int el = tid >> 4, tk = tid & 15;
-  const int e = et * 16 + el;
-  if (e < E && tk < ntok) {
-    float v = ((s_part[0][el][tk] + s_part[1][el][tk]) + s_part[2][el][tk]) + s_part[3][el][tk];
-    if (a.router_b) v += bf16_bits_to_f32(a.router_b[e]);
-    a.lg32[(size_t)(t0 + tk) * E + e] = v;
-    if (tt == 0 && tk == 0)
-      a.wn[e] = sqrtf(((s_wpart[0][el] + s_wpart[1][el]) + s_wpart[2][el]) + s_wpart[3][el]);
-  }
-}
-
-// B: one wave per token: screen, then the exact logits of its candidates in ascending order.
-template <bool gemma>
-__global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
-  const int wave = threadIdx.x >> 6;
-  const int t = blockIdx.x * 4 + wave;
-  __shared__ int s_cl[4][kMaxExperts];
-  if (t >= a.tokens) return;
-  const float *lg = a.lg32 + (size_t)t * a.experts;
-  const float *wn = a.wn;
-  const TokenScreen ts = screen_token<gemma>(a, t, [&](int e) { return lg[e]; },
-                                      [&](int e) { return wn[e]; }, s_cl[wave]);
-  // Exact logits of the candidates, four at a time (one memory latency per batch), inserted in
-  // ascending expert order.
-  TopK tk;
-  const double root = gemma ? pow((double)a.hidden, -0.5) : 1.0;
-  const uint16_t *xr = a.xr + (size_t)t * a.hidden;
-  for (int c0 = 0; c0 < ts.nc; c0 += 4) {
-    int e[4];
-    const uint16_t *rows[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      e[r] = s_cl[wave][min(c0 + r, ts.nc - 1)];
-      rows[r] = a.router_w + (size_t)e[r] * a.hidden;
-    }
-    double v[4];
-    exact_logits_rows<gemma, 4>(a, xr, rows, ts.norm, root, v);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      if (c0 + r >= ts.nc) break;
-      if (a.router_b) v[r] += (double)bf16_bits_to_f32(a.router_b[e[r]]);
-      tk.insert(v[r], e[r], a.top_k);
-    }
-  }
-  const double sg = a.shared_gate ? exact_logit<false>(a, a.x + (size_t)t * a.hidden, a.shared_gate, 1.0, 1.0) : 0.0;
-  finish_token(a, t, tk, sg);
-}
-
-// C.
-__global__ __launch_bounds__(1024) void dispatch_kernel(RouteArgs a) {
-  dispatch_batch<16>(a, a.topk_idx);
-}
-
 // ---- x as fp8 terms (MXFP4 layers) ----------------------------------------------------------------
 // One wave quantises 16 blocks of 32 columns of token t (quant_block): lane (g, l16) takes block
 // blk0 + l16, columns 8g .. 8g+7 of it.
@@ -425,6 +367,90 @@ __device__ __forceinline__ void quant_x_wave(const RouteArgs &a, int t, int blk0
 
 __device__ __forceinline__ int quant_x_waves(const RouteArgs &a) {
   return a.xq ? a.tokens * ((a.hidden / 32 + 15) / 16) : 0;
+}
+
+// ---- large batches ---------------------------------------------------------------------------
+// A: one workgroup per (16-token tile, 16-expert tile), the 4 waves splitting K; writes the
+// screening logits lg32 [T][E] and, from the first token tile, ‖w_e‖. Workgroups past the
+// tiles quantise x (MXFP4 layers), one wave per 16 blocks of a token.
+template <bool gemma>
+__global__ __launch_bounds__(256) void route_logits_kernel(RouteArgs a) {
+  warm_kernargs<sizeof(RouteArgs)>();
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int g = lane >> 4, l16 = lane & 15;
+  const int E = a.experts, T = a.tokens;
+  const int ntiles = (E + 15) / 16;
+  const int nlog = ((T + RT_TOK - 1) / RT_TOK) * ntiles;
+  if ((int)blockIdx.x >= nlog) {
+    const int w = ((int)blockIdx.x - nlog) * 4 + wave;
+    const int per_t = (a.hidden / 32 + 15) / 16;
+    if (w < quant_x_waves(a)) quant_x_wave(a, w / per_t, 16 * (w % per_t));
+    return;
+  }
+  const int tt = blockIdx.x / ntiles, et = blockIdx.x - tt * ntiles;
+  const int t0 = tt * RT_TOK;
+  const int ntok = min(RT_TOK, T - t0);
+  __shared__ float s_part[4][16][16];   // [wave][expert in tile][token]
+  __shared__ float s_wpart[4][16];
+  float wsq;
+  const f32x4 acc = tile_logits<gemma>(a, t0, ntok, et, wave, 4, wsq);
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) s_part[wave][4 * g + ii][l16] = acc[ii];
+  if (g == (l16 >> 2)) s_wpart[wave][l16] = wsq;
+  __syncthreads();
+  const int el = tid >> 4, tk = tid & 15;
+  const int e = et * 16 + el;
+  if (e < E && tk < ntok) {
+    float v = ((s_part[0][el][tk] + s_part[1][el][tk]) + s_part[2][el][tk]) + s_part[3][el][tk];
+    if (a.router_b) v += bf16_bits_to_f32(a.router_b[e]);
+    a.lg32[(size_t)(t0 + tk) * E + e] = v;
+    if (tt == 0 && tk == 0)
+      a.wn[e] = sqrtf(((s_wpart[0][el] + s_wpart[1][el]) + s_wpart[2][el]) + s_wpart[3][el]);
+  }
+}
+
+// B: one workgroup per token. Its 4 waves screen the token together, then wave w computes the
+// exact logits of candidates w, w + 4, ... (each row in exact_logits_rows' arithmetic, so the
+// values do not depend on how rows are grouped) and wave 1 the shared gate's; wave 0 ranks them
+// (TopK's order: larger value, then smaller index, whatever the insertion order) and writes the
+// token's routing.
+template <bool gemma>
+__global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
+  warm_kernargs<sizeof(RouteArgs)>();
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x;
+  __shared__ int s_cl[4][kMaxExperts];
+  __shared__ int s_rk[4][64];
+  __shared__ double s_v[kMaxExperts];
+  __shared__ double s_sg;
+  const float *lg = a.lg32 + (size_t)t * a.experts;
+  const float *wn = a.wn;
+  const TokenScreen ts = screen_token<gemma, 4>(a, t, [&](int e) { return lg[e]; },
+                                                [&](int e) { return wn[e]; }, s_cl[wave], s_rk);
+  const double root = gemma ? pow((double)a.hidden, -0.5) : 1.0;
+  const uint16_t *xr = a.xr + (size_t)t * a.hidden;
+  for (int c = wave; c < ts.nc; c += 4) {
+    const int e = s_cl[wave][c];
+    const uint16_t *rows[1] = {a.router_w + (size_t)e * a.hidden};
+    double v[1];
+    exact_logits_rows<gemma, 1>(a, xr, rows, ts.norm, root, v);
+    if (a.router_b) v[0] += (double)bf16_bits_to_f32(a.router_b[e]);
+    if (lane == 0) s_v[c] = v[0];
+  }
+  if (wave == 1 && a.shared_gate) {
+    const double sg = exact_logit<false>(a, a.x + (size_t)t * a.hidden, a.shared_gate, 1.0, 1.0);
+    if (lane == 0) s_sg = sg;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  TopK tk;
+  for (int c = 0; c < ts.nc; ++c) tk.insert(s_v[c], s_cl[0][c], a.top_k);
+  finish_token(a, t, tk, a.shared_gate ? s_sg : 0.0);
+}
+
+// C.
+__global__ __launch_bounds__(1024) void dispatch_kernel(RouteArgs a) {
+  dispatch_batch<16>(a, a.topk_idx);
 }
 
 // Batches above 16 tokens: one wave per 16 blocks of a token.
@@ -786,16 +812,12 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s, Timing tm) {
   const int etiles = (a.experts + 15) / 16;
   const bool third = a.want_dispatch != 0;
   const bool g = a.router == R_GEMMA;
-  hipExtLaunchKernelGGL(g ? route_logits_kernel<true> : route_logits_kernel<false>, dim3(ttiles * etiles), dim3(256), 0, s, tm.start,
-                        nullptr, 0, a);
+  const int qw = a.xq ? a.tokens * ((a.hidden / 32 + 15) / 16) : 0;
+  hipExtLaunchKernelGGL(g ? route_logits_kernel<true> : route_logits_kernel<false>,
+                        dim3(ttiles * etiles + (qw + 3) / 4), dim3(256), 0, s, tm.start, nullptr, 0, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (a.xq) {
-    const int qw = a.tokens * ((a.hidden / 32 + 15) / 16);
-    hipExtLaunchKernelGGL(quant_x_kernel, dim3((qw + 3) / 4), dim3(256), 0, s, nullptr, nullptr, 0, a);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
-  hipExtLaunchKernelGGL(g ? route_select_kernel<true> : route_select_kernel<false>, dim3((a.tokens + 3) / 4), dim3(256), 0, s, nullptr,
+  hipExtLaunchKernelGGL(g ? route_select_kernel<true> : route_select_kernel<false>, dim3(a.tokens), dim3(256), 0, s, nullptr,
                         third ? nullptr : tm.stop, 0, a);
   e = hipGetLastError();
   if (e != hipSuccess || !third) return e;
