@@ -97,6 +97,28 @@ __device__ __forceinline__ void quant_block(const float (&v)[8], uint32_t (&q)[N
   }
 }
 
+// quant_block with one value per lane, the block held by the 32 lanes of a half wave (lane & 31
+// = position in the block): the same term bytes and scales, since the block maximum is the same
+// and every other step is per element. q[t] holds the value's byte of term t.
+template <int NTERM>
+__device__ __forceinline__ void quant_lane(float v, uint32_t (&q)[NTERM], uint32_t (&sb)[NTERM]) {
+  float amax = fabsf(v);
+#pragma unroll
+  for (int m = 1; m < 32; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
+  const int eb = (int)((__float_as_uint(amax) >> 23) & 0xFF);
+  const int b0 = eb > 7 ? eb - 7 : 0;
+  float r = v;
+#pragma unroll
+  for (int t = 0; t < NTERM; ++t) {
+    const int bt = b0 - 4 * t > 0 ? b0 - 4 * t : 0;
+    sb[t] = (uint32_t)bt;
+    const float y = fminf(fmaxf(__builtin_amdgcn_ldexpf(r, 127 - bt), -448.f), 448.f);
+    const int w = __builtin_amdgcn_cvt_pk_fp8_f32(y, 0.f, 0, false);
+    q[t] = (uint32_t)w & 0xFFu;
+    if (t + 1 < NTERM) r -= __builtin_amdgcn_ldexpf(__builtin_amdgcn_cvt_f32_fp8(w, 0), bt - 127);
+  }
+}
+
 // ---- gated activations (device twins of the oracle's act_pair) ------------------------------
 __device__ __forceinline__ float activate(int act, float g, float u, float alpha, float limit) {
   if (act == A_SWIGLU_OAI) {

@@ -1042,7 +1042,8 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
   constexpr int NM = 1;
   extern __shared__ __align__(16) uint8_t s_xb[];   // [T][NTX] rows of mx_row_bytes(xld), then [64][H/32] scales
   __shared__ int s_idx[SMALL_T * kMaxTopK];
-  __shared__ f32x4 s_up[2][64];
+  __shared__ f32x4 s_up[2][64], s_gate[2][64];
+  __shared__ u32x4 s_bias[2][4];
   __shared__ float s_hv[SMALL_T][UP_ROWS];
   __shared__ double s_lg[4][64];
   __shared__ int s_ri[4][kMaxTopK];
@@ -1149,27 +1150,66 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
           chunk_mx1<NTX>(acc[0][0], w[0].w, o, c, gi, H, NCH > 0 && c < NCH - 1);
         });
     const f32x4 res = acc[0][0];
-    if (is_up) s_up[q][lane] = res;
-    __syncthreads();
-    if (it == (int)blockIdx.x) HH_TR(1, 3);
-    if (!is_up && l16 < ntok) {
-      const f32x4 y = up_values_mx(a, bias, res, s_up[q][lane]);
+    if (nitems > (int)gridDim.x) {
+      // Workgroups with further items: the gate waves form the activations and wave 0 writes the
+      // terms, while the other waves go on to the next item's weight stream.
+      if (is_up) s_up[q][lane] = res;
+      __syncthreads();
+      if (it == (int)blockIdx.x) HH_TR(1, 3);
+      if (!is_up && l16 < ntok) {
+        const f32x4 y = up_values_mx(a, bias, res, s_up[q][lane]);
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) s_hv[l16][16 * q + 4 * g + ii] = y[ii];
+        for (int ii = 0; ii < 4; ++ii) s_hv[l16][16 * q + 4 * g + ii] = y[ii];
+      }
+      __syncthreads();
+      if (wave == 0) {
+        // Lane (g, l16): activations 8g .. 8g+7 of the block of token column l16.
+        const int j = min(l16, ntok - 1);
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = s_hv[j][8 * g + i];
+        uint32_t hq[NTH][2], sb[NTH];
+        quant_block<NTH>(v, hq, sb);
+        if (l16 < ntok) {
+          const int t = nth_bit(tm, l16);
+          const int slot = t * S + rank_of(s_idx, t, e, K, sh);
+          store_hq(a, slot, rt, rt * UP_ROWS + 8 * g, rt * UP_ROWS + 8 * g + 4, hq, sb, g);
+        }
+      }
+      if (it == (int)blockIdx.x) HH_TR(1, 4);
+      continue;
+    }
+    // One item per workgroup: the epilogue spread over the workgroup, one (token column j,
+    // intermediate k) per thread: the gate and up sums (lane (g, l16) of tile q holds
+    // intermediates 16q + 4g + ii of column l16) and the gate bias through LDS, the activation,
+    // then the block's NTH fp8 terms with the block on the 32 lanes of a half wave (quant_lane:
+    // quant_block's bytes). Its dependent chain is a fraction of the one-wave epilogue's.
+    if (is_up) {
+      s_up[q][lane] = res;
+    } else {
+      s_gate[q][lane] = res;
+      if (l16 == 0) s_bias[q][g] = bias;
     }
     __syncthreads();
-    if (wave == 0) {
-      // Lane (g, l16): activations 8g .. 8g+7 of the block of token column l16.
-      const int j = min(l16, ntok - 1);
-      float v[8];
+    if (it == (int)blockIdx.x) HH_TR(1, 3);
+    const int nv = ntok * UP_ROWS;
+    for (int i = tid; i < nv; i += 256) {
+      const int j = i >> 5, k = i & 31, kq = k >> 4, kg = (k >> 2) & 3, ii = k & 3;
+      const uint32_t bb = s_bias[kq][kg][ii];
+      s_hv[j][k] = activate(a.act, s_gate[kq][16 * kg + j][ii] + bf16_bits_to_f32(bb & 0xFFFFu),
+                            s_up[kq][16 * kg + j][ii] + bf16_bits_to_f32(bb >> 16), a.alpha, a.limit);
+    }
+    __syncthreads();
+    for (int i = tid; i < nv; i += 256) {   // whole half waves: nv is a multiple of 32
+      const int j = i >> 5, k = i & 31;
+      uint32_t hq[NTH], sb[NTH];
+      quant_lane<NTH>(s_hv[j][k], hq, sb);
+      const int t = nth_bit(tm, j);
+      const int slot = t * S + rank_of(s_idx, t, e, K, sh);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[i] = s_hv[j][8 * g + i];
-      uint32_t hq[NTH][2], sb[NTH];
-      quant_block<NTH>(v, hq, sb);
-      if (l16 < ntok) {
-        const int t = nth_bit(tm, l16);
-        const int slot = t * S + rank_of(s_idx, t, e, K, sh);
-        store_hq(a, slot, rt, rt * UP_ROWS + 8 * g, rt * UP_ROWS + 8 * g + 4, hq, sb, g);
+      for (int tt = 0; tt < NTH; ++tt) {
+        a.hq[((size_t)slot * NTH + tt) * a.hld + rt * UP_ROWS + k] = (uint8_t)hq[tt];
+        if (k == 0) a.hs[((size_t)slot * NTH + tt) * (a.hld / 32) + rt] = (uint8_t)sb[tt];
       }
     }
     if (it == (int)blockIdx.x) HH_TR(1, 4);

@@ -65,13 +65,29 @@ __device__ __forceinline__ void dispatch_batch(const RouteArgs &a, const int32_t
     }
     return peers;
   };
-  for (int base = lo; base < hi; base += 64) {
-    const int i = base + lane;
-    const bool valid = i < hi;
-    const int e = valid ? idx[i] : 0;
-    const uint64_t peers = peers_of(valid, e);
-    if (valid && __popcll(peers & ((1ull << lane) - 1ull)) == 0) s_wc[wave][e] += __popcll(peers);
-    __builtin_amdgcn_wave_barrier();
+  // The wave's expert ids are read DCH chunks at a time, all loads issued before the first is
+  // used (one memory latency per DCH chunks, not per chunk).
+  constexpr int DCH = 16;
+  int ev[DCH];
+  auto load_ids = [&](int b0) {
+#pragma unroll
+    for (int k = 0; k < DCH; ++k) {
+      const int i = b0 + 64 * k + lane;
+      ev[k] = i < hi ? idx[i] : 0;
+    }
+  };
+  for (int b0 = lo; b0 < hi; b0 += 64 * DCH) {
+    load_ids(b0);
+#pragma unroll
+    for (int k = 0; k < DCH; ++k) {
+      const int base = b0 + 64 * k;
+      if (base >= hi) break;
+      const bool valid = base + lane < hi;
+      const int e = ev[k];
+      const uint64_t peers = peers_of(valid, e);
+      if (valid && __popcll(peers & ((1ull << lane) - 1ull)) == 0) s_wc[wave][e] += __popcll(peers);
+      __builtin_amdgcn_wave_barrier();
+    }
   }
   __syncthreads();
   // Per expert: total count, and each wave's first position relative to the expert's segment.
@@ -89,19 +105,25 @@ __device__ __forceinline__ void dispatch_batch(const RouteArgs &a, const int32_t
   __syncthreads();
   block_exclusive_scan<NW>(s_off, E, s_wave);
   const int routed_tiles = block_exclusive_scan<NW>(s_tiles, E, s_wave);
-  for (int base = lo; base < hi; base += 64) {
-    const int i = base + lane;
-    const bool valid = i < hi;
-    const int e = valid ? idx[i] : 0;
-    const uint64_t peers = peers_of(valid, e);
-    const int rank = __popcll(peers & ((1ull << lane) - 1ull));
-    if (valid) {
-      const int t = i / K, r = i - t * K;
-      a.order[s_off[e] + s_wc[wave][e] + rank] = t * a.slots + r;
+  for (int b0 = lo; b0 < hi; b0 += 64 * DCH) {
+    load_ids(b0);
+#pragma unroll
+    for (int k = 0; k < DCH; ++k) {
+      const int base = b0 + 64 * k;
+      if (base >= hi) break;
+      const int i = base + lane;
+      const bool valid = i < hi;
+      const int e = ev[k];
+      const uint64_t peers = peers_of(valid, e);
+      const int rank = __popcll(peers & ((1ull << lane) - 1ull));
+      if (valid) {
+        const int t = i / K, r = i - t * K;
+        a.order[s_off[e] + s_wc[wave][e] + rank] = t * a.slots + r;
+      }
+      __builtin_amdgcn_wave_barrier();
+      if (valid && rank == 0) s_wc[wave][e] += __popcll(peers);
+      __builtin_amdgcn_wave_barrier();
     }
-    __builtin_amdgcn_wave_barrier();
-    if (valid && rank == 0) s_wc[wave][e] += __popcll(peers);
-    __builtin_amdgcn_wave_barrier();
   }
   __syncthreads();
   // Segments and work items (expert, first position, tokens), ascending expert order.
@@ -158,9 +180,9 @@ __device__ __forceinline__ void router_operand(bool gemma, const u32x4 &xv, cons
 // wsq, Σw² of row l16 over the same columns (in the lanes of group l16 / 4; the caller sums
 // the K slices). Σw² is accumulated in fp32 like the logits: its relative error (≤ H·2^-24)
 // is far inside the factor 4 of slack the screening bound carries.
-// Chunks are loaded two at a time before either is used, so the loop costs about one memory
-// latency per two chunks.
-template <bool gemma>
+// Chunks are loaded NB at a time before any is used, so the loop costs about one memory
+// latency per NB chunks.
+template <bool gemma, int NB = 2>
 __device__ __forceinline__ f32x4 tile_logits(const RouteArgs &a, int t0, int ntok, int et, int kq, int nk,
                              float &wsq) {
   const int lane = threadIdx.x & 63, g = lane >> 4, l16 = lane & 15;
@@ -169,10 +191,10 @@ __device__ __forceinline__ f32x4 tile_logits(const RouteArgs &a, int t0, int nto
   const uint16_t *wrow = a.router_w + (size_t)min(et * 16 + l16, E - 1) * H;
   const int nch = (H + 127) / 128;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f}, wacc = {0.f, 0.f, 0.f, 0.f};
-  for (int c0 = kq; c0 < nch; c0 += 2 * nk) {
-    u32x4 wv[2][4], xv[2][4], sv[2][4];
+  for (int c0 = kq; c0 < nch; c0 += NB * nk) {
+    u32x4 wv[NB][4], xv[NB][4], sv[NB][4];
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < NB; ++b) {
       const int c = c0 + b * nk;
       const int col = min(128 * min(c, nch - 1) + 32 * g, H - 32);
       const bool ok = c < nch && 128 * c + 32 * g < H;
@@ -186,7 +208,7 @@ __device__ __forceinline__ f32x4 tile_logits(const RouteArgs &a, int t0, int nto
       }
     }
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < NB; ++b) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         u32x4 xh, xl;
@@ -370,11 +392,13 @@ __device__ __forceinline__ int quant_x_waves(const RouteArgs &a) {
 }
 
 // ---- large batches ---------------------------------------------------------------------------
-// A: one workgroup per (16-token tile, 16-expert tile), the 4 waves splitting K; writes the
-// screening logits lg32 [T][E] and, from the first token tile, ‖w_e‖. Workgroups past the
-// tiles quantise x (MXFP4 layers), one wave per 16 blocks of a token.
+// A: one workgroup per (16-token tile, 16-expert tile), its RLW waves splitting K (chunks
+// c ≡ wave mod RLW, loaded RLB at a time); writes the screening logits
+// lg32 [T][E] and, from the first token tile, ‖w_e‖. Workgroups past the tiles quantise x
+// (MXFP4 layers), one wave per 16 blocks of a token.
+constexpr int RLW = 4, RLB = 2;
 template <bool gemma>
-__global__ __launch_bounds__(256) void route_logits_kernel(RouteArgs a) {
+__global__ __launch_bounds__(64 * RLW) void route_logits_kernel(RouteArgs a) {
   warm_kernargs<sizeof(RouteArgs)>();
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, l16 = lane & 15;
@@ -382,7 +406,7 @@ __global__ __launch_bounds__(256) void route_logits_kernel(RouteArgs a) {
   const int ntiles = (E + 15) / 16;
   const int nlog = ((T + RT_TOK - 1) / RT_TOK) * ntiles;
   if ((int)blockIdx.x >= nlog) {
-    const int w = ((int)blockIdx.x - nlog) * 4 + wave;
+    const int w = ((int)blockIdx.x - nlog) * RLW + wave;
     const int per_t = (a.hidden / 32 + 15) / 16;
     if (w < quant_x_waves(a)) quant_x_wave(a, w / per_t, 16 * (w % per_t));
     return;
@@ -390,22 +414,32 @@ __global__ __launch_bounds__(256) void route_logits_kernel(RouteArgs a) {
   const int tt = blockIdx.x / ntiles, et = blockIdx.x - tt * ntiles;
   const int t0 = tt * RT_TOK;
   const int ntok = min(RT_TOK, T - t0);
-  __shared__ float s_part[4][16][16];   // [wave][expert in tile][token]
-  __shared__ float s_wpart[4][16];
+  __shared__ float s_part[RLW][16][16];   // [wave][expert in tile][token]
+  __shared__ float s_wpart[RLW][16];
   float wsq;
-  const f32x4 acc = tile_logits<gemma>(a, t0, ntok, et, wave, 4, wsq);
+  const f32x4 acc = tile_logits<gemma, RLB>(a, t0, ntok, et, wave, RLW, wsq);
 #pragma unroll
   for (int ii = 0; ii < 4; ++ii) s_part[wave][4 * g + ii][l16] = acc[ii];
   if (g == (l16 >> 2)) s_wpart[wave][l16] = wsq;
   __syncthreads();
   const int el = tid >> 4, tk = tid & 15;
   const int e = et * 16 + el;
-  if (e < E && tk < ntok) {
-    float v = ((s_part[0][el][tk] + s_part[1][el][tk]) + s_part[2][el][tk]) + s_part[3][el][tk];
+  // Pairwise over the waves' K slices (any order is inside the screening bound).
+  auto wsum = [&](auto get) {
+    float p[RLW];
+#pragma unroll
+    for (int w = 0; w < RLW; ++w) p[w] = get(w);
+#pragma unroll
+    for (int h = 1; h < RLW; h *= 2)
+#pragma unroll
+      for (int w = 0; w + h < RLW; w += 2 * h) p[w] += p[w + h];
+    return p[0];
+  };
+  if (tid < 256 && e < E && tk < ntok) {
+    float v = wsum([&](int w) { return s_part[w][el][tk]; });
     if (a.router_b) v += bf16_bits_to_f32(a.router_b[e]);
     a.lg32[(size_t)(t0 + tk) * E + e] = v;
-    if (tt == 0 && tk == 0)
-      a.wn[e] = sqrtf(((s_wpart[0][el] + s_wpart[1][el]) + s_wpart[2][el]) + s_wpart[3][el]);
+    if (tt == 0 && tk == 0) a.wn[e] = sqrtf(wsum([&](int w) { return s_wpart[w][el]; }));
   }
 }
 
@@ -450,6 +484,7 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
 
 // C.
 __global__ __launch_bounds__(1024) void dispatch_kernel(RouteArgs a) {
+  warm_kernargs<sizeof(RouteArgs)>();
   dispatch_batch<16>(a, a.topk_idx);
 }
 
@@ -814,7 +849,7 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s, Timing tm) {
   const bool g = a.router == R_GEMMA;
   const int qw = a.xq ? a.tokens * ((a.hidden / 32 + 15) / 16) : 0;
   hipExtLaunchKernelGGL(g ? route_logits_kernel<true> : route_logits_kernel<false>,
-                        dim3(ttiles * etiles + (qw + 3) / 4), dim3(256), 0, s, tm.start, nullptr, 0, a);
+                        dim3(ttiles * etiles + (qw + RLW - 1) / RLW), dim3(64 * RLW), 0, s, tm.start, nullptr, 0, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipExtLaunchKernelGGL(g ? route_select_kernel<true> : route_select_kernel<false>, dim3(a.tokens), dim3(256), 0, s, nullptr,
