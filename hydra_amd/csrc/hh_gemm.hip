@@ -48,6 +48,7 @@
 #include "hh_logit.hpp"
 
 #include <algorithm>
+#include <type_traits>
 #include <mutex>
 #include <vector>
 
@@ -168,6 +169,18 @@ template <int BITS> struct FmtMLX {
     }
     a.sb = (uint32_t)rw.sc[c] | ((uint32_t)rw.bi[c] << 16);
   }
+  // The codes only (the group's scale and bias come from elsewhere: MlxSb).
+  __device__ static void load_w(A &a, const Row &rw, int c, int g, int K) {
+    const uint8_t *p = rw.w + (64 * c + 16 * g) * BITS / 8;
+    if constexpr (BITS == 4) {
+      u32x2 v = *(const u32x2 *)p;
+      a.w[0] = v[0]; a.w[1] = v[1];
+    } else {
+      u32x4 v = *(const u32x4 *)p;
+      a.w[0] = v[0]; a.w[1] = v[1]; a.w[2] = v[2]; a.w[3] = v[3];
+    }
+    a.sb = 0u;
+  }
   __device__ static bf16x8 decode(const A &a, int j) {
     if constexpr (BITS == 4) return mlx4_to_bf16(a.w[j]);
     else return mlx8_to_bf16(a.w[2 * j], a.w[2 * j + 1]);
@@ -248,9 +261,12 @@ __device__ __forceinline__ void wave_tiles(ATile<FMT> (&t)[(PH == PH_UP ? 2 : 1)
 // The MFMA sequence of chunk c for NM A tiles × NT token tiles. `bv(st, hh, v)` returns the
 // lane's 8 B values of token tile st, term hh (x | h_hi, h_lo), step v, at columns
 // Fmt::bcol(c, g, K) + 8v.
-template <int FMT, int NM, int NT, int NH, class BV>
+// MLX: `sbf(m)`, when given, returns the (scale | bias << 16) words of D rows 4g .. 4g+3 of tile m
+// for this chunk; otherwise they come from the A operands' rows by shuffles.
+template <int FMT, int NM, int NT, int NH, class BV, class SBF = std::nullptr_t>
 __device__ __forceinline__ void chunk_mfma(f32x4 (&acc)[NM][NT], const typename Fmt<FMT>::A (&w)[NM],
-                                           const ATile<FMT> (&at)[NM], BV bv, int c, int g, int K) {
+                                           const ATile<FMT> (&at)[NM], BV bv, int c, int g, int K,
+                                           SBF sbf = nullptr) {
   using F = Fmt<FMT>;
   if constexpr (FMT == Q_BF16) {
 #pragma unroll
@@ -349,10 +365,16 @@ __device__ __forceinline__ void chunk_mfma(f32x4 (&acc)[NM][NT], const typename 
     // shuffles issued before the first is used).
 #pragma unroll
     for (int m = 0; m < NM; ++m) {
-      const int sbl = (int)w[m].sb;
       uint32_t sbs[4];
+      if constexpr (std::is_same_v<SBF, std::nullptr_t>) {
+        const int sbl = (int)w[m].sb;
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) sbs[ii] = (uint32_t)__shfl(sbl, 4 * g + ii);
+        for (int ii = 0; ii < 4; ++ii) sbs[ii] = (uint32_t)__shfl(sbl, 4 * g + ii);
+      } else {
+        const u32x4 v = sbf(m);
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) sbs[ii] = v[ii];
+      }
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
         const uint32_t sbv = sbs[ii];
@@ -376,7 +398,8 @@ __device__ __forceinline__ void chunk_mfma(f32x4 (&acc)[NM][NT], const typename 
 // chunk reload it, clamped, so the rounds before the last need no per-load test): a duplicate
 // load costs as much of the address/L1 path as a real one.
 template <int FMT> constexpr bool unit_stride() { return FMT == Q_MXFP4_W; }
-template <int FMT, int NM, int DA> struct AStream {
+// NOSB (MLX): the stream carries the codes only; the scales and biases are staged (MlxSb).
+template <int FMT, int NM, int DA, bool NOSB = false> struct AStream {
   typename Fmt<FMT>::A s[DA][NM];
   int c0, cs, n;   // first chunk, chunk stride, chunks of this wave
   __device__ __forceinline__ AStream(int first, int stride, int nch)
@@ -386,7 +409,10 @@ template <int FMT, int NM, int DA> struct AStream {
     if constexpr (unit_stride<FMT>()) c = c0 + i;
     else c = min(c0 + cs * min(i, max(n - 1, 0)), nch - 1);
 #pragma unroll
-    for (int m = 0; m < NM; ++m) Fmt<FMT>::load(s[slot][m], at[m].row, c, g, K);
+    for (int m = 0; m < NM; ++m) {
+      if constexpr (NOSB) Fmt<FMT>::load_w(s[slot][m], at[m].row, c, g, K);
+      else Fmt<FMT>::load(s[slot][m], at[m].row, c, g, K);
+    }
   }
   // The first P (default: all DA) stages; run_pf<ONE, P> issues the rest as it goes.
   template <int P = DA> __device__ __forceinline__ void fill(const ATile<FMT> (&at)[NM], int nch, int g, int K) {
@@ -659,6 +685,49 @@ __device__ __forceinline__ int rank_of(const int *s_idx, int t, int e, int K, bo
   return r;
 }
 
+// ---- MLX decode: group scales and biases staged per item ------------------------------------------
+// The (scale | bias << 16) word of every (chunk, row) of NTL 16-row tiles in LDS, sb[tile][chunk]
+// [row]: lane (g, l16) reads D rows 4g .. 4g+3 of a chunk as one 16-byte vector (chunk_mfma's
+// sbf), in place of two 2-byte loads per chunk in every lane of the weight stream and four
+// shuffles. `src(tile, kind, row)` is the row's first scale (kind 0) or bias (kind 1). Rows of a
+// multiple of 8 chunks come as 16-byte vectors of 8 values (loads issued by mlx_sb_load before
+// the weight stream, stored by mlx_sb_store after it); other rows value by value.
+constexpr int kMlxSbChunks = 64;   // staged chunks per row of the gate-up tiles: K ≤ 4096
+constexpr int kMlxSbChunksDown = 32;   // of the down tiles (one 16-row tile per 64·KS threads): K ≤ 2048
+constexpr int kMlxSbNB = 2;        // 16-byte vectors per thread (NTL · 32 · K/512 ≤ 2 · threads)
+template <int NTL, class Src>
+__device__ __forceinline__ void mlx_sb_load(u32x4 (&r)[kMlxSbNB], int nch, int tid, int nth, Src src) {
+  if (nch & 7) return;
+  const int vpr = nch >> 3, n = NTL * 32 * vpr;
+#pragma unroll
+  for (int k = 0; k < kMlxSbNB; ++k) {
+    const int v = min(tid + nth * k, n - 1);
+    const int row = (v / vpr) & 15, kind = (v / (16 * vpr)) & 1, tile = v / (32 * vpr);
+    r[k] = *(const u32x4 *)(src(tile, kind, row) + 8 * (v % vpr));
+  }
+}
+template <int NTL, int CH, class Src>
+__device__ __forceinline__ void mlx_sb_store(const u32x4 (&r)[kMlxSbNB], uint32_t (*sb)[CH][16], int nch,
+                                             int tid, int nth, Src src) {
+  if ((nch & 7) == 0) {
+    const int vpr = nch >> 3, n = NTL * 32 * vpr;
+#pragma unroll
+    for (int k = 0; k < kMlxSbNB; ++k) {
+      const int v = tid + nth * k;
+      if (v >= n) break;
+      const int row = (v / vpr) & 15, kind = (v / (16 * vpr)) & 1, tile = v / (32 * vpr), c0 = 8 * (v % vpr);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        ((uint16_t *)&sb[tile][c0 + j][row])[kind] = (uint16_t)(r[k][j >> 1] >> (16 * (j & 1)));
+    }
+  } else {
+    for (int v = tid; v < NTL * 32 * nch; v += nth) {
+      const int c = v % nch, row = (v / nch) & 15, kind = (v / (16 * nch)) & 1, tile = v / (32 * nch);
+      ((uint16_t *)&sb[tile][c][row])[kind] = src(tile, kind, row)[c];
+    }
+  }
+}
+
 // ---- decode: gate-up ----------------------------------------------------------------------------
 // Development timeline (built only with -DHH_TRACE): per workgroup, wall-clock stamps (100 MHz)
 // at fixed points of the decode kernels, [kernel][block][point]; the last call's values.
@@ -707,6 +776,8 @@ __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) 
   extern __shared__ __align__(16) uint16_t s_x[];   // [ntok][H + LDS_PAD]
   __shared__ int s_idx[SMALL_T * kMaxTopK];
   __shared__ f32x4 s_part[3][2][64];                // [gate odd | up even | up odd][q][lane]
+  constexpr bool SB = is_mlx<FMT>();                // MLX: scales and biases staged per item
+  __shared__ __align__(16) uint32_t s_sb[SB ? 2 * TPW : 1][SB ? kMlxSbChunks : 1][16];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -763,11 +834,19 @@ __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) 
     const uint8_t *blob = grp.blobs + (sh ? 0 : (size_t)e * grp.stride);
     const int rb = rt * ROWS + 16 * q;
     ATile<FMT> at[NM] = {tile_of<PH_UP, FMT>(blob, grp, rb, is_up, H, l16)};
+    // MLX tiles: gate rows of tile qq (tile index qq), then up rows (TPW + qq).
+    auto sb_src = [&](int tile, int kind, int row) {
+      const int mat = tile / TPW, orow = min(rt * ROWS + 16 * (tile % TPW) + row, grp.inter - 1);
+      return (const uint16_t *)(blob + grp.off[3 * mat + 1 + kind]) + (size_t)orow * (H / 64);
+    };
+    u32x4 sbr[kMlxSbNB];
+    if constexpr (SB) mlx_sb_load<2 * TPW>(sbr, nch, tid, NTH, sb_src);
     // The weight stream, then (first item) the x stores, which wait for the x loads only, and
-    // any further batches.
-    AStream<FMT, NM, DA> as(par, 2, nch);
+    // any further batches, and the staged scales and biases.
+    AStream<FMT, NM, DA, SB> as(par, 2, nch);
     as.fill(at, nch, g, H);
     if (x_pending) store_x();
+    if constexpr (SB) mlx_sb_store<2 * TPW, kMlxSbChunks>(sbr, s_sb, nch, tid, NTH, sb_src);
     __syncthreads();
     if (it == (int)blockIdx.x) HH_TR(1, 2);
 
@@ -775,10 +854,15 @@ __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) 
     const int my_t = nth_bit(tm, min(l16, ntok - 1));
     const uint16_t *brow = s_x + (size_t)my_t * ldx;
     f32x4 acc[NM][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
+    const int my_tile = (is_up ? TPW : 0) + q;
     as.run(at, nch, g, H, [&](const typename Fmt<FMT>::A (&w)[NM], int c) {
       const int col = Fmt<FMT>::bcol(c, g, H);
-      chunk_mfma<FMT, NM, 1, 1>(acc, w, at, [&](int, int, int v) { return *(const u32x4 *)(brow + col + Fmt<FMT>::VS * v); },
-                                c, g, H);
+      auto bv = [&](int, int, int v) { return *(const u32x4 *)(brow + col + Fmt<FMT>::VS * v); };
+      if constexpr (SB)
+        chunk_mfma<FMT, NM, 1, 1>(acc, w, at, bv, c, g, H,
+                                  [&](int) { return *(const u32x4 *)&s_sb[my_tile][c][4 * g]; });
+      else
+        chunk_mfma<FMT, NM, 1, 1>(acc, w, at, bv, c, g, H);
     });
     // Chains and gate/up meet in the (gate, even) wave of each tile. The next item's partials
     // are written only after its first barrier, which this item's epilogue wave reaches last.
@@ -1242,6 +1326,8 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
   constexpr int NM = 1;
   extern __shared__ __align__(16) uint16_t s_h[];   // [slots][2][ldh + LDS_PAD]
   __shared__ f32x4 s_odd[KS > 1 ? SMAX : 1][4];     // odd chain, lanes l16 == 0
+  constexpr bool SB = is_mlx<FMT>();                // MLX: each slot's scales and biases staged
+  __shared__ __align__(16) uint32_t s_sbd[SB ? SMAX : 1][SB ? kMlxSbChunksDown : 1][16];
   __shared__ float s_o[SMAX][16];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1334,20 +1420,33 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
 #pragma unroll
   for (int k = 0; k < HB; ++k)
     if (sid + sth * k < nvec) hr[k] = hsrc(sid + sth * k);
-  AStream<FMT, NM, DA> as(KS > 1 ? par : 0, KS, nch);
+  // MLX: the slot's 16 down rows' scales and biases, staged by the slot's waves.
+  auto sb_src = [&](int, int kind, int row) {
+    return (const uint16_t *)(blob + grp.off[7 + kind]) + (size_t)min(rb + row, H - 1) * (I / 64);
+  };
+  u32x4 sbr[kMlxSbNB];
+  if constexpr (SB) mlx_sb_load<1>(sbr, nch, sid, sth, sb_src);
+  AStream<FMT, NM, DA, SB> as(KS > 1 ? par : 0, KS, nch);
   as.fill(at, nch, g, I);
 #pragma unroll
   for (int k = 0; k < HB; ++k)
     if (sid + sth * k < nvec) hdst(sid + sth * k, hr[k]);
   for (int base = sth * HB; base < nvec; base += sth * 4) stage_batch<4>(base, sid, sth, nvec, hsrc, hdst);
+  if constexpr (SB) mlx_sb_store<1, kMlxSbChunksDown>(sbr, &s_sbd[r], nch, sid, sth, sb_src);
   __syncthreads();
   if (it == (int)blockIdx.x) HH_TR(2, 1);
 
   as.run(at, nch, g, I, [&](const typename Fmt<FMT>::A (&w)[NM], int c) {
     const int col = Fmt<FMT>::bcol(c, g, I);
     auto bv = [&](int, int hh, int v) { return *(const u32x4 *)(sb + hh * ldb + col + Fmt<FMT>::VS * v); };
-    if (KS == 1 && (c & 1)) chunk_mfma<FMT, NM, 1, 2>(acc[1], w, at, bv, c, g, I);
-    else chunk_mfma<FMT, NM, 1, 2>(acc[0], w, at, bv, c, g, I);
+    if constexpr (SB) {
+      auto sbf = [&](int) { return *(const u32x4 *)&s_sbd[r][c][4 * g]; };
+      if (KS == 1 && (c & 1)) chunk_mfma<FMT, NM, 1, 2>(acc[1], w, at, bv, c, g, I, sbf);
+      else chunk_mfma<FMT, NM, 1, 2>(acc[0], w, at, bv, c, g, I, sbf);
+    } else {
+      if (KS == 1 && (c & 1)) chunk_mfma<FMT, NM, 1, 2>(acc[1], w, at, bv, c, g, I);
+      else chunk_mfma<FMT, NM, 1, 2>(acc[0], w, at, bv, c, g, I);
+    }
   });
   }
   if constexpr (KS > 1) {
@@ -3283,6 +3382,9 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
   const int maxu = std::min(a.experts, T * a.top_k) + (S > a.top_k ? 1 : 0);
   const int imax = std::max(a.grp[0].inter, a.grp[1].inter);
   const bool mx = quant == Q_MXFP4;
+  // MLX decode stages each item's group scales and biases in LDS (kMlxSbChunks, kMlxSbChunksDown).
+  if ((quant == Q_MLX4 || quant == Q_MLX8) && (a.hidden > 64 * kMlxSbChunks || imax > 64 * kMlxSbChunksDown))
+    return hipErrorInvalidValue;
   const bool one_up = !mx || (a.hidden + 127) / 128 <= MX_ONE, one_down = !mx || (imax + 127) / 128 <= MX_ONE;
   UpSmallKernel up;
   DownSmallKernel down;
