@@ -692,8 +692,11 @@ __device__ __forceinline__ int rank_of(const int *s_idx, int t, int e, int K, bo
 // shuffles. `src(tile, kind, row)` is the row's first scale (kind 0) or bias (kind 1). Rows of a
 // multiple of 8 chunks come as 16-byte vectors of 8 values (loads issued by mlx_sb_load before
 // the weight stream, stored by mlx_sb_store after it); other rows value by value.
-constexpr int kMlxSbChunks = 64;   // staged chunks per row of the gate-up tiles: K ≤ 4096
-constexpr int kMlxSbChunksDown = 32;   // of the down tiles (one 16-row tile per 64·KS threads): K ≤ 2048
+// Staged chunks per row (the kernels take the staged variant when K fits, the per-chunk loads
+// otherwise): gate-up tiles K ≤ 4096; down tiles K ≤ 4096 with at most 4 slots per workgroup,
+// K ≤ 2048 with 9 (a 16-row tile per 64·KS threads).
+constexpr int kMlxSbChunks = 64;
+template <int SMAX> constexpr int mlx_sb_chunks_down() { return SMAX > 4 ? 32 : 64; }
 constexpr int kMlxSbNB = 2;        // 16-byte vectors per thread (NTL · 32 · K/512 ≤ 2 · threads)
 template <int NTL, class Src>
 __device__ __forceinline__ void mlx_sb_load(u32x4 (&r)[kMlxSbNB], int nch, int tid, int nth, Src src) {
@@ -768,7 +771,8 @@ constexpr int LDS_PAD = 8;        // bf16 elements of padding per staged row (ba
 // 4·TPW waves: wave w takes tile q (16 intermediates; w & 1 when TPW = 2), gate or up rows, and
 // chunk parity p (the even or odd chain of the canonical arithmetic). TPW = 1 gives twice the
 // workgroups of half the size, which spreads a decode step's few experts over more compute units.
-template <int FMT, int DA, int TPW, int XB>
+// SBS (MLX, K ≤ 64·kMlxSbChunks): the group scales and biases staged per item (MlxSb).
+template <int FMT, int DA, int TPW, int XB, bool SBS = false>
 __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) {
   warm_kernargs<sizeof(GemmArgs) + sizeof(RouteArgs)>();
   constexpr int NTH = 256 * TPW, NWV = 4 * TPW, ROWS = 16 * TPW;
@@ -776,7 +780,7 @@ __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) 
   extern __shared__ __align__(16) uint16_t s_x[];   // [ntok][H + LDS_PAD]
   __shared__ int s_idx[SMALL_T * kMaxTopK];
   __shared__ f32x4 s_part[3][2][64];                // [gate odd | up even | up odd][q][lane]
-  constexpr bool SB = is_mlx<FMT>();                // MLX: scales and biases staged per item
+  constexpr bool SB = SBS && is_mlx<FMT>();         // MLX: scales and biases staged per item
   __shared__ __align__(16) uint32_t s_sb[SB ? 2 * TPW : 1][SB ? kMlxSbChunks : 1][16];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1320,14 +1324,16 @@ __device__ __forceinline__ void down_small_item(int it, int T, int &rt, int &t) 
 // sums the chains, then the slots in rank order (sum_expert_slices, dense.metal:147;
 // ReferenceLayer.swift:194-202). SMAX = the most slots a token has under this instantiation.
 // NCH > 0 (MXFP4, single round): every slot's row has exactly NCH chunks (checked on the host).
-template <int FMT, int DA, int SMAX, int KS, int NCH = 0>
+// SBS (MLX, K ≤ 64·mlx_sb_chunks_down<SMAX>): each slot's scales and biases staged (MlxSb).
+template <int FMT, int DA, int SMAX, int KS, int NCH = 0, bool SBS = false>
 __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const int32_t *topk_idx) {
   warm_kernargs<sizeof(GemmArgs) + sizeof(void *)>();
   constexpr int NM = 1;
   extern __shared__ __align__(16) uint16_t s_h[];   // [slots][2][ldh + LDS_PAD]
   __shared__ f32x4 s_odd[KS > 1 ? SMAX : 1][4];     // odd chain, lanes l16 == 0
-  constexpr bool SB = is_mlx<FMT>();                // MLX: each slot's scales and biases staged
-  __shared__ __align__(16) uint32_t s_sbd[SB ? SMAX : 1][SB ? kMlxSbChunksDown : 1][16];
+  constexpr bool SB = SBS && is_mlx<FMT>();         // MLX: each slot's scales and biases staged
+  constexpr int SBCH = mlx_sb_chunks_down<SMAX>();
+  __shared__ __align__(16) uint32_t s_sbd[SB ? SMAX : 1][SB ? SBCH : 1][16];
   __shared__ float s_o[SMAX][16];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1432,7 +1438,7 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
   for (int k = 0; k < HB; ++k)
     if (sid + sth * k < nvec) hdst(sid + sth * k, hr[k]);
   for (int base = sth * HB; base < nvec; base += sth * 4) stage_batch<4>(base, sid, sth, nvec, hsrc, hdst);
-  if constexpr (SB) mlx_sb_store<1, kMlxSbChunksDown>(sbr, &s_sbd[r], nch, sid, sth, sb_src);
+  if constexpr (SB) mlx_sb_store<1, SBCH>(sbr, &s_sbd[r], nch, sid, sth, sb_src);
   __syncthreads();
   if (it == (int)blockIdx.x) HH_TR(2, 1);
 
@@ -3179,6 +3185,10 @@ template <int FMT> static UpSmallKernel up_small_k(bool one, int T, bool st = fa
     if (T == 1) return one ? up_small_mx<MX_ONE, true, 2> : up_small_mx<16, false, 2>;
     return one ? up_small_mx<MX_ONE, true, MX_XB_WIDE> : up_small_mx<16, false, MX_XB_WIDE>;
   }
+  else if constexpr (is_mlx<FMT>()) {
+    if (st) return T == 1 ? up_small<FMT, decode_depth<FMT>(), 1, 2, true> : up_small<FMT, decode_depth<FMT>(), 1, MX_XB_WIDE, true>;
+    return T == 1 ? up_small<FMT, decode_depth<FMT>(), 1, 2> : up_small<FMT, decode_depth<FMT>(), 1, MX_XB_WIDE>;
+  }
   else if (T == 1) return up_small<FMT, decode_depth<FMT>(), 1, 2>;
   else return up_small<FMT, decode_depth<FMT>(), 1, MX_XB_WIDE>;
 }
@@ -3190,10 +3200,21 @@ template <int FMT> static DownSmallKernel down_small_k(int slots, bool one, bool
   // Nine waves leave a third of the register file per wave: a shallower ring (also the MXFP4
   // kernel for rows longer than MX_ONE chunks).
   constexpr int D9 = decode_depth<FMT>() > 8 ? 8 : decode_depth<FMT>();
-  if (slots > 4 || !one) return down_small<FMT, D9, kMaxTopK + 1, 1>;
+  if (slots > 4 || !one) {
+    if constexpr (is_mlx<FMT>())
+      if (st) return down_small<FMT, D9, kMaxTopK + 1, 1, 0, true>;
+    return down_small<FMT, D9, kMaxTopK + 1, 1>;
+  }
   if constexpr (FMT == Q_MXFP4)
     if (st) return down_small<FMT, decode_depth<FMT>(), 4, down_ks<FMT>(4), MX_STATIC>;
+  if constexpr (is_mlx<FMT>())
+    if (st) return down_small<FMT, decode_depth<FMT>(), 4, down_ks<FMT>(4), 0, true>;
   return down_small<FMT, decode_depth<FMT>(), 4, down_ks<FMT>(4)>;
+}
+// MLX: whether the staged-scale variants take this layer (the rows' chunk counts fit LDS).
+static bool mlx_staged_up(int hidden) { return hidden <= 64 * kMlxSbChunks; }
+static bool mlx_staged_down(int slots, int imax) {
+  return imax <= 64 * (slots > 4 ? mlx_sb_chunks_down<kMaxTopK + 1>() : mlx_sb_chunks_down<4>());
 }
 
 // The ring kernel of a BF16 / MLX phase: 64-token work items (BF16 layers whose experts average
@@ -3382,9 +3403,6 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
   const int maxu = std::min(a.experts, T * a.top_k) + (S > a.top_k ? 1 : 0);
   const int imax = std::max(a.grp[0].inter, a.grp[1].inter);
   const bool mx = quant == Q_MXFP4;
-  // MLX decode stages each item's group scales and biases in LDS (kMlxSbChunks, kMlxSbChunksDown).
-  if ((quant == Q_MLX4 || quant == Q_MLX8) && (a.hidden > 64 * kMlxSbChunks || imax > 64 * kMlxSbChunksDown))
-    return hipErrorInvalidValue;
   const bool one_up = !mx || (a.hidden + 127) / 128 <= MX_ONE, one_down = !mx || (imax + 127) / 128 <= MX_ONE;
   UpSmallKernel up;
   DownSmallKernel down;
@@ -3401,8 +3419,14 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
     break;
   }
   case Q_BF16: up = up_small_k<Q_BF16>(true, T); down = down_small_k<Q_BF16>(S, true); break;
-  case Q_MLX4: up = up_small_k<Q_MLX4>(true, T); down = down_small_k<Q_MLX4>(S, true); break;
-  default: up = up_small_k<Q_MLX8>(true, T); down = down_small_k<Q_MLX8>(S, true); break;
+  case Q_MLX4:
+    up = up_small_k<Q_MLX4>(true, T, mlx_staged_up(a.hidden));
+    down = down_small_k<Q_MLX4>(S, true, mlx_staged_down(S, imax));
+    break;
+  default:
+    up = up_small_k<Q_MLX8>(true, T, mlx_staged_up(a.hidden));
+    down = down_small_k<Q_MLX8>(S, true, mlx_staged_down(S, imax));
+    break;
   }
   // The decode kernels stage rows in dynamic LDS beyond the default 64 KiB window (gfx950 has
   // 160 KiB per compute unit).
@@ -3418,7 +3442,11 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
                         (const void *)down_small_k<Q_MXFP4>(9, true), (const void *)down_small_k<Q_BF16>(9, true),
                         (const void *)down_small_k<Q_MLX4>(9, true), (const void *)down_small_k<Q_MLX8>(9, true),
                         (const void *)up_small_k<Q_MXFP4>(true, 1, true), (const void *)up_small_k<Q_MXFP4>(true, SMALL_T, true),
-                        (const void *)down_small_k<Q_MXFP4>(4, true, true)};
+                        (const void *)down_small_k<Q_MXFP4>(4, true, true),
+                        (const void *)up_small_k<Q_MLX4>(true, 1, true), (const void *)up_small_k<Q_MLX4>(true, SMALL_T, true),
+                        (const void *)up_small_k<Q_MLX8>(true, 1, true), (const void *)up_small_k<Q_MLX8>(true, SMALL_T, true),
+                        (const void *)down_small_k<Q_MLX4>(4, true, true), (const void *)down_small_k<Q_MLX4>(9, true, true),
+                        (const void *)down_small_k<Q_MLX8>(4, true, true), (const void *)down_small_k<Q_MLX8>(9, true, true)};
     // Best effort: HIP on gfx950 accepts launches up to the hardware LDS size without it, and
     // a runtime that rejects the attribute must not leave its error for the launch check below.
     for (const void *k : ks) {
@@ -3470,15 +3498,16 @@ hipError_t launch_down_small(int quant, GemmArgs a, const int32_t *topk_idx, int
   switch (quant) {
   case Q_MXFP4: down = down_small_k<Q_MXFP4>(S, one_down); break;
   case Q_BF16: down = down_small_k<Q_BF16>(S, true); break;
-  case Q_MLX4: down = down_small_k<Q_MLX4>(S, true); break;
-  default: down = down_small_k<Q_MLX8>(S, true); break;
+  case Q_MLX4: down = down_small_k<Q_MLX4>(S, true, mlx_staged_down(S, imax)); break;
+  default: down = down_small_k<Q_MLX8>(S, true, mlx_staged_down(S, imax)); break;
   }
   static std::once_flag lds_once;
   std::call_once(lds_once, [] {
     for (int sl : {1, 2, 3, 4, 5, 6, 7, 8, 9})
       for (const void *k : {(const void *)down_small_k<Q_MXFP4>(sl, true), (const void *)down_small_k<Q_MXFP4>(sl, false),
                             (const void *)down_small_k<Q_BF16>(sl, true), (const void *)down_small_k<Q_MLX4>(sl, true),
-                            (const void *)down_small_k<Q_MLX8>(sl, true)}) {
+                            (const void *)down_small_k<Q_MLX8>(sl, true), (const void *)down_small_k<Q_MLX4>(sl, true, true),
+                            (const void *)down_small_k<Q_MLX8>(sl, true, true)}) {
         (void)hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         (void)hipGetLastError();
       }

@@ -234,6 +234,17 @@ TINY = {
                       shared_intermediate=64, group_size=64),
     "bf16": F.MoEDesc(hidden=320, intermediate=192, experts=5, top_k=2, quant=F.QUANT_BF16,
                       activation=F.ACT_GELU_TANH, router=F.ROUTER_GEMMA),
+    # MLX decode stages each item's group scales and biases in LDS when the rows fit (gate-up
+    # K ≤ 4096; down K ≤ 4096 with ≤ 4 slots, ≤ 2048 with more) and loads them per chunk
+    # otherwise: a gate-up row of 65 chunks; down rows of 40 chunks with 3 slots (staged, 16-byte
+    # vectors) and with 9 slots (per chunk).
+    "mlx4-wide": F.MoEDesc(hidden=4160, intermediate=128, experts=6, top_k=2, quant=F.QUANT_MLX4,
+                           activation=F.ACT_SILU, router=F.ROUTER_SOFTMAX_TOPK_RENORM, group_size=64),
+    "mlx4-deep": F.MoEDesc(hidden=512, intermediate=2560, experts=6, top_k=3, quant=F.QUANT_MLX4,
+                           activation=F.ACT_SILU, router=F.ROUTER_SOFTMAX_TOPK_RENORM, group_size=64),
+    "mlx8-long": F.MoEDesc(hidden=256, intermediate=2560, experts=10, top_k=8, quant=F.QUANT_MLX8,
+                           activation=F.ACT_SILU, router=F.ROUTER_SOFTMAX_TOPK_RENORM,
+                           shared_intermediate=128, group_size=64),
 }
 
 
