@@ -1323,9 +1323,8 @@ __device__ __forceinline__ void down_small_item(int it, int T, int &rt, int &t) 
 // shared expert), chunk parity p when KS = 2 (both chains in one wave when KS = 1). The epilogue
 // sums the chains, then the slots in rank order (sum_expert_slices, dense.metal:147;
 // ReferenceLayer.swift:194-202). SMAX = the most slots a token has under this instantiation.
-// NCH > 0 (MXFP4, single round): every slot's row has exactly NCH chunks (checked on the host).
 // SBS (MLX, K ≤ 64·mlx_sb_chunks_down<SMAX>): each slot's scales and biases staged (MlxSb).
-template <int FMT, int DA, int SMAX, int KS, int NCH = 0, bool SBS = false>
+template <int FMT, int DA, int SMAX, int KS, bool SBS = false>
 __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const int32_t *topk_idx) {
   warm_kernargs<sizeof(GemmArgs) + sizeof(void *)>();
   constexpr int NM = 1;
@@ -1400,10 +1399,10 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
     const uint8_t *brow = my_lds;
     const uint8_t *my_sc = s_sc + l16 * nsb;
     // MXFP4: one chain. DA ≥ MX_ONE instantiations run only for rows of at most DA chunks.
-    as.template run_pf<(DA >= MX_ONE_CHUNKS), PF, NCH>(
+    as.template run_pf<(DA >= MX_ONE_CHUNKS), PF>(
         aw, nch, g, I, [&](int c) { return mx_ops<NTH>(brow, RS, a.hld, my_sc, nsb, c, g); },
         [&](const Fmt<Q_MXFP4_W>::A (&w)[NM], int c, const MxOps<NTH> &o) {
-          chunk_mx1<NTH>(acc[0][0][0], w[0].w, o, c, g, I, NCH > 0 && c < NCH - 1);
+          chunk_mx1<NTH>(acc[0][0][0], w[0].w, o, c, g, I);
         });
   } else {
   // This slot's activation (hi, lo) into LDS (the slot's two waves share it): the loads go out
@@ -3202,13 +3201,11 @@ template <int FMT> static DownSmallKernel down_small_k(int slots, bool one, bool
   constexpr int D9 = decode_depth<FMT>() > 8 ? 8 : decode_depth<FMT>();
   if (slots > 4 || !one) {
     if constexpr (is_mlx<FMT>())
-      if (st) return down_small<FMT, D9, kMaxTopK + 1, 1, 0, true>;
+      if (st) return down_small<FMT, D9, kMaxTopK + 1, 1, true>;
     return down_small<FMT, D9, kMaxTopK + 1, 1>;
   }
-  if constexpr (FMT == Q_MXFP4)
-    if (st) return down_small<FMT, decode_depth<FMT>(), 4, down_ks<FMT>(4), MX_STATIC>;
   if constexpr (is_mlx<FMT>())
-    if (st) return down_small<FMT, decode_depth<FMT>(), 4, down_ks<FMT>(4), 0, true>;
+    if (st) return down_small<FMT, decode_depth<FMT>(), 4, down_ks<FMT>(4), true>;
   return down_small<FMT, decode_depth<FMT>(), 4, down_ks<FMT>(4)>;
 }
 // MLX: whether the staged-scale variants take this layer (the rows' chunk counts fit LDS).
@@ -3401,32 +3398,15 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
   if (T < 1 || T > SMALL_T) return hipErrorInvalidValue;
   const int S = a.slots;
   const int maxu = std::min(a.experts, T * a.top_k) + (S > a.top_k ? 1 : 0);
-  const int imax = std::max(a.grp[0].inter, a.grp[1].inter);
   const bool mx = quant == Q_MXFP4;
-  const bool one_up = !mx || (a.hidden + 127) / 128 <= MX_ONE, one_down = !mx || (imax + 127) / 128 <= MX_ONE;
+  const bool one_up = !mx || (a.hidden + 127) / 128 <= MX_ONE;
   UpSmallKernel up;
-  DownSmallKernel down;
   switch (quant) {
-  case Q_MXFP4: {
-    // The static-count variants need every row of the phase at MX_STATIC chunks: the up rows run
-    // over H, the down rows over each expert group's intermediate size (the second group only
-    // when a shared slot exists).
-    const bool st_up = (a.hidden + 127) / 128 == MX_STATIC;
-    const bool st_down = (a.grp[0].inter + 127) / 128 == MX_STATIC &&
-                         (S == a.top_k || (a.grp[1].inter + 127) / 128 == MX_STATIC);
-    up = up_small_k<Q_MXFP4>(one_up, T, st_up);
-    down = down_small_k<Q_MXFP4>(S, one_down, st_down);
-    break;
-  }
-  case Q_BF16: up = up_small_k<Q_BF16>(true, T); down = down_small_k<Q_BF16>(S, true); break;
-  case Q_MLX4:
-    up = up_small_k<Q_MLX4>(true, T, mlx_staged_up(a.hidden));
-    down = down_small_k<Q_MLX4>(S, true, mlx_staged_down(S, imax));
-    break;
-  default:
-    up = up_small_k<Q_MLX8>(true, T, mlx_staged_up(a.hidden));
-    down = down_small_k<Q_MLX8>(S, true, mlx_staged_down(S, imax));
-    break;
+  // The MXFP4 static-count variant needs every up row (over H) at MX_STATIC chunks.
+  case Q_MXFP4: up = up_small_k<Q_MXFP4>(one_up, T, (a.hidden + 127) / 128 == MX_STATIC); break;
+  case Q_BF16: up = up_small_k<Q_BF16>(true, T); break;
+  case Q_MLX4: up = up_small_k<Q_MLX4>(true, T, mlx_staged_up(a.hidden)); break;
+  default: up = up_small_k<Q_MLX8>(true, T, mlx_staged_up(a.hidden)); break;
   }
   // The decode kernels stage rows in dynamic LDS beyond the default 64 KiB window (gfx950 has
   // 160 KiB per compute unit).
@@ -3442,7 +3422,6 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
                         (const void *)down_small_k<Q_MXFP4>(9, true), (const void *)down_small_k<Q_BF16>(9, true),
                         (const void *)down_small_k<Q_MLX4>(9, true), (const void *)down_small_k<Q_MLX8>(9, true),
                         (const void *)up_small_k<Q_MXFP4>(true, 1, true), (const void *)up_small_k<Q_MXFP4>(true, SMALL_T, true),
-                        (const void *)down_small_k<Q_MXFP4>(4, true, true),
                         (const void *)up_small_k<Q_MLX4>(true, 1, true), (const void *)up_small_k<Q_MLX4>(true, SMALL_T, true),
                         (const void *)up_small_k<Q_MLX8>(true, 1, true), (const void *)up_small_k<Q_MLX8>(true, SMALL_T, true),
                         (const void *)down_small_k<Q_MLX4>(4, true, true), (const void *)down_small_k<Q_MLX4>(9, true, true),
