@@ -602,15 +602,27 @@ __device__ __forceinline__ void select_batch(const GemmArgs &a, const RouteArgs 
   __shared__ int s_ci[NW][kFastCand];
   __shared__ double s_cv[NW][kFastCand];
   __shared__ double s_rv[NW][kMaxTopK];
+  __shared__ int s_rk[NW][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int T = ra.tokens, E = a.experts, K = a.top_k;
   const bool has_shared = a.slots > K;
-  for (int t = wave; t < T; t += NW) {
-    const double *lg = ra.lg64 + (size_t)t * (E + 1);
-    const TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave])
-                            : topk_fast(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave]);
-    if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
-    if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
+  if (T == 1) {
+    // One token: the NW waves rank it together; wave 0 publishes.
+    const double *lg = ra.lg64;
+    const TopK tk = E <= 64 ? topk_rank64<NW>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
+                            : topk_fast<NW>(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave], s_rk);
+    if (wave == 0) {
+      if (lane < K) s_idx[lane] = tk.index_of(lane);
+      if (blockIdx.x == 0) finish_token(ra, 0, tk, has_shared ? lg[E] : 0.0);
+    }
+  } else {
+    for (int t = wave; t < T; t += NW) {
+      const double *lg = ra.lg64 + (size_t)t * (E + 1);
+      const TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave])
+                              : topk_fast(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave]);
+      if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
+      if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
+    }
   }
   __syncthreads();
 }
@@ -1138,6 +1150,7 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
   __shared__ int s_ci[4][kFastCand];
   __shared__ double s_cv[4][kFastCand];
   __shared__ double s_rv[4][kMaxTopK];
+  __shared__ int s_rk[4][64];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1151,17 +1164,28 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
   HH_TR(1, 0);
   auto xs = mx_stage<NTX, XB>(s_xb, a.xq, a.xs, a.xld, a.hidden, T, [](int j) { return j; }, tid, 256);
   xs.load_first();
-  // Top-k of every token (wave w: tokens w, w + 4, ...); workgroup 0 writes the routing outputs.
-  for (int t = wave; t < T; t += 4) {
-    const double *lg = ra.lg64 + (size_t)t * (E + 1);
+  // Top-k of every token (wave w: tokens w, w + 4, ...; one token: the 4 waves rank it
+  // together); workgroup 0 writes the routing outputs.
+  if (T == 1) {
+    const double *lg = ra.lg64;
 #ifdef HH_TRACE
-    { volatile double first = lg[lane % E]; (void)first; if (t == 0) HH_TR(1, 6); }
+    { volatile double first = lg[lane % E]; (void)first; HH_TR(1, 6); }
 #endif
-    const TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave])
-                            : topk_fast(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave]);
-    if (t == 0) HH_TR(1, 7);
-    if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
-    if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
+    const TopK tk = E <= 64 ? topk_rank64<4>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
+                            : topk_fast<4>(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave], s_rk);
+    HH_TR(1, 7);
+    if (wave == 0) {
+      if (lane < K) s_idx[lane] = tk.index_of(lane);
+      if (blockIdx.x == 0) finish_token(ra, 0, tk, has_shared ? lg[E] : 0.0);
+    }
+  } else {
+    for (int t = wave; t < T; t += 4) {
+      const double *lg = ra.lg64 + (size_t)t * (E + 1);
+      const TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave])
+                              : topk_fast(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave]);
+      if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
+      if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
+    }
   }
   __syncthreads();
   HH_TR(1, 1);

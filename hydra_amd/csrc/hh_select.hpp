@@ -110,21 +110,53 @@ __device__ __forceinline__ TopK topk_exact(const double *lg, int E, int K) {
   return tk;
 }
 
+// Rank counting split over the NW waves of a workgroup that select the same token together
+// (every wave with identical inputs): wave w counts its share of the comparisons, and the shares
+// meet in s_part [NW][64]. Integer counts, so the sum does not depend on the split. Every wave
+// of the workgroup must call it (a barrier); the second barrier lets s_part be reused.
+template <int NW>
+__device__ __forceinline__ int coop_rank(int part, int (*s_part)[64]) {
+  if constexpr (NW == 1) {
+    return part;
+  } else {
+    const int lane = threadIdx.x & 63;
+    s_part[threadIdx.x >> 6][lane] = part;
+    __syncthreads();
+    int r = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) r += s_part[w][lane];
+    __syncthreads();
+    return r;
+  }
+}
+// Range [j0, j1) of n comparisons that wave w of NW takes.
+template <int NW> __device__ __forceinline__ void coop_range(int n, int &j0, int &j1) {
+  const int w = NW == 1 ? 0 : (int)(threadIdx.x >> 6);
+  j0 = n * w / NW;
+  j1 = n * (w + 1) / NW;
+}
+
 // The same selection for E ≤ 64 by rank counting: lane e holds logit e and counts the logits
 // that precede it (larger, or equal with a smaller index) from a copy in the wave's LDS row
 // s_lg[64]; the lanes of rank < K publish themselves in s_ri[8]. Independent LDS reads replace
-// the K dependent shuffle chains of topk_exact (the decode critical path).
-__device__ __forceinline__ TopK topk_rank64(const double *lg, int E, int K, double *s_lg, int *s_ri) {
+// the K dependent shuffle chains of topk_exact (the decode critical path). NW > 1: the waves of
+// the workgroup select this token together (coop_rank).
+template <int NW = 1>
+__device__ __forceinline__ TopK topk_rank64(const double *lg, int E, int K, double *s_lg, int *s_ri,
+                                            int (*s_part)[64] = nullptr) {
   const int lane = threadIdx.x & 63;
   const double v = lane < E ? lg[lane] : -INFINITY;
   s_lg[lane] = v;
   __builtin_amdgcn_wave_barrier();
+  int j0, j1;
+  coop_range<NW>(E, j0, j1);
   int rank = 0;
 #pragma unroll 8
-  for (int j = 0; j < E; ++j) {
+  for (int j = j0; j < j1; ++j) {
     const double o = s_lg[j];
     rank += (o > v || (o == v && j < lane)) ? 1 : 0;
   }
+  rank = coop_rank<NW>(rank, s_part);
   if (lane < E && rank < K) s_ri[rank] = lane;
   __builtin_amdgcn_wave_barrier();
   TopK tk;
@@ -156,8 +188,9 @@ __device__ __forceinline__ double readlane_f64(double v, int l) {
 // scratch; more candidates than 64 (heavy ties) rank from LDS, more than kFastCand take
 // topk_exact.
 constexpr int kFastCand = 128;
+template <int NW = 1>
 __device__ __forceinline__ TopK topk_fast(const double *lg, int E, int K, int *s_ri, double *s_rv, int *s_ci,
-                                          double *s_cv) {
+                                          double *s_cv, int (*s_part)[64] = nullptr) {
   const int lane = threadIdx.x & 63;
   double v[8];
   double m = -INFINITY;
@@ -168,11 +201,14 @@ __device__ __forceinline__ TopK topk_fast(const double *lg, int E, int K, int *s
     m = fmax(m, v[j]);
   }
   // τ: the lane maximum of rank K−1 among the 64 (ties by lane).
+  int j0, j1;
+  coop_range<NW>(64, j0, j1);
   int rank = 0;
-  for (int j = 0; j < 64; ++j) {
+  for (int j = j0; j < j1; ++j) {
     const double o = readlane_f64(m, j);
     rank += (o > m || (o == m && j < lane)) ? 1 : 0;
   }
+  rank = coop_rank<NW>(rank, s_part);
   const uint64_t at_k = __ballot(rank == K - 1);
   const double tau = readlane_f64(m, __ffsll((unsigned long long)at_k) - 1);
   // Candidates v ≥ τ, compacted into LDS (lane-major within each j).
@@ -201,19 +237,22 @@ __device__ __forceinline__ TopK topk_fast(const double *lg, int E, int K, int *s
     const double cv = mine ? s_cv[ci] : 0.0;
     const int ce = mine ? s_ci[ci] : 0;
     int r = 0;
+    int k0, k1;
+    coop_range<NW>(nc, k0, k1);
     if (nc <= 64) {
-      for (int j = 0; j < nc; ++j) {
+      for (int j = k0; j < k1; ++j) {
         const double o = readlane_f64(cv, j);
         const int oe = __builtin_amdgcn_readlane(ce, j);
         r += (o > cv || (o == cv && oe < ce)) ? 1 : 0;
       }
     } else {
-      for (int j = 0; j < nc; ++j) {
+      for (int j = k0; j < k1; ++j) {
         const double o = s_cv[j];
         const int oe = s_ci[j];
         r += (o > cv || (o == cv && oe < ce)) ? 1 : 0;
       }
     }
+    r = coop_rank<NW>(r, s_part);
     if (mine && r < K) {
       s_ri[r] = ce;
       s_rv[r] = cv;
