@@ -606,14 +606,19 @@ __device__ __forceinline__ void select_batch(const GemmArgs &a, const RouteArgs 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int T = ra.tokens, E = a.experts, K = a.top_k;
   const bool has_shared = a.slots > K;
-  if (T == 1) {
-    // One token: the NW waves rank it together; wave 0 publishes.
-    const double *lg = ra.lg64;
-    const TopK tk = E <= 64 ? topk_rank64<NW>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
-                            : topk_fast<NW>(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave], s_rk);
-    if (wave == 0) {
-      if (lane < K) s_idx[lane] = tk.index_of(lane);
-      if (blockIdx.x == 0) finish_token(ra, 0, tk, has_shared ? lg[E] : 0.0);
+  if (T == 1 || (T == 2 && NW % 2 == 0)) {
+    // One or two tokens: groups of NW / T waves rank a token together; the group's first wave
+    // publishes.
+    constexpr int G1 = NW, G2 = NW / 2 > 0 ? NW / 2 : 1;
+    const int G = T == 1 ? G1 : G2, t = wave / G;
+    const double *lg = ra.lg64 + (size_t)t * (E + 1);
+    const TopK tk = T == 1 ? (E <= 64 ? topk_rank64<G1>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
+                                      : topk_fast<G1>(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave], s_rk))
+                           : (E <= 64 ? topk_rank64<G2>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
+                                      : topk_fast<G2, 1>(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave], s_rk));
+    if (wave % G == 0) {
+      if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
+      if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
     }
   } else {
     for (int t = wave; t < T; t += NW) {
@@ -1166,17 +1171,21 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
   xs.load_first();
   // Top-k of every token (wave w: tokens w, w + 4, ...; one token: the 4 waves rank it
   // together); workgroup 0 writes the routing outputs.
-  if (T == 1) {
-    const double *lg = ra.lg64;
+  if (T <= 2) {
+    // One or two tokens: groups of 4 / T waves rank a token together.
+    const int G = T == 1 ? 4 : 2, t = wave / G;
+    const double *lg = ra.lg64 + (size_t)t * (E + 1);
 #ifdef HH_TRACE
     { volatile double first = lg[lane % E]; (void)first; HH_TR(1, 6); }
 #endif
-    const TopK tk = E <= 64 ? topk_rank64<4>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
-                            : topk_fast<4>(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave], s_rk);
+    const TopK tk = T == 1 ? (E <= 64 ? topk_rank64<4>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
+                                      : topk_fast<4>(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave], s_rk))
+                           : (E <= 64 ? topk_rank64<2>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
+                                      : topk_fast<2, 1>(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave], s_rk));
     HH_TR(1, 7);
-    if (wave == 0) {
-      if (lane < K) s_idx[lane] = tk.index_of(lane);
-      if (blockIdx.x == 0) finish_token(ra, 0, tk, has_shared ? lg[E] : 0.0);
+    if (wave % G == 0) {
+      if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
+      if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
     }
   } else {
     for (int t = wave; t < T; t += 4) {

@@ -110,28 +110,29 @@ __device__ __forceinline__ TopK topk_exact(const double *lg, int E, int K) {
   return tk;
 }
 
-// Rank counting split over the NW waves of a workgroup that select the same token together
-// (every wave with identical inputs): wave w counts its share of the comparisons, and the shares
-// meet in s_part [NW][64]. Integer counts, so the sum does not depend on the split. Every wave
-// of the workgroup must call it (a barrier); the second barrier lets s_part be reused.
+// Rank counting split over groups of NW consecutive waves of a workgroup, each group selecting
+// one token (every wave of a group with identical inputs): wave w counts its share of the
+// comparisons, and the shares meet in s_part [waves][64]. Integer counts, so the sum does not
+// depend on the split. Every wave of the workgroup must call it (barriers); the second barrier
+// lets s_part be reused.
 template <int NW>
 __device__ __forceinline__ int coop_rank(int part, int (*s_part)[64]) {
   if constexpr (NW == 1) {
     return part;
   } else {
-    const int lane = threadIdx.x & 63;
-    s_part[threadIdx.x >> 6][lane] = part;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, w0 = w - w % NW;
+    s_part[w][lane] = part;
     __syncthreads();
     int r = 0;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) r += s_part[w][lane];
+    for (int k = 0; k < NW; ++k) r += s_part[w0 + k][lane];
     __syncthreads();
     return r;
   }
 }
-// Range [j0, j1) of n comparisons that wave w of NW takes.
+// Range [j0, j1) of n comparisons that wave w of its group of NW takes.
 template <int NW> __device__ __forceinline__ void coop_range(int n, int &j0, int &j1) {
-  const int w = NW == 1 ? 0 : (int)(threadIdx.x >> 6);
+  const int w = NW == 1 ? 0 : (int)(threadIdx.x >> 6) % NW;
   j0 = n * w / NW;
   j1 = n * (w + 1) / NW;
 }
@@ -187,8 +188,11 @@ __device__ __forceinline__ double readlane_f64(double v, int l) {
 // topk_exact's. s_ri / s_rv[kMaxTopK] and s_ci[kFastCand] / s_cv[kFastCand] are the wave's LDS
 // scratch; more candidates than 64 (heavy ties) rank from LDS, more than kFastCand take
 // topk_exact.
+// NW > 1: groups of NW waves share the 64 lane maxima's ranking (one barrier pair for every
+// group, whatever its token); NWC > 1 also splits the candidates' ranking, whose barrier count
+// depends on the candidate count: only when every wave of the workgroup ranks the same token.
 constexpr int kFastCand = 128;
-template <int NW = 1>
+template <int NW = 1, int NWC = NW>
 __device__ __forceinline__ TopK topk_fast(const double *lg, int E, int K, int *s_ri, double *s_rv, int *s_ci,
                                           double *s_cv, int (*s_part)[64] = nullptr) {
   const int lane = threadIdx.x & 63;
@@ -238,7 +242,7 @@ __device__ __forceinline__ TopK topk_fast(const double *lg, int E, int K, int *s
     const int ce = mine ? s_ci[ci] : 0;
     int r = 0;
     int k0, k1;
-    coop_range<NW>(nc, k0, k1);
+    coop_range<NWC>(nc, k0, k1);
     if (nc <= 64) {
       for (int j = k0; j < k1; ++j) {
         const double o = readlane_f64(cv, j);
@@ -252,7 +256,7 @@ __device__ __forceinline__ TopK topk_fast(const double *lg, int E, int K, int *s
         r += (o > cv || (o == cv && oe < ce)) ? 1 : 0;
       }
     }
-    r = coop_rank<NW>(r, s_part);
+    r = coop_rank<NWC>(r, s_part);
     if (mine && r < K) {
       s_ri[r] = ce;
       s_rv[r] = cv;
