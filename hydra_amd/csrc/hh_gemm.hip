@@ -778,6 +778,9 @@ constexpr int MX_ONE_CHUNKS = 24; // MXFP4 decode rows of at most this many 128-
 #define HH_MX_PF 6
 #endif
 constexpr int MX_PF = HH_MX_PF;   // chunks a single-round MXFP4 decode wave issues before its staging barrier
+// The one-token gate-up instantiation issues 10 (measured: T=1 gate-up 15.0 → 14.5 µs; 10 and
+// more made the T ≥ 2 kernels and the down kernel slower).
+constexpr int MX_PF_T1 = 10;
 constexpr int kFusedMaxE = 128;   // experts of layers that take the fused decode kernel
 constexpr int LDS_PAD = 8;        // bf16 elements of padding per staged row (bank spread)
 
@@ -1240,7 +1243,7 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
     u32x4 bias = {0u, 0u, 0u, 0u};
     if (!is_up && a.expert_bias) bias = *(const u32x4 *)(blob + grp.off[2] + 4 * (rb + 4 * g));
     ATile<Q_MXFP4_W> at[NM] = {tile_of<PH_UP, Q_MXFP4_W>(blob, grp, rb, is_up, H, l16)};
-    constexpr int PF = ONE ? MX_PF : DA;
+    constexpr int PF = ONE ? (XB <= 2 ? MX_PF_T1 : MX_PF) : DA;
     AStream<Q_MXFP4_W, NM, DA> as(0, 1, nch);
     as.template fill<PF>(at, nch, g, H);
     if (x_pending) {
