@@ -575,6 +575,92 @@ __global__ __launch_bounds__(256) void logits_small_kernel(RouteArgs a) {
   if (wave == 0) HH_RT(1);
 }
 
+// The same logits with a 4-wave workgroup per (token, expert) pair (H ≤ 4096): wave u forms
+// accumulator u of exact_logit (columns 2048i + 512u + 8l .. +7, i ascending) and wave 0 adds the
+// four in exact_logit's order, (acc0 + acc1) + (acc2 + acc3), then sums the wave: the same value
+// with a quarter of the products on each wave's dependent chain. GEMMA's norm: wave u forms the
+// partial Σx² of each (step, slice u), and every wave adds them in pair_logit's order (steps
+// ascending, slices ascending within a step) before the wave sum. Workgroups past the pairs
+// quantise x (MXFP4 layers).
+template <bool gemma>
+__global__ __launch_bounds__(256) void logits_split_kernel(RouteArgs a) {
+  warm_kernargs<sizeof(RouteArgs)>();
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int E = a.experts, E1 = E + 1, H = a.hidden;
+  const int np = a.tokens * E1;
+  __shared__ double s_acc[4][64];
+  __shared__ double s_px[4][2][64];
+  if (wave == 0) HH_RT(0);
+  if ((int)blockIdx.x >= np) {
+    const int w = ((int)blockIdx.x - np) * 4 + wave;
+    if (w < quant_x_waves(a)) {
+      const int per_t = (H / 32 + 15) / 16;
+      quant_x_wave(a, w / per_t, 16 * (w % per_t));
+    }
+    return;
+  }
+  const int t = blockIdx.x / E1, e = blockIdx.x - t * E1;
+  if (e == E && !a.shared_gate) return;   // uniform over the workgroup
+  const bool sg = e == E;                 // the shared expert's gate row: plain dot, no bias
+  const bool gm = gemma && !sg;
+  const uint16_t *xr = (sg ? a.x : a.xr) + (size_t)t * H;
+  const uint16_t *wrow = sg ? a.shared_gate : a.router_w + (size_t)e * H;
+  const int u = wave, nb = H > 2048 ? 2 : 1;
+  u32x4 xv[2], wv[2], sv[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int h = 2048 * b + lane * 8 + 512 * u;
+    const int hc = min(h, H - 8);
+    xv[b] = *(const u32x4 *)(xr + hc);
+    wv[b] = *(const u32x4 *)(wrow + hc);
+    sv[b] = gm ? *(const u32x4 *)(a.router_scale + hc) : u32x4{0u, 0u, 0u, 0u};
+    if (h >= H) wv[b] = u32x4{0u, 0u, 0u, 0u};
+  }
+  double norm = 1.0, root = 1.0;
+  if (gm) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int h = 2048 * b + lane * 8 + 512 * u;
+      double px = 0.0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float xf = h < H ? bf16_bits_to_f32((xv[b][k >> 1] >> ((k & 1) * 16)) & 0xFFFF) : 0.f;
+        px += (double)(xf * xf);
+      }
+      s_px[u][b][lane] = px;
+    }
+    __syncthreads();
+    double xx = 0.0;
+    for (int b = 0; b < nb; ++b)
+#pragma unroll
+      for (int uu = 0; uu < 4; ++uu) xx += s_px[uu][b][lane];
+    xx = wave_sum_f64(xx);
+    norm = pow(xx / (double)H + (double)a.eps, -0.5);
+    root = pow((double)H, -0.5);
+  }
+  double acc = 0.0;
+  for (int b = 0; b < nb; ++b)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int sh = (k & 1) * 16;
+      const float xf = bf16_bits_to_f32((xv[b][k >> 1] >> sh) & 0xFFFF);
+      const float wf = bf16_bits_to_f32((wv[b][k >> 1] >> sh) & 0xFFFF);
+      if (gm) {
+        const double xd = (((double)xf * norm) * (double)bf16_bits_to_f32((sv[b][k >> 1] >> sh) & 0xFFFF)) * root;
+        acc = fma(xd, (double)wf, acc);
+      } else {
+        acc += (double)(xf * wf);
+      }
+    }
+  s_acc[u][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  double v = wave_sum_f64((s_acc[0][lane] + s_acc[1][lane]) + (s_acc[2][lane] + s_acc[3][lane]));
+  if (!sg && a.router_b) v += (double)bf16_bits_to_f32(a.router_b[e]);
+  if (lane == 0) a.lg64[(size_t)t * E1 + e] = v;
+  HH_RT(1);
+}
+
 // The FFN block's router (a.resid set, bf16 non-GEMMA router, T ≤ 16, H ≤ 4096): workgroup (t, g)
 // of BLK_W waves forms token t's layer input x = bf16(resid·f·norm_w) once, into LDS (its threads
 // splitting the columns; the norm factor f from every wave's own canonical Σ resid², row_sumsq's
@@ -832,6 +918,13 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s, Timing tm) {
       const int blocks = a.tokens * block_logit_groups(a.experts) + (qwaves + BLK_W - 1) / BLK_W;
       hipExtLaunchKernelGGL(logits_block_kernel, dim3(blocks), dim3(64 * BLK_W), 0, s, tm.start,
                             sel ? nullptr : tm.stop, 0, a);
+    } else if (a.hidden <= 4096 && (!g || a.tokens == 1)) {
+      // (GEMMA: every workgroup also forms its token's norm, which costs more than the split
+      // saves once the batch fills the machine; measured T=8 route 8.6 → 11.0 µs.)
+      const int pairs = a.tokens * (a.experts + 1);
+      hipExtLaunchKernelGGL(g ? logits_split_kernel<true> : logits_split_kernel<false>,
+                            dim3(pairs + (qwaves + 3) / 4), dim3(256), 0, s, tm.start, sel ? nullptr : tm.stop,
+                            0, a);
     } else {
       const int waves = a.tokens * (a.experts + 1) + qwaves;
       hipExtLaunchKernelGGL(g ? logits_small_kernel<true> : logits_small_kernel<false>,
