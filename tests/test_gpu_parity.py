@@ -249,7 +249,7 @@ TINY = {
 
 
 @pytest.mark.parametrize("name", list(TINY))
-@pytest.mark.parametrize("T", [1, 5, 70])
+@pytest.mark.parametrize("T", [1, 2, 5, 70])   # T = 1 and 2: the decode selection split over waves
 def test_layer_matches_oracle_small(torch_dev, ctx, name, T):
     from hydra_amd.layer import MoELayer
     desc = TINY[name]
