@@ -2300,7 +2300,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     tasks.tile(tau, rt, wi);
     const int4 it = item_of(slot);
     r0 = rt * C::MR;
-    ntok = it.z;
+    ntok = __builtin_amdgcn_readfirstlane(it.z);
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
       eslot[tt] = ((const int *)(order + 256 * slot))[min(16 * TT * wt + 16 * tt + l16, ntok - 1)];
@@ -2381,6 +2381,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     c = 0;
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
+      if (16 * TT * wt + 16 * tt >= ntok) break;   // padding tiles (also wt > 0 past the tokens)
       const int n = 16 * TT * wt + 16 * tt + l16;
 #pragma unroll
       for (int h = 0; h < RR; ++h) {
@@ -2645,7 +2646,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     tasks.tile(tau, rt, wi);
     const int4 it = item_of(slot);
     r0 = rt * C::MR;
-    ntok = it.z;
+    ntok = __builtin_amdgcn_readfirstlane(it.z);
 #pragma unroll
     for (int tt = 0; tt < TT; ++tt) {
       eslot[tt] = ((const int *)(order + 256 * slot))[min(16 * tt + l16, ntok - 1)];
@@ -2719,13 +2720,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             if (!ok) cur.bs[t][tt] = 127u;
           }
       }
+      // Token tiles wholly past the item's tokens (padding) are skipped: never stored.
 #pragma unroll
-      for (int t = 0; t < NTERM; ++t)
+      for (int tt = 0; tt < TT; ++tt) {
+        if (tt > 0 && 16 * tt >= ntok) break;
 #pragma unroll
-        for (int tt = 0; tt < TT; ++tt)
+        for (int t = 0; t < NTERM; ++t)
 #pragma unroll
           for (int j = 0; j < NJ; ++j)
             acc[j][tt] = smfma(ar[u][j], cur.blo[t][tt], cur.bhi[t][tt], cur.sa[j], cur.bs[t][tt], acc[j][tt]);
+      }
       if (PH == PH_UP) HH_TRS(step, 2);
       load_a(ar[u]);   // the chunk DA ahead into the slot just consumed
       if (PH == PH_UP) HH_TRS(step, 3);
@@ -2747,6 +2751,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           }
 #pragma unroll
           for (int tt = 0; tt < TT; ++tt) {
+            if (16 * tt >= ntok) break;   // padding tiles
             const int n = 16 * tt + l16;
             if constexpr (PH == PH_UP) {
               float v[8];
