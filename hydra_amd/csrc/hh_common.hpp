@@ -120,23 +120,62 @@ __device__ __forceinline__ void quant_lane(float v, uint32_t (&q)[NTERM], uint32
 }
 
 // ---- gated activations (device twins of the oracle's act_pair) ------------------------------
-__device__ __forceinline__ float activate(int act, float g, float u, float alpha, float limit) {
-  if (act == A_SWIGLU_OAI) {
-    // ReferenceOps.swiglu (ReferenceOps.swift:87-99).
-    g = fminf(g, limit);
-    u = fminf(fmaxf(u, -limit), limit);
-    return g * (1.0f / (1.0f + expf(-alpha * g))) * (u + 1.0f);
-  }
-  if (act == A_SILU) {
-    // QwenReferenceOps.siluMultiply (QwenReferenceOps.swift:149-151).
-    return g * (1.0f / (1.0f + expf(-g))) * u;
-  }
-  // Gemma4ReferenceOps.gelu (Gemma4ReferenceOps.swift:37-40); the tanh argument is clamped to
-  // ±15 where tanh is 1 to within float precision (as gemma.metal:77-88 does) so a large gate
-  // cannot produce inf/inf.
+// 1 / (1 + e^-z) in fp32 to a few ulps, with no compare or division step: e^x = 2^n · 2^f by
+// Cody–Waite reduction (x·log2 e formed as a head and a tail: the fma recovers the head's
+// rounding error, the tail carries log2 e's bits below fp32), 2^f on v_exp_f32, 2^n by ldexp;
+// the reciprocal of d = 1 + e^x is v_rcp_f32 and one Newton step r += r·(1 − d·r). x is clamped
+// to [−104, 80]: below, 2^n underflows to 0 (the factor is 1); above, the factor (< 2e-35) is
+// formed without overflow. The library expf and the IEEE division test ranges and scale their
+// operands through the one condition register (VCC), which chains every activation of a block
+// to the previous one; these steps leave independent activations free to interleave.
+__device__ __forceinline__ float sigmoid_f32(float z) {
+  const float x = fminf(fmaxf(-z, -104.0f), 80.0f);
+  const float log2e_hi = 1.44269502e+00f, log2e_lo = 1.92596299e-08f;
+  const float ph = x * log2e_hi;
+  const float pl = __builtin_fmaf(x, log2e_hi, -ph) + x * log2e_lo;
+  const float n = __builtin_rintf(ph);
+  const float e = __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f((ph - n) + pl), (int)n);
+  const float d = 1.0f + e;
+  const float r = __builtin_amdgcn_rcpf(d);
+  return __builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r);
+}
+// ReferenceOps.swiglu (ReferenceOps.swift:87-99).
+__device__ __forceinline__ float act_swiglu(float g, float u, float alpha, float limit) {
+  g = fminf(g, limit);
+  u = fminf(fmaxf(u, -limit), limit);
+  return g * sigmoid_f32(alpha * g) * (u + 1.0f);
+}
+// QwenReferenceOps.siluMultiply (QwenReferenceOps.swift:149-151).
+__device__ __forceinline__ float act_silu(float g, float u) { return g * sigmoid_f32(g) * u; }
+// Gemma4ReferenceOps.gelu (Gemma4ReferenceOps.swift:37-40), with (1 + tanh y) / 2 = 1 / (1 + e^-2y);
+// the tanh argument is clamped to ±15, where tanh is 1 to within float precision (as
+// gemma.metal:77-88 does).
+__device__ __forceinline__ float act_gelu(float g, float u) {
   float inner = 0.7978845608028654f * (g + 0.044715f * g * g * g);
   inner = fminf(fmaxf(inner, -15.0f), 15.0f);
-  return 0.5f * g * (1.0f + tanhf(inner)) * u;
+  return g * sigmoid_f32(2.0f * inner) * u;
+}
+__device__ __forceinline__ float activate(int act, float g, float u, float alpha, float limit) {
+  if (act == A_SWIGLU_OAI) return act_swiglu(g, u, alpha, limit);
+  if (act == A_SILU) return act_silu(g, u);
+  return act_gelu(g, u);
+}
+// N independent activations, the kind tested once: the N chains (exponential, division) form one
+// block, which the compiler interleaves (a test per element gives N blocks run one after the
+// other, each waiting out its own latencies). Each element's arithmetic is activate's.
+template <int N>
+__device__ __forceinline__ void activate_n(int act, const float (&g)[N], const float (&u)[N], float (&y)[N],
+                                           float alpha, float limit) {
+  if (act == A_SWIGLU_OAI) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) y[i] = act_swiglu(g[i], u[i], alpha, limit);
+  } else if (act == A_SILU) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) y[i] = act_silu(g[i], u[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) y[i] = act_gelu(g[i], u[i]);
+  }
 }
 
 // ---- kernel argument blocks -----------------------------------------------------------------

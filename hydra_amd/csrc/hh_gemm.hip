@@ -458,6 +458,15 @@ template <int FMT, int NM, int DA, bool NOSB = false> struct AStream {
       else rounds<false, false>(at, nch, g, K, pre, body);
     }
   }
+  // One round of NC chunks at this wave's first chunk and stride, NC known at compile time (the
+  // caller guarantees n == NC ≤ DA): every chunk's wait is exact. The first P chunks were issued
+  // by fill<P>; chunk u + P is issued after chunk u is computed.
+  // `pre(c)` / `body(stage, c, ops)` as in run_pf.
+  template <int NC, int P = DA, class Pre, class Body>
+  __device__ __forceinline__ void run_static(const ATile<FMT> (&at)[NM], int nch, int g, int K, Pre pre, Body body) {
+    static_assert(NC > 0 && NC <= DA && P <= NC, "a static single round");
+    rounds<true, false, P, NC>(at, nch, g, K, pre, body);
+  }
   // UNIT: chunk u of the ring is chunk u of K (one round, first chunk 0, stride 1), so chunk
   // indices, and the operand offsets derived from them, are compile-time constants.
   template <bool ONE, bool UNIT, int P = DA, int NC = 0, class Pre, class Body>
@@ -505,22 +514,28 @@ __device__ __forceinline__ f32x4 up_values(const GemmArgs &a, const uint8_t *blo
       ub[ii] = bf16_bits_to_f32(bias[2 * (i0 + ii) + 1]);
     }
   }
-  f32x4 y;
+  float gv[4], uv[4], yv[4];
 #pragma unroll
-  for (int ii = 0; ii < 4; ++ii) y[ii] = activate(a.act, gate[ii] + gb[ii], up[ii] + ub[ii], a.alpha, a.limit);
-  return y;
+  for (int ii = 0; ii < 4; ++ii) {
+    gv[ii] = gate[ii] + gb[ii];
+    uv[ii] = up[ii] + ub[ii];
+  }
+  activate_n<4>(a.act, gv, uv, yv, a.alpha, a.limit);
+  return f32x4{yv[0], yv[1], yv[2], yv[3]};
 }
 
 // up_values with the GPT-OSS bias of the 4 intermediates already loaded: 16 bytes from the bias
 // row at element 2·i0, (gate, up) bf16 pairs in order.
 __device__ __forceinline__ f32x4 up_values_mx(const GemmArgs &a, const u32x4 &bias, const f32x4 &gate,
                                               const f32x4 &up) {
-  f32x4 y;
+  float gv[4], uv[4], yv[4];
 #pragma unroll
-  for (int ii = 0; ii < 4; ++ii)
-    y[ii] = activate(a.act, gate[ii] + bf16_bits_to_f32(bias[ii] & 0xFFFFu), up[ii] + bf16_bits_to_f32(bias[ii] >> 16),
-                     a.alpha, a.limit);
-  return y;
+  for (int ii = 0; ii < 4; ++ii) {
+    gv[ii] = gate[ii] + bf16_bits_to_f32(bias[ii] & 0xFFFFu);
+    uv[ii] = up[ii] + bf16_bits_to_f32(bias[ii] >> 16);
+  }
+  activate_n<4>(a.act, gv, uv, yv, a.alpha, a.limit);
+  return f32x4{yv[0], yv[1], yv[2], yv[3]};
 }
 
 // Gate-up epilogue of 4 intermediates i0..i0+3 of slot `slot`: bias, activation, bf16 hi/lo.
@@ -792,7 +807,9 @@ constexpr int LDS_PAD = 8;        // bf16 elements of padding per staged row (ba
 // chunk parity p (the even or odd chain of the canonical arithmetic). TPW = 1 gives twice the
 // workgroups of half the size, which spreads a decode step's few experts over more compute units.
 // SBS (MLX, K ≤ 64·kMlxSbChunks): the group scales and biases staged per item (MlxSb).
-template <int FMT, int DA, int TPW, int XB, bool SBS = false>
+// NCW > 0: every wave's stream is exactly NCW chunks (K of 2·NCW chunks, checked on the host), all
+// issued before the staging barrier and waited for one by one (DA == NCW).
+template <int FMT, int DA, int TPW, int XB, bool SBS = false, int NCW = 0>
 __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) {
   warm_kernargs<sizeof(GemmArgs) + sizeof(RouteArgs)>();
   constexpr int NTH = 256 * TPW, NWV = 4 * TPW, ROWS = 16 * TPW;
@@ -879,7 +896,7 @@ __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) 
     const uint16_t *brow = s_x + (size_t)my_t * ldx;
     f32x4 acc[NM][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
     const int my_tile = (is_up ? TPW : 0) + q;
-    as.run(at, nch, g, H, [&](const typename Fmt<FMT>::A (&w)[NM], int c) {
+    auto chunk = [&](const typename Fmt<FMT>::A (&w)[NM], int c) {
       const int col = Fmt<FMT>::bcol(c, g, H);
       auto bv = [&](int, int, int v) { return *(const u32x4 *)(brow + col + Fmt<FMT>::VS * v); };
       if constexpr (SB)
@@ -887,7 +904,28 @@ __global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) 
                                   [&](int) { return *(const u32x4 *)&s_sb[my_tile][c][4 * g]; });
       else
         chunk_mfma<FMT, NM, 1, 1>(acc, w, at, bv, c, g, H);
-    });
+    };
+    if constexpr (NCW > 0) {
+      static_assert(SB, "the single-round stream takes the staged scales and biases");
+      // The chunk's x vectors and (scale | bias) words read one chunk ahead.
+      struct Ops { u32x4 b[2], sb; };
+      as.template run_static<NCW>(
+          at, nch, g, H,
+          [&](int c) {
+            const int col = Fmt<FMT>::bcol(c, g, H);
+            Ops o;
+            o.b[0] = *(const u32x4 *)(brow + col);
+            o.b[1] = *(const u32x4 *)(brow + col + Fmt<FMT>::VS);
+            o.sb = *(const u32x4 *)&s_sb[my_tile][c][4 * g];
+            return o;
+          },
+          [&](const typename Fmt<FMT>::A (&w)[NM], int c, const Ops &o) {
+            chunk_mfma<FMT, NM, 1, 1>(acc, w, at, [&](int, int, int v) { return o.b[v]; }, c, g, H,
+                                      [&](int) { return o.sb; });
+          });
+    } else {
+      as.run(at, nch, g, H, chunk);
+    }
     // Chains and gate/up meet in the (gate, even) wave of each tile. The next item's partials
     // are written only after its first barrier, which this item's epilogue wave reaches last.
     const int slot_of_part = (is_up ? 1 : 0) * 2 + par;   // 0: gate even (keeps), 1: gate odd, 2: up even, 3: up odd
@@ -2003,14 +2041,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
           if constexpr (PH == PH_UP) {
             // Tile j, lane group g: rows rw + 16j + 4g + {0..3} = (gate, up) of intermediates
             // rw/2 + 8j + 2g + {0, 1}.
-            float v[8];
+            float v[8], gv[8], uv[8];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               const f32x4 d = acc[j][st];
               const float *bb = sBias + 64 * wr + 16 * j + 4 * g;
-              v[2 * j] = activate(a.act, d[0] + bb[0], d[1] + bb[1], a.alpha, a.limit);
-              v[2 * j + 1] = activate(a.act, d[2] + bb[2], d[3] + bb[3], a.alpha, a.limit);
+              gv[2 * j] = d[0] + bb[0];
+              uv[2 * j] = d[1] + bb[1];
+              gv[2 * j + 1] = d[2] + bb[2];
+              uv[2 * j + 1] = d[3] + bb[3];
             }
+            activate_n<8>(a.act, gv, uv, v, a.alpha, a.limit);
             uint32_t hq[NTH][2], sb[NTH];
             quant_block<NTH>(v, hq, sb);
             if (n < ntok) {
@@ -2393,13 +2434,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
           for (int ii = 0; ii < 4; ++ii) bias[j][ii] = a.expert_bias ? bf16_bits_to_f32(braw[4 * h + j][ii]) : 0.f;
         if constexpr (PH == PH_UP) {
-          float v[8];
+          float v[8], gv[8], uv[8];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const f32x4 d = acc[4 * h + j][tt];
-            v[2 * j] = activate(a.act, d[0] + bias[j][0], d[1] + bias[j][1], a.alpha, a.limit);
-            v[2 * j + 1] = activate(a.act, d[2] + bias[j][2], d[3] + bias[j][3], a.alpha, a.limit);
+            gv[2 * j] = d[0] + bias[j][0];
+            uv[2 * j] = d[1] + bias[j][1];
+            gv[2 * j + 1] = d[2] + bias[j][2];
+            uv[2 * j + 1] = d[3] + bias[j][3];
           }
+          activate_n<8>(a.act, gv, uv, v, a.alpha, a.limit);
           uint32_t hq[NTH][2], sbq[NTH];
           quant_block<NTH>(v, hq, sbq);
           if (n < ntok) {
@@ -2754,13 +2798,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             if (16 * tt >= ntok) break;   // padding tiles
             const int n = 16 * tt + l16;
             if constexpr (PH == PH_UP) {
-              float v[8];
+              float v[8], gv[8], uv[8];
 #pragma unroll
               for (int j = 0; j < 4; ++j) {
                 const f32x4 d = acc[j][tt];
-                v[2 * j] = activate(a.act, d[0] + bias[j][0], d[1] + bias[j][1], a.alpha, a.limit);
-                v[2 * j + 1] = activate(a.act, d[2] + bias[j][2], d[3] + bias[j][3], a.alpha, a.limit);
+                gv[2 * j] = d[0] + bias[j][0];
+                uv[2 * j] = d[1] + bias[j][1];
+                gv[2 * j + 1] = d[2] + bias[j][2];
+                uv[2 * j + 1] = d[3] + bias[j][3];
               }
+              activate_n<8>(a.act, gv, uv, v, a.alpha, a.limit);
               uint32_t hq[NTH][2], sbq[NTH];
               quant_block<NTH>(v, hq, sbq);
               if (n < ntok) {
@@ -3219,13 +3266,17 @@ constexpr int MX_XB_WIDE = 12;
 // Rows of exactly MX_STATIC chunks (K = 2817..2944: GPT-OSS's 2880) take variants with the chunk
 // count compiled in (`st`).
 constexpr int MX_STATIC = 23;
-template <int FMT> static UpSmallKernel up_small_k(bool one, int T, bool st = false) {
+// MLX gate-up rows of exactly 2·MLX_NCW chunks (K = 2048: Qwen3.5-35B-A3B) take the single-round
+// stream of MLX_NCW chunks per wave.
+constexpr int MLX_NCW = 16;
+template <int FMT> static UpSmallKernel up_small_k(bool one, int T, bool st = false, bool stat = false) {
   if constexpr (FMT == Q_MXFP4) {
     if (one && st) return T == 1 ? up_small_mx<MX_ONE, true, 2, MX_STATIC> : up_small_mx<MX_ONE, true, MX_XB_WIDE, MX_STATIC>;
     if (T == 1) return one ? up_small_mx<MX_ONE, true, 2> : up_small_mx<16, false, 2>;
     return one ? up_small_mx<MX_ONE, true, MX_XB_WIDE> : up_small_mx<16, false, MX_XB_WIDE>;
   }
   else if constexpr (is_mlx<FMT>()) {
+    if (st && T == 1 && stat) return up_small<FMT, MLX_NCW, 1, 2, true, MLX_NCW>;
     if (st) return T == 1 ? up_small<FMT, decode_depth<FMT>(), 1, 2, true> : up_small<FMT, decode_depth<FMT>(), 1, MX_XB_WIDE, true>;
     return T == 1 ? up_small<FMT, decode_depth<FMT>(), 1, 2> : up_small<FMT, decode_depth<FMT>(), 1, MX_XB_WIDE>;
   }
@@ -3446,8 +3497,8 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
   // The MXFP4 static-count variant needs every up row (over H) at MX_STATIC chunks.
   case Q_MXFP4: up = up_small_k<Q_MXFP4>(one_up, T, (a.hidden + 127) / 128 == MX_STATIC); break;
   case Q_BF16: up = up_small_k<Q_BF16>(true, T); break;
-  case Q_MLX4: up = up_small_k<Q_MLX4>(true, T, mlx_staged_up(a.hidden)); break;
-  default: up = up_small_k<Q_MLX8>(true, T, mlx_staged_up(a.hidden)); break;
+  case Q_MLX4: up = up_small_k<Q_MLX4>(true, T, mlx_staged_up(a.hidden), (a.hidden + 63) / 64 == 2 * MLX_NCW); break;
+  default: up = up_small_k<Q_MLX8>(true, T, mlx_staged_up(a.hidden), (a.hidden + 63) / 64 == 2 * MLX_NCW); break;
   }
   // The decode kernels stage rows in dynamic LDS beyond the default 64 KiB window (gfx950 has
   // 160 KiB per compute unit).
@@ -3465,6 +3516,7 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
                         (const void *)up_small_k<Q_MXFP4>(true, 1, true), (const void *)up_small_k<Q_MXFP4>(true, SMALL_T, true),
                         (const void *)up_small_k<Q_MLX4>(true, 1, true), (const void *)up_small_k<Q_MLX4>(true, SMALL_T, true),
                         (const void *)up_small_k<Q_MLX8>(true, 1, true), (const void *)up_small_k<Q_MLX8>(true, SMALL_T, true),
+                        (const void *)up_small_k<Q_MLX4>(true, 1, true, true), (const void *)up_small_k<Q_MLX8>(true, 1, true, true),
                         (const void *)down_small_k<Q_MLX4>(4, true, true), (const void *)down_small_k<Q_MLX4>(9, true, true),
                         (const void *)down_small_k<Q_MLX8>(4, true, true), (const void *)down_small_k<Q_MLX8>(9, true, true)};
     // Best effort: HIP on gfx950 accepts launches up to the hardware LDS size without it, and
