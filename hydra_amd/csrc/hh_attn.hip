@@ -152,8 +152,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         if (base + 16 * st + 4 * g + i < last) mt = fmaxf(mt, sc[st][i]);
-    mt = fmaxf(mt, __shfl_xor(mt, 16));
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    mt = max_lane_groups(mt);
     const float mn = fmaxf(M, mt);
     const float corr = __expf(M - mn);
     float ps = 0.f;
@@ -170,8 +169,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
         phi[st >> 1][4 * (st & 1) + i] = hi;
         plo[st >> 1][4 * (st & 1) + i] = (_Float16)(p - (float)hi);
       }
-    ps += __shfl_xor(ps, 16);
-    ps += __shfl_xor(ps, 32);
+    ps = sum_lane_groups(ps);
     L = L * corr + ps;
     M = mn;
     // Lane (g, l16) holds output rows 4g .. 4g + 3: their heads' rescale factors.

@@ -60,14 +60,32 @@ __device__ __forceinline__ bf16x8 mxfp4_to_bf16(uint32_t w, float scale) {
 constexpr int NTX = 2;   // terms of the expert input x
 constexpr int NTH = 3;   // terms of the activation h
 
+// Exchanges across the 4 lane groups (rows of 16 lanes) on gfx950's row swaps, VALU instructions
+// (a shuffle is an LDS-crossbar round trip): with both operands v, permlane32_swap leaves
+// (v[l], v[l ^ 32]) in the two results of every lane, in one order or the other, and
+// permlane16_swap (v[l], v[l ^ 16]). Every lane of the wave must be active.
+__device__ __forceinline__ float max_lane_groups(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+// (g0 + g1) + (g2 + g3) of a value held by the 4 lane groups, identical in every lane (the two
+// operands of each addition come in either order: the same sum).
+__device__ __forceinline__ float sum_lane_groups(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+
 template <int NTERM>
 __device__ __forceinline__ void quant_block(const float (&v)[8], uint32_t (&q)[NTERM][2],
                                             uint32_t (&sb)[NTERM]) {
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  amax = fmaxf(amax, __shfl_xor(amax, 16));
-  amax = fmaxf(amax, __shfl_xor(amax, 32));
+  amax = max_lane_groups(amax);
   const int eb = (int)((__float_as_uint(amax) >> 23) & 0xFF);   // biased exponent (0: zero/tiny)
   const int b0 = eb > 7 ? eb - 7 : 0;
   float r[8];

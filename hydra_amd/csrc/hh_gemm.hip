@@ -193,13 +193,6 @@ template <> struct Fmt<Q_MLX8> : FmtMLX<8> {};
 template <int FMT> constexpr bool is_mlx() { return FMT == Q_MLX4 || FMT == Q_MLX8; }
 
 // ---- shared pieces of the canonical arithmetic -------------------------------------------------
-// Σ of one value held by the 4 lane groups of a token column, in a fixed pairing:
-// (g0 + g1) + (g2 + g3), identical in every lane.
-__device__ __forceinline__ float sum_lane_groups(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
-}
 
 // Sum of 8 bf16 values of one 16-byte vector, in index order.
 __device__ __forceinline__ float sum8_bf16(const u32x4 &v) {
