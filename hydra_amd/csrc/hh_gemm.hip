@@ -3185,12 +3185,23 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       steps(acc[0]);
     } else {
+      // The (scale | bias) words of D rows 4g .. 4g+3 straight from the stage (16 contiguous
+      // bytes of each), instead of the lane's own row's words moved across lanes by shuffles.
+      const uint8_t *sbb = lds + (step % S) * C::STAGE + C::OFF_SB + wave * 1024 + 16 * g;
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
         const int c = 2 * ls + p;
         if (64 * c >= K) break;
         chunk_mfma<FMT, NM, NT, NH>(acc[c & 1], cur.w[p], at_unused,
-                                    [&](int st, int hh, int v) { return curb.b[p][st][hh][v]; }, c, g, K);
+                                    [&](int st, int hh, int v) { return curb.b[p][st][hh][v]; }, c, g, K,
+                                    [&](int m) {
+                                      const u32x4 sv = *(const u32x4 *)(sbb + p * 256 + 64 * m);
+                                      const u32x4 bv = *(const u32x4 *)(sbb + 512 + p * 256 + 64 * m);
+                                      u32x4 r;
+#pragma unroll
+                                      for (int ii = 0; ii < 4; ++ii) r[ii] = (sv[ii] & 0xFFFFu) | (bv[ii] << 16);
+                                      return r;
+                                    });
       }
     }
     if (last_stage) {
