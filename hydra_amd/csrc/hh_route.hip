@@ -448,8 +448,39 @@ __global__ __launch_bounds__(64 * RLW) void route_logits_kernel(RouteArgs a) {
 // values do not depend on how rows are grouped) and wave 1 the shared gate's; wave 0 ranks them
 // (TopK's order: larger value, then smaller index, whatever the insertion order) and writes the
 // token's routing.
+// Development timeline (built only with -DHH_TRACE): wall-clock stamps (100 MHz) per workgroup of
+// the small-batch router kernels and of route_select_kernel, [block][point], read as kernel 0 of
+// the decode kernels' timeline.
+#ifdef HH_TRACE
+constexpr int kRtTraceBlocks = 4096, kRtTracePoints = 8;
+static __device__ uint64_t hh_trace_rt[kRtTraceBlocks * kRtTracePoints];
+#define HH_RT(point)                                                                               \
+  do {                                                                                             \
+    if ((threadIdx.x & 63) == 0 && blockIdx.x < kRtTraceBlocks)                                    \
+      hh_trace_rt[blockIdx.x * kRtTracePoints + (point)] = wall_clock64();                         \
+  } while (0)
+hipError_t trace_read_route(void *out, size_t bytes) {
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(hh_trace_rt), std::min(bytes, sizeof(hh_trace_rt)), 0,
+                             hipMemcpyDeviceToHost);
+}
+hipError_t trace_clear_route() {
+  static uint64_t zeros[kRtTraceBlocks * kRtTracePoints];
+  return hipMemcpyToSymbol(HIP_SYMBOL(hh_trace_rt), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
+}
+// Point 7 of route_select_kernel's rows: the token's candidate count.
+#define HH_RT_NC(nc)                                                                               \
+  do {                                                                                             \
+    if (threadIdx.x == 0 && blockIdx.x < kRtTraceBlocks) hh_trace_rt[blockIdx.x * kRtTracePoints + 7] = (uint64_t)(nc); \
+  } while (0)
+#else
+#define HH_RT(point) do {} while (0)
+#define HH_RT_NC(nc) do {} while (0)
+#endif
+
+// A T=2048 batch is 2048 four-wave workgroups: the GEMMA variant took 129 VGPRs, three per
+// compute unit (about three rounds of them); at most 128 gives four (five spills).
 template <bool gemma>
-__global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(gemma ? 4 : 5))) void route_select_kernel(RouteArgs a) {
   warm_kernargs<sizeof(RouteArgs)>();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int t = blockIdx.x;
@@ -459,8 +490,11 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
   __shared__ double s_sg;
   const float *lg = a.lg32 + (size_t)t * a.experts;
   const float *wn = a.wn;
+  if (wave == 0) HH_RT(0);
   const TokenScreen ts = screen_token<gemma, 4>(a, t, [&](int e) { return lg[e]; },
                                                 [&](int e) { return wn[e]; }, s_cl[wave], s_rk);
+  if (wave == 0) HH_RT(1);
+  HH_RT_NC(ts.nc);
   const double root = gemma ? pow((double)a.hidden, -0.5) : 1.0;
   const uint16_t *xr = a.xr + (size_t)t * a.hidden;
   for (int c = wave; c < ts.nc; c += 4) {
@@ -475,7 +509,9 @@ __global__ __launch_bounds__(256) void route_select_kernel(RouteArgs a) {
     const double sg = exact_logit<false>(a, a.x + (size_t)t * a.hidden, a.shared_gate, 1.0, 1.0);
     if (lane == 0) s_sg = sg;
   }
+  if (wave == 0) HH_RT(2);
   __syncthreads();
+  if (wave == 0) HH_RT(3);
   if (wave != 0) return;
   TopK tk;
   for (int c = 0; c < ts.nc; ++c) tk.insert(s_v[c], s_cl[0][c], a.top_k);
@@ -496,27 +532,6 @@ __global__ __launch_bounds__(256) void quant_x_kernel(RouteArgs a) {
   quant_x_wave(a, w / per_t, 16 * (w % per_t));
 }
 
-// Development timeline (built only with -DHH_TRACE): wall-clock stamps (100 MHz) of the small-batch
-// router kernel per workgroup, [block][point], read as kernel 0 of the decode kernels' timeline.
-#ifdef HH_TRACE
-constexpr int kRtTraceBlocks = 4096, kRtTracePoints = 8;
-static __device__ uint64_t hh_trace_rt[kRtTraceBlocks * kRtTracePoints];
-#define HH_RT(point)                                                                               \
-  do {                                                                                             \
-    if ((threadIdx.x & 63) == 0 && blockIdx.x < kRtTraceBlocks)                                    \
-      hh_trace_rt[blockIdx.x * kRtTracePoints + (point)] = wall_clock64();                         \
-  } while (0)
-hipError_t trace_read_route(void *out, size_t bytes) {
-  return hipMemcpyFromSymbol(out, HIP_SYMBOL(hh_trace_rt), std::min(bytes, sizeof(hh_trace_rt)), 0,
-                             hipMemcpyDeviceToHost);
-}
-hipError_t trace_clear_route() {
-  static uint64_t zeros[kRtTraceBlocks * kRtTracePoints];
-  return hipMemcpyToSymbol(HIP_SYMBOL(hh_trace_rt), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
-}
-#else
-#define HH_RT(point) do {} while (0)
-#endif
 
 // ---- small batches (T ≤ 16): every logit exactly in fp64 -----------------------------------------
 // One wave per (token, expert) pair, spread over many compute units (one compute unit's load path
