@@ -79,6 +79,23 @@ __device__ __forceinline__ float sum_lane_groups(float v) {
   return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
 
+// quant_block's term bytes regrouped for 8-byte stores: lane group g holds, for j = 0..3, the
+// 2 bytes at columns 2g + 8j of its token's 32-column block ((d0, d1) = pieces (0 | 1 << 16,
+// 2 | 3 << 16)); afterwards it holds columns 8g .. 8g + 7 ((e0, e1)), i.e. piece g of groups
+// 0..3 in order: a 4 × 4 transpose of 16-bit pieces across the lane groups (a dword swap between
+// groups g and g ^ 2, then a half-dword swap between g and g ^ 1). Every lane must be active.
+__device__ __forceinline__ void transpose_pieces(uint32_t d0, uint32_t d1, int g, uint32_t &e0, uint32_t &e1) {
+  // Groups 0, 1 keep d0 and take d0 of g + 2; groups 2, 3 keep d1 and take d1 of g − 2.
+  const auto r = __builtin_amdgcn_permlane32_swap(d0, d1, false, false);
+  const uint32_t A = r[0], B = r[1];   // (0,1): A = own d0, B = d0 of g+2; (2,3): A = d1 of g−2, B = own d1
+  const bool odd = g & 1;
+  const uint32_t S = odd ? ((A & 0xFFFFu) | (B << 16)) : ((A >> 16) | (B & 0xFFFF0000u));
+  const auto q = __builtin_amdgcn_permlane16_swap(S, S, false, false);
+  const uint32_t R = odd ? q[0] : q[1];   // S of g ^ 1
+  e0 = odd ? ((R & 0xFFFFu) | (A & 0xFFFF0000u)) : ((A & 0xFFFFu) | (R << 16));
+  e1 = odd ? ((R >> 16) | (B & 0xFFFF0000u)) : ((B & 0xFFFFu) | (R & 0xFFFF0000u));
+}
+
 template <int NTERM>
 __device__ __forceinline__ void quant_block(const float (&v)[8], uint32_t (&q)[NTERM][2],
                                             uint32_t (&sb)[NTERM]) {

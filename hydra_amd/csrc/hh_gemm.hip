@@ -2803,13 +2803,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
               activate_n<8>(a.act, gv, uv, v, a.alpha, a.limit);
               uint32_t hq[NTH][2], sbq[NTH];
               quant_block<NTH>(v, hq, sbq);
+              // Each lane's 8 contiguous bytes of every term (one store each).
+              uint32_t he[NTH][2];
+#pragma unroll
+              for (int t = 0; t < NTH; ++t) transpose_pieces(hq[t][0], hq[t][1], g, he[t][0], he[t][1]);
               if (n < ntok) {
                 const int i0 = rw / 2;
 #pragma unroll
                 for (int t = 0; t < NTH; ++t) {
-                  uint8_t *row = a.hq + ((size_t)eslot[tt] * NTH + t) * a.hld + i0 + 2 * g;
-#pragma unroll
-                  for (int j = 0; j < 4; ++j) *(uint16_t *)(row + 8 * j) = (uint16_t)(hq[t][j >> 1] >> (16 * (j & 1)));
+                  uint8_t *row = a.hq + ((size_t)eslot[tt] * NTH + t) * a.hld + i0;
+                  *(u32x2 *)(row + 8 * g) = u32x2{he[t][0], he[t][1]};
                   if (g == 0) a.hs[((size_t)eslot[tt] * NTH + t) * (a.hld / 32) + i0 / 32] = (uint8_t)sbq[t];
                 }
               }
