@@ -3379,11 +3379,11 @@ template <int PH, int RR, int TT> static bool mx3_fits(const GemmArgs &a) {
   const int K = PH == PH_UP ? a.hidden : a.grp[0].inter;
   return (K + 127) / 128 >= Mx3<PH, RR, TT>::S;
 }
-static bool mx3_wide(int phase, const GemmArgs &a) { return phase == PH_UP && a.max_work >= 64; }
+static bool mx3_wide(int phase, const GemmArgs &a) { return a.max_work >= 64; }
 static bool use_mx3(int phase, const GemmArgs &a, int nt) {
   if (a.slots != a.top_k || nt != 2) return false;
   if (!mx3_wide(phase, a)) return phase == PH_UP ? mx3_fits<PH_UP, 1, 1>(a) : mx3_fits<PH_DOWN, 1, 1>(a);
-  return mx3_fits<PH_UP, 2, 1>(a);
+  return phase == PH_UP ? mx3_fits<PH_UP, 2, 1>(a) : mx3_fits<PH_DOWN, 2, 1>(a);
 }
 
 template <int PH, int RR, int TT> static hipError_t launch_mx3(GemmArgs a, hipStream_t s, Timing tm) {
@@ -3439,7 +3439,7 @@ hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &args, hipSt
     return launch_mx3<PH_DOWN, 1, 2>(a, s, tm);
   if (quant == Q_MXFP4 && use_mx3(phase, a, nt)) {
     if (!mx3_wide(phase, a)) return phase == PH_UP ? launch_mx3<PH_UP, 1, 1>(a, s, tm) : launch_mx3<PH_DOWN, 1, 1>(a, s, tm);
-    return launch_mx3<PH_UP, 2, 1>(a, s, tm);
+    return phase == PH_UP ? launch_mx3<PH_UP, 2, 1>(a, s, tm) : launch_mx3<PH_DOWN, 2, 1>(a, s, tm);
   }
   if (quant != Q_MXFP4) {
     // BF16 / MLX: the persistent ring kernel, one workgroup per compute unit.
