@@ -148,7 +148,10 @@ constexpr int kMaxTokens = 1 << 16;  // tokens per call
 struct Scratch {
   size_t lg64, lg32, wn, topk_idx, topk_w, slot_w, seg, order, work, n_work, h_hi, h_lo, slot_out;
   size_t xq, xs, hq, hs, status, total;
+  size_t work_half, n_work_half;   // half_down: the down phase's items of tile_tokens / 2
   int slots, positions, ldh, max_work, tile_tokens, nt;
+  int max_work_half;
+  bool half_down;
   int xld, hld;   // MXFP4: row lengths of the fp8 operand terms (multiples of 512)
 };
 
@@ -195,6 +198,13 @@ Scratch plan(const hh_moe_desc &d, int T) {
   s.order = take(sizeof(int32_t) * (size_t)s.positions);
   s.work = take(sizeof(int4) * (size_t)s.max_work);
   s.n_work = take(sizeof(int32_t));
+  // MXFP4 batches of 64-token items: the down product takes 32-token items of 256 rows, which
+  // re-read the three activation terms half as often per row as 128-row tiles (a 256 × 64 tile
+  // does not fit the register file).
+  s.half_down = d.quant == HH_QUANT_MXFP4 && s.nt == 4 && !shared;
+  s.max_work_half = s.half_down ? std::min(E, A) + (A + s.tile_tokens / 2 - 1) / (s.tile_tokens / 2) : 0;
+  s.work_half = take(sizeof(int4) * (size_t)s.max_work_half);
+  s.n_work_half = take(s.half_down ? sizeof(int32_t) : 0);
   const bool mx = d.quant == HH_QUANT_MXFP4;
   s.h_hi = take(mx ? 0 : sizeof(uint16_t) * (size_t)s.positions * s.ldh);
   s.h_lo = take(mx ? 0 : sizeof(uint16_t) * (size_t)s.positions * s.ldh);
@@ -330,6 +340,9 @@ hh::RouteArgs route_args(const hh_moe_desc &d, const hh_moe_weights *w, uint8_t 
   r.work = (int4 *)(base + s.work);
   r.n_work = (int32_t *)(base + s.n_work);
   r.max_work = s.max_work;
+  r.work_half = s.half_down ? (int4 *)(base + s.work_half) : nullptr;
+  r.n_work_half = s.half_down ? (int32_t *)(base + s.n_work_half) : nullptr;
+  r.max_work_half = s.max_work_half;
   if (d.quant == HH_QUANT_MXFP4 && x) {
     r.xq = base + s.xq;
     r.xs = base + s.xs;
@@ -535,7 +548,15 @@ int forward_layer(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w, co
   rows = hh::gemm_rows_per_block(d->quant, 1);
   g.row_tiles = (d->hidden + rows - 1) / rows;
   if ((rc = phase_timing(ctx, &tm, noalloc))) return rc;
-  HH_HIP(hh::launch_gemm(1, d->quant, s.nt, g, ctx->stream, tm));
+  if (s.half_down) {
+    hh::GemmArgs gd = g;
+    gd.work = r.work_half;
+    gd.n_work = r.n_work_half;
+    gd.max_work = s.max_work_half;
+    HH_HIP(hh::launch_gemm(1, d->quant, s.nt / 2, gd, ctx->stream, tm));
+  } else {
+    HH_HIP(hh::launch_gemm(1, d->quant, s.nt, g, ctx->stream, tm));
+  }
   if ((rc = phase_timing(ctx, &tm, noalloc))) return rc;
   HH_HIP(hh::launch_combine(g.slot_out, s.slots, d->hidden, T, y, resid, ctx->stream, tm));
   ctx->dispatches += 6;   // route logits, select, dispatch, gate-up, down, combine

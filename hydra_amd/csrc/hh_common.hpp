@@ -302,6 +302,11 @@ struct RouteArgs {
   int4 *work;                   // [max_work]
   int32_t *n_work;              // [1]
   int32_t max_work;
+  // Optional (null: not written): the same routed segments in items of tile_tokens / 2 tokens,
+  // for a down phase with half the gate-up's token tile (no shared expert).
+  int4 *work_half;              // [max_work_half]
+  int32_t *n_work_half;         // [1]
+  int32_t max_work_half;
 };
 
 // The kernel's argument block into the scalar cache in one round: one dword of each 64-byte line

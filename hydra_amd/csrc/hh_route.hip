@@ -133,6 +133,20 @@ __device__ __forceinline__ void dispatch_batch(const RouteArgs &a, const int32_t
     for (int j = 0; j * TN < n; ++j)
       a.work[s_tiles[e] + j] = make_int4(e, s_off[e] + j * TN, min(TN, n - j * TN), 0);
   }
+  if (a.work_half) {
+    // The same segments in items of TN / 2 tokens (the list's users have no shared expert).
+    const int TH = TN / 2;
+    __syncthreads();   // s_tiles was read above
+    for (int e = tid; e < E; e += NT) s_tiles[e] = (s_cnt[e] + TH - 1) / TH;
+    __syncthreads();
+    const int half_tiles = block_exclusive_scan<NW>(s_tiles, E, s_wave);
+    for (int e = tid; e < E; e += NT) {
+      const int n = s_cnt[e];
+      for (int j = 0; j * TH < n; ++j)
+        a.work_half[s_tiles[e] + j] = make_int4(e, s_off[e] + j * TH, min(TH, n - j * TH), 0);
+    }
+    if (tid == 0) *a.n_work_half = half_tiles;
+  }
   int nwork = routed_tiles;
   if (a.shared_gate) {
     // The shared expert is expert id E over every token, after the routed positions.
