@@ -161,10 +161,11 @@ int token_tile_nt(const hh_moe_desc &d, int T) {
   // Prefill work items of 16·nt tokens: MXFP4 32 or 64 (below), BF16 64 once experts
   // average 64 tokens or more (the weight tile is then read once per 64 tokens), else 32.
   if (d.quant == HH_QUANT_BF16 && (int64_t)T * d.top_k >= 64 * (int64_t)d.experts) return 4;
-  // MXFP4 without a shared expert, experts averaging 32 or more tokens, rows long enough for the
-  // LDS rings: 64-token items (the gate-up and down prefill kernels' 64-token tiles; fewer tokens
-  // per expert would leave them mostly padding).
-  if (d.quant == HH_QUANT_MXFP4 && d.shared_intermediate == 0 && (int64_t)T * d.top_k >= 32 * (int64_t)d.experts &&
+  // MXFP4 without a shared expert, experts averaging 16 or more tokens, rows long enough for the
+  // LDS rings: 64-token items for the gate-up (its 256 × 64 tiles skip the MFMAs of padding token
+  // tiles, and an expert's rows are read once per 64 tokens); the down product runs the same
+  // segments as 32-token items (Scratch::half_down).
+  if (d.quant == HH_QUANT_MXFP4 && d.shared_intermediate == 0 && (int64_t)T * d.top_k >= 16 * (int64_t)d.experts &&
       d.hidden >= 1024 && d.intermediate >= 1024)
     return 4;
   return 2;
