@@ -620,10 +620,11 @@ __device__ __forceinline__ void select_batch(const GemmArgs &a, const RouteArgs 
     constexpr int G1 = NW, G2 = NW / 2 > 0 ? NW / 2 : 1;
     const int G = T == 1 ? G1 : G2, t = wave / G;
     const double *lg = ra.lg64 + (size_t)t * (E + 1);
-    const TopK tk = T == 1 ? (E <= 64 ? topk_rank64<G1>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
+    TopK tk = T == 1 ? (E <= 64 ? topk_rank64<G1>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
                                       : topk_fast<G1>(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave], s_rk))
                            : (E <= 64 ? topk_rank64<G2>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
                                       : topk_fast<G2, 1>(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave], s_rk));
+    prob_order(tk, K, ra.router);
     if (wave % G == 0) {
       if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
       if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
@@ -631,8 +632,9 @@ __device__ __forceinline__ void select_batch(const GemmArgs &a, const RouteArgs 
   } else {
     for (int t = wave; t < T; t += NW) {
       const double *lg = ra.lg64 + (size_t)t * (E + 1);
-      const TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave])
+      TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave])
                               : topk_fast(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave]);
+      prob_order(tk, K, ra.router);
       if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
       if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
     }
@@ -1212,10 +1214,11 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
 #ifdef HH_TRACE
     { volatile double first = lg[lane % E]; (void)first; HH_TR(1, 6); }
 #endif
-    const TopK tk = T == 1 ? (E <= 64 ? topk_rank64<4>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
+    TopK tk = T == 1 ? (E <= 64 ? topk_rank64<4>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
                                       : topk_fast<4>(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave], s_rk))
                            : (E <= 64 ? topk_rank64<2>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
                                       : topk_fast<2, 1>(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave], s_rk));
+    prob_order(tk, K, ra.router);
     HH_TR(1, 7);
     if (wave % G == 0) {
       if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
@@ -1224,8 +1227,9 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
   } else {
     for (int t = wave; t < T; t += 4) {
       const double *lg = ra.lg64 + (size_t)t * (E + 1);
-      const TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave])
+      TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave])
                               : topk_fast(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave]);
+      prob_order(tk, K, ra.router);
       if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
       if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
     }
@@ -1695,7 +1699,8 @@ __global__ __launch_bounds__(256, 2) void decode_mx(GemmArgs a, RouteArgs ra, Fu
     for (int e = lane; e < E1; e += 64)
       lg[e] = __hip_atomic_load(ra.lg64 + (size_t)t * E1 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_wave_barrier();
-    const TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave]) : topk_exact(lg, E, K);
+    TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave]) : topk_exact(lg, E, K);
+    prob_order(tk, K, ra.router);
     if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
     if (b == f.R) finish_token(ra, t, tk, ra.shared_gate ? lg[E] : 0.0);
     if (!up_role) {

@@ -529,6 +529,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(gemma ? 4 :
   if (wave != 0) return;
   TopK tk;
   for (int c = 0; c < ts.nc; ++c) tk.insert(s_v[c], s_cl[0][c], a.top_k);
+  prob_order(tk, a.top_k, a.router);
   finish_token(a, t, tk, a.shared_gate ? s_sg : 0.0);
 }
 
@@ -816,7 +817,8 @@ __global__ __launch_bounds__(256) void select_small_kernel(RouteArgs a) {
   __shared__ double s_cv[4][kFastCand];
   for (int t = wave; t < a.tokens; t += 4) {
     const double *lg = a.lg64 + (size_t)t * E1;
-    const TopK tk = topk_fast(lg, a.experts, a.top_k, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave]);
+    TopK tk = topk_fast(lg, a.experts, a.top_k, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave]);
+    prob_order(tk, a.top_k, a.router);
     finish_token(a, t, tk, a.shared_gate ? lg[a.experts] : 0.0);
   }
 }
@@ -899,7 +901,8 @@ __global__ __launch_bounds__(256) void select_lg64_kernel(RouteArgs a) {
   __shared__ double s_cv[4][kFastCand];
   if (t >= a.tokens) return;
   const double *lg = a.lg64 + (size_t)t * (a.experts + 1);
-  const TopK tk = topk_fast(lg, a.experts, a.top_k, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave]);
+  TopK tk = topk_fast(lg, a.experts, a.top_k, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave]);
+  prob_order(tk, a.top_k, a.router);
   finish_token(a, t, tk, a.shared_gate ? lg[a.experts] : 0.0);
 }
 

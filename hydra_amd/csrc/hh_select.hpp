@@ -74,6 +74,42 @@ struct TopK {
   }
 };
 
+// SOFTMAX_TOPK_RENORM and GEMMA rank the experts by fp64 probability exp(l − max) / Σ, ties to
+// the smaller index (QwenReferenceOps.swift:164-173, Gemma4ReferenceOps.swift:146-149). The
+// probability is monotone in the logit, so it orders the experts as the logit does except where
+// distinct logits give the same probability. Where exp(l − max) is 0 (l − max < −745.13: every
+// such expert's probability is exactly 0), the reference takes the zero-probability experts by
+// increasing index. tk holds the logit top-k; when its last ranks are of that class they are
+// replaced by the smallest expert indices outside the non-zero ranks, with logit −∞ (weight 0,
+// as the reference's 0 / Σ). Wave-uniform; a no-op unless the K-th logit is 700 below the first.
+__device__ __forceinline__ void prob_order(TopK &tk, int K, int router) {
+  if (router == R_TOPK_SOFTMAX) return;
+  const double top = tk.v[0];
+  bool low = false;
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r) low |= r < K && tk.v[r] - top < -700.0;
+  if (!low) return;
+  int nz = 0;   // ranks of non-zero probability form a prefix (monotone in the logit)
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r)
+    if (r < K && exp(tk.v[r] - top) != 0.0) nz = r + 1;
+  int e = 0;
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r) {
+    if (r >= nz && r < K) {
+      for (;;) {
+        bool used = false;
+#pragma unroll
+        for (int q = 0; q < kMaxTopK; ++q) used |= q < nz && tk.i[q] == e;
+        if (!used) break;
+        ++e;
+      }
+      tk.i[r] = e++;
+      tk.v[r] = -INFINITY;
+    }
+  }
+}
+
 // Top-k of one token from its exact logits lg[0..E) (E ≤ 512), whole wave: K rounds of a wave
 // arg-max, larger value first and the smaller index on ties.
 __device__ __forceinline__ TopK topk_exact(const double *lg, int E, int K) {

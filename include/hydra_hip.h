@@ -326,7 +326,9 @@ int hh_mlx_dequant(hh_ctx *ctx, const uint32_t *words, const uint16_t *scales,
  * of fp64 logits. Replaces routerTopK / routerTopKBatched / gemmaRouterTopK(Batched)
  * (ForwardEncoder.swift:1183-1200, 1283-1323). logits (fp64 [T][K], the selected experts'
  * logits in rank order), and shared_w (fp32 [T], the shared expert's sigmoid gate) may be
- * NULL.                                                                                        */
+ * NULL. SOFTMAX_TOPK_RENORM and GEMMA rank by fp64 probability as the reference does: experts
+ * whose exp(logit − max) is 0 tie and are taken by increasing index (weight 0, logit −inf in
+ * `logits`), QwenReferenceOps.swift:164-173, Gemma4ReferenceOps.swift:146-149.               */
 int hh_router_topk(hh_ctx *ctx, const hh_moe_desc *desc, const hh_moe_weights *w,
                    const uint16_t *x_router, int32_t tokens, double *logits,
                    int32_t *topk_idx, float *topk_w, float *shared_w);

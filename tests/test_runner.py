@@ -113,3 +113,93 @@ def test_runner_equals_calls_one_by_one(T):
         runner.close()
     finally:
         ctx.close()
+
+
+@pytest.mark.parametrize("T", [1, 64])
+def test_runner_stack_against_chained_oracle(T):
+    """The same 3-layer stack with hooks against the fp64 oracle chained layer by layer
+    (ModelRunner.swift:110-230, 418-547: per layer the token mixer, then the MoE half on the
+    residual stream): the hook is the oracle's matvec of the current residual, the block
+    `block_forward_layer`. Bars: the final residual stream and every hook output within
+    rel-L2 1e-3; every layer's top-k indices equal (read from the one-by-one calls, which the
+    test above shows equal to the runner bit for bit)."""
+    import torch
+    from hydra_amd._lib import MatrixC, check, lib
+    from hydra_amd.layer import Context, MoELayer, Runner, to_device
+    from oracle import oracle as O
+    print(f"[gpu] runner vs oracle T={T}", flush=True)
+    dev = "cuda:0"
+    ctx = Context(0)
+    try:
+        rng = np.random.default_rng(91)
+        host_layers, layers, mats, probes, norms_host = [], [], [], [], []
+        dense = torch.zeros((T, H), dtype=torch.float32, device=dev)
+        for i, (d, rb) in enumerate(DESCS):
+            hl = synth.make_layer(d, seed=92 + i, router_bits=rb)
+            host_layers.append(hl)
+            ml = MoELayer(hl, ctx)
+            gemma = d.router == F.ROUTER_GEMMA
+            nh = _norms(rng, gemma)
+            norms_host.append(nh)
+            norms = {k: (v if k == "eps" else to_device(v, dev)) for k, v in nh.items()}
+            layers.append((ml, norms, dense if gemma else None))
+            rows = H if gemma else 64
+            wh = synth.bf16_normal(100 + i, "hook", rows * H, 0.0, 0.05)
+            w = to_device(wh, dev)
+            mats.append((MatrixC(F.QUANT_BF16, rows, H, 64, C.c_void_p(w.data_ptr()), None, None, None), w, wh, rows))
+            probes.append(dense if gemma else torch.empty((T, rows), dtype=torch.float32, device=dev))
+        x0 = (rng.standard_normal((T, H)) * 2).astype(np.float32)
+
+        def hook(l, hidden):
+            check(lib().hh_expert_gemm(ctx.handle, C.byref(mats[l][0]), C.c_void_p(hidden.data_ptr()),
+                                       T, C.c_void_p(probes[l].data_ptr())))
+
+        # the oracle chained in fp64
+        hid_o = x0.astype(np.float64)
+        ref_probes, ref_idx = [], []
+        for l, hl in enumerate(host_layers):
+            _, _, wh, rows = mats[l]
+            p = O.matvec(F.QUANT_BF16, rows, H, wh, x=hid_o)
+            ref_probes.append(p)
+            gemma = hl["desc"].router == F.ROUTER_GEMMA
+            lg = O.router_logits(hl["desc"], hl, O.f64_to_bf16(
+                O.rms_norm(hid_o, O.bf16_to_f32(norms_host[l]["pre_norm"]), norms_host[l]["eps"],
+                           pow_form=gemma)) if not gemma else O.f32_to_bf16(hid_o.astype(np.float32)))
+            K = hl["desc"].top_k
+            srt = np.sort(lg, axis=1)[:, ::-1]
+            gap = (srt[:, K - 1] - srt[:, K]) / np.maximum(np.abs(srt[:, 0]), 1.0)
+            assert np.all(gap > 1e-6), "near-tie in the test data: change the seed"
+            hid_o, idx, _, _ = O.block_forward_layer(hl, norms_host[l], hid_o,
+                                                     dense_out=p if gemma else None)
+            ref_idx.append(idx)
+        # the calls one by one, with per-layer top-k indices
+        hid = torch.from_numpy(x0.copy()).to(dev)
+        idxs = [torch.empty((T, d.top_k), dtype=torch.int32, device=dev) for d, _ in DESCS]
+        torch.cuda.synchronize()
+        for l, (ml, norms, dn) in enumerate(layers):
+            hook(l, hid)
+            ml.block_forward_into(norms, hid, dn, idx=idxs[l])
+        ctx.synchronize()
+        one = hid.cpu().numpy().copy()
+        for l in range(3):
+            assert np.array_equal(idxs[l].cpu().numpy(), ref_idx[l]), l
+        # the runner
+        hid2 = torch.from_numpy(x0.copy()).to(dev)
+        for p in probes:
+            p.fill_(float("nan"))
+        torch.cuda.synchronize()
+        runner = Runner(ctx, layers)
+        runner.forward(hid2, hook=lambda l: hook(l, hid2))
+        ctx.synchronize()
+        got = hid2.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), one.view(np.uint32))
+        rel = np.linalg.norm(got - hid_o) / np.linalg.norm(hid_o)
+        assert rel < 1e-3, rel
+        for l in range(3):
+            pl = probes[l].cpu().numpy().astype(np.float64)
+            r = np.linalg.norm(pl - ref_probes[l]) / np.linalg.norm(ref_probes[l])
+            assert r < 1e-3, (l, r)
+        print(f"[gpu] runner vs oracle T={T}: rel-L2 {rel:.2e}", flush=True)
+        runner.close()
+    finally:
+        ctx.close()
