@@ -53,6 +53,15 @@ def up_bytes(desc: F.MoEDesc) -> int:
     return sum(lay.sizes[:6])
 
 
+def router_bytes(desc: F.MoEDesc, router_bits: int) -> int:
+    """Bytes of the router matrix every decode step reads: bf16 [E][H], or MLX-affine codes
+    plus a bf16 scale and bias per 64-column group."""
+    E, H = desc.experts, desc.hidden
+    if router_bits:
+        return E * H * router_bits // 8 + E * (H // 64) * 4
+    return E * H * 2
+
+
 def flops_per_token(desc: F.MoEDesc) -> float:
     H, I, K = desc.hidden, desc.intermediate, desc.top_k
     f = 2.0 * K * (2 * I * H + H * I)
@@ -65,11 +74,12 @@ class Workload:
     """`copies` resident copies of one synthetic layer and, per token count, a bank of token
     batches already in HBM."""
 
-    def __init__(self, torch, desc, copies, zipf=None, seed=0):
+    def __init__(self, torch, desc, copies, zipf=None, seed=0, router_bits=0):
         from hydra_amd.layer import Context, MoELayer
         self.torch, self.desc = torch, desc
         t0 = time.time()
-        host = synth.make_layer(desc, seed=seed, zipf=zipf)
+        host = synth.make_layer(desc, seed=seed, zipf=zipf, router_bits=router_bits)
+        self.router_bytes = router_bytes(desc, router_bits)
         log(f"{desc.experts}x{desc.hidden} layer generated in {time.time() - t0:.1f}s")
         self.ctx = Context(0)
         self.layer = MoELayer(host, self.ctx)
@@ -148,7 +158,7 @@ def measure_decode(wl, T, steps, warmup, fused=False):
     if T == 1:
         assert U == desc.top_k, f"T=1 must touch exactly top_k experts, got {U}"
     up_b = U * up_bytes(desc) + T * desc.hidden * 2
-    layer_b = U * F.streamed_expert_bytes(desc) + desc.experts * desc.hidden * 2
+    layer_b = U * F.streamed_expert_bytes(desc) + wl.router_bytes
     wl.ctx.decode_fused(-1)
     if fused:
         return {"T": T, "tokens_per_s": T / sec, "ms_per_step": sec * 1e3, "unique_experts": U,
@@ -270,10 +280,12 @@ def measure_prefill(wl, T, steps, warmup):
     }
 
 
-OTHER = [  # (name, desc, copies, prefill T): BASELINE configs[3] (both bit widths) and [4]
-    ("qwen-35b-a3b-mlx4", F.QWEN_35B_A3B_Q4, 2, 1024),
-    ("qwen-35b-a3b-mlx8", F.QWEN_35B_A3B_Q8, 2, 1024),
-    ("gemma-bf16", F.GEMMA_BF16, 2, 2048),
+OTHER = [  # (name, desc, copies, prefill T, router bits): BASELINE configs[3] (both bit
+    # widths; the router and shared gate 8-bit MLX-affine as the published Qwen checkpoints
+    # store them, Qwen35MoeConfig.swift:340-342) and [4]
+    ("qwen-35b-a3b-mlx4", F.QWEN_35B_A3B_Q4, 2, 1024, 8),
+    ("qwen-35b-a3b-mlx8", F.QWEN_35B_A3B_Q8, 2, 1024, 8),
+    ("gemma-bf16", F.GEMMA_BF16, 2, 2048, 0),
 ]
 
 
@@ -284,12 +296,13 @@ def shared_bytes(desc: F.MoEDesc) -> int:
     return F.streamed_expert_bytes(desc, desc.shared_intermediate) + desc.hidden * 2
 
 
-def measure_other(torch, name, desc, copies, T_prefill, steps, prefill=True, decode_tokens=(1, 8)):
+def measure_other(torch, name, desc, copies, T_prefill, steps, prefill=True, decode_tokens=(1, 8),
+                  router_bits=0):
     """Decode at the given batch sizes and one chunked prefill of another format: whole-layer tokens/s,
     layer GB/s on the bytes touched (distinct routed experts + shared expert + router),
     expert-product TFLOP/s for the prefill."""
     log(f"{name}: decode T={list(decode_tokens)}, prefill T={T_prefill}")
-    wl = Workload(torch, desc, copies=copies)
+    wl = Workload(torch, desc, copies=copies, router_bits=router_bits)
     dec = {}
     for T in decode_tokens:
         d = measure_decode(wl, T, steps if T == 1 else max(50, steps // 4), 20)
@@ -365,6 +378,8 @@ def main():
                     help="the 24-layer FFN-block decode stack only (for profiling)")
     ap.add_argument("--only-attention", action="store_true",
                     help="decode attention only (for profiling)")
+    ap.add_argument("--one-launch", action="store_true",
+                    help="also time the opt-in one-launch MXFP4 decode (hh_ctx_decode_fused)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one 256 MiB device-to-device copy and exit (HBM counter calibration)")
     args = ap.parse_args()
@@ -399,10 +414,11 @@ def main():
             str(k): measure_attention(torch, k) for k in [4096, 32768, 131072]}}))
         return
     if args.only_other:
-        name, desc, copies, Tp = next(o for o in OTHER if o[0] == args.only_other)
+        name, desc, copies, Tp, rb = next(o for o in OTHER if o[0] == args.only_other)
         print(json.dumps({name: measure_other(torch, name, desc, copies, Tp, args.steps,
                                               prefill=not args.no_prefill,
-                                              decode_tokens=[int(t) for t in args.decode_tokens.split(",") if t])}))
+                                              decode_tokens=[int(t) for t in args.decode_tokens.split(",") if t],
+                                              router_bits=rb)}))
         return
     decode, fused, stack = {}, {}, {}
     if not args.only_prefill:
@@ -415,7 +431,7 @@ def main():
             for T in [1, 8]:
                 log(f"decode stack of 24 layers, T={T}: eager and one HIP graph")
                 stack[T] = measure_stack(wl, T, 24, 40, 5)
-            for T in [1, 2, 4, 8]:
+            for T in ([1, 2, 4, 8] if args.one_launch else []):
                 log(f"decode T={T}, one launch")
                 fused[T] = measure_decode(wl, T, max(100, args.steps // 4), 10, fused=True)
         wl.close()
@@ -433,8 +449,9 @@ def main():
         wl.close()
     other = {}
     if not (args.no_other or args.only_t1 or args.only_prefill):
-        for name, desc, copies, Tp in OTHER:
-            other[name] = measure_other(torch, name, desc, copies, Tp, max(100, args.steps // 4))
+        for name, desc, copies, Tp, rb in OTHER:
+            other[name] = measure_other(torch, name, desc, copies, Tp, max(100, args.steps // 4),
+                                        router_bits=rb)
     cpu = None if args.no_cpu else cpu_baseline()
     if args.only_prefill:
         print(json.dumps({"prefill_gpt_oss_120b_zipf": {str(T): v for T, v in prefill.items()}}))

@@ -1039,6 +1039,10 @@ int hh_expert_gemm(hh_ctx *ctx, const hh_matrix *m, const float *x, int32_t T, f
   if (mlx && (!m->biases || m->group_size != 64)) return fail(HH_ESHAPE, "MLX matrices need biases and group_size 64");
   if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)m->weights) & 15)
     return fail(HH_EALIGN, "x, y and weights must be 16-byte aligned");
+  // The down kernels stage scales (and MLX biases) with 16-byte loads and read the MXFP4 row
+  // bias as part of the same one-expert blob.
+  if (((uintptr_t)m->scales | (uintptr_t)m->biases | (uintptr_t)m->bias) & 15)
+    return fail(HH_EALIGN, "scales, biases and bias must be 16-byte aligned");
   if (q == HH_QUANT_MXFP4 && (size_t)R * Kc / 2 > 0x7FFFFFF0u) return fail(HH_ESHAPE, "MXFP4 matrix above 2 GiB");
   if (T == 0) return HH_OK;
   HH_HIP(hipSetDevice(ctx->device));

@@ -15,6 +15,59 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
   return v;
 }
 
+// The wave sums of N values at once (N a power of two ≤ 64) as a reduce-scatter over the same
+// butterfly as wave_sum_f64 (partners l ^ 32, l ^ 16, ..., l ^ 1; every node adds the same two
+// operands, in one order or the other), so each total has wave_sum_f64's bits. While more than
+// one value is left, a level halves them: the lanes with the level's bit clear keep the first
+// half, the others the second (levels 32 and 16 on the row swaps, the rest on shuffles).
+// Returns the total of v[lane >> (6 − log2 N)]. Every lane must be active.
+__device__ __forceinline__ void swap32_f64(double &a, double &b, int m) {
+  const uint64_t ua = (uint64_t)__double_as_longlong(a), ub = (uint64_t)__double_as_longlong(b);
+  uint32_t alo = (uint32_t)ua, ahi = (uint32_t)(ua >> 32), blo = (uint32_t)ub, bhi = (uint32_t)(ub >> 32);
+  if (m == 32) {
+    const auto l = __builtin_amdgcn_permlane32_swap(alo, blo, false, false);
+    const auto h = __builtin_amdgcn_permlane32_swap(ahi, bhi, false, false);
+    alo = l[0]; blo = l[1]; ahi = h[0]; bhi = h[1];
+  } else {
+    const auto l = __builtin_amdgcn_permlane16_swap(alo, blo, false, false);
+    const auto h = __builtin_amdgcn_permlane16_swap(ahi, bhi, false, false);
+    alo = l[0]; blo = l[1]; ahi = h[0]; bhi = h[1];
+  }
+  a = __longlong_as_double((long long)(((uint64_t)ahi << 32) | alo));
+  b = __longlong_as_double((long long)(((uint64_t)bhi << 32) | blo));
+}
+template <int N>
+__device__ __forceinline__ double wave_sum_scatter_f64(double (&v)[N]) {
+  const int lane = threadIdx.x & 63;
+  int c = N;
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) {
+    if (c > 1) {
+      const int h = c / 2;
+#pragma unroll
+      for (int i = 0; i < N / 2; ++i) {
+        if (i < h) {
+          if (m >= 16) {
+            // the pair's two results hold, in every lane, its own and its partner's value of
+            // the half that lane keeps
+            double a = v[i], b = v[i + h];
+            swap32_f64(a, b, m);
+            v[i] = a + b;
+          } else {
+            const bool up = lane & m;
+            const double keep = up ? v[i + h] : v[i], send = up ? v[i] : v[i + h];
+            v[i] = keep + __shfl_xor(send, m);
+          }
+        }
+      }
+      c = h;
+    } else {
+      v[0] += __shfl_xor(v[0], m);
+    }
+  }
+  return v[0];
+}
+
 __device__ __forceinline__ double wave_max_f64(double v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmax(v, __shfl_xor(v, o));

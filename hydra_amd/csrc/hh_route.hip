@@ -823,71 +823,118 @@ __global__ __launch_bounds__(256) void select_small_kernel(RouteArgs a) {
   }
 }
 
-// ---- MLX-affine router: exact logits of every (token, row) pair on the fp64 MFMA -------------
-// One wave per (16-token tile, 16-row tile), rows 0..E-1 the router, row E the shared gate.
-// Per 64-column chunk c (one MLX group) lane (g, l16) takes row r0 + l16 and token t0 + l16 at
-// columns 64c + 16g + s, s = 0..15: step s of the chunk is one v_mfma_f64_16x16x4_f64 whose
-// k index g stands for column 64c + 16g + s in both operands, so the 16 steps cover the
-// chunk's 64 columns once. A = q·scale + bias and B = x are exact in fp64 (an 8-bit code times
-// a bf16 scale has 16 significant bits, the bias aligns within fp64's 53), so each product is
-// exact and the dot is an fp64 sum like the reference's (MLXAffine.matvec,
-// Gemma4ReferenceOps.swift:224-239). D: lane (g, l16) holds rows r0 + g + 4i (i = 0..3) of
-// token t0 + l16 (the f64 MFMA's output layout, unlike the f32 16x16 ones).
-typedef double f64x4 __attribute__((ext_vector_type(4)));
-
+// ---- MLX-affine router: fp64 logits of every (token, row) pair -----------------------------
+// Rows 0..E-1 are the router, row E the shared gate (whose input x the layer requires to equal
+// the router's, so every row reads a.xr). A row's codes are 16-byte vectors v = 0 .. V−1 of NC =
+// 128 / BITS columns each (columns NC·v ..; one MLX group holds 64 / NC vectors); lane l takes the
+// vectors l, l + 64, ... and its partial sum runs over them in that order, column by column:
+// acc = fma(q·scale + bias, x, acc), where q·scale + bias (an 8-bit code times a bf16 scale, plus
+// the bf16 bias) and its product with the bf16 x are exact in fp64, so each step rounds once, like
+// the reference's fp64 sum (MLXAffine.matvec, Gemma4ReferenceOps.swift:224-239). The logit is the
+// wave's xor-butterfly sum of the 64 partials (wave_sum_f64), plus the router bias. That order is
+// fixed per (token, row) whatever the batch size or tiling, so decode and prefill get the same
+// bits. Each wave takes R consecutive rows and walks its token range 4 tokens at a time (one
+// dequantisation per column for 4·R products); T ≤ 16: R = 1, one wave per row and every token
+// (the decode router: ≈ E + 1 waves over the whole chip); T > 16: MLX_RT_R rows over 16-token tiles.
 template <int BITS>
 __device__ __forceinline__ uint32_t mlx_code(const u32x4 &q, int s) {
   if constexpr (BITS == 8) return (q[s >> 2] >> (8 * (s & 3))) & 0xFFu;
   else return (q[s >> 3] >> (4 * (s & 7))) & 0xFu;
 }
 
-template <int BITS>
-__global__ __launch_bounds__(64) void mlx_router_logits_kernel(RouteArgs a) {
+constexpr int MLX_RT_TILE = 16;   // tokens per wave above 16 tokens
+constexpr int MLX_RT_R = 2;       // rows per wave above 16 tokens
+
+template <int BITS, int R, int J>
+__global__ __launch_bounds__(256) void mlx_router_logits_kernel(RouteArgs a) {
   warm_kernargs<sizeof(RouteArgs)>();
-  const int lane = threadIdx.x, g = lane >> 4, l16 = lane & 15;
+  constexpr int NC = 128 / BITS, XV = NC / 8, P = 4;
+  static_assert(R * P == 4 || R * P == 8 || R * P == 16, "the reduce-scatter's lane mapping");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int E = a.experts, H = a.hidden, T = a.tokens;
   const int rows = E + (a.shared_gate ? 1 : 0);
-  const int rtiles = (rows + 15) / 16;
-  const int tt = blockIdx.x / rtiles, rt = blockIdx.x - tt * rtiles;
-  const int t0 = tt * 16, r0 = rt * 16;
-  const int row = min(r0 + l16, rows - 1), tok = min(t0 + l16, T - 1);
-  const bool sg = row == E;
-  const int wpr = H * BITS / 32, gpr = H / 64;   // words and groups per row
-  const uint32_t *qrow = sg ? a.sg_words : a.rq_words + (size_t)row * wpr;
-  const uint16_t *srow = sg ? a.sg_scales : a.rq_scales + (size_t)row * gpr;
-  const uint16_t *brow = sg ? a.sg_biases : a.rq_biases + (size_t)row * gpr;
-  const uint16_t *xrow = (sg ? a.x : a.xr) + (size_t)tok * H;
-  f64x4 acc = {0.0, 0.0, 0.0, 0.0};
-  for (int c = 0; c < gpr; ++c) {
-    const int col = 64 * c + 16 * g;
-    u32x4 q;
-    if constexpr (BITS == 8) q = *(const u32x4 *)(qrow + col / 4);
-    else {
-      const u32x2 h = *(const u32x2 *)(qrow + col / 8);
-      q = u32x4{h[0], h[1], 0u, 0u};
-    }
-    const u32x4 x0 = *(const u32x4 *)(xrow + col), x1 = *(const u32x4 *)(xrow + col + 8);
-    const double sc = (double)bf16_bits_to_f32(srow[c]), bi = (double)bf16_bits_to_f32(brow[c]);
+  const int waves_per_tile = (rows + R - 1) / R, blocks_per_tile = (waves_per_tile + 3) / 4;
+  const int tile = blockIdx.x / blocks_per_tile;
+  const int wid = (blockIdx.x - tile * blocks_per_tile) * 4 + wave;
+  if (wid >= waves_per_tile) return;   // no barriers below
+  const int r0 = wid * R;
+  const int tsz = T <= RT_TOK ? T : MLX_RT_TILE;
+  const int t0 = tile * tsz, t1 = min(T, t0 + tsz);
+  const int V = H / NC, wpr = H * BITS / 32, gpr = H / 64;
+  // The rows' code vectors and group (scale, bias) of this lane, once: vectors past the row
+  // (J·64 > V) are zero codes with zero scale and bias, adding exactly nothing.
+  u32x4 q[R][J];
+  double sc[R][J], bi[R][J];
 #pragma unroll
-    for (int st = 0; st < 16; ++st) {
-      const double w = fma((double)mlx_code<BITS>(q, st), sc, bi);
-      const u32x4 &xv = st < 8 ? x0 : x1;
-      const uint32_t xb = (xv[(st & 7) >> 1] >> (16 * (st & 1))) & 0xFFFFu;
-      acc = __builtin_amdgcn_mfma_f64_16x16x4f64(w, (double)bf16_bits_to_f32(xb), acc, 0, 0, 0);
+  for (int r = 0; r < R; ++r) {
+    const int row = min(r0 + r, rows - 1);
+    const bool sg = row == E;
+    const uint32_t *qr = sg ? a.sg_words : a.rq_words + (size_t)row * wpr;
+    const uint16_t *sr = sg ? a.sg_scales : a.rq_scales + (size_t)row * gpr;
+    const uint16_t *br = sg ? a.sg_biases : a.rq_biases + (size_t)row * gpr;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const int v = lane + 64 * j, vc = min(v, V - 1);
+      q[r][j] = *(const u32x4 *)(qr + 4 * vc);
+      sc[r][j] = (double)bf16_bits_to_f32(sr[vc * NC / 64]);
+      bi[r][j] = (double)bf16_bits_to_f32(br[vc * NC / 64]);
+      if (v >= V) { q[r][j] = u32x4{0u, 0u, 0u, 0u}; sc[r][j] = 0.0; bi[r][j] = 0.0; }
     }
   }
-  const int t = t0 + l16;
-  if (t < T) {
+  for (int t = t0; t < t1; t += P) {
+    u32x4 xv[P][J][XV];
 #pragma unroll
-    for (int ii = 0; ii < 4; ++ii) {
-      const int r = r0 + g + 4 * ii;
-      if (r < rows) {
-        double v = acc[ii];
-        if (r < E && a.router_b) v += (double)bf16_bits_to_f32(a.router_b[r]);
-        a.lg64[(size_t)t * (E + 1) + r] = v;
+    for (int p = 0; p < P; ++p) {
+      const uint16_t *xr = a.xr + (size_t)min(t + p, T - 1) * H;
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const int vc = min(lane + 64 * j, V - 1);
+#pragma unroll
+        for (int u = 0; u < XV; ++u) xv[p][j][u] = *(const u32x4 *)(xr + NC * vc + 8 * u);
       }
     }
+    double acc[R][P];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int p = 0; p < P; ++p) acc[r][p] = 0.0;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int k = 0; k < NC; ++k) {
+        double x[P];
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+          x[p] = (double)bf16_bits_to_f32((xv[p][j][k >> 3][(k & 7) >> 1] >> (16 * (k & 1))) & 0xFFFFu);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const double w = fma((double)mlx_code<BITS>(q[r][j], k), sc[r][j], bi[r][j]);
+#pragma unroll
+          for (int p = 0; p < P; ++p) acc[r][p] = fma(w, x[p], acc[r][p]);
+        }
+      }
+    // all R·P sums at once; lane l ends with the total of acc index l >> (6 − log2(R·P))
+    constexpr int N = R * P, SH = N == 4 ? 4 : N == 8 ? 3 : 2;
+    double flat[N];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int p = 0; p < P; ++p) flat[r * P + p] = acc[r][p];
+    double v = wave_sum_scatter_f64<N>(flat);
+    const int i = lane >> SH, row = r0 + i / P, tp = t + i % P;
+    if (row < E && a.router_b) v += (double)bf16_bits_to_f32(a.router_b[row]);
+    if ((lane & ((1 << SH) - 1)) == 0 && row < rows && tp < t1) a.lg64[(size_t)tp * (E + 1) + row] = v;
   }
+}
+
+// The launch of mlx_router_logits_kernel for a row of H columns (J = vectors per lane).
+template <int BITS, int R>
+void *mlx_logits_fn(int H) {
+  const int J = (H / (128 / BITS) + 63) / 64;
+  if (J <= 1) return (void *)mlx_router_logits_kernel<BITS, R, 1>;
+  if (J <= 2) return (void *)mlx_router_logits_kernel<BITS, R, 2>;
+  if (J <= 4) return (void *)mlx_router_logits_kernel<BITS, R, 4>;
+  return nullptr;
 }
 
 // Top-k and weights of every token from lg64, one wave per token (batches with an MLX router).
@@ -910,14 +957,21 @@ __global__ __launch_bounds__(256) void select_lg64_kernel(RouteArgs a) {
 // decode gate-up kernel selects), dispatch (layers above 16 tokens).
 hipError_t launch_route_mlx(const RouteArgs &a, hipStream_t s, Timing tm) {
   const int rows = a.experts + (a.shared_gate ? 1 : 0);
-  const int blocks = ((a.tokens + 15) / 16) * ((rows + 15) / 16);
   const bool small = a.tokens <= RT_TOK;
+  const int R = small ? 1 : MLX_RT_R;
+  const int blocks = (small ? 1 : (a.tokens + MLX_RT_TILE - 1) / MLX_RT_TILE) * (((rows + R - 1) / R + 3) / 4);
   const bool sel = !small || a.want_dispatch == 0;
   const bool disp = !small && a.want_dispatch != 0;
   const bool quant = a.xq != nullptr;
-  hipExtLaunchKernelGGL(a.router_bits == 8 ? mlx_router_logits_kernel<8> : mlx_router_logits_kernel<4>,
-                        dim3(blocks), dim3(64), 0, s, tm.start,
-                        (sel || quant) ? nullptr : tm.stop, 0, a);
+  void *kern = a.router_bits == 8 ? (small ? mlx_logits_fn<8, 1>(a.hidden) : mlx_logits_fn<8, MLX_RT_R>(a.hidden))
+                                  : (small ? mlx_logits_fn<4, 1>(a.hidden) : mlx_logits_fn<4, MLX_RT_R>(a.hidden));
+  if (!kern) return hipErrorInvalidValue;
+  {
+    void *args[] = {(void *)&a};
+    hipError_t le = hipExtLaunchKernel(kern, dim3(blocks), dim3(256), args, 0, s, tm.start,
+                                       (sel || quant) ? nullptr : tm.stop, 0);
+    if (le != hipSuccess) return le;
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (quant) {

@@ -104,8 +104,10 @@ def block_norms_c(norms: dict) -> BlockNormsC:
 
 class Runner:
     """hh_runner: the MoE halves (FFN blocks) of a layer stack on one context. `hook(layer)`
-    (optional) runs before each layer's block and may only enqueue work on the context's
-    stream (the token mixer)."""
+    (optional) runs before each layer's block, on the host, with torch's current stream set to
+    the stream hh_runner hands it (the context's): torch work it enqueues is ordered with the
+    MoE kernels and is recorded by `capture`. An exception raised by the hook stops the stack
+    (hh_runner returns HH_EINVAL) and is re-raised by `forward` / `capture`."""
 
     def __init__(self, ctx: Context, layers: list):
         """layers: [(MoELayer, norms dict, dense_out tensor or None)]."""
@@ -114,6 +116,7 @@ class Runner:
         check(lib().hh_runner_create(ctx.handle, len(layers), C.byref(h)))
         self.handle = h
         self._keep = []
+        self._error = None
         for i, (ml, norms, dense) in enumerate(layers):
             nc = block_norms_c(norms)
             self._keep.append((ml, norms, dense, nc))
@@ -124,25 +127,36 @@ class Runner:
         check(lib().hh_runner_reserve(self.handle, max_tokens))
 
     def _hook(self, hook):
+        self._error = None
         if hook is None:
             return LAYER_HOOK()
+        dev = f"cuda:{self.ctx.device}"
+
         def fn(user, layer, stream):
             try:
-                hook(layer)
+                with torch.cuda.stream(torch.cuda.ExternalStream(stream, device=dev)):
+                    hook(layer)
                 return 0
-            except Exception:
+            except BaseException as e:   # kept for the caller; the C side sees a failure
+                self._error = e
                 return -1
         return LAYER_HOOK(fn)
 
+    def _check(self, rc):
+        if rc != 0 and self._error is not None:
+            err, self._error = self._error, None
+            raise err
+        check(rc)
+
     def forward(self, hidden: torch.Tensor, hook=None):
         cb = self._hook(hook)
-        check(lib().hh_runner_forward(self.handle, _ptr(hidden), hidden.shape[0], cb, None))
+        self._check(lib().hh_runner_forward(self.handle, _ptr(hidden), hidden.shape[0], cb, None))
 
     def capture(self, hidden: torch.Tensor, hook=None) -> "Graph":
         cb = self._hook(hook)
         g = C.c_void_p()
-        check(lib().hh_runner_capture(self.handle, _ptr(hidden), hidden.shape[0], cb, None,
-                                      C.byref(g)))
+        self._check(lib().hh_runner_capture(self.handle, _ptr(hidden), hidden.shape[0], cb, None,
+                                            C.byref(g)))
         return Graph(g, self.ctx)
 
     def close(self):

@@ -224,9 +224,8 @@ int hh_moe_block_forward(hh_ctx *ctx, const hh_moe_desc *desc, const hh_moe_weig
                          int32_t tokens, int32_t *topk_idx, float *topk_w);
 
 /* Allocation-free variant of hh_moe_forward, for callers that cannot allocate device memory
- * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
- * counterpart in the reference, whose decode path relies on scratch preallocated at start-up
- * (LayerRunner.swift:6-10); this entry needs no reservation at all. Same arguments, results
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It has
+ * no counterpart in the reference; this entry needs no reservation at all. Same arguments, results
  * bit for bit equal to hh_moe_forward's. Its scratch is a fixed array of
  * HH_NOALLOC_SCRATCH_BYTES in each device's memory, held from library load until the process
  * ends, instead of the context's arena; the call makes no hipMalloc/hipFree, never takes the
@@ -350,6 +349,8 @@ int hh_permute(hh_ctx *ctx, const int32_t *topk_idx, int32_t tokens, int32_t top
  *   BF16 : weights = bf16 [rows][cols]
  *   MLX4/MLX8: weights = words [rows][cols·bits/32] (low-order value first), scales and biases
  *          bf16 [rows][cols/group_size] (MLXAffineLayout.swift:22-66), group_size 64           */
+/* A weight matrix for the operator-level projections. Every pointer (weights, scales, biases,
+ * bias) must be 16-byte aligned (HH_EALIGN otherwise), as the tensors of a blob are.          */
 typedef struct hh_matrix {
     int32_t quant;            /* hh_quant                                                       */
     int32_t rows, cols;

@@ -148,3 +148,36 @@ def test_combine_bit_exact():
                 assert np.array_equal(y.cpu().numpy().view(np.uint32), ex.view(np.uint32)), (T, K, H)
     finally:
         ctx.close()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("field", ["scales", "biases", "bias"])
+def test_projection_refuses_unaligned_tensors(field):
+    """Scales, MLX biases and the MXFP4 row bias read from an offset view (2 bytes past a
+    16-byte boundary) are refused with HH_EALIGN before anything is enqueued; the aligned
+    matrix then runs."""
+    import torch
+    from hydra_amd._lib import lib
+    from hydra_amd.layer import Context
+    print(f"[gpu] projection alignment {field}", flush=True)
+    q = F.QUANT_MLX4 if field == "biases" else F.QUANT_MXFP4
+    ctx = Context(0)
+    try:
+        m = make_matrix(q, 64, 256, seed=34, bias=True)
+        mc, keep = _mat_c(torch, m)
+        n = keep[field].numel() * keep[field].element_size()
+        raw = torch.zeros(n + 16, dtype=torch.uint8, device="cuda:0")
+        raw[2:2 + n].copy_(keep[field].view(torch.uint8).reshape(-1))
+        setattr(mc, field, C.c_void_p(raw.data_ptr() + 2))
+        x = torch.zeros((1, 256), dtype=torch.float32, device="cuda:0")
+        y = torch.zeros((1, 64), dtype=torch.float32, device="cuda:0")
+        torch.cuda.synchronize()
+        rc = lib().hh_expert_gemm(ctx.handle, C.byref(mc), C.c_void_p(x.data_ptr()), 1,
+                                  C.c_void_p(y.data_ptr()))
+        assert rc == -2, rc      # HH_EALIGN
+        setattr(mc, field, C.c_void_p(keep[field].data_ptr()))
+        assert lib().hh_expert_gemm(ctx.handle, C.byref(mc), C.c_void_p(x.data_ptr()), 1,
+                                    C.c_void_p(y.data_ptr())) == 0
+        ctx.synchronize()
+    finally:
+        ctx.close()

@@ -203,3 +203,49 @@ def test_runner_stack_against_chained_oracle(T):
         runner.close()
     finally:
         ctx.close()
+
+
+def test_runner_hook_torch_work_and_errors():
+    """A hook's torch work runs on the stream hh_runner hands it (ordered with the blocks: a
+    copy of the residual stream taken by the hook of layer l equals the residual after layer
+    l − 1 run one by one), and an exception raised by a hook comes back out of forward()."""
+    import torch
+    from hydra_amd.layer import Context, MoELayer, Runner, to_device
+    print("[gpu] runner torch hook", flush=True)
+    dev = "cuda:0"
+    T = 8
+    ctx = Context(0)
+    try:
+        rng = np.random.default_rng(93)
+        layers = []
+        for i, (d, rb) in enumerate(DESCS[:2]):
+            ml = MoELayer(synth.make_layer(d, seed=94 + i, router_bits=rb), ctx)
+            norms = {k: (v if k == "eps" else to_device(v, dev)) for k, v in _norms(rng, False).items()}
+            layers.append((ml, norms, None))
+        x0 = (rng.standard_normal((T, H)) * 2).astype(np.float32)
+        hid = torch.from_numpy(x0.copy()).to(dev)
+        torch.cuda.synchronize()
+        after = []
+        for ml, norms, _ in layers:
+            ml.block_forward_into(norms, hid)
+            ctx.synchronize()
+            after.append(hid.cpu().numpy().copy())
+        runner = Runner(ctx, layers)
+        hid2 = torch.from_numpy(x0.copy()).to(dev)
+        snaps = [torch.empty_like(hid2) for _ in layers]
+        torch.cuda.synchronize()
+        runner.forward(hid2, hook=lambda l: snaps[l].copy_(hid2 * 1.0))
+        ctx.synchronize()
+        assert np.array_equal(snaps[0].cpu().numpy(), x0)
+        assert np.array_equal(snaps[1].cpu().numpy().view(np.uint32), after[0].view(np.uint32))
+        assert np.array_equal(hid2.cpu().numpy().view(np.uint32), after[1].view(np.uint32))
+
+        def bad(l):
+            if l == 1:
+                raise ValueError("hook failed on purpose")
+        with pytest.raises(ValueError, match="on purpose"):
+            runner.forward(hid2, hook=bad)
+        ctx.synchronize()
+        runner.close()
+    finally:
+        ctx.close()
