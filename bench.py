@@ -146,18 +146,23 @@ class Workload:
 
 
 def measure_decode(wl, T, steps, warmup, fused=False):
-    """Decode at T tokens: three launches (router logits; gate-up, selecting the top-k itself;
-    down with the rank-ordered combine), or with `fused` the one-launch kernel
-    (hh_ctx_decode_fused), whose profile records the whole layer as the route phase."""
+    """Decode at T tokens in the default launch structure: for MXFP4 layers two launches (the
+    router's workgroups first in the gate-up launch, which selects the top-k itself; down with
+    the rank-ordered combine), otherwise three (router logits, gate-up, down); or with `fused`
+    the one-launch kernel (hh_ctx_decode_fused 1), whose profile records the whole layer as the
+    route phase."""
     desc = wl.desc
-    wl.ctx.decode_fused(1 if fused else 0)
+    wl.ctx.decode_fused(1 if fused else -1)
     wl.prepare(T, bank=64)
     sec = wl.run(steps, warmup)
     phases = wl.profiled(min(steps, 200))
     U = wl.unique_experts()
     if T == 1:
         assert U == desc.top_k, f"T=1 must touch exactly top_k experts, got {U}"
-    up_b = U * up_bytes(desc) + T * desc.hidden * 2
+    # the gate-up launch of the two-launch MXFP4 decode also reads the router
+    router_in_up = desc.quant == F.QUANT_MXFP4 and wl.router_bytes == desc.experts * desc.hidden * 2 \
+        and desc.router != F.ROUTER_GEMMA and desc.experts <= 128 and desc.hidden <= 4096
+    up_b = U * up_bytes(desc) + T * desc.hidden * 2 + (wl.router_bytes if router_in_up else 0)
     layer_b = U * F.streamed_expert_bytes(desc) + wl.router_bytes
     wl.ctx.decode_fused(-1)
     if fused:
@@ -171,7 +176,7 @@ def measure_decode(wl, T, steps, warmup, fused=False):
         "down_GBps": U * (F.streamed_expert_bytes(desc) - up_bytes(desc)) / (phases[2] * 1e-3) / 1e9,
         "layer_GBps": layer_b / sec / 1e9,
         "layer_hbm_frac": layer_b / sec / 1e9 / HBM_PEAK_GBS,
-        "up_bytes_per_launch": up_b,
+        "up_bytes_per_launch": up_b, "router_in_gate_up_launch": router_in_up,
     }
 
 

@@ -18,7 +18,9 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s, Timing tm = {});
 hipError_t launch_permute(const RouteArgs &a, hipStream_t s);
 hipError_t launch_gemm(int phase, int quant, int nt, const GemmArgs &a, hipStream_t s, Timing tm);
 hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t s, Timing tm_up,
-                        Timing tm_down);
+                        Timing tm_down, const FuseArgs *fr = nullptr);
+bool fused_router_fits(int quant, int H, int E, int router, int T);
+int fused_router_flags(int T, int E);
 int gemm_rows_per_block(int quant, int phase);
 size_t decode_fused_lds(const GemmArgs &a, int T);
 bool decode_fused_fits(int H, int I, int E, int K, int shared_inter);
@@ -246,8 +248,9 @@ int ensure_arena(hh_ctx *ctx, size_t bytes) {
   return HH_OK;
 }
 
-// Flag words of the fused decode kernel, per context.
-constexpr size_t kFlagBytes = 256 * 1024;
+// Flag words of the fused decode kernels (the one-launch kernel's flags, the two-launch
+// decode's logit records), per context.
+constexpr size_t kFlagBytes = 1024 * 1024;
 
 int ensure_flags(hh_ctx *ctx) {
   if (ctx->flags) return HH_OK;
@@ -261,14 +264,20 @@ int ensure_flags(hh_ctx *ctx) {
   return HH_OK;
 }
 
-// Whether a decode call takes the fused kernel: HH_DECODE_FUSED=1 in the environment turns it
-// on (it is not yet faster than the three-launch decode).
-bool use_fused(const hh_ctx *ctx, const hh_moe_desc &d, int T) {
-  static const bool env_on = [] {
+// The decode launch structure of a context: hh_ctx_decode_fused's value, or for -1 the
+// environment's HH_DECODE_FUSED (0, 1 or 2), else 2.
+int decode_mode(const hh_ctx *ctx) {
+  static const int env_mode = [] {
     const char *v = std::getenv("HH_DECODE_FUSED");
-    return v && v[0] == '1';
+    return (v && v[0] >= '0' && v[0] <= '2' && v[1] == 0) ? v[0] - '0' : 2;
   }();
-  const bool enabled = ctx->decode_fused < 0 ? env_on : ctx->decode_fused != 0;
+  return ctx->decode_fused < 0 ? env_mode : ctx->decode_fused;
+}
+
+// Whether a decode call takes the one-launch kernel (mode 1; it is not faster than the
+// two-launch decode).
+bool use_fused(const hh_ctx *ctx, const hh_moe_desc &d, int T) {
+  const bool enabled = decode_mode(ctx) == 1;
   // Under capture the fused kernel's per-call flag epoch would be frozen into the graph.
   return enabled && !ctx->capturing && d.quant == HH_QUANT_MXFP4 && T <= kSmallT &&
          hh::decode_fused_fits(d.hidden, d.intermediate, d.experts, d.top_k, d.shared_intermediate) &&
@@ -525,7 +534,21 @@ int forward_layer(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w, co
     ctx->dispatches += 1;
     return HH_OK;
   }
-  HH_HIP(hh::launch_route(r, ctx->stream, tm));
+  // MXFP4 decode in two launches: the router runs as the first workgroups of the gate-up
+  // launch (flags in the context's flag buffer; not under capture, whose graph would freeze the
+  // call's flag epoch, and not for the allocation-free entry, which owns no flag buffer).
+  const bool fr = T <= kSmallT && !noalloc && !resid && !ctx->capturing && w->router_bits == 0 &&
+                  decode_mode(ctx) == 2 && hh::fused_router_fits(d->quant, d->hidden, d->experts, d->router, T) &&
+                  sizeof(uint32_t) * (size_t)hh::fused_router_flags(T, d->experts) <= kFlagBytes;
+  if (fr) {
+    if ((rc = ensure_flags(ctx))) return rc;
+    if (tm.start) {   // the routing phase is inside the gate-up launch: an empty profiled phase
+      HH_HIP(hipEventRecord(tm.start, ctx->stream));
+      HH_HIP(hipEventRecord(tm.stop, ctx->stream));
+    }
+  } else {
+    HH_HIP(hh::launch_route(r, ctx->stream, tm));
+  }
 
   if (T <= kSmallT) {
     // Decode: exact logits → gate-up (selects the top-k itself) → down with the rank-ordered
@@ -534,12 +557,19 @@ int forward_layer(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w, co
     if ((rc = phase_timing(ctx, &tm, noalloc))) return rc;
     if ((rc = phase_timing(ctx, &tm_down, noalloc))) return rc;
     if ((rc = phase_timing(ctx, &tm_comb, noalloc))) return rc;
-    HH_HIP(hh::launch_small(d->quant, g, r, ctx->stream, tm, tm_down));
+    hh::FuseArgs f{};
+    if (fr) {
+      f.flags = ctx->flags;
+      f.status = (uint32_t *)(base + s.status);
+      if (++ctx->epoch == 0) ++ctx->epoch;   // flags start at 0
+      f.epoch = ctx->epoch;
+    }
+    HH_HIP(hh::launch_small(d->quant, g, r, ctx->stream, tm, tm_down, fr ? &f : nullptr));
     if (tm_comb.start) {   // no combine launch: an empty profiled phase keeps the record aligned
       HH_HIP(hipEventRecord(tm_comb.start, ctx->stream));
       HH_HIP(hipEventRecord(tm_comb.stop, ctx->stream));
     }
-    ctx->dispatches += 3;
+    ctx->dispatches += fr ? 2 : 3;
     return HH_OK;
   }
   int rows = hh::gemm_rows_per_block(d->quant, 0);
@@ -647,7 +677,7 @@ int hh_ctx_profile_read(hh_ctx *ctx, double *phase_ms, int64_t *calls) {
 
 int hh_ctx_decode_fused(hh_ctx *ctx, int32_t enable) {
   if (!ctx) return fail(HH_EINVAL, "ctx is NULL");
-  if (enable < -1 || enable > 1) return fail(HH_EINVAL, "enable must be -1, 0 or 1");
+  if (enable < -1 || enable > 2) return fail(HH_EINVAL, "enable must be -1, 0, 1 or 2");
   ctx->decode_fused = enable;
   return HH_OK;
 }

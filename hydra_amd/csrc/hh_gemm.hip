@@ -792,6 +792,10 @@ constexpr int MX_PF = HH_MX_PF;   // chunks a single-round MXFP4 decode wave iss
 // more made the T ≥ 2 kernels and the down kernel slower).
 constexpr int MX_PF_T1 = 10;
 constexpr int kFusedMaxE = 128;   // experts of layers that take the fused decode kernel
+// Batches that take the two-launch decode (the router inside the gate-up launch). Larger batches
+// measured slower: each gate-up workgroup quantises every token's x itself (T = 8: ≈ 6 µs of
+// dependent rounds), and the LDS copy of the logits halves the workgroups per compute unit.
+constexpr int kFusedRouterT = 2;
 constexpr int LDS_PAD = 8;        // bf16 elements of padding per staged row (bank spread)
 
 // Persistent: work items (row tile rt of 16·TPW intermediates, u) with u < nu the batch's
@@ -805,8 +809,8 @@ constexpr int LDS_PAD = 8;        // bf16 elements of padding per staged row (ba
 // NCW > 0: every wave's stream is exactly NCW chunks (K of 2·NCW chunks, checked on the host), all
 // issued before the staging barrier and waited for one by one (DA == NCW).
 template <int FMT, int DA, int TPW, int XB, bool SBS = false, int NCW = 0>
-__global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra) {
-  warm_kernargs<sizeof(GemmArgs) + sizeof(RouteArgs)>();
+__global__ __launch_bounds__(256 * TPW) void up_small(GemmArgs a, RouteArgs ra, FuseArgs) {
+  warm_kernargs<sizeof(GemmArgs) + sizeof(RouteArgs) + sizeof(FuseArgs)>();
   constexpr int NTH = 256 * TPW, NWV = 4 * TPW, ROWS = 16 * TPW;
   constexpr int NM = 1;
   extern __shared__ __align__(16) uint16_t s_x[];   // [ntok][H + LDS_PAD]
@@ -1167,6 +1171,136 @@ __device__ __forceinline__ MxStage<NTERM, NB, RowOf, DEV> mx_stage(uint8_t *dst,
   return MxStage<NTERM, NB, RowOf, DEV>(dst, q, sc, ld, cols, nrows, row_of, id, threads);
 }
 
+// Flags between workgroups of one launch (the fused decode kernels): a flag word holds the epoch
+// of the call that last set it; epochs never repeat for a buffer, so no flag is ever cleared.
+__device__ __forceinline__ bool flags_ready(const uint32_t *flags, int n, uint32_t epoch) {
+  bool ok = true;
+  for (int i = threadIdx.x & 63; i < n; i += 64)
+    ok = ok && __hip_atomic_load(flags + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch;
+  return __ballot(!ok) == 0ull;
+}
+// Whole wave: true once flags[0..n) all hold `epoch`, false past the deadline (wall clock).
+__device__ __forceinline__ bool wave_wait(const uint32_t *flags, int n, uint32_t epoch, uint64_t deadline) {
+  for (;;) {
+    if (flags_ready(flags, n, epoch)) {
+      // Acquire: the data reads that follow are ordered after the flag reads.
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      return true;
+    }
+    if (wall_clock64() > deadline) return false;
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+// Whole workgroup: wave 0 waits, the others learn the outcome through LDS.
+__device__ __forceinline__ bool group_wait(const uint32_t *flags, int n, uint32_t epoch, uint64_t deadline,
+                                           int *s_flag) {
+  if (threadIdx.x < 64) {
+    const bool ok = wave_wait(flags, n, epoch, deadline);
+    if (threadIdx.x == 0) *s_flag = ok ? 1 : 0;
+  }
+  __syncthreads();
+  return *s_flag != 0;
+}
+__device__ __forceinline__ void store_flag(uint32_t *flag, uint32_t epoch) {
+  // Release: the writer's data stores are ordered before the flag store.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __hip_atomic_store(flag, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// A flag after data written only with device-scope stores (write-through to the agent's
+// coherence point; this wave's stores completed, wait_stores): no L2 write-back is needed, the
+// reader's device-scope loads see the data once they see the flag.
+__device__ __forceinline__ void store_flag_dev(uint32_t *flag, uint32_t epoch) {
+  __hip_atomic_store(flag, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Whole wave, readers of device-scope data only: true once flags[0..n) all hold `epoch`, false
+// past the deadline; no L2 invalidation (the data loads that follow are device-scope loads
+// issued after the flag loads returned).
+__device__ __forceinline__ bool wave_wait_dev(const uint32_t *flags, int n, uint32_t epoch, uint64_t deadline) {
+  for (;;) {
+    if (flags_ready(flags, n, epoch)) return true;
+    if (wall_clock64() > deadline) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+// Logit records of the fused router: 16 bytes {value lo, value hi, epoch, check} with check =
+// lo ^ hi ^ epoch ^ kRecSalt, written by one device-scope 16-byte store into each of the 8
+// replicas (one per XCD, so the pollers of one XCD share a copy). A reader accepts a record
+// whose epoch is the call's and whose check matches: a record whose dwords came from two
+// different stores fails the check (the value bits differ between calls).
+constexpr uint32_t kRecSalt = 0x9E3779B9u;
+constexpr int kRecReplicas = 8;
+__device__ __forceinline__ void store_logit_record(uint32_t *recs, int R, int i, double v, uint32_t epoch, int lane) {
+  const uint64_t b = (uint64_t)__double_as_longlong(v);
+  const uint32_t lo = (uint32_t)b, hi = (uint32_t)(b >> 32);
+  if (lane < kRecReplicas) {
+    const u32x4 rec = {lo, hi, epoch, lo ^ hi ^ epoch ^ kRecSalt};
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)recs, (short)0, 0x7FFFFFF0, 0x00020000);
+    __builtin_amdgcn_raw_buffer_store_b128(rec, rs, 16 * (lane * R + i), 0, kDevScope);
+  }
+}
+// Whole wave: the n logits of replica `rep` into dst[0..n) once every record holds `epoch`
+// (device-scope loads, one round trip per poll); false past the deadline.
+__device__ __forceinline__ bool wait_logit_records(const uint32_t *recs, int R, int rep, int n, uint32_t epoch,
+                                                   uint64_t deadline, double *dst) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t *base = recs + 4 * (size_t)rep * R;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7FFFFFF0, 0x00020000);
+  for (int i0 = 0; i0 < n; i0 += 64) {
+    const int i = i0 + lane;
+    for (;;) {
+      bool ok = true;
+      if (i < n) {
+        const u32x4 r = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * i, 0, kDevScope));
+        ok = r[2] == epoch && r[3] == (r[0] ^ r[1] ^ epoch ^ kRecSalt);
+        if (ok) dst[i] = __longlong_as_double((long long)(((uint64_t)r[1] << 32) | r[0]));
+      }
+      if (__ballot(!ok) == 0ull) break;
+      if (wall_clock64() > deadline) return false;
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  return true;
+}
+// Before a flag store: this wave's device-scope data stores have completed.
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// x of every token as NTX fp8 terms into LDS rows (t, j) of RS bytes, the layout MxStage gives:
+// term bytes at their columns, block scales after `xld`, the last chunk's columns past H zero
+// and their scales 2^0. Lane (g, l16) of a wave takes block 16·k + l16, columns 8g .. 8g+7
+// (quant_block).
+__device__ __forceinline__ void quant_x_lds(const uint16_t *x, int T, int H, int xld, uint8_t *s_xb, int RS) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, l16 = lane & 15;
+  const int nb = H / 32, per_t = (nb + 15) / 16;
+  for (int w = wave; w < T * per_t; w += 4) {
+    const int t = w / per_t, b = 16 * (w - t * per_t) + l16, bc = min(b, nb - 1);
+    const u32x4 xv = *(const u32x4 *)(x + (size_t)t * H + bc * 32 + 8 * g);
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      v[2 * k] = bf_lo(xv[k]);
+      v[2 * k + 1] = bf_hi(xv[k]);
+    }
+    uint32_t q[NTX][2], sb[NTX];
+    quant_block<NTX>(v, q, sb);
+    if (b < nb) {
+#pragma unroll
+      for (int j = 0; j < NTX; ++j) {
+        uint8_t *row = s_xb + (size_t)(t * NTX + j) * RS;
+        *(u32x2 *)(row + b * 32 + 8 * g) = u32x2{q[j][0], q[j][1]};
+        if (g == 0) row[xld + b] = (uint8_t)sb[j];
+      }
+    }
+  }
+  const int hp = (H + 127) & ~127, nz = (hp - H) / 16, ns = (hp - H) / 32;
+  for (int v = tid; v < T * NTX * (nz + ns); v += 256) {
+    const int rr = v / (nz + ns), k = v - rr * (nz + ns);
+    uint8_t *row = s_xb + (size_t)rr * RS;
+    if (k < nz) *(u32x4 *)(row + H + 16 * k) = u32x4{0u, 0u, 0u, 0u};
+    else row[xld + H / 32 + (k - nz)] = 127;
+  }
+}
+
+
 // Decode gate-up on the scaled MFMA, persistent: the grid holds about two workgroups per compute
 // unit; each selects the top-k of the batch once, lists the batch's distinct experts in LDS (in
 // order of first appearance in the (token, rank) table, the shared expert last) and stages every
@@ -1177,9 +1311,16 @@ __device__ __forceinline__ MxStage<NTERM, NB, RowOf, DEV> mx_stage(uint8_t *dst,
 // 0 writes them as NTH fp8 terms. Each item issues its whole weight stream at once; co-resident
 // workgroups hide one another's latency.
 // NCH > 0 (ONE only): every row of the layer has exactly NCH chunks (checked on the host).
-template <int DA, bool ONE, int XB, int NCH = 0>
-__global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) {
-  warm_kernargs<sizeof(GemmArgs) + sizeof(RouteArgs)>();
+// FR (fused router): the grid's first f.R workgroups are the router, one per (token, row) pair
+// (split_pair_logit, the router kernel's arithmetic), each storing its logit with a device-scope
+// store and then its flag; the other workgroups quantise x into LDS themselves (the router
+// kernel's terms, quant_block), wait for the R flags, read the logits with device-scope loads
+// and go on as above. Router workgroups wait for nothing and have the smaller indices, which
+// the dispatcher starts first, so every wait is for workgroups that run. Waits are bounded
+// (10 ms); a workgroup that times out sets bit 0 of *f.status and stops.
+template <int DA, bool ONE, int XB, int NCH = 0, bool FR = false>
+__global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra, FuseArgs f) {
+  warm_kernargs<sizeof(GemmArgs) + sizeof(RouteArgs) + sizeof(FuseArgs)>();
   constexpr int NM = 1;
   extern __shared__ __align__(16) uint8_t s_xb[];   // [T][NTX] rows of mx_row_bytes(xld), then [64][H/32] scales
   __shared__ int s_idx[SMALL_T * kMaxTopK];
@@ -1198,40 +1339,83 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
   const int g = lane >> 4, l16 = lane & 15;
   const int T = ra.tokens, E = a.experts, K = a.top_k, S = a.slots, H = a.hidden;
   const bool has_shared = S > K;
+  // The gate-up role's workgroup index and count.
+  const int bx = FR ? (int)blockIdx.x - f.R : (int)blockIdx.x;
+  const int gx = FR ? (int)gridDim.x - f.R : (int)gridDim.x;
+  [[maybe_unused]] __shared__ double s_lgall[FR ? kFusedRouterT : 1][FR ? kFusedMaxE + 1 : 1];
+  [[maybe_unused]] __shared__ int s_flag;
+  [[maybe_unused]] uint64_t deadline = 0;
+  if constexpr (FR) {
+    deadline = wall_clock64() + 1000000;   // 10 ms at 100 MHz
+    if (bx < 0) {
+      // ---- router: logit of pair blockIdx.x ----
+      HH_TR(1, 0);
+      __shared__ double s_acc[4][64];
+      __shared__ double s_px[4][2][64];
+      const int E1 = E + 1, t = (int)blockIdx.x / E1, e = (int)blockIdx.x - t * E1;
+      double v = 0.0;
+      if (e < E || has_shared) v = split_pair_logit<false>(ra, t, e, s_acc, s_px);
+      if (wave == 0) store_logit_record(f.flags, f.R, (int)blockIdx.x, v, f.epoch, lane);
+      HH_TR(1, 1);
+      return;
+    }
+  }
 
   // x terms of every token: first batch of loads now (they do not depend on the routing), stored
-  // with the first item.
+  // with the first item. FR: quantised here into the same LDS rows while the router runs.
   const int RS = mx_row_bytes(a.xld);
   HH_TR(1, 0);
   auto xs = mx_stage<NTX, XB>(s_xb, a.xq, a.xs, a.xld, a.hidden, T, [](int j) { return j; }, tid, 256);
-  xs.load_first();
+  if constexpr (FR) {
+    quant_x_lds(ra.x, T, H, a.xld, s_xb, RS);
+    HH_TR(1, 6);
+    if (wave == 0) {
+      // the records of this workgroup's XCD (workgroups are dealt to the 8 XCDs round robin)
+      const bool ok = wait_logit_records(f.flags, f.R, (int)blockIdx.x % kRecReplicas, f.R, f.epoch,
+                                         deadline, &s_lgall[0][0]);
+      if (lane == 0) s_flag = ok ? 1 : 0;
+    }
+    __syncthreads();
+    if (!s_flag) {
+      if (tid == 0) atomicOr(f.status, 1u);
+      return;
+    }
+    HH_TR(1, 7);
+  } else {
+    xs.load_first();
+  }
+  // The fp64 logits of token t: the router's output, or (FR) the workgroup's LDS copy.
+  auto logits_of = [&](int t) -> const double * {
+    if constexpr (FR) return &s_lgall[0][0] + (size_t)t * (E + 1);
+    else return ra.lg64 + (size_t)t * (E + 1);
+  };
   // Top-k of every token (wave w: tokens w, w + 4, ...; one token: the 4 waves rank it
   // together); workgroup 0 writes the routing outputs.
   if (T <= 2) {
     // One or two tokens: groups of 4 / T waves rank a token together.
     const int G = T == 1 ? 4 : 2, t = wave / G;
-    const double *lg = ra.lg64 + (size_t)t * (E + 1);
+    const double *lg = logits_of(t);
 #ifdef HH_TRACE
-    { volatile double first = lg[lane % E]; (void)first; HH_TR(1, 6); }
+    if (!FR) { volatile double first = lg[lane % E]; (void)first; HH_TR(1, 6); }
 #endif
     TopK tk = T == 1 ? (E <= 64 ? topk_rank64<4>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
                                       : topk_fast<4>(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave], s_rk))
                            : (E <= 64 ? topk_rank64<2>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
                                       : topk_fast<2, 1>(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave], s_rk));
     prob_order(tk, K, ra.router);
-    HH_TR(1, 7);
+    if (!FR) HH_TR(1, 7);
     if (wave % G == 0) {
       if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
-      if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
+      if (bx == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
     }
   } else {
     for (int t = wave; t < T; t += 4) {
-      const double *lg = ra.lg64 + (size_t)t * (E + 1);
+      const double *lg = logits_of(t);
       TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave])
                               : topk_fast(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave]);
       prob_order(tk, K, ra.router);
       if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
-      if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
+      if (bx == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
     }
   }
   __syncthreads();
@@ -1247,8 +1431,8 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
   const int nsb = H / 32;                            // scale bytes per row
   uint8_t *s_sc = s_xb + (size_t)T * NTX * RS;      // [64][nsb]
   const int nsv = scale_vectors(64, H);
-  bool x_pending = true;
-  if constexpr (XB > 2) {
+  bool x_pending = !FR;
+  if constexpr (XB > 2 && !FR) {
     // Batches of several tokens: the x terms landed during the selection; they are stored before
     // the first item's weight stream takes its registers.
     xs.store_first();
@@ -1256,7 +1440,7 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
     xs.pad();
     x_pending = false;
   }
-  for (int it = blockIdx.x; it < nitems; it += gridDim.x) {
+  for (int it = bx; it < nitems; it += gx) {
     const bool sh = it >= nu * rtr;
     const int u = sh ? nu : it / rtr;
     const int rt = sh ? it - nu * rtr : it % rtr;
@@ -1292,7 +1476,7 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
       if (tid + 256 * k < nsv) *(u32x4 *)(s_sc + 16 * (tid + 256 * k)) = scv[k];
     for (int v = tid + 512; v < nsv; v += 256) *(u32x4 *)(s_sc + 16 * v) = *(const u32x4 *)(gsc + 16 * v);
     __syncthreads();
-    if (it == (int)blockIdx.x) HH_TR(1, 2);
+    if (it == bx) HH_TR(1, 2);
 
     const uint8_t *my_sc = s_sc + (2 * (16 * q + l16) + (is_up ? 1 : 0)) * nsb;
     // The lane group as a value opaque to the compiler in each item: otherwise every chunk's
@@ -1309,12 +1493,12 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
           chunk_mx1<NTX>(acc[0][0], w[0].w, o, c, gi, H, NCH > 0 && c < NCH - 1);
         });
     const f32x4 res = acc[0][0];
-    if (nitems > (int)gridDim.x) {
+    if (nitems > gx) {
       // Workgroups with further items: the gate waves form the activations and wave 0 writes the
       // terms, while the other waves go on to the next item's weight stream.
       if (is_up) s_up[q][lane] = res;
       __syncthreads();
-      if (it == (int)blockIdx.x) HH_TR(1, 3);
+      if (it == bx) HH_TR(1, 3);
       if (!is_up && l16 < ntok) {
         const f32x4 y = up_values_mx(a, bias, res, s_up[q][lane]);
 #pragma unroll
@@ -1335,7 +1519,7 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
           store_hq(a, slot, rt, rt * UP_ROWS + 8 * g, rt * UP_ROWS + 8 * g + 4, hq, sb, g);
         }
       }
-      if (it == (int)blockIdx.x) HH_TR(1, 4);
+      if (it == bx) HH_TR(1, 4);
       continue;
     }
     // One item per workgroup: the epilogue spread over the workgroup, one (token column j,
@@ -1350,7 +1534,7 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
       if (l16 == 0) s_bias[q][g] = bias;
     }
     __syncthreads();
-    if (it == (int)blockIdx.x) HH_TR(1, 3);
+    if (it == bx) HH_TR(1, 3);
     const int nv = ntok * UP_ROWS;
     for (int i = tid; i < nv; i += 256) {
       const int j = i >> 5, k = i & 31, kq = k >> 4, kg = (k >> 2) & 3, ii = k & 3;
@@ -1371,7 +1555,7 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra) 
         if (k == 0) a.hs[((size_t)slot * NTH + tt) * (a.hld / 32) + rt] = (uint8_t)sb[tt];
       }
     }
-    if (it == (int)blockIdx.x) HH_TR(1, 4);
+    if (it == bx) HH_TR(1, 4);
     // s_hv and s_sc are rewritten by the next item only after its first barrier.
   }
   HH_TR(1, 5);
@@ -1568,78 +1752,6 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
 // any XCD, without cache maintenance. Workgroups only wait for workgroups of smaller index,
 // which the dispatcher starts first, so every wait is for one that is running or done. Waits are
 // bounded (10 ms): a workgroup that times out sets bit 0 of `status` and its outputs are NaN.
-__device__ __forceinline__ bool flags_ready(const uint32_t *flags, int n, uint32_t epoch) {
-  bool ok = true;
-  for (int i = threadIdx.x & 63; i < n; i += 64)
-    ok = ok && __hip_atomic_load(flags + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch;
-  return __ballot(!ok) == 0ull;
-}
-// Whole wave: true once flags[0..n) all hold `epoch`, false past the deadline (wall clock).
-__device__ __forceinline__ bool wave_wait(const uint32_t *flags, int n, uint32_t epoch, uint64_t deadline) {
-  for (;;) {
-    if (flags_ready(flags, n, epoch)) {
-      // Acquire: the data reads that follow are ordered after the flag reads.
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      return true;
-    }
-    if (wall_clock64() > deadline) return false;
-    __builtin_amdgcn_s_sleep(2);
-  }
-}
-// Whole workgroup: wave 0 waits, the others learn the outcome through LDS.
-__device__ __forceinline__ bool group_wait(const uint32_t *flags, int n, uint32_t epoch, uint64_t deadline,
-                                           int *s_flag) {
-  if (threadIdx.x < 64) {
-    const bool ok = wave_wait(flags, n, epoch, deadline);
-    if (threadIdx.x == 0) *s_flag = ok ? 1 : 0;
-  }
-  __syncthreads();
-  return *s_flag != 0;
-}
-__device__ __forceinline__ void store_flag(uint32_t *flag, uint32_t epoch) {
-  // Release: the writer's data stores are ordered before the flag store.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __hip_atomic_store(flag, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Before a flag store: this wave's device-scope data stores have completed.
-__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
-// x of every token as NTX fp8 terms into LDS rows (t, j) of RS bytes, the layout MxStage gives:
-// term bytes at their columns, block scales after `xld`, the last chunk's columns past H zero
-// and their scales 2^0. Lane (g, l16) of a wave takes block 16·k + l16, columns 8g .. 8g+7
-// (quant_block).
-__device__ __forceinline__ void quant_x_lds(const uint16_t *x, int T, int H, int xld, uint8_t *s_xb, int RS) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, l16 = lane & 15;
-  const int nb = H / 32, per_t = (nb + 15) / 16;
-  for (int w = wave; w < T * per_t; w += 4) {
-    const int t = w / per_t, b = 16 * (w - t * per_t) + l16, bc = min(b, nb - 1);
-    const u32x4 xv = *(const u32x4 *)(x + (size_t)t * H + bc * 32 + 8 * g);
-    float v[8];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      v[2 * k] = bf_lo(xv[k]);
-      v[2 * k + 1] = bf_hi(xv[k]);
-    }
-    uint32_t q[NTX][2], sb[NTX];
-    quant_block<NTX>(v, q, sb);
-    if (b < nb) {
-#pragma unroll
-      for (int j = 0; j < NTX; ++j) {
-        uint8_t *row = s_xb + (size_t)(t * NTX + j) * RS;
-        *(u32x2 *)(row + b * 32 + 8 * g) = u32x2{q[j][0], q[j][1]};
-        if (g == 0) row[xld + b] = (uint8_t)sb[j];
-      }
-    }
-  }
-  const int hp = (H + 127) & ~127, nz = (hp - H) / 16, ns = (hp - H) / 32;
-  for (int v = tid; v < T * NTX * (nz + ns); v += 256) {
-    const int rr = v / (nz + ns), k = v - rr * (nz + ns);
-    uint8_t *row = s_xb + (size_t)rr * RS;
-    if (k < nz) *(u32x4 *)(row + H + 16 * k) = u32x4{0u, 0u, 0u, 0u};
-    else row[xld + H / 32 + (k - nz)] = 127;
-  }
-}
-
 template <bool GEMMA>
 __global__ __launch_bounds__(256, 2) void decode_mx(GemmArgs a, RouteArgs ra, FuseArgs f) {
   constexpr int NM = 1, DA = MX_ONE_CHUNKS;
@@ -3260,7 +3372,7 @@ template <int PH, int FMT> constexpr int ring_rt() {
 
 // ---- launch table -----------------------------------------------------------------------------
 typedef void (*GemmKernel)(GemmArgs);
-typedef void (*UpSmallKernel)(GemmArgs, RouteArgs);
+typedef void (*UpSmallKernel)(GemmArgs, RouteArgs, FuseArgs);
 typedef void (*DownSmallKernel)(GemmArgs, const int32_t *);
 
 // Register ring depth of the decode weight stream, in chunks (per lane per chunk: MXFP4 16 B +
@@ -3281,8 +3393,12 @@ constexpr int MX_STATIC = 23;
 // MLX gate-up rows of exactly 2·MLX_NCW chunks (K = 2048: Qwen3.5-35B-A3B) take the single-round
 // stream of MLX_NCW chunks per wave.
 constexpr int MLX_NCW = 16;
-template <int FMT> static UpSmallKernel up_small_k(bool one, int T, bool st = false, bool stat = false) {
+template <int FMT> static UpSmallKernel up_small_k(bool one, int T, bool st = false, bool stat = false, bool fr = false) {
   if constexpr (FMT == Q_MXFP4) {
+    if (fr) {   // the fused router: single-round rows only
+      if (st) return T == 1 ? up_small_mx<MX_ONE, true, 2, MX_STATIC, true> : up_small_mx<MX_ONE, true, MX_XB_WIDE, MX_STATIC, true>;
+      return T == 1 ? up_small_mx<MX_ONE, true, 2, 0, true> : up_small_mx<MX_ONE, true, MX_XB_WIDE, 0, true>;
+    }
     if (one && st) return T == 1 ? up_small_mx<MX_ONE, true, 2, MX_STATIC> : up_small_mx<MX_ONE, true, MX_XB_WIDE, MX_STATIC>;
     if (T == 1) return one ? up_small_mx<MX_ONE, true, 2> : up_small_mx<16, false, 2>;
     return one ? up_small_mx<MX_ONE, true, MX_XB_WIDE> : up_small_mx<16, false, MX_XB_WIDE>;
@@ -3496,8 +3612,15 @@ static int resident_per_cu(const void *kernel, int threads, size_t lds) {
   return n;
 }
 
+bool fused_router_fits(int quant, int H, int E, int router, int T) {
+  return quant == Q_MXFP4 && router != R_GEMMA && H <= 4096 && (H + 127) / 128 <= MX_ONE && E <= kFusedMaxE &&
+         T >= 1 && T <= kFusedRouterT;
+}
+// Flag-buffer words of the fused router's logit records: 8 replicas × T·(E+1) records × 4.
+int fused_router_flags(int T, int E) { return 4 * kRecReplicas * T * (E + 1); }
+
 hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t s, Timing tm_up,
-                        Timing tm_down) {
+                        Timing tm_down, const FuseArgs *fr) {
   const int T = ra.tokens;
   if (T < 1 || T > SMALL_T) return hipErrorInvalidValue;
   const int S = a.slots;
@@ -3507,7 +3630,7 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
   UpSmallKernel up;
   switch (quant) {
   // The MXFP4 static-count variant needs every up row (over H) at MX_STATIC chunks.
-  case Q_MXFP4: up = up_small_k<Q_MXFP4>(one_up, T, (a.hidden + 127) / 128 == MX_STATIC); break;
+  case Q_MXFP4: up = up_small_k<Q_MXFP4>(one_up, T, (a.hidden + 127) / 128 == MX_STATIC, false, fr != nullptr); break;
   case Q_BF16: up = up_small_k<Q_BF16>(true, T); break;
   case Q_MLX4: up = up_small_k<Q_MLX4>(true, T, mlx_staged_up(a.hidden), (a.hidden + 63) / 64 == 2 * MLX_NCW); break;
   default: up = up_small_k<Q_MLX8>(true, T, mlx_staged_up(a.hidden), (a.hidden + 63) / 64 == 2 * MLX_NCW); break;
@@ -3530,7 +3653,9 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
                         (const void *)up_small_k<Q_MLX8>(true, 1, true), (const void *)up_small_k<Q_MLX8>(true, SMALL_T, true),
                         (const void *)up_small_k<Q_MLX4>(true, 1, true, true), (const void *)up_small_k<Q_MLX8>(true, 1, true, true),
                         (const void *)down_small_k<Q_MLX4>(4, true, true), (const void *)down_small_k<Q_MLX4>(9, true, true),
-                        (const void *)down_small_k<Q_MLX8>(4, true, true), (const void *)down_small_k<Q_MLX8>(9, true, true)};
+                        (const void *)down_small_k<Q_MLX8>(4, true, true), (const void *)down_small_k<Q_MLX8>(9, true, true),
+                        (const void *)up_small_k<Q_MXFP4>(true, 1, true, false, true), (const void *)up_small_k<Q_MXFP4>(true, SMALL_T, true, false, true),
+                        (const void *)up_small_k<Q_MXFP4>(true, 1, false, false, true), (const void *)up_small_k<Q_MXFP4>(true, SMALL_T, false, false, true)};
     // Best effort: HIP on gfx950 accepts launches up to the hardware LDS size without it, and
     // a runtime that rejects the attribute must not leave its error for the launch check below.
     for (const void *k : ks) {
@@ -3552,7 +3677,13 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
   // larger than that leaves workgroups waiting for earlier ones to exit.
   const int up_per_cu = std::min(mx ? 2 : 4, resident_per_cu((const void *)up, 256, lds_up));
   const int up_grid = std::min(up_per_cu * ncu, a.row_tiles * maxu);
-  hipExtLaunchKernelGGL(up, dim3(up_grid), dim3(256), lds_up, s, tm_up.start, tm_up.stop, 0, a, ra);
+  FuseArgs f{};
+  if (fr) {
+    if (!fused_router_fits(quant, a.hidden, a.experts, ra.router, T)) return hipErrorInvalidValue;
+    f = *fr;
+    f.R = T * (a.experts + 1);
+  }
+  hipExtLaunchKernelGGL(up, dim3(f.R + up_grid), dim3(256), lds_up, s, tm_up.start, tm_up.stop, 0, a, ra, f);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   return launch_down_small(quant, a, ra.topk_idx, T, s, tm_down);

@@ -232,4 +232,75 @@ __device__ __forceinline__ void exact_logits_rows(const RouteArgs &a, const uint
   for (int r = 0; r < R; ++r) out[r] = wave_sum_f64((acc[r][0] + acc[r][1]) + (acc[r][2] + acc[r][3]));
 }
 
+// Logit of (token t, row e; e == E the shared expert's gate row) with the 4 waves of a workgroup
+// (H ≤ 4096): wave u forms accumulator u of exact_logit (columns 2048i + 512u + 8l .. +7, i
+// ascending) and wave 0 adds the four in exact_logit's order, (acc0 + acc1) + (acc2 + acc3), then
+// sums the wave: the same value with a quarter of the products on each wave's dependent chain.
+// GEMMA's norm: wave u forms the partial Σx² of each (step, slice u), and every wave adds them in
+// pair_logit's order (steps ascending, slices ascending within a step) before the wave sum.
+// Every wave of the workgroup calls it (barriers); wave 0 returns the logit, the others 0.
+template <bool gemma>
+__device__ __forceinline__ double split_pair_logit(const RouteArgs &a, int t, int e, double (*s_acc)[64],
+                                                   double (*s_px)[2][64]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int E = a.experts, H = a.hidden;
+  const bool sg = e == E;                 // the shared expert's gate row: plain dot, no bias
+  const bool gm = gemma && !sg;
+  const uint16_t *xr = (sg ? a.x : a.xr) + (size_t)t * H;
+  const uint16_t *wrow = sg ? a.shared_gate : a.router_w + (size_t)e * H;
+  const int u = wave, nb = H > 2048 ? 2 : 1;
+  u32x4 xv[2], wv[2], sv[2];
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int h = 2048 * b + lane * 8 + 512 * u;
+    const int hc = min(h, H - 8);
+    xv[b] = *(const u32x4 *)(xr + hc);
+    wv[b] = *(const u32x4 *)(wrow + hc);
+    sv[b] = gm ? *(const u32x4 *)(a.router_scale + hc) : u32x4{0u, 0u, 0u, 0u};
+    if (h >= H) wv[b] = u32x4{0u, 0u, 0u, 0u};
+  }
+  double norm = 1.0, root = 1.0;
+  if (gm) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int h = 2048 * b + lane * 8 + 512 * u;
+      double px = 0.0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float xf = h < H ? bf16_bits_to_f32((xv[b][k >> 1] >> ((k & 1) * 16)) & 0xFFFF) : 0.f;
+        px += (double)(xf * xf);
+      }
+      s_px[u][b][lane] = px;
+    }
+    __syncthreads();
+    double xx = 0.0;
+    for (int b = 0; b < nb; ++b)
+#pragma unroll
+      for (int uu = 0; uu < 4; ++uu) xx += s_px[uu][b][lane];
+    xx = wave_sum_f64(xx);
+    norm = pow(xx / (double)H + (double)a.eps, -0.5);
+    root = pow((double)H, -0.5);
+  }
+  double acc = 0.0;
+  for (int b = 0; b < nb; ++b)
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int sh = (k & 1) * 16;
+      const float xf = bf16_bits_to_f32((xv[b][k >> 1] >> sh) & 0xFFFF);
+      const float wf = bf16_bits_to_f32((wv[b][k >> 1] >> sh) & 0xFFFF);
+      if (gm) {
+        const double xd = (((double)xf * norm) * (double)bf16_bits_to_f32((sv[b][k >> 1] >> sh) & 0xFFFF)) * root;
+        acc = fma(xd, (double)wf, acc);
+      } else {
+        acc += (double)(xf * wf);
+      }
+    }
+  s_acc[u][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return 0.0;
+  double v = wave_sum_f64((s_acc[0][lane] + s_acc[1][lane]) + (s_acc[2][lane] + s_acc[3][lane]));
+  if (!sg && a.router_b) v += (double)bf16_bits_to_f32(a.router_b[e]);
+  return v;
+}
+
 }  // namespace hh

@@ -48,7 +48,8 @@ class Context:
         check(lib().hh_ctx_reserve(self.handle, C.byref(d), max_tokens))
 
     def decode_fused(self, enable: int):
-        """1: MXFP4 decode calls in one fused launch, 0: three launches, -1: the default."""
+        """MXFP4 decode launches: 2 two (router inside the gate-up launch), 1 one fused launch,
+        0 three, -1 the default (HH_DECODE_FUSED in the environment, else 2)."""
         check(lib().hh_ctx_decode_fused(self.handle, int(enable)))
 
     def profile(self, enable: bool = True):

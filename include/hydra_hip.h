@@ -149,11 +149,14 @@ const char *hh_last_error(void);
  * and the number of profiled forward calls, and clears the record.                           */
 int hh_ctx_profile(hh_ctx *ctx, int32_t enable);
 int hh_ctx_profile_read(hh_ctx *ctx, double *phase_ms /* [4] */, int64_t *calls);
-/* Decode calls (at most 16 tokens) of MXFP4 layers without a shared expert, top_k <= 4 and
- * E <= 128 in one launch (router, gate-up and down roles) instead of three, with the same
- * results bit for bit; the profile then records the whole layer as phase 0. No counterpart in
- * the reference: a scheduling choice of this implementation. enable: 1 on, 0 off, -1 the
- * default (the environment variable HH_DECODE_FUSED=1 turns it on).                          */
+/* The launch structure of MXFP4 decode calls (at most 16 tokens), with the same results bit
+ * for bit in every mode. 0: three launches (router, gate-up, down). 2: two launches, the router
+ * as the first workgroups of the gate-up launch (bf16 non-GEMMA routers, H <= 4096, E <= 128;
+ * other layers, calls under capture and the allocation-free entry take three); the profile then
+ * records the routing phase as empty. 1: one launch (router, gate-up and down roles; no shared
+ * expert, top_k <= 4, E <= 128), whose profile records the whole layer as phase 0. -1: the
+ * default, the environment variable HH_DECODE_FUSED (0, 1 or 2) or else 2. No counterpart in
+ * the reference: a scheduling choice of this implementation.                               */
 int hh_ctx_decode_fused(hh_ctx *ctx, int32_t enable);
 
 /* ---- description helpers ------------------------------------------------------------------ */

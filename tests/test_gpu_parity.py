@@ -344,10 +344,12 @@ FUSED_CASES = {
 
 @pytest.mark.parametrize("name", list(FUSED_CASES))
 def test_fused_decode_equals_three_launch_decode(torch_dev, ctx, name):
-    """The one-launch decode (hh_ctx_decode_fused) against the three-launch decode, bit for bit
-    (outputs, top-k indices and weights), over a sequence of batch sizes. The two paths
+    """The two-launch decode (router workgroups inside the gate-up launch, hh_ctx_decode_fused
+    2, the default) and the one-launch decode (1) against the three-launch decode (0), bit for
+    bit (outputs, top-k indices and weights), over a sequence of batch sizes. The paths
     alternate on one context with new tokens at every step, so a fused call that read data left
-    in the scratch by an earlier call (another batch size, other tokens) would show."""
+    in the scratch or the flags by an earlier call (another batch size, other tokens) would
+    show."""
     from hydra_amd.layer import MoELayer
     desc, Ts = FUSED_CASES[name]
     say(f"fused decode {name}")
@@ -357,12 +359,13 @@ def test_fused_decode_equals_three_launch_decode(torch_dev, ctx, name):
             x = synth.make_tokens(desc.hidden, T, seed=60 + i)
             ctx.decode_fused(0)
             ya, ia, wa = (v.cpu().numpy() for v in L.forward(x))
-            ctx.decode_fused(1)
-            yb, ib, wb = (v.cpu().numpy() for v in L.forward(x))
-            assert np.array_equal(ia, ib), (name, T)
-            assert np.array_equal(wa.view(np.uint32), wb.view(np.uint32)), (name, T)
-            assert not np.isnan(yb).any(), (name, T)
-            assert np.array_equal(ya.view(np.uint32), yb.view(np.uint32)), (name, T)
+            for mode in (2, 1, -1):
+                ctx.decode_fused(mode)
+                yb, ib, wb = (v.cpu().numpy() for v in L.forward(x))
+                assert np.array_equal(ia, ib), (name, T, mode)
+                assert np.array_equal(wa.view(np.uint32), wb.view(np.uint32)), (name, T, mode)
+                assert not np.isnan(yb).any(), (name, T, mode)
+                assert np.array_equal(ya.view(np.uint32), yb.view(np.uint32)), (name, T, mode)
     finally:
         ctx.decode_fused(-1)
 
