@@ -61,6 +61,7 @@ struct hh_ctx {
   // flag values; `epoch` is the value of the last call.
   uint32_t *flags = nullptr;
   uint32_t epoch = 0;
+  uint32_t fused_calls = 0;    // one-launch decode calls so far (the counter region parity)
   int decode_fused = -1;   // 1 on, 0 off, -1 the environment's choice
   int device = 0;
   hipStream_t stream = nullptr;
@@ -281,7 +282,7 @@ bool use_fused(const hh_ctx *ctx, const hh_moe_desc &d, int T) {
   // Under capture the fused kernel's per-call flag epoch would be frozen into the graph.
   return enabled && !ctx->capturing && d.quant == HH_QUANT_MXFP4 && T <= kSmallT &&
          hh::decode_fused_fits(d.hidden, d.intermediate, d.experts, d.top_k, d.shared_intermediate) &&
-         sizeof(uint32_t) * (size_t)hh::decode_fused_flags(kSmallT, d.experts, d.top_k, d.intermediate) <= kFlagBytes;
+         sizeof(uint32_t) * ((size_t)hh::decode_fused_flags(kSmallT, d.experts, d.top_k, d.intermediate) + 128) <= kFlagBytes;
 }
 
 int check_desc(const hh_moe_desc *d) {
@@ -522,6 +523,8 @@ int forward_layer(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w, co
     f.status = (uint32_t *)(base + s.status);
     if (++ctx->epoch == 0) ++ctx->epoch;   // flags start at 0
     f.epoch = ctx->epoch;
+    f.seq = ctx->fused_calls++;
+    f.ctr = ctx->flags + kFlagBytes / sizeof(uint32_t) - 128;   // the last 2·64 words
     HH_HIP(hh::launch_decode_fused(d->router == HH_ROUTER_GEMMA, g, r, f, ctx->stream, tm));
     for (int p = 1; p < 4; ++p) {   // the other phases are empty: keep the record aligned
       hh::Timing te;

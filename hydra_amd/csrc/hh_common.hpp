@@ -336,6 +336,8 @@ struct FuseArgs {
   uint32_t *flags;    // [R] router workgroups, then the gate-up items
   uint32_t *status;   // bit 0: a wait timed out
   uint32_t epoch;     // this call's flag value (never repeats for a buffer)
+  uint32_t seq;       // one-launch decode: the context's count of earlier one-launch calls
+  uint32_t *ctr;      // one-launch decode: the two counter regions (2·64 words)
   int32_t R, U, D;    // workgroups per role
 };
 

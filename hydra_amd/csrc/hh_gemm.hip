@@ -1171,57 +1171,9 @@ __device__ __forceinline__ MxStage<NTERM, NB, RowOf, DEV> mx_stage(uint8_t *dst,
   return MxStage<NTERM, NB, RowOf, DEV>(dst, q, sc, ld, cols, nrows, row_of, id, threads);
 }
 
-// Flags between workgroups of one launch (the fused decode kernels): a flag word holds the epoch
-// of the call that last set it; epochs never repeat for a buffer, so no flag is ever cleared.
-__device__ __forceinline__ bool flags_ready(const uint32_t *flags, int n, uint32_t epoch) {
-  bool ok = true;
-  for (int i = threadIdx.x & 63; i < n; i += 64)
-    ok = ok && __hip_atomic_load(flags + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == epoch;
-  return __ballot(!ok) == 0ull;
-}
-// Whole wave: true once flags[0..n) all hold `epoch`, false past the deadline (wall clock).
-__device__ __forceinline__ bool wave_wait(const uint32_t *flags, int n, uint32_t epoch, uint64_t deadline) {
-  for (;;) {
-    if (flags_ready(flags, n, epoch)) {
-      // Acquire: the data reads that follow are ordered after the flag reads.
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      return true;
-    }
-    if (wall_clock64() > deadline) return false;
-    __builtin_amdgcn_s_sleep(2);
-  }
-}
-// Whole workgroup: wave 0 waits, the others learn the outcome through LDS.
-__device__ __forceinline__ bool group_wait(const uint32_t *flags, int n, uint32_t epoch, uint64_t deadline,
-                                           int *s_flag) {
-  if (threadIdx.x < 64) {
-    const bool ok = wave_wait(flags, n, epoch, deadline);
-    if (threadIdx.x == 0) *s_flag = ok ? 1 : 0;
-  }
-  __syncthreads();
-  return *s_flag != 0;
-}
-__device__ __forceinline__ void store_flag(uint32_t *flag, uint32_t epoch) {
-  // Release: the writer's data stores are ordered before the flag store.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __hip_atomic_store(flag, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// A flag after data written only with device-scope stores (write-through to the agent's
-// coherence point; this wave's stores completed, wait_stores): no L2 write-back is needed, the
-// reader's device-scope loads see the data once they see the flag.
-__device__ __forceinline__ void store_flag_dev(uint32_t *flag, uint32_t epoch) {
-  __hip_atomic_store(flag, epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Whole wave, readers of device-scope data only: true once flags[0..n) all hold `epoch`, false
-// past the deadline; no L2 invalidation (the data loads that follow are device-scope loads
-// issued after the flag loads returned).
-__device__ __forceinline__ bool wave_wait_dev(const uint32_t *flags, int n, uint32_t epoch, uint64_t deadline) {
-  for (;;) {
-    if (flags_ready(flags, n, epoch)) return true;
-    if (wall_clock64() > deadline) return false;
-    __builtin_amdgcn_s_sleep(1);
-  }
-}
+// Data between workgroups of one launch (the fused decode kernels) is announced by words that
+// hold the epoch of the call that wrote them; epochs never repeat for a buffer, so no word is
+// ever cleared.
 // Logit records of the fused router: 16 bytes {value lo, value hi, epoch, check} with check =
 // lo ^ hi ^ epoch ^ kRecSalt, written by one device-scope 16-byte store into each of the 8
 // replicas (one per XCD, so the pollers of one XCD share a copy). A reader accepts a record
@@ -1736,22 +1688,39 @@ __global__ __launch_bounds__(64 * SMAX * KS) void down_small(GemmArgs a, const i
 
 // ---- decode, fused: one launch per MXFP4 layer ------------------------------------------------------
 // Workgroups take one of three roles by blockIdx, in dependency order:
-//   [0, R)        router: one wave per (token, expert) pair computes its exact fp64 logit into
-//                 the exchange buffer; then the workgroup's flag.
-//   [R, R+U)      gate-up: quantise x into LDS (every workgroup itself), wait for the router
-//                 flags, select the top-k and build the plan (as up_small_mx), then items
-//                 it = role index, + U, ...; an item's h terms go to the exchange buffer, then
-//                 the item's flag.
-//   [R+U, R+U+D)  down: select the top-k of the batch, then items (16 hidden rows, token),
-//                 wave r = slot r: issue the weight stream and scales, wait for the flags of the
-//                 gate-up items of the slot's expert, stage its h terms and compute; the rank-
-//                 ordered slot sum goes to y.
-// Data passed between workgroups (logits, h terms) is written with device-scope stores and read
-// with device-scope loads (kDevScope); a writer's stores have completed before it stores the
-// flag (flags are device-scope atomics), so a reader that has seen the flag reads the new data on
-// any XCD, without cache maintenance. Workgroups only wait for workgroups of smaller index,
-// which the dispatcher starts first, so every wait is for one that is running or done. Waits are
-// bounded (10 ms): a workgroup that times out sets bit 0 of `status` and its outputs are NaN.
+//   [0, R)        router: one workgroup per (token, row) pair (split_pair_logit) writes its logit
+//                 as a record into the 8 replicas (store_logit_record), as up_small_mx's FR role.
+//   [R, R+U)      gate-up: quantise x into LDS (every workgroup itself), wait for the records of
+//                 its XCD's replica, select the top-k and build the plan (as up_small_mx), then
+//                 items it = role index, + U, ...; an item's h terms go to the exchange buffer with
+//                 device-scope stores, then the item adds one to its expert's counter.
+//   [R+U, R+U+D)  down: the same records and selection, then items (16 hidden rows, token), wave
+//                 r = slot r: issue the weight stream and scales, wait until the counter of the
+//                 slot's expert holds all its gate-up items, stage its h terms with device-scope
+//                 loads and compute; the rank-ordered slot sum goes to y.
+// Counters sit in two regions of kFusedCtr words at f.ctr, apart from the records (whose extent
+// varies with the batch size); the context's n-th one-launch
+// call (f.seq = n) counts in region n & 1 with atomic adds, and its first gate-up workgroup
+// zeroes the other region for the next one-launch call (which starts only after this launch
+// ends). Data passed between workgroups is
+// written with device-scope stores, completed (vmcnt 0) before the record or counter that
+// announces it, and read with device-scope loads issued after the announcement was read, so a
+// reader sees it on any XCD without cache maintenance. Workgroups only wait for workgroups of
+// smaller index, which the dispatcher starts first. Waits are bounded (10 ms): a workgroup that
+// times out sets bit 0 of `status` and its outputs are NaN.
+constexpr int kFusedCtr = 64;   // counter words per region (distinct experts of a call ≤ 16·4)
+// Whole wave: true once *c holds n, false past the deadline. Polls are spaced (≈ 0.2 µs) so
+// that hundreds of waiting waves leave the memory atomics to the writers.
+__device__ __forceinline__ bool wait_count(const uint32_t *c, uint32_t n, uint64_t deadline) {
+  for (;;) {
+    uint32_t v = 0;
+    if ((threadIdx.x & 63) == 0) v = __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (__builtin_amdgcn_readfirstlane(v) == n) return true;
+    if (wall_clock64() > deadline) return false;
+    __builtin_amdgcn_s_sleep(8);
+  }
+}
+
 template <bool GEMMA>
 __global__ __launch_bounds__(256, 2) void decode_mx(GemmArgs a, RouteArgs ra, FuseArgs f) {
   constexpr int NM = 1, DA = MX_ONE_CHUNKS;
@@ -1761,7 +1730,7 @@ __global__ __launch_bounds__(256, 2) void decode_mx(GemmArgs a, RouteArgs ra, Fu
   __shared__ f32x4 s_up[2][64];
   __shared__ float s_hv[SMALL_T][UP_ROWS];
   __shared__ double s_lg[4][64];
-  __shared__ double s_row[4][kFusedMaxE + 1];
+  __shared__ double s_lgall[SMALL_T * (kFusedMaxE + 1)];
   __shared__ int s_ri[4][kMaxTopK];
   __shared__ float s_o[4][16];
   __shared__ int s_flag, s_bad;
@@ -1772,29 +1741,32 @@ __global__ __launch_bounds__(256, 2) void decode_mx(GemmArgs a, RouteArgs ra, Fu
   const int T = ra.tokens, E = a.experts, E1 = E + 1, K = a.top_k, S = a.slots, H = a.hidden;
   const int b = blockIdx.x;
   const uint64_t deadline = wall_clock64() + 1000000;   // 10 ms at 100 MHz
+  uint32_t *ctr_base = f.ctr;
+  uint32_t *ctr = ctr_base + kFusedCtr * (f.seq & 1);                   // this call's, per plan expert
 
   // ---- router ----
   if (b < f.R) {
-    const int p = b * 4 + wave;
-    if (p < T * E1) {
-      const int t = p / E1, e = p - t * E1;
-      if (e < E || ra.shared_gate) {
-        const double v = pair_logit<GEMMA>(ra, t, e);
-        if (lane == 0) __hip_atomic_store(ra.lg64 + (size_t)t * E1 + e, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
-    wait_stores();
-    __syncthreads();
-    if (tid == 0) store_flag(f.flags + b, f.epoch);
+    __shared__ double s_acc[4][64];
+    __shared__ double s_px[4][2][64];
+    const int t = b / E1, e = b - t * E1;
+    double v = 0.0;
+    if (e < E || ra.shared_gate) v = split_pair_logit<GEMMA>(ra, t, e, s_acc, s_px);
+    if (wave == 0) store_logit_record(f.flags, f.R, b, v, f.epoch, lane);
     return;
   }
 
   const bool up_role = b < f.R + f.U;
+  if (up_role) HH_TR(1, 0); else HH_TR(2, 0);
   if (tid == 0) s_bad = 0;
   // Gate-up workgroups quantise x while the router runs.
   const int RS = mx_row_bytes(a.xld);
   if (up_role) quant_x_lds(ra.x, T, H, a.xld, s_dyn, RS);
-  if (!group_wait(f.flags, f.R, f.epoch, deadline, &s_flag)) {
+  if (wave == 0) {
+    const bool ok = wait_logit_records(f.flags, f.R, b % kRecReplicas, f.R, f.epoch, deadline, s_lgall);
+    if (lane == 0) s_flag = ok ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_flag) {
     if (tid == 0) atomicOr(f.status, 1u);
     if (!up_role) {
       // Down items of this workgroup: NaN rows.
@@ -1806,11 +1778,7 @@ __global__ __launch_bounds__(256, 2) void decode_mx(GemmArgs a, RouteArgs ra, Fu
   // Top-k of every token (wave w: tokens w, w + 4, ...). The first gate-up workgroup writes the
   // routing outputs; down workgroups keep the weights.
   for (int t = wave; t < T; t += 4) {
-    // The token's logits into LDS with device-scope loads, then the selection from there.
-    double *lg = s_row[wave];
-    for (int e = lane; e < E1; e += 64)
-      lg[e] = __hip_atomic_load(ra.lg64 + (size_t)t * E1 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_wave_barrier();
+    const double *lg = s_lgall + (size_t)t * E1;
     TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave]) : topk_exact(lg, E, K);
     prob_order(tk, K, ra.router);
     if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
@@ -1827,8 +1795,11 @@ __global__ __launch_bounds__(256, 2) void decode_mx(GemmArgs a, RouteArgs ra, Fu
   const int nu = plan.nu;
   const int rtr = a.grp[0].inter / UP_ROWS;
   const int nitems = nu * rtr;
+  if (up_role) HH_TR(1, 1); else HH_TR(2, 1);
 
   if (up_role) {
+    if (b == f.R && tid < kFusedCtr)   // the next call's counters
+      __hip_atomic_store(ctr_base + kFusedCtr * ((f.seq + 1) & 1) + tid, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // ---- gate-up: as up_small_mx with x already in LDS ----
     const int q = wave & 1;
     const bool is_up = wave >= 2;
@@ -1869,6 +1840,7 @@ __global__ __launch_bounds__(256, 2) void decode_mx(GemmArgs a, RouteArgs ra, Fu
           at, nch, gi, H, [&](int c) { return mx_ops<NTX>(brow, RS, a.xld, my_sc, nsb, c, gi); },
           [&](const Fmt<Q_MXFP4_W>::A (&w)[NM], int c, const MxOps<NTX> &o) { chunk_mx1<NTX>(acc, w[0].w, o, c, gi, H); });
       if (is_up) s_up[q][lane] = acc;
+      if (it == b - f.R) HH_TR(1, 2);
       __syncthreads();
       if (!is_up && l16 < ntok) {
         const f32x4 y = up_values_mx(a, bias, acc, s_up[q][lane]);
@@ -1889,7 +1861,8 @@ __global__ __launch_bounds__(256, 2) void decode_mx(GemmArgs a, RouteArgs ra, Fu
           store_hq<true>(a, slot, rt, rt * UP_ROWS + 8 * g, rt * UP_ROWS + 8 * g + 4, hq, sb, g);
         }
         wait_stores();
-        if (lane == 0) store_flag(f.flags + f.R + it, f.epoch);
+        if (lane == 0) __hip_atomic_fetch_add(ctr + u, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (it == b - f.R) HH_TR(1, 3);
       }
     }
     return;
@@ -1920,6 +1893,7 @@ __global__ __launch_bounds__(256, 2) void decode_mx(GemmArgs a, RouteArgs ra, Fu
       ATile<Q_MXFP4_W> aw[NM] = {tile_of<PH_DOWN, Q_MXFP4_W>(blob, grp, rb, false, I, l16)};
       AStream<Q_MXFP4_W, NM, DA> as(0, 1, nch);
       as.fill(aw, nch, g, I);
+      if (it == b - f.R - f.U && r == 0) HH_TR(2, 2);
       float db[4] = {0.f, 0.f, 0.f, 0.f};
       if (a.expert_bias && l16 == 0) {
         const uint16_t *bias = (const uint16_t *)(blob + grp.off[5]);
@@ -1928,11 +1902,12 @@ __global__ __launch_bounds__(256, 2) void decode_mx(GemmArgs a, RouteArgs ra, Fu
       }
       // The h terms of this slot exist once every gate-up item of its expert is done.
       const int u = plan.index_of(e);
-      const bool ok = wave_wait(f.flags + f.R + u * rtr, rtr, f.epoch, deadline);
+      const bool ok = wait_count(ctr + u, (uint32_t)rtr, deadline);
       if (!ok && lane == 0) {
         s_bad = 1;
         atomicOr(f.status, 1u);
       }
+      if (it == b - f.R - f.U && r == 0) HH_TR(2, 3);
       // The lane id as a value opaque to the compiler in each item, so the staging addresses are
       // computed here rather than hoisted out of the item loop and held across it.
       int li = lane;
@@ -1948,12 +1923,14 @@ __global__ __launch_bounds__(256, 2) void decode_mx(GemmArgs a, RouteArgs ra, Fu
       hs.pad();
       __builtin_amdgcn_s_waitcnt(0xc07f);   // this wave's LDS stores (lgkmcnt 0)
       __builtin_amdgcn_wave_barrier();
+      if (it == b - f.R - f.U && r == 0) HH_TR(2, 4);
       const uint8_t *my_sc = s_sc + l16 * nsb;
       int gi = g;
       asm volatile("" : "+v"(gi));
       as.template run_pf<true>(
           aw, nch, gi, I, [&](int c) { return mx_ops<NTH>(my_lds, RSH, a.hld, my_sc, nsb, c, gi); },
           [&](const Fmt<Q_MXFP4_W>::A (&w)[NM], int c, const MxOps<NTH> &o) { chunk_mx1<NTH>(acc, w[0].w, o, c, gi, I); });
+      if (it == b - f.R - f.U && r == 0) HH_TR(2, 5);
       if (l16 == 0) {
         const float w = s_w[t * K + r];
 #pragma unroll
@@ -1966,6 +1943,7 @@ __global__ __launch_bounds__(256, 2) void decode_mx(GemmArgs a, RouteArgs ra, Fu
       for (int qq = 1; qq < K; ++qq) y += s_o[qq][tid];
       a.y[(size_t)t * H + rb + tid] = s_bad ? __builtin_nanf("") : y;
     }
+    if (it == b - f.R - f.U) HH_TR(2, 6);
     __syncthreads();   // the next item rewrites the LDS rows and s_o
   }
 }
@@ -3760,9 +3738,12 @@ bool decode_fused_fits(int H, int I, int E, int K, int shared_inter) {
   return shared_inter == 0 && K <= 4 && E <= kFusedMaxE && (H + 127) / 128 <= MX_ONE && (I + 127) / 128 <= MX_ONE && H % 32 == 0 &&
          I % 32 == 0;
 }
-// Router workgroups and gate-up item flags of a T-token call.
+// Flag-buffer words of a T-token call's logit records (8 replicas × T·(E+1) × 4 words); the
+// counters (2·kFusedCtr words) are at the end of the buffer.
 int decode_fused_flags(int T, int E, int K, int I) {
-  return (T * (E + 1) + 3) / 4 + std::min(E, T * K) * (I / UP_ROWS);
+  (void)I;
+  (void)K;
+  return 4 * kRecReplicas * T * (E + 1);
 }
 hipError_t launch_decode_fused(bool gemma, GemmArgs a, const RouteArgs &ra, FuseArgs f, hipStream_t s, Timing tm) {
   const int T = ra.tokens;
@@ -3782,7 +3763,7 @@ hipError_t launch_decode_fused(bool gemma, GemmArgs a, const RouteArgs &ra, Fuse
   });
   const int nup = std::min(a.experts, T * a.top_k) * (a.grp[0].inter / UP_ROWS);
   a.row_tiles = a.hidden / 16;
-  f.R = (T * (a.experts + 1) + 3) / 4;
+  f.R = T * (a.experts + 1);
   // Every gate-up item has its own workgroup: every down item needs all items of its experts, so
   // a second round of items would hold up the whole layer. Down workgroups beyond the resident
   // capacity start as earlier ones finish.
