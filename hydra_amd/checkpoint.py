@@ -275,6 +275,106 @@ def gpt_oss_resident_tensors(hidden: int, experts: int, layers: int, heads: int 
     return out
 
 
+def gemma4_resident_tensors(hidden: int = 2816, experts: int = 128, layers: int = 30,
+                            intermediate: int = 2112, heads: int = 16, sliding_head_dim: int = 256,
+                            sliding_kv_heads: int = 8, global_head_dim: int = 512,
+                            global_kv_heads: int = 2, vocab: int = 262_144,
+                            key_equals_value: bool = True):
+    """Gemma 4's resident tensor list in placement order, (name, bytes), all BF16: per layer
+    (Gemma4Config.residentTensors(atLayer:), Gemma4Config.swift:175-215) the attention with the
+    geometry of its pattern (every sixth layer full: head_dim 512 and 2 kv heads, no v_proj when
+    K equals V; the others sliding), the dense MLP, the expert branch's norms and router; then
+    the final norm and the tied embedding (Gemma4Config.swift:218-225). Defaults: 26B-A4B."""
+    out = []
+    for l in range(layers):
+        p = f"model.language_model.layers.{l}"
+        full = (l + 1) % 6 == 0
+        hd, kv = (global_head_dim, global_kv_heads) if full else (sliding_head_dim, sliding_kv_heads)
+        q, kvd = heads * hd, kv * hd
+        out += [(f"{p}.input_layernorm.weight", 2 * hidden),
+                (f"{p}.self_attn.q_proj.weight", 2 * q * hidden),
+                (f"{p}.self_attn.q_norm.weight", 2 * hd),
+                (f"{p}.self_attn.k_proj.weight", 2 * kvd * hidden),
+                (f"{p}.self_attn.k_norm.weight", 2 * hd)]
+        if not (key_equals_value and full):
+            out.append((f"{p}.self_attn.v_proj.weight", 2 * kvd * hidden))
+        out += [(f"{p}.self_attn.o_proj.weight", 2 * hidden * q),
+                (f"{p}.post_attention_layernorm.weight", 2 * hidden),
+                (f"{p}.pre_feedforward_layernorm.weight", 2 * hidden),
+                (f"{p}.mlp.gate_proj.weight", 2 * intermediate * hidden),
+                (f"{p}.mlp.up_proj.weight", 2 * intermediate * hidden),
+                (f"{p}.mlp.down_proj.weight", 2 * hidden * intermediate),
+                (f"{p}.post_feedforward_layernorm_1.weight", 2 * hidden),
+                (f"{p}.pre_feedforward_layernorm_2.weight", 2 * hidden),
+                (f"{p}.router.proj.weight", 2 * experts * hidden),
+                (f"{p}.router.scale", 2 * hidden),
+                (f"{p}.router.per_expert_scale", 2 * experts),
+                (f"{p}.post_feedforward_layernorm_2.weight", 2 * hidden),
+                (f"{p}.post_feedforward_layernorm.weight", 2 * hidden),
+                (f"{p}.layer_scalar", 2)]
+    out.append(("model.language_model.norm.weight", 2 * hidden))
+    out.append(("model.language_model.embed_tokens.weight", 2 * vocab * hidden))
+    return out
+
+
+def _mlx_parts(stem: str, rows: int, cols: int, bits: int, group: int):
+    """The three tensors of an MLX-affine matrix (MLXAffineLayout.swift:45-54): codes, then bf16
+    scales and biases per group."""
+    words = cols // (32 // bits)
+    return [(f"{stem}.weight", rows * words * 4), (f"{stem}.scales", rows * (cols // group) * 2),
+            (f"{stem}.biases", rows * (cols // group) * 2)]
+
+
+def qwen35_resident_tensors(hidden: int = 2048, experts: int = 256, layers: int = 40,
+                            vocab: int = 248_320, full_interval: int = 4, heads: int = 16,
+                            kv_heads: int = 2, head_dim: int = 256, output_gate: bool = True,
+                            lin_key_heads: int = 16, lin_value_heads: int = 32,
+                            lin_key_dim: int = 128, lin_value_dim: int = 128, conv_kernel: int = 4,
+                            shared_intermediate: int = 512, quant_bits: int = 4,
+                            gate_bits: int = 8, group: int = 64):
+    """Qwen3.5/3.6-MoE's resident tensor list in placement order, (name, bytes)
+    (Qwen35MoeConfig.residentTensors, Qwen35MoeConfig.swift:292-355): per layer the input norm,
+    the attention (every `full_interval`-th layer) or the linear-attention block, the
+    post-attention norm, the router and shared-expert gate (MLX `gate_bits`) and the shared
+    expert (MLX `quant_bits`); then the final norm, the embedding and the untied head. Defaults:
+    the published 35B-A3B 4-bit build."""
+    out = []
+    q, kvd = heads * head_dim, kv_heads * head_dim
+    qrows = 2 * q if output_gate else q
+    conv = 2 * lin_key_heads * lin_key_dim + lin_value_heads * lin_value_dim
+    for l in range(layers):
+        p = f"language_model.model.layers.{l}"
+        out.append((f"{p}.input_layernorm.weight", 2 * hidden))
+        if (l + 1) % full_interval == 0:
+            out += _mlx_parts(f"{p}.self_attn.q_proj", qrows, hidden, quant_bits, group)
+            out += _mlx_parts(f"{p}.self_attn.k_proj", kvd, hidden, quant_bits, group)
+            out += _mlx_parts(f"{p}.self_attn.v_proj", kvd, hidden, quant_bits, group)
+            out += _mlx_parts(f"{p}.self_attn.o_proj", hidden, q, quant_bits, group)
+            out += [(f"{p}.self_attn.q_norm.weight", 2 * head_dim),
+                    (f"{p}.self_attn.k_norm.weight", 2 * head_dim)]
+        else:
+            vd = lin_value_heads * lin_value_dim
+            out += _mlx_parts(f"{p}.linear_attn.in_proj_qkv", conv, hidden, quant_bits, group)
+            out += _mlx_parts(f"{p}.linear_attn.in_proj_z", vd, hidden, quant_bits, group)
+            out += _mlx_parts(f"{p}.linear_attn.in_proj_b", lin_value_heads, hidden, quant_bits, group)
+            out += _mlx_parts(f"{p}.linear_attn.in_proj_a", lin_value_heads, hidden, quant_bits, group)
+            out += _mlx_parts(f"{p}.linear_attn.out_proj", hidden, vd, quant_bits, group)
+            out += [(f"{p}.linear_attn.conv1d.weight", 2 * conv * conv_kernel),
+                    (f"{p}.linear_attn.A_log", 2 * lin_value_heads),
+                    (f"{p}.linear_attn.dt_bias", 2 * lin_value_heads),
+                    (f"{p}.linear_attn.norm.weight", 2 * lin_value_dim)]
+        out.append((f"{p}.post_attention_layernorm.weight", 2 * hidden))
+        out += _mlx_parts(f"{p}.mlp.gate", experts, hidden, gate_bits, group)
+        out += _mlx_parts(f"{p}.mlp.shared_expert_gate", 1, hidden, gate_bits, group)
+        for part in ("gate_proj", "up_proj"):
+            out += _mlx_parts(f"{p}.mlp.shared_expert.{part}", shared_intermediate, hidden, quant_bits, group)
+        out += _mlx_parts(f"{p}.mlp.shared_expert.down_proj", hidden, shared_intermediate, quant_bits, group)
+    out.append(("language_model.model.norm.weight", 2 * hidden))
+    out += _mlx_parts("language_model.model.embed_tokens", vocab, hidden, quant_bits, group)
+    out += _mlx_parts("language_model.lm_head", vocab, hidden, quant_bits, group)
+    return out
+
+
 def resident_placements(tensors):
     """{name: (offset, bytes)}: each tensor at the next 256-byte aligned offset, in order
     (HydraLayout.init, HydraLayout.swift:52-70)."""
@@ -286,15 +386,38 @@ def resident_placements(tensors):
     return out
 
 
+def family_resident_tensors(family: str, model: dict, desc: F.MoEDesc, dims: dict | None = None):
+    """The resident tensor list of a .hydra installation of `family`, from the manifest's model
+    counts (layers, hidden size, experts, vocabulary) and `dims`: the family function's other
+    keyword arguments (attention geometry and so on; omitted ones take the published model's)."""
+    dims = dict(dims or {})
+    L, H, E = model["layerCount"], desc.hidden, desc.experts
+    if family == "gpt-oss":
+        return gpt_oss_resident_tensors(H, E, L, **dims)
+    if family == "gemma4":
+        dims.setdefault("vocab", model.get("vocabSize", 262_144))
+        return gemma4_resident_tensors(hidden=H, experts=E, layers=L, **dims)
+    if family == "qwen3.5-moe":
+        dims.setdefault("vocab", model.get("vocabSize", 248_320))
+        dims.setdefault("quant_bits", desc.bits)
+        dims.setdefault("shared_intermediate", desc.shared_intermediate)
+        dims.setdefault("group", desc.group_size)
+        return qwen35_resident_tensors(hidden=H, experts=E, layers=L, **dims)
+    raise CheckpointError(f"unknown family {family!r} (gpt-oss, gemma4, qwen3.5-moe)")
+
+
 def load_hydra_layer(path: str, desc: F.MoEDesc, family: str, layer: int,
                      ctx: Context | None = None, device: int = 0, router_checkpoint=None,
-                     attention=(64, 64, 8)) -> MoELayer:
+                     attention=(64, 64, 8), resident_dims: dict | None = None) -> MoELayer:
     """The MoE half of layer `layer` of a .hydra installation, resident in HBM. The experts come
     from experts/layer_NN.bin as they are (checked against the manifest's count and stride and
-    this build's blob layout). The router: for GPT-OSS from resident.bin at the placement of
-    `model.layers.L.mlp.router.{weight,bias}` (resident order of GptOssConfig, attention dims
-    (heads, head_dim, kv_heads) = `attention`); for the other families from
-    `router_checkpoint` (a safetensors checkpoint or directory), as load_moe_layer reads it."""
+    this build's blob layout). The router tensors (Qwen: also the shared expert and its gate)
+    come from resident.bin at their placements in the family's resident order
+    (HydraLayout.swift:52-70; GptOssConfig.swift:148-166, Gemma4Config.swift:175-225,
+    Qwen35MoeConfig.swift:292-355), the model's shape from the manifest and `resident_dims`
+    (GPT-OSS: `attention` = (heads, head_dim, kv_heads)); or, when `router_checkpoint` (a
+    safetensors checkpoint or directory) is given, from that checkpoint, as load_moe_layer reads
+    them."""
     m = hydra_manifest(path)
     model, lay_m = m["model"], m["layout"]
     lay = F.blob_layout(desc)
@@ -310,31 +433,45 @@ def load_hydra_layer(path: str, desc: F.MoEDesc, family: str, layer: int,
     if not os.path.exists(fn) or os.path.getsize(fn) != desc.experts * lay.stride:
         raise CheckpointError(f"{fn}: missing or not {desc.experts} blobs of {lay.stride} bytes")
     blobs = np.memmap(fn, dtype=np.uint8, mode="r", shape=(desc.experts, lay.stride))
-    tensors = {}
-    if family == "gpt-oss":
-        heads, head_dim, kv_heads = attention
-        place = resident_placements(gpt_oss_resident_tensors(desc.hidden, desc.experts,
-                                                             model["layerCount"], heads, head_dim,
-                                                             kv_heads))
-        rfn = os.path.join(path, "resident.bin")
-        res = np.memmap(rfn, dtype=np.uint8, mode="r")
-        for key, suffix in [("router_weight", "weight"), ("router_bias", "bias")]:
-            if key == "router_bias" and not desc.expert_bias:
-                continue
-            off, nb = place[f"model.layers.{layer}.mlp.router.{suffix}"]
-            if off + nb > res.size:
-                raise CheckpointError(f"{rfn}: shorter than the router placement of layer {layer}")
-            tensors[key] = np.array(res[off:off + nb]).view(np.uint16)
-        router_bits = 0
-    else:
-        if router_checkpoint is None:
-            raise CheckpointError(f"{family}: the router comes from router_checkpoint (its resident "
-                                  f"placement is not described here)")
+    router_bits = 0
+    if router_checkpoint is not None:
         ck = router_checkpoint if isinstance(router_checkpoint, Checkpoint) else Checkpoint(router_checkpoint)
         router_bits = _quantised_router_bits(ck, desc, family, layer)
-        for key, (name, dt, shape, req) in router_sources(desc, family, layer, router_bits).items():
-            if req or name in ck:
-                tensors[key] = np.array(ck.tensor(name, dt, shape))
+
+        def fetch(name, dt, shape):
+            return np.array(ck.tensor(name, dt, shape))
+
+        def present(name):
+            return name in ck
+    else:
+        dims = dict(resident_dims or {})
+        if family == "gpt-oss":
+            heads, head_dim, kv_heads = attention
+            dims.update(heads=heads, head_dim=head_dim, kv_heads=kv_heads)
+        place = resident_placements(family_resident_tensors(family, model, desc, dims))
+        rfn = os.path.join(path, "resident.bin")
+        res = np.memmap(rfn, dtype=np.uint8, mode="r")
+        if family == "qwen3.5-moe":
+            router_bits = dims.get("gate_bits", 8)
+        npdt = {"BF16": np.uint16, "U32": np.uint32, "U8": np.uint8}
+
+        def fetch(name, dt, shape):
+            if name not in place:
+                raise CheckpointError(f"{rfn}: no resident placement for {name}")
+            off, nb = place[name]
+            want = int(np.prod(shape)) * np.dtype(npdt[dt]).itemsize
+            if nb != want:
+                raise CheckpointError(f"{name}: {nb} resident bytes, the description needs {want}")
+            if off + nb > res.size:
+                raise CheckpointError(f"{rfn}: shorter than the placement of {name}")
+            return np.array(res[off:off + nb]).view(npdt[dt]).reshape(shape)
+
+        def present(name):
+            return name in place
+    tensors = {}
+    for key, (name, dt, shape, req) in router_sources(desc, family, layer, router_bits).items():
+        if req or present(name):
+            tensors[key] = fetch(name, dt, shape)
     ctx = ctx or Context(device)
     dev = torch.device(f"cuda:{ctx.device}")
     torch.cuda.synchronize(dev)
@@ -344,19 +481,15 @@ def load_hydra_layer(path: str, desc: F.MoEDesc, family: str, layer: int,
         a = np.ascontiguousarray(data)
         if key.endswith("_words"):
             a = a.view(np.int32)
-        elif a.dtype == np.uint8:
-            a = a.view(np.int16)
-        elif a.dtype == np.uint16:
+        elif a.dtype in (np.uint8, np.uint16):
             a = a.view(np.int16)
         dt[key] = torch.from_numpy(a.copy()).to(dev)
     if desc.shared_intermediate:
-        shared = expert_sources(desc, family, layer, shared=True)
-        ck = router_checkpoint if isinstance(router_checkpoint, Checkpoint) else Checkpoint(router_checkpoint)
         slay = F.blob_layout(desc, desc.shared_intermediate)
         blob = np.zeros(slay.stride, np.uint8)
-        for slot, name, dtn, shape in shared:
+        for slot, name, dtn, shape in expert_sources(desc, family, layer, shared=True):
             blob[slay.offsets[slot]:slay.offsets[slot] + slay.sizes[slot]] = \
-                np.asarray(ck.tensor(name, dtn, shape)).reshape(-1)
+                np.asarray(fetch(name, dtn, shape)).view(np.uint8).reshape(-1)
         dt["shared_expert"] = torch.from_numpy(blob).to(dev)
     torch.cuda.synchronize(dev)
     return MoELayer.resident(desc, experts, lay.stride, dt, ctx, router_bits=router_bits)

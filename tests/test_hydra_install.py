@@ -148,3 +148,124 @@ def test_hydra_qwen_layer_with_router_from_checkpoint(tmp_path):
             assert torch.equal(i0, i1) and torch.equal(w0, w1) and torch.equal(y0, y1)
     finally:
         ctx.close()
+
+
+# ---- Gemma 4 and Qwen3.5-MoE resident inventories ---------------------------------------------
+# Pinned by the reference's own tests: Gemma4ConfigTests.swift:47-59 (v_proj on sliding layers
+# only), :79-100 (tied embedding resident, resident floor 4.2-4.8 GiB and above GPT-OSS-20B's,
+# install 48-52 GB); Qwen35MoeConfigTests.swift:81-133 (names, expert pool 16.5-17.5 GiB,
+# text-only total 17-19 GiB, pool share above 0.85, the 8-bit build's resident set larger).
+
+def test_gemma4_resident_list_matches_reference_tests():
+    t = CK.gemma4_resident_tensors()
+    names = [n for n, _ in t]
+    assert any(n.endswith("layers.0.self_attn.v_proj.weight") for n in names)
+    assert not any(n.endswith("layers.5.self_attn.v_proj.weight") for n in names)
+    assert not any("v_norm" in n or "lm_head" in n for n in names)
+    assert "model.language_model.embed_tokens.weight" in names
+    resident = sum(b for _, b in t)
+    assert 4.2 < resident / 2**30 < 4.8
+    gpt20 = sum(b for _, b in CK.gpt_oss_resident_tensors(2880, 32, 24)) + 2 * 2880 + 1_158_266_880
+    assert resident > gpt20
+    pool = 30 * 128 * F.blob_layout(F.GEMMA_BF16).payload
+    assert 48 < (pool + resident) / 1e9 < 52
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_qwen35_resident_list_matches_reference_tests(bits):
+    desc = F.QWEN_35B_A3B_Q4 if bits == 4 else F.QWEN_35B_A3B_Q8
+    t = CK.qwen35_resident_tensors(quant_bits=bits)
+    names = {n for n, _ in t}
+    p = "language_model.model.layers"
+    for n in [f"{p}.0.linear_attn.in_proj_qkv.weight", f"{p}.0.linear_attn.conv1d.weight",
+              f"{p}.0.linear_attn.A_log", f"{p}.0.linear_attn.dt_bias", f"{p}.3.self_attn.q_proj.weight",
+              f"{p}.3.self_attn.q_norm.weight", f"{p}.0.mlp.gate.weight",
+              f"{p}.0.mlp.shared_expert.up_proj.weight", f"{p}.0.mlp.shared_expert_gate.weight",
+              "language_model.model.embed_tokens.weight", "language_model.lm_head.weight"]:
+        assert n in names, n
+    assert f"{p}.0.self_attn.q_proj.weight" not in names
+    assert f"{p}.3.linear_attn.in_proj_qkv.weight" not in names
+    resident = sum(b for _, b in t) / 2**30
+    pool = 40 * 256 * F.blob_layout(desc).payload / 2**30
+    if bits == 4:
+        assert 16.5 < pool < 17.5
+        assert 17.0 < pool + resident < 19.0
+        assert pool / (pool + resident) > 0.85
+    else:
+        four = sum(b for _, b in CK.qwen35_resident_tensors(quant_bits=4)) / 2**30
+        assert resident > four
+
+
+SMALL_GEMMA = dict(intermediate=96, heads=2, sliding_head_dim=32, sliding_kv_heads=1,
+                   global_head_dim=64, global_kv_heads=1)
+SMALL_QWEN = dict(heads=2, kv_heads=1, head_dim=64, lin_key_heads=1, lin_value_heads=2,
+                  lin_key_dim=64, lin_value_dim=64)
+
+
+def write_family_install(root, family, desc, layer_dict, dims, vocab=16):
+    """A .hydra of `family` with LAYERS layers: resident.bin holding layer LAYER's router
+    tensors (Qwen: also the shared expert and its gate) at their placements, random bytes
+    elsewhere; experts/layer_NN.bin the packed blobs."""
+    lay = F.blob_layout(desc)
+    os.makedirs(os.path.join(root, "experts"), exist_ok=True)
+    model = {"name": "synthetic", "layerCount": LAYERS, "expertCount": desc.experts,
+             "expertsPerToken": desc.top_k, "hiddenSize": desc.hidden, "vocabSize": vocab}
+    json.dump({"format": "hydra/1", "model": model,
+               "layout": {"expertStrideBytes": lay.stride, "expertPayloadBytes": lay.payload,
+                          "residentBytes": 0, "embeddingBytes": 0, "tensorAlignment": 256,
+                          "pageAlignment": 16384}}, open(os.path.join(root, "manifest.json"), "w"))
+    place = CK.resident_placements(CK.family_resident_tensors(family, model, desc, dims))
+    end = max(o + b for o, b in place.values())
+    res = synth.random_bytes(6, "resident", end)
+
+    def put(name, arr):
+        off, nb = place[name]
+        raw = np.ascontiguousarray(arr).view(np.uint8).reshape(-1)
+        assert raw.size == nb, (name, raw.size, nb)
+        res[off:off + nb] = raw
+    srcs = CK.router_sources(desc, family, LAYER, layer_dict.get("router_bits", 0))
+    for key, (name, _, _, req) in srcs.items():
+        if key in layer_dict:
+            put(name, layer_dict[key])
+    if desc.shared_intermediate:
+        slay = F.blob_layout(desc, desc.shared_intermediate)
+        blob = layer_dict["shared_expert"]
+        for slot, name, _, _ in CK.expert_sources(desc, family, LAYER, shared=True):
+            put(name, blob[slay.offsets[slot]:slay.offsets[slot] + slay.sizes[slot]])
+    res.tofile(os.path.join(root, "resident.bin"))
+    layer_dict["experts"].tofile(os.path.join(root, "experts", f"layer_{LAYER:02d}.bin"))
+
+
+FAMILY_CASES = {
+    "gemma4": (F.MoEDesc(hidden=256, intermediate=128, experts=8, top_k=2, quant=F.QUANT_BF16,
+                         activation=F.ACT_GELU_TANH, router=F.ROUTER_GEMMA, router_eps=1e-6),
+               0, SMALL_GEMMA),
+    "qwen3.5-moe": (F.MoEDesc(hidden=256, intermediate=128, experts=8, top_k=2, quant=F.QUANT_MLX4,
+                              activation=F.ACT_SILU, router=F.ROUTER_SOFTMAX_TOPK_RENORM,
+                              shared_intermediate=128, group_size=64), 8, SMALL_QWEN),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("family", list(FAMILY_CASES))
+def test_hydra_family_layer_from_resident_bin(tmp_path, family):
+    """Gemma's router (projection, scale, per-expert scale) and Qwen's 8-bit MLX router, shared
+    gate and shared expert read from resident.bin: the loaded layer equals the synthetic one
+    bit for bit, in decode and prefill."""
+    import torch
+    from hydra_amd.layer import Context, MoELayer
+    desc, rb, dims = FAMILY_CASES[family]
+    print(f"[gpu] .hydra {family} layer from resident.bin", flush=True)
+    layer = synth.make_layer(desc, seed=11, router_bits=rb)
+    write_family_install(str(tmp_path), family, desc, layer, dims)
+    ctx = Context(0)
+    try:
+        loaded = CK.load_hydra_layer(str(tmp_path), desc, family, LAYER, ctx=ctx, resident_dims=dims)
+        ref = MoELayer(layer, ctx)
+        for T in (1, 40):
+            x = synth.make_tokens(desc.hidden, T, seed=30 + T)
+            y0, i0, w0 = ref.forward(x)
+            y1, i1, w1 = loaded.forward(x)
+            assert torch.equal(i0, i1) and torch.equal(w0, w1) and torch.equal(y0, y1)
+    finally:
+        ctx.close()
