@@ -793,8 +793,9 @@ constexpr int MX_PF = HH_MX_PF;   // chunks a single-round MXFP4 decode wave iss
 constexpr int MX_PF_T1 = 10;
 constexpr int kFusedMaxE = 128;   // experts of layers that take the fused decode kernel
 // Batches that take the two-launch decode (the router inside the gate-up launch). Larger batches
-// measured slower: each gate-up workgroup quantises every token's x itself (T = 8: ≈ 6 µs of
-// dependent rounds), and the LDS copy of the logits halves the workgroups per compute unit.
+// measured no faster (T = 4: 69.3k against 69.1–69.8k tokens/s) or slower (T = 8: 75k against
+// 92k): every gate-up workgroup quantises every token's x itself, and the LDS copy of the logits
+// leaves fewer workgroups per compute unit.
 constexpr int kFusedRouterT = 2;
 constexpr int LDS_PAD = 8;        // bf16 elements of padding per staged row (bank spread)
 
@@ -1222,10 +1223,23 @@ __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)
 // (quant_block).
 __device__ __forceinline__ void quant_x_lds(const uint16_t *x, int T, int H, int xld, uint8_t *s_xb, int RS) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, l16 = lane & 15;
-  const int nb = H / 32, per_t = (nb + 15) / 16;
-  for (int w = wave; w < T * per_t; w += 4) {
-    const int t = w / per_t, b = 16 * (w - t * per_t) + l16, bc = min(b, nb - 1);
-    const u32x4 xv = *(const u32x4 *)(x + (size_t)t * H + bc * 32 + 8 * g);
+  const int nb = H / 32, per_t = (nb + 15) / 16, nw = T * per_t;
+  // A wave's tasks w, w + 4, ... in batches of QXB: every load of a batch is issued before the
+  // first is used (one memory latency per batch, not per task).
+  constexpr int QXB = 6;
+  for (int w0 = wave; w0 < nw; w0 += 4 * QXB) {
+    u32x4 xb[QXB];
+#pragma unroll
+    for (int k = 0; k < QXB; ++k) {
+      const int w = min(w0 + 4 * k, nw - 1), t = w / per_t, bc = min(16 * (w - t * per_t) + l16, nb - 1);
+      xb[k] = *(const u32x4 *)(x + (size_t)t * H + bc * 32 + 8 * g);
+    }
+#pragma unroll
+    for (int k = 0; k < QXB; ++k) {
+    const int w = w0 + 4 * k;
+    if (w >= nw) break;
+    const int t = w / per_t, b = 16 * (w - t * per_t) + l16;
+    const u32x4 xv = xb[k];
     float v[8];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -1241,6 +1255,7 @@ __device__ __forceinline__ void quant_x_lds(const uint16_t *x, int T, int H, int
         *(u32x2 *)(row + b * 32 + 8 * g) = u32x2{q[j][0], q[j][1]};
         if (g == 0) row[xld + b] = (uint8_t)sb[j];
       }
+    }
     }
   }
   const int hp = (H + 127) & ~127, nz = (hp - H) / 16, ns = (hp - H) / 32;

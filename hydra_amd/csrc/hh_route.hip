@@ -33,6 +33,41 @@
 
 namespace hh {
 
+// Development timeline (built only with -DHH_TRACE): wall-clock stamps (100 MHz) per workgroup of
+// the small-batch router kernels and of route_select_kernel, [block][point], read as kernel 0 of
+// the decode kernels' timeline.
+#ifdef HH_TRACE
+constexpr int kRtTraceBlocks = 4096, kRtTracePoints = 8;
+static __device__ uint64_t hh_trace_rt[kRtTraceBlocks * kRtTracePoints];
+#define HH_RT(point)                                                                               \
+  do {                                                                                             \
+    if ((threadIdx.x & 63) == 0 && blockIdx.x < kRtTraceBlocks)                                    \
+      hh_trace_rt[blockIdx.x * kRtTracePoints + (point)] = wall_clock64();                         \
+  } while (0)
+hipError_t trace_read_route(void *out, size_t bytes) {
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(hh_trace_rt), std::min(bytes, sizeof(hh_trace_rt)), 0,
+                             hipMemcpyDeviceToHost);
+}
+hipError_t trace_clear_route() {
+  static uint64_t zeros[kRtTraceBlocks * kRtTracePoints];
+  return hipMemcpyToSymbol(HIP_SYMBOL(hh_trace_rt), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
+}
+// Point 7 of route_select_kernel's rows: the token's candidate count.
+#define HH_RT_NC(nc)                                                                               \
+  do {                                                                                             \
+    if (threadIdx.x == 0 && blockIdx.x < kRtTraceBlocks) hh_trace_rt[blockIdx.x * kRtTracePoints + 7] = (uint64_t)(nc); \
+  } while (0)
+// The dispatch workgroup's stamps: row kRtTraceBlocks − 1, wave 0.
+#define HH_DS(point)                                                                               \
+  do {                                                                                             \
+    if (threadIdx.x == 0) hh_trace_rt[(kRtTraceBlocks - 1) * kRtTracePoints + (point)] = wall_clock64(); \
+  } while (0)
+#else
+#define HH_DS(point) do {} while (0)
+#define HH_RT(point) do {} while (0)
+#define HH_RT_NC(nc) do {} while (0)
+#endif
+
 // Stable token→expert permutation of the whole batch by one workgroup of NW waves; `idx` is
 // the top-k table [T][K] (global or LDS). Wave w owns the contiguous assignment range
 // [w·R, (w+1)·R): pass 1 counts its assignments per expert, a scan over (expert, wave) gives every
@@ -53,6 +88,7 @@ __device__ __forceinline__ void dispatch_batch(const RouteArgs &a, const int32_t
   const int TN = a.tile_tokens;
   const int R = ((A + NW - 1) / NW + 63) & ~63;     // assignments per wave, whole chunks
   const int lo = min(wave * R, A), hi = min(lo + R, A);
+  HH_DS(0);
   for (int e = tid; e < NW * kMaxExperts; e += NT) (&s_wc[0][0])[e] = 0;
   __syncthreads();
   const int nbits = E > 1 ? 32 - __clz(E - 1) : 1;
@@ -89,7 +125,9 @@ __device__ __forceinline__ void dispatch_batch(const RouteArgs &a, const int32_t
       __builtin_amdgcn_wave_barrier();
     }
   }
+  HH_DS(1);
   __syncthreads();
+  HH_DS(2);
   // Per expert: total count, and each wave's first position relative to the expert's segment.
   for (int e = tid; e < E; e += NT) {
     int run = 0;
@@ -105,6 +143,7 @@ __device__ __forceinline__ void dispatch_batch(const RouteArgs &a, const int32_t
   __syncthreads();
   block_exclusive_scan<NW>(s_off, E, s_wave);
   const int routed_tiles = block_exclusive_scan<NW>(s_tiles, E, s_wave);
+  HH_DS(3);
   for (int b0 = lo; b0 < hi; b0 += 64 * DCH) {
     load_ids(b0);
 #pragma unroll
@@ -125,7 +164,9 @@ __device__ __forceinline__ void dispatch_batch(const RouteArgs &a, const int32_t
       __builtin_amdgcn_wave_barrier();
     }
   }
+  HH_DS(4);
   __syncthreads();
+  HH_DS(5);
   // Segments and work items (expert, first position, tokens), ascending expert order.
   for (int e = tid; e < E; e += NT) {
     a.seg[e] = s_off[e];
@@ -161,6 +202,7 @@ __device__ __forceinline__ void dispatch_batch(const RouteArgs &a, const int32_t
     a.seg[E + 1] = A;
   }
   if (tid == 0) *a.n_work = nwork;
+  HH_DS(6);
 }
 
 
@@ -462,34 +504,7 @@ __global__ __launch_bounds__(64 * RLW) void route_logits_kernel(RouteArgs a) {
 // values do not depend on how rows are grouped) and wave 1 the shared gate's; wave 0 ranks them
 // (TopK's order: larger value, then smaller index, whatever the insertion order) and writes the
 // token's routing.
-// Development timeline (built only with -DHH_TRACE): wall-clock stamps (100 MHz) per workgroup of
-// the small-batch router kernels and of route_select_kernel, [block][point], read as kernel 0 of
-// the decode kernels' timeline.
-#ifdef HH_TRACE
-constexpr int kRtTraceBlocks = 4096, kRtTracePoints = 8;
-static __device__ uint64_t hh_trace_rt[kRtTraceBlocks * kRtTracePoints];
-#define HH_RT(point)                                                                               \
-  do {                                                                                             \
-    if ((threadIdx.x & 63) == 0 && blockIdx.x < kRtTraceBlocks)                                    \
-      hh_trace_rt[blockIdx.x * kRtTracePoints + (point)] = wall_clock64();                         \
-  } while (0)
-hipError_t trace_read_route(void *out, size_t bytes) {
-  return hipMemcpyFromSymbol(out, HIP_SYMBOL(hh_trace_rt), std::min(bytes, sizeof(hh_trace_rt)), 0,
-                             hipMemcpyDeviceToHost);
-}
-hipError_t trace_clear_route() {
-  static uint64_t zeros[kRtTraceBlocks * kRtTracePoints];
-  return hipMemcpyToSymbol(HIP_SYMBOL(hh_trace_rt), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice);
-}
-// Point 7 of route_select_kernel's rows: the token's candidate count.
-#define HH_RT_NC(nc)                                                                               \
-  do {                                                                                             \
-    if (threadIdx.x == 0 && blockIdx.x < kRtTraceBlocks) hh_trace_rt[blockIdx.x * kRtTracePoints + 7] = (uint64_t)(nc); \
-  } while (0)
-#else
-#define HH_RT(point) do {} while (0)
-#define HH_RT_NC(nc) do {} while (0)
-#endif
+
 
 // A T=2048 batch is 2048 four-wave workgroups: the GEMMA variant took 129 VGPRs, three per
 // compute unit (about three rounds of them); at most 128 gives four (five spills).
