@@ -339,6 +339,10 @@ FUSED_CASES = {
     "mxfp4-ragged": (TINY["mxfp4-ragged"], [3, 16, 1, 7]),
     "gpt-oss-20b": (F.GPT_OSS_20B, [1, 4, 16, 2, 8, 1]),
     "gpt-oss-120b": (F.GPT_OSS_120B, [1, 8, 3]),
+    # the BF16 / MLX decode gate-up kernel with its fused routers (bf16 GEMMA, 8-bit MLX)
+    "gemma-bf16": (F.GEMMA_BF16, [1, 2, 5, 1]),
+    "qwen-mlx4-router8": (F.QWEN_35B_A3B_Q4, [1, 2, 3, 1], 8),
+    "qwen-mlx8-bf16router": (F.QWEN_35B_A3B_Q8, [2, 1]),
 }
 
 
@@ -351,9 +355,9 @@ def test_fused_decode_equals_three_launch_decode(torch_dev, ctx, name):
     in the scratch or the flags by an earlier call (another batch size, other tokens) would
     show."""
     from hydra_amd.layer import MoELayer
-    desc, Ts = FUSED_CASES[name]
+    desc, Ts, *rb = FUSED_CASES[name]
     say(f"fused decode {name}")
-    L = MoELayer(synth.make_layer(desc, seed=51), ctx)
+    L = MoELayer(synth.make_layer(desc, seed=51, router_bits=rb[0] if rb else 0), ctx)
     try:
         for i, T in enumerate(Ts):
             x = synth.make_tokens(desc.hidden, T, seed=60 + i)
