@@ -1279,12 +1279,14 @@ __device__ __forceinline__ void quant_x_lds(const uint16_t *x, int T, int H, int
 // workgroups hide one another's latency.
 // NCH > 0 (ONE only): every row of the layer has exactly NCH chunks (checked on the host).
 // FR (fused router): the grid's first f.R workgroups are the router, one per (token, row) pair
-// (split_pair_logit, the router kernel's arithmetic), each storing its logit with a device-scope
-// store and then its flag; the other workgroups quantise x into LDS themselves (the router
-// kernel's terms, quant_block), wait for the R flags, read the logits with device-scope loads
-// and go on as above. Router workgroups wait for nothing and have the smaller indices, which
-// the dispatcher starts first, so every wait is for workgroups that run. Waits are bounded
-// (10 ms); a workgroup that times out sets bit 0 of *f.status and stops.
+// (split_pair_logit, the router kernel's arithmetic), each storing its logit as a checksummed
+// record into the 8 per-XCD replicas (store_logit_record); the other workgroups quantise x into
+// LDS themselves (the router kernel's terms, quant_block), then wave 0 polls its XCD's replica
+// until every record carries the call's epoch (wait_logit_records: device-scope loads, no
+// fences, the logits arriving with the same load that shows them ready) and the selection reads
+// them from LDS. Router workgroups wait for nothing and have the smaller indices, which the
+// dispatcher starts first, so every wait is for workgroups that run. Waits are bounded (10 ms);
+// a workgroup that times out sets bit 0 of *f.status and stops.
 template <int DA, bool ONE, int XB, int NCH = 0, bool FR = false>
 __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra, FuseArgs f) {
   warm_kernargs<sizeof(GemmArgs) + sizeof(RouteArgs) + sizeof(FuseArgs)>();
