@@ -599,6 +599,28 @@ __device__ __forceinline__ void stage_batch(int base, int id, int threads, int n
   }
 }
 
+// Development timeline (built only with -DHH_TRACE): per workgroup, wall-clock stamps (100 MHz)
+// at fixed points of the decode kernels, [kernel][block][point]; the last call's values.
+#ifdef HH_TRACE
+constexpr int kTraceBlocks = 4096, kTracePoints = 8;
+static __device__ uint64_t hh_trace_buf[3 * kTraceBlocks * kTracePoints];
+#define HH_TR(kern, point)                                                                     \
+  do {                                                                                         \
+    if (threadIdx.x == 0 && blockIdx.x < kTraceBlocks)                                         \
+      hh_trace_buf[((kern) * kTraceBlocks + blockIdx.x) * kTracePoints + (point)] = wall_clock64(); \
+  } while (0)
+// Per-step stamps (core clock) of MFMA wave 0 of workgroup 0 of the MXFP4 prefill gate-up:
+// hh_trace_buf[2][step][point], steps < kTraceBlocks.
+#define HH_TRS(step, point)                                                                      \
+  do {                                                                                           \
+    if (threadIdx.x == 0 && blockIdx.x == 0 && (step) < kTraceBlocks)                            \
+      hh_trace_buf[(2 * kTraceBlocks + (step)) * kTracePoints + (point)] = clock64();            \
+  } while (0)
+#else
+#define HH_TR(kern, point) do {} while (0)
+#define HH_TRS(step, point) do {} while (0)
+#endif
+
 // ---- decode prologue -----------------------------------------------------------------------------
 // Every decode gate-up workgroup selects the top-k of every token of the batch itself from the
 // exact fp64 logits (wave w: tokens w, w + NW, ...) into s_idx [T][K], so the decode step needs no
@@ -634,10 +656,12 @@ __device__ __forceinline__ void select_batch(const GemmArgs &a, const RouteArgs 
       const double *lg = ra.lg64 + (size_t)t * (E + 1);
       TopK tk = E <= 64 ? topk_rank64(lg, E, K, s_lg[wave], s_ri[wave])
                               : topk_fast(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave]);
+      if (t == wave) HH_TR(1, 5);
       prob_order(tk, K, ra.router);
       if (lane < K) s_idx[t * K + lane] = tk.index_of(lane);
       if (blockIdx.x == 0) finish_token(ra, t, tk, has_shared ? lg[E] : 0.0);
     }
+    HH_TR(1, 6);
   }
   __syncthreads();
 }
@@ -759,28 +783,6 @@ __device__ __forceinline__ void mlx_sb_store(const u32x4 (&r)[kMlxSbNB], uint32_
 }
 
 // ---- decode: gate-up ----------------------------------------------------------------------------
-// Development timeline (built only with -DHH_TRACE): per workgroup, wall-clock stamps (100 MHz)
-// at fixed points of the decode kernels, [kernel][block][point]; the last call's values.
-#ifdef HH_TRACE
-constexpr int kTraceBlocks = 4096, kTracePoints = 8;
-static __device__ uint64_t hh_trace_buf[3 * kTraceBlocks * kTracePoints];
-#define HH_TR(kern, point)                                                                     \
-  do {                                                                                         \
-    if (threadIdx.x == 0 && blockIdx.x < kTraceBlocks)                                         \
-      hh_trace_buf[((kern) * kTraceBlocks + blockIdx.x) * kTracePoints + (point)] = wall_clock64(); \
-  } while (0)
-// Per-step stamps (core clock) of MFMA wave 0 of workgroup 0 of the MXFP4 prefill gate-up:
-// hh_trace_buf[2][step][point], steps < kTraceBlocks.
-#define HH_TRS(step, point)                                                                      \
-  do {                                                                                           \
-    if (threadIdx.x == 0 && blockIdx.x == 0 && (step) < kTraceBlocks)                            \
-      hh_trace_buf[(2 * kTraceBlocks + (step)) * kTracePoints + (point)] = clock64();            \
-  } while (0)
-#else
-#define HH_TR(kern, point) do {} while (0)
-#define HH_TRS(step, point) do {} while (0)
-#endif
-
 constexpr int SMALL_T = 16;       // largest batch of the decode kernels
 constexpr int UP_ROWS = 32;       // intermediates per up_small workgroup (2 tiles × {gate, up})
 constexpr int MX_ONE_CHUNKS = 24; // MXFP4 decode rows of at most this many 128-column chunks stream in one round
