@@ -149,7 +149,7 @@ constexpr int kMaxTokens = 1 << 16;  // tokens per call
 
 // Scratch carve-up for T tokens of a layer shaped like d. All offsets 256-byte aligned.
 struct Scratch {
-  size_t lg64, lg32, wn, topk_idx, topk_w, slot_w, seg, order, work, n_work, h_hi, h_lo, slot_out;
+  size_t lg64, lg32, wn, topk_idx, topk_w, slot_w, seg, order, work, n_work, h_hi, h_lo, slot_out, dcount;
   size_t xq, xs, hq, hs, status, total;
   size_t work_half, n_work_half;   // half_down: the down phase's items of tile_tokens / 2
   int slots, positions, ldh, max_work, tile_tokens, nt;
@@ -202,6 +202,7 @@ Scratch plan(const hh_moe_desc &d, int T) {
   s.order = take(sizeof(int32_t) * (size_t)s.positions);
   s.work = take(sizeof(int4) * (size_t)s.max_work);
   s.n_work = take(sizeof(int32_t));
+  s.dcount = take((size_t)A >= (size_t)hh::DB_MIN_ASSIGN ? sizeof(int32_t) * hh::DB_MAX * E : 0);
   // MXFP4 batches of 64-token items: the down product takes 32-token items of 256 rows, which
   // re-read the three activation terms half as often per row as 128-row tiles (a 256 × 64 tile
   // does not fit the register file).
@@ -350,6 +351,7 @@ hh::RouteArgs route_args(const hh_moe_desc &d, const hh_moe_weights *w, uint8_t 
   r.order = (int32_t *)(base + s.order);
   r.work = (int4 *)(base + s.work);
   r.n_work = (int32_t *)(base + s.n_work);
+  r.dcount = (size_t)T * d.top_k >= (size_t)hh::DB_MIN_ASSIGN ? (int32_t *)(base + s.dcount) : nullptr;
   r.max_work = s.max_work;
   r.work_half = s.half_down ? (int4 *)(base + s.work_half) : nullptr;
   r.n_work_half = s.half_down ? (int32_t *)(base + s.n_work_half) : nullptr;

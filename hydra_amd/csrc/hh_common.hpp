@@ -8,6 +8,10 @@ namespace hh {
 
 enum Quant { Q_MXFP4 = 0, Q_MLX4 = 1, Q_MLX8 = 2, Q_BF16 = 3 };
 enum Act { A_SWIGLU_OAI = 0, A_SILU = 1, A_GELU_TANH = 2 };
+// Multi-block dispatch (hh_route.hip): at most DB_MAX blocks, taken from DB_MIN_ASSIGN (token, rank)
+// assignments on; the count buffer holds DB_MAX · E words.
+constexpr int DB_MAX = 64, DB_MIN_ASSIGN = 4096;
+
 enum Router { R_TOPK_SOFTMAX = 0, R_SOFTMAX_TOPK_RENORM = 1, R_GEMMA = 2 };
 
 constexpr int kMaxTopK = 8;
@@ -305,6 +309,7 @@ struct RouteArgs {
   // Optional (null: not written): the same routed segments in items of tile_tokens / 2 tokens,
   // for a down phase with half the gate-up's token tile (no shared expert).
   int4 *work_half;              // [max_work_half]
+  int32_t *dcount;              // [dispatch blocks][E]: per-block expert counts (multi-block dispatch)
   int32_t *n_work_half;         // [1]
   int32_t max_work_half;
 };

@@ -206,6 +206,179 @@ __device__ __forceinline__ void dispatch_batch(const RouteArgs &a, const int32_t
 }
 
 
+// ---- multi-block dispatch (large batches) ---------------------------------------------------------
+// The same stable grouping as dispatch_batch over DB_MAX or fewer 256-thread workgroups, in two
+// launches: dispatch_count_kernel writes each block's per-expert counts, dispatch_scatter_kernel
+// gives every block its first position inside each expert's segment (the segments of all experts
+// before it, plus the same expert's counts of the earlier blocks) and writes its assignments'
+// positions in (t, r) order, as dispatch_batch does within one workgroup. Every block also forms
+// the segment offsets and the work lists' tile offsets and writes the items of the experts
+// e ≡ block (mod blocks); block 0 writes the segment table and the item counts. A single
+// 1024-thread workgroup was bound by its compute unit's issue rate (≈ 80 instructions per 64
+// assignments per pass on 16 waves sharing 4 SIMDs).
+__host__ __device__ inline int dispatch_blocks(int A) {
+  const int nb = (A + 255) / 256;
+  return nb < 1 ? 1 : (nb > DB_MAX ? DB_MAX : nb);
+}
+// Assignments per block: whole 256-assignment groups (4 waves × 64).
+__host__ __device__ inline int dispatch_range(int A, int nb) { return (((A + nb - 1) / nb) + 255) & ~255; }
+
+__global__ __launch_bounds__(256) void dispatch_count_kernel(RouteArgs a) {
+  warm_kernargs<sizeof(RouteArgs)>();
+  __shared__ int s_c[kMaxExperts];
+  const int tid = threadIdx.x, E = a.experts, A = a.tokens * a.top_k;
+  const int R = dispatch_range(A, gridDim.x), lo = blockIdx.x * R, hi = min(lo + R, A);
+  for (int e = tid; e < E; e += 256) s_c[e] = 0;
+  __syncthreads();
+  for (int i = lo + tid; i < hi; i += 256) atomicAdd(&s_c[a.topk_idx[i]], 1);
+  __syncthreads();
+  for (int e = tid; e < E; e += 256) a.dcount[(size_t)blockIdx.x * E + e] = s_c[e];
+}
+
+__global__ __launch_bounds__(256) void dispatch_scatter_kernel(RouteArgs a) {
+  warm_kernargs<sizeof(RouteArgs)>();
+  constexpr int NW = 4;
+  __shared__ int s_off[kMaxExperts];      // segment offsets (exclusive scan of the totals)
+  __shared__ int s_tot[kMaxExperts];
+  __shared__ int s_tiles[kMaxExperts];
+  __shared__ int s_wc[NW][kMaxExperts];   // per wave: count, then running position
+  __shared__ int s_wave[NW];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int E = a.experts, K = a.top_k, T = a.tokens, A = T * K, TN = a.tile_tokens;
+  const int NB = gridDim.x, b = blockIdx.x;
+  const int R = dispatch_range(A, NB), blo = b * R, bhi = min(blo + R, A);
+  const int RW = R / NW, lo = min(blo + wave * RW, bhi), hi = min(lo + RW, bhi);
+  // Totals, and this block's first position per expert relative to the expert's segment.
+  int pre[2] = {0, 0};
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int e = tid + 256 * k;
+    if (e < E) {
+      int p = 0, t = 0;
+#pragma unroll 8
+      for (int bb = 0; bb < NB; ++bb) {
+        const int c = a.dcount[(size_t)bb * E + e];
+        p += bb < b ? c : 0;
+        t += c;
+      }
+      pre[k] = p;
+      s_tot[e] = t;
+      s_off[e] = t;
+    }
+  }
+  for (int e = tid; e < NW * kMaxExperts; e += 256) (&s_wc[0][0])[e] = 0;
+  __syncthreads();
+  block_exclusive_scan<NW>(s_off, E, s_wave);
+  const int nbits = E > 1 ? 32 - __clz(E - 1) : 1;
+  auto peers_of = [&](bool valid, int e) {
+    uint64_t peers = __ballot(valid);
+    for (int bb = 0; bb < nbits; ++bb) {
+      const uint64_t m = __ballot(valid && ((e >> bb) & 1));
+      peers &= ((e >> bb) & 1) ? m : ~m;
+    }
+    return peers;
+  };
+  constexpr int DCH = 8;
+  int ev[DCH];
+  auto load_ids = [&](int b0) {
+#pragma unroll
+    for (int k = 0; k < DCH; ++k) {
+      const int i = b0 + 64 * k + lane;
+      ev[k] = i < hi ? a.topk_idx[i] : 0;
+    }
+  };
+  // Pass 1: the wave's count per expert.
+  for (int b0 = lo; b0 < hi; b0 += 64 * DCH) {
+    load_ids(b0);
+#pragma unroll
+    for (int k = 0; k < DCH; ++k) {
+      const int base = b0 + 64 * k;
+      if (base >= hi) break;
+      const bool valid = base + lane < hi;
+      const int e = ev[k];
+      const uint64_t peers = peers_of(valid, e);
+      if (valid && __popcll(peers & ((1ull << lane) - 1ull)) == 0) s_wc[wave][e] += __popcll(peers);
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  __syncthreads();
+  // Each wave's first position per expert: segment offset + earlier blocks + earlier waves.
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int e = tid + 256 * k;
+    if (e < E) {
+      int run = s_off[e] + pre[k];
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const int c = s_wc[w][e];
+        s_wc[w][e] = run;
+        run += c;
+      }
+    }
+  }
+  __syncthreads();
+  // Pass 2: positions.
+  for (int b0 = lo; b0 < hi; b0 += 64 * DCH) {
+    load_ids(b0);
+#pragma unroll
+    for (int k = 0; k < DCH; ++k) {
+      const int base = b0 + 64 * k;
+      if (base >= hi) break;
+      const int i = base + lane;
+      const bool valid = i < hi;
+      const int e = ev[k];
+      const uint64_t peers = peers_of(valid, e);
+      const int rank = __popcll(peers & ((1ull << lane) - 1ull));
+      if (valid) {
+        const int t = i / K, r = i - t * K;
+        a.order[s_wc[wave][e] + rank] = t * a.slots + r;
+      }
+      __builtin_amdgcn_wave_barrier();
+      if (valid && rank == 0) s_wc[wave][e] += __popcll(peers);
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  // Work items (expert, first position, tokens) in ascending expert order; this block writes the
+  // items of the experts e ≡ b (mod NB).
+  for (int e = tid; e < E; e += 256) s_tiles[e] = (s_tot[e] + TN - 1) / TN;
+  __syncthreads();
+  const int routed_tiles = block_exclusive_scan<NW>(s_tiles, E, s_wave);
+  for (int e = b + NB * tid; e < E; e += NB * 256) {
+    const int n = s_tot[e];
+    for (int j = 0; j * TN < n; ++j) a.work[s_tiles[e] + j] = make_int4(e, s_off[e] + j * TN, min(TN, n - j * TN), 0);
+  }
+  if (a.work_half) {
+    const int TH = TN / 2;
+    __syncthreads();   // s_tiles was read above
+    for (int e = tid; e < E; e += 256) s_tiles[e] = (s_tot[e] + TH - 1) / TH;
+    __syncthreads();
+    const int half_tiles = block_exclusive_scan<NW>(s_tiles, E, s_wave);
+    for (int e = b + NB * tid; e < E; e += NB * 256) {
+      const int n = s_tot[e];
+      for (int j = 0; j * TH < n; ++j)
+        a.work_half[s_tiles[e] + j] = make_int4(e, s_off[e] + j * TH, min(TH, n - j * TH), 0);
+    }
+    if (b == 0 && tid == 0) *a.n_work_half = half_tiles;
+  }
+  int nwork = routed_tiles;
+  if (a.shared_gate) {
+    // The shared expert is expert id E over every token, after the routed positions.
+    for (int t = b * 256 + tid; t < T; t += NB * 256) a.order[A + t] = t * a.slots + K;
+    const int st = (T + TN - 1) / TN;
+    for (int j = b * 256 + tid; j < st; j += NB * 256)
+      a.work[routed_tiles + j] = make_int4(E, A + j * TN, min(TN, T - j * TN), 0);
+    nwork += st;
+    if (b == 0 && tid == 0) { a.seg[E] = A; a.seg[E + 1] = A + T; }
+  } else if (b == 0 && tid == 0) {
+    a.seg[E] = A;
+    a.seg[E + 1] = A;
+  }
+  if (b == 0) {
+    for (int e = tid; e < E; e += 256) a.seg[e] = s_off[e];
+    if (tid == 0) *a.n_work = nwork;
+  }
+}
+
 constexpr int RT_TOK = 16;          // tokens per route workgroup
 constexpr int RT_MAXCAND = 64;      // exact-recompute candidates handled per pass
 
@@ -913,6 +1086,22 @@ __global__ __launch_bounds__(256) void select_lg64_kernel(RouteArgs a) {
   finish_token(a, t, tk, a.shared_gate ? lg[a.experts] : 0.0);
 }
 
+// The dispatch of a batch's top-k table: one workgroup up to DB_MIN_ASSIGN assignments (or
+// without a count buffer), else the two multi-block launches.
+static hipError_t launch_dispatch(const RouteArgs &a, hipStream_t s, hipEvent_t stop) {
+  const int A = a.tokens * a.top_k;
+  if (A < DB_MIN_ASSIGN || !a.dcount) {
+    hipExtLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, nullptr, stop, 0, a);
+    return hipGetLastError();
+  }
+  const int nb = dispatch_blocks(A);
+  hipExtLaunchKernelGGL(dispatch_count_kernel, dim3(nb), dim3(256), 0, s, nullptr, nullptr, 0, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipExtLaunchKernelGGL(dispatch_scatter_kernel, dim3(nb), dim3(256), 0, s, nullptr, stop, 0, a);
+  return hipGetLastError();
+}
+
 // The MLX-router sequence: exact logits, x terms (MXFP4 layers), selection (unless the layer's
 // decode gate-up kernel selects), dispatch (layers above 16 tokens).
 hipError_t launch_route_mlx(const RouteArgs &a, hipStream_t s, Timing tm) {
@@ -944,8 +1133,7 @@ hipError_t launch_route_mlx(const RouteArgs &a, hipStream_t s, Timing tm) {
   hipExtLaunchKernelGGL(select_lg64_kernel, dim3((a.tokens + 3) / 4), dim3(256), 0, s, nullptr,
                         disp ? nullptr : tm.stop, 0, a);
   if ((e = hipGetLastError()) != hipSuccess || !disp) return e;
-  hipExtLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, nullptr, tm.stop, 0, a);
-  return hipGetLastError();
+  return launch_dispatch(a, s, tm.stop);
 }
 }  // namespace hh
 
@@ -995,12 +1183,8 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s, Timing tm) {
                         third ? nullptr : tm.stop, 0, a);
   e = hipGetLastError();
   if (e != hipSuccess || !third) return e;
-  hipExtLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, nullptr, tm.stop, 0, a);
-  return hipGetLastError();
+  return launch_dispatch(a, s, tm.stop);
 }
 // Stand-alone permutation of a given top-k table (hh_permute).
-hipError_t launch_permute(const RouteArgs &a, hipStream_t s) {
-  hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, a);
-  return hipGetLastError();
-}
+hipError_t launch_permute(const RouteArgs &a, hipStream_t s) { return launch_dispatch(a, s, nullptr); }
 }  // namespace hh
