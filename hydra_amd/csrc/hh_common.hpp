@@ -9,8 +9,15 @@ namespace hh {
 enum Quant { Q_MXFP4 = 0, Q_MLX4 = 1, Q_MLX8 = 2, Q_BF16 = 3 };
 enum Act { A_SWIGLU_OAI = 0, A_SILU = 1, A_GELU_TANH = 2 };
 // Multi-block dispatch (hh_route.hip): at most DB_MAX blocks, taken from DB_MIN_ASSIGN (token, rank)
-// assignments on; the count buffer holds DB_MAX · E words.
-constexpr int DB_MAX = 64, DB_MIN_ASSIGN = 4096;
+// assignments on; the count buffer holds DB_MAX · E words [block][expert]. In the layer the
+// router-logits launch zeroes it and the selection adds each assignment's count (finish_token).
+constexpr int DB_MAX = 64, DB_MIN_ASSIGN = 1024;
+__host__ __device__ inline int dispatch_blocks(int A) {
+  const int nb = (A + 255) / 256;
+  return nb < 1 ? 1 : (nb > DB_MAX ? DB_MAX : nb);
+}
+// Assignments per block: whole 256-assignment groups (4 waves × 64).
+__host__ __device__ inline int dispatch_range(int A, int nb) { return (((A + nb - 1) / nb) + 255) & ~255; }
 
 enum Router { R_TOPK_SOFTMAX = 0, R_SOFTMAX_TOPK_RENORM = 1, R_GEMMA = 2 };
 

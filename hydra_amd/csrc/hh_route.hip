@@ -216,12 +216,6 @@ __device__ __forceinline__ void dispatch_batch(const RouteArgs &a, const int32_t
 // e ≡ block (mod blocks); block 0 writes the segment table and the item counts. A single
 // 1024-thread workgroup was bound by its compute unit's issue rate (≈ 80 instructions per 64
 // assignments per pass on 16 waves sharing 4 SIMDs).
-__host__ __device__ inline int dispatch_blocks(int A) {
-  const int nb = (A + 255) / 256;
-  return nb < 1 ? 1 : (nb > DB_MAX ? DB_MAX : nb);
-}
-// Assignments per block: whole 256-assignment groups (4 waves × 64).
-__host__ __device__ inline int dispatch_range(int A, int nb) { return (((A + nb - 1) / nb) + 255) & ~255; }
 
 __global__ __launch_bounds__(256) void dispatch_count_kernel(RouteArgs a) {
   warm_kernargs<sizeof(RouteArgs)>();
@@ -254,12 +248,14 @@ __global__ __launch_bounds__(256) void dispatch_scatter_kernel(RouteArgs a) {
   for (int k = 0; k < 2; ++k) {
     const int e = tid + 256 * k;
     if (e < E) {
+      int c[DB_MAX];   // every block's count in one round of loads
+#pragma unroll
+      for (int bb = 0; bb < DB_MAX; ++bb) c[bb] = bb < NB ? a.dcount[(size_t)bb * E + e] : 0;
       int p = 0, t = 0;
-#pragma unroll 8
-      for (int bb = 0; bb < NB; ++bb) {
-        const int c = a.dcount[(size_t)bb * E + e];
-        p += bb < b ? c : 0;
-        t += c;
+#pragma unroll
+      for (int bb = 0; bb < DB_MAX; ++bb) {
+        p += bb < b ? c[bb] : 0;
+        t += c[bb];
       }
       pre[k] = p;
       s_tot[e] = t;
@@ -626,9 +622,18 @@ __device__ __forceinline__ int quant_x_waves(const RouteArgs &a) {
 // lg32 [T][E] and, from the first token tile, ‖w_e‖. Workgroups past the tiles quantise x
 // (MXFP4 layers), one wave per 16 blocks of a token.
 constexpr int RLW = 4, RLB = 2;
+// Zeroes the multi-block dispatch's count buffer (the selection launch that follows adds to it);
+// every workgroup of the calling launch takes a slice.
+__device__ __forceinline__ void zero_dispatch_counts(const RouteArgs &a) {
+  if (!a.dcount || !a.want_dispatch) return;
+  const int n = DB_MAX * a.experts;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) a.dcount[i] = 0;
+}
+
 template <bool gemma>
 __global__ __launch_bounds__(64 * RLW) void route_logits_kernel(RouteArgs a) {
   warm_kernargs<sizeof(RouteArgs)>();
+  zero_dispatch_counts(a);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, l16 = lane & 15;
   const int E = a.experts, T = a.tokens;
@@ -981,6 +986,7 @@ constexpr int MLX_RT_R = 2;       // rows per wave above 16 tokens
 template <int BITS, int R, int J>
 __global__ __launch_bounds__(256) void mlx_router_logits_kernel(RouteArgs a) {
   warm_kernargs<sizeof(RouteArgs)>();
+  zero_dispatch_counts(a);
   constexpr int NC = 128 / BITS, XV = NC / 8, P = 4;
   static_assert(R * P == 4 || R * P == 8 || R * P == 16, "the reduce-scatter's lane mapping");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1086,18 +1092,21 @@ __global__ __launch_bounds__(256) void select_lg64_kernel(RouteArgs a) {
   finish_token(a, t, tk, a.shared_gate ? lg[a.experts] : 0.0);
 }
 
-// The dispatch of a batch's top-k table: one workgroup up to DB_MIN_ASSIGN assignments (or
-// without a count buffer), else the two multi-block launches.
-static hipError_t launch_dispatch(const RouteArgs &a, hipStream_t s, hipEvent_t stop) {
+// The dispatch of a batch's top-k table: one workgroup below DB_MIN_ASSIGN assignments (or
+// without a count buffer), else the multi-block scatter, after dispatch_count_kernel unless the
+// selection already counted (`counted`).
+static hipError_t launch_dispatch(const RouteArgs &a, hipStream_t s, hipEvent_t stop, bool counted) {
   const int A = a.tokens * a.top_k;
   if (A < DB_MIN_ASSIGN || !a.dcount) {
     hipExtLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(1024), 0, s, nullptr, stop, 0, a);
     return hipGetLastError();
   }
   const int nb = dispatch_blocks(A);
-  hipExtLaunchKernelGGL(dispatch_count_kernel, dim3(nb), dim3(256), 0, s, nullptr, nullptr, 0, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  hipError_t e;
+  if (!counted) {
+    hipExtLaunchKernelGGL(dispatch_count_kernel, dim3(nb), dim3(256), 0, s, nullptr, nullptr, 0, a);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
   hipExtLaunchKernelGGL(dispatch_scatter_kernel, dim3(nb), dim3(256), 0, s, nullptr, stop, 0, a);
   return hipGetLastError();
 }
@@ -1133,7 +1142,7 @@ hipError_t launch_route_mlx(const RouteArgs &a, hipStream_t s, Timing tm) {
   hipExtLaunchKernelGGL(select_lg64_kernel, dim3((a.tokens + 3) / 4), dim3(256), 0, s, nullptr,
                         disp ? nullptr : tm.stop, 0, a);
   if ((e = hipGetLastError()) != hipSuccess || !disp) return e;
-  return launch_dispatch(a, s, tm.stop);
+  return launch_dispatch(a, s, tm.stop, true);
 }
 }  // namespace hh
 
@@ -1183,8 +1192,8 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s, Timing tm) {
                         third ? nullptr : tm.stop, 0, a);
   e = hipGetLastError();
   if (e != hipSuccess || !third) return e;
-  return launch_dispatch(a, s, tm.stop);
+  return launch_dispatch(a, s, tm.stop, true);
 }
 // Stand-alone permutation of a given top-k table (hh_permute).
-hipError_t launch_permute(const RouteArgs &a, hipStream_t s) { return launch_dispatch(a, s, nullptr); }
+hipError_t launch_permute(const RouteArgs &a, hipStream_t s) { return launch_dispatch(a, s, nullptr, false); }
 }  // namespace hh

@@ -349,6 +349,11 @@ __device__ __forceinline__ void finish_token(const RouteArgs &a, int t, const To
     if (a.topk_w) a.topk_w[(size_t)t * K + lane] = (float)w;
     a.slot_w[(size_t)t * a.slots + lane] = (float)w;
     if (a.logits) a.logits[(size_t)t * K + lane] = v;
+    if (a.dcount && a.want_dispatch) {
+      // the multi-block dispatch's count of this assignment's block (integer adds: any order)
+      const int A = a.tokens * K, i = t * K + lane;
+      atomicAdd(&a.dcount[(size_t)(i / dispatch_range(A, dispatch_blocks(A))) * a.experts + e], 1);
+    }
   }
   if (a.shared_gate && lane == 0) {
     // σ of the shared gate row, applied to the shared expert's output
