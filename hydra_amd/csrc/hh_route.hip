@@ -463,7 +463,7 @@ struct TokenScreen {
 // every wave); the 64-lane ranking splits over them through s_rk [NW][64].
 template <bool gemma, int NW = 1, class LG, class WN>
 __device__ __forceinline__ TokenScreen screen_token(const RouteArgs &a, int t, LG lgf, WN wnf, int *cl,
-                                                    int (*s_rk)[64] = nullptr) {
+                                                    int (*s_rk)[64] = nullptr, double coef = -1.0) {
   const int lane = threadIdx.x & 63;
   const int E = a.experts, H = a.hidden, K = a.top_k;
   const uint16_t *xr = a.xr + (size_t)t * H;
@@ -503,8 +503,9 @@ __device__ __forceinline__ TokenScreen screen_token(const RouteArgs &a, int t, L
   TokenScreen ts;
   ts.norm = gemma ? pow(xx / (double)H + (double)a.eps, -0.5) : 1.0;
   const double fscale = gemma ? ts.norm * pow((double)H, -0.5) : 1.0;   // logit = fscale·Σu·w
-  // |fp32 − exact| ≤ fscale·(2·H·2^-23·‖u‖‖w‖) + 2^-22·|logit| (bias add, final scaling).
-  const float cb = (float)(fscale * 2.0 * H * 1.1920928955078125e-07 * sqrt(uu));
+  // |fp32 − exact| ≤ fscale·(2·H·2^-23·‖u‖‖w‖) + 2^-22·|logit| (bias add, final scaling); a
+  // screen with another bound passes its coefficient of ‖u‖·wnf(e) (`coef`).
+  const float cb = (float)(fscale * (coef > 0.0 ? coef : 2.0 * H * 1.1920928955078125e-07) * sqrt(uu));
   float lb[8], ub[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -983,22 +984,18 @@ __device__ __forceinline__ uint32_t mlx_code(const u32x4 &q, int s) {
 constexpr int MLX_RT_TILE = 16;   // tokens per wave above 16 tokens
 constexpr int MLX_RT_R = 2;       // rows per wave above 16 tokens
 
-template <int BITS, int R, int J>
-__global__ __launch_bounds__(256) void mlx_router_logits_kernel(RouteArgs a) {
-  warm_kernargs<sizeof(RouteArgs)>();
-  zero_dispatch_counts(a);
-  constexpr int NC = 128 / BITS, XV = NC / 8, P = 4;
-  static_assert(R * P == 4 || R * P == 8 || R * P == 16, "the reduce-scatter's lane mapping");
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// The fp64 logits of rows row_of(0) .. row_of(R−1) (row E: the shared gate) for tokens t0 .. t1−1,
+// one wave, in the arithmetic above: lane l's code vectors l, l + 64, ... (J per lane, zero past
+// the row) summed column by column in fp64, the R·P wave sums of each P-token group on one
+// reduce-scatter butterfly, plus the router bias. `out(v, r, token)` is called by one lane per
+// total, for r < nr and tokens < t1 only. A (token, row) value does not depend on R, P, t0, t1,
+// the other rows or the token's place in its group.
+template <int BITS, int R, int J, int P, class RowOf, class Out>
+__device__ __forceinline__ void mlx_rows_logits(const RouteArgs &a, RowOf row_of, int nr, int t0, int t1, Out out) {
+  constexpr int NC = 128 / BITS, XV = NC / 8;
+  static_assert(R * P == 1 || R * P == 4 || R * P == 8 || R * P == 16, "the reduce-scatter's lane mapping");
+  const int lane = threadIdx.x & 63;
   const int E = a.experts, H = a.hidden, T = a.tokens;
-  const int rows = E + (a.shared_gate ? 1 : 0);
-  const int waves_per_tile = (rows + R - 1) / R, blocks_per_tile = (waves_per_tile + 3) / 4;
-  const int tile = blockIdx.x / blocks_per_tile;
-  const int wid = (blockIdx.x - tile * blocks_per_tile) * 4 + wave;
-  if (wid >= waves_per_tile) return;   // no barriers below
-  const int r0 = wid * R;
-  const int tsz = T <= RT_TOK ? T : MLX_RT_TILE;
-  const int t0 = tile * tsz, t1 = min(T, t0 + tsz);
   const int V = H / NC, wpr = H * BITS / 32, gpr = H / 64;
   // The rows' code vectors and group (scale, bias) of this lane, once: vectors past the row
   // (J·64 > V) are zero codes with zero scale and bias, adding exactly nothing.
@@ -1006,7 +1003,7 @@ __global__ __launch_bounds__(256) void mlx_router_logits_kernel(RouteArgs a) {
   double sc[R][J], bi[R][J];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int row = min(r0 + r, rows - 1);
+    const int row = row_of(r);
     const bool sg = row == E;
     const uint32_t *qr = sg ? a.sg_words : a.rq_words + (size_t)row * wpr;
     const uint16_t *sr = sg ? a.sg_scales : a.rq_scales + (size_t)row * gpr;
@@ -1052,18 +1049,175 @@ __global__ __launch_bounds__(256) void mlx_router_logits_kernel(RouteArgs a) {
           for (int p = 0; p < P; ++p) acc[r][p] = fma(w, x[p], acc[r][p]);
         }
       }
-    // all R·P sums at once; lane l ends with the total of acc index l >> (6 − log2(R·P))
-    constexpr int N = R * P, SH = N == 4 ? 4 : N == 8 ? 3 : 2;
+    // all R·P sums at once; lane l ends with the total of acc index l >> (6 − log2(R·P)) (one
+    // sum: the plain butterfly, the same additions)
+    constexpr int N = R * P, SH = N == 1 ? 6 : N == 4 ? 4 : N == 8 ? 3 : 2;
     double flat[N];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int p = 0; p < P; ++p) flat[r * P + p] = acc[r][p];
-    double v = wave_sum_scatter_f64<N>(flat);
-    const int i = lane >> SH, row = r0 + i / P, tp = t + i % P;
+    double v;
+    if constexpr (N == 1) v = wave_sum_f64(flat[0]);
+    else v = wave_sum_scatter_f64<N>(flat);
+    const int i = lane >> SH, r = i / P, tp = t + i % P;
+    const int row = row_of(min(r, R - 1));
     if (row < E && a.router_b) v += (double)bf16_bits_to_f32(a.router_b[row]);
-    if ((lane & ((1 << SH) - 1)) == 0 && row < rows && tp < t1) a.lg64[(size_t)tp * (E + 1) + row] = v;
+    if ((lane & ((1 << SH) - 1)) == 0 && r < nr && tp < t1) out(v, r, tp);
   }
+}
+
+template <int BITS, int R, int J>
+__global__ __launch_bounds__(256) void mlx_router_logits_kernel(RouteArgs a) {
+  warm_kernargs<sizeof(RouteArgs)>();
+  zero_dispatch_counts(a);
+  const int wave = threadIdx.x >> 6;
+  const int E = a.experts, T = a.tokens;
+  const int rows = E + (a.shared_gate ? 1 : 0);
+  const int waves_per_tile = (rows + R - 1) / R, blocks_per_tile = (waves_per_tile + 3) / 4;
+  const int tile = blockIdx.x / blocks_per_tile;
+  const int wid = (blockIdx.x - tile * blocks_per_tile) * 4 + wave;
+  if (wid >= waves_per_tile) return;   // no barriers below
+  const int tsz = T <= RT_TOK ? T : MLX_RT_TILE;
+  const int t0 = tile * tsz, t1 = min(T, t0 + tsz);
+  const int r0 = wid * R;
+  mlx_rows_logits<BITS, R, J, 4>(a, [&](int r) { return min(r0 + r, rows - 1); }, rows - r0, t0, t1,
+                                 [&](double v, int r, int tp) { a.lg64[(size_t)tp * (E + 1) + r0 + r] = v; });
+}
+
+// ---- MLX-affine router above 16 tokens: screen on the MFMA, exact logits of the candidates ----
+// Screening logit of (token t, row e) on the bf16 MFMA: per 64-column group g, P_g = Σ q·x (codes
+// ≤ 255 are exact in bf16, each q·x exact in fp32; the MFMA adds 64 of them in fp32) and
+// X_g = Σ x (fp32), then l += s_g·P_g + b_g·X_g in fp32. Against the exact Σ (q·s + b)·x:
+// |l − exact| ≤ (63 + 2 + 1 + NG)·u·Σ_c (|s|·q + |b|)·|x| + O(u²) ≤ kMlxScreenCoef·‖v_e‖·‖x_t‖ with
+// v_c = |s_g|·q_c + |b_g|, u = 2^-24, NG ≤ 64 groups: the coefficient 256·u is twice that
+// (rounding modes aside). Each workgroup takes a 16-token × 16-row tile, its 4 waves the groups
+// g ≡ wave (mod 4); in a group, lane group gg supplies columns 16gg .. 16gg+15 (both MFMAs of the
+// group, A and B alike, so any column order is the same sum's terms). The first token tile also
+// writes ‖v_e‖ (rounded up) to wn. Selection then recomputes the candidates exactly
+// (mlx_select_kernel), so the screen's order of additions does not matter.
+constexpr double kMlxScreenCoef = 256.0 * 5.9604644775390625e-08;
+constexpr int MLX_SG_MAX = 64;   // groups per row (H ≤ 4096)
+template <int BITS>
+__global__ __launch_bounds__(256) void mlx_screen_kernel(RouteArgs a) {
+  warm_kernargs<sizeof(RouteArgs)>();
+  zero_dispatch_counts(a);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, gg = lane >> 4, l16 = lane & 15;
+  const int E = a.experts, H = a.hidden, T = a.tokens, NG = H / 64;
+  const int etiles = (E + 15) / 16;
+  const int tt = blockIdx.x / etiles, et = blockIdx.x - tt * etiles;
+  const int t0 = tt * 16, e0 = et * 16;
+  const int ntok = min(16, T - t0);
+  __shared__ float2 s_sb[16][MLX_SG_MAX];   // (scale, bias) of the tile's rows; rows past E: 0
+  __shared__ float s_part[4][16][16];        // [wave][row][token]
+  __shared__ float s_wn[4][16];
+  for (int i = tid; i < 16 * NG; i += 256) {
+    const int r = i / NG, g = i - r * NG, e = e0 + r;
+    float2 v = {0.f, 0.f};
+    if (e < E) v = {bf16_bits_to_f32(a.rq_scales[(size_t)e * NG + g]), bf16_bits_to_f32(a.rq_biases[(size_t)e * NG + g])};
+    s_sb[r][g] = v;
+  }
+  __syncthreads();
+  const int row = min(e0 + l16, E - 1);
+  const bool row_ok = e0 + l16 < E;
+  const uint16_t *xr = a.xr + (size_t)(t0 + min(l16, ntok - 1)) * H;
+  const uint8_t *qrow = (const uint8_t *)a.rq_words + (size_t)row * (H * BITS / 8);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float vv = 0.f;   // Σ v² of this lane's columns of row l16 (first token tile)
+  for (int g = wave; g < NG; g += 4) {
+    const int c = 64 * g + 16 * gg;
+    // 16 codes of row l16, as two bf16x8 A operands
+    u32x4 qv;
+    if constexpr (BITS == 8) {
+      qv = *(const u32x4 *)(qrow + c);
+    } else {
+      const u32x2 q = *(const u32x2 *)(qrow + c / 2);
+      qv = u32x4{q[0], q[1], 0u, 0u};
+    }
+    u32x4 a0, a1;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const uint32_t c0 = mlx_code<BITS>(qv, 2 * kk), c1 = mlx_code<BITS>(qv, 2 * kk + 1);
+      const uint32_t lo = f32_to_bf16_bits((float)(row_ok ? c0 : 0u)), hi = f32_to_bf16_bits((float)(row_ok ? c1 : 0u));
+      const uint32_t pk = lo | (hi << 16);
+      if (kk < 4) a0[kk] = pk; else a1[kk - 4] = pk;
+      if (tt == 0) {
+        const float2 sbv = s_sb[l16][g];
+        const float v0 = fabsf(sbv.x) * (float)c0 + fabsf(sbv.y), v1 = fabsf(sbv.x) * (float)c1 + fabsf(sbv.y);
+        vv = fmaf(v0, v0, fmaf(v1, v1, vv));
+      }
+    }
+    const u32x4 b0 = *(const u32x4 *)(xr + c), b1 = *(const u32x4 *)(xr + c + 8);
+    f32x4 p = {0.f, 0.f, 0.f, 0.f};
+    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a0), as_bf16x8(b0), p, 0, 0, 0);
+    p = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a1), as_bf16x8(b1), p, 0, 0, 0);
+    // Σx of the group for token l16: this lane's 16 columns, then the 4 lane groups
+    float xs = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xs += (bf_lo(b0[q]) + bf_hi(b0[q])) + (bf_lo(b1[q]) + bf_hi(b1[q]));
+    xs += __shfl_xor(xs, 16);
+    xs += __shfl_xor(xs, 32);
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const float2 sbv = s_sb[4 * gg + ii][g];
+      acc[ii] += fmaf(sbv.x, p[ii], sbv.y * xs);
+    }
+  }
+#pragma unroll
+  for (int ii = 0; ii < 4; ++ii) s_part[wave][4 * gg + ii][l16] = acc[ii];
+  if (tt == 0) {
+    vv += __shfl_xor(vv, 16);
+    vv += __shfl_xor(vv, 32);
+    if (gg == 0) s_wn[wave][l16] = vv;
+  }
+  __syncthreads();
+  const int er = tid >> 4, tk = tid & 15, e = e0 + er;
+  if (e < E && tk < ntok) {
+    float v = (s_part[0][er][tk] + s_part[1][er][tk]) + (s_part[2][er][tk] + s_part[3][er][tk]);
+    if (a.router_b) v += bf16_bits_to_f32(a.router_b[e]);
+    a.lg32[(size_t)(t0 + tk) * E + e] = v;
+    // ‖v_e‖, rounded up: the fp32 sums of squares are within a few hundred ulps
+    if (tt == 0 && tk == 0)
+      a.wn[e] = sqrtf((s_wn[0][er] + s_wn[1][er]) + (s_wn[2][er] + s_wn[3][er])) * 1.0001f + 1e-30f;
+  }
+}
+
+// One workgroup per token: the 4 waves screen it (screen_token with the MLX screen's bound), then
+// wave w computes the exact logits of candidates w, w + 4, ... with mlx_rows_logits (the decode
+// router's values, bit for bit) and wave 1 the shared gate's; wave 0 ranks them and writes the
+// token's routing (as route_select_kernel).
+template <int BITS, int J>
+__global__ __launch_bounds__(256) void mlx_select_kernel(RouteArgs a) {
+  warm_kernargs<sizeof(RouteArgs)>();
+  const int wave = threadIdx.x >> 6;
+  const int t = blockIdx.x, E = a.experts;
+  __shared__ int s_cl[4][kMaxExperts];
+  __shared__ int s_rk[4][64];
+  __shared__ double s_v[kMaxExperts];
+  __shared__ double s_sg;
+  const float *lg = a.lg32 + (size_t)t * E;
+  const TokenScreen ts = screen_token<false, 4>(a, t, [&](int e) { return lg[e]; }, [&](int e) { return a.wn[e]; },
+                                                s_cl[wave], s_rk, kMlxScreenCoef);
+  // wave w: candidates w, w + 4, ... (one row of the one token per pass); wave 1 also the
+  // shared gate's row
+  const int *cl = s_cl[wave];
+  for (int c0 = wave; c0 < ts.nc; c0 += 4)
+    mlx_rows_logits<BITS, 1, J, 1>(a, [&](int) { return cl[c0]; }, 1, t, t + 1, [&](double v, int, int) { s_v[c0] = v; });
+  if (wave == 1 && a.shared_gate)
+    mlx_rows_logits<BITS, 1, J, 1>(a, [&](int) { return E; }, 1, t, t + 1, [&](double v, int, int) { s_sg = v; });
+  __syncthreads();
+  if (wave != 0) return;
+  TopK tk;
+  for (int c = 0; c < ts.nc; ++c) tk.insert(s_v[c], s_cl[0][c], a.top_k);
+  prob_order(tk, a.top_k, a.router);
+  finish_token(a, t, tk, a.shared_gate ? s_sg : 0.0);
+}
+template <int BITS> void *mlx_select_fn(int H) {
+  const int J = (H / (128 / BITS) + 63) / 64;
+  if (J <= 1) return (void *)mlx_select_kernel<BITS, 1>;
+  if (J <= 2) return (void *)mlx_select_kernel<BITS, 2>;
+  if (J <= 4) return (void *)mlx_select_kernel<BITS, 4>;
+  return nullptr;
 }
 
 // The launch of mlx_router_logits_kernel for a row of H columns (J = vectors per lane).
@@ -1116,6 +1270,25 @@ static hipError_t launch_dispatch(const RouteArgs &a, hipStream_t s, hipEvent_t 
 hipError_t launch_route_mlx(const RouteArgs &a, hipStream_t s, Timing tm) {
   const int rows = a.experts + (a.shared_gate ? 1 : 0);
   const bool small = a.tokens <= RT_TOK;
+  if (!small && a.hidden % 64 == 0 && a.hidden <= 64 * MLX_SG_MAX) {
+    // screen on the MFMA, then the candidates' exact logits
+    const bool disp = a.want_dispatch != 0;
+    void *screen = a.router_bits == 8 ? (void *)mlx_screen_kernel<8> : (void *)mlx_screen_kernel<4>;
+    void *select = a.router_bits == 8 ? mlx_select_fn<8>(a.hidden) : mlx_select_fn<4>(a.hidden);
+    if (!select) return hipErrorInvalidValue;
+    void *args[] = {(void *)&a};
+    const int blocks = ((a.tokens + 15) / 16) * ((a.experts + 15) / 16);
+    hipError_t e = hipExtLaunchKernel(screen, dim3(blocks), dim3(256), args, 0, s, tm.start, nullptr, 0);
+    if (e != hipSuccess) return e;
+    if (a.xq) {
+      const int qw = a.tokens * ((a.hidden / 32 + 15) / 16);
+      hipExtLaunchKernelGGL(quant_x_kernel, dim3((qw + 3) / 4), dim3(256), 0, s, nullptr, nullptr, 0, a);
+      if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
+    e = hipExtLaunchKernel(select, dim3(a.tokens), dim3(256), args, 0, s, nullptr, disp ? nullptr : tm.stop, 0);
+    if (e != hipSuccess || !disp) return e;
+    return launch_dispatch(a, s, tm.stop, true);
+  }
   const int R = small ? 1 : MLX_RT_R;
   const int blocks = (small ? 1 : (a.tokens + MLX_RT_TILE - 1) / MLX_RT_TILE) * (((rows + R - 1) / R + 3) / 4);
   const bool sel = !small || a.want_dispatch == 0;
