@@ -724,7 +724,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(gemma ? 4 :
   TopK tk;
   for (int c = 0; c < ts.nc; ++c) tk.insert(s_v[c], s_cl[0][c], a.top_k);
   prob_order(tk, a.top_k, a.router);
-  finish_token(a, t, tk, a.shared_gate ? s_sg : 0.0);
+  finish_token<true>(a, t, tk, a.shared_gate ? s_sg : 0.0);
 }
 
 // C.
@@ -1210,7 +1210,7 @@ __global__ __launch_bounds__(256) void mlx_select_kernel(RouteArgs a) {
   TopK tk;
   for (int c = 0; c < ts.nc; ++c) tk.insert(s_v[c], s_cl[0][c], a.top_k);
   prob_order(tk, a.top_k, a.router);
-  finish_token(a, t, tk, a.shared_gate ? s_sg : 0.0);
+  finish_token<true>(a, t, tk, a.shared_gate ? s_sg : 0.0);
 }
 template <int BITS> void *mlx_select_fn(int H) {
   const int J = (H / (128 / BITS) + 63) / 64;
@@ -1243,7 +1243,7 @@ __global__ __launch_bounds__(256) void select_lg64_kernel(RouteArgs a) {
   const double *lg = a.lg64 + (size_t)t * (a.experts + 1);
   TopK tk = topk_fast(lg, a.experts, a.top_k, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave]);
   prob_order(tk, a.top_k, a.router);
-  finish_token(a, t, tk, a.shared_gate ? lg[a.experts] : 0.0);
+  finish_token<true>(a, t, tk, a.shared_gate ? lg[a.experts] : 0.0);
 }
 
 // The dispatch of a batch's top-k table: one workgroup below DB_MIN_ASSIGN assignments (or

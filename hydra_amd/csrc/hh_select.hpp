@@ -339,6 +339,9 @@ __device__ __forceinline__ double token_weight(const RouteArgs &a, const TopK &t
 
 // Weights of one token's selection (whole wave; lane r < K handles rank r). Writes
 // topk_idx/topk_w/slot_w (and logits, shared_w when given).
+// COUNT (the selection kernels above 16 tokens): also add each assignment to the multi-block
+// dispatch's count of its block (the decode kernels leave it out, which keeps their code as it is).
+template <bool COUNT = false>
 __device__ __forceinline__ void finish_token(const RouteArgs &a, int t, const TopK &tk, double sg_logit) {
   const int K = a.top_k, lane = threadIdx.x & 63;
   double v;
@@ -349,7 +352,7 @@ __device__ __forceinline__ void finish_token(const RouteArgs &a, int t, const To
     if (a.topk_w) a.topk_w[(size_t)t * K + lane] = (float)w;
     a.slot_w[(size_t)t * a.slots + lane] = (float)w;
     if (a.logits) a.logits[(size_t)t * K + lane] = v;
-    if (a.dcount && a.want_dispatch) {
+    if (COUNT && a.dcount && a.want_dispatch) {
       // the multi-block dispatch's count of this assignment's block (integer adds: any order)
       const int A = a.tokens * K, i = t * K + lane;
       atomicAdd(&a.dcount[(size_t)(i / dispatch_range(A, dispatch_blocks(A))) * a.experts + e], 1);

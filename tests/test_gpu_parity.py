@@ -196,10 +196,12 @@ def test_permute_is_stable_grouping(torch_dev, ctx):
     torch = torch_dev
     say("permute")
     rng = np.random.default_rng(9)
-    # one workgroup below 4096 assignments; from 4096 on the multi-block dispatch (17 blocks with a
-    # partial last one, 64 blocks with empty trailing ones, 512 experts, a skewed load)
+    # one workgroup below 1024 assignments; from 1024 on the multi-block dispatch (exactly 1024 and
+    # one below it, 17 blocks with a partial last one, 64 blocks with empty trailing ones, 512
+    # experts, a skewed load)
     for T, K, E, skew in [(1, 4, 32, 0), (7, 2, 5, 0), (300, 8, 256, 0), (2048, 4, 128, 0),
-                          (1000, 8, 512, 0), (1031, 4, 7, 0), (8193, 2, 64, 0), (4096, 2, 300, 1.1)]:
+                          (1000, 8, 512, 0), (256, 4, 7, 0), (341, 3, 9, 0), (1031, 4, 7, 0),
+                          (8193, 2, 64, 0), (4096, 2, 300, 1.1)]:
         p = None
         if skew:
             p = 1.0 / np.arange(1, E + 1) ** skew
