@@ -183,13 +183,14 @@ def measure_decode(wl, T, steps, warmup, fused=False):
 def measure_stack(wl, T, layers, steps, warmup):
     """The MoE halves of a GPT-OSS-20B decode stack (24 layers) at T tokens through hh_runner:
     per layer the FFN block (RMSNorm, router, experts, residual) on one fp32 residual stream,
-    layer l on weight copy l % copies, no host synchronisation between layers; run eagerly and
-    as one captured HIP graph. Returns µs per layer of both."""
+    layer l on weight copy l % copies, no host synchronisation between layers; run eagerly (the
+    default decode structure, and three launches per block) and as one captured HIP graph (three
+    launches per block). Returns µs per layer of each."""
     from hydra_amd.layer import MoELayer, Runner
     torch = wl.torch
     dev = "cuda:0"
     desc = wl.desc
-    wl.ctx.decode_fused(0)
+    wl.ctx.decode_fused(0)   # capture takes the three-launch structure
     g = torch.Generator(device=dev).manual_seed(7)
     norm = {"pre_norm": (torch.rand(desc.hidden, device=dev, generator=g) + 0.5).bfloat16().view(torch.int16),
             "eps": 1e-5}
@@ -211,6 +212,9 @@ def measure_stack(wl, T, layers, steps, warmup):
         wl.ctx.synchronize()
         return (time.perf_counter() - t0) / steps
 
+    eager3 = timed(lambda: runner.forward(hidden))   # three launches per block, as the graph
+    hidden.copy_(base)
+    wl.ctx.decode_fused(-1)   # the default decode structure (two launches for one or two tokens)
     eager = timed(lambda: runner.forward(hidden))
     hidden.copy_(base)
     torch.cuda.synchronize()
@@ -218,8 +222,8 @@ def measure_stack(wl, T, layers, steps, warmup):
     replay = timed(graph.launch)
     graph.close()
     runner.close()
-    wl.ctx.decode_fused(-1)
     return {"T": T, "layers": layers, "eager_us_per_layer": eager / layers * 1e6,
+            "eager_three_launch_us_per_layer": eager3 / layers * 1e6,
             "graph_us_per_layer": replay / layers * 1e6, "graph_tokens_per_s": T / replay,
             "eager_tokens_per_s": T / eager,
             "what": "hh_runner FFN blocks (RMSNorm + MoE + residual) of 24 GPT-OSS-20B layers"}

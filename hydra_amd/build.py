@@ -18,7 +18,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libhydra_hip.so")
-SOURCES = ["hh_api.hip", "hh_route.hip", "hh_gemm.hip", "hh_ops.hip", "hh_attn.hip", "hh_block.hip", "hh_proj.hip"]
+SOURCES = ["hh_api.hip", "hh_route.hip", "hh_gemm.hip", "hh_gemm_block.hip", "hh_ops.hip", "hh_attn.hip", "hh_block.hip", "hh_proj.hip"]
 
 
 def hipcc() -> str:

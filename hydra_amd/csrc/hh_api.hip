@@ -541,8 +541,10 @@ int forward_layer(hh_ctx *ctx, const hh_moe_desc *d, const hh_moe_weights *w, co
   }
   // MXFP4 decode in two launches: the router runs as the first workgroups of the gate-up
   // launch (flags in the context's flag buffer; not under capture, whose graph would freeze the
-  // call's flag epoch, and not for the allocation-free entry, which owns no flag buffer).
-  const bool fr = T <= kSmallT && !noalloc && !resid && !ctx->capturing && w->router_bits == 0 &&
+  // call's flag epoch, and not for the allocation-free entry, which owns no flag buffer). In the
+  // FFN block (bin) those workgroups, and the gate-up workgroups' x terms, form x from the
+  // residual rows themselves.
+  const bool fr = T <= kSmallT && !noalloc && (!resid || bin) && !ctx->capturing && w->router_bits == 0 &&
                   decode_mode(ctx) == 2 && hh::fused_router_fits(d->quant, d->hidden, d->experts, d->router, T) &&
                   sizeof(uint32_t) * (size_t)hh::fused_router_flags(T, d->experts) <= kFlagBytes;
   if (fr) {

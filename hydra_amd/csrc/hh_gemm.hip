@@ -1269,6 +1269,62 @@ __device__ __forceinline__ void quant_x_lds(const uint16_t *x, int T, int H, int
   }
 }
 
+// quant_x_lds for the FFN block (ra.resid set, T ≤ 2): x = bf16(resid·f·norm_w) formed from the
+// residual rows as the block's norm kernel rounds it (f from row_sumsq, every wave for every
+// token), then quantised as quant_x_lds into the same LDS layout.
+__device__ __forceinline__ void quant_x_lds_block(const RouteArgs &ra, int T, int H, int xld, uint8_t *s_xb, int RS) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, l16 = lane & 15;
+  const int nb = H / 32, per_t = (nb + 15) / 16, nw = T * per_t;
+  double f[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+    if (t < T) f[t] = norm_factor(row_sumsq(ra.resid + (size_t)t * H, H), H, (double)ra.norm_eps, ra.norm_pow);
+  constexpr int QXB = 4;
+  for (int w0 = wave; w0 < nw; w0 += 4 * QXB) {
+    f32x4 xb[QXB][2];
+    u32x4 nv[QXB];
+#pragma unroll
+    for (int k = 0; k < QXB; ++k) {
+      const int w = min(w0 + 4 * k, nw - 1), t = w / per_t, bc = min(16 * (w - t * per_t) + l16, nb - 1);
+      const float *xr = ra.resid + (size_t)t * H + bc * 32 + 8 * g;
+      xb[k][0] = *(const f32x4 *)xr;
+      xb[k][1] = *(const f32x4 *)(xr + 4);
+      nv[k] = *(const u32x4 *)(ra.norm_w + bc * 32 + 8 * g);
+    }
+#pragma unroll
+    for (int k = 0; k < QXB; ++k) {
+      const int w = w0 + 4 * k;
+      if (w >= nw) break;
+      const int t = w / per_t, b = 16 * (w - t * per_t) + l16;
+      const double ft = t == 0 ? f[0] : f[1];
+      float v[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const float nf = bf16_bits_to_f32((nv[k][c >> 1] >> (16 * (c & 1))) & 0xFFFFu);
+        const float xv = c < 4 ? xb[k][0][c] : xb[k][1][c - 4];
+        v[c] = bf16_bits_to_f32(f64_to_bf16_bits((double)xv * ft * (double)nf));
+      }
+      uint32_t q[NTX][2], sb[NTX];
+      quant_block<NTX>(v, q, sb);
+      if (b < nb) {
+#pragma unroll
+        for (int j = 0; j < NTX; ++j) {
+          uint8_t *row = s_xb + (size_t)(t * NTX + j) * RS;
+          *(u32x2 *)(row + b * 32 + 8 * g) = u32x2{q[j][0], q[j][1]};
+          if (g == 0) row[xld + b] = (uint8_t)sb[j];
+        }
+      }
+    }
+  }
+  const int hp = (H + 127) & ~127, nz = (hp - H) / 16, ns = (hp - H) / 32;
+  for (int v = tid; v < T * NTX * (nz + ns); v += 256) {
+    const int rr = v / (nz + ns), k = v - rr * (nz + ns);
+    uint8_t *row = s_xb + (size_t)rr * RS;
+    if (k < nz) *(u32x4 *)(row + H + 16 * k) = u32x4{0u, 0u, 0u, 0u};
+    else row[xld + H / 32 + (k - nz)] = 127;
+  }
+}
+
 
 // Decode gate-up on the scaled MFMA, persistent: the grid holds about two workgroups per compute
 // unit; each selects the top-k of the batch once, lists the batch's distinct experts in LDS (in
@@ -1289,7 +1345,7 @@ __device__ __forceinline__ void quant_x_lds(const uint16_t *x, int T, int H, int
 // them from LDS. Router workgroups wait for nothing and have the smaller indices, which the
 // dispatcher starts first, so every wait is for workgroups that run. Waits are bounded (10 ms);
 // a workgroup that times out sets bit 0 of *f.status and stops.
-template <int DA, bool ONE, int XB, int NCH = 0, bool FR = false>
+template <int DA, bool ONE, int XB, int NCH = 0, int FR = 0>
 __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra, FuseArgs f) {
   warm_kernargs<sizeof(GemmArgs) + sizeof(RouteArgs) + sizeof(FuseArgs)>();
   constexpr int NM = 1;
@@ -1325,7 +1381,10 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra, 
       __shared__ double s_px[4][2][64];
       const int E1 = E + 1, t = (int)blockIdx.x / E1, e = (int)blockIdx.x - t * E1;
       double v = 0.0;
-      if (e < E || has_shared) v = split_pair_logit<false>(ra, t, e, s_acc, s_px);
+      if (e < E || has_shared) {
+        if constexpr (FR == 2) v = block_pair_logit(ra, t, e, s_acc);
+        else v = split_pair_logit<false>(ra, t, e, s_acc, s_px);
+      }
       if (wave == 0) store_logit_record(f.flags, f.R, (int)blockIdx.x, v, f.epoch, lane);
       HH_TR(1, 1);
       return;
@@ -1338,7 +1397,8 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra, 
   HH_TR(1, 0);
   auto xs = mx_stage<NTX, XB>(s_xb, a.xq, a.xs, a.xld, a.hidden, T, [](int j) { return j; }, tid, 256);
   if constexpr (FR) {
-    quant_x_lds(ra.x, T, H, a.xld, s_xb, RS);
+    if constexpr (FR == 2) quant_x_lds_block(ra, T, H, a.xld, s_xb, RS);
+    else quant_x_lds(ra.x, T, H, a.xld, s_xb, RS);
     HH_TR(1, 6);
     if (wave == 0) {
       // the records of this workgroup's XCD (workgroups are dealt to the 8 XCDs round robin)
@@ -2194,6 +2254,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   }
 }
 
+#ifndef HH_GEMM_KERNELS_ONLY
 // y[t][j] = Σ_r slot[t·slots + r][j] in rank order (sum_expert_slices, dense.metal:147; the
 // shared expert's slot comes last as in QwenReferenceLayer.swift:399-404).
 __global__ __launch_bounds__(256) void combine_kernel(const float *slot_out, int slots, int H,
@@ -2214,6 +2275,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *slot_out, int
     *(f32x4 *)(y + t * H + j) = s;
   }
 }
+#endif
 
 // ---- prefill, MXFP4: persistent pipeline with direct-to-LDS loads -----------------------------
 // One 512-thread workgroup per compute unit takes tasks τ = blockIdx.x, + gridDim.x, ... in
@@ -3390,11 +3452,15 @@ constexpr int MX_STATIC = 23;
 // MLX gate-up rows of exactly 2·MLX_NCW chunks (K = 2048: Qwen3.5-35B-A3B) take the single-round
 // stream of MLX_NCW chunks per wave.
 constexpr int MLX_NCW = 16;
-template <int FMT> static UpSmallKernel up_small_k(bool one, int T, bool st = false, bool stat = false, bool fr = false) {
+#ifndef HH_GEMM_KERNELS_ONLY
+// fr: 0 none, 1 the fused router over x, 2 the fused router over the FFN block's residual.
+UpSmallKernel up_small_block_k(bool st, int T);
+template <int FMT> static UpSmallKernel up_small_k(bool one, int T, bool st = false, bool stat = false, int fr = 0) {
   if constexpr (FMT == Q_MXFP4) {
-    if (fr) {   // the fused router: single-round rows only
-      if (st) return T == 1 ? up_small_mx<MX_ONE, true, 2, MX_STATIC, true> : up_small_mx<MX_ONE, true, MX_XB_WIDE, MX_STATIC, true>;
-      return T == 1 ? up_small_mx<MX_ONE, true, 2, 0, true> : up_small_mx<MX_ONE, true, MX_XB_WIDE, 0, true>;
+    if (fr == 2) return up_small_block_k(st, T);   // the fused router: single-round rows only
+    if (fr) {
+      if (st) return T == 1 ? up_small_mx<MX_ONE, true, 2, MX_STATIC, 1> : up_small_mx<MX_ONE, true, MX_XB_WIDE, MX_STATIC, 1>;
+      return T == 1 ? up_small_mx<MX_ONE, true, 2, 0, 1> : up_small_mx<MX_ONE, true, MX_XB_WIDE, 0, 1>;
     }
     if (one && st) return T == 1 ? up_small_mx<MX_ONE, true, 2, MX_STATIC> : up_small_mx<MX_ONE, true, MX_XB_WIDE, MX_STATIC>;
     if (T == 1) return one ? up_small_mx<MX_ONE, true, 2> : up_small_mx<16, false, 2>;
@@ -3627,7 +3693,7 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
   UpSmallKernel up;
   switch (quant) {
   // The MXFP4 static-count variant needs every up row (over H) at MX_STATIC chunks.
-  case Q_MXFP4: up = up_small_k<Q_MXFP4>(one_up, T, (a.hidden + 127) / 128 == MX_STATIC, false, fr != nullptr); break;
+  case Q_MXFP4: up = up_small_k<Q_MXFP4>(one_up, T, (a.hidden + 127) / 128 == MX_STATIC, false, !fr ? 0 : ra.resid ? 2 : 1); break;
   case Q_BF16: up = up_small_k<Q_BF16>(true, T); break;
   case Q_MLX4: up = up_small_k<Q_MLX4>(true, T, mlx_staged_up(a.hidden), (a.hidden + 63) / 64 == 2 * MLX_NCW); break;
   default: up = up_small_k<Q_MLX8>(true, T, mlx_staged_up(a.hidden), (a.hidden + 63) / 64 == 2 * MLX_NCW); break;
@@ -3652,7 +3718,9 @@ hipError_t launch_small(int quant, GemmArgs a, const RouteArgs &ra, hipStream_t 
                         (const void *)down_small_k<Q_MLX4>(4, true, true), (const void *)down_small_k<Q_MLX4>(9, true, true),
                         (const void *)down_small_k<Q_MLX8>(4, true, true), (const void *)down_small_k<Q_MLX8>(9, true, true),
                         (const void *)up_small_k<Q_MXFP4>(true, 1, true, false, true), (const void *)up_small_k<Q_MXFP4>(true, SMALL_T, true, false, true),
-                        (const void *)up_small_k<Q_MXFP4>(true, 1, false, false, true), (const void *)up_small_k<Q_MXFP4>(true, SMALL_T, false, false, true)};
+                        (const void *)up_small_k<Q_MXFP4>(true, 1, false, false, true), (const void *)up_small_k<Q_MXFP4>(true, SMALL_T, false, false, true),
+                        (const void *)up_small_k<Q_MXFP4>(true, 1, true, false, 2), (const void *)up_small_k<Q_MXFP4>(true, SMALL_T, true, false, 2),
+                        (const void *)up_small_k<Q_MXFP4>(true, 1, false, false, 2), (const void *)up_small_k<Q_MXFP4>(true, SMALL_T, false, false, 2)};
     // Best effort: HIP on gfx950 accepts launches up to the hardware LDS size without it, and
     // a runtime that rejects the attribute must not leave its error for the launch check below.
     for (const void *k : ks) {
@@ -3804,5 +3872,15 @@ hipError_t launch_combine(const float *slot_out, int slots, int H, int T, float 
   return hipGetLastError();
 }
 
-}  // namespace hh
+#else
+// The FFN block's MXFP4 gate-up kernels with the fused router, compiled in a translation unit of
+// their own (hh_gemm_block.hip): adding them leaves the code object of the other kernels as it
+// was (the decode kernels' speed had moved with it).
+UpSmallKernel up_small_block_k(bool st, int T) {
+  if (st) return T == 1 ? up_small_mx<MX_ONE, true, 2, MX_STATIC, 2> : up_small_mx<MX_ONE, true, MX_XB_WIDE, MX_STATIC, 2>;
+  return T == 1 ? up_small_mx<MX_ONE, true, 2, 0, 2> : up_small_mx<MX_ONE, true, MX_XB_WIDE, 0, 2>;
+}
 
+#endif
+
+}  // namespace hh

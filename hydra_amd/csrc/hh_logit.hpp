@@ -6,6 +6,7 @@
 // Gemma4ReferenceOps.router (:131-156).
 #pragma once
 #include "hh_common.hpp"
+#include "hh_norm.hpp"
 
 namespace hh {
 
@@ -295,6 +296,81 @@ __device__ __forceinline__ double split_pair_logit(const RouteArgs &a, int t, in
         acc += (double)(xf * wf);
       }
     }
+  s_acc[u][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return 0.0;
+  double v = wave_sum_f64((s_acc[0][lane] + s_acc[1][lane]) + (s_acc[2][lane] + s_acc[3][lane]));
+  if (!sg && a.router_b) v += (double)bf16_bits_to_f32(a.router_b[e]);
+  return v;
+}
+
+// split_pair_logit for the FFN block (non-GEMMA router, H ≤ 4096), whose layer input x is not in
+// memory: each wave loads token t's residual row in row_sumsq's layout (lane l: columns 2048i +
+// 512u + 8l .. +7), sums its squares in row_sumsq's order and butterfly, takes the norm factor f
+// and rounds its own slice u to x = bf16(resid·f·norm_w), the values the block's norm kernel
+// writes; the products, the per-slice sums and the wave sum are split_pair_logit's. Row E (the
+// shared gate) takes the same x. Every global load goes out before the first arithmetic.
+__device__ __forceinline__ double block_pair_logit(const RouteArgs &a, int t, int e, double (*s_acc)[64]) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int E = a.experts, H = a.hidden;
+  const bool sg = e == E;
+  const uint16_t *wrow = sg ? a.shared_gate : a.router_w + (size_t)e * H;
+  const float *x = a.resid + (size_t)t * H;
+  const int u = wave, nb = H > 2048 ? 2 : 1;
+  f32x4 xv[2][4][2];
+  u32x4 wv[2], nv[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int uu = 0; uu < 4; ++uu) {
+      const int h = 2048 * i + 512 * uu + 8 * lane;
+      const int hc = min(h, H - 8);
+      xv[i][uu][0] = *(const f32x4 *)(x + hc);
+      xv[i][uu][1] = *(const f32x4 *)(x + hc + 4);
+      if (h >= H) xv[i][uu][0] = xv[i][uu][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const int h = 2048 * b + 512 * u + 8 * lane;
+    const int hc = min(h, H - 8);
+    wv[b] = *(const u32x4 *)(wrow + hc);
+    nv[b] = *(const u32x4 *)(a.norm_w + hc);
+    if (h >= H) wv[b] = u32x4{0u, 0u, 0u, 0u};
+  }
+  double ss = 0.0;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int uu = 0; uu < 4; ++uu)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const double d = xv[i][uu][k >> 2][k & 3];
+        ss += d * d;
+      }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  const double f = norm_factor(ss, H, (double)a.norm_eps, a.norm_pow);
+  double acc = 0.0;
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    if (b >= nb) break;
+    f32x4 x0 = xv[b][0][0], x1 = xv[b][0][1];   // slice u of step b (u is wave-uniform)
+#pragma unroll
+    for (int uu = 1; uu < 4; ++uu)
+      if (u == uu) {
+        x0 = xv[b][uu][0];
+        x1 = xv[b][uu][1];
+      }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int sh = (k & 1) * 16;
+      const float rv = k < 4 ? x0[k] : x1[k - 4];
+      const float nf = bf16_bits_to_f32((nv[b][k >> 1] >> sh) & 0xFFFF);
+      const float xf = bf16_bits_to_f32(f64_to_bf16_bits((double)rv * f * (double)nf));
+      const float wf = bf16_bits_to_f32((wv[b][k >> 1] >> sh) & 0xFFFF);
+      acc += (double)(xf * wf);
+    }
+  }
   s_acc[u][lane] = acc;
   __syncthreads();
   if (wave != 0) return 0.0;

@@ -17,7 +17,11 @@ pytestmark = pytest.mark.gpu
 REL_L2 = 1e-3
 
 CASES = {
-    "gpt-oss-20b": (F.GPT_OSS_20B, [1, 8, 40]),
+    "gpt-oss-20b": (F.GPT_OSS_20B, [1, 2, 8, 40]),
+    # a shared expert (its gate row in the router) and H past a 512-column slice
+    "mxfp4-shared": (F.MoEDesc(hidden=640, intermediate=128, experts=6, top_k=2, quant=F.QUANT_MXFP4,
+                               activation=F.ACT_SWIGLU_OAI, router=F.ROUTER_SOFTMAX_TOPK_RENORM,
+                               shared_intermediate=128, expert_bias=1), [1, 2, 5]),
     "qwen-q4": (F.QWEN_35B_A3B_Q4, [1, 24]),
     "gemma-bf16": (F.GEMMA_BF16, [1, 40]),
 }

@@ -348,6 +348,10 @@ FUSED_CASES = {
     "mxfp4-ragged": (TINY["mxfp4-ragged"], [3, 16, 1, 7]),
     "gpt-oss-20b": (F.GPT_OSS_20B, [1, 4, 16, 2, 8, 1]),
     "gpt-oss-120b": (F.GPT_OSS_120B, [1, 8, 3]),
+    # the shared expert's gate row in the MXFP4 router workgroups; H past a 512-column slice
+    "mxfp4-shared": (F.MoEDesc(hidden=640, intermediate=128, experts=6, top_k=2, quant=F.QUANT_MXFP4,
+                               activation=F.ACT_SWIGLU_OAI, router=F.ROUTER_SOFTMAX_TOPK_RENORM,
+                               shared_intermediate=128, expert_bias=1), [1, 2, 5, 1]),
     # the BF16 / MLX decode gate-up kernel with its fused routers (bf16 GEMMA, 8-bit MLX)
     "gemma-bf16": (F.GEMMA_BF16, [1, 2, 5, 1]),
     "qwen-mlx4-router8": (F.QWEN_35B_A3B_Q4, [1, 2, 3, 1], 8),
