@@ -16,9 +16,10 @@
 // fp64 (one wave per (token, expert) pair, spread over many compute units). In the layer, the
 // decode gate-up kernel then selects from those logits itself (hh_select.hpp), so routing a
 // decode step is one launch and needs no dispatch; the operator entry hh_router_topk runs
-// select_small_kernel instead. Larger batches run A over a (token tile × expert tile) grid
-// (route_logits_kernel), B one wave per token (route_select_kernel) and C in one workgroup
-// (dispatch_kernel), ordered by the stream.
+// select_small_kernel instead. Larger batches run A over a (token tile × expert tiles) grid
+// (route_logits_kernel), B one workgroup per token below 1024 tokens (route_select_kernel) or one
+// wave per token from there (route_select_wave_kernel), and C (dispatch_kernel, or the
+// multi-block dispatch from 1024 assignments), ordered by the stream.
 //
 // Reference: router_topk / router_topk_batch (attention.metal:249, batch.metal:430),
 // gemma_router_topk (gemma.metal:158), ReferenceOps.router (ReferenceOps.swift:173-183),
@@ -399,58 +400,6 @@ __device__ __forceinline__ void router_operand(bool gemma, const u32x4 &xv, cons
   }
 }
 
-// Screening logits of a 16-token × 16-expert tile over the 128-column chunks c ≡ kq (mod nk):
-// lane (g, l16) supplies router row et·16 + l16 (A) and token t0 + l16 (B) at columns
-// 128c + 32g + 8v. Returns the D fragment (experts 4g..4g+3 of the tile, token l16) and, in
-// wsq, Σw² of row l16 over the same columns (in the lanes of group l16 / 4; the caller sums
-// the K slices). Σw² is accumulated in fp32 like the logits: its relative error (≤ H·2^-24)
-// is far inside the factor 4 of slack the screening bound carries.
-// Chunks are loaded NB at a time before any is used, so the loop costs about one memory
-// latency per NB chunks.
-template <bool gemma, int NB = 2>
-__device__ __forceinline__ f32x4 tile_logits(const RouteArgs &a, int t0, int ntok, int et, int kq, int nk,
-                             float &wsq) {
-  const int lane = threadIdx.x & 63, g = lane >> 4, l16 = lane & 15;
-  const int E = a.experts, H = a.hidden;
-  const uint16_t *xr = a.xr + (size_t)(t0 + min(l16, ntok - 1)) * H;
-  const uint16_t *wrow = a.router_w + (size_t)min(et * 16 + l16, E - 1) * H;
-  const int nch = (H + 127) / 128;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f}, wacc = {0.f, 0.f, 0.f, 0.f};
-  for (int c0 = kq; c0 < nch; c0 += NB * nk) {
-    u32x4 wv[NB][4], xv[NB][4], sv[NB][4];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const int c = c0 + b * nk;
-      const int col = min(128 * min(c, nch - 1) + 32 * g, H - 32);
-      const bool ok = c < nch && 128 * c + 32 * g < H;
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        // Unconditional (clamped) loads, masked afterwards (see exact_logit).
-        wv[b][v] = *(const u32x4 *)(wrow + col + 8 * v);
-        xv[b][v] = *(const u32x4 *)(xr + col + 8 * v);
-        sv[b][v] = gemma ? *(const u32x4 *)(a.router_scale + col + 8 * v) : u32x4{0u, 0u, 0u, 0u};
-        if (!ok) wv[b][v] = u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        u32x4 xh, xl;
-        router_operand(gemma, xv[b][v], sv[b][v], xh, xl);
-        wacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[b][v]), as_bf16x8(wv[b][v]), wacc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[b][v]), as_bf16x8(xh), acc, 0, 0, 0);
-        if constexpr (gemma)
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[b][v]), as_bf16x8(xl), acc, 0, 0, 0);
-      }
-    }
-  }
-  // ‖w_i‖² is the diagonal of W·Wᵀ: row i sits in lane (g = i/4, l16 = i), element i % 4;
-  // the lanes of lane group l16 / 4 return it (0 elsewhere).
-  wsq = (g == (l16 >> 2)) ? wacc[l16 & 3] : 0.f;
-  return acc;
-}
-
 // Screening result of one token: candidate count and the GEMMA normaliser of its input.
 struct TokenScreen {
   int nc = 0;
@@ -459,8 +408,9 @@ struct TokenScreen {
 
 // Screens token t (one wave): bounds every fp32 logit lgf(e) by err_e, θ = the K-th largest
 // lower bound, and writes the candidates {e : ub_e ≥ θ} to cl[] in ascending order.
-// NW > 1: the NW waves of the workgroup screen the same token together (identical results in
-// every wave); the 64-lane ranking splits over them through s_rk [NW][64].
+// NW > 1: groups of NW consecutive waves of the workgroup each screen one token together
+// (identical results in every wave of a group); the 64-lane ranking splits over a group's waves
+// through s_rk [waves][64]. Every wave of the workgroup calls it (one barrier).
 template <bool gemma, int NW = 1, class LG, class WN>
 __device__ __forceinline__ TokenScreen screen_token(const RouteArgs &a, int t, LG lgf, WN wnf, int *cl,
                                                     int (*s_rk)[64] = nullptr, double coef = -1.0) {
@@ -528,7 +478,7 @@ __device__ __forceinline__ TokenScreen screen_token(const RouteArgs &a, int t, L
   for (int j = 0; j < 8; ++j) mx = fmaxf(mx, lb[j]);
   int rk = 0;
   {
-    const int j0 = NW > 1 ? (64 / NW) * (int)(threadIdx.x >> 6) : 0;
+    const int j0 = NW > 1 ? (64 / NW) * ((int)(threadIdx.x >> 6) % NW) : 0;
 #pragma unroll 4
     for (int jj = 0; jj < 64 / NW; ++jj) {
       const int j = j0 + jj;
@@ -537,11 +487,12 @@ __device__ __forceinline__ TokenScreen screen_token(const RouteArgs &a, int t, L
     }
   }
   if constexpr (NW > 1) {
+    const int w0 = (int)(threadIdx.x >> 6) - (int)(threadIdx.x >> 6) % NW;   // the group's first wave
     s_rk[threadIdx.x >> 6][lane] = rk;
     __syncthreads();
     rk = 0;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) rk += s_rk[w][lane];
+    for (int w = 0; w < NW; ++w) rk += s_rk[w0 + w][lane];
   }
   const float tau = __builtin_bit_cast(
       float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx), __ffsll((unsigned long long)__ballot(rk == K - 1)) - 1));
@@ -618,11 +569,6 @@ __device__ __forceinline__ int quant_x_waves(const RouteArgs &a) {
 }
 
 // ---- large batches ---------------------------------------------------------------------------
-// A: one workgroup per (16-token tile, 16-expert tile), its RLW waves splitting K (chunks
-// c ≡ wave mod RLW, loaded RLB at a time); writes the screening logits
-// lg32 [T][E] and, from the first token tile, ‖w_e‖. Workgroups past the tiles quantise x
-// (MXFP4 layers), one wave per 16 blocks of a token.
-constexpr int RLW = 4, RLB = 2;
 // Zeroes the multi-block dispatch's count buffer (the selection launch that follows adds to it);
 // every workgroup of the calling launch takes a slice.
 __device__ __forceinline__ void zero_dispatch_counts(const RouteArgs &a) {
@@ -631,51 +577,111 @@ __device__ __forceinline__ void zero_dispatch_counts(const RouteArgs &a) {
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) a.dcount[i] = 0;
 }
 
-template <bool gemma>
-__global__ __launch_bounds__(64 * RLW) void route_logits_kernel(RouteArgs a) {
+// A: the screening logits lg32 [T][E] on the bf16 MFMA and, from the first token tile, ‖w_e‖
+// (the diagonal of W·Wᵀ, accumulated in fp32 like the logits: its relative error ≤ H·2^-24 is
+// far inside the factor 4 of slack the screening bound carries). One workgroup per (16-token
+// tile, RET consecutive 16-expert tiles), its RLW2 waves splitting K (chunks c ≡ wave mod RLW2;
+// lane (g, l16) supplies router row l16 of a tile and token l16 at columns 128c + 32g + 8v). A
+// chunk's token operand (GEMMA: the bf16 hi/lo split of x·scale) is loaded and formed once for
+// the RET expert tiles. Any order of the fp32 sums lies inside the screening bound. Workgroups
+// past the tiles quantise x (MXFP4 layers), one wave per 16 blocks of a token.
+constexpr int RLW2 = 8;
+template <bool gemma, int RET>
+__global__ __launch_bounds__(64 * RLW2) void route_logits_kernel(RouteArgs a) {
   warm_kernargs<sizeof(RouteArgs)>();
   zero_dispatch_counts(a);
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, l16 = lane & 15;
-  const int E = a.experts, T = a.tokens;
-  const int ntiles = (E + 15) / 16;
-  const int nlog = ((T + RT_TOK - 1) / RT_TOK) * ntiles;
+  const int E = a.experts, T = a.tokens, H = a.hidden;
+  const int ntiles = (E + 15) / 16, ngr = (ntiles + RET - 1) / RET;
+  const int nlog = ((T + RT_TOK - 1) / RT_TOK) * ngr;
   if ((int)blockIdx.x >= nlog) {
-    const int w = ((int)blockIdx.x - nlog) * RLW + wave;
-    const int per_t = (a.hidden / 32 + 15) / 16;
+    const int w = ((int)blockIdx.x - nlog) * RLW2 + wave;
+    const int per_t = (H / 32 + 15) / 16;
     if (w < quant_x_waves(a)) quant_x_wave(a, w / per_t, 16 * (w % per_t));
     return;
   }
-  const int tt = blockIdx.x / ntiles, et = blockIdx.x - tt * ntiles;
-  const int t0 = tt * RT_TOK;
-  const int ntok = min(RT_TOK, T - t0);
-  __shared__ float s_part[RLW][16][16];   // [wave][expert in tile][token]
-  __shared__ float s_wpart[RLW][16];
-  float wsq;
-  const f32x4 acc = tile_logits<gemma, RLB>(a, t0, ntok, et, wave, RLW, wsq);
+  const int tt = blockIdx.x / ngr, eg = blockIdx.x - tt * ngr;
+  const int t0 = tt * RT_TOK, ntok = min(RT_TOK, T - t0);
+  const bool want_wn = tt == 0;
+  const uint16_t *xr = a.xr + (size_t)(t0 + min(l16, ntok - 1)) * H;
+  const uint16_t *wrow[RET];
 #pragma unroll
-  for (int ii = 0; ii < 4; ++ii) s_part[wave][4 * g + ii][l16] = acc[ii];
-  if (g == (l16 >> 2)) s_wpart[wave][l16] = wsq;
+  for (int j = 0; j < RET; ++j) wrow[j] = a.router_w + (size_t)min((eg * RET + j) * 16 + l16, E - 1) * H;
+  f32x4 acc[RET], wacc[RET];
+#pragma unroll
+  for (int j = 0; j < RET; ++j) acc[j] = wacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int nch = (H + 127) / 128;
+  for (int c = wave; c < nch; c += RLW2) {
+    const int col = min(128 * c + 32 * g, H - 32);
+    const bool ok = 128 * c + 32 * g < H;
+    u32x4 xv[4], sv[4], wv[RET][4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      xv[v] = *(const u32x4 *)(xr + col + 8 * v);
+      sv[v] = gemma ? *(const u32x4 *)(a.router_scale + col + 8 * v) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int j = 0; j < RET; ++j) {
+        wv[j][v] = *(const u32x4 *)(wrow[j] + col + 8 * v);   // clamped, masked below
+        if (!ok) wv[j][v] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      u32x4 xh, xl;
+      router_operand(gemma, xv[v], sv[v], xh, xl);
+#pragma unroll
+      for (int j = 0; j < RET; ++j) {
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[j][v]), as_bf16x8(xh), acc[j], 0, 0, 0);
+        if constexpr (gemma)
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[j][v]), as_bf16x8(xl), acc[j], 0, 0, 0);
+        if (want_wn)
+          wacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[j][v]), as_bf16x8(wv[j][v]), wacc[j], 0, 0, 0);
+      }
+    }
+  }
+  __shared__ float s_part[RLW2][RET][16][16];   // [wave][tile][expert in tile][token]
+  __shared__ float s_wpart[RLW2][RET][16];
+#pragma unroll
+  for (int j = 0; j < RET; ++j) {
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) s_part[wave][j][4 * g + ii][l16] = acc[j][ii];
+    // Σw² of row l16 is the diagonal of W·Wᵀ: lane (g = l16 / 4, l16), element l16 % 4.
+    if (want_wn && g == (l16 >> 2)) s_wpart[wave][j][l16] = wacc[j][l16 & 3];
+  }
   __syncthreads();
-  const int el = tid >> 4, tk = tid & 15;
-  const int e = et * 16 + el;
-  // Pairwise over the waves' K slices (any order is inside the screening bound).
   auto wsum = [&](auto get) {
-    float p[RLW];
+    float p[RLW2];
 #pragma unroll
-    for (int w = 0; w < RLW; ++w) p[w] = get(w);
+    for (int w = 0; w < RLW2; ++w) p[w] = get(w);
 #pragma unroll
-    for (int h = 1; h < RLW; h *= 2)
+    for (int h = 1; h < RLW2; h *= 2)
 #pragma unroll
-      for (int w = 0; w + h < RLW; w += 2 * h) p[w] += p[w + h];
+      for (int w = 0; w + h < RLW2; w += 2 * h) p[w] += p[w + h];
     return p[0];
   };
-  if (tid < 256 && e < E && tk < ntok) {
-    float v = wsum([&](int w) { return s_part[w][el][tk]; });
-    if (a.router_b) v += bf16_bits_to_f32(a.router_b[e]);
-    a.lg32[(size_t)(t0 + tk) * E + e] = v;
-    if (tt == 0 && tk == 0) a.wn[e] = sqrtf(wsum([&](int w) { return s_wpart[w][el]; }));
+  for (int q = tid; q < RET * 256; q += 64 * RLW2) {
+    const int j = q >> 8, el = (q >> 4) & 15, tk = q & 15;
+    const int e = (eg * RET + j) * 16 + el;
+    if (e < E && tk < ntok) {
+      float v = wsum([&](int w) { return s_part[w][j][el][tk]; });
+      if (a.router_b) v += bf16_bits_to_f32(a.router_b[e]);
+      a.lg32[(size_t)(t0 + tk) * E + e] = v;
+      if (want_wn && tk == 0) a.wn[e] = sqrtf(wsum([&](int w) { return s_wpart[w][j][el]; }));
+    }
   }
+}
+// Expert tiles per workgroup of route_logits_kernel: the most (up to 4) that still leave
+// 256 logit workgroups.
+static int wide_ret(int T, int E) {
+  const int tt = (T + RT_TOK - 1) / RT_TOK, nt = (E + 15) / 16;
+  for (int r : {4, 2})
+    if (tt * ((nt + r - 1) / r) >= 256) return r;
+  return 1;
+}
+template <bool gemma> static void *wide_logits_fn(int ret) {
+  return ret == 4 ? (void *)route_logits_kernel<gemma, 4>
+                  : ret == 2 ? (void *)route_logits_kernel<gemma, 2> : (void *)route_logits_kernel<gemma, 1>;
 }
 
 // B: one workgroup per token. Its 4 waves screen the token together, then wave w computes the
@@ -685,8 +691,8 @@ __global__ __launch_bounds__(64 * RLW) void route_logits_kernel(RouteArgs a) {
 // token's routing.
 
 
-// A T=2048 batch is 2048 four-wave workgroups: the GEMMA variant took 129 VGPRs, three per
-// compute unit (about three rounds of them); at most 128 gives four (five spills).
+// The GEMMA variant took 129 VGPRs, three workgroups per compute unit; at most 128 gives four
+// (five spills).
 template <bool gemma>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(gemma ? 4 : 5))) void route_select_kernel(RouteArgs a) {
   warm_kernargs<sizeof(RouteArgs)>();
@@ -725,6 +731,59 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(gemma ? 4 :
   for (int c = 0; c < ts.nc; ++c) tk.insert(s_v[c], s_cl[0][c], a.top_k);
   prob_order(tk, a.top_k, a.router);
   finish_token<true>(a, t, tk, a.shared_gate ? s_sg : 0.0);
+}
+
+// B for batches of at least kSelWaveT tokens: one wave per token, four tokens per workgroup, so
+// that every token's wave is resident at once (2048 tokens are two waves per SIMD) where the
+// four-wave form above ran in rounds of workgroups. The wave screens its token alone
+// (screen_token, NW = 1: the same bounds and candidates), computes the candidates' exact
+// logits RSEL rows at a time (exact_logits_rows: each row's arithmetic is the one-row form's,
+// so the same values) and the shared gate's, then ranks them and writes the token's routing:
+// the same routing as route_select_kernel's.
+constexpr int kSelWaveT = 1024;
+constexpr int RSEL = 4;
+template <bool gemma>
+__global__ __launch_bounds__(256) void route_select_wave_kernel(RouteArgs a) {
+  warm_kernargs<sizeof(RouteArgs)>();
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wave;
+  __shared__ int s_cl[4][kMaxExperts];
+  __shared__ double s_v[4][kMaxExperts];
+  if (t >= a.tokens) return;
+  if (wave == 0) HH_RT(0);
+  const int H = a.hidden;
+  const float *lg = a.lg32 + (size_t)t * a.experts;
+  const float *wn = a.wn;
+  int *cl = s_cl[wave];
+  const TokenScreen ts = screen_token<gemma, 1>(a, t, [&](int e) { return lg[e]; }, [&](int e) { return wn[e]; }, cl);
+  if (wave == 0) HH_RT(1);
+  if (wave == 0) HH_RT_NC(ts.nc);
+  const double root = gemma ? pow((double)H, -0.5) : 1.0;
+  const uint16_t *xr = a.xr + (size_t)t * H;
+  for (int c0 = 0; c0 < ts.nc; c0 += RSEL) {
+    const uint16_t *rows[RSEL];
+    int es[RSEL];
+#pragma unroll
+    for (int r = 0; r < RSEL; ++r) {
+      es[r] = cl[min(c0 + r, ts.nc - 1)];
+      rows[r] = a.router_w + (size_t)es[r] * H;
+    }
+    double v[RSEL];
+    exact_logits_rows<gemma, RSEL>(a, xr, rows, ts.norm, root, v);
+#pragma unroll
+    for (int r = 0; r < RSEL; ++r) {
+      if (a.router_b) v[r] += (double)bf16_bits_to_f32(a.router_b[es[r]]);
+      if (lane == 0 && c0 + r < ts.nc) s_v[wave][c0 + r] = v[r];
+    }
+  }
+  const double sg = a.shared_gate ? exact_logit<false>(a, a.x + (size_t)t * H, a.shared_gate, 1.0, 1.0) : 0.0;
+  if (wave == 0) HH_RT(2);
+  __builtin_amdgcn_wave_barrier();
+  TopK tk;
+  for (int c = 0; c < ts.nc; ++c) tk.insert(s_v[wave][c], cl[c], a.top_k);
+  prob_order(tk, a.top_k, a.router);
+  finish_token<true>(a, t, tk, sg);
+  if (wave == 0) HH_RT(3);
 }
 
 // C.
@@ -1357,12 +1416,22 @@ hipError_t launch_route(const RouteArgs &a, hipStream_t s, Timing tm) {
   const bool third = a.want_dispatch != 0;
   const bool g = a.router == R_GEMMA;
   const int qw = a.xq ? a.tokens * ((a.hidden / 32 + 15) / 16) : 0;
-  hipExtLaunchKernelGGL(g ? route_logits_kernel<true> : route_logits_kernel<false>,
-                        dim3(ttiles * etiles + (qw + RLW - 1) / RLW), dim3(64 * RLW), 0, s, tm.start, nullptr, 0, a);
+  {
+    const int ret = wide_ret(a.tokens, a.experts);
+    void *k = g ? wide_logits_fn<true>(ret) : wide_logits_fn<false>(ret);
+    void *args[] = {(void *)&a};
+    const int blocks = ttiles * ((etiles + ret - 1) / ret) + (qw + RLW2 - 1) / RLW2;
+    hipError_t le = hipExtLaunchKernel(k, dim3(blocks), dim3(64 * RLW2), args, 0, s, tm.start, nullptr, 0);
+    if (le != hipSuccess) return le;
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipExtLaunchKernelGGL(g ? route_select_kernel<true> : route_select_kernel<false>, dim3(a.tokens), dim3(256), 0, s, nullptr,
-                        third ? nullptr : tm.stop, 0, a);
+  if (a.tokens >= kSelWaveT && a.hidden <= 4096)
+    hipExtLaunchKernelGGL(g ? route_select_wave_kernel<true> : route_select_wave_kernel<false>, dim3((a.tokens + 3) / 4),
+                          dim3(256), 0, s, nullptr, third ? nullptr : tm.stop, 0, a);
+  else
+    hipExtLaunchKernelGGL(g ? route_select_kernel<true> : route_select_kernel<false>, dim3(a.tokens), dim3(256), 0, s,
+                          nullptr, third ? nullptr : tm.stop, 0, a);
   e = hipGetLastError();
   if (e != hipSuccess || !third) return e;
   return launch_dispatch(a, s, tm.stop, true);

@@ -153,7 +153,7 @@ ROUTER_CASES = {
 
 
 @pytest.mark.parametrize("name", list(ROUTER_CASES))
-@pytest.mark.parametrize("T", [5, 96])
+@pytest.mark.parametrize("T", [5, 96, 1030])   # 1030: the one-wave-per-token selection, a ragged last workgroup
 def test_router_indices_bit_exact(torch_dev, ctx, name, T):
     from hydra_amd._lib import check, desc_c, lib
     from hydra_amd.layer import MoELayer
@@ -486,8 +486,10 @@ def test_router_near_ties_resolved_exactly(torch_dev, ctx, router):
     L = MoELayer(layer, ctx)
     d = desc_c(desc)
     ref_all = O.router_logits(desc, layer, x_all)
-    for T in (64, 8):   # the screened multi-workgroup path and the one-workgroup path
-        x = x_all[:T]
+    # the screened multi-workgroup path, the one-workgroup path and (1027 tokens: the rows
+    # repeated) the one-wave-per-token selection
+    for T in (64, 8, 1027):
+        x = np.resize(x_all, (T, desc.hidden))
         idx = torch.empty((T, 4), dtype=torch.int32, device="cuda:0")
         w = torch.empty((T, 4), dtype=torch.float32, device="cuda:0")
         xd = dev(torch, x)
@@ -497,7 +499,7 @@ def test_router_near_ties_resolved_exactly(torch_dev, ctx, router):
         got = idx.cpu().numpy()
         for t in range(T):
             if router == F.ROUTER_TOPK_SOFTMAX:
-                ri, _ = O.router_topk_softmax(ref_all[t], 4)
+                ri, _ = O.router_topk_softmax(ref_all[t % 64], 4)
             else:
-                ri, _ = O.router_softmax_topk_renorm(ref_all[t], 4)
+                ri, _ = O.router_softmax_topk_renorm(ref_all[t % 64], 4)
             assert np.array_equal(got[t], ri), (T, t, got[t], ri)

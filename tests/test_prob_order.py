@@ -149,8 +149,10 @@ def test_gpu_router_topk_zero_probabilities(name, bits):
         d = desc_c(desc)
         x_all = _tokens(desc.hidden, 48, 73)
         _, ridx, rw, _ = O.moe_forward(layer, x_all)
-        for T in (1, 8, 48):      # one-token, small-batch and screened (T > 16) selection
-            x = to_device(x_all[:T], "cuda:0")
+        # one-token, small-batch, screened (T > 16) and one-wave-per-token (T ≥ 1024; the 48
+        # rows repeated) selection
+        for T in (1, 8, 48, 1025):
+            x = to_device(np.resize(x_all, (T, desc.hidden)), "cuda:0")
             idx = torch.full((T, 8), -1, dtype=torch.int32, device="cuda:0")
             w = torch.empty((T, 8), dtype=torch.float32, device="cuda:0")
             torch.cuda.synchronize()
@@ -158,8 +160,9 @@ def test_gpu_router_topk_zero_probabilities(name, bits):
                                        None, _p(idx), _p(w), None))
             ctx.synchronize()
             got = idx.cpu().numpy()
-            assert np.array_equal(got, ridx[:T]), (T, got[0], ridx[0])
-            assert np.max(np.abs(w.cpu().numpy() - rw[:T])) < 1e-6
+            ri, rwt = np.resize(ridx, (T, 8)), np.resize(rw, (T, 8))
+            assert np.array_equal(got, ri), (T, got[0], ri[0])
+            assert np.max(np.abs(w.cpu().numpy() - rwt)) < 1e-6
     finally:
         ctx.close()
 
