@@ -90,8 +90,12 @@ def test_gpu_mlx_router_topk_exact(bits):
         x_all = synth.make_tokens(QWEN_SMALL.hidden, 100, seed=10)
         ref = O.router_logits(QWEN_SMALL, layer, x_all)
         _, ridx_all, rw_all, rsw_all = O.moe_forward(layer, x_all)
-        for T in (5, 100):          # the one-workgroup selection and the per-token selection
-            x = to_device(x_all[:T], "cuda:0")
+        # the one-workgroup selection and the per-token selection (1029 tokens: the 100 rows
+        # repeated; the multi-block dispatch)
+        for T in (5, 100, 1029):
+            x = to_device(np.resize(x_all, (T, QWEN_SMALL.hidden)), "cuda:0")
+            ridx, rw, rsw = (np.resize(v, (T,) + v.shape[1:]) for v in (ridx_all, rw_all, rsw_all))
+            rref = np.resize(ref, (T, ref.shape[1]))
             idx = torch.full((T, 8), -1, dtype=torch.int32, device="cuda:0")
             w = torch.empty((T, 8), dtype=torch.float32, device="cuda:0")
             lg = torch.empty((T, 8), dtype=torch.float64, device="cuda:0")
@@ -101,11 +105,11 @@ def test_gpu_mlx_router_topk_exact(bits):
                                        _p(lg), _p(idx), _p(w), _p(sw)))
             ctx.synchronize()
             got = idx.cpu().numpy()
-            assert np.array_equal(got, ridx_all[:T]), T
-            sel = np.take_along_axis(ref[:T], got.astype(np.int64), axis=1)
+            assert np.array_equal(got, ridx), T
+            sel = np.take_along_axis(rref, got.astype(np.int64), axis=1)
             assert np.max(np.abs(lg.cpu().numpy() - sel)) <= 1e-12 * np.max(np.abs(sel))
-            assert np.max(np.abs(w.cpu().numpy() - rw_all[:T])) < 1e-6
-            assert np.max(np.abs(sw.cpu().numpy() - rsw_all[:T])) < 1e-6
+            assert np.max(np.abs(w.cpu().numpy() - rw)) < 1e-6
+            assert np.max(np.abs(sw.cpu().numpy() - rsw)) < 1e-6
     finally:
         ctx.close()
 
