@@ -612,33 +612,44 @@ __global__ __launch_bounds__(64 * RLW2) void route_logits_kernel(RouteArgs a) {
 #pragma unroll
   for (int j = 0; j < RET; ++j) acc[j] = wacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int nch = (H + 127) / 128;
-  for (int c = wave; c < nch; c += RLW2) {
-    const int col = min(128 * c + 32 * g, H - 32);
-    const bool ok = 128 * c + 32 * g < H;
+  struct Chunk {
     u32x4 xv[4], sv[4], wv[RET][4];
+  };
+  // Chunk c's operands (columns past H: clamped loads, zero weights).
+  auto load = [&](Chunk &k, int c) {
+    const int cc = min(c, nch - 1);
+    const int col = min(128 * cc + 32 * g, H - 32);
+    const bool ok = 128 * cc + 32 * g < H;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      xv[v] = *(const u32x4 *)(xr + col + 8 * v);
-      sv[v] = gemma ? *(const u32x4 *)(a.router_scale + col + 8 * v) : u32x4{0u, 0u, 0u, 0u};
+      k.xv[v] = *(const u32x4 *)(xr + col + 8 * v);
+      k.sv[v] = gemma ? *(const u32x4 *)(a.router_scale + col + 8 * v) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int j = 0; j < RET; ++j) {
-        wv[j][v] = *(const u32x4 *)(wrow[j] + col + 8 * v);   // clamped, masked below
-        if (!ok) wv[j][v] = u32x4{0u, 0u, 0u, 0u};
+        k.wv[j][v] = *(const u32x4 *)(wrow[j] + col + 8 * v);
+        if (!ok) k.wv[j][v] = u32x4{0u, 0u, 0u, 0u};
       }
     }
+  };
+  auto add = [&](const Chunk &k) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       u32x4 xh, xl;
-      router_operand(gemma, xv[v], sv[v], xh, xl);
+      router_operand(gemma, k.xv[v], k.sv[v], xh, xl);
 #pragma unroll
       for (int j = 0; j < RET; ++j) {
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[j][v]), as_bf16x8(xh), acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k.wv[j][v]), as_bf16x8(xh), acc[j], 0, 0, 0);
         if constexpr (gemma)
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[j][v]), as_bf16x8(xl), acc[j], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k.wv[j][v]), as_bf16x8(xl), acc[j], 0, 0, 0);
         if (want_wn)
-          wacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(wv[j][v]), as_bf16x8(wv[j][v]), wacc[j], 0, 0, 0);
+          wacc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(k.wv[j][v]), as_bf16x8(k.wv[j][v]), wacc[j], 0, 0, 0);
       }
     }
+  };
+  for (int c = wave; c < nch; c += RLW2) {
+    Chunk k;
+    load(k, c);
+    add(k);
   }
   __shared__ float s_part[RLW2][RET][16][16];   // [wave][tile][expert in tile][token]
   __shared__ float s_wpart[RLW2][RET][16];
