@@ -149,6 +149,11 @@ ROUTER_CASES = {
     "gpt-oss-120b-zipf": (F.GPT_OSS_120B, 1.1),
     "qwen-q4": (F.QWEN_35B_A3B_Q4, None),
     "gemma": (F.GEMMA_BF16, None),
+    # 19 expert tiles, the last one partial: at 1030 tokens four tiles per screening workgroup,
+    # its last group ragged; H past a 512-column slice
+    "e300": (F.MoEDesc(hidden=640, intermediate=64, experts=300, top_k=6, quant=F.QUANT_MXFP4,
+                       activation=F.ACT_SWIGLU_OAI, router=F.ROUTER_SOFTMAX_TOPK_RENORM,
+                       expert_bias=1), None),
 }
 
 
