@@ -1364,7 +1364,10 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra, 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, l16 = lane & 15;
-  const int T = ra.tokens, E = a.experts, K = a.top_k, S = a.slots, H = a.hidden;
+  // The instances with two x vectors per thread (XB = 2) are launched for one token only
+  // (up_small_k): their token count is compiled in.
+  constexpr bool T1 = XB <= 2;
+  const int T = T1 ? 1 : ra.tokens, E = a.experts, K = a.top_k, S = a.slots, H = a.hidden;
   const bool has_shared = S > K;
   // The gate-up role's workgroup index and count.
   const int bx = FR ? (int)blockIdx.x - f.R : (int)blockIdx.x;
@@ -1422,14 +1425,14 @@ __global__ __launch_bounds__(256, 2) void up_small_mx(GemmArgs a, RouteArgs ra, 
   };
   // Top-k of every token (wave w: tokens w, w + 4, ...; one token: the 4 waves rank it
   // together); workgroup 0 writes the routing outputs.
-  if (T <= 2) {
+  if (T1 || T <= 2) {
     // One or two tokens: groups of 4 / T waves rank a token together.
-    const int G = T == 1 ? 4 : 2, t = wave / G;
+    const int G = (T1 || T == 1) ? 4 : 2, t = T1 ? 0 : wave / G;
     const double *lg = logits_of(t);
 #ifdef HH_TRACE
     if (!FR) { volatile double first = lg[lane % E]; (void)first; HH_TR(1, 6); }
 #endif
-    TopK tk = T == 1 ? (E <= 64 ? topk_rank64<4>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
+    TopK tk = (T1 || T == 1) ? (E <= 64 ? topk_rank64<4>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
                                       : topk_fast<4>(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave], s_rk))
                            : (E <= 64 ? topk_rank64<2>(lg, E, K, s_lg[wave], s_ri[wave], s_rk)
                                       : topk_fast<2, 1>(lg, E, K, s_ri[wave], s_rv[wave], s_ci[wave], s_cv[wave], s_rk));
