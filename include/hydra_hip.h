@@ -150,10 +150,11 @@ const char *hh_last_error(void);
 int hh_ctx_profile(hh_ctx *ctx, int32_t enable);
 int hh_ctx_profile_read(hh_ctx *ctx, double *phase_ms /* [4] */, int64_t *calls);
 /* The launch structure of MXFP4 decode calls (at most 16 tokens), with the same results bit
- * for bit in every mode. 0: three launches (router, gate-up, down). 2: two launches, the router
- * as the first workgroups of the gate-up launch (1 or 2 tokens, bf16 non-GEMMA routers,
- * H <= 4096, E <= 128; other calls, calls under capture and the allocation-free entry take
- * three); the profile then records the routing phase as empty. 1: one launch (router, gate-up and down roles; no shared
+ * for bit in every mode; hh_moe_block_forward follows it too. 0: three launches (router,
+ * gate-up, down). 2: two launches, the router as the first workgroups of the gate-up launch
+ * (1 or 2 tokens, bf16 non-GEMMA routers, H <= 4096, E <= 128; other calls, calls under capture
+ * and the allocation-free entry take three); the profile then records the routing phase as
+ * empty. 1: one launch (router, gate-up and down roles; no shared
  * expert, top_k <= 4, E <= 128), whose profile records the whole layer as phase 0. -1: the
  * default, the environment variable HH_DECODE_FUSED (0, 1 or 2) or else 2. No counterpart in
  * the reference: a scheduling choice of this implementation.                               */
