@@ -630,18 +630,19 @@ int hh_ctx_create(hh_ctx **out, int32_t device) {
 
 int hh_ctx_destroy(hh_ctx *ctx) {
   if (!ctx) return HH_OK;
-  hipSetDevice(ctx->device);
+  // Teardown is best effort: every resource is released whatever an earlier release returned.
+  (void)hipSetDevice(ctx->device);
   if (ctx->capturing) {   // abandon an unfinished capture
     hipGraph_t g = nullptr;
-    if (hipStreamEndCapture(ctx->stream, &g) == hipSuccess && g) hipGraphDestroy(g);
+    if (hipStreamEndCapture(ctx->stream, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
     ctx->capturing = false;
   }
-  if (ctx->stream) hipStreamSynchronize(ctx->stream);
-  if (ctx->arena) hipFree(ctx->arena);
-  if (ctx->attn) hipFree(ctx->attn);
-  if (ctx->flags) hipFree(ctx->flags);
-  for (hipEvent_t ev : ctx->events) hipEventDestroy(ev);
-  if (ctx->stream) hipStreamDestroy(ctx->stream);
+  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  if (ctx->arena) (void)hipFree(ctx->arena);
+  if (ctx->attn) (void)hipFree(ctx->attn);
+  if (ctx->flags) (void)hipFree(ctx->flags);
+  for (hipEvent_t ev : ctx->events) (void)hipEventDestroy(ev);
+  if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   delete ctx;
   return HH_OK;
 }
@@ -846,7 +847,7 @@ int hh_ctx_capture_end(hh_ctx *ctx, hh_graph **out) {
   hipGraphExec_t exec = nullptr;
   const hipError_t e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
   if (e != hipSuccess) {
-    hipGraphDestroy(graph);
+    (void)hipGraphDestroy(graph);
     return hip_fail(e, "hipGraphInstantiate");
   }
   hh_graph *g = new hh_graph;
@@ -870,10 +871,10 @@ int hh_graph_launch(hh_graph *g) {
 
 int hh_graph_destroy(hh_graph *g) {
   if (!g) return HH_OK;
-  hipSetDevice(g->ctx->device);
-  hipStreamSynchronize(g->ctx->stream);
-  if (g->exec) hipGraphExecDestroy(g->exec);
-  if (g->graph) hipGraphDestroy(g->graph);
+  (void)hipSetDevice(g->ctx->device);   // best effort, as hh_ctx_destroy
+  (void)hipStreamSynchronize(g->ctx->stream);
+  if (g->exec) (void)hipGraphExecDestroy(g->exec);
+  if (g->graph) (void)hipGraphDestroy(g->graph);
   g->ctx->live_graphs -= 1;
   delete g;
   return HH_OK;
