@@ -297,6 +297,28 @@ def test_prefill_equals_token_by_token_bit_for_bit(torch_dev, ctx, name):
     assert np.array_equal(np.concatenate(parts).view(np.uint32), y_all.view(np.uint32))
 
 
+@pytest.mark.parametrize("name", ["mxfp4", "mlx4", "bf16"])
+def test_large_batch_equals_token_by_token_bit_for_bit(torch_dev, ctx, name):
+    """From 1024 tokens the selection takes one wave per token and the grouping the multi-block
+    dispatch: a 1100-token batch's outputs, top-k and weights equal single-token calls bit for bit
+    (sampled tokens, the last workgroup's ragged ones included), and so do uneven chunks."""
+    from hydra_amd.layer import MoELayer
+    desc = TINY[name]
+    say(f"large batch == decode {name}")
+    layer = synth.make_layer(desc, seed=43)
+    T = 1100
+    x = synth.make_tokens(desc.hidden, T, seed=44)
+    L = MoELayer(layer, ctx)
+    y_all, idx_all, w_all = (v.cpu().numpy() for v in L.forward(x))
+    for t in [0, 1, 511, 1023, 1024, 1097, 1098, 1099]:
+        y1, i1, w1 = (v.cpu().numpy() for v in L.forward(x[t:t + 1]))
+        assert np.array_equal(i1[0], idx_all[t]), t
+        assert np.array_equal(w1[0].view(np.uint32), w_all[t].view(np.uint32)), t
+        assert np.array_equal(y1[0].view(np.uint32), y_all[t].view(np.uint32)), t
+    parts = [L.forward(x[a:b])[0].cpu().numpy() for a, b in [(0, 17), (17, 1041), (1041, 1100)]]
+    assert np.array_equal(np.concatenate(parts).view(np.uint32), y_all.view(np.uint32))
+
+
 WIDE = {
     "mxfp4-wide": TINY["mxfp4-wide"],
     # Gate-up rows of ≥ 12 chunks: the register-ring gate-up kernel (64-token items at T=300: the
