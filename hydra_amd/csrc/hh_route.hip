@@ -748,11 +748,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(gemma ? 4 :
 // that every token's wave is resident at once (2048 tokens are two waves per SIMD) where the
 // four-wave form above ran in rounds of workgroups. The wave screens its token alone
 // (screen_token, NW = 1: the same bounds and candidates), computes the candidates' exact
-// logits RSEL rows at a time (exact_logits_rows: each row's arithmetic is the one-row form's,
+// logits sel_rows() rows at a time (exact_logits_rows: each row's arithmetic is the one-row form's,
 // so the same values) and the shared gate's, then ranks them and writes the token's routing:
 // the same routing as route_select_kernel's.
 constexpr int kSelWaveT = 1024;
-constexpr int RSEL = 4;
+// Candidate rows per batch: GEMMA's top-8 screens ≈ 9 candidates, in batches of 4 (5 and 6 were
+// slower: 49.5 / 52 against 46 µs at T=2048); the top-4 routers ≈ 4.3, mostly one batch of 5
+// (27.4 → 25.2 µs on the 120B layer at T=2048).
+template <bool gemma> constexpr int sel_rows() { return gemma ? 4 : 5; }
 template <bool gemma>
 __global__ __launch_bounds__(256) void route_select_wave_kernel(RouteArgs a) {
   warm_kernargs<sizeof(RouteArgs)>();
@@ -771,6 +774,7 @@ __global__ __launch_bounds__(256) void route_select_wave_kernel(RouteArgs a) {
   if (wave == 0) HH_RT_NC(ts.nc);
   const double root = gemma ? pow((double)H, -0.5) : 1.0;
   const uint16_t *xr = a.xr + (size_t)t * H;
+  constexpr int RSEL = sel_rows<gemma>();
   for (int c0 = 0; c0 < ts.nc; c0 += RSEL) {
     const uint16_t *rows[RSEL];
     int es[RSEL];
